@@ -1,0 +1,118 @@
+/* C ABI of the MI355X nested Gated DeltaNet op (libngdn.so, gfx950).
+ *
+ * Plain pointers to device memory, sizes and a HIP stream (passed as void*,
+ * a hipStream_t). Every entry point validates its arguments, launches
+ * asynchronously on the given stream and returns 0, or a nonzero NGDN_E*
+ * code with a message available from ngdn_last_error(). Nothing is allocated
+ * inside the library: callers pass every output and workspace buffer.
+ * Entry points are re-entrant; the error message is kept per thread.
+ *
+ * Tensor layouts follow the reference op (nested_gdn2/ops/chunk.py:722-766):
+ *   q [B,T,H,L,K]; k, b [B,T,H,K]; v, w [B,T,H,V]; g [B,T,H,K] fp32;
+ *   mix [B,T,H,L]; initial/final state [B,H,L,K,V] fp32;
+ *   query_banks [L-1,H,Nmax,K]; key_projections [L-1,H,K,V];
+ *   b/g_projections [L-1,H,V,K]; w_projections [L-1,H,V,V].
+ * All contiguous. "dtype" is the element type of the float tensors other than
+ * g and the states: NGDN_F32 or NGDN_BF16. Chunk size is 64.
+ * Working tensors between the entry points ([B,H,NT,...], NT = ceil(T/64))
+ * are described at each function.
+ */
+#ifndef NGDN_H
+#define NGDN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NGDN_OK 0
+#define NGDN_EINVAL 1   /* bad shape, dtype, pointer or option */
+#define NGDN_ELAUNCH 2  /* the HIP runtime refused a launch */
+
+#define NGDN_F32 0
+#define NGDN_BF16 1
+
+typedef struct ngdn_dims {
+  int32_t B, T, H, L, K, V;
+  int32_t dtype;
+  float scale;
+} ngdn_dims;
+
+/* Last error message on this thread ("" when none). */
+const char* ngdn_last_error(void);
+/* Library version, major * 10000 + minor * 100 + patch. */
+int32_t ngdn_version(void);
+/* Offload architecture the library was built for ("gfx950"). */
+const char* ngdn_arch(void);
+
+/* Level-0 per-chunk terms: the intra-chunk half of fla's chunk_gdn2_fwd as
+ * called at nested_gdn2/ops/chunk.py:236-248 (semantics ops/naive.py:329-358).
+ * Outputs (working dtype unless noted): W [B,H,NT,64,K], U [B,H,NT,64,V],
+ * KtT [B,H,NT,K,64], Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64],
+ * gam [B,H,NT,K] fp32. */
+int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
+                          const void* v, const float* g, const void* b,
+                          const void* w, void* W, void* U, void* KtT, void* Qg,
+                          void* Aqk, float* gam, void* stream);
+
+/* Level-0 state recurrence over chunks: the inter-chunk half of fla's
+ * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
+ * Writes hT [B,H,NT,V,K] (state entering each chunk, transposed, working
+ * dtype), vnT [B,H,NT,V,64] (the chunk's new values, transposed) and
+ * final_state[:, :, 0] (fp32). initial_state may be NULL (zeros). */
+int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
+                         const void* KtT, const float* gam,
+                         const float* initial_state, void* hT, void* vnT,
+                         float* final_state, void* stream);
+
+/* Promotion probe of level `level` >= 1: PROBES[promotion] applied to the
+ * lower level's state after each of this level's firings
+ * (ops/probe.py:69-136, gathered as in ops/chunk.py:58-93).
+ * below: level 0 -> hT from ngdn_l0_scan_fwd (NG_below = NT);
+ *        level >= 2 -> the lower level's fp32 group states [B,NG_below,H,K,V].
+ * final_state: [B,H,L,K,V] holding the lower level's final state.
+ * bpT, gpT [L-1,H,K,V] and wpT [L-1,H,V,V] are the b/g/w projections with
+ * their last two axes swapped. promotion: 0 learned, 1 merge (n_queries = K).
+ * Outputs for firing i in [0, NF), NF = NT / f_here, laid out [B,H,NF,...]:
+ * A = keys*b*e^g [N,K], KT = keys^T [K,N], U = values*w [N,V] (working dtype),
+ * gam = e^g [K] fp32. keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
+ * receive the probe outputs in the reference layout when not NULL. */
+int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
+                       int32_t n_queries, int32_t f_below, int32_t f_here,
+                       const void* below, int32_t ng_below,
+                       const float* final_state, const void* query_banks,
+                       int32_t n_max, const void* key_projections,
+                       const void* bpT, const void* wpT, const void* gpT,
+                       void* A, void* KT, void* U, float* gam, float* keys,
+                       float* vals, float* bo, float* wo, float* go,
+                       void* stream);
+
+/* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
+ * probe's scan-ready pairs: NF firings, NG = ceil(NT / f) stored group
+ * states. Writes states [B,NG,H,K,V] fp32 (state entering each group; groups
+ * past the last firing hold the final state) and final_state[:, :, level].
+ * initial_state may be NULL. */
+int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
+                            int32_t nf, int32_t ng, const void* A,
+                            const void* KT, const void* U, const float* gam,
+                            const float* initial_state, float* states,
+                            float* final_state, void* stream);
+
+/* Output for every token (ops/chunk.py:129-156, 250-251, 285-286):
+ * o = mix_0 (Qg h + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[group].
+ * states[l] (l = 1..L-1) is level l's fp32 group states with ng[l] groups and
+ * firing interval f[l]; entries at l = 0 are ignored. o [B,T,H,V] in the
+ * working dtype. reads, when not NULL, receives each level's unmixed read,
+ * fp32 [L,B,T,H,V]. */
+int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
+                        const void* hT, const void* vnT, const void* q,
+                        const void* mix, const float* const* states,
+                        const int32_t* ng, const int32_t* f, void* o,
+                        float* reads, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NGDN_H */

@@ -1,0 +1,90 @@
+"""ctypes binding of libngdn.so (the C ABI declared in include/ngdn.h).
+
+torch is imported first so that the HIP runtime torch ships with is the one
+the library binds to (both carry the soname libamdhip64.so.7); device
+pointers and streams then pass between them unchanged.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libngdn.so")
+
+NGDN_F32 = 0
+NGDN_BF16 = 1
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("T", ctypes.c_int32), ("H", ctypes.c_int32),
+                ("L", ctypes.c_int32), ("K", ctypes.c_int32), ("V", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("scale", ctypes.c_float)]
+
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+PD = ctypes.POINTER(Dims)
+
+# name -> argtypes (all return int32 status unless listed in _RESTYPES)
+SIGNATURES = {
+    "ngdn_last_error": [],
+    "ngdn_version": [],
+    "ngdn_arch": [],
+    "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P],
+    "ngdn_l0_scan_fwd": [PD, P, P, P, P, P, P, P, P, P],
+    "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P,
+                       P, P, P, P, P, P, P, P, P, P],
+    "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P],
+    "ngdn_output_fwd": [PD, P, P, P, P, P, P, P, P, P, P, P, P],
+}
+_RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}
+
+_lib = None
+
+
+class NgdnError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library. Raises if it has not been built: there is no
+    fallback path."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NgdnError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                f"g.build()'` (or make -C nested_recurrent_memory_amd/csrc)")
+        so = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(so, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int32)
+        _lib = so
+    return _lib
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().ngdn_last_error().decode()
+        raise NgdnError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (or NULL for None)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def dims(B, T, H, L, K, V, dtype_code, scale):
+    return Dims(B, T, H, L, K, V, dtype_code, float(scale))

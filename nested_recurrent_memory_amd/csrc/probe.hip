@@ -1,0 +1,229 @@
+// Promotion probe: turn the level below into the pairs and gates this level
+// writes at one firing (nested_gdn2/ops/probe.py:34-136).
+//
+// learned (ops/probe.py:69-102):
+//   Vals = Bank[:N] S            [N,V]
+//   u    = Vals Wk^T             [N,K]   keys = u / max(|u|, 1e-12)
+//   b    = sigmoid(Vals Bp - 4)  [N,K]
+//   w    = sigmoid(Vals Wp)      [N,V]
+//   g    = -mean_n softplus(Vals Gp - 4)   [K]   (fp32)
+// merge (ops/probe.py:105-136): keys = I, Vals = S, same gates.
+//
+// The gathered state is the lower level's state after this level's firing
+// (ops/chunk.py:39-93). Outputs are written in the form the scan consumes:
+// A = keys*b*e^g, KT = keys^T, U = Vals*w, gam = e^g.
+// One workgroup per (batch, head, firing); the five N x K x V products run on
+// MFMA with the gates in fp32.
+#include "ngdn_kernels.h"
+
+namespace ngdn {
+
+template <typename E, int K, int N, bool MERGE>
+__global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
+  constexpr int V = K;
+  constexpr int LD = K + 8;
+  constexpr bool SEP = !std::is_same<E, float>::value;   // separate fp32 copy of Vals
+  constexpr int LDF = SEP ? V + 1 : LD;
+  constexpr int NKS = K / Mma<E>::KS;
+  constexpr int NTK = (N / 16) * (K / 16) / 4;             // [N,K] tiles per wave
+  typedef typename Mma<E>::Frag Frag;
+
+  constexpr size_t SZ_S = MERGE ? 0 : sizeof(E) * V * LD;
+  constexpr size_t SZ_VE = sizeof(E) * N * LD;
+  constexpr size_t SZ_VF = SEP ? sizeof(float) * N * LDF : 0;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_S + SZ_VE + SZ_VF + sizeof(float) * (N + K) + 16];
+  E* s_S = reinterpret_cast<E*>(smem);
+  E* s_VE = reinterpret_cast<E*>(smem + SZ_S);
+  float* s_Vf = SEP ? reinterpret_cast<float*>(smem + SZ_S + SZ_VE) : reinterpret_cast<float*>(s_VE);
+  float* s_nrm = reinterpret_cast<float*>(smem + SZ_S + SZ_VE + SZ_VF);
+  float* s_gs = s_nrm + N;
+
+  const int NF = a.NF, H = a.H;
+  const int i = blockIdx.x % NF;
+  const int bh = blockIdx.x / NF;
+  const int h = bh % H, b = bh / H;
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+
+  // ---- the gathered lower state
+  const int src = ((i + 1) * a.f_here) / a.f_below;
+  const bool fin = src >= a.NGb;
+  const float* Sf = nullptr;    // [K][V] fp32 source
+  const E* Sh = nullptr;        // [V][K] working-dtype source
+  if (fin) Sf = a.below_fin + b * a.bf_sb + h * a.bf_sh;
+  else if (a.below_mode == 1)
+    Sf = static_cast<const float*>(a.below) + (((size_t)b * a.NGb + src) * H + h) * K * V;
+  else
+    Sh = static_cast<const E*>(a.below) + (((size_t)b * H + h) * a.NGb + src) * V * K;
+
+  if (!MERGE) {
+    // S^T into LDS, k contiguous
+    if (Sh) {
+      for (int e = tid; e < V * K; e += 256) s_S[(e / K) * LD + e % K] = Sh[e];
+    } else {
+      for (int e = tid; e < V * K; e += 256) {
+        const int k = e / V, v = e % V;
+        s_S[v * LD + k] = from_f<E>(Sf[e]);
+      }
+    }
+  } else {
+    // Vals = S, row k
+    if (Sh) {
+      for (int e = tid; e < V * K; e += 256) {
+        const int v = e / K, k = e % K;
+        const float x = to_f(Sh[e]);
+        s_VE[k * LD + v] = from_f<E>(x);
+        if (SEP) s_Vf[k * LDF + v] = x;
+      }
+    } else {
+      for (int e = tid; e < V * K; e += 256) {
+        const int k = e / V, v = e % V;
+        const float x = Sf[e];
+        s_VE[k * LD + v] = from_f<E>(x);
+        if (SEP) s_Vf[k * LDF + v] = x;
+      }
+    }
+  }
+  for (int e = tid; e < N + K; e += 256) s_nrm[e] = 0.f;
+  __syncthreads();
+
+  const size_t fo = ((size_t)bh * NF + i);                 // scan-ready firing index
+  const size_t ro = (((size_t)b * NF + i) * H + h);        // reference-format index
+
+  // ---- Vals = Bank[:N] S
+  if (!MERGE) {
+    const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
+    for (int g = wv; g < (N / 16) * (V / 16); g += 4) {
+      const int rt = g / (V / 16), ct = g % (V / 16);
+      f4 acc = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_S + ct * 16 * LD, LD, K);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
+        s_VE[n * LD + v] = from_f<E>(acc[r]);
+        if (SEP) s_Vf[n * LDF + v] = acc[r];
+      }
+    }
+    __syncthreads();
+  }
+  if (a.vals) {
+    for (int e = tid; e < N * V; e += 256)
+      a.vals[ro * N * V + e] = s_Vf[(e / V) * LDF + e % V];
+  }
+
+  // ---- projections of Vals: A operand s_VE (reduce over V), B from global
+  auto proj_tile = [&](const E* Pt, int rt, int ct) -> f4 {
+    // Pt: [cols][V] with V contiguous
+    return mma_tile<E>(f4_zero(), s_VE + rt * 16 * LD, LD, Pt + (size_t)ct * 16 * V, V, V);
+  };
+  const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V;
+  const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V;
+  const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V;
+  const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V;
+
+  f4 ut[NTK], bt[NTK];
+#pragma unroll
+  for (int t = 0; t < NTK; ++t) {
+    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
+    // decay logits: column sums of softplus over the N pairs
+    {
+      f4 x = proj_tile(gpH, rt, ct);
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s += softplusf_(x[r] - 4.f);
+      s += __shfl_xor(s, 16, WAVE);
+      s += __shfl_xor(s, 32, WAVE);
+      if (lane < 16) atomicAdd(&s_gs[ct * 16 + lane], s);
+    }
+    // erase gate
+    {
+      f4 x = proj_tile(bpH, rt, ct);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bt[t][r] = sigmoidf_(x[r] - 4.f);
+    }
+    // write keys (learned)
+    if (!MERGE) {
+      ut[t] = proj_tile(kpH, rt, ct);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s = ut[t][r] * ut[t][r];
+        s += __shfl_xor(s, 1, WAVE);
+        s += __shfl_xor(s, 2, WAVE);
+        s += __shfl_xor(s, 4, WAVE);
+        s += __shfl_xor(s, 8, WAVE);
+        if ((lane & 15) == 0) atomicAdd(&s_nrm[rt * 16 + acc_row(r)], s);
+      }
+    }
+  }
+  // write gate, and U = Vals * w
+  {
+    E* Uo = static_cast<E*>(a.U) + fo * N * V;
+    for (int g = wv; g < (N / 16) * (V / 16); g += 4) {
+      const int rt = g / (V / 16), ct = g % (V / 16);
+      f4 x = proj_tile(wpH, rt, ct);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
+        const float w = sigmoidf_(x[r]);
+        Uo[n * V + v] = from_f<E>(s_Vf[n * LDF + v] * w);
+        if (a.wo) a.wo[ro * N * V + n * V + v] = w;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- finalize: g, keys, A = keys*b*e^g, KT = keys^T
+  if (tid < K) {
+    const float g = -s_gs[tid] / (float)N;
+    a.gam[fo * K + tid] = expf(g);
+    if (a.go) a.go[ro * K + tid] = g;
+  }
+  E* Ao = static_cast<E*>(a.A) + fo * N * K;
+  E* KTo = static_cast<E*>(a.KT) + fo * K * N;
+#pragma unroll
+  for (int t = 0; t < NTK; ++t) {
+    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
+    const int k = ct * 16 + acc_col();
+    const float gam = expf(-s_gs[k] / (float)N);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = rt * 16 + acc_row(r);
+      float key;
+      if (MERGE) key = (n == k) ? 1.f : 0.f;
+      else key = ut[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
+      Ao[n * K + k] = from_f<E>(key * bt[t][r] * gam);
+      KTo[k * N + n] = from_f<E>(key);
+      if (a.keys) a.keys[ro * N * K + n * K + k] = key;
+      if (a.bo) a.bo[ro * N * K + n * K + k] = bt[t][r];
+    }
+  }
+}
+
+template <typename E, int K, int N, bool MERGE>
+static hipError_t launch_probe(const ProbeArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * a.NF);
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((probe_fwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <typename E>
+static hipError_t probe_dispatch(const ProbeArgs& a, int K, hipStream_t st) {
+  if (a.V != K) return hipErrorInvalidValue;
+  if (a.merge) {
+    if (a.N != K) return hipErrorInvalidValue;
+    if (K == 64) return launch_probe<E, 64, 64, true>(a, st);
+    if (K == 128) return launch_probe<E, 128, 128, true>(a, st);
+    return hipErrorInvalidValue;
+  }
+#define NGDN_PR(KK, NN) \
+  if (K == KK && a.N == NN) return launch_probe<E, KK, NN, false>(a, st);
+  NGDN_PR(64, 16) NGDN_PR(64, 32) NGDN_PR(64, 64) NGDN_PR(64, 128)
+  NGDN_PR(128, 16) NGDN_PR(128, 32) NGDN_PR(128, 64) NGDN_PR(128, 128)
+#undef NGDN_PR
+  return hipErrorInvalidValue;
+}
+
+hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st) {
+  return dtype == NGDN_BF16 ? probe_dispatch<bf16>(a, K, st) : probe_dispatch<float>(a, K, st);
+}
+
+}  // namespace ngdn

@@ -1,0 +1,183 @@
+// The sequential half of every level: a chain of delta-rule steps
+//   Vn = U - A S,   S <- diag(gam) S + BT Vn
+// run per (batch, head, 32-column slice of V) with the fp32 state held in
+// registers across all steps.
+//
+// Level 0 (the state recurrence of fla's chunk_gdn2_fwd, reached from
+// nested_gdn2/ops/chunk.py:236-248; semantics ops/naive.py:367-392): one step
+// per chunk with A = W, BT = Kt^T, U = U, gam = e^gc_last.
+// Levels >= 1 (ops/update_fwd.py:21-128): one step per firing with
+// A = keys * b * e^g, BT = keys^T, U = values * w, gam = e^g, which is
+// S' = e^g S - keys^T ((keys*b)(e^g S)) + keys^T (values*w).
+//
+// Columns of V never interact, so a workgroup owns BV = 32 of them and the
+// grid is B*H*(V/32). Per step: the state slice is written (transposed, in the
+// working dtype) to LDS as the B operand of A S; Vn goes through LDS as the B
+// operand of BT Vn. A and BT fragments are read straight from global memory,
+// each wave reading the rows only it needs.
+#include "ngdn_kernels.h"
+
+namespace ngdn {
+
+template <typename E, int K, int M>
+__global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
+  constexpr int BV = 32;
+  constexpr int CT = BV / 16;                 // column tiles
+  constexpr int RTS = K / 16;                 // state row tiles
+  constexpr int TPW = RTS * CT / 4;           // state tiles per wave
+  constexpr int RTV = M / 16;                 // Vn row tiles
+  constexpr int LDS_ST = K + 8;
+  constexpr int LDS_VN = M + 8;
+  constexpr int NSM = (M + Mma<E>::KS - 1) / Mma<E>::KS;   // k-steps over M
+  constexpr bool PADM = (M % Mma<E>::KS) != 0;
+  typedef typename Mma<E>::Frag Frag;
+  __shared__ __attribute__((aligned(16))) E s_ST[BV * LDS_ST];
+  __shared__ __attribute__((aligned(16))) E s_VnT[BV * LDS_VN];
+
+  const int V = a.V, S = a.S, H = a.H;
+  const int nvt = V / BV;
+  const int vt = blockIdx.x % nvt;
+  const int bh = blockIdx.x / nvt;
+  const int h = bh % H, b = bh / H;
+  const int v0 = vt * BV;
+  const int lane = lane_id(), wv = wave_id();
+
+  // state tiles of this wave: rt = g / CT, ct = g % CT
+  f4 st[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = rt * 16 + acc_row(r), v = v0 + ct * 16 + acc_col();
+      st[i][r] = a.init ? a.init[b * a.init_sb + h * a.init_sh + (long long)k * V + v] : 0.f;
+    }
+  }
+
+  const E* Ab = static_cast<const E*>(a.A) + (size_t)bh * S * M * K;
+  const E* Bb = static_cast<const E*>(a.BT) + (size_t)bh * S * K * M;
+  const E* Ub = static_cast<const E*>(a.U) + (size_t)bh * S * M * V;
+  const float* Gb = a.gam + (size_t)bh * S * K;
+
+  auto store_state = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col(), v = v0 + vl;
+      if (a.state_mode == 0) {
+        E* hp = static_cast<E*>(a.states) + (((size_t)bh * S + j) * V + v) * K + k0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hp[r] = from_f<E>(st[i][r]);
+      } else {
+        float* sp = static_cast<float*>(a.states) + (((size_t)b * a.NG + j) * H + h) * K * V;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sp[(size_t)(k0 + r) * V + v] = st[i][r];
+      }
+    }
+  };
+
+  for (int j = 0; j < S; ++j) {
+    // ---- state entering step j: to global and (transposed) to LDS
+    store_state(j);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_ST[vl * LDS_ST + k0 + r] = from_f<E>(st[i][r]);
+    }
+    __syncthreads();
+
+    // ---- Vn = U - A S
+    const E* Aj = Ab + (size_t)j * M * K;
+    const E* Uj = Ub + (size_t)j * M * V;
+    for (int rt = wv; rt < RTV; rt += 4) {
+      Frag af[K / Mma<E>::KS];
+      const E* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < K / Mma<E>::KS; ++s) af[s] = Mma<E>::load(arow + s * Mma<E>::KS);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        f4 acc = f4_zero();
+        const E* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < K / Mma<E>::KS; ++s)
+          acc = Mma<E>::mma(acc, af[s], Mma<E>::load(brow + s * Mma<E>::KS));
+        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+        float vn[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          vn[r] = to_f(Uj[(size_t)(m0 + r) * V + v0 + vl]) - acc[r];
+          s_VnT[vl * LDS_VN + m0 + r] = from_f<E>(vn[r]);
+        }
+        if (a.vnT) {
+          E* vp = static_cast<E*>(a.vnT) + (((size_t)bh * S + j) * V + v0 + vl) * M + m0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vp[r] = from_f<E>(vn[r]);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- S <- diag(gam) S + BT Vn
+    const E* Bj = Bb + (size_t)j * K * M;
+    const float* Gj = Gb + (size_t)j * K;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[i][r] *= Gj[rt * 16 + acc_row(r)];
+      const E* arow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      const E* brow = s_VnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < NSM; ++s) {
+        // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
+        const bool live = !PADM || (s * Mma<E>::KS + kofs<E>(lane) < M);
+        Frag fa = Mma<E>::make([](int) { return 0.f; }), fb = fa;
+        if (live) {
+          fa = Mma<E>::load(arow + s * Mma<E>::KS);
+          fb = Mma<E>::load(brow + s * Mma<E>::KS);
+        }
+        st[i] = Mma<E>::mma(st[i], fa, fb);
+      }
+    }
+    // no barrier needed here: the next writes to s_ST do not alias s_VnT, and
+    // the next writes to s_VnT follow the next step's barrier
+  }
+  if (a.state_mode == 1) {
+    for (int j = S; j < a.NG; ++j) store_state(j);
+  }
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = rt * 16 + acc_row(r), v = v0 + ct * 16 + acc_col();
+      a.fin[b * a.fin_sb + h * a.fin_sh + (long long)k * V + v] = st[i][r];
+    }
+  }
+}
+
+template <typename E, int K, int M>
+static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * (a.V / 32));
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st) {
+  if (a.V % 32 != 0) return hipErrorInvalidValue;
+#define NGDN_SC(E, KK, MM) \
+  if (K == KK && a.M == MM) return launch_scan<E, KK, MM>(a, st);
+#define NGDN_SC_K(E, KK) NGDN_SC(E, KK, 16) NGDN_SC(E, KK, 32) NGDN_SC(E, KK, 64) NGDN_SC(E, KK, 128)
+  if (dtype == NGDN_BF16) {
+    NGDN_SC_K(bf16, 64) NGDN_SC_K(bf16, 128)
+  } else {
+    NGDN_SC_K(float, 64) NGDN_SC_K(float, 128)
+  }
+#undef NGDN_SC_K
+#undef NGDN_SC
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ngdn

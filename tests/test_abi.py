@@ -1,0 +1,73 @@
+"""CPU-side checks of the C ABI: the library loads and exports every entry
+point include/ngdn.h declares; argument validation runs before any launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from nested_recurrent_memory_amd import _lib, chunk_nested_gdn2
+from nested_recurrent_memory_amd.inputs import NAMES, make_inputs
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "ngdn.h")).read()
+    return sorted(set(re.findall(r"\b(ngdn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "ngdn_last_error" in names and "ngdn_l0_intra_fwd" in names
+    # every declared symbol has a ctypes signature on the Python side
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    so = _lib.lib()
+    for name in _declared():
+        assert hasattr(so, name), name
+    assert so.ngdn_arch() == b"gfx950"
+    assert so.ngdn_version() >= 100
+
+
+def test_invalid_arguments_return_error_without_launch():
+    so = _lib.lib()
+    d = _lib.dims(1, 64, 1, 1, 96, 64, _lib.NGDN_BF16, 0.1)   # K=96 unsupported
+    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 12), None)
+    assert rc == 1
+    assert b"K=96" in so.ngdn_last_error()
+    d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
+    rc = so.ngdn_probe_fwd(ctypes.byref(d), 1, 0, 24, 1, 2, None, 0, None, None, 32,
+                           *([None] * 14))
+    assert rc == 1 and b"power of two" in so.ngdn_last_error()
+
+
+def _base(**kw):
+    cfg = dict(B=1, T=256, H=2, K=64, V=64, L=2, N=32, intervals=(1, 2))
+    cfg.update(kw)
+    inp = make_inputs(**cfg)
+    return {n: inp[n] for n in NAMES}, cfg["L"]
+
+
+@pytest.mark.parametrize("bad_bt", [16, 32, 128])
+def test_rejects_non_64_chunk_size(bad_bt):
+    inp, L = _base()
+    with pytest.raises((ValueError, AssertionError)):
+        chunk_nested_gdn2(**inp, L=L, chunk_size=bad_bt)
+
+
+@pytest.mark.parametrize("bad", [4, 8, 24])
+def test_rejects_bad_n_queries(bad):
+    inp, L = _base(n_queries=(bad,))
+    with pytest.raises(ValueError, match="power of two"):
+        chunk_nested_gdn2(**inp, L=L, chunk_size=64)
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    inp, L = _base()
+    with pytest.raises(RuntimeError, match="GPU"):
+        chunk_nested_gdn2(**inp, L=L)

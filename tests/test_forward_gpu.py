@@ -1,0 +1,144 @@
+"""Forward parity of the HIP path against the CPU oracle (float64).
+
+Tolerances (written into every assertion): fp32 inputs 1e-5; bf16 inputs
+max-abs 2e-3 / rel 1e-2 against the fp32-or-better oracle on identical inputs.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import _golden
+import ngdn_oracle as ref
+from nested_recurrent_memory_amd import _lib, chunk_nested_gdn2
+from nested_recurrent_memory_amd.inputs import NAMES, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-5, atol=1e-5),
+       torch.bfloat16: dict(rtol=1e-2, atol=2e-3)}
+
+
+def _gpu(inp):
+    return {n: inp[n].to("cuda") for n in NAMES}
+
+
+def _oracle(inp, L, promotion="learned", init=None):
+    return ref.chunk_forward(*[inp[n] for n in NAMES], L=L, initial_state=init,
+                             output_final_state=True, promotion=promotion,
+                             out_dtype=torch.float64)
+
+
+# ------------------------------------------------------------- level-0 chunk terms
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("K,V,T,g_scale", [(64, 64, 192, 0.1), (128, 128, 130, 1.0),
+                                           (64, 128, 128, 30.0), (128, 64, 64, 2.0)])
+def test_l0_intra_terms(dtype, K, V, T, g_scale):
+    print(f"l0_intra dtype={dtype} K={K} V={V} T={T} g_scale={g_scale}", flush=True)
+    B, H, L = 2, 2, 1
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=V, L=L, N=16, intervals=(1,), dtype=dtype,
+                      g_scale=g_scale)
+    NT = -(-T // 64)
+    scale = K ** -0.5
+    code = _lib.NGDN_BF16 if dtype == torch.bfloat16 else _lib.NGDN_F32
+    g = {n: inp[n].to("cuda").contiguous() for n in ("q", "k", "v", "g", "b", "w")}
+    e = lambda *s, dt=dtype: torch.empty(*s, device="cuda", dtype=dt)  # noqa: E731
+    out = dict(W=e(B, H, NT, 64, K), U=e(B, H, NT, 64, V), KtT=e(B, H, NT, K, 64),
+               Qg=e(B, H, NT, 64, K), Aqk=e(B, H, NT, 64, 64), gam=e(B, H, NT, K, dt=torch.float32))
+    d = _lib.dims(B, T, H, L, K, V, code, scale)
+    P = _lib.ptr
+    _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(g[n]) for n in ("q", "k", "v", "g", "b", "w")),
+              *(P(out[n]) for n in ("W", "U", "KtT", "Qg", "Aqk", "gam")), _lib.stream_of(g["q"]))
+    torch.cuda.synchronize()
+
+    pad = NT * 64 - T
+
+    def prep(x):
+        x = x.double().transpose(1, 2)
+        if pad:
+            x = torch.nn.functional.pad(x, (0, 0) * (x.dim() - 3) + (0, pad))
+        return x.reshape(B, H, NT, 64, *x.shape[3:])
+    t = ref.l0_chunk_terms(prep(inp["q"])[..., 0, :], prep(inp["k"]), prep(inp["v"]),
+                           prep(inp["g"]), prep(inp["b"]), prep(inp["w"]), scale)
+    tol = TOL[dtype]
+    got = {n: out[n].double().cpu() for n in out}
+    torch.testing.assert_close(got["gam"], t["gam"], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(got["Aqk"], t["Aqk"], **tol)
+    torch.testing.assert_close(got["Qg"], t["Qg"], **tol)
+    torch.testing.assert_close(got["KtT"], t["Kt"].transpose(-1, -2), **tol)
+    torch.testing.assert_close(got["W"], t["W"], **tol)
+    torch.testing.assert_close(got["U"], t["U"], **tol)
+
+
+# ------------------------------------------------------------- whole forward
+
+#  B,   T, H,   K, L,  N, firing,    n_queries
+CASES = [
+    (1, 128, 2, 64, 2, 16, (1, 2), None),
+    (2, 256, 2, 64, 2, 16, (1, 2), None),
+    (1, 256, 4, 64, 2, 32, (1, 4), None),
+    (2, 512, 2, 64, 3, 16, (1, 2, 4), None),
+    (1, 512, 2, 64, 3, 32, (1, 2, 4), (32, 16)),
+    (1, 256, 2, 128, 2, 16, (1, 2), None),
+    (1, 256, 2, 64, 2, 16, (1, 1), None),
+    (1, 320, 2, 64, 3, 16, (1, 2, 3), None),
+    (1, 200, 2, 64, 3, 16, (1, 2, 4), None),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("promotion", ["learned", "merge"])
+@pytest.mark.parametrize("B,T,H,K,L,N,firing,nq", CASES)
+def test_forward_matches_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
+    print(f"forward B={B} T={T} H={H} K={K} L={L} N={N} f={firing} nq={nq} "
+          f"{promotion} {dtype}", flush=True)
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=K, L=L, N=N, intervals=firing, n_queries=nq,
+                      dtype=dtype, g_scale=1.0, style="reftest")
+    o, s = chunk_nested_gdn2(**_gpu(inp), L=L, output_final_state=True, promotion=promotion)
+    o_ref, s_ref = _oracle(inp, L, promotion)
+    torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[dtype])
+    torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("promotion", ["learned", "merge"])
+def test_forward_with_initial_state(dtype, promotion):
+    inp = make_inputs(B=2, T=256, H=2, K=64, V=64, L=3, N=16, intervals=(1, 2, 4),
+                      dtype=dtype, g_scale=0.5)
+    gen = torch.Generator().manual_seed(5)
+    init = torch.randn(2, 2, 3, 64, 64, generator=gen) * 0.1
+    o, s = chunk_nested_gdn2(**_gpu(inp), L=3, initial_state=init.cuda(),
+                             output_final_state=True, promotion=promotion)
+    o_ref, s_ref = _oracle(inp, 3, promotion, init=init.double())
+    torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[dtype])
+    torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[dtype])
+
+
+@pytest.mark.parametrize("name", ["c0", "l3_learned", "l3_merge", "l2_bf16"])
+def test_forward_golden(name):
+    """Against the vectors the reference's own naive op produced (float32)."""
+    cfg, inp, init, promotion, exp, _ = _golden.load(name)
+    o, s = chunk_nested_gdn2(**_gpu(inp), L=cfg["L"],
+                             initial_state=init.cuda() if init is not None else None,
+                             output_final_state=True, promotion=promotion)
+    tol = TOL[cfg["dtype"]]
+    if exp["o"].dtype == torch.bfloat16:
+        # both sides round to bf16 once; allow one bf16 ulp beyond the tolerance
+        torch.testing.assert_close(o.float().cpu(), exp["o"].float(), rtol=1.5e-2, atol=2e-3)
+    else:
+        torch.testing.assert_close(o.float().cpu(), exp["o"], **tol)
+    torch.testing.assert_close(s.cpu(), exp["final_state"], **tol)
+
+
+def test_l1_config0_and_large_decay():
+    """Config 0 (single level, fp32) and the reference's large-decay regime."""
+    for g_scale in (0.1, 16.0):
+        inp = make_inputs(B=1, T=512, H=2, K=64, V=64, L=1, N=16, intervals=(1,),
+                          dtype=torch.float32, g_scale=g_scale)
+        o, s = chunk_nested_gdn2(**_gpu(inp), L=1, output_final_state=True)
+        o_ref, s_ref = _oracle(inp, 1)
+        assert torch.isfinite(o).all() and torch.isfinite(s).all()
+        torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[torch.float32])
+        torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[torch.float32])
