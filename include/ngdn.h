@@ -50,11 +50,15 @@ const char* ngdn_arch(void);
  * called at nested_gdn2/ops/chunk.py:236-248 (semantics ops/naive.py:329-358).
  * Outputs (working dtype unless noted): W [B,H,NT,64,K], U [B,H,NT,64,V],
  * KtT [B,H,NT,K,64], Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64],
- * gam [B,H,NT,K] fp32. */
+ * gam [B,H,NT,K] fp32. Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64]
+ * and AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
+ * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
+ * may be NULL (inference). */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, void* W, void* U, void* KtT, void* Qg,
-                          void* Aqk, float* gam, void* stream);
+                          void* Aqk, float* gam, void* Kt, void* WT, void* QgT,
+                          void* AqkT, void* TT, void* stream);
 
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
@@ -76,7 +80,8 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
  * their last two axes swapped. promotion: 0 learned, 1 merge (n_queries = K).
  * Outputs for firing i in [0, NF), NF = NT / f_here, laid out [B,H,NF,...]:
  * A = keys*b*e^g [N,K], KT = keys^T [K,N], U = values*w [N,V] (working dtype),
- * gam = e^g [K] fp32. keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
+ * gam = e^g [K] fp32; for the backward, keysN = keys [N,K] and AT = A^T
+ * [K,N] (may be NULL). keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
  * receive the probe outputs in the reference layout when not NULL. */
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
@@ -84,9 +89,9 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
-                       void* A, void* KT, void* U, float* gam, float* keys,
-                       float* vals, float* bo, float* wo, float* go,
-                       void* stream);
+                       void* A, void* KT, void* U, float* gam, void* keysN,
+                       void* AT, float* keys, float* vals, float* bo, float* wo,
+                       float* go, void* stream);
 
 /* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
  * probe's scan-ready pairs: NF firings, NG = ceil(NT / f) stored group
@@ -110,6 +115,102 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
                         const void* mix, const float* const* states,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* reads, void* stream);
+
+/* ---------------------------------------------------------------- backward
+ * The backward of ChunkNestedGDN2Function (ops/chunk.py:650-719,
+ * chunk_nested_gdn2_bwd :374-564), one entry point per stage. */
+
+/* Output backward per chunk (ops/chunk.py:423-449): dmix for every level
+ * (fp32 [B,T,H,L]) and dq[..., l, :] for l >= 1 (working dtype [B,T,H,L,K]);
+ * inputs as for ngdn_output_fwd plus do [B,T,H,V]. */
+int32_t ngdn_output_bwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
+                        const void* hT, const void* vnT, const void* q,
+                        const void* mix, const float* const* states,
+                        const int32_t* ng, const int32_t* f, const void* dout,
+                        void* dq, float* dmix, void* stream);
+
+/* Read gradient of level `level`'s group states (read_level_bwd,
+ * ops/chunk.py:307-336): d_states fp32 [B,ng,H,K,V], written. */
+int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
+                            int32_t ng, const void* q, const void* mix,
+                            const void* dout, float* d_states, void* stream);
+
+/* Reverse level-0 state recurrence (the vendored fla dh kernel with dh_ext,
+ * ops/_vendor/common_chunk_delta_h.py:25-380). Kt [B,H,NT,64,K],
+ * WT/QgT [B,H,NT,K,64], AqkT [B,H,NT,64,64] from ngdn_l0_intra_fwd; inj
+ * (fp32 [B,H,nf1,K,V], may be NULL) is level 1's gradient of the state
+ * entering chunk (i+1)*f1, added before that chunk's step (the reference's
+ * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
+ * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
+ * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (working dtype), and
+ * d_initial[:, :, 0] when not NULL. */
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
+                         const float* gam, const void* AqkT, const void* QgT,
+                         const void* dout, const void* mix, int32_t f1,
+                         const float* inj, int32_t nf1, const float* d_final,
+                         void* dSp, void* dVn, void* dVnT, float* d_initial,
+                         void* stream);
+
+/* Reverse write scan of level `level` >= 1 (ops/update_bwd.py:19-164): keys
+ * [B,H,NF,N,K] and AT = (keys*b*e^g)^T [B,H,NF,K,N] from ngdn_probe_fwd, gam
+ * [B,H,NF,K]; d_states fp32 [B,NG,H,K,V] (read gradients plus the level
+ * above's scatter); d_final [B,H,L,K,V]. Writes dSp fp32 [B,H,NF,K,V], dvn
+ * fp32 [B,H,NF,N,V] and d_initial[:, :, level] when not NULL. */
+int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
+                            int32_t nf, int32_t ng, const void* keys,
+                            const void* AT, const float* gam,
+                            const float* d_states, const float* d_final,
+                            float* dSp, float* dvn, float* d_initial,
+                            void* stream);
+
+/* Level-0 chunk backward, state half: dQg, dKt [B,H,NT,64,K], dWT
+ * [B,H,NT,K,64], dAqk [B,H,NT,64,64] (working dtype), dgam fp32 [B,H,NT,K]. */
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const void* hT, const void* dSp,
+                          const void* vnT, const void* dVn, const void* dout,
+                          const void* mix, void* dQg, void* dWT, void* dKt,
+                          void* dAqk, float* dgam, void* stream);
+
+/* Level-0 chunk backward, intra half: writes dq[..., 0, :], dk, dv, db, dw
+ * (working dtype) and dg (fp32 [B,T,H,K]). W, U, TT from ngdn_l0_intra_fwd. */
+int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
+                          const void* v, const float* g, const void* b,
+                          const void* w, const void* W, const void* U,
+                          const void* TT, const void* dQg, const void* dWT,
+                          const void* dKt, const void* dAqk, const float* dgam,
+                          const void* dVnT, void* dq, void* dk, void* dv,
+                          float* dg, void* db, void* dw, void* stream);
+
+/* Backward of level `level`'s firings through its update and probe.
+ * Sources/parameters as for ngdn_probe_fwd plus kpT [L-1,H,V,K] (key
+ * projections transposed), bankT [L-1,H,K,n_max] (banks transposed), and the
+ * untransposed bp, gp [L-1,H,V,K], wp [L-1,H,V,V]. states fp32 [B,ng,H,K,V]
+ * are this level's group states; dSp, dvn from ngdn_upper_scan_bwd.
+ * Workspace (working dtype): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K],
+ * ws_dxw, ws_dvals [B,H,NF,N,V]. dbank fp32 [L-1,H,n_max,K] accumulates. The
+ * gradient of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is
+ * added to d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
+int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
+                       int32_t n_queries, int32_t f_below, int32_t f_here,
+                       const void* below, int32_t ng_below,
+                       const float* final_state, const void* query_banks,
+                       int32_t n_max, const void* key_projections,
+                       const void* bpT, const void* wpT, const void* gpT,
+                       const void* kpT, const void* bankT, const void* bp,
+                       const void* wp, const void* gp, const float* states,
+                       int32_t ng, const float* dSp, const float* dvn,
+                       void* ws_vals, void* ws_du, void* ws_dxb, void* ws_dxg,
+                       void* ws_dxw, void* ws_dvals, float* dbank, float* inj,
+                       float* d_below, float* d_final, void* stream);
+
+/* Per-head parameter gradients of level `level` summed over all its firings
+ * (the leaf gradients of the probe replay, ops/chunk.py:502-517), from the
+ * workspace of ngdn_probe_bwd; accumulated into fp32 dkp [L-1,H,K,V] (learned
+ * only), dbp [L-1,H,V,K], dwp [L-1,H,V,V], dgp [L-1,H,V,K]. */
+int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
+                         int32_t n_pairs, int32_t nf, const void* ws_vals,
+                         const void* ws_du, const void* ws_dxb,
+                         const void* ws_dxg, const void* ws_dxw, float* dkp,
+                         float* dbp, float* dwp, float* dgp, void* stream);
 
 #ifdef __cplusplus
 }

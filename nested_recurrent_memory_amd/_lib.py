@@ -29,17 +29,26 @@ P = ctypes.c_void_p
 I32 = ctypes.c_int32
 PD = ctypes.POINTER(Dims)
 
-# name -> argtypes (all return int32 status unless listed in _RESTYPES)
+# name -> argtypes (all return an int32 status unless listed in _RESTYPES)
 SIGNATURES = {
     "ngdn_last_error": [],
     "ngdn_version": [],
     "ngdn_arch": [],
-    "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P],
+    "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P] * 5 + [P],
     "ngdn_l0_scan_fwd": [PD, P, P, P, P, P, P, P, P, P],
-    "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P,
-                       P, P, P, P, P, P, P, P, P, P],
+    "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
+                      + [P] * 11 + [P],
     "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_output_fwd": [PD, P, P, P, P, P, P, P, P, P, P, P, P],
+    "ngdn_output_bwd": [PD] + [P] * 9 + [P, P, P] + [P],
+    "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P],
+    "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, P],
+    "ngdn_upper_scan_bwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
+    "ngdn_l0_bwd_state": [PD] + [P] * 6 + [P] * 5 + [P],
+    "ngdn_l0_bwd_intra": [PD] + [P] * 6 + [P] * 3 + [P] * 6 + [P] * 6 + [P],
+    "ngdn_probe_bwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P,
+                       P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
+    "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
 }
 _RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}
 

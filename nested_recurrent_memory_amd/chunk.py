@@ -78,9 +78,9 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
 
 
 def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
-             init, promotion):
+             init, promotion, train):
     """Runs the forward kernels. Returns (o, final_state [B,H,L,K,V] fp32,
-    saved working tensors)."""
+    working tensors kept for the backward when ``train``)."""
     B, T, H, _, K = q.shape
     V = v.shape[-1]
     dev = q.device
@@ -94,51 +94,172 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     st = _lib.stream_of(q_)
     P = _lib.ptr
     e = lambda *s, dt=wd: torch.empty(*s, device=dev, dtype=dt)  # noqa: E731
+    opt = lambda *s: e(*s) if train else None  # noqa: E731
 
     W, U, Qg = e(B, H, NT, 64, K), e(B, H, NT, 64, V), e(B, H, NT, 64, K)
     KtT, Aqk = e(B, H, NT, K, 64), e(B, H, NT, 64, 64)
     gam = e(B, H, NT, K, dt=torch.float32)
+    Kt, WT, QgT = opt(B, H, NT, 64, K), opt(B, H, NT, K, 64), opt(B, H, NT, K, 64)
+    AqkT, TT = opt(B, H, NT, 64, 64), opt(B, H, NT, 64, 64)
     _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
-              P(W), P(U), P(KtT), P(Qg), P(Aqk), P(gam), st)
+              P(W), P(U), P(KtT), P(Qg), P(Aqk), P(gam), P(Kt), P(WT), P(QgT), P(AqkT),
+              P(TT), st)
     hT, vnT = e(B, H, NT, V, K), e(B, H, NT, V, 64)
     final = torch.empty(B, H, L, K, V, device=dev, dtype=torch.float32)
     _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), P(W), P(U), P(KtT), P(gam), P(init_),
               P(hT), P(vnT), P(final), st)
 
     states = [None] * L
+    levels = [None] * L
     merge = promotion == "merge"
+    par = {}
     if L > 1:
-        qb_, kp_ = cvt(qb), cvt(kp)
-        bpT = bp.to(wd).transpose(-1, -2).contiguous()
-        wpT = wp.to(wd).transpose(-1, -2).contiguous()
-        gpT = gp.to(wd).transpose(-1, -2).contiguous()
+        par = _params(qb, kp, bp, wp, gp, wd, train)
     for lvl in range(1, L):
         fh, fb = f[lvl], f[lvl - 1]
         nf, ng = n_firings(NT, fh), n_groups(NT, fh)
         N = K if merge else nq[lvl - 1]
-        A_ = e(B, H, max(nf, 1), N, K)
-        KT_ = e(B, H, max(nf, 1), K, N)
-        U_ = e(B, H, max(nf, 1), N, V)
-        gm_ = e(B, H, max(nf, 1), K, dt=torch.float32)
+        nf1 = max(nf, 1)
+        A_, KT_, U_ = e(B, H, nf1, N, K), e(B, H, nf1, K, N), e(B, H, nf1, N, V)
+        gm_ = e(B, H, nf1, K, dt=torch.float32)
+        keysN, AT_ = opt(B, H, nf1, N, K), opt(B, H, nf1, K, N)
         below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
         if nf > 0:
             _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
-                      P(below), ngb, P(final), P(qb_), qb_.shape[2], P(kp_),
-                      P(bpT), P(wpT), P(gpT), P(A_), P(KT_), P(U_), P(gm_),
-                      None, None, None, None, None, st)
+                      P(below), ngb, P(final), P(par["qb"]), par["nmax"], P(par["kp"]),
+                      P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(A_), P(KT_), P(U_),
+                      P(gm_), P(keysN), P(AT_), None, None, None, None, None, st)
         S_l = torch.empty(B, ng, H, K, V, device=dev, dtype=torch.float32)
         _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, N, nf, ng, P(A_), P(KT_),
                   P(U_), P(gm_), P(init_), P(S_l), P(final), st)
         states[lvl] = S_l
+        levels[lvl] = dict(N=N, nf=nf, ng=ng, keys=keysN, AT=AT_, gam=gm_)
 
     o = e(B, T, H, V)
+    sp, ngs, fs = _level_arrays(states, NT, f, L)
+    _lib.call("ngdn_output_fwd", ctypes.byref(d), P(Qg), P(Aqk), P(hT), P(vnT), P(q_),
+              P(mix_), sp, ngs, fs, P(o), None, st)
+    saved = None
+    if train:
+        saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
+                     KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
+                     hT=hT, vnT=vnT, states=states, levels=levels, final=final, par=par,
+                     code=code, wd=wd)
+    return o, final, saved
+
+
+def _params(qb, kp, bp, wp, gp, wd, train):
+    """Per-level parameters in the layouts the kernels read: originals, the
+    projections with their last two axes swapped, and (for the backward) the
+    bank and key projections transposed. The bank is padded to a multiple of
+    8 rows so every row start is 16-byte aligned."""
+    nmax = qb.shape[2]
+    nmax8 = -(-nmax // 8) * 8
+    qb_ = qb.to(wd)
+    if nmax8 != nmax:
+        qb_ = torch.nn.functional.pad(qb_, (0, 0, 0, nmax8 - nmax))
+    t = lambda x: x.to(wd).transpose(-1, -2).contiguous()  # noqa: E731
+    par = dict(qb=qb_.contiguous(), nmax=nmax8, kp=kp.to(wd).contiguous(),
+               bpT=t(bp), wpT=t(wp), gpT=t(gp))
+    if train:
+        par.update(kpT=t(kp), bankT=t(qb_), bp=bp.to(wd).contiguous(),
+                   wp=wp.to(wd).contiguous(), gp=gp.to(wd).contiguous())
+    return par
+
+
+def _level_arrays(states, NT, f, L):
     sp = (ctypes.c_void_p * L)(*([None] + [s.data_ptr() for s in states[1:]]))
     ngs = (ctypes.c_int32 * L)(*([0] + [n_groups(NT, f[l]) for l in range(1, L)]))
     fs = (ctypes.c_int32 * L)(*f)
-    _lib.call("ngdn_output_fwd", ctypes.byref(d), P(Qg), P(Aqk), P(hT), P(vnT), P(q_),
-              P(mix_), sp, ngs, fs, P(o), None, st)
-    saved = dict(W=W, U=U, Qg=Qg, KtT=KtT, Aqk=Aqk, gam=gam, hT=hT, vnT=vnT, states=states)
-    return o, final, saved
+    return sp, ngs, fs
+
+
+def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
+    """Runs the backward kernels (ops/chunk.py:374-564, mirrored). Returns the
+    gradients in the working dtype (fp32 for g, the states and parameters)."""
+    q_, k_, v_, b_, w_, mix_, g_ = (sv[n] for n in ("q", "k", "v", "b", "w", "mix", "g"))
+    B, T, H, _, K = q_.shape
+    V = v_.shape[-1]
+    dev = q_.device
+    wd, code = sv["wd"], sv["code"]
+    NT = -(-T // 64)
+    d = _lib.dims(B, T, H, L, K, V, code, scale)
+    st = _lib.stream_of(q_)
+    P = _lib.ptr
+    e = lambda *s, dt=wd: torch.empty(*s, device=dev, dtype=dt)  # noqa: E731
+    z32 = lambda *s: torch.zeros(*s, device=dev, dtype=torch.float32)  # noqa: E731
+    do_ = do.to(wd).contiguous()
+    merge = promotion == "merge"
+    states, levels, par, final = sv["states"], sv["levels"], sv["par"], sv["final"]
+
+    # reads: dmix for every level, dq for levels >= 1
+    dq = e(B, T, H, L, K)
+    dmix = e(B, T, H, L, dt=torch.float32)
+    sp, ngs, fs = _level_arrays(states, NT, f, L)
+    _lib.call("ngdn_output_bwd", ctypes.byref(d), P(sv["Qg"]), P(sv["Aqk"]), P(sv["hT"]),
+              P(sv["vnT"]), P(q_), P(mix_), sp, ngs, fs, P(do_), P(dq), P(dmix), st)
+
+    d_final = (dfinal.to(torch.float32).contiguous().clone() if dfinal is not None
+               else z32(B, H, L, K, V))
+    d_init = z32(B, H, L, K, V) if has_init else None
+    d_states = [None] * L
+    for lvl in range(1, L):
+        ng = n_groups(NT, f[lvl])
+        d_states[lvl] = e(B, ng, H, K, V, dt=torch.float32)
+        _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng, P(q_), P(mix_),
+                  P(do_), P(d_states[lvl]), st)
+
+    dqb = dkp = dbp = dwp = dgp = None
+    inj, nf1 = None, 0
+    if L > 1:
+        nmax8 = par["nmax"]
+        dqb = z32(L - 1, H, nmax8, K)
+        dkp, dbp = z32(L - 1, H, K, V), z32(L - 1, H, V, K)
+        dwp, dgp = z32(L - 1, H, V, V), z32(L - 1, H, V, K)
+    for lvl in range(L - 1, 0, -1):
+        lv = levels[lvl]
+        N, nf, ng = lv["N"], lv["nf"], lv["ng"]
+        nfa = max(nf, 1)
+        dSp = e(B, H, nfa, K, V, dt=torch.float32)
+        dvn = e(B, H, nfa, N, V, dt=torch.float32)
+        _lib.call("ngdn_upper_scan_bwd", ctypes.byref(d), lvl, N, nf, ng, P(lv["keys"]),
+                  P(lv["AT"]), P(lv["gam"]), P(d_states[lvl]), P(d_final), P(dSp), P(dvn),
+                  P(d_init), st)
+        if nf == 0:
+            continue
+        ws = [e(B, H, nf, N, K) for _ in range(4)] + [e(B, H, nf, N, V) for _ in range(2)]
+        fh, fb = f[lvl], f[lvl - 1]
+        if lvl == 1:
+            inj, nf1 = e(B, H, nf, K, V, dt=torch.float32), nf
+            below, ngb, d_below = sv["hT"], NT, None
+        else:
+            below, ngb, d_below = states[lvl - 1], n_groups(NT, fb), d_states[lvl - 1]
+        _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh, P(below), ngb,
+                  P(final), P(par["qb"]), par["nmax"], P(par["kp"]), P(par["bpT"]),
+                  P(par["wpT"]), P(par["gpT"]), P(par["kpT"]), P(par["bankT"]), P(par["bp"]),
+                  P(par["wp"]), P(par["gp"]), P(states[lvl]), ng, P(dSp), P(dvn),
+                  *(P(x) for x in ws), P(dqb), P(inj if lvl == 1 else None), P(d_below),
+                  P(d_final), st)
+        _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf, P(ws[0]),
+                  P(ws[1]), P(ws[2]), P(ws[3]), P(ws[4]), P(dkp), P(dbp), P(dwp), P(dgp), st)
+
+    # level 0
+    dSp0, dVn0, dVnT0 = e(B, H, NT, K, V), e(B, H, NT, 64, V), e(B, H, NT, V, 64)
+    _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), P(sv["Kt"]), P(sv["WT"]), P(sv["gam"]),
+              P(sv["AqkT"]), P(sv["QgT"]), P(do_), P(mix_), f[1] if L > 1 else 1, P(inj), nf1,
+              P(d_final), P(dSp0), P(dVn0), P(dVnT0), P(d_init), st)
+    dQg, dKt, dWT = e(B, H, NT, 64, K), e(B, H, NT, 64, K), e(B, H, NT, K, 64)
+    dAqk, dgam = e(B, H, NT, 64, 64), e(B, H, NT, K, dt=torch.float32)
+    _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(sv["hT"]), P(dSp0), P(sv["vnT"]), P(dVn0),
+              P(do_), P(mix_), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam), st)
+    dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
+    dg = e(B, T, H, K, dt=torch.float32)
+    _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
+              P(sv["W"]), P(sv["U"]), P(sv["TT"]), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam),
+              P(dVnT0), P(dq), P(dk), P(dv), P(dg), P(db), P(dw), st)
+    if dqb is not None:
+        dqb = dqb[:, :, :par["qb"].shape[2]]
+    return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
 
 
 class ChunkNestedGDN2Function(torch.autograd.Function):
@@ -158,21 +279,39 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         K = q.shape[-1]
         if scale is None:
             scale = K ** -0.5
+        # the backward's extra layouts are written only when a gradient is wanted
+        train = any(ctx.needs_input_grad)
         o, final, saved = _forward(q, k, v, g, b, w, mix_weights, query_banks,
                                    key_projections, b_projections, w_projections,
                                    g_projections, nq, f, L, scale, initial_state,
-                                   promotion)
+                                   promotion, train)
         o = o.to(q.dtype)
         ctx.meta = (L, scale, f, nq, initial_state is not None, promotion)
-        ctx.save_for_backward(q, k, v, g, b, w, mix_weights, query_banks,
-                              key_projections, b_projections, w_projections,
-                              g_projections, initial_state)
+        ctx.dtypes = [None if t is None else t.dtype
+                      for t in (q, k, v, g, b, w, mix_weights, query_banks, key_projections,
+                                b_projections, w_projections, g_projections, initial_state)]
+        ctx.nmax = query_banks.shape[2] if L > 1 else 0
         ctx.saved_fwd = saved
         return o, (final if output_final_state else None)
 
     @staticmethod
     def backward(ctx, do, dfinal):
-        raise NotImplementedError("backward kernels are not built yet")
+        L, scale, f, nq, has_init, promotion = ctx.meta
+        sv = ctx.saved_fwd
+        if sv is None:
+            raise RuntimeError("chunk_nested_gdn2: no saved state for the backward")
+        grads = _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion)
+        ctx.saved_fwd = None
+        (dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, dinit) = grads
+        dts = ctx.dtypes
+        out = [dq, dk, dv, dg, db, dw, dmix]
+        out = [x.to(dt) for x, dt in zip(out, dts[:7])]
+        if L > 1:
+            out += [x.to(dt) for x, dt in zip((dqb, dkp, dbp, dwp, dgp), dts[7:12])]
+        else:
+            out += [None] * 5
+        return (*out, None, None, None, None,
+                dinit.to(dts[12]) if dinit is not None else None, None, None, None)
 
 
 def chunk_nested_gdn2(q, k, v, g, b, w, mix_weights, query_banks, key_projections,

@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "ngdn_kernels.h"
 
 namespace {
@@ -50,12 +52,13 @@ const char* ngdn_arch(void) { return "gfx950"; }
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, void* W, void* U, void* KtT, void* Qg,
-                          void* Aqk, float* gam, void* stream) {
+                          void* Aqk, float* gam, void* Kt, void* WT, void* QgT,
+                          void* AqkT, void* TT, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_intra_fwd")) return r;
   if (!q || !k || !v || !g || !b || !w || !W || !U || !KtT || !Qg || !Aqk || !gam)
     return fail(NGDN_EINVAL, "ngdn_l0_intra_fwd: NULL tensor");
-  ngdn::L0IntraArgs a{q, k, v, g, b, w, W, U, KtT, Qg, Aqk, gam,
+  ngdn::L0IntraArgs a{q, k, v, g, b, w, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT,
                       d->B, d->T, d->H, d->L, nchunks(d), d->scale};
   return launched(ngdn::l0_intra_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_intra_fwd");
@@ -86,9 +89,9 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
-                       void* A, void* KT, void* U, float* gam, float* keys,
-                       float* vals, float* bo, float* wo, float* go,
-                       void* stream) {
+                       void* A, void* KT, void* U, float* gam, void* keysN,
+                       void* AT, float* keys, float* vals, float* bo, float* wo,
+                       float* go, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_fwd")) return r;
   if (level < 1 || level >= d->L)
@@ -123,7 +126,7 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.kp = lvl(key_projections, hkv);
   a.bpT = lvl(bpT, hkv); a.wpT = lvl(wpT, hkv); a.gpT = lvl(gpT, hkv);
   a.merge = promotion;
-  a.A = A; a.KT = KT; a.U = U; a.gam = gam;
+  a.A = A; a.KT = KT; a.U = U; a.gam = gam; a.keysN = keysN; a.AT = AT;
   a.keys = keys; a.vals = vals; a.bo = bo; a.wo = wo; a.go = go;
   a.B = d->B; a.H = d->H; a.NF = NT / f_here; a.N = N; a.V = d->V;
   if (a.NF == 0) return NGDN_OK;
@@ -179,6 +182,223 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
   a.o = o; a.reads = reads;
   a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
   return launched(ngdn::output_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream), "ngdn_output_fwd");
+}
+
+
+int32_t ngdn_output_bwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
+                        const void* hT, const void* vnT, const void* q,
+                        const void* mix, const float* const* states,
+                        const int32_t* ng, const int32_t* f, const void* dout,
+                        void* dq, float* dmix, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_output_bwd")) return r;
+  if (d->K != d->V)
+    return fail(NGDN_EINVAL, "ngdn_output_bwd: K == V required, got %d, %d", d->K, d->V);
+  if (!Qg || !Aqk || !hT || !vnT || !q || !mix || !dout || !dq || !dmix)
+    return fail(NGDN_EINVAL, "ngdn_output_bwd: NULL tensor");
+  ngdn::OutputBwdArgs a{};
+  a.f.Qg = Qg; a.f.Aqk = Aqk; a.f.hT = hT; a.f.vnT = vnT; a.f.q = q; a.f.mix = mix;
+  for (int l = 1; l < d->L; ++l) {
+    if (!states || !states[l] || !ng || !f || f[l] <= 0)
+      return fail(NGDN_EINVAL, "ngdn_output_bwd: level %d states missing", l);
+    a.f.states[l] = states[l]; a.f.NGl[l] = ng[l]; a.f.f[l] = f[l];
+  }
+  a.f.B = d->B; a.f.T = d->T; a.f.H = d->H; a.f.L = d->L; a.f.NT = nchunks(d); a.f.scale = d->scale;
+  a.dout = dout; a.dq = dq; a.dmix = dmix;
+  return launched(ngdn::output_bwd(a, d->dtype, d->K, d->V, (hipStream_t)stream), "ngdn_output_bwd");
+}
+
+int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
+                            int32_t ng, const void* q, const void* mix,
+                            const void* dout, float* d_states, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_read_state_bwd")) return r;
+  if (level < 1 || level >= d->L || f <= 0 || ng != (nchunks(d) + f - 1) / f)
+    return fail(NGDN_EINVAL, "ngdn_read_state_bwd: level %d / interval %d / groups %d inconsistent",
+                level, f, ng);
+  if (d->K != d->V) return fail(NGDN_EINVAL, "ngdn_read_state_bwd: K == V required");
+  if (!q || !mix || !dout || !d_states) return fail(NGDN_EINVAL, "ngdn_read_state_bwd: NULL tensor");
+  ngdn::ReadStateBwdArgs a{q, mix, dout, d_states, d->B, d->T, d->H, d->L, level, f, ng, d->scale};
+  return launched(ngdn::read_state_bwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
+                  "ngdn_read_state_bwd");
+}
+
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
+                         const float* gam, const void* AqkT, const void* QgT,
+                         const void* dout, const void* mix, int32_t f1,
+                         const float* inj, int32_t nf1, const float* d_final,
+                         void* dSp, void* dVn, void* dVnT, float* d_initial,
+                         void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_l0_scan_bwd")) return r;
+  if (!Kt || !WT || !gam || !AqkT || !QgT || !dout || !mix || !dSp || !dVn)
+    return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: NULL tensor");
+  const int NT = nchunks(d);
+  if (inj && (f1 <= 0 || nf1 != NT / f1))
+    return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: injection count %d inconsistent with f1=%d", nf1, f1);
+  const long long skv = (long long)d->K * d->V;
+  ngdn::ScanBwdArgs a{};
+  a.Bop = Kt; a.AT = WT; a.gam = gam;
+  a.AqkT = AqkT; a.QgT = QgT; a.dout = dout; a.mix = mix; a.T = d->T; a.L = d->L;
+  a.inj = inj; a.inj_every = inj ? f1 : 1; a.inj_nf = nf1;
+  a.d_states = nullptr; a.NG = NT;
+  a.d_final = d_final; a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
+  a.dSp = dSp; a.dsp_mode = 0; a.dVn = dVn; a.dvn_mode = 0; a.dVnT = dVnT;
+  a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
+  a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
+  return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
+}
+
+int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
+                            int32_t nf, int32_t ng, const void* keys,
+                            const void* AT, const float* gam,
+                            const float* d_states, const float* d_final,
+                            float* dSp, float* dvn, float* d_initial,
+                            void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_upper_scan_bwd")) return r;
+  if (level < 1 || level >= d->L)
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: level %d outside [1, L=%d)", level, d->L);
+  if (!pow2_ge16(n_pairs))
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: pairs per firing must be a power of two >= 16 "
+                "(and <= 128), got %d", n_pairs);
+  if (!(ng - 1 <= nf && nf <= ng) || nf < 0)
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: NF=%d inconsistent with NG=%d", nf, ng);
+  if ((nf > 0 && (!keys || !AT || !gam || !dSp || !dvn)) || !d_states)
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: NULL tensor");
+  const long long skv = (long long)d->K * d->V;
+  ngdn::ScanBwdArgs a{};
+  a.Bop = keys; a.AT = AT; a.gam = gam;
+  a.d_states = d_states; a.NG = ng;
+  a.d_final = d_final ? d_final + (long long)level * skv : nullptr;
+  a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
+  a.dSp = dSp; a.dsp_mode = 1; a.dVn = dvn; a.dvn_mode = 1;
+  a.dinit = d_initial ? d_initial + (long long)level * skv : nullptr;
+  a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
+  a.B = d->B; a.H = d->H; a.S = nf; a.M = n_pairs; a.V = d->V;
+  return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_bwd");
+}
+
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const void* hT, const void* dSp,
+                          const void* vnT, const void* dVn, const void* dout,
+                          const void* mix, void* dQg, void* dWT, void* dKt,
+                          void* dAqk, float* dgam, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_l0_bwd_state")) return r;
+  if (!hT || !dSp || !vnT || !dVn || !dout || !mix || !dQg || !dWT || !dKt || !dAqk || !dgam)
+    return fail(NGDN_EINVAL, "ngdn_l0_bwd_state: NULL tensor");
+  ngdn::L0BwdStateArgs a{hT, dSp, vnT, dVn, dout, mix, dQg, dWT, dKt, dAqk, dgam,
+                         d->B, d->T, d->H, d->L, nchunks(d)};
+  return launched(ngdn::l0_bwd_state(a, d->dtype, d->K, d->V, (hipStream_t)stream),
+                  "ngdn_l0_bwd_state");
+}
+
+int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
+                          const void* v, const float* g, const void* b,
+                          const void* w, const void* W, const void* U,
+                          const void* TT, const void* dQg, const void* dWT,
+                          const void* dKt, const void* dAqk, const float* dgam,
+                          const void* dVnT, void* dq, void* dk, void* dv,
+                          float* dg, void* db, void* dw, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_l0_bwd_intra")) return r;
+  if (!q || !k || !v || !g || !b || !w || !W || !U || !TT || !dQg || !dWT || !dKt || !dAqk ||
+      !dgam || !dVnT || !dq || !dk || !dv || !dg || !db || !dw)
+    return fail(NGDN_EINVAL, "ngdn_l0_bwd_intra: NULL tensor");
+  ngdn::L0BwdIntraArgs a{q, k, v, g, b, w, W, U, TT, dQg, dWT, dKt, dAqk, dgam, dVnT,
+                         dq, dk, dv, dg, db, dw, d->B, d->T, d->H, d->L, nchunks(d), d->scale};
+  return launched(ngdn::l0_bwd_intra(a, d->dtype, d->K, d->V, (hipStream_t)stream),
+                  "ngdn_l0_bwd_intra");
+}
+
+int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
+                       int32_t n_queries, int32_t f_below, int32_t f_here,
+                       const void* below, int32_t ng_below,
+                       const float* final_state, const void* query_banks,
+                       int32_t n_max, const void* key_projections,
+                       const void* bpT, const void* wpT, const void* gpT,
+                       const void* kpT, const void* bankT, const void* bp,
+                       const void* wp, const void* gp, const float* states,
+                       int32_t ng, const float* dSp, const float* dvn,
+                       void* ws_vals, void* ws_du, void* ws_dxb, void* ws_dxg,
+                       void* ws_dxw, void* ws_dvals, float* dbank, float* inj,
+                       float* d_below, float* d_final, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_probe_bwd")) return r;
+  if (level < 1 || level >= d->L || d->K != d->V || (promotion != 0 && promotion != 1))
+    return fail(NGDN_EINVAL, "ngdn_probe_bwd: bad level %d / promotion %d / K,V", level, promotion);
+  const int N = promotion == 1 ? d->K : n_queries;
+  if (!pow2_ge16(N))
+    return fail(NGDN_EINVAL, "ngdn_probe_bwd: pairs per firing must be a power of two >= 16, got %d", N);
+  if (promotion == 0 && (n_queries > n_max || n_max % 8 != 0 || !query_banks || !key_projections ||
+                         !kpT || !bankT || !dbank))
+    return fail(NGDN_EINVAL, "ngdn_probe_bwd: bank of %d rows (a multiple of 8 >= n_queries=%d) "
+                "and its transposes are required", n_max, n_queries);
+  if (f_below <= 0 || f_here <= 0) return fail(NGDN_EINVAL, "ngdn_probe_bwd: bad intervals");
+  if (!below || !final_state || !bpT || !wpT || !gpT || !bp || !wp || !gp || !states || !dSp ||
+      !dvn || !ws_vals || !ws_du || !ws_dxb || !ws_dxg || !ws_dxw || !ws_dvals)
+    return fail(NGDN_EINVAL, "ngdn_probe_bwd: NULL tensor");
+  if (level == 1 ? !inj : (!d_below || !d_final))
+    return fail(NGDN_EINVAL, "ngdn_probe_bwd: lower-level gradient destination missing");
+  const int NT = nchunks(d);
+  const long long skv = (long long)d->K * d->V;
+  ngdn::ProbeBwdArgs a{};
+  a.f.below = below; a.f.below_mode = level == 1 ? 0 : 1; a.f.NGb = ng_below;
+  a.f.below_fin = final_state + (long long)(level - 1) * skv;
+  a.f.bf_sh = d->L * skv; a.f.bf_sb = d->H * a.f.bf_sh;
+  a.f.f_below = f_below; a.f.f_here = f_here;
+  const size_t hkv = (size_t)d->H * skv;
+  const size_t esz = d->dtype == NGDN_BF16 ? 2 : 4;
+  auto lvl = [&](const void* p, size_t per) -> const void* {
+    return p ? static_cast<const char*>(p) + (size_t)(level - 1) * per * esz : nullptr;
+  };
+  a.f.bank = lvl(query_banks, (size_t)d->H * n_max * d->K); a.f.Nmax = n_max;
+  a.f.kp = lvl(key_projections, hkv);
+  a.f.bpT = lvl(bpT, hkv); a.f.wpT = lvl(wpT, hkv); a.f.gpT = lvl(gpT, hkv);
+  a.f.merge = promotion;
+  a.f.B = d->B; a.f.H = d->H; a.f.NF = NT / f_here; a.f.N = N; a.f.V = d->V;
+  a.kpT = lvl(kpT, hkv); a.bankT = lvl(bankT, (size_t)d->H * n_max * d->K);
+  a.bp = lvl(bp, hkv); a.wp = lvl(wp, hkv); a.gp = lvl(gp, hkv);
+  a.Sg = states; a.NG = ng;
+  a.dSp = dSp; a.dvn = dvn;
+  a.wsV = ws_vals; a.wsdu = ws_du; a.wsdxb = ws_dxb; a.wsdxg = ws_dxg; a.wsdxw = ws_dxw;
+  a.wsdV = ws_dvals;
+  a.dbank = dbank ? dbank + (size_t)(level - 1) * d->H * n_max * d->K : nullptr;
+  a.inj = inj; a.d_below = d_below;
+  a.d_below_fin = d_final ? d_final + (long long)(level - 1) * skv : nullptr;
+  if (a.f.NF == 0) return NGDN_OK;
+  return launched(ngdn::probe_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_probe_bwd");
+}
+
+int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
+                         int32_t n_pairs, int32_t nf, const void* ws_vals,
+                         const void* ws_du, const void* ws_dxb,
+                         const void* ws_dxg, const void* ws_dxw, float* dkp,
+                         float* dbp, float* dwp, float* dgp, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_param_grads")) return r;
+  if (level < 1 || level >= d->L || d->K != d->V)
+    return fail(NGDN_EINVAL, "ngdn_param_grads: bad level %d or K != V", level);
+  if (!ws_vals || !ws_dxb || !ws_dxg || !ws_dxw || !dbp || !dwp || !dgp ||
+      (promotion == 0 && (!ws_du || !dkp)))
+    return fail(NGDN_EINVAL, "ngdn_param_grads: NULL tensor");
+  if (nf <= 0) return NGDN_OK;
+  const size_t off = (size_t)(level - 1) * d->H * d->K * d->V;
+  const int split = std::max(1, std::min(32, (d->B * nf + 3) / 4));
+  hipStream_t st = (hipStream_t)stream;
+  ngdn::AtBArgs a{};
+  a.B = d->B; a.H = d->H; a.NF = nf; a.N = n_pairs; a.X = d->K; a.Y = d->V; a.split = split;
+  hipError_t e = hipSuccess;
+  if (promotion == 0) {
+    a.A = ws_du; a.Bm = ws_vals; a.C = dkp + off;                  // dWk = du^T Vals
+    if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
+  }
+  a.A = ws_vals; a.Bm = ws_dxb; a.C = dbp + off;                   // dBp = Vals^T dxb
+  if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
+  a.A = ws_vals; a.Bm = ws_dxw; a.C = dwp + off;                   // dWp = Vals^T dxw
+  if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
+  a.A = ws_vals; a.Bm = ws_dxg; a.C = dgp + off;                   // dGp = Vals^T dxg
+  return launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads");
 }
 
 }  // extern "C"

@@ -1,0 +1,407 @@
+// Level-0 chunk backward: the gradients the reference takes from fla's
+// chunk_gdn2_bwd helpers (nested_gdn2/ops/_vendor/gdn2_chunk_bwd.py:104-177:
+// chunk_kda_bwd_dAv, chunk_gdn2_bwd_wy_dqkg_fused, chunk_gdn2_bwd_intra and
+// the reverse chunk_local_cumsum), derived here from the chunk form
+// (ops/naive.py:329-392):
+//   Vn = U - W S,  o = Qg S + Aqk Vn,  S' = diag(gam) S + Kt^T Vn,
+//   W = T X_w, U = T X_u, T = (I + A)^-1, X_w = b k e^gc, X_u = w v.
+// Given dO = mix_0 do, the state gradient after the chunk dS' and dVn from the
+// reverse scan:
+//   state half (l0_bwd_state):
+//     dQg = dO S^T, dW = -dVn S^T, dKt = Vn dS'^T, dAqk = mask(dO Vn^T),
+//     dgam = rowsum(dS' * S)
+//   intra half (l0_bwd_intra):
+//     dX_u = T^T dVn, dX_w = T^T dW, dA = -mask(dX_w W^T + dX_u U^T)
+//     then through the decay products of A and Aqk, the gates and the
+//     cumulative sum of g (reverse cumsum within the chunk).
+#include "l0_common.h"
+
+namespace ngdn {
+
+template <typename E, int K, int V>
+__global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
+  constexpr int C = CH;
+  constexpr int LDV = V + 8;
+  constexpr int CTK = K / 16;
+  constexpr int NKV = V / Mma<E>::KS;
+  typedef typename Mma<E>::Frag Frag;
+  __shared__ __attribute__((aligned(16))) E s_S[K * LDV];
+  __shared__ __attribute__((aligned(16))) E s_Vn[C * LDV];
+
+  const int NT = a.NT, H = a.H, T = a.T;
+  const int n = blockIdx.x % NT;
+  const int bh = blockIdx.x / NT;
+  const int h = bh % H, b = bh / H;
+  const int t0 = n * C;
+  const int nvalid = min(C, T - t0);
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const size_t cix = (size_t)bh * NT + n;
+
+  {
+    const E* hT = static_cast<const E*>(a.hT) + cix * V * K;
+    for (int e = tid; e < V * K; e += 256) s_S[(e % K) * LDV + e / K] = hT[e];
+    const E* vT = static_cast<const E*>(a.vnT) + cix * V * C;
+    for (int e = tid; e < V * C; e += 256) s_Vn[(e % C) * LDV + e / C] = vT[e];
+  }
+  __syncthreads();
+
+  // A fragments of this wave's 16 rows: dO (from do and mix_0), dVn, Vn
+  const int ri = wv * 16 + (lane & 15);
+  const E* dop = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V;
+  const float m0 = ri < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + ri) * H * a.L + (size_t)h * a.L]) : 0.f;
+  const E* dvn = static_cast<const E*>(a.dVn) + cix * C * V + (size_t)ri * V;
+  Frag fo[NKV], fd[NKV], fv[NKV];
+#pragma unroll
+  for (int s = 0; s < NKV; ++s) {
+    const int v0 = s * Mma<E>::KS + kofs<E>(lane);
+    fo[s] = Mma<E>::make([&](int e) {
+      return ri < nvalid ? to_f(dop[(size_t)(t0 + ri) * H * V + v0 + e]) * m0 : 0.f;
+    });
+    fd[s] = Mma<E>::load(dvn + v0);
+    fv[s] = Mma<E>::load(s_Vn + ri * LDV + v0);
+  }
+  const E* dsp = static_cast<const E*>(a.dSp) + cix * K * V;
+  E* dQg = static_cast<E*>(a.dQg) + cix * C * K;
+  E* dWT = static_cast<E*>(a.dWT) + cix * K * C;
+  E* dKt = static_cast<E*>(a.dKt) + cix * C * K;
+#pragma unroll 2
+  for (int ct = 0; ct < CTK; ++ct) {
+    f4 aq = f4_zero(), aw = f4_zero(), ak = f4_zero();
+    const E* srow = s_S + (ct * 16 + (lane & 15)) * LDV + kofs<E>(lane);
+    const E* drow = dsp + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
+#pragma unroll
+    for (int s = 0; s < NKV; ++s) {
+      const Frag sb = Mma<E>::load(srow + s * Mma<E>::KS);
+      aq = Mma<E>::mma(aq, fo[s], sb);
+      aw = Mma<E>::mma(aw, fd[s], sb);
+      ak = Mma<E>::mma(ak, fv[s], Mma<E>::load(drow + s * Mma<E>::KS));
+    }
+    const int i0 = wv * 16 + acc_row(0), k = ct * 16 + acc_col();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      dQg[(i0 + r) * K + k] = from_f<E>(aq[r]);
+      dKt[(i0 + r) * K + k] = from_f<E>(ak[r]);
+      dWT[k * C + i0 + r] = from_f<E>(-aw[r]);
+    }
+  }
+  // dAqk = dO Vn^T, lower including the diagonal
+  E* dAq = static_cast<E*>(a.dAqk) + cix * C * C;
+  for (int J = 0; J < 4; ++J) {
+    f4 acc = f4_zero();
+    if (J <= wv) {
+      const E* vrow = s_Vn + (J * 16 + (lane & 15)) * LDV + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < NKV; ++s) acc = Mma<E>::mma(acc, fo[s], Mma<E>::load(vrow + s * Mma<E>::KS));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
+      dAq[i * C + j] = from_f<E>(j <= i ? acc[r] : 0.f);
+    }
+  }
+  // dgam_k = sum_v dS'[k][v] S[k][v]
+  {
+    constexpr int TPK = 256 / K;           // threads per row k
+    const int k = tid / TPK, part = tid % TPK;
+    float s = 0.f;
+    for (int v = part; v < V; v += TPK) s += to_f(dsp[(size_t)k * V + v]) * to_f(s_S[k * LDV + v]);
+#pragma unroll
+    for (int o = 1; o < TPK; o <<= 1) s += __shfl_xor(s, o, WAVE);
+    if (part == 0) a.dgam[cix * K + k] = s;
+  }
+}
+
+template <typename E, int K, int V>
+__global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
+  constexpr int C = CH;
+  constexpr int GL = K + GCP;
+  constexpr int LDK = K + 8, LDV = V + 8;
+  constexpr int CTK = K / 16, CTV = V / 16;
+  constexpr int KS = Mma<E>::KS;
+  typedef typename Mma<E>::Frag Frag;
+  constexpr size_t SZ_GC = sizeof(float) * C * GL;
+  constexpr size_t SZ_DX = sizeof(E) * C * (LDK + LDV);
+  constexpr size_t SZ_DG = sizeof(float) * C * GL;
+  constexpr size_t SZ_R = SZ_DX > SZ_DG ? SZ_DX : SZ_DG;
+  constexpr size_t SZ_DA = sizeof(float) * 2 * C * AT_LD;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R + SZ_DA + sizeof(float) * K];
+  float* s_gc = reinterpret_cast<float*>(smem);
+  E* s_dXw = reinterpret_cast<E*>(smem + SZ_GC);
+  E* s_dXu = s_dXw + C * LDK;
+  float* s_dgc = reinterpret_cast<float*>(smem + SZ_GC);
+  float* s_dA = reinterpret_cast<float*>(smem + SZ_GC + SZ_R);
+  float* s_dQ = s_dA + C * AT_LD;
+  float* s_col = s_dQ + C * AT_LD;
+
+  const int NT = a.NT, H = a.H, T = a.T;
+  const int n = blockIdx.x % NT;
+  const int bh = blockIdx.x / NT;
+  const int h = bh % H, b = bh / H;
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const size_t cix = (size_t)bh * NT + n;
+  ChunkIn<E, K, V> in;
+  in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, T, H, a.L, a.scale);
+  const int t0 = in.t0, nvalid = in.nvalid;
+
+  // ---- 1. gc, dAqk (fp32 in LDS)
+  l0_cumsum(s_gc, in);
+  {
+    const E* dq = static_cast<const E*>(a.dAqk) + cix * C * C;
+    for (int e = tid; e < C * C; e += 256) s_dQ[(e / C) * AT_LD + e % C] = to_f(dq[e]);
+    for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns rows 16w..16w+15
+  const int ri = wv * 16 + (lane & 15);
+  f4 dxw[CTK];
+  {
+    Frag tf[C / KS];
+    const E* tt = static_cast<const E*>(a.TT) + cix * C * C + (size_t)ri * C + kofs<E>(lane);
+#pragma unroll
+    for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::load(tt + s * KS);
+    const E* dvT = static_cast<const E*>(a.dVnT) + cix * V * C;
+    const E* dwT = static_cast<const E*>(a.dWT) + cix * K * C;
+    E* dvo = static_cast<E*>(a.dv) + ((size_t)b * T * H + h) * V;
+    E* dwo = static_cast<E*>(a.dw) + ((size_t)b * T * H + h) * V;
+    for (int ct = 0; ct < CTV; ++ct) {
+      f4 acc = f4_zero();
+      const E* br = dvT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::load(br + s * KS));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wv * 16 + acc_row(r), vv = ct * 16 + acc_col();
+        s_dXu[i * LDV + vv] = from_f<E>(acc[r]);
+        if (i < nvalid) {
+          dvo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.W_(i, vv));
+          dwo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.V_(i, vv));
+        }
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CTK; ++ct) {
+      f4 acc = f4_zero();
+      const E* br = dwT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::load(br + s * KS));
+      dxw[ct] = acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        s_dXw[(wv * 16 + acc_row(r)) * LDK + ct * 16 + acc_col()] = from_f<E>(acc[r]);
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower
+  {
+    const E* Wg = static_cast<const E*>(a.W) + cix * C * K;
+    const E* Ug = static_cast<const E*>(a.U) + cix * C * V;
+    for (int J = 0; J < 4; ++J) {
+      f4 acc = f4_zero();
+      if (J <= wv) {
+        acc = mma_tile<E>(acc, s_dXw + wv * 16 * LDK, LDK, Wg + (size_t)J * 16 * K, K, K);
+        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LDV, LDV, Ug + (size_t)J * 16 * V, V, V);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
+        s_dA[i * AT_LD + j] = (j < i) ? -acc[r] : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  const bool safe = l0_block_safe<K>(s_gc, wv);
+  const int R0 = 16 * wv;
+
+  // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w:
+  //   sum_j dA_ij k_j e^(gc_i - gc_j) = e^(gc_i - gc_r) sum_j dA_ij [k_j e^(gc_r - gc_j)]
+  f4 dbk[CTK], dqa[CTK];
+#pragma unroll
+  for (int ct = 0; ct < CTK; ++ct) { dbk[ct] = f4_zero(); dqa[ct] = f4_zero(); }
+  {
+    const int jmax = 16 * (wv + 1);
+    const int jlim = safe ? jmax : R0;           // unsafe: diagonal block done exactly below
+    const int nst = (jmax + KS - 1) / KS;
+    for (int s = 0; s < nst; ++s) {
+      const int j0 = s * KS + kofs<E>(lane);
+      const Frag fa = Mma<E>::make([&](int e) { return j0 + e < jlim ? s_dA[ri * AT_LD + j0 + e] : 0.f; });
+      const Frag fq = Mma<E>::make([&](int e) { return j0 + e < jlim ? s_dQ[ri * AT_LD + j0 + e] : 0.f; });
+#pragma unroll
+      for (int ct = 0; ct < CTK; ++ct) {
+        const int kc = ct * 16 + (lane & 15);
+        const Frag fb = Mma<E>::make([&](int e) {
+          const int j = j0 + e;
+          if (j >= jlim) return 0.f;
+          return in.K_(j, kc) * expf(fminf(s_gc[R0 * GL + kc] - s_gc[j * GL + kc], 88.f));
+        });
+        dbk[ct] = Mma<E>::mma(dbk[ct], fa, fb);
+        dqa[ct] = Mma<E>::mma(dqa[ct], fq, fb);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CTK; ++ct) {
+      const int kc = ct * 16 + acc_col();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = R0 + acc_row(r);
+        const float f = expf(s_gc[i * GL + kc] - s_gc[R0 * GL + kc]);
+        float xb = dbk[ct][r] * f, xq = dqa[ct][r] * f;
+        if (!safe) {
+          for (int j = R0; j <= i; ++j) {
+            const float d = in.K_(j, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
+            if (j < i) xb += s_dA[i * AT_LD + j] * d;
+            xq += s_dQ[i * AT_LD + j] * d;
+          }
+        }
+        dbk[ct][r] = xb;
+        dqa[ct][r] = xq;
+      }
+    }
+  }
+
+  // ---- 4b. dk from A and Aqk, rows j of block J = w:
+  //   sum_i (dA_ij bk_i + dAqk_ij q_i) e^(gc_i - gc_j)
+  //   = e^(gc_e - gc_j) sum_i (...) e^(gc_i - gc_e),  e = last row of block J
+  f4 dka[CTK];
+#pragma unroll
+  for (int ct = 0; ct < CTK; ++ct) dka[ct] = f4_zero();
+  {
+    const int RE = R0 + 15;
+    const int i0 = (R0 / KS) * KS;
+    const int ilo = safe ? R0 : R0 + 16;         // unsafe: diagonal block done exactly below
+    const int rj = R0 + (lane & 15);
+    for (int s = 0; s < (C - i0) / KS; ++s) {
+      const int ib = i0 + s * KS + kofs<E>(lane);
+      const Frag fa = Mma<E>::make([&](int e) { return ib + e >= ilo ? s_dA[(ib + e) * AT_LD + rj] : 0.f; });
+      const Frag fq = Mma<E>::make([&](int e) { return ib + e >= ilo ? s_dQ[(ib + e) * AT_LD + rj] : 0.f; });
+#pragma unroll
+      for (int ct = 0; ct < CTK; ++ct) {
+        const int kc = ct * 16 + (lane & 15);
+        const Frag fbb = Mma<E>::make([&](int e) {
+          const int i = ib + e;
+          if (i < ilo) return 0.f;
+          return in.B_(i, kc) * in.K_(i, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
+        });
+        const Frag fbq = Mma<E>::make([&](int e) {
+          const int i = ib + e;
+          if (i < ilo) return 0.f;
+          return in.Q_(i, kc) * in.scale * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
+        });
+        dka[ct] = Mma<E>::mma(dka[ct], fa, fbb);
+        dka[ct] = Mma<E>::mma(dka[ct], fq, fbq);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CTK; ++ct) {
+      const int kc = ct * 16 + acc_col();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = R0 + acc_row(r);
+        float x = dka[ct][r] * expf(s_gc[RE * GL + kc] - s_gc[j * GL + kc]);
+        if (!safe) {
+          for (int i = j; i < R0 + 16; ++i) {
+            const float d = expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
+            x += (s_dA[i * AT_LD + j] * in.B_(i, kc) * in.K_(i, kc) +
+                  s_dQ[i * AT_LD + j] * in.Q_(i, kc) * in.scale) * d;
+          }
+        }
+        dka[ct][r] = x;
+      }
+    }
+  }
+
+  // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
+  {
+    const E* dQg = static_cast<const E*>(a.dQg) + cix * C * K;
+    const E* dKt = static_cast<const E*>(a.dKt) + cix * C * K;
+    const size_t tok = (size_t)b * T * H + h;
+    E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
+    E* dko = static_cast<E*>(a.dk) + tok * K;
+    E* dbo = static_cast<E*>(a.db) + tok * K;
+#pragma unroll
+    for (int ct = 0; ct < CTK; ++ct) {
+      const int kc = ct * 16 + acc_col();
+      const float glast = s_gc[(C - 1) * GL + kc];
+      float colsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = R0 + acc_row(r);
+        const float gcv = s_gc[i * GL + kc];
+        const float eg = expf(gcv), ekt = expf(glast - gcv);
+        const float bi = in.B_(i, kc), ki = in.K_(i, kc), qh = in.Q_(i, kc) * in.scale;
+        const float gq = to_f(dQg[i * K + kc]), gk = to_f(dKt[i * K + kc]);
+        const float xw = dxw[ct][r];
+        const float dqh = dqa[ct][r] + gq * eg;
+        const float db_ = dbk[ct][r] * ki + xw * ki * eg;
+        const float dk_ = dka[ct][r] + dbk[ct][r] * bi + xw * bi * eg + gk * ekt;
+        const float dgc = bi * ki * dbk[ct][r] + qh * dqa[ct][r] - ki * dka[ct][r] +
+                          xw * bi * ki * eg + gq * qh * eg - gk * ki * ekt;
+        colsum += gk * ki * ekt;
+        s_dgc[i * GL + kc] = dgc;
+        if (i < nvalid) {
+          dqo[(size_t)(t0 + i) * H * a.L * K + kc] = from_f<E>(dqh * in.scale);
+          dko[(size_t)(t0 + i) * H * K + kc] = from_f<E>(dk_);
+          dbo[(size_t)(t0 + i) * H * K + kc] = from_f<E>(db_);
+        }
+      }
+      colsum += __shfl_xor(colsum, 16, WAVE);
+      colsum += __shfl_xor(colsum, 32, WAVE);
+      if (lane < 16) atomicAdd(&s_col[kc], colsum);
+    }
+  }
+  __syncthreads();
+
+  // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
+  // every Kt and gam
+  if (tid < K) {
+    const float* dgam = a.dgam + cix * K;
+    float run = s_col[tid] + dgam[tid] * expf(s_gc[(C - 1) * GL + tid]);
+    float* dgo = a.dg + ((size_t)b * T * H + h) * K;
+    for (int i = C - 1; i >= 0; --i) {
+      run += s_dgc[i * GL + tid];
+      if (i < nvalid) dgo[(size_t)(t0 + i) * H * K + tid] = run;
+    }
+  }
+}
+
+template <typename E, int K, int V>
+static hipError_t launch_l0_bwd_state(const L0BwdStateArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * a.NT);
+  hipLaunchKernelGGL((l0_bwd_state_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <typename E, int K, int V>
+static hipError_t launch_l0_bwd_intra(const L0BwdIntraArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * a.NT);
+  hipLaunchKernelGGL((l0_bwd_intra_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStream_t st) {
+#define NGDN_BS(E, KK, VV) \
+  if (K == KK && V == VV) return launch_l0_bwd_state<E, KK, VV>(a, st);
+  if (dtype == NGDN_BF16) {
+    NGDN_BS(bf16, 64, 64) NGDN_BS(bf16, 64, 128) NGDN_BS(bf16, 128, 64) NGDN_BS(bf16, 128, 128)
+  } else {
+    NGDN_BS(float, 64, 64) NGDN_BS(float, 64, 128) NGDN_BS(float, 128, 64) NGDN_BS(float, 128, 128)
+  }
+#undef NGDN_BS
+  return hipErrorInvalidValue;
+}
+
+hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st) {
+#define NGDN_BI(E, KK, VV) \
+  if (K == KK && V == VV) return launch_l0_bwd_intra<E, KK, VV>(a, st);
+  if (dtype == NGDN_BF16) {
+    NGDN_BI(bf16, 64, 64) NGDN_BI(bf16, 64, 128) NGDN_BI(bf16, 128, 64) NGDN_BI(bf16, 128, 128)
+  } else {
+    NGDN_BI(float, 64, 64) NGDN_BI(float, 64, 128) NGDN_BI(float, 128, 64) NGDN_BI(float, 128, 128)
+  }
+#undef NGDN_BI
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ngdn

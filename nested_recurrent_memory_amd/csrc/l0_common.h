@@ -1,0 +1,218 @@
+// Per-chunk level-0 building blocks shared by the forward (l0_intra.hip) and
+// backward (l0_bwd.hip) kernels. A workgroup of 4 waves owns one
+// (batch, head, chunk); wave w owns block-row w (16 rows) wherever rows split.
+#pragma once
+
+#include "ngdn_kernels.h"
+
+namespace ngdn {
+
+// Inputs of one chunk in the reference layout.
+template <typename E, int K, int V>
+struct ChunkIn {
+  const E* q; const E* k; const E* b; const E* v; const E* w; const float* g;
+  size_t rowQ, rowK, rowV;
+  int t0, nvalid;
+  float scale;
+
+  __device__ __forceinline__ void init(const void* q_, const void* k_, const void* v_,
+                                       const float* g_, const void* b_, const void* w_,
+                                       int bi, int h, int n, int T, int H, int L, float sc) {
+    const size_t bt = (size_t)bi * T * H + h;
+    q = static_cast<const E*>(q_) + bt * L * K;
+    k = static_cast<const E*>(k_) + bt * K;
+    b = static_cast<const E*>(b_) + bt * K;
+    v = static_cast<const E*>(v_) + bt * V;
+    w = static_cast<const E*>(w_) + bt * V;
+    g = g_ + bt * K;
+    rowQ = (size_t)H * L * K; rowK = (size_t)H * K; rowV = (size_t)H * V;
+    t0 = n * CH;
+    nvalid = min(CH, T - t0);
+    scale = sc;
+  }
+  // element loads, zero past the sequence end
+  __device__ __forceinline__ float ld(const E* p, size_t row, int i, int c) const {
+    return i < nvalid ? to_f(p[(size_t)(t0 + i) * row + c]) : 0.f;
+  }
+  __device__ __forceinline__ float K_(int i, int c) const { return ld(k, rowK, i, c); }
+  __device__ __forceinline__ float B_(int i, int c) const { return ld(b, rowK, i, c); }
+  __device__ __forceinline__ float Q_(int i, int c) const { return ld(q, rowQ, i, c); }
+  __device__ __forceinline__ float V_(int i, int c) const { return ld(v, rowV, i, c); }
+  __device__ __forceinline__ float W_(int i, int c) const { return ld(w, rowV, i, c); }
+};
+
+constexpr int GCP = 1;   // padding of gc rows
+constexpr int AT_LD = CH + 1;
+
+// gc[i][k] = sum_{s<=i} g_s[k] within the chunk (zero past the end).
+template <typename E, int K, int V>
+__device__ __forceinline__ void l0_cumsum(float* s_gc, const ChunkIn<E, K, V>& in) {
+  const int tid = threadIdx.x;
+  if (tid < K) {
+    float acc = 0.f;
+    for (int i = 0; i < CH; ++i) {
+      if (i < in.nvalid) acc += in.g[(size_t)(in.t0 + i) * in.rowK + tid];
+      s_gc[i * (K + GCP) + tid] = acc;
+    }
+  }
+}
+
+// Largest decay inside 16-row block I, over every row and channel:
+// max (gc[16 I] - gc[j]). When it is at most 80 nats, factors e^(gc_r - gc_j)
+// for j in the block stay inside fp32 range.
+template <int K>
+__device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
+  const int lane = lane_id(), r = 16 * I;
+  float dmax = 0.f;
+  for (int e = lane; e < 16 * K; e += WAVE) {
+    const int j = r + e / K, c = e % K;
+    dmax = fmaxf(dmax, s_gc[r * (K + GCP) + c] - s_gc[j * (K + GCP) + c]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, o, WAVE));
+  return dmax <= 80.f;
+}
+
+// A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
+// Aqk (lower incl. diagonal) to global [64][64]; when aqkT_out != null also its
+// transpose. Wave w computes block-row w.
+template <typename E, int K, int V>
+__device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
+                                           const ChunkIn<E, K, V>& in, E* aqk_out,
+                                           E* aqkT_out) {
+  constexpr int GL = K + GCP;
+  constexpr int NKS = K / Mma<E>::KS;
+  typedef typename Mma<E>::Frag Frag;
+  const int lane = lane_id(), I = wave_id(), r = 16 * I;
+  const bool safe = l0_block_safe<K>(s_gc, I);
+  const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
+  Frag lf[NKS], qf[NKS];
+  const int ri = r + (lane & 15);
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+    lf[s] = Mma<E>::make([&](int e) {
+      const int c = c0 + e;
+      return in.B_(ri, c) * in.K_(ri, c) * expf(s_gc[ri * GL + c] - s_gc[r * GL + c]);
+    });
+    if (want_q)
+      qf[s] = Mma<E>::make([&](int e) {
+        const int c = c0 + e;
+        return in.Q_(ri, c) * in.scale * expf(s_gc[ri * GL + c] - s_gc[r * GL + c]);
+      });
+  }
+  for (int J = 0; J < 4; ++J) {
+    f4 accA = f4_zero(), accQ = f4_zero();
+    if (J <= I) {
+      const int rj = 16 * J + (lane & 15);
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+        Frag kf = Mma<E>::make([&](int e) {
+          const int c = c0 + e;
+          const float x = s_gc[r * GL + c] - s_gc[rj * GL + c];
+          return in.K_(rj, c) * expf(J < I ? x : fminf(x, 88.f));
+        });
+        accA = Mma<E>::mma(accA, lf[s], kf);
+        if (want_q) accQ = Mma<E>::mma(accQ, qf[s], kf);
+      }
+      if (J == I && !safe) {
+        // exact pairwise form for this diagonal tile
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = r + acc_row(rr), j = 16 * J + acc_col();
+          float sa = 0.f, sq = 0.f;
+          if (j <= i) {
+            for (int c = 0; c < K; ++c) {
+              const float d = expf(fminf(s_gc[i * GL + c] - s_gc[j * GL + c], 0.f));
+              const float kj = in.K_(j, c);
+              sa += in.B_(i, c) * in.K_(i, c) * kj * d;
+              if (want_q) sq += in.Q_(i, c) * kj * d;
+            }
+          }
+          accA[rr] = sa;
+          accQ[rr] = sq * in.scale;
+        }
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = r + acc_row(rr), j = 16 * J + acc_col();
+      s_A[i * AT_LD + j] = (j < i) ? accA[rr] : 0.f;
+      const E qv = from_f<E>((j <= i) ? accQ[rr] : 0.f);
+      if (aqk_out) aqk_out[i * CH + j] = qv;
+      if (aqkT_out) aqkT_out[j * CH + i] = qv;
+    }
+  }
+}
+
+// T = (I + A)^-1 by 16-row blocks: diagonal blocks by forward substitution,
+// then T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ by sub-diagonal. s_P is scratch
+// [3][16][17]. Ends with a barrier.
+__device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s_P) {
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  if (wv == 0) {
+    const int I = lane >> 4, c = lane & 15, o = 16 * I;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float val = (i == c) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j)
+        if (j >= c) val -= s_A[(o + i) * AT_LD + o + j] * t[j];
+      t[i] = (i >= c) ? val : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s_T[(o + i) * AT_LD + o + c] = t[i];
+  } else {
+    for (int e = tid - WAVE; e < CH * CH; e += 3 * WAVE) {
+      const int i = e / CH, j = e % CH;
+      if ((i >> 4) != (j >> 4)) s_T[i * AT_LD + j] = 0.f;
+    }
+  }
+  __syncthreads();
+  for (int d = 1; d < 4; ++d) {
+    const int nb = 4 - d;
+    for (int e = tid; e < nb * 256; e += 256) {
+      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
+      const int I = d + blk, J = I - d;
+      float acc = 0.f;
+      for (int m = 16 * J; m < 16 * I; ++m)
+        acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * AT_LD + 16 * J + j];
+      s_P[blk * 272 + i * 17 + j] = acc;
+    }
+    __syncthreads();
+    for (int e = tid; e < nb * 256; e += 256) {
+      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
+      const int I = d + blk, J = I - d;
+      float acc = 0.f;
+#pragma unroll
+      for (int m = 0; m < 16; ++m)
+        acc += s_T[(16 * I + i) * AT_LD + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
+      s_T[(16 * I + i) * AT_LD + 16 * J + j] = -acc;
+    }
+    __syncthreads();
+  }
+}
+
+// Right-hand sides transposed into s_X [(K+V)][LDX]: X[k][c] = b k e^gc,
+// X[K+v][c] = w v.
+template <typename E, int K, int V, int LDX>
+__device__ __forceinline__ void l0_build_X(E* s_X, const float* s_gc, const ChunkIn<E, K, V>& in) {
+  const int tid = threadIdx.x;
+  for (int e = tid; e < CH * K; e += 256) {
+    const int c = e / K, kk = e % K;
+    s_X[kk * LDX + c] = from_f<E>(in.B_(c, kk) * in.K_(c, kk) * expf(s_gc[c * (K + GCP) + kk]));
+  }
+  for (int e = tid; e < CH * V; e += 256) {
+    const int c = e / V, vv = e % V;
+    s_X[(K + vv) * LDX + c] = from_f<E>(in.W_(c, vv) * in.V_(c, vv));
+  }
+}
+
+// MFMA depth for block-row I of a lower-triangular left operand.
+template <typename E> __device__ __forceinline__ int tri_depth(int I) {
+  return min(CH, ((16 * (I + 1) + Mma<E>::KS - 1) / Mma<E>::KS) * Mma<E>::KS);
+}
+
+}  // namespace ngdn

@@ -8,10 +8,12 @@
 //   A_ij = sum_k b_i k_i k_j e^(gc_i - gc_j)             j <  i
 //   T    = (I + A)^-1
 //   W    = T (b * k * e^gc),  U = T (w * v)
-//   Kt_i = k_i * e^(gc_last - gc_i)                      (stored transposed)
+//   Kt_i = k_i * e^(gc_last - gc_i)
 //   Qg   = scale * q0 * e^gc
 //   Aqk  = sum_k scale q_i k_j e^(gc_i - gc_j)            j <= i
 //   gam  = e^gc_last
+// The forward consumes W, U, Kt^T, Qg, Aqk; the reverse scan consumes the
+// transposed copies Kt, W^T, Qg^T, Aqk^T, written when their pointers are set.
 //
 // One workgroup (4 waves) per (batch, head, chunk). Decay products are formed
 // without overflow: inside block-row I (16 rows starting at r = 16 I) every
@@ -20,7 +22,7 @@
 // e^(decay over at most 15 tokens), and when that could leave fp32 range
 // (more than 80 nats in some channel) the diagonal tile is recomputed pair by
 // pair with clamped exponents, exactly as the reference does.
-#include "ngdn_kernels.h"
+#include "l0_common.h"
 
 namespace ngdn {
 
@@ -28,18 +30,16 @@ template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int C = CH;
   constexpr int LDX = C + 8;                 // k-contiguous rows of length C
-  const int NT = a.NT, H = a.H, T = a.T;
+  constexpr int GL = K + GCP;
+  const int NT = a.NT, H = a.H;
   const int n = blockIdx.x % NT;
   const int bh = blockIdx.x / NT;
   const int h = bh % H, b = bh / H;
-  const int t0 = n * C;
-  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const int wv = wave_id(), tid = threadIdx.x;
 
   // LDS: gc (fp32), then a region used first for A/T (fp32), then for the
-  // transposed right-hand sides X (E), then for Kt^T (E); T in E.
-  constexpr int GC_LD = K + 1;
-  constexpr int AT_LD = C + 1;
-  constexpr size_t SZ_GC = sizeof(float) * C * GC_LD;
+  // transposed right-hand sides X (E), then for Kt^T / Qg^T staging (E); T in E.
+  constexpr size_t SZ_GC = sizeof(float) * C * GL;
   constexpr size_t SZ_AT = sizeof(float) * 2 * C * AT_LD + sizeof(float) * 3 * 16 * 17;
   constexpr size_t SZ_X = sizeof(E) * (K + V) * LDX;
   constexpr size_t SZ_R = SZ_AT > SZ_X ? SZ_AT : SZ_X;
@@ -53,212 +53,85 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   E* s_X = reinterpret_cast<E*>(region);
   E* s_TE = reinterpret_cast<E*>(smem + SZ_GC + SZ_R);
 
-  const size_t rowK = (size_t)H * K;          // token stride of k, b, g
-  const size_t rowV = (size_t)H * V;          // token stride of v, w
-  const size_t rowQ = (size_t)H * a.L * K;    // token stride of q
-  const E* qp = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * a.L * K;
-  const E* kp = static_cast<const E*>(a.k) + ((size_t)b * T * H + h) * K;
-  const E* bp = static_cast<const E*>(a.b) + ((size_t)b * T * H + h) * K;
-  const E* vp = static_cast<const E*>(a.v) + ((size_t)b * T * H + h) * V;
-  const E* wp = static_cast<const E*>(a.w) + ((size_t)b * T * H + h) * V;
-  const float* gp = a.g + ((size_t)b * T * H + h) * K;
-  const int nvalid = min(C, T - t0);           // rows past T are zero padding
+  ChunkIn<E, K, V> in;
+  in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, a.T, H, a.L, a.scale);
+  const size_t cix = (size_t)bh * NT + n;
 
   // ---- 1. in-chunk cumulative log decay
-  if (tid < K) {
-    float acc = 0.f;
-    for (int i = 0; i < C; ++i) {
-      if (i < nvalid) acc += gp[(size_t)(t0 + i) * rowK + tid];
-      s_gc[i * GC_LD + tid] = acc;
-    }
-  }
+  l0_cumsum(s_gc, in);
   __syncthreads();
 
-  auto ld = [&](const E* base, size_t stride, int i, int c) -> float {
-    return i < nvalid ? to_f(base[(size_t)(t0 + i) * stride + c]) : 0.f;
-  };
-
-  // ---- 2. A and Aqk, wave w owns block-row I = w
-  {
-    const int I = wv, r = 16 * I;
-    typedef typename Mma<E>::Frag Frag;
-    constexpr int NKS = K / Mma<E>::KS;
-    // largest decay across the 16 rows of this block, any channel
-    float dmax = 0.f;
-    for (int e = lane; e < 16 * K; e += WAVE) {
-      const int j = r + e / K, c = e % K;
-      dmax = fmaxf(dmax, s_gc[r * GC_LD + c] - s_gc[j * GC_LD + c]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, o, WAVE));
-    const bool safe = dmax <= 80.f;
-
-    Frag lf[NKS], qf[NKS];
-    const int ri = r + (lane & 15);
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-      lf[s] = Mma<E>::make([&](int e) {
-        const int c = c0 + e;
-        const float d = expf(s_gc[ri * GC_LD + c] - s_gc[r * GC_LD + c]);
-        return ld(bp, rowK, ri, c) * ld(kp, rowK, ri, c) * d;
-      });
-      qf[s] = Mma<E>::make([&](int e) {
-        const int c = c0 + e;
-        const float d = expf(s_gc[ri * GC_LD + c] - s_gc[r * GC_LD + c]);
-        return ld(qp, rowQ, ri, c) * a.scale * d;
-      });
-    }
-    E* aqk = static_cast<E*>(a.Aqk) + (((size_t)b * H + h) * NT + n) * C * C;
-    for (int J = 0; J < 4; ++J) {
-      f4 accA = f4_zero(), accQ = f4_zero();
-      if (J <= I) {
-        const int rj = 16 * J + (lane & 15);
-#pragma unroll
-        for (int s = 0; s < NKS; ++s) {
-          const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-          Frag kf = Mma<E>::make([&](int e) {
-            const int c = c0 + e;
-            const float x = s_gc[r * GC_LD + c] - s_gc[rj * GC_LD + c];
-            return ld(kp, rowK, rj, c) * expf(J < I ? x : fminf(x, 88.f));
-          });
-          accA = Mma<E>::mma(accA, lf[s], kf);
-          accQ = Mma<E>::mma(accQ, qf[s], kf);
-        }
-        if (J == I && !safe) {
-          // exact pairwise form for this diagonal tile
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int i = r + acc_row(rr), j = 16 * J + acc_col();
-            float sa = 0.f, sq = 0.f;
-            if (j <= i) {
-              for (int c = 0; c < K; ++c) {
-                const float d = expf(fminf(s_gc[i * GC_LD + c] - s_gc[j * GC_LD + c], 0.f));
-                const float kj = ld(kp, rowK, j, c);
-                sa += ld(bp, rowK, i, c) * ld(kp, rowK, i, c) * kj * d;
-                sq += ld(qp, rowQ, i, c) * kj * d;
-              }
-            }
-            accA[rr] = sa;
-            accQ[rr] = sq * a.scale;
-          }
-        }
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = r + acc_row(rr), j = 16 * J + acc_col();
-        s_A[i * AT_LD + j] = (j < i) ? accA[rr] : 0.f;
-        aqk[i * C + j] = from_f<E>((j <= i) ? accQ[rr] : 0.f);
-      }
-    }
-  }
+  // ---- 2. A and Aqk
+  l0_build_A(s_A, s_gc, in, static_cast<E*>(a.Aqk) + cix * C * C,
+             a.AqkT ? static_cast<E*>(a.AqkT) + cix * C * C : nullptr);
   __syncthreads();
 
-  // ---- 3. T = (I + A)^-1, by 16-row blocks
-  if (wv == 0) {
-    // diagonal blocks: lane = (block, column), forward substitution
-    const int I = lane >> 4, c = lane & 15, o = 16 * I;
-    float t[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float val = (i == c) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j)
-        if (j >= c) val -= s_A[(o + i) * AT_LD + o + j] * t[j];
-      t[i] = (i >= c) ? val : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s_T[(o + i) * AT_LD + o + c] = t[i];
-  } else {
-    // zero everything off the diagonal blocks; lower blocks are filled below
-    for (int e = tid - WAVE; e < C * C; e += 3 * WAVE) {
-      const int i = e / C, j = e % C;
-      if ((i >> 4) != (j >> 4)) s_T[i * AT_LD + j] = 0.f;
-    }
-  }
-  __syncthreads();
-  for (int d = 1; d < 4; ++d) {
-    const int nb = 4 - d;   // blocks (I, I-d), I = d..3
-    // P_IJ = sum_{M=J}^{I-1} A_IM T_MJ
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
-      const int I = d + blk, J = I - d;
-      float acc = 0.f;
-      for (int m = 16 * J; m < 16 * I; ++m)
-        acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * AT_LD + 16 * J + j];
-      s_P[blk * 272 + i * 17 + j] = acc;
-    }
-    __syncthreads();
-    // T_IJ = -T_II P_IJ
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
-      const int I = d + blk, J = I - d;
-      float acc = 0.f;
-#pragma unroll
-      for (int m = 0; m < 16; ++m)
-        acc += s_T[(16 * I + i) * AT_LD + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
-      s_T[(16 * I + i) * AT_LD + 16 * J + j] = -acc;
-    }
-    __syncthreads();
-  }
+  // ---- 3. T = (I + A)^-1
+  l0_invert(s_A, s_T, s_P);
   for (int e = tid; e < C * C; e += 256) {
     const int i = e / C, j = e % C;
     s_TE[i * LDX + j] = from_f<E>(s_T[i * AT_LD + j]);
+    if (a.TT) static_cast<E*>(a.TT)[cix * C * C + e] = from_f<E>(s_T[j * AT_LD + i]);
   }
   __syncthreads();
 
-  // ---- 4. right-hand sides, transposed: X[k][c] = b k e^gc, X[K+v][c] = w v
-  for (int e = tid; e < C * K; e += 256) {
-    const int c = e / K, kk = e % K;
-    const float x = ld(bp, rowK, c, kk) * ld(kp, rowK, c, kk) * expf(s_gc[c * GC_LD + kk]);
-    s_X[kk * LDX + c] = from_f<E>(x);
-  }
-  for (int e = tid; e < C * V; e += 256) {
-    const int c = e / V, vv = e % V;
-    s_X[(K + vv) * LDX + c] = from_f<E>(ld(wp, rowV, c, vv) * ld(vp, rowV, c, vv));
-  }
+  // ---- 4. right-hand sides, transposed
+  l0_build_X<E, K, V, LDX>(s_X, s_gc, in);
   __syncthreads();
 
   // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w
   {
     const int I = wv;
-    const int kd = min(C, ((16 * (I + 1) + Mma<E>::KS - 1) / Mma<E>::KS) * Mma<E>::KS);
-    E* Wo = static_cast<E*>(a.W) + (((size_t)b * H + h) * NT + n) * C * K;
-    E* Uo = static_cast<E*>(a.U) + (((size_t)b * H + h) * NT + n) * C * V;
+    const int kd = tri_depth<E>(I);
+    E* Wo = static_cast<E*>(a.W) + cix * C * K;
+    E* Uo = static_cast<E*>(a.U) + cix * C * V;
+    E* WTo = a.WT ? static_cast<E*>(a.WT) + cix * K * C : nullptr;
     for (int tc = 0; tc < (K + V) / 16; ++tc) {
       f4 acc = mma_tile<E>(f4_zero(), s_TE + 16 * I * LDX, LDX, s_X + 16 * tc * LDX, LDX, kd);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = 16 * I + acc_row(rr), col = 16 * tc + acc_col();
-        if (col < K) Wo[i * K + col] = from_f<E>(acc[rr]);
-        else Uo[i * V + (col - K)] = from_f<E>(acc[rr]);
+        if (col < K) {
+          Wo[i * K + col] = from_f<E>(acc[rr]);
+          if (WTo) WTo[col * C + i] = from_f<E>(acc[rr]);
+        } else {
+          Uo[i * V + (col - K)] = from_f<E>(acc[rr]);
+        }
       }
     }
   }
   __syncthreads();
 
-  // ---- 6. Kt^T, Qg, gam
-  E* s_kt = s_X;   // reuse: [K][LDX]
+  // ---- 6. Kt (and its transpose), Qg (and its transpose), gam
+  E* s_kt = s_X;             // reuse: [K][LDX]
+  E* s_qg = s_X + K * LDX;   // [K][LDX]; fits since (K + V) >= 2 K when V >= K,
+                             // otherwise Qg^T goes straight to global below
+  const bool qg_in_lds = V >= K;
   for (int e = tid; e < C * K; e += 256) {
     const int c = e / K, kk = e % K;
-    const float x = ld(kp, rowK, c, kk) * expf(s_gc[(C - 1) * GC_LD + kk] - s_gc[c * GC_LD + kk]);
-    s_kt[kk * LDX + c] = from_f<E>(x);
+    const float gcv = s_gc[c * GL + kk];
+    s_kt[kk * LDX + c] = from_f<E>(in.K_(c, kk) * expf(s_gc[(C - 1) * GL + kk] - gcv));
+    const float qg = in.Q_(c, kk) * in.scale * expf(gcv);
+    static_cast<E*>(a.Qg)[cix * C * K + c * K + kk] = from_f<E>(qg);
+    if (qg_in_lds) s_qg[kk * LDX + c] = from_f<E>(qg);
+    else if (a.QgT) static_cast<E*>(a.QgT)[cix * K * C + kk * C + c] = from_f<E>(qg);
   }
-  {
-    E* Qo = static_cast<E*>(a.Qg) + (((size_t)b * H + h) * NT + n) * C * K;
-    for (int e = tid; e < C * K; e += 256) {
-      const int c = e / K, kk = e % K;
-      Qo[c * K + kk] = from_f<E>(ld(qp, rowQ, c, kk) * a.scale * expf(s_gc[c * GC_LD + kk]));
-    }
-    if (tid < K)
-      a.gam[(((size_t)b * H + h) * NT + n) * K + tid] = expf(s_gc[(C - 1) * GC_LD + tid]);
-  }
+  if (tid < K) a.gam[cix * K + tid] = expf(s_gc[(C - 1) * GL + tid]);
   __syncthreads();
   {
-    E* Ko = static_cast<E*>(a.KtT) + (((size_t)b * H + h) * NT + n) * K * C;
+    E* Ko = static_cast<E*>(a.KtT) + cix * K * C;
+    E* QTo = a.QgT ? static_cast<E*>(a.QgT) + cix * K * C : nullptr;
     for (int e = tid; e < K * C; e += 256) {
       const int kk = e / C, c = e % C;
       Ko[kk * C + c] = s_kt[kk * LDX + c];
+      if (QTo && qg_in_lds) QTo[kk * C + c] = s_qg[kk * LDX + c];
+    }
+    if (a.Kt) {
+      E* Kn = static_cast<E*>(a.Kt) + cix * C * K;
+      for (int e = tid; e < C * K; e += 256) {
+        const int c = e / K, kk = e % K;
+        Kn[c * K + kk] = s_kt[kk * LDX + c];
+      }
     }
   }
 }

@@ -10,11 +10,14 @@ namespace ngdn {
 // q [B,T,H,L,K] (level-0 slice read), k, b [B,T,H,K], v, w [B,T,H,V] in the
 // working dtype, g [B,T,H,K] fp32. Outputs, per (b, h, chunk):
 // W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64], Qg [B,H,NT,64,K],
-// Aqk [B,H,NT,64,64] in the working dtype; gam [B,H,NT,K] fp32.
+// Aqk [B,H,NT,64,64] in the working dtype; gam [B,H,NT,K] fp32. When set,
+// the transposed copies for the reverse scan: Kt [B,H,NT,64,K],
+// WT [B,H,NT,K,64], QgT [B,H,NT,K,64], AqkT [B,H,NT,64,64].
 struct L0IntraArgs {
   const void* q; const void* k; const void* v; const float* g;
   const void* b; const void* w;
   void* W; void* U; void* KtT; void* Qg; void* Aqk; float* gam;
+  void* Kt; void* WT; void* QgT; void* AqkT; void* TT;
   int B, T, H, L, NT;
   float scale;
 };
@@ -36,6 +39,29 @@ struct ScanArgs {
   int B, H, S, M, V;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
+
+// Reverse of scan_fwd. Bop [B*H,S,M,K] (= BT^T: level 0 Kt, upper keys),
+// AT [B*H,S,K,M] (= A^T), gam [B*H,S,K]. Level 0 sets AqkT [B*H,S,64,64],
+// QgT [B*H,S,K,64], dout [B,T,H,V], mix [B,T,H,L] and inj (fp32
+// [B*H,inj_nf,K,V], added before step j when (j+1) % inj_every == 0). Upper
+// levels set d_states (fp32 [B,NG,H,K,V], added after step j, and for every
+// stored group past the last step before the first). d_final seeds the state
+// gradient. Outputs: dSp [B*H,S,K,V] (gradient of the state after each step;
+// dsp_mode 0 working dtype, 1 fp32), dVn [B*H,S,M,V] (dvn_mode likewise),
+// dinit (fp32 [K][V] at strides) when set.
+struct ScanBwdArgs {
+  const void* Bop; const void* AT; const float* gam;
+  const void* AqkT; const void* QgT; const void* dout; const void* mix; int T, L;
+  const float* inj; int inj_every, inj_nf;
+  const float* d_states; int NG;
+  const float* d_final; long long df_sb, df_sh;
+  void* dSp; int dsp_mode;
+  void* dVn; int dvn_mode;
+  void* dVnT;                 // optional: dVn^T [B*H,S,V,M], working dtype
+  float* dinit; long long di_sb, di_sh;
+  int B, H, S, M, V;
+};
+hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st);
 
 }  // namespace ngdn
 
@@ -59,10 +85,46 @@ struct ProbeArgs {
   const void* kp; const void* bpT; const void* wpT; const void* gpT;
   int merge;
   void* A; void* KT; void* U; float* gam;
+  void* keysN; void* AT;   // optional: keys [B,H,NF,N,K], A^T [B,H,NF,K,N] for the reverse scan
   float* keys; float* vals; float* bo; float* wo; float* go;
   int B, H, NF, N, V;
 };
 hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
+
+// Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
+// the autograd replay of ops/chunk.py:339-371,486-517, derived in closed
+// form). One workgroup per (batch, head, firing i). Inputs: the probe's
+// sources and parameters as for probe_fwd (plus kpT = key_proj^T [H,V,K] and
+// bankT [H,K,Nmax], original bp [H,V,K], wp [H,V,V], gp [H,V,K]); this
+// level's group states Sg fp32 [B,NG,H,K,V]; the reverse scan's dSp (fp32
+// [B,H,NF,K,V], gradient of the state after firing i) and dvn (fp32
+// [B,H,NF,N,V]). Workspace (working dtype, [B,H,NF,N,*]): Vals, du, dxb,
+// dxg [N,K-or-V], dxw, dVals [N,V]; the parameter-gradient reduction reads
+// them. dbank (fp32 [H,Nmax,K]) is accumulated atomically.
+// The gradient of the gathered lower state goes to: inj (level 1; fp32
+// [B,H,NF,K,V], written) or d_below (level >= 2; fp32 [B,NGb,H,K,V], added)
+// / d_below_fin (fp32 [K][V] at strides, added) when the firing reads the
+// lower final state.
+struct ProbeBwdArgs {
+  ProbeArgs f;                // below/params as in the forward (f.A .. unused)
+  const void* kpT; const void* bankT; const void* bp; const void* wp; const void* gp;
+  const float* Sg; int NG;
+  const float* dSp; const float* dvn;
+  void* wsV; void* wsdu; void* wsdxb; void* wsdxg; void* wsdxw; void* wsdV;
+  float* dbank;
+  float* inj; float* d_below; float* d_below_fin;
+};
+hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st);
+
+// C_h[X][Y] += sum over rows m = (b, i, n) of A[b,h,i,n,X] B[b,h,i,n,Y]
+// (working dtype in, fp32 out, accumulated atomically), for the per-head
+// parameter gradients of a level: one workgroup per (head, slice of items).
+struct AtBArgs {
+  const void* A; const void* Bm; float* C;
+  int B, H, NF, N, X, Y;
+  int split;
+};
+hipError_t atb_accumulate(const AtBArgs& a, int dtype, hipStream_t st);
 
 }  // namespace ngdn
 
@@ -85,5 +147,59 @@ struct OutputArgs {
   float scale;
 };
 hipError_t output_fwd(const OutputArgs& a, int dtype, int K, int V, hipStream_t st);
+
+// Backward of the output for one chunk (ops/chunk.py:423-449):
+//   dmix_l = <do, read_l>  for every level (reads recomputed as in output_fwd)
+//   dq_l   = scale (mix_l do) S_l[group]^T   for l >= 1
+// dq [B,T,H,L,K] receives levels >= 1 (working dtype); dmix [B,T,H,L] fp32.
+struct OutputBwdArgs {
+  OutputArgs f;
+  const void* dout;
+  void* dq; float* dmix;
+};
+hipError_t output_bwd(const OutputBwdArgs& a, int dtype, int K, int V, hipStream_t st);
+
+// Gradient of each upper level's group states from its reads
+// (read_level_bwd, ops/chunk.py:307-336):
+//   dS_l[j] = sum_{t in group j} scale q_l[t]^T (mix_l[t] do[t])
+// One workgroup per (batch, group, head); d_states fp32 [B,NG,H,K,V] written.
+struct ReadStateBwdArgs {
+  const void* q; const void* mix; const void* dout;
+  float* d_states;
+  int B, T, H, L, level, f, NG;
+  float scale;
+};
+hipError_t read_state_bwd(const ReadStateBwdArgs& a, int dtype, int K, int V, hipStream_t st);
+
+// Level-0 chunk backward, state-dependent half, per (b, h, chunk):
+//   dQg = dO S^T, dW = -dVn S^T, dKt = Vn dS'^T, dAqk = dO Vn^T (j <= i),
+//   dgam_k = sum_v dS'[k][v] S[k][v]
+// with S = h (hT), dS' the state gradient after the chunk, dO = mix_0 do.
+// Outputs dQg, dW, dKt [B,H,NT,64,K], dAqk [B,H,NT,64,64] (working dtype),
+// dgam [B,H,NT,K] fp32.
+struct L0BwdStateArgs {
+  const void* hT; const void* dSp; const void* vnT; const void* dVn;
+  const void* dout; const void* mix;
+  void* dQg; void* dWT; void* dKt; void* dAqk; float* dgam;
+  int B, T, H, L, NT;
+};
+hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStream_t st);
+
+// Level-0 chunk backward, intra-chunk half (through T = (I+A)^-1, the decay
+// products and the cumulative sum), per (b, h, chunk). Reads the forward's
+// W [.,64,K], U [.,64,V] and TT = T^T [.,64,64], the state half's dQg, dKt
+// [.,64,K], dWT = dW^T [.,K,64], dAqk [.,64,64], dgam [.,K], and the scan's
+// dVnT = dVn^T [.,V,64]. Writes dq[..., 0, :], dk, dv, db, dw (working dtype)
+// and dg (fp32).
+struct L0BwdIntraArgs {
+  const void* q; const void* k; const void* v; const float* g; const void* b; const void* w;
+  const void* W; const void* U; const void* TT;
+  const void* dQg; const void* dWT; const void* dKt; const void* dAqk; const float* dgam;
+  const void* dVnT;
+  void* dq; void* dk; void* dv; float* dg; void* db; void* dw;
+  int B, T, H, L, NT;
+  float scale;
+};
+hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
 }  // namespace ngdn

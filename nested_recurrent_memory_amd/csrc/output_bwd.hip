@@ -1,0 +1,224 @@
+// Backward of the output and of the upper-level reads
+// (nested_gdn2/ops/chunk.py:307-336 read_level_bwd, :423-449).
+//
+// output_bwd, per (batch, head, chunk):
+//   read_0 = Qg h_n + Aqk Vn,  read_l = scale q_l S_l[group]   (recomputed)
+//   dmix_l[t] = sum_v do[t][v] read_l[t][v]
+//   dq_l      = scale (mix_l do) S_l[group]^T        (l >= 1)
+// read_state_bwd, per (batch, group, head) of one level l >= 1:
+//   dS_l[j] = scale sum_{t in group j} q_l[t]^T (mix_l[t] do[t])
+#include "ngdn_kernels.h"
+
+namespace ngdn {
+
+template <typename E, int K, int V>
+__global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
+  const OutputArgs& a = ab.f;
+  constexpr int C = CH;
+  constexpr int LD = K + 8;
+  constexpr int LDV = V + 8;
+  constexpr int CTV = V / 16;
+  constexpr int CTK = K / 16;
+  constexpr size_t SZ_A = sizeof(E) * C * (LD > LDV ? LD : LDV);
+  constexpr size_t SZ_B = sizeof(E) * (V * LD > K * LDV ? V * LD : K * LDV);
+  __shared__ __attribute__((aligned(16))) char smem[SZ_A + SZ_B];
+  E* s_A = reinterpret_cast<E*>(smem);
+  E* s_B = reinterpret_cast<E*>(smem + SZ_A);
+
+  const int NT = a.NT, H = a.H, T = a.T, L = a.L;
+  const int n = blockIdx.x % NT;
+  const int bh = blockIdx.x / NT;
+  const int h = bh % H, b = bh / H;
+  const int t0 = n * C;
+  const int nvalid = min(C, T - t0);
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const size_t cix = ((size_t)bh * NT + n);
+
+  const E* mixp = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L;
+  const E* dop = static_cast<const E*>(ab.dout) + ((size_t)b * T * H + h) * V;
+  auto mixw = [&](int i, int l) -> float {
+    return i < nvalid ? to_f(mixp[(size_t)(t0 + i) * H * L + l]) : 0.f;
+  };
+  auto dov = [&](int i, int v) -> float {
+    return i < nvalid ? to_f(dop[(size_t)(t0 + i) * H * V + v]) : 0.f;
+  };
+
+  f4 acc[CTV];
+  auto run = [&](int kd) {
+#pragma unroll
+    for (int c = 0; c < CTV; ++c)
+      acc[c] = mma_tile<E>(acc[c], s_A + wv * 16 * LD, LD, s_B + c * 16 * LD, LD, kd);
+  };
+  // dmix[t, l] = sc * <do[t], acc[t]>; one lane group per row, no races
+  auto dmix = [&](int l, float sc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r);
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < CTV; ++c) s += dov(i, c * 16 + acc_col()) * acc[c][r];
+      s += __shfl_xor(s, 1, WAVE);
+      s += __shfl_xor(s, 2, WAVE);
+      s += __shfl_xor(s, 4, WAVE);
+      s += __shfl_xor(s, 8, WAVE);
+      if ((lane & 15) == 0 && i < nvalid)
+        ab.dmix[((size_t)b * T + t0 + i) * H * L + (size_t)h * L + l] = s * sc;
+    }
+  };
+
+  // ---- level 0 read
+#pragma unroll
+  for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
+  {
+    const E* Qg = static_cast<const E*>(a.Qg) + cix * C * K;
+    const E* hT = static_cast<const E*>(a.hT) + cix * V * K;
+    for (int e = tid; e < C * K; e += 256) s_A[(e / K) * LD + e % K] = Qg[e];
+    for (int e = tid; e < V * K; e += 256) s_B[(e / K) * LD + e % K] = hT[e];
+  }
+  __syncthreads();
+  run(K);
+  __syncthreads();
+  {
+    const E* Aq = static_cast<const E*>(a.Aqk) + cix * C * C;
+    const E* vT = static_cast<const E*>(a.vnT) + cix * V * C;
+    for (int e = tid; e < C * C; e += 256) s_A[(e / C) * LD + e % C] = Aq[e];
+    for (int e = tid; e < V * C; e += 256) s_B[(e / C) * LD + e % C] = vT[e];
+  }
+  __syncthreads();
+  run(C);
+  dmix(0, 1.f);
+  __syncthreads();
+
+  // ---- upper levels
+  const E* qb = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K;
+  E* dqb = static_cast<E*>(ab.dq) + ((size_t)b * T * H + h) * L * K;
+  for (int l = 1; l < L; ++l) {
+    const int grp = n / a.f[l];
+    const float* S = a.states[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * K * V;
+    for (int e = tid; e < C * K; e += 256) {
+      const int i = e / K, k = e % K;
+      s_A[i * LD + k] = i < nvalid ? qb[(size_t)(t0 + i) * H * L * K + (size_t)l * K + k] : from_f<E>(0.f);
+    }
+    for (int e = tid; e < K * V; e += 256) {
+      const int k = e / V, v = e % V;
+      s_B[v * LD + k] = from_f<E>(S[e]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
+    run(K);
+    dmix(l, a.scale);
+    __syncthreads();
+    // dq_l = scale (mix_l do) S^T: A = mix_l do [C][V], Bt = S [K][V]
+    for (int e = tid; e < K * V; e += 256) s_B[(e / V) * LDV + e % V] = from_f<E>(S[e]);
+    for (int e = tid; e < C * V; e += 256) {
+      const int i = e / V, v = e % V;
+      s_A[i * LDV + v] = from_f<E>(dov(i, v) * mixw(i, l));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CTK; ++c) {
+      f4 d = mma_tile<E>(f4_zero(), s_A + wv * 16 * LDV, LDV, s_B + c * 16 * LDV, LDV, V);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wv * 16 + acc_row(r);
+        if (i < nvalid)
+          dqb[(size_t)(t0 + i) * H * L * K + (size_t)l * K + c * 16 + acc_col()] =
+              from_f<E>(d[r] * a.scale);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename E, int K, int V>
+__global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a) {
+  constexpr int C = CH;
+  constexpr int LD = C + 8;
+  constexpr int TPW = (K / 16) * (V / 16) / 4;
+  __shared__ __attribute__((aligned(16))) E s_qT[K * LD];
+  __shared__ __attribute__((aligned(16))) E s_dT[V * LD];
+
+  const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
+  const int j = blockIdx.x % NG;
+  const int bh = blockIdx.x / NG;
+  const int h = bh % H, b = bh / H;
+  const int wv = wave_id(), tid = threadIdx.x;
+  const int NT = (T + C - 1) / C;
+  const E* qb = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K + (size_t)l * K;
+  const E* mb = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L + l;
+  const E* db = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V;
+
+  f4 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = f4_zero();
+  const int n1 = min((j + 1) * a.f, NT);
+  for (int n = j * a.f; n < n1; ++n) {
+    const int t0 = n * C;
+    for (int e = tid; e < C * K; e += 256) {
+      const int c = e / K, k = e % K, t = t0 + c;
+      s_qT[k * LD + c] = t < T ? qb[(size_t)t * H * L * K + k] : from_f<E>(0.f);
+    }
+    for (int e = tid; e < C * V; e += 256) {
+      const int c = e / V, v = e % V, t = t0 + c;
+      float x = 0.f;
+      if (t < T) x = to_f(db[(size_t)t * H * V + v]) * to_f(mb[(size_t)t * H * L]);
+      s_dT[v * LD + c] = from_f<E>(x);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / (V / 16), ct = g % (V / 16);
+      acc[i] = mma_tile<E>(acc[i], s_qT + rt * 16 * LD, LD, s_dT + ct * 16 * LD, LD, C);
+    }
+    __syncthreads();
+  }
+  float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int g = wv * TPW + i, rt = g / (V / 16), ct = g % (V / 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      out[(size_t)(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = acc[i][r] * a.scale;
+  }
+}
+
+template <typename E, int K, int V>
+static hipError_t launch_output_bwd(const OutputBwdArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.f.B * a.f.H * a.f.NT);
+  hipLaunchKernelGGL((output_bwd_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t output_bwd(const OutputBwdArgs& a, int dtype, int K, int V, hipStream_t st) {
+#define NGDN_OB(E, KK, VV) \
+  if (K == KK && V == VV) return launch_output_bwd<E, KK, VV>(a, st);
+  if (dtype == NGDN_BF16) {
+    NGDN_OB(bf16, 64, 64) NGDN_OB(bf16, 128, 128)
+  } else {
+    NGDN_OB(float, 64, 64) NGDN_OB(float, 128, 128)
+  }
+#undef NGDN_OB
+  return hipErrorInvalidValue;
+}
+
+template <typename E, int K, int V>
+static hipError_t launch_read_state_bwd(const ReadStateBwdArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * a.NG);
+  hipLaunchKernelGGL((read_state_bwd_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t read_state_bwd(const ReadStateBwdArgs& a, int dtype, int K, int V, hipStream_t st) {
+#define NGDN_RS(E, KK, VV) \
+  if (K == KK && V == VV) return launch_read_state_bwd<E, KK, VV>(a, st);
+  if (dtype == NGDN_BF16) {
+    NGDN_RS(bf16, 64, 64) NGDN_RS(bf16, 128, 128)
+  } else {
+    NGDN_RS(float, 64, 64) NGDN_RS(float, 128, 128)
+  }
+#undef NGDN_RS
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ngdn

@@ -189,8 +189,11 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
       float key;
       if (MERGE) key = (n == k) ? 1.f : 0.f;
       else key = ut[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
-      Ao[n * K + k] = from_f<E>(key * bt[t][r] * gam);
-      KTo[k * N + n] = from_f<E>(key);
+      const E av = from_f<E>(key * bt[t][r] * gam), kv = from_f<E>(key);
+      Ao[n * K + k] = av;
+      KTo[k * N + n] = kv;
+      if (a.AT) static_cast<E*>(a.AT)[fo * K * N + k * N + n] = av;
+      if (a.keysN) static_cast<E*>(a.keysN)[fo * N * K + n * K + k] = kv;
       if (a.keys) a.keys[ro * N * K + n * K + k] = key;
       if (a.bo) a.bo[ro * N * K + n * K + k] = bt[t][r];
     }

@@ -37,12 +37,12 @@ def test_library_exports_every_declared_symbol():
 def test_invalid_arguments_return_error_without_launch():
     so = _lib.lib()
     d = _lib.dims(1, 64, 1, 1, 96, 64, _lib.NGDN_BF16, 0.1)   # K=96 unsupported
-    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 12), None)
+    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 18))
     assert rc == 1
     assert b"K=96" in so.ngdn_last_error()
     d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
     rc = so.ngdn_probe_fwd(ctypes.byref(d), 1, 0, 24, 1, 2, None, 0, None, None, 32,
-                           *([None] * 14))
+                           *([None] * 16))
     assert rc == 1 and b"power of two" in so.ngdn_last_error()
 
 

@@ -46,11 +46,14 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     g = {n: inp[n].to("cuda").contiguous() for n in ("q", "k", "v", "g", "b", "w")}
     e = lambda *s, dt=dtype: torch.empty(*s, device="cuda", dtype=dt)  # noqa: E731
     out = dict(W=e(B, H, NT, 64, K), U=e(B, H, NT, 64, V), KtT=e(B, H, NT, K, 64),
-               Qg=e(B, H, NT, 64, K), Aqk=e(B, H, NT, 64, 64), gam=e(B, H, NT, K, dt=torch.float32))
+               Qg=e(B, H, NT, 64, K), Aqk=e(B, H, NT, 64, 64), gam=e(B, H, NT, K, dt=torch.float32),
+               Kt=e(B, H, NT, 64, K), WT=e(B, H, NT, K, 64), QgT=e(B, H, NT, K, 64),
+               AqkT=e(B, H, NT, 64, 64))
     d = _lib.dims(B, T, H, L, K, V, code, scale)
     P = _lib.ptr
     _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(g[n]) for n in ("q", "k", "v", "g", "b", "w")),
-              *(P(out[n]) for n in ("W", "U", "KtT", "Qg", "Aqk", "gam")), _lib.stream_of(g["q"]))
+              *(P(out[n]) for n in ("W", "U", "KtT", "Qg", "Aqk", "gam")),
+              *(P(out[n]) for n in ("Kt", "WT", "QgT", "AqkT")), _lib.stream_of(g["q"]))
     torch.cuda.synchronize()
 
     pad = NT * 64 - T
@@ -70,6 +73,11 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     torch.testing.assert_close(got["KtT"], t["Kt"].transpose(-1, -2), **tol)
     torch.testing.assert_close(got["W"], t["W"], **tol)
     torch.testing.assert_close(got["U"], t["U"], **tol)
+    # transposed copies are exact copies
+    assert torch.equal(got["Kt"], got["KtT"].transpose(-1, -2))
+    assert torch.equal(got["WT"], got["W"].transpose(-1, -2))
+    assert torch.equal(got["QgT"], got["Qg"].transpose(-1, -2))
+    assert torch.equal(got["AqkT"], got["Aqk"].transpose(-1, -2))
 
 
 # ------------------------------------------------------------- whole forward
