@@ -257,8 +257,6 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
               P(sv["W"]), P(sv["U"]), P(sv["TT"]), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam),
               P(dVnT0), P(dq), P(dk), P(dv), P(dg), P(db), P(dw), st)
-    if dqb is not None:
-        dqb = dqb[:, :, :par["qb"].shape[2]]
     return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
 
 
@@ -307,6 +305,7 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         out = [dq, dk, dv, dg, db, dw, dmix]
         out = [x.to(dt) for x, dt in zip(out, dts[:7])]
         if L > 1:
+            dqb = dqb[:, :, :ctx.nmax]          # drop the alignment padding rows
             out += [x.to(dt) for x, dt in zip((dqb, dkp, dbp, dwp, dgp), dts[7:12])]
         else:
             out += [None] * 5

@@ -231,13 +231,18 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
       for (int ct = 0; ct < CTK; ++ct) {
         const int kc = ct * 16 + (lane & 15);
-        const Frag fb = Mma<E>::make([&](int e) {
+        Frag fb, fl;
+        Mma<E>::make_split([&](int e) {
           const int j = j0 + e;
           if (j >= jlim) return 0.f;
           return in.K_(j, kc) * expf(fminf(s_gc[R0 * GL + kc] - s_gc[j * GL + kc], 88.f));
-        });
+        }, fb, fl);
         dbk[ct] = Mma<E>::mma(dbk[ct], fa, fb);
         dqa[ct] = Mma<E>::mma(dqa[ct], fq, fb);
+        if (Mma<E>::SPLIT) {
+          dbk[ct] = Mma<E>::mma(dbk[ct], fa, fl);
+          dqa[ct] = Mma<E>::mma(dqa[ct], fq, fl);
+        }
       }
     }
 #pragma unroll
@@ -279,18 +284,23 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
       for (int ct = 0; ct < CTK; ++ct) {
         const int kc = ct * 16 + (lane & 15);
-        const Frag fbb = Mma<E>::make([&](int e) {
+        Frag fbb, fbl, fqb, fql;
+        Mma<E>::make_split([&](int e) {
           const int i = ib + e;
           if (i < ilo) return 0.f;
           return in.B_(i, kc) * in.K_(i, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
-        });
-        const Frag fbq = Mma<E>::make([&](int e) {
+        }, fbb, fbl);
+        Mma<E>::make_split([&](int e) {
           const int i = ib + e;
           if (i < ilo) return 0.f;
           return in.Q_(i, kc) * in.scale * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
-        });
+        }, fqb, fql);
         dka[ct] = Mma<E>::mma(dka[ct], fa, fbb);
-        dka[ct] = Mma<E>::mma(dka[ct], fq, fbq);
+        dka[ct] = Mma<E>::mma(dka[ct], fq, fqb);
+        if (Mma<E>::SPLIT) {
+          dka[ct] = Mma<E>::mma(dka[ct], fa, fbl);
+          dka[ct] = Mma<E>::mma(dka[ct], fq, fql);
+        }
       }
     }
 #pragma unroll

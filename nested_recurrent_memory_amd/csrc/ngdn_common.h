@@ -53,6 +53,19 @@ template <> struct Mma<bf16> {
     for (int e = 0; e < 8; ++e) r[e] = (bf16)f(e);
     return r;
   }
+  // x = hi + lo to about 16 mantissa bits: products against an operand built
+  // this way keep fp32-level agreement between sums that must cancel.
+  template <typename F>
+  __device__ __forceinline__ static void make_split(F f, Frag& hi, Frag& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = f(e);
+      const bf16 h = (bf16)x;
+      hi[e] = h;
+      lo[e] = (bf16)(x - (float)h);
+    }
+  }
+  static constexpr bool SPLIT = true;
 };
 
 template <> struct Mma<float> {
@@ -65,6 +78,12 @@ template <> struct Mma<float> {
   __device__ __forceinline__ static Frag load(const float* p) { return *p; }
   template <typename F>
   __device__ __forceinline__ static Frag make(F f) { return f(0); }
+  template <typename F>
+  __device__ __forceinline__ static void make_split(F f, Frag& hi, Frag& lo) {
+    hi = f(0);
+    lo = 0.f;
+  }
+  static constexpr bool SPLIT = false;
 };
 
 template <typename E> __device__ __forceinline__ int kofs(int lane) {

@@ -73,8 +73,13 @@ def _run(inp, L, promotion, dtype, init=None, with_dfinal=False, seed=1):
 
 
 def _check(ours, want, dtype):
+    errors = []
     for n in want:
-        _close(n, ours[n], want[n], dtype)
+        try:
+            _close(n, ours[n], want[n], dtype)
+        except AssertionError as e:
+            errors.append(str(e))
+    assert not errors, "\n".join(errors)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
