@@ -1,0 +1,264 @@
+"""Benchmark of the nested GDN op, forward + backward, on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+A step is one forward and one backward of ``chunk_nested_gdn2`` over one
+batch of synthetic inputs at the configuration BASELINE.json quotes its
+metric on (c2: B=4, T=8192, H=16, K=V=128, 3 levels firing every 1/4/16
+chunks, 64 queries per level, bf16 inputs, fp32 state). Inputs are already
+resident in HBM when the timed region starts. Prints one JSON line.
+
+The line carries:
+  roofline      the dominant kernel (entry point) of the step: its algorithmic
+                bytes or flops per launch divided by its average launch time,
+                timed with events on the launch stream over the timed region;
+  cpu_baseline  the CPU restatement (oracle/ngdn_oracle.py, float32 PyTorch)
+                timed on a bounded sample of the same workload, extrapolated.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from nested_recurrent_memory_amd import _lib, chunk_nested_gdn2  # noqa: E402
+from nested_recurrent_memory_amd.inputs import CONFIGS, LEAVES  # noqa: E402
+from nested_recurrent_memory_amd.schedule import n_firings, n_groups  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, GB/s
+MFMA_BF16_TFLOPS = 2500.0        # dense bf16
+MFMA_FP32_TFLOPS = 157.3
+
+
+def gpu_inputs(cfg, seed=0):
+    """Inputs of the configuration's distributions, drawn on the GPU."""
+    B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
+    dt = cfg["dtype"]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g, device="cuda", dtype=torch.float32)  # noqa: E731
+    F = torch.nn.functional
+    inp = dict(
+        q=F.normalize(r(B, T, H, L, K), dim=-1).to(dt),
+        k=F.normalize(r(B, T, H, K), dim=-1).to(dt),
+        v=r(B, T, H, V).to(dt),
+        g=-F.softplus(r(B, T, H, K)) * cfg["g_scale"],
+        b=torch.sigmoid(r(B, T, H, K)).to(dt),
+        w=torch.sigmoid(r(B, T, H, V)).to(dt),
+        mix_weights=torch.softmax(r(B, T, H, L), dim=-1).to(dt),
+        query_banks=(r(L - 1, H, N, K) * K ** -0.5).to(dt),
+        key_projections=(r(L - 1, H, K, V) * V ** -0.5).to(dt),
+        b_projections=(r(L - 1, H, V, K) * V ** -0.5).to(dt),
+        w_projections=(r(L - 1, H, V, V) * V ** -0.5).to(dt),
+        g_projections=(r(L - 1, H, V, K) * V ** -0.5).to(dt),
+        n_queries_per_level=tuple([N] * (L - 1)),
+        firing_intervals=tuple(cfg["intervals"]),
+    )
+    return inp
+
+
+def work_model(cfg):
+    """Algorithmic bytes and flops per launch of each entry point at cfg (one
+    fwd+bwd step), from the tensors each reads and writes once and its dense
+    tile products (2 m n k). Units: bytes, flop."""
+    B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
+    f = cfg["intervals"]
+    es = 2 if cfg["dtype"] == torch.bfloat16 else 4
+    C = 64
+    NT = -(-T // C)
+    units = B * H * NT                       # chunk-heads
+    ck, cv, cc = C * K * es, C * V * es, C * C * es
+    kv_e, kv_f = K * V * es, K * V * 4
+    m = {}
+    # level-0 intra: reads q0,k,b,v,w + g (fp32); writes W,U,KtT,Qg,Aqk,gam
+    # and the backward layouts Kt, WT, QgT, AqkT, TT
+    m["ngdn_l0_intra_fwd"] = (
+        units * (3 * ck + 2 * cv + C * K * 4 + 4 * ck + cv + cc + K * 4 + 3 * ck + 2 * cc),
+        units * (2 * 2 * C * C * K + 2 * C * C * (K + V) + C ** 3 // 3))
+    # level-0 scan: reads W, U, KtT, gam; writes hT, vnT; + final
+    m["ngdn_l0_scan_fwd"] = (units * (2 * ck + cv + K * 4 + kv_e + cv) + B * H * kv_f,
+                             units * 2 * 2 * C * K * V)
+    # output: Qg, hT, Aqk, vnT, q of upper levels, mix; upper states once per group; o
+    up_states = sum(B * H * n_groups(NT, f[l]) * kv_f for l in range(1, L))
+    m["ngdn_output_fwd"] = (
+        units * (ck + kv_e + cc + cv + (L - 1) * ck + C * L * es + cv) + up_states,
+        units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 2 * C * K * V))
+    m["ngdn_output_bwd"] = (
+        units * (ck + kv_e + cc + cv + (L - 1) * ck + C * L * es + cv + (L - 1) * ck + C * L * 4)
+        + up_states,
+        units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 4 * C * K * V))
+    # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
+    m["ngdn_l0_scan_bwd"] = (units * (3 * ck + cc + K * 4 + cv + C * es + kv_e + 2 * cv),
+                             units * (2 * C * K * V * 3 + 2 * C * C * V))
+    # level-0 chunk backward, state half: hT, dSp, vnT, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
+    m["ngdn_l0_bwd_state"] = (units * (2 * kv_e + 3 * cv + C * es + 3 * ck + cc + K * 4),
+                              units * (3 * 2 * C * K * V + 2 * C * C * V))
+    # level-0 chunk backward, intra half: q0,k,b,v,w,g, W,U,TT, dQg,dWT,dKt,dAqk,dgam,dVnT
+    # -> dq0,dk,dv,dg,db,dw
+    m["ngdn_l0_bwd_intra"] = (
+        units * (3 * ck + 2 * cv + C * K * 4 + ck + cv + cc + 3 * ck + cc + K * 4 + cv
+                 + 3 * ck + 2 * cv + C * K * 4),
+        units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
+    for lvl in range(1, L):
+        nf = n_firings(NT, f[lvl])
+        fu = B * H * nf
+        nk = N * K * es
+        m[f"ngdn_probe_fwd.{lvl}"] = (fu * (kv_e + 3 * nk + 4 * K) + H * (N * K + 4 * K * V) * es,
+                                      fu * 5 * 2 * N * K * V)
+        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * n_groups(NT, f[lvl]) * kv_f,
+                                           fu * 2 * 2 * N * K * V)
+    return m, units
+
+
+def step_fn(inp, leaves, L, do):
+    def step():
+        o, _ = chunk_nested_gdn2(**{**inp, **leaves}, L=L)
+        o.backward(do)
+    return step
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """The CPU restatement (float32 PyTorch) on one-head slices of the
+    workload, forward + backward, extrapolated to the whole step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ngdn_oracle
+
+    from nested_recurrent_memory_amd.inputs import make_cotangent, make_inputs
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    B, T, H = cfg["B"], cfg["T"], cfg["H"]
+    one = dict(cfg)
+    one.update(B=1, H=1)
+    done, t_total, slices = 0, 0.0, 0
+    while t_total < budget_s and slices < B * H:
+        inp = make_inputs(**one, seed=slices)
+        lv = {n: inp[n].float().requires_grad_(True) for n in LEAVES}
+        args = [lv[n] for n in LEAVES] + [inp["n_queries_per_level"], inp["firing_intervals"]]
+        t0 = time.perf_counter()
+        o, _ = ngdn_oracle.chunk_forward(*args, L=cfg["L"], output_final_state=True,
+                                         dtype=torch.float32, out_dtype=torch.float32)
+        o.backward(make_cotangent(o.shape))
+        t_total += time.perf_counter() - t0
+        slices += 1
+        done += T
+    per_slice = t_total / slices
+    full = per_slice * B * H
+    return {"value": B * T / full, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{slices} of the {B * H} (batch, head) slices (T={T}) forward+backward, "
+                      f"{t_total:.1f} s, scaled by {B * H}/{slices}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-table", action="store_true",
+                    help="also print per-entry-point times to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the op shards by batch or head with no communication inside it)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = dict(CONFIGS[args.config])
+    L = cfg["L"]
+    inp = gpu_inputs(cfg)
+    leaves = {n: inp[n].detach().clone().requires_grad_(True) for n in LEAVES}
+    B, T, H, V = cfg["B"], cfg["T"], cfg["H"], cfg["V"]
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    do = torch.randn(B, T, H, V, generator=gen, device="cuda").to(cfg["dtype"])
+    step = step_fn(inp, leaves, L, do)
+
+    for _ in range(args.warmup):
+        step()
+        for t in leaves.values():
+            t.grad = None
+    torch.cuda.synchronize()
+
+    _lib.TIMING = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        for t in leaves.values():
+            t.grad = None
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timing, _lib.TIMING = _lib.TIMING, None
+
+    ms = {}
+    for name, evs in timing.items():
+        ms[name] = sum(s.elapsed_time(e) for s, e in evs) / len(evs)
+    per_step = {n: sum(s.elapsed_time(e) for s, e in evs) / args.steps for n, evs in timing.items()}
+
+    model, units = work_model(cfg)
+    # per-launch algorithmic work of each entry point; upper levels keyed by
+    # level, in call order within a step
+    dom = max(per_step, key=per_step.get)
+    dom_work = model.get(dom)
+    roof = None
+    if dom_work is not None:
+        nbytes, flops = dom_work
+        t = ms[dom] * 1e-3
+        gbs = nbytes / t / 1e9
+        tfs = flops / t / 1e12
+        peak_f = MFMA_BF16_TFLOPS if cfg["dtype"] == torch.bfloat16 else MFMA_FP32_TFLOPS
+        hbm_bound = (nbytes / (HBM_PEAK_GBS * 1e9)) >= (flops / (peak_f * 1e12))
+        if hbm_bound:
+            roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "algorithmic_bytes": nbytes, "avg_ms": round(ms[dom], 4)}
+        else:
+            roof = {"kernel": dom, "bound": "mfma", "achieved": round(tfs, 2), "peak": peak_f,
+                    "unit": "TFLOP/s", "frac": round(tfs / peak_f, 4), "traffic": None,
+                    "algorithmic_flops": flops, "avg_ms": round(ms[dom], 4)}
+    if args.kernel_table:
+        for n in sorted(per_step, key=per_step.get, reverse=True):
+            w = model.get(n)
+            extra = ""
+            if w:
+                t = ms[n] * 1e-3
+                extra = f"  {w[0] / t / 1e9:8.1f} GB/s  {w[1] / t / 1e12:7.2f} TFLOP/s"
+            print(f"{n:28s} {per_step[n]:8.3f} ms/step  {ms[n]:8.3f} ms/launch{extra}",
+                  file=sys.stderr)
+
+    ms_step = elapsed / args.steps * 1e3
+    tokens = B * T * args.steps
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
+    line = {
+        "metric": "tokens/s fwd+bwd nested GDN op (B4,T8192,H16,d128,3 lvl)",
+        "value": round(tokens / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: chunk_nested_gdn2 forward+backward", "B": B,
+                   "T": T, "H": H, "K": cfg["K"], "V": V, "L": L,
+                   "firing_intervals": list(cfg["intervals"]), "n_queries": cfg["N"],
+                   "chunk": 64, "state": "fp32"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -77,8 +77,24 @@ def lib():
     return _lib
 
 
-def call(name, *args):
-    rc = getattr(lib(), name)(*args)
+# When set to a dict, every entry point call is bracketed by two timing events
+# recorded on torch's current stream (the stream the kernels are launched on):
+# TIMING[name] collects (start, end) event pairs.
+TIMING = None
+
+
+def call(name, *args, tag=None):
+    """Calls entry point ``name``; raises NgdnError on a nonzero status.
+    ``tag`` names the call in TIMING (default: the entry point)."""
+    if TIMING is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        rc = getattr(lib(), name)(*args)
+        end.record()
+        TIMING.setdefault(tag or name, []).append((start, end))
+    else:
+        rc = getattr(lib(), name)(*args)
     if rc != 0:
         msg = lib().ngdn_last_error().decode()
         raise NgdnError(f"{name} failed ({rc}): {msg}")

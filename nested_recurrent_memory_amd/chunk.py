@@ -128,10 +128,12 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
             _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
                       P(below), ngb, P(final), P(par["qb"]), par["nmax"], P(par["kp"]),
                       P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(A_), P(KT_), P(U_),
-                      P(gm_), P(keysN), P(AT_), None, None, None, None, None, st)
+                      P(gm_), P(keysN), P(AT_), None, None, None, None, None, st,
+                      tag=f"ngdn_probe_fwd.{lvl}")
         S_l = torch.empty(B, ng, H, K, V, device=dev, dtype=torch.float32)
         _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, N, nf, ng, P(A_), P(KT_),
-                  P(U_), P(gm_), P(init_), P(S_l), P(final), st)
+                  P(U_), P(gm_), P(init_), P(S_l), P(final), st,
+                  tag=f"ngdn_upper_scan_fwd.{lvl}")
         states[lvl] = S_l
         levels[lvl] = dict(N=N, nf=nf, ng=ng, keys=keysN, AT=AT_, gam=gm_)
 
@@ -207,7 +209,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         ng = n_groups(NT, f[lvl])
         d_states[lvl] = e(B, ng, H, K, V, dt=torch.float32)
         _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng, P(q_), P(mix_),
-                  P(do_), P(d_states[lvl]), st)
+                  P(do_), P(d_states[lvl]), st, tag=f"ngdn_read_state_bwd.{lvl}")
 
     dqb = dkp = dbp = dwp = dgp = None
     inj, nf1 = None, 0
@@ -224,7 +226,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         dvn = e(B, H, nfa, N, V, dt=torch.float32)
         _lib.call("ngdn_upper_scan_bwd", ctypes.byref(d), lvl, N, nf, ng, P(lv["keys"]),
                   P(lv["AT"]), P(lv["gam"]), P(d_states[lvl]), P(d_final), P(dSp), P(dvn),
-                  P(d_init), st)
+                  P(d_init), st, tag=f"ngdn_upper_scan_bwd.{lvl}")
         if nf == 0:
             continue
         ws = [e(B, H, nf, N, K) for _ in range(4)] + [e(B, H, nf, N, V) for _ in range(2)]
@@ -239,9 +241,10 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                   P(par["wpT"]), P(par["gpT"]), P(par["kpT"]), P(par["bankT"]), P(par["bp"]),
                   P(par["wp"]), P(par["gp"]), P(states[lvl]), ng, P(dSp), P(dvn),
                   *(P(x) for x in ws), P(dqb), P(inj if lvl == 1 else None), P(d_below),
-                  P(d_final), st)
+                  P(d_final), st, tag=f"ngdn_probe_bwd.{lvl}")
         _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf, P(ws[0]),
-                  P(ws[1]), P(ws[2]), P(ws[3]), P(ws[4]), P(dkp), P(dbp), P(dwp), P(dgp), st)
+                  P(ws[1]), P(ws[2]), P(ws[3]), P(ws[4]), P(dkp), P(dbp), P(dwp), P(dgp), st,
+                  tag=f"ngdn_param_grads.{lvl}")
 
     # level 0
     dSp0, dVn0, dVnT0 = e(B, H, NT, K, V), e(B, H, NT, 64, V), e(B, H, NT, V, 64)
