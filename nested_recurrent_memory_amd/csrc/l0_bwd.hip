@@ -118,20 +118,30 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr int LDK = K + 8, LDV = V + 8;
   constexpr int CTK = K / 16, CTV = V / 16;
   constexpr int KS = Mma<E>::KS;
+  // bf16: the chunk's k, b, q rows are staged in LDS; fp32 (a test-only path)
+  // reads them from global memory to stay inside the LDS budget
+  constexpr bool STAGE = !std::is_same<E, float>::value;
   typedef typename Mma<E>::Frag Frag;
+  typedef Mma<float> MF;
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_DX = sizeof(E) * C * (LDK + LDV);
-  constexpr size_t SZ_DG = sizeof(float) * C * GL;
-  constexpr size_t SZ_R = SZ_DX > SZ_DG ? SZ_DX : SZ_DG;
+  constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDK : 0;
   constexpr size_t SZ_DA = sizeof(float) * 2 * C * AT_LD;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R + SZ_DA + sizeof(float) * K];
+  constexpr int RW = (LDK + LDV) > 2 * LDK ? (LDK + LDV) : 2 * LDK;
+  constexpr size_t SZ_R = sizeof(E) * C * RW;
+  static_assert(C * GL <= 2 * C * AT_LD, "dgc must fit the dA region");
+  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_IN + SZ_DA + SZ_R + sizeof(float) * K];
   float* s_gc = reinterpret_cast<float*>(smem);
-  E* s_dXw = reinterpret_cast<E*>(smem + SZ_GC);
-  E* s_dXu = s_dXw + C * LDK;
-  float* s_dgc = reinterpret_cast<float*>(smem + SZ_GC);
-  float* s_dA = reinterpret_cast<float*>(smem + SZ_GC + SZ_R);
+  E* s_k = reinterpret_cast<E*>(smem + SZ_GC);
+  E* s_b = s_k + C * LDK;
+  E* s_q = s_b + C * LDK;
+  float* s_dA = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN);
   float* s_dQ = s_dA + C * AT_LD;
-  float* s_col = s_dQ + C * AT_LD;
+  float* s_dgc = s_dA;                       // after the decay backward
+  E* s_dXw = reinterpret_cast<E*>(smem + SZ_GC + SZ_IN + SZ_DA);
+  E* s_dXu = s_dXw + C * LDK;
+  E* s_dQg = s_dXw;                          // after the dA product
+  E* s_dKt = s_dXw + C * LDK;
+  float* s_col = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN + SZ_DA + SZ_R);
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -143,7 +153,22 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, T, H, a.L, a.scale);
   const int t0 = in.t0, nvalid = in.nvalid;
 
-  // ---- 1. gc, dAqk (fp32 in LDS)
+  auto KV = [&](int i, int c) -> float {
+    if constexpr (STAGE) return to_f(s_k[i * LDK + c]); else return in.K_(i, c);
+  };
+  auto BV = [&](int i, int c) -> float {
+    if constexpr (STAGE) return to_f(s_b[i * LDK + c]); else return in.B_(i, c);
+  };
+  auto QV = [&](int i, int c) -> float {
+    if constexpr (STAGE) return to_f(s_q[i * LDK + c]); else return in.Q_(i, c);
+  };
+
+  // ---- 1. gc, the chunk's rows, dAqk (fp32 in LDS)
+  if constexpr (STAGE) {
+    stage_rows<E>(s_k, LDK, in.k + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
+    stage_rows<E>(s_b, LDK, in.b + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
+    stage_rows<E>(s_q, LDK, in.q + (size_t)t0 * in.rowQ, in.rowQ, C, K, nvalid);
+  }
   l0_cumsum(s_gc, in);
   {
     const E* dq = static_cast<const E*>(a.dAqk) + cix * C * C;
@@ -211,38 +236,30 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     }
   }
   __syncthreads();
+  // dQg and dKt of this chunk, for the final assembly
+  stage_rows<E>(s_dQg, LDK, static_cast<const E*>(a.dQg) + cix * C * K, K, C, K, C);
+  stage_rows<E>(s_dKt, LDK, static_cast<const E*>(a.dKt) + cix * C * K, K, C, K, C);
 
   const bool safe = l0_block_safe<K>(s_gc, wv);
   const int R0 = 16 * wv;
 
-  // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w:
+  // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w
   //   sum_j dA_ij k_j e^(gc_i - gc_j) = e^(gc_i - gc_r) sum_j dA_ij [k_j e^(gc_r - gc_j)]
+  // on fp32 MFMA: these sums cancel against those of 4b inside dg
   f4 dbk[CTK], dqa[CTK];
 #pragma unroll
   for (int ct = 0; ct < CTK; ++ct) { dbk[ct] = f4_zero(); dqa[ct] = f4_zero(); }
   {
-    const int jmax = 16 * (wv + 1);
-    const int jlim = safe ? jmax : R0;           // unsafe: diagonal block done exactly below
-    const int nst = (jmax + KS - 1) / KS;
-    for (int s = 0; s < nst; ++s) {
-      const int j0 = s * KS + kofs<E>(lane);
-      const Frag fa = Mma<E>::make([&](int e) { return j0 + e < jlim ? s_dA[ri * AT_LD + j0 + e] : 0.f; });
-      const Frag fq = Mma<E>::make([&](int e) { return j0 + e < jlim ? s_dQ[ri * AT_LD + j0 + e] : 0.f; });
+    const int jlim = safe ? R0 + 16 : R0;     // unsafe: diagonal block done exactly below
+    for (int j0 = 0; j0 < jlim; j0 += MF::KS) {
+      const int j = j0 + (lane >> 4);
+      const float fa = s_dA[ri * AT_LD + j], fq = s_dQ[ri * AT_LD + j];
 #pragma unroll
       for (int ct = 0; ct < CTK; ++ct) {
         const int kc = ct * 16 + (lane & 15);
-        Frag fb, fl;
-        Mma<E>::make_split([&](int e) {
-          const int j = j0 + e;
-          if (j >= jlim) return 0.f;
-          return in.K_(j, kc) * expf(fminf(s_gc[R0 * GL + kc] - s_gc[j * GL + kc], 88.f));
-        }, fb, fl);
-        dbk[ct] = Mma<E>::mma(dbk[ct], fa, fb);
-        dqa[ct] = Mma<E>::mma(dqa[ct], fq, fb);
-        if (Mma<E>::SPLIT) {
-          dbk[ct] = Mma<E>::mma(dbk[ct], fa, fl);
-          dqa[ct] = Mma<E>::mma(dqa[ct], fq, fl);
-        }
+        const float fb = KV(j, kc) * expf(fminf(s_gc[R0 * GL + kc] - s_gc[j * GL + kc], 88.f));
+        dbk[ct] = MF::mma(dbk[ct], fa, fb);
+        dqa[ct] = MF::mma(dqa[ct], fq, fb);
       }
     }
 #pragma unroll
@@ -255,7 +272,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         float xb = dbk[ct][r] * f, xq = dqa[ct][r] * f;
         if (!safe) {
           for (int j = R0; j <= i; ++j) {
-            const float d = in.K_(j, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
+            const float d = KV(j, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
             if (j < i) xb += s_dA[i * AT_LD + j] * d;
             xq += s_dQ[i * AT_LD + j] * d;
           }
@@ -274,33 +291,17 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   for (int ct = 0; ct < CTK; ++ct) dka[ct] = f4_zero();
   {
     const int RE = R0 + 15;
-    const int i0 = (R0 / KS) * KS;
-    const int ilo = safe ? R0 : R0 + 16;         // unsafe: diagonal block done exactly below
+    const int ilo = safe ? R0 : R0 + 16;       // unsafe: diagonal block done exactly below
     const int rj = R0 + (lane & 15);
-    for (int s = 0; s < (C - i0) / KS; ++s) {
-      const int ib = i0 + s * KS + kofs<E>(lane);
-      const Frag fa = Mma<E>::make([&](int e) { return ib + e >= ilo ? s_dA[(ib + e) * AT_LD + rj] : 0.f; });
-      const Frag fq = Mma<E>::make([&](int e) { return ib + e >= ilo ? s_dQ[(ib + e) * AT_LD + rj] : 0.f; });
+    for (int i0 = ilo; i0 < C; i0 += MF::KS) {
+      const int i = i0 + (lane >> 4);
+      const float fa = s_dA[i * AT_LD + rj], fq = s_dQ[i * AT_LD + rj];
 #pragma unroll
       for (int ct = 0; ct < CTK; ++ct) {
         const int kc = ct * 16 + (lane & 15);
-        Frag fbb, fbl, fqb, fql;
-        Mma<E>::make_split([&](int e) {
-          const int i = ib + e;
-          if (i < ilo) return 0.f;
-          return in.B_(i, kc) * in.K_(i, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
-        }, fbb, fbl);
-        Mma<E>::make_split([&](int e) {
-          const int i = ib + e;
-          if (i < ilo) return 0.f;
-          return in.Q_(i, kc) * in.scale * expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
-        }, fqb, fql);
-        dka[ct] = Mma<E>::mma(dka[ct], fa, fbb);
-        dka[ct] = Mma<E>::mma(dka[ct], fq, fqb);
-        if (Mma<E>::SPLIT) {
-          dka[ct] = Mma<E>::mma(dka[ct], fa, fbl);
-          dka[ct] = Mma<E>::mma(dka[ct], fq, fql);
-        }
+        const float d = expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
+        dka[ct] = MF::mma(dka[ct], fa, BV(i, kc) * KV(i, kc) * d);
+        dka[ct] = MF::mma(dka[ct], fq, QV(i, kc) * in.scale * d);
       }
     }
 #pragma unroll
@@ -313,19 +314,18 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         if (!safe) {
           for (int i = j; i < R0 + 16; ++i) {
             const float d = expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
-            x += (s_dA[i * AT_LD + j] * in.B_(i, kc) * in.K_(i, kc) +
-                  s_dQ[i * AT_LD + j] * in.Q_(i, kc) * in.scale) * d;
+            x += (s_dA[i * AT_LD + j] * BV(i, kc) * KV(i, kc) +
+                  s_dQ[i * AT_LD + j] * QV(i, kc) * in.scale) * d;
           }
         }
         dka[ct][r] = x;
       }
     }
   }
+  __syncthreads();   // s_dgc overwrites s_dA / s_dQ
 
   // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
   {
-    const E* dQg = static_cast<const E*>(a.dQg) + cix * C * K;
-    const E* dKt = static_cast<const E*>(a.dKt) + cix * C * K;
     const size_t tok = (size_t)b * T * H + h;
     E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
     E* dko = static_cast<E*>(a.dk) + tok * K;
@@ -340,8 +340,8 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         const int i = R0 + acc_row(r);
         const float gcv = s_gc[i * GL + kc];
         const float eg = expf(gcv), ekt = expf(glast - gcv);
-        const float bi = in.B_(i, kc), ki = in.K_(i, kc), qh = in.Q_(i, kc) * in.scale;
-        const float gq = to_f(dQg[i * K + kc]), gk = to_f(dKt[i * K + kc]);
+        const float bi = BV(i, kc), ki = KV(i, kc), qh = QV(i, kc) * in.scale;
+        const float gq = to_f(s_dQg[i * LDK + kc]), gk = to_f(s_dKt[i * LDK + kc]);
         const float xw = dxw[ct][r];
         const float dqh = dqa[ct][r] + gq * eg;
         const float db_ = dbk[ct][r] * ki + xw * ki * eg;

@@ -82,7 +82,7 @@ def _check(ours, want, dtype):
     assert not errors, "\n".join(errors)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("T,K", [(128, 64), (192, 128), (100, 64)])
 def test_level0_gradients(dtype, T, K):
     print(f"level0 grads T={T} K={K} {dtype}", flush=True)
@@ -106,7 +106,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 @pytest.mark.parametrize("B,T,H,K,L,N,firing,nq", CASES)
 def test_gradients_match_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
@@ -118,7 +118,7 @@ def test_gradients_match_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
     _check(ours, want, dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 def test_initial_state_and_final_state_gradients(dtype, promotion):
     inp = make_inputs(B=2, T=256, H=2, K=64, V=64, L=3, N=16, intervals=(1, 2, 4),

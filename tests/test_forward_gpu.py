@@ -32,7 +32,7 @@ def _oracle(inp, L, promotion="learned", init=None):
 
 # ------------------------------------------------------------- level-0 chunk terms
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("K,V,T,g_scale", [(64, 64, 192, 0.1), (128, 128, 130, 1.0),
                                            (64, 128, 128, 30.0), (128, 64, 64, 2.0)])
 def test_l0_intra_terms(dtype, K, V, T, g_scale):
@@ -96,7 +96,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 @pytest.mark.parametrize("B,T,H,K,L,N,firing,nq", CASES)
 def test_forward_matches_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
@@ -110,7 +110,7 @@ def test_forward_matches_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
     torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 def test_forward_with_initial_state(dtype, promotion):
     inp = make_inputs(B=2, T=256, H=2, K=64, V=64, L=3, N=16, intervals=(1, 2, 4),
