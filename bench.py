@@ -70,49 +70,50 @@ def work_model(cfg):
     tile products (2 m n k). Units: bytes, flop."""
     B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
     f = cfg["intervals"]
-    es = 2 if cfg["dtype"] == torch.bfloat16 else 4
+    es = 2 if cfg["dtype"] == torch.bfloat16 else 4   # inputs, parameters, gradients
     C = 64
     NT = -(-T // C)
     units = B * H * NT                       # chunk-heads
-    ck, cv, cc = C * K * es, C * V * es, C * C * es
-    kv_e, kv_f = K * V * es, K * V * 4
+    ck, cv, cc = C * K * es, C * V * es, C * C * es   # input tiles of one chunk
+    wk, wv, wc = C * K * 4, C * V * 4, C * C * 4      # fp32 working tiles
+    kv = K * V * 4                                    # one state
     m = {}
     # level-0 intra: reads q0,k,b,v,w + g (fp32); writes W,U,KtT,Qg,Aqk,gam
     # and the backward layouts Kt, WT, QgT, AqkT, TT
     m["ngdn_l0_intra_fwd"] = (
-        units * (3 * ck + 2 * cv + C * K * 4 + 4 * ck + cv + cc + K * 4 + 3 * ck + 2 * cc),
+        units * (3 * ck + 2 * cv + C * K * 4 + 4 * wk + wv + wc + K * 4 + 3 * wk + 2 * wc),
         units * (2 * 2 * C * C * K + 2 * C * C * (K + V) + C ** 3 // 3))
     # level-0 scan: reads W, U, KtT, gam; writes hT, vnT; + final
-    m["ngdn_l0_scan_fwd"] = (units * (2 * ck + cv + K * 4 + kv_e + cv) + B * H * kv_f,
+    m["ngdn_l0_scan_fwd"] = (units * (2 * wk + wv + K * 4 + kv + wv) + B * H * kv,
                              units * 2 * 2 * C * K * V)
     # output: Qg, hT, Aqk, vnT, q of upper levels, mix; upper states once per group; o
-    up_states = sum(B * H * n_groups(NT, f[l]) * kv_f for l in range(1, L))
+    up_states = sum(B * H * n_groups(NT, f[l]) * kv for l in range(1, L))
     m["ngdn_output_fwd"] = (
-        units * (ck + kv_e + cc + cv + (L - 1) * ck + C * L * es + cv) + up_states,
+        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv) + up_states,
         units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 2 * C * K * V))
     m["ngdn_output_bwd"] = (
-        units * (ck + kv_e + cc + cv + (L - 1) * ck + C * L * es + cv + (L - 1) * ck + C * L * 4)
+        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv + (L - 1) * ck + C * L * 4)
         + up_states,
         units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 4 * C * K * V))
     # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
-    m["ngdn_l0_scan_bwd"] = (units * (3 * ck + cc + K * 4 + cv + C * es + kv_e + 2 * cv),
+    m["ngdn_l0_scan_bwd"] = (units * (3 * wk + wc + K * 4 + cv + C * es + kv + 2 * wv),
                              units * (2 * C * K * V * 3 + 2 * C * C * V))
     # level-0 chunk backward, state half: hT, dSp, vnT, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
-    m["ngdn_l0_bwd_state"] = (units * (2 * kv_e + 3 * cv + C * es + 3 * ck + cc + K * 4),
+    m["ngdn_l0_bwd_state"] = (units * (2 * kv + 2 * wv + cv + C * es + 3 * wk + wc + K * 4),
                               units * (3 * 2 * C * K * V + 2 * C * C * V))
     # level-0 chunk backward, intra half: q0,k,b,v,w,g, W,U,TT, dQg,dWT,dKt,dAqk,dgam,dVnT
     # -> dq0,dk,dv,dg,db,dw
     m["ngdn_l0_bwd_intra"] = (
-        units * (3 * ck + 2 * cv + C * K * 4 + ck + cv + cc + 3 * ck + cc + K * 4 + cv
+        units * (3 * ck + 2 * cv + C * K * 4 + wk + wv + wc + 3 * wk + wc + K * 4 + wv
                  + 3 * ck + 2 * cv + C * K * 4),
         units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     for lvl in range(1, L):
         nf = n_firings(NT, f[lvl])
         fu = B * H * nf
-        nk = N * K * es
-        m[f"ngdn_probe_fwd.{lvl}"] = (fu * (kv_e + 3 * nk + 4 * K) + H * (N * K + 4 * K * V) * es,
+        nk = N * K * 4
+        m[f"ngdn_probe_fwd.{lvl}"] = (fu * (kv + 3 * nk + 4 * K) + H * (N * K + 4 * K * V) * es,
                                       fu * 5 * 2 * N * K * V)
-        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * n_groups(NT, f[lvl]) * kv_f,
+        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * n_groups(NT, f[lvl]) * kv,
                                            fu * 2 * 2 * N * K * V)
     return m, units
 

@@ -12,10 +12,12 @@
  *   mix [B,T,H,L]; initial/final state [B,H,L,K,V] fp32;
  *   query_banks [L-1,H,Nmax,K]; key_projections [L-1,H,K,V];
  *   b/g_projections [L-1,H,V,K]; w_projections [L-1,H,V,V].
- * All contiguous. "dtype" is the element type of the float tensors other than
- * g and the states: NGDN_F32 or NGDN_BF16. Chunk size is 64.
+ * All contiguous. "dtype" is the element type of the op's inputs and
+ * parameters (other than g and the states) and of its gradients: NGDN_F32 or
+ * NGDN_BF16. Chunk size is 64.
  * Working tensors between the entry points ([B,H,NT,...], NT = ceil(T/64))
- * are described at each function.
+ * are fp32 whatever the dtype (declared float*), and are described at each
+ * function.
  */
 #ifndef NGDN_H
 #define NGDN_H
@@ -48,26 +50,26 @@ const char* ngdn_arch(void);
 
 /* Level-0 per-chunk terms: the intra-chunk half of fla's chunk_gdn2_fwd as
  * called at nested_gdn2/ops/chunk.py:236-248 (semantics ops/naive.py:329-358).
- * Outputs (working dtype unless noted): W [B,H,NT,64,K], U [B,H,NT,64,V],
- * KtT [B,H,NT,K,64], Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64],
- * gam [B,H,NT,K] fp32. Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64]
- * and AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
+ * Outputs: W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64],
+ * Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64], gam [B,H,NT,K].
+ * Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64] and
+ * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
  * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
  * may be NULL (inference). */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
-                          const void* w, void* W, void* U, void* KtT, void* Qg,
-                          void* Aqk, float* gam, void* Kt, void* WT, void* QgT,
-                          void* AqkT, void* TT, void* stream);
+                          const void* w, float* W, float* U, float* KtT, float* Qg,
+                          float* Aqk, float* gam, float* Kt, float* WT, float* QgT,
+                          float* AqkT, float* TT, void* stream);
 
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
- * Writes hT [B,H,NT,V,K] (state entering each chunk, transposed, working
- * dtype), vnT [B,H,NT,V,64] (the chunk's new values, transposed) and
- * final_state[:, :, 0] (fp32). initial_state may be NULL (zeros). */
-int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
-                         const void* KtT, const float* gam,
-                         const float* initial_state, void* hT, void* vnT,
+ * Writes hT [B,H,NT,V,K] (state entering each chunk, transposed), vnT
+ * [B,H,NT,V,64] (the chunk's new values, transposed) and final_state[:, :, 0].
+ * initial_state may be NULL (zeros). */
+int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
+                         const float* KtT, const float* gam,
+                         const float* initial_state, float* hT, float* vnT,
                          float* final_state, void* stream);
 
 /* Promotion probe of level `level` >= 1: PROBES[promotion] applied to the
@@ -79,18 +81,18 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
  * bpT, gpT [L-1,H,K,V] and wpT [L-1,H,V,V] are the b/g/w projections with
  * their last two axes swapped. promotion: 0 learned, 1 merge (n_queries = K).
  * Outputs for firing i in [0, NF), NF = NT / f_here, laid out [B,H,NF,...]:
- * A = keys*b*e^g [N,K], KT = keys^T [K,N], U = values*w [N,V] (working dtype),
- * gam = e^g [K] fp32; for the backward, keysN = keys [N,K] and AT = A^T
+ * A = keys*b*e^g [N,K], KT = keys^T [K,N], U = values*w [N,V],
+ * gam = e^g [K]; for the backward, keysN = keys [N,K] and AT = A^T
  * [K,N] (may be NULL). keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
  * receive the probe outputs in the reference layout when not NULL. */
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const void* below, int32_t ng_below,
+                       const float* below, int32_t ng_below,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
-                       void* A, void* KT, void* U, float* gam, void* keysN,
-                       void* AT, float* keys, float* vals, float* bo, float* wo,
+                       float* A, float* KT, float* U, float* gam, float* keysN,
+                       float* AT, float* keys, float* vals, float* bo, float* wo,
                        float* go, void* stream);
 
 /* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
@@ -99,8 +101,8 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
  * past the last firing hold the final state) and final_state[:, :, level].
  * initial_state may be NULL. */
 int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
-                            int32_t nf, int32_t ng, const void* A,
-                            const void* KT, const void* U, const float* gam,
+                            int32_t nf, int32_t ng, const float* A,
+                            const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
                             float* final_state, void* stream);
 
@@ -110,8 +112,8 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
  * firing interval f[l]; entries at l = 0 are ignored. o [B,T,H,V] in the
  * working dtype. reads, when not NULL, receives each level's unmixed read,
  * fp32 [L,B,T,H,V]. */
-int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
-                        const void* hT, const void* vnT, const void* q,
+int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                        const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* reads, void* stream);
@@ -123,8 +125,8 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
 /* Output backward per chunk (ops/chunk.py:423-449): dmix for every level
  * (fp32 [B,T,H,L]) and dq[..., l, :] for l >= 1 (working dtype [B,T,H,L,K]);
  * inputs as for ngdn_output_fwd plus do [B,T,H,V]. */
-int32_t ngdn_output_bwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
-                        const void* hT, const void* vnT, const void* q,
+int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                        const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
                         const int32_t* ng, const int32_t* f, const void* dout,
                         void* dq, float* dmix, void* stream);
@@ -142,13 +144,13 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
  * entering chunk (i+1)*f1, added before that chunk's step (the reference's
  * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
- * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (working dtype), and
- * d_initial[:, :, 0] when not NULL. */
-int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
-                         const float* gam, const void* AqkT, const void* QgT,
+ * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64], and d_initial[:, :, 0]
+ * when not NULL. */
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
+                         const float* gam, const float* AqkT, const float* QgT,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
-                         void* dSp, void* dVn, void* dVnT, float* d_initial,
+                         float* dSp, float* dVn, float* dVnT, float* d_initial,
                          void* stream);
 
 /* Reverse write scan of level `level` >= 1 (ops/update_bwd.py:19-164): keys
@@ -157,27 +159,27 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
  * above's scatter); d_final [B,H,L,K,V]. Writes dSp fp32 [B,H,NF,K,V], dvn
  * fp32 [B,H,NF,N,V] and d_initial[:, :, level] when not NULL. */
 int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
-                            int32_t nf, int32_t ng, const void* keys,
-                            const void* AT, const float* gam,
+                            int32_t nf, int32_t ng, const float* keys,
+                            const float* AT, const float* gam,
                             const float* d_states, const float* d_final,
                             float* dSp, float* dvn, float* d_initial,
                             void* stream);
 
 /* Level-0 chunk backward, state half: dQg, dKt [B,H,NT,64,K], dWT
- * [B,H,NT,K,64], dAqk [B,H,NT,64,64] (working dtype), dgam fp32 [B,H,NT,K]. */
-int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const void* hT, const void* dSp,
-                          const void* vnT, const void* dVn, const void* dout,
-                          const void* mix, void* dQg, void* dWT, void* dKt,
-                          void* dAqk, float* dgam, void* stream);
+ * [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam [B,H,NT,K]. */
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* hT, const float* dSp,
+                          const float* vnT, const float* dVn, const void* dout,
+                          const void* mix, float* dQg, float* dWT, float* dKt,
+                          float* dAqk, float* dgam, void* stream);
 
 /* Level-0 chunk backward, intra half: writes dq[..., 0, :], dk, dv, db, dw
  * (working dtype) and dg (fp32 [B,T,H,K]). W, U, TT from ngdn_l0_intra_fwd. */
 int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
-                          const void* w, const void* W, const void* U,
-                          const void* TT, const void* dQg, const void* dWT,
-                          const void* dKt, const void* dAqk, const float* dgam,
-                          const void* dVnT, void* dq, void* dk, void* dv,
+                          const void* w, const float* W, const float* U,
+                          const float* TT, const float* dQg, const float* dWT,
+                          const float* dKt, const float* dAqk, const float* dgam,
+                          const float* dVnT, void* dq, void* dk, void* dv,
                           float* dg, void* db, void* dw, void* stream);
 
 /* Backward of level `level`'s firings through its update and probe.
@@ -185,21 +187,21 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
  * projections transposed), bankT [L-1,H,K,n_max] (banks transposed), and the
  * untransposed bp, gp [L-1,H,V,K], wp [L-1,H,V,V]. states fp32 [B,ng,H,K,V]
  * are this level's group states; dSp, dvn from ngdn_upper_scan_bwd.
- * Workspace (working dtype): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K],
+ * Workspace (fp32): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K],
  * ws_dxw, ws_dvals [B,H,NF,N,V]. dbank fp32 [L-1,H,n_max,K] accumulates. The
  * gradient of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is
  * added to d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const void* below, int32_t ng_below,
+                       const float* below, int32_t ng_below,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
                        const void* kpT, const void* bankT, const void* bp,
                        const void* wp, const void* gp, const float* states,
                        int32_t ng, const float* dSp, const float* dvn,
-                       void* ws_vals, void* ws_du, void* ws_dxb, void* ws_dxg,
-                       void* ws_dxw, void* ws_dvals, float* dbank, float* inj,
+                       float* ws_vals, float* ws_du, float* ws_dxb, float* ws_dxg,
+                       float* ws_dxw, float* ws_dvals, float* dbank, float* inj,
                        float* d_below, float* d_final, void* stream);
 
 /* Per-head parameter gradients of level `level` summed over all its firings
@@ -207,9 +209,9 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
  * workspace of ngdn_probe_bwd; accumulated into fp32 dkp [L-1,H,K,V] (learned
  * only), dbp [L-1,H,V,K], dwp [L-1,H,V,V], dgp [L-1,H,V,K]. */
 int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
-                         int32_t n_pairs, int32_t nf, const void* ws_vals,
-                         const void* ws_du, const void* ws_dxb,
-                         const void* ws_dxg, const void* ws_dxw, float* dkp,
+                         int32_t n_pairs, int32_t nf, const float* ws_vals,
+                         const float* ws_du, const float* ws_dxb,
+                         const float* ws_dxg, const float* ws_dxw, float* dkp,
                          float* dbp, float* dwp, float* dgp, void* stream);
 
 #ifdef __cplusplus

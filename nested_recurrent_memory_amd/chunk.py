@@ -94,17 +94,19 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     st = _lib.stream_of(q_)
     P = _lib.ptr
     e = lambda *s, dt=wd: torch.empty(*s, device=dev, dtype=dt)  # noqa: E731
-    opt = lambda *s: e(*s) if train else None  # noqa: E731
+    # working tensors between the kernels are fp32 whatever the input dtype
+    f32 = lambda *s: e(*s, dt=torch.float32)  # noqa: E731
+    opt = lambda *s: f32(*s) if train else None  # noqa: E731
 
-    W, U, Qg = e(B, H, NT, 64, K), e(B, H, NT, 64, V), e(B, H, NT, 64, K)
-    KtT, Aqk = e(B, H, NT, K, 64), e(B, H, NT, 64, 64)
-    gam = e(B, H, NT, K, dt=torch.float32)
+    W, U, Qg = f32(B, H, NT, 64, K), f32(B, H, NT, 64, V), f32(B, H, NT, 64, K)
+    KtT, Aqk = f32(B, H, NT, K, 64), f32(B, H, NT, 64, 64)
+    gam = f32(B, H, NT, K)
     Kt, WT, QgT = opt(B, H, NT, 64, K), opt(B, H, NT, K, 64), opt(B, H, NT, K, 64)
     AqkT, TT = opt(B, H, NT, 64, 64), opt(B, H, NT, 64, 64)
     _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
               P(W), P(U), P(KtT), P(Qg), P(Aqk), P(gam), P(Kt), P(WT), P(QgT), P(AqkT),
               P(TT), st)
-    hT, vnT = e(B, H, NT, V, K), e(B, H, NT, V, 64)
+    hT, vnT = f32(B, H, NT, V, K), f32(B, H, NT, V, 64)
     final = torch.empty(B, H, L, K, V, device=dev, dtype=torch.float32)
     _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), P(W), P(U), P(KtT), P(gam), P(init_),
               P(hT), P(vnT), P(final), st)
@@ -120,8 +122,8 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         nf, ng = n_firings(NT, fh), n_groups(NT, fh)
         N = K if merge else nq[lvl - 1]
         nf1 = max(nf, 1)
-        A_, KT_, U_ = e(B, H, nf1, N, K), e(B, H, nf1, K, N), e(B, H, nf1, N, V)
-        gm_ = e(B, H, nf1, K, dt=torch.float32)
+        A_, KT_, U_ = f32(B, H, nf1, N, K), f32(B, H, nf1, K, N), f32(B, H, nf1, N, V)
+        gm_ = f32(B, H, nf1, K)
         keysN, AT_ = opt(B, H, nf1, N, K), opt(B, H, nf1, K, N)
         below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
         if nf > 0:
@@ -229,7 +231,8 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                   P(d_init), st, tag=f"ngdn_upper_scan_bwd.{lvl}")
         if nf == 0:
             continue
-        ws = [e(B, H, nf, N, K) for _ in range(4)] + [e(B, H, nf, N, V) for _ in range(2)]
+        ws = ([e(B, H, nf, N, K, dt=torch.float32) for _ in range(4)]
+              + [e(B, H, nf, N, V, dt=torch.float32) for _ in range(2)])
         fh, fb = f[lvl], f[lvl - 1]
         if lvl == 1:
             inj, nf1 = e(B, H, nf, K, V, dt=torch.float32), nf
@@ -247,12 +250,13 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                   tag=f"ngdn_param_grads.{lvl}")
 
     # level 0
-    dSp0, dVn0, dVnT0 = e(B, H, NT, K, V), e(B, H, NT, 64, V), e(B, H, NT, V, 64)
+    f32 = lambda *s: e(*s, dt=torch.float32)  # noqa: E731
+    dSp0, dVn0, dVnT0 = f32(B, H, NT, K, V), f32(B, H, NT, 64, V), f32(B, H, NT, V, 64)
     _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), P(sv["Kt"]), P(sv["WT"]), P(sv["gam"]),
               P(sv["AqkT"]), P(sv["QgT"]), P(do_), P(mix_), f[1] if L > 1 else 1, P(inj), nf1,
               P(d_final), P(dSp0), P(dVn0), P(dVnT0), P(d_init), st)
-    dQg, dKt, dWT = e(B, H, NT, 64, K), e(B, H, NT, 64, K), e(B, H, NT, K, 64)
-    dAqk, dgam = e(B, H, NT, 64, 64), e(B, H, NT, K, dt=torch.float32)
+    dQg, dKt, dWT = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K), f32(B, H, NT, K, 64)
+    dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
     _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(sv["hT"]), P(dSp0), P(sv["vnT"]), P(dVn0),
               P(do_), P(mix_), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam), st)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)

@@ -51,9 +51,9 @@ const char* ngdn_arch(void) { return "gfx950"; }
 
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
-                          const void* w, void* W, void* U, void* KtT, void* Qg,
-                          void* Aqk, float* gam, void* Kt, void* WT, void* QgT,
-                          void* AqkT, void* TT, void* stream) {
+                          const void* w, float* W, float* U, float* KtT, float* Qg,
+                          float* Aqk, float* gam, float* Kt, float* WT, float* QgT,
+                          float* AqkT, float* TT, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_intra_fwd")) return r;
   if (!q || !k || !v || !g || !b || !w || !W || !U || !KtT || !Qg || !Aqk || !gam)
@@ -64,9 +64,9 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                   "ngdn_l0_intra_fwd");
 }
 
-int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
-                         const void* KtT, const float* gam,
-                         const float* initial_state, void* hT, void* vnT,
+int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
+                         const float* KtT, const float* gam,
+                         const float* initial_state, float* hT, float* vnT,
                          float* final_state, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_fwd")) return r;
@@ -85,12 +85,12 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const void* W, const void* U,
 
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const void* below, int32_t ng_below,
+                       const float* below, int32_t ng_below,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
-                       void* A, void* KT, void* U, float* gam, void* keysN,
-                       void* AT, float* keys, float* vals, float* bo, float* wo,
+                       float* A, float* KT, float* U, float* gam, float* keysN,
+                       float* AT, float* keys, float* vals, float* bo, float* wo,
                        float* go, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_fwd")) return r;
@@ -134,8 +134,8 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
 }
 
 int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
-                            int32_t nf, int32_t ng, const void* A,
-                            const void* KT, const void* U, const float* gam,
+                            int32_t nf, int32_t ng, const float* A,
+                            const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
                             float* final_state, void* stream) {
   g_err[0] = 0;
@@ -161,8 +161,8 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_fwd");
 }
 
-int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
-                        const void* hT, const void* vnT, const void* q,
+int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                        const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* reads, void* stream) {
@@ -185,8 +185,8 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
 }
 
 
-int32_t ngdn_output_bwd(const ngdn_dims* d, const void* Qg, const void* Aqk,
-                        const void* hT, const void* vnT, const void* q,
+int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                        const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
                         const int32_t* ng, const int32_t* f, const void* dout,
                         void* dq, float* dmix, void* stream) {
@@ -223,11 +223,11 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
                   "ngdn_read_state_bwd");
 }
 
-int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
-                         const float* gam, const void* AqkT, const void* QgT,
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
+                         const float* gam, const float* AqkT, const float* QgT,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
-                         void* dSp, void* dVn, void* dVnT, float* d_initial,
+                         float* dSp, float* dVn, float* dVnT, float* d_initial,
                          void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_bwd")) return r;
@@ -243,15 +243,15 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const void* Kt, const void* WT,
   a.inj = inj; a.inj_every = inj ? f1 : 1; a.inj_nf = nf1;
   a.d_states = nullptr; a.NG = NT;
   a.d_final = d_final; a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
-  a.dSp = dSp; a.dsp_mode = 0; a.dVn = dVn; a.dvn_mode = 0; a.dVnT = dVnT;
+  a.dSp = dSp; a.dVn = dVn; a.dVnT = dVnT;
   a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
 }
 
 int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
-                            int32_t nf, int32_t ng, const void* keys,
-                            const void* AT, const float* gam,
+                            int32_t nf, int32_t ng, const float* keys,
+                            const float* AT, const float* gam,
                             const float* d_states, const float* d_final,
                             float* dSp, float* dvn, float* d_initial,
                             void* stream) {
@@ -272,17 +272,17 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   a.d_states = d_states; a.NG = ng;
   a.d_final = d_final ? d_final + (long long)level * skv : nullptr;
   a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
-  a.dSp = dSp; a.dsp_mode = 1; a.dVn = dvn; a.dvn_mode = 1;
+  a.dSp = dSp; a.dVn = dvn; a.dVnT = nullptr;
   a.dinit = d_initial ? d_initial + (long long)level * skv : nullptr;
   a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = nf; a.M = n_pairs; a.V = d->V;
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_bwd");
 }
 
-int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const void* hT, const void* dSp,
-                          const void* vnT, const void* dVn, const void* dout,
-                          const void* mix, void* dQg, void* dWT, void* dKt,
-                          void* dAqk, float* dgam, void* stream) {
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* hT, const float* dSp,
+                          const float* vnT, const float* dVn, const void* dout,
+                          const void* mix, float* dQg, float* dWT, float* dKt,
+                          float* dAqk, float* dgam, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_bwd_state")) return r;
   if (!hT || !dSp || !vnT || !dVn || !dout || !mix || !dQg || !dWT || !dKt || !dAqk || !dgam)
@@ -295,10 +295,10 @@ int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const void* hT, const void* dSp,
 
 int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
-                          const void* w, const void* W, const void* U,
-                          const void* TT, const void* dQg, const void* dWT,
-                          const void* dKt, const void* dAqk, const float* dgam,
-                          const void* dVnT, void* dq, void* dk, void* dv,
+                          const void* w, const float* W, const float* U,
+                          const float* TT, const float* dQg, const float* dWT,
+                          const float* dKt, const float* dAqk, const float* dgam,
+                          const float* dVnT, void* dq, void* dk, void* dv,
                           float* dg, void* db, void* dw, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_bwd_intra")) return r;
@@ -313,15 +313,15 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
 
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const void* below, int32_t ng_below,
+                       const float* below, int32_t ng_below,
                        const float* final_state, const void* query_banks,
                        int32_t n_max, const void* key_projections,
                        const void* bpT, const void* wpT, const void* gpT,
                        const void* kpT, const void* bankT, const void* bp,
                        const void* wp, const void* gp, const float* states,
                        int32_t ng, const float* dSp, const float* dvn,
-                       void* ws_vals, void* ws_du, void* ws_dxb, void* ws_dxg,
-                       void* ws_dxw, void* ws_dvals, float* dbank, float* inj,
+                       float* ws_vals, float* ws_du, float* ws_dxb, float* ws_dxg,
+                       float* ws_dxw, float* ws_dvals, float* dbank, float* inj,
                        float* d_below, float* d_final, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_bwd")) return r;
@@ -371,9 +371,9 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
 }
 
 int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
-                         int32_t n_pairs, int32_t nf, const void* ws_vals,
-                         const void* ws_du, const void* ws_dxb,
-                         const void* ws_dxg, const void* ws_dxw, float* dkp,
+                         int32_t n_pairs, int32_t nf, const float* ws_vals,
+                         const float* ws_du, const float* ws_dxb,
+                         const float* ws_dxg, const float* ws_dxw, float* dkp,
                          float* dbp, float* dwp, float* dgp, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_param_grads")) return r;

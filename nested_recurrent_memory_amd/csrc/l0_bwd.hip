@@ -21,12 +21,14 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   constexpr int C = CH;
-  constexpr int LDV = V + 8;
+  constexpr int LDV = V + 4;
   constexpr int CTK = K / 16;
-  constexpr int NKV = V / Mma<E>::KS;
-  typedef typename Mma<E>::Frag Frag;
-  __shared__ __attribute__((aligned(16))) E s_S[K * LDV];
-  __shared__ __attribute__((aligned(16))) E s_Vn[C * LDV];
+  constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
+  constexpr int NKV = V / KS;
+  typedef typename Mma<E>::SFrag SF;
+  __shared__ __attribute__((aligned(16))) float s_S[K * LDV];   // S rows (v contiguous)
+  __shared__ __attribute__((aligned(16))) float s_Vn[C * LDV];  // Vn rows
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -38,65 +40,67 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   const size_t cix = (size_t)bh * NT + n;
 
   {
-    const E* hT = static_cast<const E*>(a.hT) + cix * V * K;
+    const float* hT = a.hT + cix * V * K;
     for (int e = tid; e < V * K; e += 256) s_S[(e % K) * LDV + e / K] = hT[e];
-    const E* vT = static_cast<const E*>(a.vnT) + cix * V * C;
+    const float* vT = a.vnT + cix * V * C;
     for (int e = tid; e < V * C; e += 256) s_Vn[(e % C) * LDV + e / C] = vT[e];
   }
   __syncthreads();
 
   // A fragments of this wave's 16 rows: dO (from do and mix_0), dVn, Vn
   const int ri = wv * 16 + (lane & 15);
-  const E* dop = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V;
+  const int rc = min(ri, nvalid - 1);
+  const E* dop = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V + (size_t)(t0 + rc) * H * V;
   const float m0 = ri < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + ri) * H * a.L + (size_t)h * a.L]) : 0.f;
-  const E* dvn = static_cast<const E*>(a.dVn) + cix * C * V + (size_t)ri * V;
-  Frag fo[NKV], fd[NKV], fv[NKV];
+  const float* dvn = a.dVn + cix * C * V + (size_t)ri * V;
+  SF fo[NKV], fd[NKV], fv[NKV];
 #pragma unroll
   for (int s = 0; s < NKV; ++s) {
-    const int v0 = s * Mma<E>::KS + kofs<E>(lane);
-    fo[s] = Mma<E>::make([&](int e) {
-      return ri < nvalid ? to_f(dop[(size_t)(t0 + ri) * H * V + v0 + e]) * m0 : 0.f;
-    });
-    fd[s] = Mma<E>::load(dvn + v0);
-    fv[s] = Mma<E>::load(s_Vn + ri * LDV + v0);
+    const int v0 = s * KS + kofs<E>(lane);
+    float x[KPL];
+    ld_vals<E>(dop + v0, x);
+    fo[s] = Mma<E>::makes([&](int e) { return x[e] * m0; });
+    fd[s] = Mma<E>::ld(dvn + v0);
+    fv[s] = Mma<E>::ld(s_Vn + ri * LDV + v0);
   }
-  const E* dsp = static_cast<const E*>(a.dSp) + cix * K * V;
-  E* dQg = static_cast<E*>(a.dQg) + cix * C * K;
-  E* dWT = static_cast<E*>(a.dWT) + cix * K * C;
-  E* dKt = static_cast<E*>(a.dKt) + cix * C * K;
+  const float* dsp = a.dSp + cix * K * V;
+  float* dQg = a.dQg + cix * C * K;
+  float* dWT = a.dWT + cix * K * C;
+  float* dKt = a.dKt + cix * C * K;
 #pragma unroll 2
   for (int ct = 0; ct < CTK; ++ct) {
     f4 aq = f4_zero(), aw = f4_zero(), ak = f4_zero();
-    const E* srow = s_S + (ct * 16 + (lane & 15)) * LDV + kofs<E>(lane);
-    const E* drow = dsp + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
+    const float* srow = s_S + (ct * 16 + (lane & 15)) * LDV + kofs<E>(lane);
+    const float* drow = dsp + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
 #pragma unroll
     for (int s = 0; s < NKV; ++s) {
-      const Frag sb = Mma<E>::load(srow + s * Mma<E>::KS);
+      const SF sb = Mma<E>::ld(srow + s * KS);
       aq = Mma<E>::mma(aq, fo[s], sb);
       aw = Mma<E>::mma(aw, fd[s], sb);
-      ak = Mma<E>::mma(ak, fv[s], Mma<E>::load(drow + s * Mma<E>::KS));
+      ak = Mma<E>::mma(ak, fv[s], Mma<E>::ld(drow + s * KS));
     }
     const int i0 = wv * 16 + acc_row(0), k = ct * 16 + acc_col();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      dQg[(i0 + r) * K + k] = from_f<E>(aq[r]);
-      dKt[(i0 + r) * K + k] = from_f<E>(ak[r]);
-      dWT[k * C + i0 + r] = from_f<E>(-aw[r]);
+      dQg[(i0 + r) * K + k] = aq[r];
+      dKt[(i0 + r) * K + k] = ak[r];
+      aw[r] = -aw[r];
     }
+    *reinterpret_cast<f4*>(dWT + k * C + i0) = aw;
   }
   // dAqk = dO Vn^T, lower including the diagonal
-  E* dAq = static_cast<E*>(a.dAqk) + cix * C * C;
+  float* dAq = a.dAqk + cix * C * C;
   for (int J = 0; J < 4; ++J) {
     f4 acc = f4_zero();
     if (J <= wv) {
-      const E* vrow = s_Vn + (J * 16 + (lane & 15)) * LDV + kofs<E>(lane);
+      const float* vrow = s_Vn + (J * 16 + (lane & 15)) * LDV + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < NKV; ++s) acc = Mma<E>::mma(acc, fo[s], Mma<E>::load(vrow + s * Mma<E>::KS));
+      for (int s = 0; s < NKV; ++s) acc = Mma<E>::mma(acc, fo[s], Mma<E>::ld(vrow + s * KS));
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
-      dAq[i * C + j] = from_f<E>(j <= i ? acc[r] : 0.f);
+      dAq[i * C + j] = j <= i ? acc[r] : 0.f;
     }
   }
   // dgam_k = sum_v dS'[k][v] S[k][v]
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
     constexpr int TPK = 256 / K;           // threads per row k
     const int k = tid / TPK, part = tid % TPK;
     float s = 0.f;
-    for (int v = part; v < V; v += TPK) s += to_f(dsp[(size_t)k * V + v]) * to_f(s_S[k * LDV + v]);
+    for (int v = part; v < V; v += TPK) s += dsp[(size_t)k * V + v] * s_S[k * LDV + v];
 #pragma unroll
     for (int o = 1; o < TPK; o <<= 1) s += __shfl_xor(s, o, WAVE);
     if (part == 0) a.dgam[cix * K + k] = s;
@@ -115,33 +119,34 @@ template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr int C = CH;
   constexpr int GL = K + GCP;
-  constexpr int LDK = K + 8, LDV = V + 8;
+  constexpr int LDK = K + 8;                 // staged input rows (E)
+  constexpr int LXK = K + 4, LXV = V + 4;    // fp32 rows
   constexpr int CTK = K / 16, CTV = V / 16;
   constexpr int KS = Mma<E>::KS;
   // bf16: the chunk's k, b, q rows are staged in LDS; fp32 (a test-only path)
   // reads them from global memory to stay inside the LDS budget
   constexpr bool STAGE = !std::is_same<E, float>::value;
-  typedef typename Mma<E>::Frag Frag;
+  typedef typename Mma<E>::SFrag SF;
   typedef Mma<float> MF;
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
   constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDK : 0;
+  // region R: dX_w, dX_u (fp32); after the dA product: dA, dAqk; after the
+  // decay backward: the cumulative-decay gradient
+  constexpr size_t SZ_X = sizeof(float) * C * (LXK + LXV);
   constexpr size_t SZ_DA = sizeof(float) * 2 * C * AT_LD;
-  constexpr int RW = (LDK + LDV) > 2 * LDK ? (LDK + LDV) : 2 * LDK;
-  constexpr size_t SZ_R = sizeof(E) * C * RW;
+  constexpr size_t SZ_R = SZ_X > SZ_DA ? SZ_X : SZ_DA;
   static_assert(C * GL <= 2 * C * AT_LD, "dgc must fit the dA region");
-  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_IN + SZ_DA + SZ_R + sizeof(float) * K];
+  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_IN + SZ_R + sizeof(float) * K];
   float* s_gc = reinterpret_cast<float*>(smem);
   E* s_k = reinterpret_cast<E*>(smem + SZ_GC);
   E* s_b = s_k + C * LDK;
   E* s_q = s_b + C * LDK;
-  float* s_dA = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN);
+  float* s_dXw = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN);
+  float* s_dXu = s_dXw + C * LXK;
+  float* s_dA = s_dXw;                       // after the dA product
   float* s_dQ = s_dA + C * AT_LD;
   float* s_dgc = s_dA;                       // after the decay backward
-  E* s_dXw = reinterpret_cast<E*>(smem + SZ_GC + SZ_IN + SZ_DA);
-  E* s_dXu = s_dXw + C * LDK;
-  E* s_dQg = s_dXw;                          // after the dA product
-  E* s_dKt = s_dXw + C * LDK;
-  float* s_col = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN + SZ_DA + SZ_R);
+  float* s_col = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN + SZ_R);
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -163,41 +168,36 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     if constexpr (STAGE) return to_f(s_q[i * LDK + c]); else return in.Q_(i, c);
   };
 
-  // ---- 1. gc, the chunk's rows, dAqk (fp32 in LDS)
+  // ---- 1. gc and the chunk's rows
   if constexpr (STAGE) {
     stage_rows<E>(s_k, LDK, in.k + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
     stage_rows<E>(s_b, LDK, in.b + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
     stage_rows<E>(s_q, LDK, in.q + (size_t)t0 * in.rowQ, in.rowQ, C, K, nvalid);
   }
   l0_cumsum(s_gc, in);
-  {
-    const E* dq = static_cast<const E*>(a.dAqk) + cix * C * C;
-    for (int e = tid; e < C * C; e += 256) s_dQ[(e / C) * AT_LD + e % C] = to_f(dq[e]);
-    for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
-  }
-  __syncthreads();
+  for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
 
   // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns rows 16w..16w+15
   const int ri = wv * 16 + (lane & 15);
   f4 dxw[CTK];
   {
-    Frag tf[C / KS];
-    const E* tt = static_cast<const E*>(a.TT) + cix * C * C + (size_t)ri * C + kofs<E>(lane);
+    SF tf[C / KS];
+    const float* tt = a.TT + cix * C * C + (size_t)ri * C + kofs<E>(lane);
 #pragma unroll
-    for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::load(tt + s * KS);
-    const E* dvT = static_cast<const E*>(a.dVnT) + cix * V * C;
-    const E* dwT = static_cast<const E*>(a.dWT) + cix * K * C;
+    for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::ld(tt + s * KS);
+    const float* dvT = a.dVnT + cix * V * C;
+    const float* dwT = a.dWT + cix * K * C;
     E* dvo = static_cast<E*>(a.dv) + ((size_t)b * T * H + h) * V;
     E* dwo = static_cast<E*>(a.dw) + ((size_t)b * T * H + h) * V;
     for (int ct = 0; ct < CTV; ++ct) {
       f4 acc = f4_zero();
-      const E* br = dvT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+      const float* br = dvT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::load(br + s * KS));
+      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::ld(br + s * KS));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = wv * 16 + acc_row(r), vv = ct * 16 + acc_col();
-        s_dXu[i * LDV + vv] = from_f<E>(acc[r]);
+        s_dXu[i * LXV + vv] = acc[r];
         if (i < nvalid) {
           dvo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.W_(i, vv));
           dwo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.V_(i, vv));
@@ -207,38 +207,45 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
     for (int ct = 0; ct < CTK; ++ct) {
       f4 acc = f4_zero();
-      const E* br = dwT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+      const float* br = dwT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::load(br + s * KS));
+      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::ld(br + s * KS));
       dxw[ct] = acc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        s_dXw[(wv * 16 + acc_row(r)) * LDK + ct * 16 + acc_col()] = from_f<E>(acc[r]);
+      for (int r = 0; r < 4; ++r) s_dXw[(wv * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()] = acc[r];
     }
   }
   __syncthreads();
 
-  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower
+  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until R is free)
+  f4 dat[4];
   {
-    const E* Wg = static_cast<const E*>(a.W) + cix * C * K;
-    const E* Ug = static_cast<const E*>(a.U) + cix * C * V;
+    const float* Wg = a.W + cix * C * K;
+    const float* Ug = a.U + cix * C * V;
+#pragma unroll
     for (int J = 0; J < 4; ++J) {
       f4 acc = f4_zero();
       if (J <= wv) {
-        acc = mma_tile<E>(acc, s_dXw + wv * 16 * LDK, LDK, Wg + (size_t)J * 16 * K, K, K);
-        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LDV, LDV, Ug + (size_t)J * 16 * V, V, V);
+        acc = mma_tile<E>(acc, s_dXw + wv * 16 * LXK, LXK, Wg + (size_t)J * 16 * K, K, K);
+        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LXV, LXV, Ug + (size_t)J * 16 * V, V, V);
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
-        s_dA[i * AT_LD + j] = (j < i) ? -acc[r] : 0.f;
-      }
+      dat[J] = acc;
     }
   }
   __syncthreads();
-  // dQg and dKt of this chunk, for the final assembly
-  stage_rows<E>(s_dQg, LDK, static_cast<const E*>(a.dQg) + cix * C * K, K, C, K, C);
-  stage_rows<E>(s_dKt, LDK, static_cast<const E*>(a.dKt) + cix * C * K, K, C, K, C);
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
+      s_dA[i * AT_LD + j] = (j < i) ? -dat[J][r] : 0.f;
+    }
+  }
+  {
+    const float* dq = a.dAqk + cix * C * C;
+    for (int e = tid; e < C * C; e += 256) s_dQ[(e / C) * AT_LD + e % C] = dq[e];
+  }
+  __syncthreads();
 
   const bool safe = l0_block_safe<K>(s_gc, wv);
   const int R0 = 16 * wv;
@@ -326,6 +333,8 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 
   // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
   {
+    const float* dQg = a.dQg + cix * C * K;
+    const float* dKt = a.dKt + cix * C * K;
     const size_t tok = (size_t)b * T * H + h;
     E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
     E* dko = static_cast<E*>(a.dk) + tok * K;
@@ -341,7 +350,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         const float gcv = s_gc[i * GL + kc];
         const float eg = expf(gcv), ekt = expf(glast - gcv);
         const float bi = BV(i, kc), ki = KV(i, kc), qh = QV(i, kc) * in.scale;
-        const float gq = to_f(s_dQg[i * LDK + kc]), gk = to_f(s_dKt[i * LDK + kc]);
+        const float gq = dQg[i * K + kc], gk = dKt[i * K + kc];
         const float xw = dxw[ct][r];
         const float dqh = dqa[ct][r] + gq * eg;
         const float db_ = dbk[ct][r] * ki + xw * ki * eg;

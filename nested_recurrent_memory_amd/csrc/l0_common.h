@@ -39,6 +39,15 @@ struct ChunkIn {
   __device__ __forceinline__ float Q_(int i, int c) const { return ld(q, rowQ, i, c); }
   __device__ __forceinline__ float V_(int i, int c) const { return ld(v, rowV, i, c); }
   __device__ __forceinline__ float W_(int i, int c) const { return ld(w, rowV, i, c); }
+  // Mma<E>::KPL consecutive elements of row i from column c0 (zero past the end)
+  __device__ __forceinline__ void vals(const E* p, size_t row, int i, int c0, float* out) const {
+    if (i < nvalid) {
+      ld_vals<E>(p + (size_t)(t0 + i) * row + c0, out);
+    } else {
+#pragma unroll
+      for (int e = 0; e < Mma<E>::KPL; ++e) out[e] = 0.f;
+    }
+  }
 };
 
 constexpr int GCP = 1;   // padding of gc rows
@@ -73,17 +82,32 @@ struct ChunkLds {
   __device__ __forceinline__ float Q_(int i, int c) const { return to_f(q[i * LD + c]); }
 };
 
-// gc[i][k] = sum_{s<=i} g_s[k] within the chunk (zero past the end).
+// gc[i][k] = sum_{s<=i} g_s[k] within the chunk (zero past the end), into
+// s_gc [64][K + GCP]. TPC = 256 / K adjacent lanes share column k, each
+// summing 64 / TPC consecutive rows in registers (independent, coalesced
+// loads); the segment offsets come from the neighbouring lanes.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_cumsum(float* s_gc, const ChunkIn<E, K, V>& in) {
-  const int tid = threadIdx.x;
-  if (tid < K) {
-    float acc = 0.f;
-    for (int i = 0; i < CH; ++i) {
-      if (i < in.nvalid) acc += in.g[(size_t)(in.t0 + i) * in.rowK + tid];
-      s_gc[i * (K + GCP) + tid] = acc;
-    }
+  constexpr int TPC = 256 / K;
+  constexpr int SEG = CH / TPC;
+  const int tid = threadIdx.x, c = tid / TPC, part = tid % TPC;
+  float x[SEG];
+#pragma unroll
+  for (int r = 0; r < SEG; ++r) {
+    const int i = part * SEG + r;
+    x[r] = i < in.nvalid ? in.g[(size_t)(in.t0 + i) * in.rowK + c] : 0.f;
   }
+#pragma unroll
+  for (int r = 1; r < SEG; ++r) x[r] += x[r - 1];
+  const int base = lane_id() & ~(TPC - 1);
+  float off = 0.f;
+#pragma unroll
+  for (int p = 0; p < TPC - 1; ++p) {
+    const float t = __shfl(x[SEG - 1], base + p, WAVE);
+    if (p < part) off += t;
+  }
+#pragma unroll
+  for (int r = 0; r < SEG; ++r) s_gc[(part * SEG + r) * (K + GCP) + c] = x[r] + off;
 }
 
 // Largest decay inside 16-row block I, over every row and channel:
@@ -103,32 +127,36 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 }
 
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
-// Aqk (lower incl. diagonal) to global [64][64]; when aqkT_out != null also its
-// transpose. Wave w computes block-row w.
+// Aqk (lower incl. diagonal) to global fp32 [64][64]; when aqkT_out != null
+// also its transpose. Wave w computes block-row w.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
-                                           const ChunkIn<E, K, V>& in, E* aqk_out,
-                                           E* aqkT_out) {
+                                           const ChunkIn<E, K, V>& in, float* aqk_out,
+                                           float* aqkT_out) {
   constexpr int GL = K + GCP;
   constexpr int NKS = K / Mma<E>::KS;
-  typedef typename Mma<E>::Frag Frag;
+  constexpr int KPL = Mma<E>::KPL;
+  typedef typename Mma<E>::SFrag SF;
   const int lane = lane_id(), I = wave_id(), r = 16 * I;
   const bool safe = l0_block_safe<K>(s_gc, I);
   const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
-  Frag lf[NKS], qf[NKS];
+  SF lf[NKS], qf[NKS];
   const int ri = r + (lane & 15);
 #pragma unroll
   for (int s = 0; s < NKS; ++s) {
     const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-    lf[s] = Mma<E>::make([&](int e) {
-      const int c = c0 + e;
-      return in.B_(ri, c) * in.K_(ri, c) * expf(s_gc[ri * GL + c] - s_gc[r * GL + c]);
+    float bv[KPL], kv[KPL], qv[KPL];
+    in.vals(in.b, in.rowK, ri, c0, bv);
+    in.vals(in.k, in.rowK, ri, c0, kv);
+    lf[s] = Mma<E>::makes([&](int e) {
+      return bv[e] * kv[e] * expf(s_gc[ri * GL + c0 + e] - s_gc[r * GL + c0 + e]);
     });
-    if (want_q)
-      qf[s] = Mma<E>::make([&](int e) {
-        const int c = c0 + e;
-        return in.Q_(ri, c) * in.scale * expf(s_gc[ri * GL + c] - s_gc[r * GL + c]);
+    if (want_q) {
+      in.vals(in.q, in.rowQ, ri, c0, qv);
+      qf[s] = Mma<E>::makes([&](int e) {
+        return qv[e] * in.scale * expf(s_gc[ri * GL + c0 + e] - s_gc[r * GL + c0 + e]);
       });
+    }
   }
   for (int J = 0; J < 4; ++J) {
     f4 accA = f4_zero(), accQ = f4_zero();
@@ -137,10 +165,11 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
 #pragma unroll
       for (int s = 0; s < NKS; ++s) {
         const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-        Frag kf = Mma<E>::make([&](int e) {
-          const int c = c0 + e;
-          const float x = s_gc[r * GL + c] - s_gc[rj * GL + c];
-          return in.K_(rj, c) * expf(J < I ? x : fminf(x, 88.f));
+        float kv[KPL];
+        in.vals(in.k, in.rowK, rj, c0, kv);
+        const SF kf = Mma<E>::makes([&](int e) {
+          const float x = s_gc[r * GL + c0 + e] - s_gc[rj * GL + c0 + e];
+          return kv[e] * expf(J < I ? x : fminf(x, 88.f));
         });
         accA = Mma<E>::mma(accA, lf[s], kf);
         if (want_q) accQ = Mma<E>::mma(accQ, qf[s], kf);
@@ -164,20 +193,22 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
         }
       }
     }
+    f4 qt;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = r + acc_row(rr), j = 16 * J + acc_col();
       s_A[i * AT_LD + j] = (j < i) ? accA[rr] : 0.f;
-      const E qv = from_f<E>((j <= i) ? accQ[rr] : 0.f);
-      if (aqk_out) aqk_out[i * CH + j] = qv;
-      if (aqkT_out) aqkT_out[j * CH + i] = qv;
+      qt[rr] = (j <= i) ? accQ[rr] : 0.f;
+      if (aqk_out) aqk_out[i * CH + j] = qt[rr];
     }
+    if (aqkT_out) *reinterpret_cast<f4*>(aqkT_out + (16 * J + acc_col()) * CH + r + acc_row(0)) = qt;
   }
 }
 
 // T = (I + A)^-1 by 16-row blocks: diagonal blocks by forward substitution,
-// then T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ by sub-diagonal. s_P is scratch
-// [3][16][17]. Ends with a barrier.
+// then T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ by sub-diagonal. s_T has row
+// stride LDT; s_P is scratch [3][16][17]. Ends with a barrier.
+template <int LDT>
 __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s_P) {
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   if (wv == 0) {
@@ -192,11 +223,11 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
       t[i] = (i >= c) ? val : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s_T[(o + i) * AT_LD + o + c] = t[i];
+    for (int i = 0; i < 16; ++i) s_T[(o + i) * LDT + o + c] = t[i];
   } else {
     for (int e = tid - WAVE; e < CH * CH; e += 3 * WAVE) {
       const int i = e / CH, j = e % CH;
-      if ((i >> 4) != (j >> 4)) s_T[i * AT_LD + j] = 0.f;
+      if ((i >> 4) != (j >> 4)) s_T[i * LDT + j] = 0.f;
     }
   }
   __syncthreads();
@@ -207,7 +238,7 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
       const int I = d + blk, J = I - d;
       float acc = 0.f;
       for (int m = 16 * J; m < 16 * I; ++m)
-        acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * AT_LD + 16 * J + j];
+        acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * LDT + 16 * J + j];
       s_P[blk * 272 + i * 17 + j] = acc;
     }
     __syncthreads();
@@ -217,25 +248,25 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
       float acc = 0.f;
 #pragma unroll
       for (int m = 0; m < 16; ++m)
-        acc += s_T[(16 * I + i) * AT_LD + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
-      s_T[(16 * I + i) * AT_LD + 16 * J + j] = -acc;
+        acc += s_T[(16 * I + i) * LDT + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
+      s_T[(16 * I + i) * LDT + 16 * J + j] = -acc;
     }
     __syncthreads();
   }
 }
 
-// Right-hand sides transposed into s_X [(K+V)][LDX]: X[k][c] = b k e^gc,
+// Right-hand sides transposed into s_X fp32 [(K+V)][LDX]: X[k][c] = b k e^gc,
 // X[K+v][c] = w v.
 template <typename E, int K, int V, int LDX>
-__device__ __forceinline__ void l0_build_X(E* s_X, const float* s_gc, const ChunkIn<E, K, V>& in) {
+__device__ __forceinline__ void l0_build_X(float* s_X, const float* s_gc, const ChunkIn<E, K, V>& in) {
   const int tid = threadIdx.x;
   for (int e = tid; e < CH * K; e += 256) {
     const int c = e / K, kk = e % K;
-    s_X[kk * LDX + c] = from_f<E>(in.B_(c, kk) * in.K_(c, kk) * expf(s_gc[c * (K + GCP) + kk]));
+    s_X[kk * LDX + c] = in.B_(c, kk) * in.K_(c, kk) * expf(s_gc[c * (K + GCP) + kk]);
   }
   for (int e = tid; e < CH * V; e += 256) {
     const int c = e / V, vv = e % V;
-    s_X[(K + vv) * LDX + c] = from_f<E>(in.W_(c, vv) * in.V_(c, vv));
+    s_X[(K + vv) * LDX + c] = in.W_(c, vv) * in.V_(c, vv);
   }
 }
 

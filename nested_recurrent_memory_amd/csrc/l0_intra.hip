@@ -14,6 +14,8 @@
 //   gam  = e^gc_last
 // The forward consumes W, U, Kt^T, Qg, Aqk; the reverse scan consumes the
 // transposed copies Kt, W^T, Qg^T, Aqk^T, written when their pointers are set.
+// Every output is fp32; for bf16 inputs the products run on bf16 MFMA with
+// the derived operands split in two (ngdn_common.h).
 //
 // One workgroup (4 waves) per (batch, head, chunk). Decay products are formed
 // without overflow: inside block-row I (16 rows starting at r = 16 I) every
@@ -29,7 +31,7 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int C = CH;
-  constexpr int LDX = C + 8;                 // k-contiguous rows of length C
+  constexpr int LDX = C + 4;                 // fp32 rows of length C, 16-byte aligned
   constexpr int GL = K + GCP;
   const int NT = a.NT, H = a.H;
   const int n = blockIdx.x % NT;
@@ -37,21 +39,21 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   const int h = bh % H, b = bh / H;
   const int wv = wave_id(), tid = threadIdx.x;
 
-  // LDS: gc (fp32), then a region used first for A/T (fp32), then for the
-  // transposed right-hand sides X (E), then for Kt^T / Qg^T staging (E); T in E.
+  // LDS: gc, T (fp32, MFMA rows), then a region used first for A and the
+  // inversion scratch, then for the transposed right-hand sides X, then for
+  // the Kt^T / Qg^T staging.
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_AT = sizeof(float) * 2 * C * AT_LD + sizeof(float) * 3 * 16 * 17;
-  constexpr size_t SZ_X = sizeof(E) * (K + V) * LDX;
-  constexpr size_t SZ_R = SZ_AT > SZ_X ? SZ_AT : SZ_X;
-  constexpr size_t SZ_TE = sizeof(E) * C * LDX;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R + SZ_TE];
+  constexpr size_t SZ_T = sizeof(float) * C * LDX;
+  constexpr size_t SZ_AP = sizeof(float) * C * AT_LD + sizeof(float) * 3 * 16 * 17;
+  constexpr size_t SZ_X = sizeof(float) * (K + V) * LDX;
+  constexpr size_t SZ_R = SZ_AP > SZ_X ? SZ_AP : SZ_X;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_T + SZ_R];
   float* s_gc = reinterpret_cast<float*>(smem);
-  char* region = smem + SZ_GC;
+  float* s_T = reinterpret_cast<float*>(smem + SZ_GC);
+  char* region = smem + SZ_GC + SZ_T;
   float* s_A = reinterpret_cast<float*>(region);
-  float* s_T = s_A + C * AT_LD;
-  float* s_P = s_T + C * AT_LD;               // [3][16][17]
-  E* s_X = reinterpret_cast<E*>(region);
-  E* s_TE = reinterpret_cast<E*>(smem + SZ_GC + SZ_R);
+  float* s_P = s_A + C * AT_LD;               // [3][16][17]
+  float* s_X = reinterpret_cast<float*>(region);
 
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, a.T, H, a.L, a.scale);
@@ -62,20 +64,17 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   __syncthreads();
 
   // ---- 2. A and Aqk
-  l0_build_A(s_A, s_gc, in, static_cast<E*>(a.Aqk) + cix * C * C,
-             a.AqkT ? static_cast<E*>(a.AqkT) + cix * C * C : nullptr);
+  l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr);
   __syncthreads();
 
   // ---- 3. T = (I + A)^-1
-  l0_invert(s_A, s_T, s_P);
-  for (int e = tid; e < C * C; e += 256) {
-    const int i = e / C, j = e % C;
-    s_TE[i * LDX + j] = from_f<E>(s_T[i * AT_LD + j]);
-    if (a.TT) static_cast<E*>(a.TT)[cix * C * C + e] = from_f<E>(s_T[j * AT_LD + i]);
+  l0_invert<LDX>(s_A, s_T, s_P);
+  if (a.TT) {
+    float* tt = a.TT + cix * C * C;
+    for (int e = tid; e < C * C; e += 256) tt[e] = s_T[(e % C) * LDX + e / C];
   }
-  __syncthreads();
 
-  // ---- 4. right-hand sides, transposed
+  // ---- 4. right-hand sides, transposed (s_A and s_P are dead)
   l0_build_X<E, K, V, LDX>(s_X, s_gc, in);
   __syncthreads();
 
@@ -83,51 +82,53 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   {
     const int I = wv;
     const int kd = tri_depth<E>(I);
-    E* Wo = static_cast<E*>(a.W) + cix * C * K;
-    E* Uo = static_cast<E*>(a.U) + cix * C * V;
-    E* WTo = a.WT ? static_cast<E*>(a.WT) + cix * K * C : nullptr;
+    float* Wo = a.W + cix * C * K;
+    float* Uo = a.U + cix * C * V;
+    float* WTo = a.WT ? a.WT + cix * K * C : nullptr;
     for (int tc = 0; tc < (K + V) / 16; ++tc) {
-      f4 acc = mma_tile<E>(f4_zero(), s_TE + 16 * I * LDX, LDX, s_X + 16 * tc * LDX, LDX, kd);
+      f4 acc = mma_tile<E>(f4_zero(), s_T + 16 * I * LDX, LDX, s_X + 16 * tc * LDX, LDX, kd);
+      const int i0 = 16 * I + acc_row(0), col = 16 * tc + acc_col();
+      if (col < K) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = 16 * I + acc_row(rr), col = 16 * tc + acc_col();
-        if (col < K) {
-          Wo[i * K + col] = from_f<E>(acc[rr]);
-          if (WTo) WTo[col * C + i] = from_f<E>(acc[rr]);
-        } else {
-          Uo[i * V + (col - K)] = from_f<E>(acc[rr]);
-        }
+        for (int rr = 0; rr < 4; ++rr) Wo[(i0 + rr) * K + col] = acc[rr];
+        if (WTo) *reinterpret_cast<f4*>(WTo + col * C + i0) = acc;
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) Uo[(i0 + rr) * V + (col - K)] = acc[rr];
       }
     }
   }
   __syncthreads();
 
   // ---- 6. Kt (and its transpose), Qg (and its transpose), gam
-  E* s_kt = s_X;             // reuse: [K][LDX]
-  E* s_qg = s_X + K * LDX;   // [K][LDX]; fits since (K + V) >= 2 K when V >= K,
-                             // otherwise Qg^T goes straight to global below
+  float* s_kt = s_X;             // reuse: [K][LDX]
+  float* s_qg = s_X + K * LDX;   // [K][LDX]; fits since (K + V) >= 2 K when V >= K,
+                                 // otherwise Qg^T goes straight to global below
   const bool qg_in_lds = V >= K;
+  float* Qgo = a.Qg + cix * C * K;
   for (int e = tid; e < C * K; e += 256) {
     const int c = e / K, kk = e % K;
     const float gcv = s_gc[c * GL + kk];
-    s_kt[kk * LDX + c] = from_f<E>(in.K_(c, kk) * expf(s_gc[(C - 1) * GL + kk] - gcv));
+    s_kt[kk * LDX + c] = in.K_(c, kk) * expf(s_gc[(C - 1) * GL + kk] - gcv);
     const float qg = in.Q_(c, kk) * in.scale * expf(gcv);
-    static_cast<E*>(a.Qg)[cix * C * K + c * K + kk] = from_f<E>(qg);
-    if (qg_in_lds) s_qg[kk * LDX + c] = from_f<E>(qg);
-    else if (a.QgT) static_cast<E*>(a.QgT)[cix * K * C + kk * C + c] = from_f<E>(qg);
+    Qgo[c * K + kk] = qg;
+    if (qg_in_lds) s_qg[kk * LDX + c] = qg;
+    else if (a.QgT) a.QgT[cix * K * C + kk * C + c] = qg;
   }
   if (tid < K) a.gam[cix * K + tid] = expf(s_gc[(C - 1) * GL + tid]);
   __syncthreads();
   {
-    E* Ko = static_cast<E*>(a.KtT) + cix * K * C;
-    E* QTo = a.QgT ? static_cast<E*>(a.QgT) + cix * K * C : nullptr;
-    for (int e = tid; e < K * C; e += 256) {
-      const int kk = e / C, c = e % C;
-      Ko[kk * C + c] = s_kt[kk * LDX + c];
-      if (QTo && qg_in_lds) QTo[kk * C + c] = s_qg[kk * LDX + c];
+    // rows of 64 as 16-byte vectors
+    float* Ko = a.KtT + cix * K * C;
+    float* QTo = a.QgT ? a.QgT + cix * K * C : nullptr;
+    for (int e = tid; e < K * C / 4; e += 256) {
+      const int kk = e / (C / 4), c = (e % (C / 4)) * 4;
+      *reinterpret_cast<f4*>(Ko + kk * C + c) = *reinterpret_cast<const f4*>(s_kt + kk * LDX + c);
+      if (QTo && qg_in_lds)
+        *reinterpret_cast<f4*>(QTo + kk * C + c) = *reinterpret_cast<const f4*>(s_qg + kk * LDX + c);
     }
     if (a.Kt) {
-      E* Kn = static_cast<E*>(a.Kt) + cix * C * K;
+      float* Kn = a.Kt + cix * C * K;
       for (int e = tid; e < C * K; e += 256) {
         const int c = e / K, kk = e % K;
         Kn[c * K + kk] = s_kt[kk * LDX + c];

@@ -33,19 +33,60 @@ template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x
 __device__ __forceinline__ f4 f4_zero() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // ---------------------------------------------------------------- MFMA
+//
+// Operands come in two kinds. Exact operands are the op's bf16 inputs and
+// parameters. Derived operands (everything computed: W, U, T, states, Vn,
+// gradients) are stored in fp32. For bf16 inputs a derived value x enters the
+// bf16 matrix core as a pair x = hi + lo (each bf16, together about 16
+// mantissa bits) and a product takes 2 MFMAs (exact x derived: a*hi + a*lo) or
+// 3 (derived x derived: hi*hi + hi*lo + lo*hi; lo*lo is below fp32 rounding of
+// the sum). This keeps bf16 results within fp32-level agreement of an exact
+// evaluation at bf16 matrix-core rates. For fp32 inputs both kinds are plain
+// fp32 and every product is one fp32 MFMA.
+//
+// The fragment type follows the pointer: ld(const bf16*) gives an exact
+// fragment, ld(const float*) a derived one.
 
 template <typename E> struct Mma;
 
 template <> struct Mma<bf16> {
   static constexpr int KS = 32;   // k per instruction
   static constexpr int KPL = 8;   // k-values per lane
-  typedef bf16x8 Frag;
+  typedef bf16x8 Frag;            // exact
+  struct SFrag { bf16x8 hi, lo; };  // derived, split
   __device__ __forceinline__ static f4 mma(f4 acc, Frag a, Frag b) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
   }
-  __device__ __forceinline__ static Frag load(const bf16* p) {
+  __device__ __forceinline__ static f4 mma(f4 acc, Frag a, SFrag b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b.lo, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b.hi, acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f4 mma(f4 acc, SFrag a, Frag b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b, acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f4 mma(f4 acc, SFrag a, SFrag b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static Frag ld(const bf16* p) {
     return *reinterpret_cast<const bf16x8*>(p);
   }
+  __device__ __forceinline__ static SFrag ld(const float* p) {
+    const f4 x0 = *reinterpret_cast<const f4*>(p);
+    const f4 x1 = *reinterpret_cast<const f4*>(p + 4);
+    SFrag r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r.hi[e] = hi_of(x0[e]);
+      r.lo[e] = lo_of(x0[e], r.hi[e]);
+      r.hi[e + 4] = hi_of(x1[e]);
+      r.lo[e + 4] = lo_of(x1[e], r.hi[e + 4]);
+    }
+    return r;
+  }
+  // exact values (inputs, or products known to be exact in bf16)
   template <typename F>
   __device__ __forceinline__ static Frag make(F f) {  // f(e) -> float, e < KPL
     Frag r;
@@ -53,37 +94,45 @@ template <> struct Mma<bf16> {
     for (int e = 0; e < 8; ++e) r[e] = (bf16)f(e);
     return r;
   }
-  // x = hi + lo to about 16 mantissa bits: products against an operand built
-  // this way keep fp32-level agreement between sums that must cancel.
+  // derived values
   template <typename F>
-  __device__ __forceinline__ static void make_split(F f, Frag& hi, Frag& lo) {
+  __device__ __forceinline__ static SFrag makes(F f) {
+    SFrag r;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = f(e);
-      const bf16 h = (bf16)x;
-      hi[e] = h;
-      lo[e] = (bf16)(x - (float)h);
+      r.hi[e] = hi_of(x);
+      r.lo[e] = lo_of(x, r.hi[e]);
     }
+    return r;
   }
-  static constexpr bool SPLIT = true;
+  __device__ __forceinline__ static Frag zero() {
+    Frag r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (bf16)0.f;
+    return r;
+  }
+  __device__ __forceinline__ static SFrag szero() { return SFrag{zero(), zero()}; }
+  // x = hi + lo: hi is x rounded to bf16, lo the rounded remainder
+  __device__ __forceinline__ static bf16 hi_of(float x) { return (bf16)x; }
+  __device__ __forceinline__ static bf16 lo_of(float x, bf16 hi) { return (bf16)(x - (float)hi); }
 };
 
 template <> struct Mma<float> {
   static constexpr int KS = 4;
   static constexpr int KPL = 1;
   typedef float Frag;
-  __device__ __forceinline__ static f4 mma(f4 acc, Frag a, Frag b) {
+  typedef float SFrag;
+  __device__ __forceinline__ static f4 mma(f4 acc, float a, float b) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
   }
-  __device__ __forceinline__ static Frag load(const float* p) { return *p; }
+  __device__ __forceinline__ static float ld(const float* p) { return *p; }
   template <typename F>
-  __device__ __forceinline__ static Frag make(F f) { return f(0); }
+  __device__ __forceinline__ static float make(F f) { return f(0); }
   template <typename F>
-  __device__ __forceinline__ static void make_split(F f, Frag& hi, Frag& lo) {
-    hi = f(0);
-    lo = 0.f;
-  }
-  static constexpr bool SPLIT = false;
+  __device__ __forceinline__ static float makes(F f) { return f(0); }
+  __device__ __forceinline__ static float zero() { return 0.f; }
+  __device__ __forceinline__ static float szero() { return 0.f; }
 };
 
 template <typename E> __device__ __forceinline__ int kofs(int lane) {
@@ -91,21 +140,54 @@ template <typename E> __device__ __forceinline__ int kofs(int lane) {
 }
 
 // D[16x16] += A[16 x kd] * B[kd x 16], A row-major (k contiguous, stride lda),
-// B given as Bt[16][kd] (k contiguous, stride ldb). kd a multiple of KS.
-template <typename E>
-__device__ __forceinline__ f4 mma_tile(f4 acc, const E* A, int lda, const E* Bt,
+// B given as Bt[16][kd] (k contiguous, stride ldb). kd a multiple of KS. Each
+// of A and Bt is exact (E) or derived (float) storage.
+template <typename E, typename TA, typename TB>
+__device__ __forceinline__ f4 mma_tile(f4 acc, const TA* A, int lda, const TB* Bt,
                                        int ldb, int kd) {
   const int l = lane_id();
-  const E* pa = A + (l & 15) * lda + kofs<E>(l);
-  const E* pb = Bt + (l & 15) * ldb + kofs<E>(l);
+  const TA* pa = A + (l & 15) * lda + kofs<E>(l);
+  const TB* pb = Bt + (l & 15) * ldb + kofs<E>(l);
   for (int k = 0; k < kd; k += Mma<E>::KS)
-    acc = Mma<E>::mma(acc, Mma<E>::load(pa + k), Mma<E>::load(pb + k));
+    acc = Mma<E>::mma(acc, Mma<E>::ld(pa + k), Mma<E>::ld(pb + k));
   return acc;
 }
+
+// Mma<E>::KPL consecutive elements at p as floats (one 16-byte load for bf16).
+template <typename E>
+__device__ __forceinline__ void ld_vals(const E* p, float* out) {
+  if constexpr (std::is_same<E, float>::value) {
+    out[0] = *p;
+  } else {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+  }
+}
+
+// Row padding (elements) that keeps rows 16-byte aligned and staggers banks.
+template <typename T> constexpr int pad16() { return 16 / (int)sizeof(T); }
 
 // Accumulator element (r) of this lane lives at (row, col) of the 16x16 tile.
 __device__ __forceinline__ int acc_row(int r) { return 4 * (lane_id() >> 4) + r; }
 __device__ __forceinline__ int acc_col() { return lane_id() & 15; }
+
+// Stages rows x cols fp32 (row stride src_ld) into LDS rows of stride ld with
+// 16-byte accesses.
+__device__ __forceinline__ void stage_f32(float* dst, int ld, const float* src, int src_ld,
+                                          int rows, int cols) {
+  const int segs = cols / 4;
+  for (int e = threadIdx.x; e < rows * segs; e += blockDim.x) {
+    const int r = e / segs, c = (e % segs) * 4;
+    *reinterpret_cast<f4*>(dst + r * ld + c) = *reinterpret_cast<const f4*>(src + (size_t)r * src_ld + c);
+  }
+}
+
+// S [K][V] fp32 into LDS as S^T [V][ld] (k contiguous).
+template <int K, int V>
+__device__ __forceinline__ void stage_state_T(float* dst, int ld, const float* S) {
+  for (int e = threadIdx.x; e < K * V; e += blockDim.x) dst[(e % V) * ld + e / V] = S[e];
+}
 
 // ---------------------------------------------------------------- misc
 

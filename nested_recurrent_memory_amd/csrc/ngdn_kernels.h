@@ -8,16 +8,16 @@ namespace ngdn {
 
 // Level-0 intra-chunk forward. Inputs in the reference layout (contiguous):
 // q [B,T,H,L,K] (level-0 slice read), k, b [B,T,H,K], v, w [B,T,H,V] in the
-// working dtype, g [B,T,H,K] fp32. Outputs, per (b, h, chunk):
+// working dtype, g [B,T,H,K] fp32. Outputs (fp32), per (b, h, chunk):
 // W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64], Qg [B,H,NT,64,K],
-// Aqk [B,H,NT,64,64] in the working dtype; gam [B,H,NT,K] fp32. When set,
-// the transposed copies for the reverse scan: Kt [B,H,NT,64,K],
-// WT [B,H,NT,K,64], QgT [B,H,NT,K,64], AqkT [B,H,NT,64,64].
+// Aqk [B,H,NT,64,64], gam [B,H,NT,K]. When set, the transposed copies for the
+// backward: Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64],
+// AqkT [B,H,NT,64,64], TT [B,H,NT,64,64] (= T^T).
 struct L0IntraArgs {
   const void* q; const void* k; const void* v; const float* g;
   const void* b; const void* w;
-  void* W; void* U; void* KtT; void* Qg; void* Aqk; float* gam;
-  void* Kt; void* WT; void* QgT; void* AqkT; void* TT;
+  float* W; float* U; float* KtT; float* Qg; float* Aqk; float* gam;
+  float* Kt; float* WT; float* QgT; float* AqkT; float* TT;
   int B, T, H, L, NT;
   float scale;
 };
@@ -25,16 +25,16 @@ hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream
 
 // A sequence of delta-rule steps per (b, h):
 //   Vn = U - A S;   S <- diag(gam) S + BT Vn
-// A [B*H,S,M,K], BT [B*H,S,K,M], U [B*H,S,M,V] in the working dtype, gam
-// [B*H,S,K] fp32. The state entering each step is stored: mode 0 as
-// hT [B,H,S,V,K] in the working dtype (level 0, chunk states), mode 1 as fp32
-// [B,NG,H,K,V] (upper levels, group states; NG >= S, extra groups hold the
-// final state). vnT [B,H,S,V,M] (working dtype) receives Vn when not null.
+// A [B*H,S,M,K], BT [B*H,S,K,M], U [B*H,S,M,V], gam [B*H,S,K], all fp32. The
+// state entering each step is stored (fp32): mode 0 as hT [B,H,S,V,K] (level
+// 0, chunk states), mode 1 as [B,NG,H,K,V] (upper levels, group states;
+// NG >= S, extra groups hold the final state). vnT [B,H,S,V,M] receives Vn
+// when not null.
 struct ScanArgs {
-  const void* A; const void* BT; const void* U; const float* gam;
+  const float* A; const float* BT; const float* U; const float* gam;
   const float* init; long long init_sb, init_sh;
-  void* states; int state_mode; int NG;
-  void* vnT;
+  float* states; int state_mode; int NG;
+  float* vnT;
   float* fin; long long fin_sb, fin_sh;
   int B, H, S, M, V;
 };
@@ -46,18 +46,19 @@ hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 // [B*H,inj_nf,K,V], added before step j when (j+1) % inj_every == 0). Upper
 // levels set d_states (fp32 [B,NG,H,K,V], added after step j, and for every
 // stored group past the last step before the first). d_final seeds the state
-// gradient. Outputs: dSp [B*H,S,K,V] (gradient of the state after each step;
-// dsp_mode 0 working dtype, 1 fp32), dVn [B*H,S,M,V] (dvn_mode likewise),
-// dinit (fp32 [K][V] at strides) when set.
+// gradient. Outputs (fp32): dSp [B*H,S,K,V] (gradient of the state after
+// each step), dVn [B*H,S,M,V], dVnT = dVn^T [B*H,S,V,M] (when set), dinit
+// ([K][V] at strides, when set). All working tensors are fp32; dout and mix
+// are in the working dtype.
 struct ScanBwdArgs {
-  const void* Bop; const void* AT; const float* gam;
-  const void* AqkT; const void* QgT; const void* dout; const void* mix; int T, L;
+  const float* Bop; const float* AT; const float* gam;
+  const float* AqkT; const float* QgT; const void* dout; const void* mix; int T, L;
   const float* inj; int inj_every, inj_nf;
   const float* d_states; int NG;
   const float* d_final; long long df_sb, df_sh;
-  void* dSp; int dsp_mode;
-  void* dVn; int dvn_mode;
-  void* dVnT;                 // optional: dVn^T [B*H,S,V,M], working dtype
+  float* dSp;
+  float* dVn;
+  float* dVnT;
   float* dinit; long long di_sb, di_sh;
   int B, H, S, M, V;
 };
@@ -70,22 +71,22 @@ namespace ngdn {
 // Promotion probe for one level (ops/probe.py:34-136), one workgroup per
 // (batch, firing, head). Reads the lower level's state after this level's
 // firing i: stored state src = ((i+1) f_here) / f_below, or the lower final
-// state when src == NGb. below_mode 0: hT [B,H,NGb,V,K] (working dtype);
-// below_mode 1: fp32 [B,NGb,H,K,V]. Parameters are this level's slices in the
+// state when src == NGb. below_mode 0: hT [B,H,NGb,V,K]; below_mode 1:
+// [B,NGb,H,K,V] (both fp32). Parameters are this level's slices in the
 // working dtype: bank [H,Nmax,K], kp [H,K,V], and the transposed projections
 // bpT [H,K,V] (= b_proj^T), wpT [H,V,V] (= w_proj^T), gpT [H,K,V].
-// Scan-ready outputs [B,H,NF,...]: A = keys*b*e^g [N,K], KT = keys^T [K,N],
-// U = vals*w [N,V] (working dtype), gam = e^g [K] fp32. Reference-format
-// outputs (fp32, [B,NF,H,...]) are written when their pointers are set.
+// Scan-ready outputs [B,H,NF,...] (fp32): A = keys*b*e^g [N,K], KT = keys^T
+// [K,N], U = vals*w [N,V], gam = e^g [K]. Reference-format outputs (fp32,
+// [B,NF,H,...]) are written when their pointers are set.
 struct ProbeArgs {
-  const void* below; int below_mode; int NGb;
+  const float* below; int below_mode; int NGb;
   const float* below_fin; long long bf_sb, bf_sh;
   int f_below, f_here;
   const void* bank; int Nmax;
   const void* kp; const void* bpT; const void* wpT; const void* gpT;
   int merge;
-  void* A; void* KT; void* U; float* gam;
-  void* keysN; void* AT;   // optional: keys [B,H,NF,N,K], A^T [B,H,NF,K,N] for the reverse scan
+  float* A; float* KT; float* U; float* gam;
+  float* keysN; float* AT;   // optional: keys [B,H,NF,N,K], A^T [B,H,NF,K,N] for the reverse scan
   float* keys; float* vals; float* bo; float* wo; float* go;
   int B, H, NF, N, V;
 };
@@ -98,7 +99,7 @@ hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
 // bankT [H,K,Nmax], original bp [H,V,K], wp [H,V,V], gp [H,V,K]); this
 // level's group states Sg fp32 [B,NG,H,K,V]; the reverse scan's dSp (fp32
 // [B,H,NF,K,V], gradient of the state after firing i) and dvn (fp32
-// [B,H,NF,N,V]). Workspace (working dtype, [B,H,NF,N,*]): Vals, du, dxb,
+// [B,H,NF,N,V]). Workspace (fp32, [B,H,NF,N,*]): Vals, du, dxb,
 // dxg [N,K-or-V], dxw, dVals [N,V]; the parameter-gradient reduction reads
 // them. dbank (fp32 [H,Nmax,K]) is accumulated atomically.
 // The gradient of the gathered lower state goes to: inj (level 1; fp32
@@ -110,17 +111,17 @@ struct ProbeBwdArgs {
   const void* kpT; const void* bankT; const void* bp; const void* wp; const void* gp;
   const float* Sg; int NG;
   const float* dSp; const float* dvn;
-  void* wsV; void* wsdu; void* wsdxb; void* wsdxg; void* wsdxw; void* wsdV;
+  float* wsV; float* wsdu; float* wsdxb; float* wsdxg; float* wsdxw; float* wsdV;
   float* dbank;
   float* inj; float* d_below; float* d_below_fin;
 };
 hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st);
 
 // C_h[X][Y] += sum over rows m = (b, i, n) of A[b,h,i,n,X] B[b,h,i,n,Y]
-// (working dtype in, fp32 out, accumulated atomically), for the per-head
-// parameter gradients of a level: one workgroup per (head, slice of items).
+// (fp32, accumulated atomically), for the per-head parameter gradients of a
+// level: one workgroup per (head, slice of items).
 struct AtBArgs {
-  const void* A; const void* Bm; float* C;
+  const float* A; const float* Bm; float* C;
   int B, H, NF, N, X, Y;
   int split;
 };
@@ -134,12 +135,12 @@ constexpr int MAXL = 8;
 
 // Output of the whole op for one chunk (ops/chunk.py:250-286; ops/naive.py:376-390):
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[n / f_l]
-// Level-0 terms from the intra/scan kernels ([B,H,NT,...], working dtype);
+// Level-0 terms from the intra/scan kernels ([B,H,NT,...], fp32);
 // q [B,T,H,L,K], mix [B,T,H,L] (working dtype); upper states fp32
 // [B,NG_l,H,K,V]. o [B,T,H,V] in the working dtype. When reads is set, each
 // level's unmixed read is also written, fp32 [L,B,T,H,V].
 struct OutputArgs {
-  const void* Qg; const void* Aqk; const void* hT; const void* vnT;
+  const float* Qg; const float* Aqk; const float* hT; const float* vnT;
   const void* q; const void* mix;
   const float* states[MAXL]; int NGl[MAXL]; int f[MAXL];
   void* o; float* reads;
@@ -175,12 +176,12 @@ hipError_t read_state_bwd(const ReadStateBwdArgs& a, int dtype, int K, int V, hi
 //   dQg = dO S^T, dW = -dVn S^T, dKt = Vn dS'^T, dAqk = dO Vn^T (j <= i),
 //   dgam_k = sum_v dS'[k][v] S[k][v]
 // with S = h (hT), dS' the state gradient after the chunk, dO = mix_0 do.
-// Outputs dQg, dW, dKt [B,H,NT,64,K], dAqk [B,H,NT,64,64] (working dtype),
-// dgam [B,H,NT,K] fp32.
+// Outputs (fp32) dQg, dKt [B,H,NT,64,K], dWT [B,H,NT,K,64], dAqk
+// [B,H,NT,64,64], dgam [B,H,NT,K]; dout and mix in the working dtype.
 struct L0BwdStateArgs {
-  const void* hT; const void* dSp; const void* vnT; const void* dVn;
+  const float* hT; const float* dSp; const float* vnT; const float* dVn;
   const void* dout; const void* mix;
-  void* dQg; void* dWT; void* dKt; void* dAqk; float* dgam;
+  float* dQg; float* dWT; float* dKt; float* dAqk; float* dgam;
   int B, T, H, L, NT;
 };
 hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStream_t st);
@@ -193,9 +194,9 @@ hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStr
 // and dg (fp32).
 struct L0BwdIntraArgs {
   const void* q; const void* k; const void* v; const float* g; const void* b; const void* w;
-  const void* W; const void* U; const void* TT;
-  const void* dQg; const void* dWT; const void* dKt; const void* dAqk; const float* dgam;
-  const void* dVnT;
+  const float* W; const float* U; const float* TT;
+  const float* dQg; const float* dWT; const float* dKt; const float* dAqk; const float* dgam;
+  const float* dVnT;
   void* dq; void* dk; void* dv; float* dg; void* db; void* dw;
   int B, T, H, L, NT;
   float scale;

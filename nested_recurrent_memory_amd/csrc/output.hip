@@ -3,8 +3,9 @@
 // the per-token mix, written once (ops/chunk.py:129-156 read_level and the
 // accumulation at :250-251,285-286; ops/naive.py:376-390).
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l (scale q_l) S_l[group]
-// Each product is staged through LDS as [64 x kd] x [kd x V] and run on MFMA;
-// wave w owns output rows 16w..16w+15.
+// Each product runs on MFMA with the right operand staged in LDS (fp32) and the
+// left operand's rows read from global by the wave that owns them; wave w owns
+// output rows 16w..16w+15.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -12,10 +13,11 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   constexpr int C = CH;
-  constexpr int LD = K + 8;
+  constexpr int LD = K + 4;
+  constexpr int LDC = C + 4;
   constexpr int CTV = V / 16;
-  __shared__ __attribute__((aligned(16))) E s_A[C * LD];
-  __shared__ __attribute__((aligned(16))) E s_B[V * LD];
+  constexpr int KS = Mma<E>::KS;
+  __shared__ __attribute__((aligned(16))) float s_B[V * (LD > LDC ? LD : LDC)];
 
   const int NT = a.NT, H = a.H, T = a.T, L = a.L;
   const int n = blockIdx.x % NT;
@@ -25,6 +27,7 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   const int nvalid = min(C, T - t0);
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const size_t cix = ((size_t)bh * NT + n);
+  const int ri = wv * 16 + (lane & 15);      // A-operand row of this lane
 
   const E* mixp = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L;
   auto mixw = [&](int i, int l) -> float {
@@ -36,10 +39,15 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   for (int c = 0; c < CTV; ++c) out[c] = f4_zero();
   f4 acc[CTV];
 
-  auto run = [&](int kd) {
+  // acc[c] += A[rows of this wave][0:kd] * s_B[c-th 16 rows][0:kd]^T, the A
+  // rows read from global (fp32 derived or exact inputs)
+  auto run = [&](const auto* arow, int ldb, int kd) {
+    for (int k0 = 0; k0 < kd; k0 += KS) {
+      const auto fa = Mma<E>::ld(arow + k0);
 #pragma unroll
-    for (int c = 0; c < CTV; ++c)
-      acc[c] = mma_tile<E>(acc[c], s_A + wv * 16 * LD, LD, s_B + c * 16 * LD, LD, kd);
+      for (int c = 0; c < CTV; ++c)
+        acc[c] = Mma<E>::mma(acc[c], fa, Mma<E>::ld(s_B + (c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + k0));
+    }
   };
   auto fold = [&](int l, float sc) {
 #pragma unroll
@@ -56,47 +64,29 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
     }
   };
 
-  // ---- level 0: Qg h
+  // ---- level 0: Qg h + Aqk Vn
 #pragma unroll
   for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-  {
-    const E* Qg = static_cast<const E*>(a.Qg) + cix * C * K;
-    const E* hT = static_cast<const E*>(a.hT) + cix * V * K;
-    for (int e = tid; e < C * K; e += 256) s_A[(e / K) * LD + e % K] = Qg[e];
-    for (int e = tid; e < V * K; e += 256) s_B[(e / K) * LD + e % K] = hT[e];
-  }
+  stage_f32(s_B, LD, a.hT + cix * V * K, K, V, K);
   __syncthreads();
-  run(K);
+  run(a.Qg + cix * C * K + (size_t)ri * K + kofs<E>(lane), LD, K);
   __syncthreads();
-  // ---- level 0: Aqk Vn
-  {
-    const E* Aq = static_cast<const E*>(a.Aqk) + cix * C * C;
-    const E* vT = static_cast<const E*>(a.vnT) + cix * V * C;
-    for (int e = tid; e < C * C; e += 256) s_A[(e / C) * LD + e % C] = Aq[e];
-    for (int e = tid; e < V * C; e += 256) s_B[(e / C) * LD + e % C] = vT[e];
-  }
+  stage_f32(s_B, LDC, a.vnT + cix * V * C, C, V, C);
   __syncthreads();
-  run(C);
+  run(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), LDC, C);
   fold(0, 1.f);
   __syncthreads();
 
-  // ---- upper levels
-  const E* qb = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K;
+  // ---- upper levels: (scale q_l) S_l[group], q rows exact
+  const E* qrow = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K +
+                  (size_t)(t0 + min(ri, nvalid - 1)) * H * L * K + kofs<E>(lane);
   for (int l = 1; l < L; ++l) {
     const int grp = n / a.f[l];
-    const float* S = a.states[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * K * V;
-    for (int e = tid; e < C * K; e += 256) {
-      const int i = e / K, k = e % K;
-      s_A[i * LD + k] = i < nvalid ? qb[(size_t)(t0 + i) * H * L * K + (size_t)l * K + k] : from_f<E>(0.f);
-    }
-    for (int e = tid; e < K * V; e += 256) {
-      const int k = e / V, v = e % V;
-      s_B[v * LD + k] = from_f<E>(S[e]);
-    }
+    stage_state_T<K, V>(s_B, LD, a.states[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * K * V);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-    run(K);
+    run(qrow + (size_t)l * K, LD, K);   // rows past the end repeat the last row; fold drops them
     fold(l, a.scale);
     __syncthreads();
   }

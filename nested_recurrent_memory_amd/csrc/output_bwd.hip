@@ -15,15 +15,16 @@ template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   const OutputArgs& a = ab.f;
   constexpr int C = CH;
-  constexpr int LD = K + 8;
-  constexpr int LDV = V + 8;
+  constexpr int LD = K + 4;
+  constexpr int LDV = V + 4;
+  constexpr int LDC = C + 4;
   constexpr int CTV = V / 16;
   constexpr int CTK = K / 16;
-  constexpr size_t SZ_A = sizeof(E) * C * (LD > LDV ? LD : LDV);
-  constexpr size_t SZ_B = sizeof(E) * (V * LD > K * LDV ? V * LD : K * LDV);
-  __shared__ __attribute__((aligned(16))) char smem[SZ_A + SZ_B];
-  E* s_A = reinterpret_cast<E*>(smem);
-  E* s_B = reinterpret_cast<E*>(smem + SZ_A);
+  constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
+  constexpr int ROWS = V > K ? V : K;
+  constexpr int LDM = LD > LDV ? (LD > LDC ? LD : LDC) : (LDV > LDC ? LDV : LDC);
+  __shared__ __attribute__((aligned(16))) float s_B[ROWS * LDM];
 
   const int NT = a.NT, H = a.H, T = a.T, L = a.L;
   const int n = blockIdx.x % NT;
@@ -31,8 +32,10 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   const int h = bh % H, b = bh / H;
   const int t0 = n * C;
   const int nvalid = min(C, T - t0);
-  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const int lane = lane_id(), wv = wave_id();
   const size_t cix = ((size_t)bh * NT + n);
+  const int ri = wv * 16 + (lane & 15);      // A-operand row of this lane
+  const int rc = min(ri, nvalid - 1);        // a valid row to read in its place
 
   const E* mixp = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L;
   const E* dop = static_cast<const E*>(ab.dout) + ((size_t)b * T * H + h) * V;
@@ -44,10 +47,13 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   };
 
   f4 acc[CTV];
-  auto run = [&](int kd) {
+  auto run = [&](const auto* arow, int ldb, int kd) {
+    for (int k0 = 0; k0 < kd; k0 += KS) {
+      const auto fa = Mma<E>::ld(arow + k0);
 #pragma unroll
-    for (int c = 0; c < CTV; ++c)
-      acc[c] = mma_tile<E>(acc[c], s_A + wv * 16 * LD, LD, s_B + c * 16 * LD, LD, kd);
+      for (int c = 0; c < CTV; ++c)
+        acc[c] = Mma<E>::mma(acc[c], fa, Mma<E>::ld(s_B + (c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + k0));
+    }
   };
   // dmix[t, l] = sc * <do[t], acc[t]>; one lane group per row, no races
   auto dmix = [&](int l, float sc) {
@@ -69,56 +75,48 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   // ---- level 0 read
 #pragma unroll
   for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-  {
-    const E* Qg = static_cast<const E*>(a.Qg) + cix * C * K;
-    const E* hT = static_cast<const E*>(a.hT) + cix * V * K;
-    for (int e = tid; e < C * K; e += 256) s_A[(e / K) * LD + e % K] = Qg[e];
-    for (int e = tid; e < V * K; e += 256) s_B[(e / K) * LD + e % K] = hT[e];
-  }
+  stage_f32(s_B, LD, a.hT + cix * V * K, K, V, K);
   __syncthreads();
-  run(K);
+  run(a.Qg + cix * C * K + (size_t)ri * K + kofs<E>(lane), LD, K);
   __syncthreads();
-  {
-    const E* Aq = static_cast<const E*>(a.Aqk) + cix * C * C;
-    const E* vT = static_cast<const E*>(a.vnT) + cix * V * C;
-    for (int e = tid; e < C * C; e += 256) s_A[(e / C) * LD + e % C] = Aq[e];
-    for (int e = tid; e < V * C; e += 256) s_B[(e / C) * LD + e % C] = vT[e];
-  }
+  stage_f32(s_B, LDC, a.vnT + cix * V * C, C, V, C);
   __syncthreads();
-  run(C);
+  run(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), LDC, C);
   dmix(0, 1.f);
   __syncthreads();
 
   // ---- upper levels
-  const E* qb = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K;
+  const E* qrow = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K +
+                  (size_t)(t0 + rc) * H * L * K + kofs<E>(lane);
+  const E* drow = dop + (size_t)(t0 + rc) * H * V + kofs<E>(lane);
   E* dqb = static_cast<E*>(ab.dq) + ((size_t)b * T * H + h) * L * K;
   for (int l = 1; l < L; ++l) {
     const int grp = n / a.f[l];
     const float* S = a.states[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * K * V;
-    for (int e = tid; e < C * K; e += 256) {
-      const int i = e / K, k = e % K;
-      s_A[i * LD + k] = i < nvalid ? qb[(size_t)(t0 + i) * H * L * K + (size_t)l * K + k] : from_f<E>(0.f);
-    }
-    for (int e = tid; e < K * V; e += 256) {
-      const int k = e / V, v = e % V;
-      s_B[v * LD + k] = from_f<E>(S[e]);
-    }
+    stage_state_T<K, V>(s_B, LD, S);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-    run(K);
+    run(qrow + (size_t)l * K, LD, K);   // rows past the end repeat the last row; dmix drops them
     dmix(l, a.scale);
     __syncthreads();
-    // dq_l = scale (mix_l do) S^T: A = mix_l do [C][V], Bt = S [K][V]
-    for (int e = tid; e < K * V; e += 256) s_B[(e / V) * LDV + e % V] = from_f<E>(S[e]);
-    for (int e = tid; e < C * V; e += 256) {
-      const int i = e / V, v = e % V;
-      s_A[i * LDV + v] = from_f<E>(dov(i, v) * mixw(i, l));
+    // dq_l = scale (mix_l do) S^T: A = mix_l do [C][V] (this wave's rows), Bt = S [K][V]
+    stage_f32(s_B, LDV, S, V, K, V);
+    const float m = ri < nvalid ? mixw(ri, l) : 0.f;
+    typename Mma<E>::SFrag fa[V / KS];
+#pragma unroll
+    for (int s = 0; s < V / KS; ++s) {
+      float x[KPL];
+      ld_vals<E>(drow + s * KS, x);
+      fa[s] = Mma<E>::makes([&](int e) { return x[e] * m; });
     }
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < CTK; ++c) {
-      f4 d = mma_tile<E>(f4_zero(), s_A + wv * 16 * LDV, LDV, s_B + c * 16 * LDV, LDV, V);
+      f4 d = f4_zero();
+#pragma unroll
+      for (int s = 0; s < V / KS; ++s)
+        d = Mma<E>::mma(d, fa[s], Mma<E>::ld(s_B + (c * 16 + (lane & 15)) * LDV + kofs<E>(lane) + s * KS));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = wv * 16 + acc_row(r);
@@ -134,10 +132,11 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a) {
   constexpr int C = CH;
-  constexpr int LD = C + 8;
+  constexpr int LDQ = C + 8;     // exact q^T rows
+  constexpr int LDD = C + 4;     // fp32 (mix do)^T rows
   constexpr int TPW = (K / 16) * (V / 16) / 4;
-  __shared__ __attribute__((aligned(16))) E s_qT[K * LD];
-  __shared__ __attribute__((aligned(16))) E s_dT[V * LD];
+  __shared__ __attribute__((aligned(16))) E s_qT[K * LDQ];
+  __shared__ __attribute__((aligned(16))) float s_dT[V * LDD];
 
   const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
   const int j = blockIdx.x % NG;
@@ -157,19 +156,19 @@ __global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a)
     const int t0 = n * C;
     for (int e = tid; e < C * K; e += 256) {
       const int c = e / K, k = e % K, t = t0 + c;
-      s_qT[k * LD + c] = t < T ? qb[(size_t)t * H * L * K + k] : from_f<E>(0.f);
+      s_qT[k * LDQ + c] = t < T ? qb[(size_t)t * H * L * K + k] : from_f<E>(0.f);
     }
     for (int e = tid; e < C * V; e += 256) {
       const int c = e / V, v = e % V, t = t0 + c;
       float x = 0.f;
       if (t < T) x = to_f(db[(size_t)t * H * V + v]) * to_f(mb[(size_t)t * H * L]);
-      s_dT[v * LD + c] = from_f<E>(x);
+      s_dT[v * LDD + c] = x;
     }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / (V / 16), ct = g % (V / 16);
-      acc[i] = mma_tile<E>(acc[i], s_qT + rt * 16 * LD, LD, s_dT + ct * 16 * LD, LD, C);
+      acc[i] = mma_tile<E>(acc[i], s_qT + rt * 16 * LDQ, LDQ, s_dT + ct * 16 * LDD, LDD, C);
     }
     __syncthreads();
   }

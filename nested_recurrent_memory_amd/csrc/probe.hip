@@ -13,7 +13,8 @@
 // (ops/chunk.py:39-93). Outputs are written in the form the scan consumes:
 // A = keys*b*e^g, KT = keys^T, U = Vals*w, gam = e^g.
 // One workgroup per (batch, head, firing); the five N x K x V products run on
-// MFMA with the gates in fp32.
+// MFMA (exact bf16 parameters against the fp32 state / Vals split in two) with
+// the gates in fp32.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -21,22 +22,14 @@ namespace ngdn {
 template <typename E, int K, int N, bool MERGE>
 __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   constexpr int V = K;
-  constexpr int LD = K + 8;
-  constexpr bool SEP = !std::is_same<E, float>::value;   // separate fp32 copy of Vals
-  constexpr int LDF = SEP ? V + 1 : LD;
-  constexpr int NKS = K / Mma<E>::KS;
+  constexpr int LD = K + 4;                                // fp32 rows
   constexpr int NTK = (N / 16) * (K / 16) / 4;             // [N,K] tiles per wave
-  typedef typename Mma<E>::Frag Frag;
-
-  constexpr size_t SZ_S = MERGE ? 0 : sizeof(E) * V * LD;
-  constexpr size_t SZ_VE = sizeof(E) * N * LD;
-  constexpr size_t SZ_VF = SEP ? sizeof(float) * N * LDF : 0;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_S + SZ_VE + SZ_VF + sizeof(float) * (N + K) + 16];
-  E* s_S = reinterpret_cast<E*>(smem);
-  E* s_VE = reinterpret_cast<E*>(smem + SZ_S);
-  float* s_Vf = SEP ? reinterpret_cast<float*>(smem + SZ_S + SZ_VE) : reinterpret_cast<float*>(s_VE);
-  float* s_nrm = reinterpret_cast<float*>(smem + SZ_S + SZ_VE + SZ_VF);
-  float* s_gs = s_nrm + N;
+  // S^T (learned) and then Vals share one buffer
+  constexpr int ROWS = (MERGE ? N : (V > N ? V : N));
+  __shared__ __attribute__((aligned(16))) float s_buf[ROWS * LD];
+  __shared__ float s_nrm[N], s_gs[K];
+  float* s_S = s_buf;      // [V][LD]: S^T, k contiguous
+  float* s_V = s_buf;      // [N][LD]: Vals, v contiguous
 
   const int NF = a.NF, H = a.H;
   const int i = blockIdx.x % NF;
@@ -47,72 +40,59 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   // ---- the gathered lower state
   const int src = ((i + 1) * a.f_here) / a.f_below;
   const bool fin = src >= a.NGb;
-  const float* Sf = nullptr;    // [K][V] fp32 source
-  const E* Sh = nullptr;        // [V][K] working-dtype source
+  const float* Sf = nullptr;    // [K][V] source
+  const float* Sh = nullptr;    // [V][K] source (level-0 chunk states)
   if (fin) Sf = a.below_fin + b * a.bf_sb + h * a.bf_sh;
-  else if (a.below_mode == 1)
-    Sf = static_cast<const float*>(a.below) + (((size_t)b * a.NGb + src) * H + h) * K * V;
-  else
-    Sh = static_cast<const E*>(a.below) + (((size_t)b * H + h) * a.NGb + src) * V * K;
+  else if (a.below_mode == 1) Sf = a.below + (((size_t)b * a.NGb + src) * H + h) * K * V;
+  else Sh = a.below + (((size_t)b * H + h) * a.NGb + src) * V * K;
 
-  if (!MERGE) {
-    // S^T into LDS, k contiguous
-    if (Sh) {
-      for (int e = tid; e < V * K; e += 256) s_S[(e / K) * LD + e % K] = Sh[e];
-    } else {
-      for (int e = tid; e < V * K; e += 256) {
-        const int k = e / V, v = e % V;
-        s_S[v * LD + k] = from_f<E>(Sf[e]);
-      }
-    }
-  } else {
-    // Vals = S, row k
-    if (Sh) {
-      for (int e = tid; e < V * K; e += 256) {
-        const int v = e / K, k = e % K;
-        const float x = to_f(Sh[e]);
-        s_VE[k * LD + v] = from_f<E>(x);
-        if (SEP) s_Vf[k * LDF + v] = x;
+  // learned: S^T rows (k contiguous); merge: Vals = S rows (v contiguous)
+  {
+    const float* same = MERGE ? Sf : Sh;     // already in the wanted orientation
+    const float* swap = MERGE ? Sh : Sf;
+    if (same) {
+      for (int e = tid; e < V * K / 4; e += 256) {
+        const int r = e / (K / 4), c = (e % (K / 4)) * 4;
+        *reinterpret_cast<f4*>(s_buf + r * LD + c) = *reinterpret_cast<const f4*>(same + r * K + c);
       }
     } else {
-      for (int e = tid; e < V * K; e += 256) {
-        const int k = e / V, v = e % V;
-        const float x = Sf[e];
-        s_VE[k * LD + v] = from_f<E>(x);
-        if (SEP) s_Vf[k * LDF + v] = x;
-      }
+      for (int e = tid; e < V * K; e += 256) s_buf[(e % K) * LD + e / K] = swap[e];
     }
   }
-  for (int e = tid; e < N + K; e += 256) s_nrm[e] = 0.f;
+  for (int e = tid; e < N; e += 256) s_nrm[e] = 0.f;
+  for (int e = tid; e < K; e += 256) s_gs[e] = 0.f;
   __syncthreads();
 
   const size_t fo = ((size_t)bh * NF + i);                 // scan-ready firing index
   const size_t ro = (((size_t)b * NF + i) * H + h);        // reference-format index
 
-  // ---- Vals = Bank[:N] S
+  // ---- Vals = Bank[:N] S (tiles in registers, then over S^T)
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
-    for (int g = wv; g < (N / 16) * (V / 16); g += 4) {
-      const int rt = g / (V / 16), ct = g % (V / 16);
-      f4 acc = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_S + ct * 16 * LD, LD, K);
+    f4 vt[NTK];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        s_VE[n * LD + v] = from_f<E>(acc[r]);
-        if (SEP) s_Vf[n * LDF + v] = acc[r];
-      }
+    for (int t = 0; t < NTK; ++t) {
+      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+      vt[t] = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_S + ct * 16 * LD, LD, K);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NTK; ++t) {
+      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_V[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vt[t][r];
     }
     __syncthreads();
   }
   if (a.vals) {
     for (int e = tid; e < N * V; e += 256)
-      a.vals[ro * N * V + e] = s_Vf[(e / V) * LDF + e % V];
+      a.vals[ro * N * V + e] = s_V[(e / V) * LD + e % V];
   }
 
-  // ---- projections of Vals: A operand s_VE (reduce over V), B from global
+  // ---- projections of Vals: A operand s_V (reduce over V), B from global
   auto proj_tile = [&](const E* Pt, int rt, int ct) -> f4 {
     // Pt: [cols][V] with V contiguous
-    return mma_tile<E>(f4_zero(), s_VE + rt * 16 * LD, LD, Pt + (size_t)ct * 16 * V, V, V);
+    return mma_tile<E>(f4_zero(), s_V + rt * 16 * LD, LD, Pt + (size_t)ct * 16 * V, V, V);
   };
   const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V;
   const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V;
@@ -155,7 +135,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   }
   // write gate, and U = Vals * w
   {
-    E* Uo = static_cast<E*>(a.U) + fo * N * V;
+    float* Uo = a.U + fo * N * V;
     for (int g = wv; g < (N / 16) * (V / 16); g += 4) {
       const int rt = g / (V / 16), ct = g % (V / 16);
       f4 x = proj_tile(wpH, rt, ct);
@@ -163,7 +143,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
         const float w = sigmoidf_(x[r]);
-        Uo[n * V + v] = from_f<E>(s_Vf[n * LDF + v] * w);
+        Uo[n * V + v] = s_V[n * LD + v] * w;
         if (a.wo) a.wo[ro * N * V + n * V + v] = w;
       }
     }
@@ -176,27 +156,29 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
     a.gam[fo * K + tid] = expf(g);
     if (a.go) a.go[ro * K + tid] = g;
   }
-  E* Ao = static_cast<E*>(a.A) + fo * N * K;
-  E* KTo = static_cast<E*>(a.KT) + fo * K * N;
+  float* Ao = a.A + fo * N * K;
+  float* KTo = a.KT + fo * K * N;
 #pragma unroll
   for (int t = 0; t < NTK; ++t) {
     const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    const int k = ct * 16 + acc_col();
+    const int k = ct * 16 + acc_col(), n0 = rt * 16 + acc_row(0);
     const float gam = expf(-s_gs[k] / (float)N);
+    f4 kv4, av4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int n = rt * 16 + acc_row(r);
+      const int n = n0 + r;
       float key;
       if (MERGE) key = (n == k) ? 1.f : 0.f;
       else key = ut[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
-      const E av = from_f<E>(key * bt[t][r] * gam), kv = from_f<E>(key);
-      Ao[n * K + k] = av;
-      KTo[k * N + n] = kv;
-      if (a.AT) static_cast<E*>(a.AT)[fo * K * N + k * N + n] = av;
-      if (a.keysN) static_cast<E*>(a.keysN)[fo * N * K + n * K + k] = kv;
+      kv4[r] = key;
+      av4[r] = key * bt[t][r] * gam;
+      Ao[n * K + k] = av4[r];
+      if (a.keysN) a.keysN[fo * N * K + n * K + k] = key;
       if (a.keys) a.keys[ro * N * K + n * K + k] = key;
       if (a.bo) a.bo[ro * N * K + n * K + k] = bt[t][r];
     }
+    *reinterpret_cast<f4*>(KTo + k * N + n0) = kv4;
+    if (a.AT) *reinterpret_cast<f4*>(a.AT + fo * K * N + k * N + n0) = av4;
   }
 }
 

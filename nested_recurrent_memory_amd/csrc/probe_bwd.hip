@@ -15,7 +15,7 @@
 //   dS_below = Bank^T dVals (learned) or dVals (merge),
 //   dBank   += dVals S_below^T
 // Parameter gradients other than the bank are reduced afterwards over all
-// firings of a head (atb_accumulate) from the workspace written here.
+// firings of a head (atb_accumulate) from the fp32 workspace written here.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -24,14 +24,16 @@ template <typename E, int K, int N, bool MERGE>
 __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   const ProbeArgs& a = ab.f;
   constexpr int V = K;
-  constexpr int LD = K + 8;
+  constexpr int LD = K + 4;                        // fp32 rows
+  constexpr int LDN = N + 4;
   constexpr int NTK = (N / 16) * (K / 16) / 4;     // [N,K] (= [N,V]) tiles per wave
-  constexpr int NKS = K / Mma<E>::KS;
-  constexpr int NR1 = V * (LD > N + 8 ? LD : N + 8);
+  constexpr int KS = Mma<E>::KS;
+  constexpr int NKS = K / KS;
+  constexpr int NR1 = V * (LD > LDN ? LD : LDN);
   constexpr int RX = N > K ? N : K;
-  typedef typename Mma<E>::Frag Frag;
-  __shared__ __attribute__((aligned(16))) E s_R1[NR1];     // S^T, then s^T, then dVals^T
-  __shared__ __attribute__((aligned(16))) E s_X[RX * LD];  // kb, then vn, then S_below
+  typedef typename Mma<E>::SFrag SF;
+  __shared__ __attribute__((aligned(16))) float s_R1[NR1];     // S^T, then s^T, then dVals^T
+  __shared__ __attribute__((aligned(16))) float s_X[RX * LD];  // kb, then vn, then S_below
   __shared__ float s_nrm[N], s_rd[N], s_gs[K], s_dg[K];
 
   const int NF = a.NF, H = a.H;
@@ -44,24 +46,22 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // ---- the gathered lower state (as in probe_fwd)
   const int src = ((i + 1) * a.f_here) / a.f_below;
   const bool fin = src >= a.NGb;
-  const float* Sf = nullptr;
-  const E* Sh = nullptr;
+  const float* Sf = nullptr;    // [K][V]
+  const float* Sh = nullptr;    // [V][K] (level-0 chunk states)
   if (fin) Sf = a.below_fin + b * a.bf_sb + h * a.bf_sh;
-  else if (a.below_mode == 1)
-    Sf = static_cast<const float*>(a.below) + (((size_t)b * a.NGb + src) * H + h) * K * V;
-  else
-    Sh = static_cast<const E*>(a.below) + (((size_t)b * H + h) * a.NGb + src) * V * K;
-  auto sbelow = [&](int k, int v) -> float { return Sh ? to_f(Sh[(size_t)v * K + k]) : Sf[(size_t)k * V + v]; };
+  else if (a.below_mode == 1) Sf = a.below + (((size_t)b * a.NGb + src) * H + h) * K * V;
+  else Sh = a.below + (((size_t)b * H + h) * a.NGb + src) * V * K;
+  auto sbelow = [&](int k, int v) -> float { return Sh ? Sh[(size_t)v * K + k] : Sf[(size_t)k * V + v]; };
 
   const float* Sj = ab.Sg + (((size_t)b * ab.NG + i) * H + h) * K * V;   // state before firing i
   const float* dSp = ab.dSp + fo * K * V;
   const float* dvn = ab.dvn + fo * N * V;
-  E* wsV = static_cast<E*>(ab.wsV) + fo * N * V;
-  E* wsdu = static_cast<E*>(ab.wsdu) + fo * N * K;
-  E* wsdxb = static_cast<E*>(ab.wsdxb) + fo * N * K;
-  E* wsdxg = static_cast<E*>(ab.wsdxg) + fo * N * K;
-  E* wsdxw = static_cast<E*>(ab.wsdxw) + fo * N * V;
-  E* wsdV = static_cast<E*>(ab.wsdV) + fo * N * V;
+  float* wsV = ab.wsV + fo * N * V;
+  float* wsdu = ab.wsdu + fo * N * K;
+  float* wsdxb = ab.wsdxb + fo * N * K;
+  float* wsdxg = ab.wsdxg + fo * N * K;
+  float* wsdxw = ab.wsdxw + fo * N * V;
+  float* wsdV = ab.wsdV + fo * N * V;
 
   for (int e = tid; e < N; e += 256) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
   for (int e = tid; e < K; e += 256) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
@@ -69,9 +69,9 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // ---- A. Vals
   if (!MERGE) {
     if (Sh) {
-      for (int e = tid; e < V * K; e += 256) s_R1[(e / K) * LD + e % K] = Sh[e];
+      stage_f32(s_R1, LD, Sh, K, V, K);
     } else {
-      for (int e = tid; e < V * K; e += 256) s_R1[(e % V) * LD + e / V] = from_f<E>(Sf[e]);
+      stage_state_T<K, V>(s_R1, LD, Sf);
     }
     __syncthreads();
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
@@ -81,10 +81,10 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
       f4 acc = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_R1 + ct * 16 * LD, LD, K);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        wsV[(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = from_f<E>(acc[r]);
+        wsV[(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = acc[r];
     }
   } else {
-    for (int e = tid; e < K * V; e += 256) wsV[e] = from_f<E>(sbelow(e / V, e % V));
+    for (int e = tid; e < K * V; e += 256) wsV[e] = sbelow(e / V, e % V);
   }
   __syncthreads();
 
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // ---- C. s^T into LDS, kb into LDS
   for (int e = tid; e < K * V; e += 256) {
     const int k = e / V, v = e % V;
-    s_R1[v * LD + k] = from_f<E>(gam(k) * Sj[e]);
+    s_R1[v * LD + k] = gam(k) * Sj[e];
   }
 #pragma unroll
   for (int t = 0; t < NTK; ++t) {
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       s_X[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] =
-          from_f<E>(keyval(u, rt, ct, r) * sigmoidf_(xb[r] - 4.f));
+          keyval(u, rt, ct, r) * sigmoidf_(xb[r] - 4.f);
   }
   __syncthreads();
   // vn = vals * w - kb s;  dw-side terms
@@ -154,11 +154,11 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     for (int r = 0; r < 4; ++r) {
       const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
       const float w = sigmoidf_(xw[r]);
-      const float val = to_f(wsV[n * V + v]);
+      const float val = wsV[n * V + v];
       const float dv = dvn[n * V + v];
       vnt[t][r] = val * w - ks[r];
       dvd[t][r] = dv * w;
-      wsdxw[n * V + v] = from_f<E>(dv * val * w * (1.f - w));
+      wsdxw[n * V + v] = dv * val * w * (1.f - w);
     }
   }
   __syncthreads();
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      s_X[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = from_f<E>(vnt[t][r]);
+      s_X[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vnt[t][r];
   }
   __syncthreads();
 
@@ -184,11 +184,11 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     const float* qrow = dSp + (size_t)kc * V;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      const int v0 = s * Mma<E>::KS + kofs<E>(lane);
-      const Frag fa = Mma<E>::make([&](int e) { return drow[v0 + e]; });
-      const Frag fs = Mma<E>::make([&](int e) { return gk * srow[v0 + e]; });
-      const Frag fv = Mma<E>::load(s_X + (rt * 16 + (lane & 15)) * LD + v0);
-      const Frag fq = Mma<E>::make([&](int e) { return qrow[v0 + e]; });
+      const int v0 = s * KS + kofs<E>(lane);
+      const SF fa = Mma<E>::ld(drow + v0);
+      const SF fs = Mma<E>::makes([&](int e) { return gk * srow[v0 + e]; });
+      const SF fv = Mma<E>::ld(s_X + (rt * 16 + (lane & 15)) * LD + v0);
+      const SF fq = Mma<E>::ld(qrow + v0);
       P = Mma<E>::mma(P, fa, fs);
       Q = Mma<E>::mma(Q, fv, fq);
     }
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
       const float dbg = -P[r] * key;
       cs += key * bb * P[r];
       dkt[t][r] = dkey;
-      wsdxb[n * K + k] = from_f<E>(dbg * bb * (1.f - bb));
+      wsdxb[n * K + k] = dbg * bb * (1.f - bb);
       if (!MERGE) {
         float rd = key * dkey;
         rd += __shfl_xor(rd, 1, WAVE);
@@ -242,9 +242,9 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
         const float key = u[r] / fmaxf(nr, 1e-12f);
         // F.normalize: below the clamp the denominator is the constant eps
         const float du = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) / nr : dkt[t][r] / 1e-12f;
-        wsdu[n * K + k] = from_f<E>(du);
+        wsdu[n * K + k] = du;
       }
-      wsdxg[n * K + k] = from_f<E>(-(s_dg[k] / (float)N) * sigmoidf_(xg[r] - 4.f));
+      wsdxg[n * K + k] = -(s_dg[k] / (float)N) * sigmoidf_(xg[r] - 4.f);
     }
   }
   __syncthreads();
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     const E* bp = static_cast<const E*>(ab.bp) + (size_t)h * V * K;
     const E* wp = static_cast<const E*>(ab.wp) + (size_t)h * V * V;
     const E* gp = static_cast<const E*>(ab.gp) + (size_t)h * V * K;
-    E* s_dVT = s_R1;   // [V][N + 8]
+    float* s_dVT = s_R1;   // [V][LDN]
 #pragma unroll
     for (int t = 0; t < NTK; ++t) {
       const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
@@ -268,13 +268,13 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        wsdV[n * V + v] = from_f<E>(acc[r]);
-        s_dVT[v * (N + 8) + n] = from_f<E>(acc[r]);
+        wsdV[n * V + v] = acc[r];
+        s_dVT[v * LDN + n] = acc[r];
       }
     }
     if (!MERGE) {
       // S_below rows k (v contiguous) for dBank
-      for (int e = tid; e < K * V; e += 256) s_X[(e / V) * LD + e % V] = from_f<E>(sbelow(e / V, e % V));
+      for (int e = tid; e < K * V; e += 256) s_X[(e / V) * LD + e % V] = sbelow(e / V, e % V);
     }
   }
   __syncthreads();
@@ -298,21 +298,22 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     }
   } else {
     const E* bankT = static_cast<const E*>(ab.bankT) + (size_t)h * K * a.Nmax;
-    const E* s_dVT = s_R1;
+    const float* s_dVT = s_R1;
     constexpr int NTKV = (K / 16) * (V / 16) / 4;
     for (int t = 0; t < NTKV; ++t) {
       const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
       f4 acc = f4_zero();
       const E* arow = bankT + (size_t)(rt * 16 + (lane & 15)) * a.Nmax + kofs<E>(lane);
-      const E* brow = s_dVT + (ct * 16 + (lane & 15)) * (N + 8) + kofs<E>(lane);
-      constexpr int NSN = (N + Mma<E>::KS - 1) / Mma<E>::KS;
+      const float* brow = s_dVT + (ct * 16 + (lane & 15)) * LDN + kofs<E>(lane);
+      constexpr int NSN = (N + KS - 1) / KS;
 #pragma unroll
       for (int s = 0; s < NSN; ++s) {
-        const bool live = s * Mma<E>::KS + kofs<E>(lane) < N;
-        Frag fa = Mma<E>::make([](int) { return 0.f; }), fb = fa;
+        const bool live = s * KS + kofs<E>(lane) < N;
+        typename Mma<E>::Frag fa = Mma<E>::zero();
+        SF fb = Mma<E>::szero();
         if (live) {
-          fa = Mma<E>::load(arow + s * Mma<E>::KS);
-          fb = Mma<E>::load(brow + s * Mma<E>::KS);
+          fa = Mma<E>::ld(arow + s * KS);
+          fb = Mma<E>::ld(brow + s * KS);
         }
         acc = Mma<E>::mma(acc, fa, fb);
       }
@@ -336,10 +337,10 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
 
 template <typename E, int X, int Y>
 __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
-  constexpr int LDM = 32 + 8;
+  constexpr int LDM = 32 + 4;
   constexpr int TPW = (X / 16) * (Y / 16) / 4;
-  __shared__ __attribute__((aligned(16))) E s_AT[X * LDM];
-  __shared__ __attribute__((aligned(16))) E s_BT[Y * LDM];
+  __shared__ __attribute__((aligned(16))) float s_AT[X * LDM];
+  __shared__ __attribute__((aligned(16))) float s_BT[Y * LDM];
   const int H = a.H, NF = a.NF, N = a.N;
   const int part = blockIdx.x % a.split;
   const int h = blockIdx.x / a.split;
@@ -353,17 +354,17 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
   for (int it = it0; it < it1; ++it) {
     const int b = it / NF, i = it % NF;
     const size_t base = (((size_t)b * H + h) * NF + i) * N;
-    const E* Ap = static_cast<const E*>(a.A) + base * X;
-    const E* Bp = static_cast<const E*>(a.Bm) + base * Y;
+    const float* Ap = a.A + base * X;
+    const float* Bp = a.Bm + base * Y;
     for (int n0 = 0; n0 < N; n0 += 32) {
       // 32 rows of the reduction, transposed into LDS (zero past N)
       for (int e = tid; e < 32 * X; e += 256) {
         const int n = e / X, x = e % X;
-        s_AT[x * LDM + n] = n0 + n < N ? Ap[(size_t)(n0 + n) * X + x] : from_f<E>(0.f);
+        s_AT[x * LDM + n] = n0 + n < N ? Ap[(size_t)(n0 + n) * X + x] : 0.f;
       }
       for (int e = tid; e < 32 * Y; e += 256) {
         const int n = e / Y, y = e % Y;
-        s_BT[y * LDM + n] = n0 + n < N ? Bp[(size_t)(n0 + n) * Y + y] : from_f<E>(0.f);
+        s_BT[y * LDM + n] = n0 + n < N ? Bp[(size_t)(n0 + n) * Y + y] : 0.f;
       }
       __syncthreads();
 #pragma unroll

@@ -11,10 +11,11 @@
 // S' = e^g S - keys^T ((keys*b)(e^g S)) + keys^T (values*w).
 //
 // Columns of V never interact, so a workgroup owns BV = 32 of them and the
-// grid is B*H*(V/32). Per step: the state slice is written (transposed, in the
-// working dtype) to LDS as the B operand of A S; Vn goes through LDS as the B
-// operand of BT Vn. A and BT fragments are read straight from global memory,
-// each wave reading the rows only it needs.
+// grid is B*H*(V/32). Per step: the state slice is written (transposed, fp32)
+// to LDS as the B operand of A S; Vn goes through LDS as the B operand of
+// BT Vn. A and BT fragments are read straight from global memory, each wave
+// reading the rows only it needs. Every operand is derived (fp32); for bf16
+// inputs each product is three bf16 MFMAs on split operands.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -26,13 +27,14 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   constexpr int RTS = K / 16;                 // state row tiles
   constexpr int TPW = RTS * CT / 4;           // state tiles per wave
   constexpr int RTV = M / 16;                 // Vn row tiles
-  constexpr int LDS_ST = K + 8;
-  constexpr int LDS_VN = M + 8;
-  constexpr int NSM = (M + Mma<E>::KS - 1) / Mma<E>::KS;   // k-steps over M
-  constexpr bool PADM = (M % Mma<E>::KS) != 0;
-  typedef typename Mma<E>::Frag Frag;
-  __shared__ __attribute__((aligned(16))) E s_ST[BV * LDS_ST];
-  __shared__ __attribute__((aligned(16))) E s_VnT[BV * LDS_VN];
+  constexpr int LDS_ST = K + 4;
+  constexpr int LDS_VN = M + 4;
+  constexpr int KS = Mma<E>::KS;
+  constexpr int NSM = (M + KS - 1) / KS;      // k-steps over M
+  constexpr bool PADM = (M % KS) != 0;
+  typedef typename Mma<E>::SFrag SF;
+  __shared__ __attribute__((aligned(16))) float s_ST[BV * LDS_ST];
+  __shared__ __attribute__((aligned(16))) float s_VnT[BV * LDS_VN];
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
@@ -54,9 +56,9 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     }
   }
 
-  const E* Ab = static_cast<const E*>(a.A) + (size_t)bh * S * M * K;
-  const E* Bb = static_cast<const E*>(a.BT) + (size_t)bh * S * K * M;
-  const E* Ub = static_cast<const E*>(a.U) + (size_t)bh * S * M * V;
+  const float* Ab = a.A + (size_t)bh * S * M * K;
+  const float* Bb = a.BT + (size_t)bh * S * K * M;
+  const float* Ub = a.U + (size_t)bh * S * M * V;
   const float* Gb = a.gam + (size_t)bh * S * K;
 
   auto store_state = [&](int j) {
@@ -65,11 +67,9 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col(), v = v0 + vl;
       if (a.state_mode == 0) {
-        E* hp = static_cast<E*>(a.states) + (((size_t)bh * S + j) * V + v) * K + k0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hp[r] = from_f<E>(st[i][r]);
+        *reinterpret_cast<f4*>(a.states + (((size_t)bh * S + j) * V + v) * K + k0) = st[i];
       } else {
-        float* sp = static_cast<float*>(a.states) + (((size_t)b * a.NG + j) * H + h) * K * V;
+        float* sp = a.states + (((size_t)b * a.NG + j) * H + h) * K * V;
 #pragma unroll
         for (int r = 0; r < 4; ++r) sp[(size_t)(k0 + r) * V + v] = st[i][r];
       }
@@ -83,60 +83,53 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_ST[vl * LDS_ST + k0 + r] = from_f<E>(st[i][r]);
+      *reinterpret_cast<f4*>(s_ST + vl * LDS_ST + k0) = st[i];
     }
     __syncthreads();
 
     // ---- Vn = U - A S
-    const E* Aj = Ab + (size_t)j * M * K;
-    const E* Uj = Ub + (size_t)j * M * V;
+    const float* Aj = Ab + (size_t)j * M * K;
+    const float* Uj = Ub + (size_t)j * M * V;
     for (int rt = wv; rt < RTV; rt += 4) {
-      Frag af[K / Mma<E>::KS];
-      const E* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+      SF af[K / KS];
+      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < K / Mma<E>::KS; ++s) af[s] = Mma<E>::load(arow + s * Mma<E>::KS);
+      for (int s = 0; s < K / KS; ++s) af[s] = Mma<E>::ld(arow + s * KS);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         f4 acc = f4_zero();
-        const E* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+        const float* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < K / Mma<E>::KS; ++s)
-          acc = Mma<E>::mma(acc, af[s], Mma<E>::load(brow + s * Mma<E>::KS));
+        for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, af[s], Mma<E>::ld(brow + s * KS));
         const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-        float vn[4];
+        f4 vn;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          vn[r] = to_f(Uj[(size_t)(m0 + r) * V + v0 + vl]) - acc[r];
-          s_VnT[vl * LDS_VN + m0 + r] = from_f<E>(vn[r]);
-        }
-        if (a.vnT) {
-          E* vp = static_cast<E*>(a.vnT) + (((size_t)bh * S + j) * V + v0 + vl) * M + m0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) vp[r] = from_f<E>(vn[r]);
-        }
+        for (int r = 0; r < 4; ++r) vn[r] = Uj[(size_t)(m0 + r) * V + v0 + vl] - acc[r];
+        *reinterpret_cast<f4*>(s_VnT + vl * LDS_VN + m0) = vn;
+        if (a.vnT)
+          *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
       }
     }
     __syncthreads();
 
     // ---- S <- diag(gam) S + BT Vn
-    const E* Bj = Bb + (size_t)j * K * M;
+    const float* Bj = Bb + (size_t)j * K * M;
     const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
 #pragma unroll
       for (int r = 0; r < 4; ++r) st[i][r] *= Gj[rt * 16 + acc_row(r)];
-      const E* arow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
-      const E* brow = s_VnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+      const float* arow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      const float* brow = s_VnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
         // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
-        const bool live = !PADM || (s * Mma<E>::KS + kofs<E>(lane) < M);
-        Frag fa = Mma<E>::make([](int) { return 0.f; }), fb = fa;
+        const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
+        SF fa = Mma<E>::szero(), fb = fa;
         if (live) {
-          fa = Mma<E>::load(arow + s * Mma<E>::KS);
-          fb = Mma<E>::load(brow + s * Mma<E>::KS);
+          fa = Mma<E>::ld(arow + s * KS);
+          fb = Mma<E>::ld(brow + s * KS);
         }
         st[i] = Mma<E>::mma(st[i], fa, fb);
       }

@@ -16,7 +16,9 @@
 // Levels >= 1 (ops/update_bwd.py:93-158): after group j's firing, the read
 // gradient of the state entering group j joins: dS += d_states[j].
 //
-// Stores, per step: dS' (the gradient of the state after it) and dVn.
+// Stores, per step (fp32): dS' (the gradient of the state after it) and dVn.
+// Every operand but do is derived; for bf16 inputs each product is three bf16
+// MFMAs on split operands.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -28,14 +30,15 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int RTS = K / 16;
   constexpr int TPW = RTS * CT / 4;
   constexpr int RTV = M / 16;
-  constexpr int LDS_ST = K + 8;
-  constexpr int LDS_VN = M + 8;
-  constexpr int NSM = (M + Mma<E>::KS - 1) / Mma<E>::KS;
-  constexpr bool PADM = (M % Mma<E>::KS) != 0;
-  typedef typename Mma<E>::Frag Frag;
-  __shared__ __attribute__((aligned(16))) E s_dST[BV * LDS_ST];
-  __shared__ __attribute__((aligned(16))) E s_dVnT[BV * LDS_VN];
-  __shared__ __attribute__((aligned(16))) E s_dOT[BV * LDS_VN];
+  constexpr int LDS_ST = K + 4;
+  constexpr int LDS_VN = M + 4;
+  constexpr int KS = Mma<E>::KS;
+  constexpr int NSM = (M + KS - 1) / KS;
+  constexpr bool PADM = (M % KS) != 0;
+  typedef typename Mma<E>::SFrag SF;
+  __shared__ __attribute__((aligned(16))) float s_dST[BV * LDS_ST];
+  __shared__ __attribute__((aligned(16))) float s_dVnT[BV * LDS_VN];
+  __shared__ __attribute__((aligned(16))) float s_dOT[BV * LDS_VN];
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
@@ -45,8 +48,6 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   const int v0 = vt * BV;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const bool l0 = a.QgT != nullptr;
-
-  auto zero = []() { return Mma<E>::make([](int) { return 0.f; }); };
 
   f4 ds[TPW];
 #pragma unroll
@@ -73,8 +74,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   if (a.d_states)
     for (int j = a.NG - 1; j >= S; --j) add_kv(dstates(j));
 
-  const E* Bb = static_cast<const E*>(a.Bop) + (size_t)bh * S * M * K;
-  const E* Ab = static_cast<const E*>(a.AT) + (size_t)bh * S * K * M;
+  const float* Bb = a.Bop + (size_t)bh * S * M * K;
+  const float* Ab = a.AT + (size_t)bh * S * K * M;
   const float* Gb = a.gam + (size_t)bh * S * K;
   const E* dob = l0 ? static_cast<const E*>(a.dout) + ((size_t)b * a.T * H + h) * V : nullptr;
   const E* mixb = l0 ? static_cast<const E*>(a.mix) + ((size_t)b * a.T * H + h) * a.L : nullptr;
@@ -88,13 +89,10 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+      float* o = a.dSp + ((size_t)bh * S + j) * K * V + (size_t)k0 * V + v0 + vl;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const size_t o = ((size_t)bh * S + j) * K * V + (size_t)(k0 + r) * V + v0 + vl;
-        if (a.dsp_mode == 0) static_cast<E*>(a.dSp)[o] = from_f<E>(ds[i][r]);
-        else static_cast<float*>(a.dSp)[o] = ds[i][r];
-        s_dST[vl * LDS_ST + k0 + r] = from_f<E>(ds[i][r]);
-      }
+      for (int r = 0; r < 4; ++r) o[(size_t)r * V] = ds[i][r];
+      *reinterpret_cast<f4*>(s_dST + vl * LDS_ST + k0) = ds[i];
     }
     if (l0) {
       // dO^T for this chunk's rows and this V slice
@@ -103,77 +101,70 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
         float x = 0.f;
         if (t < a.T)
           x = to_f(dob[(size_t)t * H * V + v0 + vl]) * to_f(mixb[(size_t)t * H * a.L]);
-        s_dOT[vl * LDS_VN + c] = from_f<E>(x);
+        s_dOT[vl * LDS_VN + c] = x;
       }
     }
     __syncthreads();
 
     // ---- dVn = Bop dS' (+ Aqk^T dO)
-    const E* Bj = Bb + (size_t)j * M * K;
+    const float* Bj = Bb + (size_t)j * M * K;
     for (int rt = wv; rt < RTV; rt += 4) {
-      Frag bf[K / Mma<E>::KS];
-      const E* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+      SF bf[K / KS];
+      const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < K / Mma<E>::KS; ++s) bf[s] = Mma<E>::load(brow + s * Mma<E>::KS);
+      for (int s = 0; s < K / KS; ++s) bf[s] = Mma<E>::ld(brow + s * KS);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         f4 acc = f4_zero();
-        const E* srow = s_dST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+        const float* srow = s_dST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < K / Mma<E>::KS; ++s)
-          acc = Mma<E>::mma(acc, bf[s], Mma<E>::load(srow + s * Mma<E>::KS));
+        for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, bf[s], Mma<E>::ld(srow + s * KS));
         if (l0) {
-          const E* qrow = static_cast<const E*>(a.AqkT) + ((size_t)bh * S + j) * M * M +
-                          (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
-          const E* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+          const float* qrow = a.AqkT + ((size_t)bh * S + j) * M * M +
+                              (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+          const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSM; ++s)
-            acc = Mma<E>::mma(acc, Mma<E>::load(qrow + s * Mma<E>::KS), Mma<E>::load(orow + s * Mma<E>::KS));
+            acc = Mma<E>::mma(acc, Mma<E>::ld(qrow + s * KS), Mma<E>::ld(orow + s * KS));
         }
         const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+        float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const size_t o = ((size_t)bh * S + j) * M * V + (size_t)(m0 + r) * V + v0 + vl;
-          if (a.dvn_mode == 0) static_cast<E*>(a.dVn)[o] = from_f<E>(acc[r]);
-          else static_cast<float*>(a.dVn)[o] = acc[r];
-          s_dVnT[vl * LDS_VN + m0 + r] = from_f<E>(acc[r]);
-        }
-        if (a.dVnT) {
-          E* p = static_cast<E*>(a.dVnT) + (((size_t)bh * S + j) * V + v0 + vl) * M + m0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) p[r] = from_f<E>(acc[r]);
-        }
+        for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
+        *reinterpret_cast<f4*>(s_dVnT + vl * LDS_VN + m0) = acc;
+        if (a.dVnT)
+          *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;
       }
     }
     __syncthreads();
 
     // ---- dS = diag(gam) dS' - A^T dVn (+ Qg^T dO)
-    const E* Aj = Ab + (size_t)j * K * M;
+    const float* Aj = Ab + (size_t)j * K * M;
     const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       f4 acc = f4_zero();
-      const E* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
-      const E* vrow = s_dVnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      const float* vrow = s_dVnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
-        const bool live = !PADM || (s * Mma<E>::KS + kofs<E>(lane) < M);
-        Frag fa = zero(), fb = zero();
+        const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
+        SF fa = Mma<E>::szero(), fb = fa;
         if (live) {
-          fa = Mma<E>::load(arow + s * Mma<E>::KS);
-          fb = Mma<E>::load(vrow + s * Mma<E>::KS);
+          fa = Mma<E>::ld(arow + s * KS);
+          fb = Mma<E>::ld(vrow + s * KS);
         }
         acc = Mma<E>::mma(acc, fa, fb);
       }
       f4 qacc = f4_zero();
       if (l0) {
-        const E* qrow = static_cast<const E*>(a.QgT) + ((size_t)bh * S + j) * K * M +
-                        (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
-        const E* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+        const float* qrow = a.QgT + ((size_t)bh * S + j) * K * M +
+                            (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+        const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < NSM; ++s)
-          qacc = Mma<E>::mma(qacc, Mma<E>::load(qrow + s * Mma<E>::KS), Mma<E>::load(orow + s * Mma<E>::KS));
+          qacc = Mma<E>::mma(qacc, Mma<E>::ld(qrow + s * KS), Mma<E>::ld(orow + s * KS));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)

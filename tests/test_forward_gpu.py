@@ -44,16 +44,17 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     scale = K ** -0.5
     code = _lib.NGDN_BF16 if dtype == torch.bfloat16 else _lib.NGDN_F32
     g = {n: inp[n].to("cuda").contiguous() for n in ("q", "k", "v", "g", "b", "w")}
-    e = lambda *s, dt=dtype: torch.empty(*s, device="cuda", dtype=dt)  # noqa: E731
+    # the per-chunk terms are fp32 working tensors whatever the input dtype
+    e = lambda *s: torch.empty(*s, device="cuda", dtype=torch.float32)  # noqa: E731
     out = dict(W=e(B, H, NT, 64, K), U=e(B, H, NT, 64, V), KtT=e(B, H, NT, K, 64),
-               Qg=e(B, H, NT, 64, K), Aqk=e(B, H, NT, 64, 64), gam=e(B, H, NT, K, dt=torch.float32),
+               Qg=e(B, H, NT, 64, K), Aqk=e(B, H, NT, 64, 64), gam=e(B, H, NT, K),
                Kt=e(B, H, NT, 64, K), WT=e(B, H, NT, K, 64), QgT=e(B, H, NT, K, 64),
-               AqkT=e(B, H, NT, 64, 64))
+               AqkT=e(B, H, NT, 64, 64), TT=e(B, H, NT, 64, 64))
     d = _lib.dims(B, T, H, L, K, V, code, scale)
     P = _lib.ptr
     _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(g[n]) for n in ("q", "k", "v", "g", "b", "w")),
               *(P(out[n]) for n in ("W", "U", "KtT", "Qg", "Aqk", "gam")),
-              *(P(out[n]) for n in ("Kt", "WT", "QgT", "AqkT")), _lib.stream_of(g["q"]))
+              *(P(out[n]) for n in ("Kt", "WT", "QgT", "AqkT", "TT")), _lib.stream_of(g["q"]))
     torch.cuda.synchronize()
 
     pad = NT * 64 - T
@@ -73,6 +74,7 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     torch.testing.assert_close(got["KtT"], t["Kt"].transpose(-1, -2), **tol)
     torch.testing.assert_close(got["W"], t["W"], **tol)
     torch.testing.assert_close(got["U"], t["U"], **tol)
+    torch.testing.assert_close(got["TT"], t["T"].transpose(-1, -2), **tol)
     # transposed copies are exact copies
     assert torch.equal(got["Kt"], got["KtT"].transpose(-1, -2))
     assert torch.equal(got["WT"], got["W"].transpose(-1, -2))
