@@ -39,6 +39,23 @@ struct ChunkIn {
   __device__ __forceinline__ float Q_(int i, int c) const { return ld(q, rowQ, i, c); }
   __device__ __forceinline__ float V_(int i, int c) const { return ld(v, rowV, i, c); }
   __device__ __forceinline__ float W_(int i, int c) const { return ld(w, rowV, i, c); }
+  // 16 bytes of row i from column c0 as floats (zero past the end)
+  static constexpr int VE = 16 / (int)sizeof(E);
+  __device__ __forceinline__ void vec16(const E* p, size_t row, int i, int c0, float* out) const {
+    if (i < nvalid) {
+      const E* src = p + (size_t)(t0 + i) * row + c0;
+      if constexpr (std::is_same<E, float>::value) {
+        const f4 x = *reinterpret_cast<const f4*>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = x[e];
+      } else {
+        ld_vals<E>(src, out);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) out[e] = 0.f;
+    }
+  }
   // Mma<E>::KPL consecutive elements of row i from column c0 (zero past the end)
   __device__ __forceinline__ void vals(const E* p, size_t row, int i, int c0, float* out) const {
     if (i < nvalid) {
@@ -126,13 +143,20 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
   return dmax <= 80.f;
 }
 
+// Per-row outputs written while the chunk's rows are in registers (forward
+// only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
+// row-major [64][K] and transposed [K][64].
+struct RowOut {
+  float* Qg; float* QgT; float* Kt; float* KtT;
+};
+
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
 // Aqk (lower incl. diagonal) to global fp32 [64][64]; when aqkT_out != null
 // also its transpose. Wave w computes block-row w.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
                                            const ChunkIn<E, K, V>& in, float* aqk_out,
-                                           float* aqkT_out) {
+                                           float* aqkT_out, const RowOut& ro = RowOut{}) {
   constexpr int GL = K + GCP;
   constexpr int NKS = K / Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
@@ -145,17 +169,30 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
 #pragma unroll
   for (int s = 0; s < NKS; ++s) {
     const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-    float bv[KPL], kv[KPL], qv[KPL];
+    float bv[KPL], kv[KPL], qv[KPL], gi[KPL];
     in.vals(in.b, in.rowK, ri, c0, bv);
     in.vals(in.k, in.rowK, ri, c0, kv);
+#pragma unroll
+    for (int e = 0; e < KPL; ++e) gi[e] = s_gc[ri * GL + c0 + e];
     lf[s] = Mma<E>::makes([&](int e) {
-      return bv[e] * kv[e] * expf(s_gc[ri * GL + c0 + e] - s_gc[r * GL + c0 + e]);
+      return bv[e] * kv[e] * expf(gi[e] - s_gc[r * GL + c0 + e]);
     });
+    if (want_q || ro.Qg) in.vals(in.q, in.rowQ, ri, c0, qv);
     if (want_q) {
-      in.vals(in.q, in.rowQ, ri, c0, qv);
       qf[s] = Mma<E>::makes([&](int e) {
-        return qv[e] * in.scale * expf(s_gc[ri * GL + c0 + e] - s_gc[r * GL + c0 + e]);
+        return qv[e] * in.scale * expf(gi[e] - s_gc[r * GL + c0 + e]);
       });
+    }
+    if (ro.Qg) {
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) {
+        const float qg = qv[e] * in.scale * expf(gi[e]);
+        const float kt = kv[e] * expf(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
+        ro.Qg[ri * K + c0 + e] = qg;
+        if (ro.QgT) ro.QgT[(c0 + e) * CH + ri] = qg;
+        if (ro.Kt) ro.Kt[ri * K + c0 + e] = kt;
+        ro.KtT[(c0 + e) * CH + ri] = kt;
+      }
     }
   }
   for (int J = 0; J < 4; ++J) {

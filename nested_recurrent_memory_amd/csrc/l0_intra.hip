@@ -31,29 +31,31 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int C = CH;
-  constexpr int LDX = C + 4;                 // fp32 rows of length C, 16-byte aligned
-  constexpr int GL = K + GCP;
+  constexpr int GL = K + GCP;                // gc rows, then X_w rows
+  constexpr int LT = C + 4;                  // T rows, 16-byte aligned for fragment loads
+  constexpr int LU = V + GCP;                // X_u rows
+  constexpr int KS = Mma<E>::KS;
+  typedef typename Mma<E>::SFrag SF;
   const int NT = a.NT, H = a.H;
   const int n = blockIdx.x % NT;
   const int bh = blockIdx.x / NT;
   const int h = bh % H, b = bh / H;
-  const int wv = wave_id(), tid = threadIdx.x;
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
 
-  // LDS: gc, T (fp32, MFMA rows), then a region used first for A and the
-  // inversion scratch, then for the transposed right-hand sides X, then for
-  // the Kt^T / Qg^T staging.
+  // LDS: gc (later overwritten in place by X_w = b k e^gc), and a region
+  // holding A, T and the inversion scratch, later X_u = w v. Each wave keeps
+  // its 16 rows of T in registers across the reuse.
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_T = sizeof(float) * C * LDX;
-  constexpr size_t SZ_AP = sizeof(float) * C * AT_LD + sizeof(float) * 3 * 16 * 17;
-  constexpr size_t SZ_X = sizeof(float) * (K + V) * LDX;
-  constexpr size_t SZ_R = SZ_AP > SZ_X ? SZ_AP : SZ_X;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_T + SZ_R];
+  constexpr size_t SZ_ATP = sizeof(float) * (C * AT_LD + C * LT + 3 * 16 * 17);
+  constexpr size_t SZ_XU = sizeof(float) * C * LU;
+  constexpr size_t SZ_R = SZ_ATP > SZ_XU ? SZ_ATP : SZ_XU;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R];
   float* s_gc = reinterpret_cast<float*>(smem);
-  float* s_T = reinterpret_cast<float*>(smem + SZ_GC);
-  char* region = smem + SZ_GC + SZ_T;
-  float* s_A = reinterpret_cast<float*>(region);
-  float* s_P = s_A + C * AT_LD;               // [3][16][17]
-  float* s_X = reinterpret_cast<float*>(region);
+  float* s_xw = s_gc;
+  float* s_A = reinterpret_cast<float*>(smem + SZ_GC);
+  float* s_T = s_A + C * AT_LD;
+  float* s_P = s_T + C * LT;                   // [3][16][17]
+  float* s_xu = s_A;
 
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, a.T, H, a.L, a.scale);
@@ -63,75 +65,82 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   l0_cumsum(s_gc, in);
   __syncthreads();
 
-  // ---- 2. A and Aqk
-  l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr);
-  __syncthreads();
-
-  // ---- 3. T = (I + A)^-1
-  l0_invert<LDX>(s_A, s_T, s_P);
-  if (a.TT) {
-    float* tt = a.TT + cix * C * C;
-    for (int e = tid; e < C * C; e += 256) tt[e] = s_T[(e % C) * LDX + e / C];
-  }
-
-  // ---- 4. right-hand sides, transposed (s_A and s_P are dead)
-  l0_build_X<E, K, V, LDX>(s_X, s_gc, in);
-  __syncthreads();
-
-  // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w
+  // ---- 2. A and Aqk; Qg, Kt and their transposes while the rows are loaded
   {
-    const int I = wv;
-    const int kd = tri_depth<E>(I);
+    RowOut ro{a.Qg + cix * C * K, a.QgT ? a.QgT + cix * K * C : nullptr,
+              a.Kt ? a.Kt + cix * C * K : nullptr, a.KtT + cix * K * C};
+    l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr, ro);
+  }
+  if (tid < K) a.gam[cix * K + tid] = expf(s_gc[(C - 1) * GL + tid]);
+  __syncthreads();
+
+  // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
+  l0_invert<LT>(s_A, s_T, s_P);
+  const int I = wv, R0 = 16 * I;
+  const int kd = tri_depth<E>(I);
+  SF tf[C / KS];
+  {
+    const float* trow = s_T + (R0 + (lane & 15)) * LT + kofs<E>(lane);
+#pragma unroll
+    for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::ld(trow + s * KS);
+    if (a.TT) {
+      // TT[j][i] = T[i][j] for this wave's rows i: 16 lanes per column j
+      float* tt = a.TT + cix * C * C;
+      const int i = R0 + (lane & 15);
+      for (int j = lane >> 4; j < C; j += 4) tt[j * C + i] = s_T[i * LT + j];
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. right-hand sides: X_w = b k e^gc in place of gc, X_u = w v over A/T
+  {
+    constexpr int VE = ChunkIn<E, K, V>::VE;    // elements per 16-byte load
+    for (int e = tid; e < C * K / VE; e += 256) {
+      const int m = e / (K / VE), c = (e % (K / VE)) * VE;
+      float bv[VE], kv[VE];
+      in.vec16(in.b, in.rowK, m, c, bv);
+      in.vec16(in.k, in.rowK, m, c, kv);
+#pragma unroll
+      for (int j = 0; j < VE; ++j) s_xw[m * GL + c + j] = bv[j] * kv[j] * expf(s_xw[m * GL + c + j]);
+    }
+    for (int e = tid; e < C * V / VE; e += 256) {
+      const int m = e / (V / VE), c = (e % (V / VE)) * VE;
+      float wv_[VE], vv[VE];
+      in.vec16(in.w, in.rowV, m, c, wv_);
+      in.vec16(in.v, in.rowV, m, c, vv);
+#pragma unroll
+      for (int j = 0; j < VE; ++j) s_xu[m * LU + c + j] = wv_[j] * vv[j];
+    }
+  }
+  __syncthreads();
+
+  // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w. The B fragments
+  // gather KPL consecutive rows m of one column.
+  {
     float* Wo = a.W + cix * C * K;
     float* Uo = a.U + cix * C * V;
     float* WTo = a.WT ? a.WT + cix * K * C : nullptr;
+    const int i0 = R0 + acc_row(0);
     for (int tc = 0; tc < (K + V) / 16; ++tc) {
-      f4 acc = mma_tile<E>(f4_zero(), s_T + 16 * I * LDX, LDX, s_X + 16 * tc * LDX, LDX, kd);
-      const int i0 = 16 * I + acc_row(0), col = 16 * tc + acc_col();
-      if (col < K) {
+      const bool isw = tc < K / 16;
+      const int col = (isw ? tc : tc - K / 16) * 16 + (lane & 15);
+      const float* xb = isw ? s_xw + col : s_xu + col;
+      const int ld = isw ? GL : LU;
+      f4 acc = f4_zero();
+#pragma unroll
+      for (int s = 0; s < C / KS; ++s) {
+        if (s * KS < kd) {   // T is zero past the block diagonal
+          const int m0 = s * KS + kofs<E>(lane);
+          acc = Mma<E>::mma(acc, tf[s], Mma<E>::makes([&](int e) { return xb[(m0 + e) * ld]; }));
+        }
+      }
+      if (isw) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) Wo[(i0 + rr) * K + col] = acc[rr];
         if (WTo) *reinterpret_cast<f4*>(WTo + col * C + i0) = acc;
       } else {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Uo[(i0 + rr) * V + (col - K)] = acc[rr];
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- 6. Kt (and its transpose), Qg (and its transpose), gam
-  float* s_kt = s_X;             // reuse: [K][LDX]
-  float* s_qg = s_X + K * LDX;   // [K][LDX]; fits since (K + V) >= 2 K when V >= K,
-                                 // otherwise Qg^T goes straight to global below
-  const bool qg_in_lds = V >= K;
-  float* Qgo = a.Qg + cix * C * K;
-  for (int e = tid; e < C * K; e += 256) {
-    const int c = e / K, kk = e % K;
-    const float gcv = s_gc[c * GL + kk];
-    s_kt[kk * LDX + c] = in.K_(c, kk) * expf(s_gc[(C - 1) * GL + kk] - gcv);
-    const float qg = in.Q_(c, kk) * in.scale * expf(gcv);
-    Qgo[c * K + kk] = qg;
-    if (qg_in_lds) s_qg[kk * LDX + c] = qg;
-    else if (a.QgT) a.QgT[cix * K * C + kk * C + c] = qg;
-  }
-  if (tid < K) a.gam[cix * K + tid] = expf(s_gc[(C - 1) * GL + tid]);
-  __syncthreads();
-  {
-    // rows of 64 as 16-byte vectors
-    float* Ko = a.KtT + cix * K * C;
-    float* QTo = a.QgT ? a.QgT + cix * K * C : nullptr;
-    for (int e = tid; e < K * C / 4; e += 256) {
-      const int kk = e / (C / 4), c = (e % (C / 4)) * 4;
-      *reinterpret_cast<f4*>(Ko + kk * C + c) = *reinterpret_cast<const f4*>(s_kt + kk * LDX + c);
-      if (QTo && qg_in_lds)
-        *reinterpret_cast<f4*>(QTo + kk * C + c) = *reinterpret_cast<const f4*>(s_qg + kk * LDX + c);
-    }
-    if (a.Kt) {
-      float* Kn = a.Kt + cix * C * K;
-      for (int e = tid; e < C * K; e += 256) {
-        const int c = e / K, kk = e % K;
-        Kn[c * K + kk] = s_kt[kk * LDX + c];
+        for (int rr = 0; rr < 4; ++rr) Uo[(i0 + rr) * V + col] = acc[rr];
       }
     }
   }
