@@ -118,35 +118,38 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr int C = CH;
-  constexpr int GL = K + GCP;
-  constexpr int LDK = K + 8;                 // staged input rows (E)
-  constexpr int LXK = K + 4, LXV = V + 4;    // fp32 rows
+  constexpr int NH = K > 64 ? 64 : K;          // columns per pass of the decay backward
+  constexpr int NPASS = K / NH;
+  constexpr int CTH = NH / 16;
+  constexpr int GH = NH + GCP;                 // gc rows of one pass
+  constexpr int LDI = NH + 16 / (int)sizeof(E); // staged input rows of one pass
+  constexpr int LXK = K + 4, LXV = V + 4;      // fp32 rows
   constexpr int CTK = K / 16, CTV = V / 16;
   constexpr int KS = Mma<E>::KS;
-  // bf16: the chunk's k, b, q rows are staged in LDS; fp32 (a test-only path)
-  // reads them from global memory to stay inside the LDS budget
+  // bf16: each pass stages the chunk's k, b, q columns in LDS; fp32 (a
+  // test-only path) reads them from global memory
   constexpr bool STAGE = !std::is_same<E, float>::value;
   typedef typename Mma<E>::SFrag SF;
   typedef Mma<float> MF;
-  constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDK : 0;
-  // region R: dX_w, dX_u (fp32); after the dA product: dA, dAqk; after the
-  // decay backward: the cumulative-decay gradient
+  // Phases 2-3 hold dX_w, dX_u; phases 4-6 reuse the space for dA, dAqk and,
+  // per pass, gc (later its gradient, in place) and the k, b, q columns.
   constexpr size_t SZ_X = sizeof(float) * C * (LXK + LXV);
   constexpr size_t SZ_DA = sizeof(float) * 2 * C * AT_LD;
-  constexpr size_t SZ_R = SZ_X > SZ_DA ? SZ_X : SZ_DA;
-  static_assert(C * GL <= 2 * C * AT_LD, "dgc must fit the dA region");
-  __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_IN + SZ_R + sizeof(float) * K];
-  float* s_gc = reinterpret_cast<float*>(smem);
-  E* s_k = reinterpret_cast<E*>(smem + SZ_GC);
-  E* s_b = s_k + C * LDK;
-  E* s_q = s_b + C * LDK;
-  float* s_dXw = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN);
+  constexpr size_t SZ_G = sizeof(float) * C * GH;
+  constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDI : 0;
+  constexpr size_t SZ_P = SZ_DA + SZ_G + SZ_IN;
+  constexpr size_t SZ_R = SZ_X > SZ_P ? SZ_X : SZ_P;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * 2 * K];
+  float* s_dXw = reinterpret_cast<float*>(smem);
   float* s_dXu = s_dXw + C * LXK;
-  float* s_dA = s_dXw;                       // after the dA product
+  float* s_dA = reinterpret_cast<float*>(smem);
   float* s_dQ = s_dA + C * AT_LD;
-  float* s_dgc = s_dA;                       // after the decay backward
-  float* s_col = reinterpret_cast<float*>(smem + SZ_GC + SZ_IN + SZ_R);
+  float* s_g = reinterpret_cast<float*>(smem + SZ_DA);
+  E* s_k = reinterpret_cast<E*>(smem + SZ_DA + SZ_G);
+  E* s_b = s_k + C * LDI;
+  E* s_q = s_b + C * LDI;
+  float* s_gl = reinterpret_cast<float*>(smem + SZ_R);   // gc of the last row, per column
+  float* s_col = s_gl + K;
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -157,24 +160,6 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, T, H, a.L, a.scale);
   const int t0 = in.t0, nvalid = in.nvalid;
-
-  auto KV = [&](int i, int c) -> float {
-    if constexpr (STAGE) return to_f(s_k[i * LDK + c]); else return in.K_(i, c);
-  };
-  auto BV = [&](int i, int c) -> float {
-    if constexpr (STAGE) return to_f(s_b[i * LDK + c]); else return in.B_(i, c);
-  };
-  auto QV = [&](int i, int c) -> float {
-    if constexpr (STAGE) return to_f(s_q[i * LDK + c]); else return in.Q_(i, c);
-  };
-
-  // ---- 1. gc and the chunk's rows
-  if constexpr (STAGE) {
-    stage_rows<E>(s_k, LDK, in.k + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
-    stage_rows<E>(s_b, LDK, in.b + (size_t)t0 * in.rowK, in.rowK, C, K, nvalid);
-    stage_rows<E>(s_q, LDK, in.q + (size_t)t0 * in.rowQ, in.rowQ, C, K, nvalid);
-  }
-  l0_cumsum(s_gc, in);
   for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
 
   // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns rows 16w..16w+15
@@ -217,7 +202,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   }
   __syncthreads();
 
-  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until R is free)
+  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
   f4 dat[4];
   {
     const float* Wg = a.W + cix * C * K;
@@ -245,120 +230,142 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     const float* dq = a.dAqk + cix * C * C;
     for (int e = tid; e < C * C; e += 256) s_dQ[(e / C) * AT_LD + e % C] = dq[e];
   }
-  __syncthreads();
 
-  const bool safe = l0_block_safe<K>(s_gc, wv);
   const int R0 = 16 * wv;
+  const float* dQg = a.dQg + cix * C * K;
+  const float* dKt = a.dKt + cix * C * K;
+  const size_t tok = (size_t)b * T * H + h;
+  E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
+  E* dko = static_cast<E*>(a.dk) + tok * K;
+  E* dbo = static_cast<E*>(a.db) + tok * K;
+  float* dgo = a.dg + tok * K;
+  const float* dgam = a.dgam + cix * K;
 
-  // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w
-  //   sum_j dA_ij k_j e^(gc_i - gc_j) = e^(gc_i - gc_r) sum_j dA_ij [k_j e^(gc_r - gc_j)]
-  // on fp32 MFMA: these sums cancel against those of 4b inside dg
-  f4 dbk[CTK], dqa[CTK];
 #pragma unroll
-  for (int ct = 0; ct < CTK; ++ct) { dbk[ct] = f4_zero(); dqa[ct] = f4_zero(); }
-  {
-    const int jlim = safe ? R0 + 16 : R0;     // unsafe: diagonal block done exactly below
-    for (int j0 = 0; j0 < jlim; j0 += MF::KS) {
-      const int j = j0 + (lane >> 4);
-      const float fa = s_dA[ri * AT_LD + j], fq = s_dQ[ri * AT_LD + j];
-#pragma unroll
-      for (int ct = 0; ct < CTK; ++ct) {
-        const int kc = ct * 16 + (lane & 15);
-        const float fb = KV(j, kc) * expf(fminf(s_gc[R0 * GL + kc] - s_gc[j * GL + kc], 88.f));
-        dbk[ct] = MF::mma(dbk[ct], fa, fb);
-        dqa[ct] = MF::mma(dqa[ct], fq, fb);
-      }
+  for (int p = 0; p < NPASS; ++p) {
+    const int c0 = p * NH;
+    auto KV = [&](int i, int kl) -> float {
+      if constexpr (STAGE) return to_f(s_k[i * LDI + kl]); else return in.K_(i, c0 + kl);
+    };
+    auto BV = [&](int i, int kl) -> float {
+      if constexpr (STAGE) return to_f(s_b[i * LDI + kl]); else return in.B_(i, c0 + kl);
+    };
+    auto QV = [&](int i, int kl) -> float {
+      if constexpr (STAGE) return to_f(s_q[i * LDI + kl]); else return in.Q_(i, c0 + kl);
+    };
+
+    // ---- 4. this pass's gc and input columns
+    cumsum_cols<NH, GH>(s_g, in, c0, s_gl + c0);
+    if constexpr (STAGE) {
+      stage_rows<E>(s_k, LDI, in.k + (size_t)t0 * in.rowK + c0, in.rowK, C, NH, nvalid);
+      stage_rows<E>(s_b, LDI, in.b + (size_t)t0 * in.rowK + c0, in.rowK, C, NH, nvalid);
+      stage_rows<E>(s_q, LDI, in.q + (size_t)t0 * in.rowQ + c0, in.rowQ, C, NH, nvalid);
     }
+    __syncthreads();
+    const bool safe = block_safe<NH, GH>(s_g, wv);
+
+    // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w
+    //   sum_j dA_ij k_j e^(gc_i - gc_j) = e^(gc_i - gc_r) sum_j dA_ij [k_j e^(gc_r - gc_j)]
+    // on fp32 MFMA: these sums cancel against those of 4b inside dg
+    f4 dbk[CTH], dqa[CTH];
 #pragma unroll
-    for (int ct = 0; ct < CTK; ++ct) {
-      const int kc = ct * 16 + acc_col();
+    for (int ct = 0; ct < CTH; ++ct) { dbk[ct] = f4_zero(); dqa[ct] = f4_zero(); }
+    {
+      const int jlim = safe ? R0 + 16 : R0;     // unsafe: diagonal block done exactly below
+      for (int j0 = 0; j0 < jlim; j0 += MF::KS) {
+        const int j = j0 + (lane >> 4);
+        const float fa = s_dA[ri * AT_LD + j], fq = s_dQ[ri * AT_LD + j];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = R0 + acc_row(r);
-        const float f = expf(s_gc[i * GL + kc] - s_gc[R0 * GL + kc]);
-        float xb = dbk[ct][r] * f, xq = dqa[ct][r] * f;
-        if (!safe) {
-          for (int j = R0; j <= i; ++j) {
-            const float d = KV(j, kc) * expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
-            if (j < i) xb += s_dA[i * AT_LD + j] * d;
-            xq += s_dQ[i * AT_LD + j] * d;
-          }
+        for (int ct = 0; ct < CTH; ++ct) {
+          const int kl = ct * 16 + (lane & 15);
+          const float fb = KV(j, kl) * expf(fminf(s_g[R0 * GH + kl] - s_g[j * GH + kl], 88.f));
+          dbk[ct] = MF::mma(dbk[ct], fa, fb);
+          dqa[ct] = MF::mma(dqa[ct], fq, fb);
         }
-        dbk[ct][r] = xb;
-        dqa[ct][r] = xq;
       }
-    }
-  }
-
-  // ---- 4b. dk from A and Aqk, rows j of block J = w:
-  //   sum_i (dA_ij bk_i + dAqk_ij q_i) e^(gc_i - gc_j)
-  //   = e^(gc_e - gc_j) sum_i (...) e^(gc_i - gc_e),  e = last row of block J
-  f4 dka[CTK];
 #pragma unroll
-  for (int ct = 0; ct < CTK; ++ct) dka[ct] = f4_zero();
-  {
-    const int RE = R0 + 15;
-    const int ilo = safe ? R0 : R0 + 16;       // unsafe: diagonal block done exactly below
-    const int rj = R0 + (lane & 15);
-    for (int i0 = ilo; i0 < C; i0 += MF::KS) {
-      const int i = i0 + (lane >> 4);
-      const float fa = s_dA[i * AT_LD + rj], fq = s_dQ[i * AT_LD + rj];
+      for (int ct = 0; ct < CTH; ++ct) {
+        const int kl = ct * 16 + acc_col();
 #pragma unroll
-      for (int ct = 0; ct < CTK; ++ct) {
-        const int kc = ct * 16 + (lane & 15);
-        const float d = expf(fminf(s_gc[i * GL + kc] - s_gc[RE * GL + kc], 88.f));
-        dka[ct] = MF::mma(dka[ct], fa, BV(i, kc) * KV(i, kc) * d);
-        dka[ct] = MF::mma(dka[ct], fq, QV(i, kc) * in.scale * d);
-      }
-    }
-#pragma unroll
-    for (int ct = 0; ct < CTK; ++ct) {
-      const int kc = ct * 16 + acc_col();
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = R0 + acc_row(r);
-        float x = dka[ct][r] * expf(s_gc[RE * GL + kc] - s_gc[j * GL + kc]);
-        if (!safe) {
-          for (int i = j; i < R0 + 16; ++i) {
-            const float d = expf(fminf(s_gc[i * GL + kc] - s_gc[j * GL + kc], 0.f));
-            x += (s_dA[i * AT_LD + j] * BV(i, kc) * KV(i, kc) +
-                  s_dQ[i * AT_LD + j] * QV(i, kc) * in.scale) * d;
+        for (int r = 0; r < 4; ++r) {
+          const int i = R0 + acc_row(r);
+          const float f = expf(s_g[i * GH + kl] - s_g[R0 * GH + kl]);
+          float xb = dbk[ct][r] * f, xq = dqa[ct][r] * f;
+          if (!safe) {
+            for (int j = R0; j <= i; ++j) {
+              const float d = KV(j, kl) * expf(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
+              if (j < i) xb += s_dA[i * AT_LD + j] * d;
+              xq += s_dQ[i * AT_LD + j] * d;
+            }
           }
+          dbk[ct][r] = xb;
+          dqa[ct][r] = xq;
         }
-        dka[ct][r] = x;
       }
     }
-  }
-  __syncthreads();   // s_dgc overwrites s_dA / s_dQ
 
-  // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
-  {
-    const float* dQg = a.dQg + cix * C * K;
-    const float* dKt = a.dKt + cix * C * K;
-    const size_t tok = (size_t)b * T * H + h;
-    E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
-    E* dko = static_cast<E*>(a.dk) + tok * K;
-    E* dbo = static_cast<E*>(a.db) + tok * K;
+    // ---- 4b. dk from A and Aqk, rows j of block J = w:
+    //   sum_i (dA_ij bk_i + dAqk_ij q_i) e^(gc_i - gc_j)
+    //   = e^(gc_e - gc_j) sum_i (...) e^(gc_i - gc_e),  e = last row of block J
+    f4 dka[CTH];
 #pragma unroll
-    for (int ct = 0; ct < CTK; ++ct) {
-      const int kc = ct * 16 + acc_col();
-      const float glast = s_gc[(C - 1) * GL + kc];
+    for (int ct = 0; ct < CTH; ++ct) dka[ct] = f4_zero();
+    {
+      const int RE = R0 + 15;
+      const int ilo = safe ? R0 : R0 + 16;       // unsafe: diagonal block done exactly below
+      const int rj = R0 + (lane & 15);
+      for (int i0 = ilo; i0 < C; i0 += MF::KS) {
+        const int i = i0 + (lane >> 4);
+        const float fa = s_dA[i * AT_LD + rj], fq = s_dQ[i * AT_LD + rj];
+#pragma unroll
+        for (int ct = 0; ct < CTH; ++ct) {
+          const int kl = ct * 16 + (lane & 15);
+          const float d = expf(fminf(s_g[i * GH + kl] - s_g[RE * GH + kl], 88.f));
+          dka[ct] = MF::mma(dka[ct], fa, BV(i, kl) * KV(i, kl) * d);
+          dka[ct] = MF::mma(dka[ct], fq, QV(i, kl) * in.scale * d);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < CTH; ++ct) {
+        const int kl = ct * 16 + acc_col();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = R0 + acc_row(r);
+          float x = dka[ct][r] * expf(s_g[RE * GH + kl] - s_g[j * GH + kl]);
+          if (!safe) {
+            for (int i = j; i < R0 + 16; ++i) {
+              const float d = expf(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
+              x += (s_dA[i * AT_LD + j] * BV(i, kl) * KV(i, kl) +
+                    s_dQ[i * AT_LD + j] * QV(i, kl) * in.scale) * d;
+            }
+          }
+          dka[ct][r] = x;
+        }
+      }
+    }
+    __syncthreads();   // the cumulative-decay gradient overwrites gc in place
+
+    // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
+#pragma unroll
+    for (int ct = 0; ct < CTH; ++ct) {
+      const int kl = ct * 16 + acc_col(), kc = c0 + kl;
+      const float glast = s_gl[kc];
       float colsum = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = R0 + acc_row(r);
-        const float gcv = s_gc[i * GL + kc];
+        const float gcv = s_g[i * GH + kl];
         const float eg = expf(gcv), ekt = expf(glast - gcv);
-        const float bi = BV(i, kc), ki = KV(i, kc), qh = QV(i, kc) * in.scale;
+        const float bi = BV(i, kl), ki = KV(i, kl), qh = QV(i, kl) * in.scale;
         const float gq = dQg[i * K + kc], gk = dKt[i * K + kc];
-        const float xw = dxw[ct][r];
+        const float xw = dxw[p * CTH + ct][r];
         const float dqh = dqa[ct][r] + gq * eg;
         const float db_ = dbk[ct][r] * ki + xw * ki * eg;
         const float dk_ = dka[ct][r] + dbk[ct][r] * bi + xw * bi * eg + gk * ekt;
         const float dgc = bi * ki * dbk[ct][r] + qh * dqa[ct][r] - ki * dka[ct][r] +
                           xw * bi * ki * eg + gq * qh * eg - gk * ki * ekt;
         colsum += gk * ki * ekt;
-        s_dgc[i * GL + kc] = dgc;
+        s_g[i * GH + kl] = dgc;
         if (i < nvalid) {
           dqo[(size_t)(t0 + i) * H * a.L * K + kc] = from_f<E>(dqh * in.scale);
           dko[(size_t)(t0 + i) * H * K + kc] = from_f<E>(dk_);
@@ -369,19 +376,19 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       colsum += __shfl_xor(colsum, 32, WAVE);
       if (lane < 16) atomicAdd(&s_col[kc], colsum);
     }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
-  // every Kt and gam
-  if (tid < K) {
-    const float* dgam = a.dgam + cix * K;
-    float run = s_col[tid] + dgam[tid] * expf(s_gc[(C - 1) * GL + tid]);
-    float* dgo = a.dg + ((size_t)b * T * H + h) * K;
-    for (int i = C - 1; i >= 0; --i) {
-      run += s_dgc[i * GL + tid];
-      if (i < nvalid) dgo[(size_t)(t0 + i) * H * K + tid] = run;
+    // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
+    // every Kt and gam
+    if (tid < NH) {
+      const int kc = c0 + tid;
+      float run = s_col[kc] + dgam[kc] * expf(s_gl[kc]);
+      for (int i = C - 1; i >= 0; --i) {
+        run += s_g[i * GH + tid];
+        if (i < nvalid) dgo[(size_t)(t0 + i) * H * K + kc] = run;
+      }
     }
+    __syncthreads();   // the next pass restages gc and the inputs
   }
 }
 

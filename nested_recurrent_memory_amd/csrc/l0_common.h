@@ -99,20 +99,22 @@ struct ChunkLds {
   __device__ __forceinline__ float Q_(int i, int c) const { return to_f(q[i * LD + c]); }
 };
 
-// gc[i][k] = sum_{s<=i} g_s[k] within the chunk (zero past the end), into
-// s_gc [64][K + GCP]. TPC = 256 / K adjacent lanes share column k, each
-// summing 64 / TPC consecutive rows in registers (independent, coalesced
-// loads); the segment offsets come from the neighbouring lanes.
-template <typename E, int K, int V>
-__device__ __forceinline__ void l0_cumsum(float* s_gc, const ChunkIn<E, K, V>& in) {
-  constexpr int TPC = 256 / K;
+// gc[i][c] = sum_{s<=i} g_s[c0 + c] within the chunk (zero past the end) for
+// the NC columns from c0, into dst [64][LDG]; glast (when set) receives row
+// 63. TPC = 256 / NC adjacent lanes share a column, each summing 64 / TPC
+// consecutive rows in registers (independent loads); the segment offsets come
+// from the neighbouring lanes.
+template <int NC, int LDG, typename E, int K, int V>
+__device__ __forceinline__ void cumsum_cols(float* dst, const ChunkIn<E, K, V>& in, int c0,
+                                            float* glast) {
+  constexpr int TPC = 256 / NC;
   constexpr int SEG = CH / TPC;
   const int tid = threadIdx.x, c = tid / TPC, part = tid % TPC;
   float x[SEG];
 #pragma unroll
   for (int r = 0; r < SEG; ++r) {
     const int i = part * SEG + r;
-    x[r] = i < in.nvalid ? in.g[(size_t)(in.t0 + i) * in.rowK + c] : 0.f;
+    x[r] = i < in.nvalid ? in.g[(size_t)(in.t0 + i) * in.rowK + c0 + c] : 0.f;
   }
 #pragma unroll
   for (int r = 1; r < SEG; ++r) x[r] += x[r - 1];
@@ -124,23 +126,34 @@ __device__ __forceinline__ void l0_cumsum(float* s_gc, const ChunkIn<E, K, V>& i
     if (p < part) off += t;
   }
 #pragma unroll
-  for (int r = 0; r < SEG; ++r) s_gc[(part * SEG + r) * (K + GCP) + c] = x[r] + off;
+  for (int r = 0; r < SEG; ++r) dst[(part * SEG + r) * LDG + c] = x[r] + off;
+  if (glast && part == TPC - 1) glast[c] = x[SEG - 1] + off;
 }
 
-// Largest decay inside 16-row block I, over every row and channel:
+// gc over all K columns into s_gc [64][K + GCP].
+template <typename E, int K, int V>
+__device__ __forceinline__ void l0_cumsum(float* s_gc, const ChunkIn<E, K, V>& in) {
+  cumsum_cols<K, K + GCP>(s_gc, in, 0, static_cast<float*>(nullptr));
+}
+
+// Largest decay inside 16-row block I over NC columns of gc (row stride LDG):
 // max (gc[16 I] - gc[j]). When it is at most 80 nats, factors e^(gc_r - gc_j)
 // for j in the block stay inside fp32 range.
-template <int K>
-__device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
+template <int NC, int LDG>
+__device__ __forceinline__ bool block_safe(const float* gc, int I) {
   const int lane = lane_id(), r = 16 * I;
   float dmax = 0.f;
-  for (int e = lane; e < 16 * K; e += WAVE) {
-    const int j = r + e / K, c = e % K;
-    dmax = fmaxf(dmax, s_gc[r * (K + GCP) + c] - s_gc[j * (K + GCP) + c]);
+  for (int e = lane; e < 16 * NC; e += WAVE) {
+    const int j = r + e / NC, c = e % NC;
+    dmax = fmaxf(dmax, gc[r * LDG + c] - gc[j * LDG + c]);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, o, WAVE));
   return dmax <= 80.f;
+}
+template <int K>
+__device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
+  return block_safe<K, K + GCP>(s_gc, I);
 }
 
 // Per-row outputs written while the chunk's rows are in registers (forward
