@@ -65,12 +65,13 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
  * Writes hT [B,H,NT,V,K] (state entering each chunk, transposed), vnT
- * [B,H,NT,V,64] (the chunk's new values, transposed) and final_state[:, :, 0].
- * initial_state may be NULL (zeros). */
+ * [B,H,NT,V,64] (the chunk's new values, transposed) and final_state[:, :, 0];
+ * for the backward, when not NULL, h [B,H,NT,K,V] (the same states as rows)
+ * and vn [B,H,NT,64,V]. initial_state may be NULL (zeros). */
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam,
                          const float* initial_state, float* hT, float* vnT,
-                         float* final_state, void* stream);
+                         float* h, float* vn, float* final_state, void* stream);
 
 /* Promotion probe of level `level` >= 1: PROBES[promotion] applied to the
  * lower level's state after each of this level's firings
@@ -98,23 +99,24 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
 /* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
  * probe's scan-ready pairs: NF firings, NG = ceil(NT / f) stored group
  * states. Writes states [B,NG,H,K,V] fp32 (state entering each group; groups
- * past the last firing hold the final state) and final_state[:, :, level].
- * initial_state may be NULL. */
+ * past the last firing hold the final state), statesT [B,NG,H,V,K] (the same,
+ * transposed; may be NULL) and final_state[:, :, level]. initial_state may be
+ * NULL. */
 int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* A,
                             const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
-                            float* final_state, void* stream);
+                            float* statesT, float* final_state, void* stream);
 
 /* Output for every token (ops/chunk.py:129-156, 250-251, 285-286):
  * o = mix_0 (Qg h + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[group].
- * states[l] (l = 1..L-1) is level l's fp32 group states with ng[l] groups and
- * firing interval f[l]; entries at l = 0 are ignored. o [B,T,H,V] in the
- * working dtype. reads, when not NULL, receives each level's unmixed read,
- * fp32 [L,B,T,H,V]. */
+ * statesT[l] (l = 1..L-1) is level l's transposed group states
+ * [B,ng[l],H,V,K] (from ngdn_upper_scan_fwd) with firing interval f[l];
+ * entries at l = 0 are ignored. o [B,T,H,V] in the working dtype. reads, when
+ * not NULL, receives each level's unmixed read, fp32 [L,B,T,H,V]. */
 int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
-                        const void* mix, const float* const* states,
+                        const void* mix, const float* const* statesT,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* reads, void* stream);
 
@@ -124,12 +126,14 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
 
 /* Output backward per chunk (ops/chunk.py:423-449): dmix for every level
  * (fp32 [B,T,H,L]) and dq[..., l, :] for l >= 1 (working dtype [B,T,H,L,K]);
- * inputs as for ngdn_output_fwd plus do [B,T,H,V]. */
+ * inputs as for ngdn_output_fwd plus the untransposed group states
+ * states[l] [B,ng[l],H,K,V] and do [B,T,H,V]. */
 int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
-                        const int32_t* ng, const int32_t* f, const void* dout,
-                        void* dq, float* dmix, void* stream);
+                        const float* const* statesT, const int32_t* ng,
+                        const int32_t* f, const void* dout, void* dq,
+                        float* dmix, void* stream);
 
 /* Read gradient of level `level`'s group states (read_level_bwd,
  * ops/chunk.py:307-336): d_states fp32 [B,ng,H,K,V], written. */
@@ -165,10 +169,11 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             float* dSp, float* dvn, float* d_initial,
                             void* stream);
 
-/* Level-0 chunk backward, state half: dQg, dKt [B,H,NT,64,K], dWT
- * [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam [B,H,NT,K]. */
-int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* hT, const float* dSp,
-                          const float* vnT, const float* dVn, const void* dout,
+/* Level-0 chunk backward, state half, from h and vn of ngdn_l0_scan_fwd:
+ * dQg, dKt [B,H,NT,64,K], dWT [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam
+ * [B,H,NT,K]. */
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* h, const float* dSp,
+                          const float* vn, const float* dVn, const void* dout,
                           const void* mix, float* dQg, float* dWT, float* dKt,
                           float* dAqk, float* dgam, void* stream);
 

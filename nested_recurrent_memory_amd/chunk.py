@@ -107,11 +107,13 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
               P(W), P(U), P(KtT), P(Qg), P(Aqk), P(gam), P(Kt), P(WT), P(QgT), P(AqkT),
               P(TT), st)
     hT, vnT = f32(B, H, NT, V, K), f32(B, H, NT, V, 64)
+    h_, vn_ = opt(B, H, NT, K, V), opt(B, H, NT, 64, V)
     final = torch.empty(B, H, L, K, V, device=dev, dtype=torch.float32)
     _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), P(W), P(U), P(KtT), P(gam), P(init_),
-              P(hT), P(vnT), P(final), st)
+              P(hT), P(vnT), P(h_), P(vn_), P(final), st)
 
-    states = [None] * L
+    states = [None] * L       # group states as rows [B,NG,H,K,V]
+    statesT = [None] * L      # and transposed [B,NG,H,V,K]
     levels = [None] * L
     merge = promotion == "merge"
     par = {}
@@ -132,22 +134,23 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                       P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(A_), P(KT_), P(U_),
                       P(gm_), P(keysN), P(AT_), None, None, None, None, None, st,
                       tag=f"ngdn_probe_fwd.{lvl}")
-        S_l = torch.empty(B, ng, H, K, V, device=dev, dtype=torch.float32)
+        S_l, ST_l = f32(B, ng, H, K, V), f32(B, ng, H, V, K)
         _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, N, nf, ng, P(A_), P(KT_),
-                  P(U_), P(gm_), P(init_), P(S_l), P(final), st,
+                  P(U_), P(gm_), P(init_), P(S_l), P(ST_l), P(final), st,
                   tag=f"ngdn_upper_scan_fwd.{lvl}")
-        states[lvl] = S_l
+        states[lvl], statesT[lvl] = S_l, ST_l
         levels[lvl] = dict(N=N, nf=nf, ng=ng, keys=keysN, AT=AT_, gam=gm_)
 
     o = e(B, T, H, V)
-    sp, ngs, fs = _level_arrays(states, NT, f, L)
+    spT, ngs, fs = _level_arrays(statesT, NT, f, L)
     _lib.call("ngdn_output_fwd", ctypes.byref(d), P(Qg), P(Aqk), P(hT), P(vnT), P(q_),
-              P(mix_), sp, ngs, fs, P(o), None, st)
+              P(mix_), spT, ngs, fs, P(o), None, st)
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
                      KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
-                     hT=hT, vnT=vnT, states=states, levels=levels, final=final, par=par,
+                     hT=hT, vnT=vnT, h=h_, vn=vn_, states=states, statesT=statesT,
+                     levels=levels, final=final, par=par,
                      code=code, wd=wd)
     return o, final, saved
 
@@ -200,8 +203,9 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     dq = e(B, T, H, L, K)
     dmix = e(B, T, H, L, dt=torch.float32)
     sp, ngs, fs = _level_arrays(states, NT, f, L)
+    spT, _, _ = _level_arrays(sv["statesT"], NT, f, L)
     _lib.call("ngdn_output_bwd", ctypes.byref(d), P(sv["Qg"]), P(sv["Aqk"]), P(sv["hT"]),
-              P(sv["vnT"]), P(q_), P(mix_), sp, ngs, fs, P(do_), P(dq), P(dmix), st)
+              P(sv["vnT"]), P(q_), P(mix_), sp, spT, ngs, fs, P(do_), P(dq), P(dmix), st)
 
     d_final = (dfinal.to(torch.float32).contiguous().clone() if dfinal is not None
                else z32(B, H, L, K, V))
@@ -257,7 +261,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
               P(d_final), P(dSp0), P(dVn0), P(dVnT0), P(d_init), st)
     dQg, dKt, dWT = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K), f32(B, H, NT, K, 64)
     dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
-    _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(sv["hT"]), P(dSp0), P(sv["vnT"]), P(dVn0),
+    _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(sv["h"]), P(dSp0), P(sv["vn"]), P(dVn0),
               P(do_), P(mix_), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam), st)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
     dg = e(B, T, H, K, dt=torch.float32)

@@ -67,7 +67,7 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam,
                          const float* initial_state, float* hT, float* vnT,
-                         float* final_state, void* stream) {
+                         float* h, float* vn, float* final_state, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_fwd")) return r;
   if (!W || !U || !KtT || !gam || !hT || !final_state)
@@ -76,8 +76,8 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
   ngdn::ScanArgs a{};
   a.A = W; a.BT = KtT; a.U = U; a.gam = gam;
   a.init = initial_state; a.init_sh = d->L * skv; a.init_sb = d->H * a.init_sh;
-  a.states = hT; a.state_mode = 0; a.NG = nchunks(d);
-  a.vnT = vnT;
+  a.st_vk = hT; a.st_kv = h; a.state_mode = 0; a.NG = nchunks(d);
+  a.vnT = vnT; a.vn = vn;
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");
@@ -137,7 +137,7 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* A,
                             const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
-                            float* final_state, void* stream) {
+                            float* statesT, float* final_state, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_upper_scan_fwd")) return r;
   if (level < 1 || level >= d->L)
@@ -154,8 +154,8 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   a.A = A; a.BT = KT; a.U = U; a.gam = gam;
   a.init = initial_state ? initial_state + (long long)level * skv : nullptr;
   a.init_sh = d->L * skv; a.init_sb = d->H * a.init_sh;
-  a.states = states; a.state_mode = 1; a.NG = ng;
-  a.vnT = nullptr;
+  a.st_kv = states; a.st_vk = statesT; a.state_mode = 1; a.NG = ng;
+  a.vnT = nullptr; a.vn = nullptr;
   a.fin = final_state + (long long)level * skv; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nf; a.M = n_pairs; a.V = d->V;
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_fwd");
@@ -163,7 +163,7 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
 
 int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
-                        const void* mix, const float* const* states,
+                        const void* mix, const float* const* statesT,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* reads, void* stream) {
   g_err[0] = 0;
@@ -175,9 +175,9 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
   ngdn::OutputArgs a{};
   a.Qg = Qg; a.Aqk = Aqk; a.hT = hT; a.vnT = vnT; a.q = q; a.mix = mix;
   for (int l = 1; l < d->L; ++l) {
-    if (!states || !states[l] || !ng || !f || f[l] <= 0)
+    if (!statesT || !statesT[l] || !ng || !f || f[l] <= 0)
       return fail(NGDN_EINVAL, "ngdn_output_fwd: level %d states missing", l);
-    a.states[l] = states[l]; a.NGl[l] = ng[l]; a.f[l] = f[l];
+    a.statesT[l] = statesT[l]; a.NGl[l] = ng[l]; a.f[l] = f[l];
   }
   a.o = o; a.reads = reads;
   a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
@@ -188,8 +188,9 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
 int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* states,
-                        const int32_t* ng, const int32_t* f, const void* dout,
-                        void* dq, float* dmix, void* stream) {
+                        const float* const* statesT, const int32_t* ng,
+                        const int32_t* f, const void* dout, void* dq,
+                        float* dmix, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_output_bwd")) return r;
   if (d->K != d->V)
@@ -199,9 +200,9 @@ int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
   ngdn::OutputBwdArgs a{};
   a.f.Qg = Qg; a.f.Aqk = Aqk; a.f.hT = hT; a.f.vnT = vnT; a.f.q = q; a.f.mix = mix;
   for (int l = 1; l < d->L; ++l) {
-    if (!states || !states[l] || !ng || !f || f[l] <= 0)
+    if (!states || !states[l] || !statesT || !statesT[l] || !ng || !f || f[l] <= 0)
       return fail(NGDN_EINVAL, "ngdn_output_bwd: level %d states missing", l);
-    a.f.states[l] = states[l]; a.f.NGl[l] = ng[l]; a.f.f[l] = f[l];
+    a.f.states[l] = states[l]; a.f.statesT[l] = statesT[l]; a.f.NGl[l] = ng[l]; a.f.f[l] = f[l];
   }
   a.f.B = d->B; a.f.T = d->T; a.f.H = d->H; a.f.L = d->L; a.f.NT = nchunks(d); a.f.scale = d->scale;
   a.dout = dout; a.dq = dq; a.dmix = dmix;
@@ -279,15 +280,15 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_bwd");
 }
 
-int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* hT, const float* dSp,
-                          const float* vnT, const float* dVn, const void* dout,
+int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* h, const float* dSp,
+                          const float* vn, const float* dVn, const void* dout,
                           const void* mix, float* dQg, float* dWT, float* dKt,
                           float* dAqk, float* dgam, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_bwd_state")) return r;
-  if (!hT || !dSp || !vnT || !dVn || !dout || !mix || !dQg || !dWT || !dKt || !dAqk || !dgam)
+  if (!h || !dSp || !vn || !dVn || !dout || !mix || !dQg || !dWT || !dKt || !dAqk || !dgam)
     return fail(NGDN_EINVAL, "ngdn_l0_bwd_state: NULL tensor");
-  ngdn::L0BwdStateArgs a{hT, dSp, vnT, dVn, dout, mix, dQg, dWT, dKt, dAqk, dgam,
+  ngdn::L0BwdStateArgs a{h, dSp, vn, dVn, dout, mix, dQg, dWT, dKt, dAqk, dgam,
                          d->B, d->T, d->H, d->L, nchunks(d)};
   return launched(ngdn::l0_bwd_state(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_bwd_state");

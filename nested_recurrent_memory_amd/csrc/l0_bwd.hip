@@ -28,7 +28,6 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   constexpr int NKV = V / KS;
   typedef typename Mma<E>::SFrag SF;
   __shared__ __attribute__((aligned(16))) float s_S[K * LDV];   // S rows (v contiguous)
-  __shared__ __attribute__((aligned(16))) float s_Vn[C * LDV];  // Vn rows
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -39,13 +38,7 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const size_t cix = (size_t)bh * NT + n;
 
-  {
-    const float* hT = a.hT + cix * V * K;
-    for (int e = tid; e < V * K; e += 256) s_S[(e % K) * LDV + e / K] = hT[e];
-    const float* vT = a.vnT + cix * V * C;
-    for (int e = tid; e < V * C; e += 256) s_Vn[(e % C) * LDV + e / C] = vT[e];
-  }
-  __syncthreads();
+  stage_f32(s_S, LDV, a.h + cix * K * V, V, K, V);
 
   // A fragments of this wave's 16 rows: dO (from do and mix_0), dVn, Vn
   const int ri = wv * 16 + (lane & 15);
@@ -53,6 +46,7 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   const E* dop = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V + (size_t)(t0 + rc) * H * V;
   const float m0 = ri < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + ri) * H * a.L + (size_t)h * a.L]) : 0.f;
   const float* dvn = a.dVn + cix * C * V + (size_t)ri * V;
+  const float* vnc = a.vn + cix * C * V;
   SF fo[NKV], fd[NKV], fv[NKV];
 #pragma unroll
   for (int s = 0; s < NKV; ++s) {
@@ -61,8 +55,9 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
     ld_vals<E>(dop + v0, x);
     fo[s] = Mma<E>::makes([&](int e) { return x[e] * m0; });
     fd[s] = Mma<E>::ld(dvn + v0);
-    fv[s] = Mma<E>::ld(s_Vn + ri * LDV + v0);
+    fv[s] = Mma<E>::ld(vnc + (size_t)ri * V + v0);
   }
+  __syncthreads();
   const float* dsp = a.dSp + cix * K * V;
   float* dQg = a.dQg + cix * C * K;
   float* dWT = a.dWT + cix * K * C;
@@ -88,12 +83,12 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
     }
     *reinterpret_cast<f4*>(dWT + k * C + i0) = aw;
   }
-  // dAqk = dO Vn^T, lower including the diagonal
+  // dAqk = dO Vn^T, lower including the diagonal (Vn rows from global)
   float* dAq = a.dAqk + cix * C * C;
   for (int J = 0; J < 4; ++J) {
     f4 acc = f4_zero();
     if (J <= wv) {
-      const float* vrow = s_Vn + (J * 16 + (lane & 15)) * LDV + kofs<E>(lane);
+      const float* vrow = vnc + (size_t)(J * 16 + (lane & 15)) * V + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NKV; ++s) acc = Mma<E>::mma(acc, fo[s], Mma<E>::ld(vrow + s * KS));
     }

@@ -26,15 +26,16 @@ hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream
 // A sequence of delta-rule steps per (b, h):
 //   Vn = U - A S;   S <- diag(gam) S + BT Vn
 // A [B*H,S,M,K], BT [B*H,S,K,M], U [B*H,S,M,V], gam [B*H,S,K], all fp32. The
-// state entering each step is stored (fp32): mode 0 as hT [B,H,S,V,K] (level
-// 0, chunk states), mode 1 as [B,NG,H,K,V] (upper levels, group states;
-// NG >= S, extra groups hold the final state). vnT [B,H,S,V,M] receives Vn
-// when not null.
+// state entering each step is stored (fp32) as S rows (st_kv, [K][V]) and/or
+// S^T rows (st_vk, [V][K]), each optional: mode 0 per (b, h, step) at
+// [B,H,S,...] (level 0, chunk states), mode 1 per (b, group, h) at
+// [B,NG,H,...] (upper levels, group states; NG >= S, extra groups hold the
+// final state). vnT [B,H,S,V,M] and vn [B,H,S,M,V] receive Vn when set.
 struct ScanArgs {
   const float* A; const float* BT; const float* U; const float* gam;
   const float* init; long long init_sb, init_sh;
-  float* states; int state_mode; int NG;
-  float* vnT;
+  float* st_kv; float* st_vk; int state_mode; int NG;
+  float* vnT; float* vn;
   float* fin; long long fin_sb, fin_sh;
   int B, H, S, M, V;
 };
@@ -136,13 +137,14 @@ constexpr int MAXL = 8;
 // Output of the whole op for one chunk (ops/chunk.py:250-286; ops/naive.py:376-390):
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[n / f_l]
 // Level-0 terms from the intra/scan kernels ([B,H,NT,...], fp32);
-// q [B,T,H,L,K], mix [B,T,H,L] (working dtype); upper states fp32
-// [B,NG_l,H,K,V]. o [B,T,H,V] in the working dtype. When reads is set, each
-// level's unmixed read is also written, fp32 [L,B,T,H,V].
+// q [B,T,H,L,K], mix [B,T,H,L] (working dtype); upper group states fp32, as
+// S^T rows [B,NG_l,H,V,K] (statesT, the reads) and S rows [B,NG_l,H,K,V]
+// (states, the backward's dq). o [B,T,H,V] in the working dtype. When reads
+// is set, each level's unmixed read is also written, fp32 [L,B,T,H,V].
 struct OutputArgs {
   const float* Qg; const float* Aqk; const float* hT; const float* vnT;
   const void* q; const void* mix;
-  const float* states[MAXL]; int NGl[MAXL]; int f[MAXL];
+  const float* states[MAXL]; const float* statesT[MAXL]; int NGl[MAXL]; int f[MAXL];
   void* o; float* reads;
   int B, T, H, L, NT;
   float scale;
@@ -175,11 +177,12 @@ hipError_t read_state_bwd(const ReadStateBwdArgs& a, int dtype, int K, int V, hi
 // Level-0 chunk backward, state-dependent half, per (b, h, chunk):
 //   dQg = dO S^T, dW = -dVn S^T, dKt = Vn dS'^T, dAqk = dO Vn^T (j <= i),
 //   dgam_k = sum_v dS'[k][v] S[k][v]
-// with S = h (hT), dS' the state gradient after the chunk, dO = mix_0 do.
-// Outputs (fp32) dQg, dKt [B,H,NT,64,K], dWT [B,H,NT,K,64], dAqk
-// [B,H,NT,64,64], dgam [B,H,NT,K]; dout and mix in the working dtype.
+// with S = h (rows [K][V]), Vn rows [64][V], dS' the state gradient after the
+// chunk, dO = mix_0 do. Outputs (fp32) dQg, dKt [B,H,NT,64,K], dWT
+// [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam [B,H,NT,K]; dout and mix in the
+// working dtype.
 struct L0BwdStateArgs {
-  const float* hT; const float* dSp; const float* vnT; const float* dVn;
+  const float* h; const float* dSp; const float* vn; const float* dVn;
   const void* dout; const void* mix;
   float* dQg; float* dWT; float* dKt; float* dAqk; float* dgam;
   int B, T, H, L, NT;

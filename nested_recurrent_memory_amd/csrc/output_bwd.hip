@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   for (int l = 1; l < L; ++l) {
     const int grp = n / a.f[l];
     const float* S = a.states[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * K * V;
-    stage_state_T<K, V>(s_B, LD, S);
+    stage_f32(s_B, LD, a.statesT[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * V * K, K, V, K);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();

@@ -62,16 +62,16 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   const float* Gb = a.gam + (size_t)bh * S * K;
 
   auto store_state = [&](int j) {
+    const size_t base = (a.state_mode == 0 ? (size_t)bh * S + j
+                                           : ((size_t)b * a.NG + j) * H + h) * K * V;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col(), v = v0 + vl;
-      if (a.state_mode == 0) {
-        *reinterpret_cast<f4*>(a.states + (((size_t)bh * S + j) * V + v) * K + k0) = st[i];
-      } else {
-        float* sp = a.states + (((size_t)b * a.NG + j) * H + h) * K * V;
+      if (a.st_vk) *reinterpret_cast<f4*>(a.st_vk + base + (size_t)v * K + k0) = st[i];
+      if (a.st_kv) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sp[(size_t)(k0 + r) * V + v] = st[i][r];
+        for (int r = 0; r < 4; ++r) a.st_kv[base + (size_t)(k0 + r) * V + v] = st[i][r];
       }
     }
   };
@@ -108,6 +108,11 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
         *reinterpret_cast<f4*>(s_VnT + vl * LDS_VN + m0) = vn;
         if (a.vnT)
           *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
+        if (a.vn) {
+          float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
+        }
       }
     }
     __syncthreads();
