@@ -165,6 +165,37 @@ __device__ __forceinline__ void ld_vals(const E* p, float* out) {
   }
 }
 
+// N consecutive fp32 values at p (16-byte loads when N is a multiple of 4).
+template <int N>
+__device__ __forceinline__ void ld_raw(const float* p, float* out) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int e = 0; e < N; e += 4) {
+      const f4 x = *reinterpret_cast<const f4*>(p + e);
+      out[e] = x[0]; out[e + 1] = x[1]; out[e + 2] = x[2]; out[e + 3] = x[3];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = p[e];
+  }
+}
+
+// Splits a grid of G = NB * NS blocks into (b, s), b in [0, NB), s in [0, NS),
+// so that the NS slices of one b run on the same XCD (blocks are dealt to the
+// 8 XCDs round robin, block x on XCD x % 8). Falls back to b = x / NS when
+// NB is not a multiple of 8.
+__device__ __forceinline__ void xcd_split(int x, int G, int NS, int& b, int& s) {
+  const int NB = G / NS;
+  if (NB % 8 != 0) {
+    b = x / NS;
+    s = x % NS;
+    return;
+  }
+  const int xcd = x % 8, r = x / 8;
+  b = (r / NS) * 8 + xcd;
+  s = r % NS;
+}
+
 // Row padding (elements) that keeps rows 16-byte aligned and staggers banks.
 template <typename T> constexpr int pad16() { return 16 / (int)sizeof(T); }
 

@@ -11,11 +11,13 @@
 // S' = e^g S - keys^T ((keys*b)(e^g S)) + keys^T (values*w).
 //
 // Columns of V never interact, so a workgroup owns BV = 32 of them and the
-// grid is B*H*(V/32). Per step: the state slice is written (transposed, fp32)
+// grid is B*H*(V/32), the slices of one (batch, head) placed on one XCD so
+// they share its L2. Per step: the state slice is written (transposed, fp32)
 // to LDS as the B operand of A S; Vn goes through LDS as the B operand of
-// BT Vn. A and BT fragments are read straight from global memory, each wave
-// reading the rows only it needs. Every operand is derived (fp32); for bf16
-// inputs each product is three bf16 MFMAs on split operands.
+// BT Vn. A, BT, U and gam do not depend on the state: each wave reads the
+// rows it needs one step ahead into registers, so the loads of step j+1
+// overlap step j. Every operand is derived (fp32); for bf16 inputs each
+// product is three bf16 MFMAs on split operands.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -26,25 +28,29 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
   constexpr int TPW = RTS * CT / 4;           // state tiles per wave
+  constexpr int TRT = TPW / CT;               // distinct state row tiles per wave
   constexpr int RTV = M / 16;                 // Vn row tiles
+  constexpr int RPW = (RTV + 3) / 4;          // Vn row tiles per wave (at most)
   constexpr int LDS_ST = K + 4;
   constexpr int LDS_VN = M + 4;
   constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
+  constexpr int NSK = K / KS;                 // k-steps over K
   constexpr int NSM = (M + KS - 1) / KS;      // k-steps over M
   constexpr bool PADM = (M % KS) != 0;
-  typedef typename Mma<E>::SFrag SF;
+  static_assert(TPW % CT == 0, "state tiles of a wave come in whole rows");
   __shared__ __attribute__((aligned(16))) float s_ST[BV * LDS_ST];
   __shared__ __attribute__((aligned(16))) float s_VnT[BV * LDS_VN];
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
-  const int vt = blockIdx.x % nvt;
-  const int bh = blockIdx.x / nvt;
+  int vt, bh;
+  xcd_split(blockIdx.x, gridDim.x, nvt, bh, vt);
   const int h = bh % H, b = bh / H;
   const int v0 = vt * BV;
   const int lane = lane_id(), wv = wave_id();
 
-  // state tiles of this wave: rt = g / CT, ct = g % CT
+  // state tiles of this wave: g = wv * TPW + i, rt = g / CT, ct = g % CT
   f4 st[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
@@ -61,6 +67,48 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   const float* Ub = a.U + (size_t)bh * S * M * V;
   const float* Gb = a.gam + (size_t)bh * S * K;
 
+  // Operands of one step, read a step ahead: they do not depend on the state.
+  struct Ops {
+    float a[RPW][NSK][KPL];     // A rows of this wave's Vn tiles
+    float u[RPW][CT][4];        // U at the Vn tiles
+    float bt[TRT][NSM][KPL];    // BT rows of this wave's state tiles
+    float g[TRT][4];            // gam at the state rows
+  };
+  auto load = [&](int j, Ops& o) {
+    const float* Aj = Ab + (size_t)j * M * K;
+    const float* Uj = Ub + (size_t)j * M * V;
+    const float* Bj = Bb + (size_t)j * K * M;
+    const float* Gj = Gb + (size_t)j * K;
+#pragma unroll
+    for (int p = 0; p < RPW; ++p) {
+      const int rt = wv + 4 * p;
+      if (rt < RTV) {
+        const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < NSK; ++s) ld_raw<KPL>(arow + s * KS, o.a[p][s]);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o.u[p][ct][r] = Uj[(size_t)(rt * 16 + acc_row(r)) * V + v0 + ct * 16 + acc_col()];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TRT; ++t) {
+      const int rt = (wv * TPW) / CT + t;
+      const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < NSM; ++s) {
+        if (!PADM || s * KS + kofs<E>(lane) < M) ld_raw<KPL>(brow + s * KS, o.bt[t][s]);
+        else
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) o.bt[t][s][e] = 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
+    }
+  };
+
   auto store_state = [&](int j) {
     const size_t base = (a.state_mode == 0 ? (size_t)bh * S + j
                                            : ((size_t)b * a.NG + j) * H + h) * K * V;
@@ -76,7 +124,12 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     }
   };
 
+  Ops nxt;
+  if (S > 0) load(0, nxt);
   for (int j = 0; j < S; ++j) {
+    const Ops cur = nxt;
+    if (j + 1 < S) load(j + 1, nxt);
+
     // ---- state entering step j: to global and (transposed) to LDS
     store_state(j);
 #pragma unroll
@@ -88,55 +141,49 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     __syncthreads();
 
     // ---- Vn = U - A S
-    const float* Aj = Ab + (size_t)j * M * K;
-    const float* Uj = Ub + (size_t)j * M * V;
-    for (int rt = wv; rt < RTV; rt += 4) {
-      SF af[K / KS];
-      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < K / KS; ++s) af[s] = Mma<E>::ld(arow + s * KS);
+    for (int p = 0; p < RPW; ++p) {
+      const int rt = wv + 4 * p;
+      if (rt < RTV) {
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        f4 acc = f4_zero();
-        const float* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+        for (int ct = 0; ct < CT; ++ct) {
+          f4 acc = f4_zero();
+          const float* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, af[s], Mma<E>::ld(brow + s * KS));
-        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-        f4 vn;
+          for (int s = 0; s < NSK; ++s)
+            acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.a[p][s][e]; }),
+                              Mma<E>::ld(brow + s * KS));
+          const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+          f4 vn;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[r] = Uj[(size_t)(m0 + r) * V + v0 + vl] - acc[r];
-        *reinterpret_cast<f4*>(s_VnT + vl * LDS_VN + m0) = vn;
-        if (a.vnT)
-          *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
-        if (a.vn) {
-          float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
+          for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][ct][r] - acc[r];
+          *reinterpret_cast<f4*>(s_VnT + vl * LDS_VN + m0) = vn;
+          if (a.vnT)
+            *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
+          if (a.vn) {
+            float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
+            for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
+          }
         }
       }
     }
     __syncthreads();
 
     // ---- S <- diag(gam) S + BT Vn
-    const float* Bj = Bb + (size_t)j * K * M;
-    const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int t = i / CT, ct = i % CT;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) st[i][r] *= Gj[rt * 16 + acc_row(r)];
-      const float* arow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      for (int r = 0; r < 4; ++r) st[i][r] *= cur.g[t][r];
       const float* brow = s_VnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
         // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
-        SF fa = Mma<E>::szero(), fb = fa;
-        if (live) {
-          fa = Mma<E>::ld(arow + s * KS);
-          fb = Mma<E>::ld(brow + s * KS);
-        }
-        st[i] = Mma<E>::mma(st[i], fa, fb);
+        typename Mma<E>::SFrag fb = Mma<E>::szero();
+        if (live) fb = Mma<E>::ld(brow + s * KS);
+        st[i] = Mma<E>::mma(st[i], Mma<E>::makes([&](int e) { return cur.bt[t][s][e]; }), fb);
       }
     }
     // no barrier needed here: the next writes to s_ST do not alias s_VnT, and

@@ -18,7 +18,9 @@
 //
 // Stores, per step (fp32): dS' (the gradient of the state after it) and dVn.
 // Every operand but do is derived; for bf16 inputs each product is three bf16
-// MFMAs on split operands.
+// MFMAs on split operands. As in the forward scan, the slices of one (batch,
+// head) share an XCD and each step's operands (which do not depend on the
+// state gradient) are read one step ahead into registers.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -29,21 +31,26 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int CT = BV / 16;
   constexpr int RTS = K / 16;
   constexpr int TPW = RTS * CT / 4;
+  constexpr int TRT = TPW / CT;               // distinct state row tiles per wave
   constexpr int RTV = M / 16;
+  constexpr int RPW = (RTV + 3) / 4;          // dVn row tiles per wave (at most)
   constexpr int LDS_ST = K + 4;
   constexpr int LDS_VN = M + 4;
   constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
+  constexpr int NSK = K / KS;
   constexpr int NSM = (M + KS - 1) / KS;
   constexpr bool PADM = (M % KS) != 0;
-  typedef typename Mma<E>::SFrag SF;
+  constexpr int DOE = M * BV / 256;           // dO elements staged per thread
+  static_assert(TPW % CT == 0, "state tiles of a wave come in whole rows");
   __shared__ __attribute__((aligned(16))) float s_dST[BV * LDS_ST];
   __shared__ __attribute__((aligned(16))) float s_dVnT[BV * LDS_VN];
   __shared__ __attribute__((aligned(16))) float s_dOT[BV * LDS_VN];
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
-  const int vt = blockIdx.x % nvt;
-  const int bh = blockIdx.x / nvt;
+  int vt, bh;
+  xcd_split(blockIdx.x, gridDim.x, nvt, bh, vt);
   const int h = bh % H, b = bh / H;
   const int v0 = vt * BV;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
@@ -59,20 +66,27 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       ds[i][r] = a.d_final ? a.d_final[b * a.df_sb + h * a.df_sh + (long long)k * V + v] : 0.f;
     }
   }
-  auto add_kv = [&](const float* src) {   // ds += src[K][V]
+  // values of a [K][V] fp32 array at this wave's state tiles
+  auto read_kv = [&](const float* src, f4* out) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        ds[i][r] += src[(size_t)(rt * 16 + acc_row(r)) * V + v0 + ct * 16 + acc_col()];
+        out[i][r] = src[(size_t)(rt * 16 + acc_row(r)) * V + v0 + ct * 16 + acc_col()];
     }
   };
   auto dstates = [&](int j) {
     return a.d_states + (((size_t)b * a.NG + j) * H + h) * K * V;
   };
-  if (a.d_states)
-    for (int j = a.NG - 1; j >= S; --j) add_kv(dstates(j));
+  if (a.d_states) {
+    for (int j = a.NG - 1; j >= S; --j) {
+      f4 x[TPW];
+      read_kv(dstates(j), x);
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) ds[i] += x[i];
+    }
+  }
 
   const float* Bb = a.Bop + (size_t)bh * S * M * K;
   const float* Ab = a.AT + (size_t)bh * S * K * M;
@@ -80,9 +94,83 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   const E* dob = l0 ? static_cast<const E*>(a.dout) + ((size_t)b * a.T * H + h) * V : nullptr;
   const E* mixb = l0 ? static_cast<const E*>(a.mix) + ((size_t)b * a.T * H + h) * a.L : nullptr;
 
+  // Operands of one step, read a step ahead: they do not depend on the state gradient.
+  struct Ops {
+    float bop[RPW][NSK][KPL];   // Bop rows of this wave's dVn tiles
+    float aqk[RPW][NSM][KPL];   // Aqk^T rows (level 0)
+    float at[TRT][NSM][KPL];    // A^T rows of this wave's state tiles
+    float qg[TRT][NSM][KPL];    // Qg^T rows (level 0)
+    float g[TRT][4];
+    float dov[DOE];             // mix_0 do at this thread's staging slots (level 0)
+    f4 add[TPW];                // injection (level 0) or read gradient (upper) of the step
+    bool has_add;
+  };
+  auto load = [&](int j, Ops& o) {
+    const float* Bj = Bb + (size_t)j * M * K;
+    const float* Aj = Ab + (size_t)j * K * M;
+    const float* Gj = Gb + (size_t)j * K;
+#pragma unroll
+    for (int p = 0; p < RPW; ++p) {
+      const int rt = wv + 4 * p;
+      if (rt < RTV) {
+        const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < NSK; ++s) ld_raw<KPL>(brow + s * KS, o.bop[p][s]);
+        if (l0) {
+          const float* qrow = a.AqkT + ((size_t)bh * S + j) * M * M +
+                              (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+#pragma unroll
+          for (int s = 0; s < NSM; ++s) ld_raw<KPL>(qrow + s * KS, o.aqk[p][s]);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TRT; ++t) {
+      const int rt = (wv * TPW) / CT + t;
+      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < NSM; ++s) {
+        if (!PADM || s * KS + kofs<E>(lane) < M) ld_raw<KPL>(arow + s * KS, o.at[t][s]);
+        else
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) o.at[t][s][e] = 0.f;
+      }
+      if (l0) {
+        const float* qrow = a.QgT + ((size_t)bh * S + j) * K * M +
+                            (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < NSM; ++s) ld_raw<KPL>(qrow + s * KS, o.qg[t][s]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
+    }
+    if (l0) {
+#pragma unroll
+      for (int q = 0; q < DOE; ++q) {
+        const int e = tid + q * 256, c = e / BV, vl = e % BV, t = j * M + c;
+        o.dov[q] = t < a.T ? to_f(dob[(size_t)t * H * V + v0 + vl]) * to_f(mixb[(size_t)t * H * a.L]) : 0.f;
+      }
+    }
+    // added before the step (level-0 injection) or after it (upper read gradient)
+    o.has_add = false;
+    if (a.inj && (j + 1) % a.inj_every == 0) {
+      read_kv(a.inj + ((size_t)bh * a.inj_nf + (j + 1) / a.inj_every - 1) * K * V, o.add);
+      o.has_add = true;
+    } else if (a.d_states) {
+      read_kv(dstates(j), o.add);
+      o.has_add = true;
+    }
+  };
+
+  Ops nxt;
+  if (S > 0) load(S - 1, nxt);
   for (int j = S - 1; j >= 0; --j) {
-    if (a.inj && (j + 1) % a.inj_every == 0)
-      add_kv(a.inj + ((size_t)bh * a.inj_nf + (j + 1) / a.inj_every - 1) * K * V);
+    const Ops cur = nxt;
+    if (j > 0) load(j - 1, nxt);
+    if (a.inj && cur.has_add) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
+    }
 
     // ---- store dS' and stage it (transposed) as the B operand of Bop dS'
 #pragma unroll
@@ -95,82 +183,74 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       *reinterpret_cast<f4*>(s_dST + vl * LDS_ST + k0) = ds[i];
     }
     if (l0) {
-      // dO^T for this chunk's rows and this V slice
-      for (int e = tid; e < M * BV; e += 256) {
-        const int c = e / BV, vl = e % BV, t = j * M + c;
-        float x = 0.f;
-        if (t < a.T)
-          x = to_f(dob[(size_t)t * H * V + v0 + vl]) * to_f(mixb[(size_t)t * H * a.L]);
-        s_dOT[vl * LDS_VN + c] = x;
+#pragma unroll
+      for (int q = 0; q < DOE; ++q) {
+        const int e = tid + q * 256, c = e / BV, vl = e % BV;
+        s_dOT[vl * LDS_VN + c] = cur.dov[q];
       }
     }
     __syncthreads();
 
     // ---- dVn = Bop dS' (+ Aqk^T dO)
-    const float* Bj = Bb + (size_t)j * M * K;
-    for (int rt = wv; rt < RTV; rt += 4) {
-      SF bf[K / KS];
-      const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < K / KS; ++s) bf[s] = Mma<E>::ld(brow + s * KS);
+    for (int p = 0; p < RPW; ++p) {
+      const int rt = wv + 4 * p;
+      if (rt < RTV) {
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        f4 acc = f4_zero();
-        const float* srow = s_dST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+        for (int ct = 0; ct < CT; ++ct) {
+          f4 acc = f4_zero();
+          const float* srow = s_dST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, bf[s], Mma<E>::ld(srow + s * KS));
-        if (l0) {
-          const float* qrow = a.AqkT + ((size_t)bh * S + j) * M * M +
-                              (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
-          const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+          for (int s = 0; s < NSK; ++s)
+            acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.bop[p][s][e]; }),
+                              Mma<E>::ld(srow + s * KS));
+          if (l0) {
+            const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSM; ++s)
-            acc = Mma<E>::mma(acc, Mma<E>::ld(qrow + s * KS), Mma<E>::ld(orow + s * KS));
+            for (int s = 0; s < NSM; ++s)
+              acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.aqk[p][s][e]; }),
+                                Mma<E>::ld(orow + s * KS));
+          }
+          const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+          float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
+          *reinterpret_cast<f4*>(s_dVnT + vl * LDS_VN + m0) = acc;
+          if (a.dVnT)
+            *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;
         }
-        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-        float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
-        *reinterpret_cast<f4*>(s_dVnT + vl * LDS_VN + m0) = acc;
-        if (a.dVnT)
-          *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;
       }
     }
     __syncthreads();
 
     // ---- dS = diag(gam) dS' - A^T dVn (+ Qg^T dO)
-    const float* Aj = Ab + (size_t)j * K * M;
-    const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int t = i / CT, ct = i % CT;
       f4 acc = f4_zero();
-      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
       const float* vrow = s_dVnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
-        SF fa = Mma<E>::szero(), fb = fa;
-        if (live) {
-          fa = Mma<E>::ld(arow + s * KS);
-          fb = Mma<E>::ld(vrow + s * KS);
-        }
-        acc = Mma<E>::mma(acc, fa, fb);
+        typename Mma<E>::SFrag fb = Mma<E>::szero();
+        if (live) fb = Mma<E>::ld(vrow + s * KS);
+        acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.at[t][s][e]; }), fb);
       }
       f4 qacc = f4_zero();
       if (l0) {
-        const float* qrow = a.QgT + ((size_t)bh * S + j) * K * M +
-                            (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
         const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < NSM; ++s)
-          qacc = Mma<E>::mma(qacc, Mma<E>::ld(qrow + s * KS), Mma<E>::ld(orow + s * KS));
+          qacc = Mma<E>::mma(qacc, Mma<E>::makes([&](int e) { return cur.qg[t][s][e]; }),
+                             Mma<E>::ld(orow + s * KS));
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        ds[i][r] = Gj[rt * 16 + acc_row(r)] * ds[i][r] - acc[r] + qacc[r];
+      for (int r = 0; r < 4; ++r) ds[i][r] = cur.g[t][r] * ds[i][r] - acc[r] + qacc[r];
     }
-    if (a.d_states) add_kv(dstates(j));
+    if (a.d_states && cur.has_add) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
+    }
     // s_dOT and s_dVnT are rewritten by the next step
     __syncthreads();
   }
