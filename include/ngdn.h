@@ -188,25 +188,30 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
                           float* dg, void* db, void* dw, void* stream);
 
 /* Backward of level `level`'s firings through its update and probe.
- * Sources/parameters as for ngdn_probe_fwd plus kpT [L-1,H,V,K] (key
- * projections transposed), bankT [L-1,H,K,n_max] (banks transposed), and the
- * untransposed bp, gp [L-1,H,V,K], wp [L-1,H,V,V]. states fp32 [B,ng,H,K,V]
+ * The lower level's states as rows (below_kv) and transposed (below_vk):
+ * level 1 -> h and hT from ngdn_l0_scan_fwd (NG_below = NT); level >= 2 ->
+ * the lower level's states and statesT from ngdn_upper_scan_fwd. Parameters
+ * as for ngdn_probe_fwd plus kpT [L-1,H,V,K] (key projections transposed),
+ * bankT [L-1,H,K,n_max] (banks transposed), and the untransposed bp, gp
+ * [L-1,H,V,K], wp [L-1,H,V,V]. states [B,ng,H,K,V] and statesT [B,ng,H,V,K]
  * are this level's group states; dSp, dvn from ngdn_upper_scan_bwd.
- * Workspace (fp32): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K],
- * ws_dxw, ws_dvals [B,H,NF,N,V]. dbank fp32 [L-1,H,n_max,K] accumulates. The
- * gradient of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is
- * added to d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
+ * Workspace (fp32): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K], ws_dxw,
+ * ws_dvals [B,H,NF,N,V]. dbank fp32 [L-1,H,n_max,K] accumulates. The gradient
+ * of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is added to
+ * d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const float* below, int32_t ng_below,
-                       const float* final_state, const void* query_banks,
-                       int32_t n_max, const void* key_projections,
-                       const void* bpT, const void* wpT, const void* gpT,
-                       const void* kpT, const void* bankT, const void* bp,
-                       const void* wp, const void* gp, const float* states,
-                       int32_t ng, const float* dSp, const float* dvn,
-                       float* ws_vals, float* ws_du, float* ws_dxb, float* ws_dxg,
-                       float* ws_dxw, float* ws_dvals, float* dbank, float* inj,
+                       const float* below_kv, const float* below_vk,
+                       int32_t ng_below, const float* final_state,
+                       const void* query_banks, int32_t n_max,
+                       const void* key_projections, const void* bpT,
+                       const void* wpT, const void* gpT, const void* kpT,
+                       const void* bankT, const void* bp, const void* wp,
+                       const void* gp, const float* states,
+                       const float* statesT, int32_t ng, const float* dSp,
+                       const float* dvn, float* ws_vals, float* ws_du,
+                       float* ws_dxb, float* ws_dxg, float* ws_dxw,
+                       float* ws_dvals, float* dbank, float* inj,
                        float* d_below, float* d_final, void* stream);
 
 /* Per-head parameter gradients of level `level` summed over all its firings

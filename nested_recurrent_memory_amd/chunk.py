@@ -240,15 +240,17 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         fh, fb = f[lvl], f[lvl - 1]
         if lvl == 1:
             inj, nf1 = e(B, H, nf, K, V, dt=torch.float32), nf
-            below, ngb, d_below = sv["hT"], NT, None
+            b_kv, b_vk, ngb, d_below = sv["h"], sv["hT"], NT, None
         else:
-            below, ngb, d_below = states[lvl - 1], n_groups(NT, fb), d_states[lvl - 1]
-        _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh, P(below), ngb,
-                  P(final), P(par["qb"]), par["nmax"], P(par["kp"]), P(par["bpT"]),
-                  P(par["wpT"]), P(par["gpT"]), P(par["kpT"]), P(par["bankT"]), P(par["bp"]),
-                  P(par["wp"]), P(par["gp"]), P(states[lvl]), ng, P(dSp), P(dvn),
-                  *(P(x) for x in ws), P(dqb), P(inj if lvl == 1 else None), P(d_below),
-                  P(d_final), st, tag=f"ngdn_probe_bwd.{lvl}")
+            b_kv, b_vk = states[lvl - 1], sv["statesT"][lvl - 1]
+            ngb, d_below = n_groups(NT, fb), d_states[lvl - 1]
+        _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh, P(b_kv),
+                  P(b_vk), ngb, P(final), P(par["qb"]), par["nmax"], P(par["kp"]),
+                  P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(par["kpT"]), P(par["bankT"]),
+                  P(par["bp"]), P(par["wp"]), P(par["gp"]), P(states[lvl]),
+                  P(sv["statesT"][lvl]), ng, P(dSp), P(dvn), *(P(x) for x in ws), P(dqb),
+                  P(inj if lvl == 1 else None), P(d_below), P(d_final), st,
+                  tag=f"ngdn_probe_bwd.{lvl}")
         _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf, P(ws[0]),
                   P(ws[1]), P(ws[2]), P(ws[3]), P(ws[4]), P(dkp), P(dbp), P(dwp), P(dgp), st,
                   tag=f"ngdn_param_grads.{lvl}")

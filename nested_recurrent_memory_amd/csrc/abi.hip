@@ -314,15 +314,17 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
 
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
-                       const float* below, int32_t ng_below,
-                       const float* final_state, const void* query_banks,
-                       int32_t n_max, const void* key_projections,
-                       const void* bpT, const void* wpT, const void* gpT,
-                       const void* kpT, const void* bankT, const void* bp,
-                       const void* wp, const void* gp, const float* states,
-                       int32_t ng, const float* dSp, const float* dvn,
-                       float* ws_vals, float* ws_du, float* ws_dxb, float* ws_dxg,
-                       float* ws_dxw, float* ws_dvals, float* dbank, float* inj,
+                       const float* below_kv, const float* below_vk,
+                       int32_t ng_below, const float* final_state,
+                       const void* query_banks, int32_t n_max,
+                       const void* key_projections, const void* bpT,
+                       const void* wpT, const void* gpT, const void* kpT,
+                       const void* bankT, const void* bp, const void* wp,
+                       const void* gp, const float* states,
+                       const float* statesT, int32_t ng, const float* dSp,
+                       const float* dvn, float* ws_vals, float* ws_du,
+                       float* ws_dxb, float* ws_dxg, float* ws_dxw,
+                       float* ws_dvals, float* dbank, float* inj,
                        float* d_below, float* d_final, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_bwd")) return r;
@@ -336,15 +338,17 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: bank of %d rows (a multiple of 8 >= n_queries=%d) "
                 "and its transposes are required", n_max, n_queries);
   if (f_below <= 0 || f_here <= 0) return fail(NGDN_EINVAL, "ngdn_probe_bwd: bad intervals");
-  if (!below || !final_state || !bpT || !wpT || !gpT || !bp || !wp || !gp || !states || !dSp ||
-      !dvn || !ws_vals || !ws_du || !ws_dxb || !ws_dxg || !ws_dxw || !ws_dvals)
+  if (!below_kv || !below_vk || !final_state || !bpT || !wpT || !gpT || !bp || !wp || !gp ||
+      !states || !statesT || !dSp || !dvn || !ws_vals || !ws_du || !ws_dxb || !ws_dxg ||
+      !ws_dxw || !ws_dvals)
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: NULL tensor");
   if (level == 1 ? !inj : (!d_below || !d_final))
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: lower-level gradient destination missing");
   const int NT = nchunks(d);
   const long long skv = (long long)d->K * d->V;
   ngdn::ProbeBwdArgs a{};
-  a.f.below = below; a.f.below_mode = level == 1 ? 0 : 1; a.f.NGb = ng_below;
+  a.f.below = nullptr; a.f.below_mode = level == 1 ? 0 : 1; a.f.NGb = ng_below;
+  a.below_kv = below_kv; a.below_vk = below_vk;
   a.f.below_fin = final_state + (long long)(level - 1) * skv;
   a.f.bf_sh = d->L * skv; a.f.bf_sb = d->H * a.f.bf_sh;
   a.f.f_below = f_below; a.f.f_here = f_here;
@@ -360,7 +364,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.f.B = d->B; a.f.H = d->H; a.f.NF = NT / f_here; a.f.N = N; a.f.V = d->V;
   a.kpT = lvl(kpT, hkv); a.bankT = lvl(bankT, (size_t)d->H * n_max * d->K);
   a.bp = lvl(bp, hkv); a.wp = lvl(wp, hkv); a.gp = lvl(gp, hkv);
-  a.Sg = states; a.NG = ng;
+  a.Sg = states; a.SgT = statesT; a.NG = ng;
   a.dSp = dSp; a.dvn = dvn;
   a.wsV = ws_vals; a.wsdu = ws_du; a.wsdxb = ws_dxb; a.wsdxg = ws_dxg; a.wsdxw = ws_dxw;
   a.wsdV = ws_dvals;

@@ -95,10 +95,12 @@ hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
 
 // Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
 // the autograd replay of ops/chunk.py:339-371,486-517, derived in closed
-// form). One workgroup per (batch, head, firing i). Inputs: the probe's
-// sources and parameters as for probe_fwd (plus kpT = key_proj^T [H,V,K] and
-// bankT [H,K,Nmax], original bp [H,V,K], wp [H,V,V], gp [H,V,K]); this
-// level's group states Sg fp32 [B,NG,H,K,V]; the reverse scan's dSp (fp32
+// form). One workgroup of 8 waves per (batch, head, firing i). Inputs: the
+// lower level's states as rows and transposed (below_kv / below_vk, same
+// layout modes as probe_fwd's below), the parameters as for probe_fwd (plus
+// kpT = key_proj^T [H,V,K] and bankT [H,K,Nmax], original bp [H,V,K], wp
+// [H,V,V], gp [H,V,K]); this level's group states Sg [B,NG,H,K,V] and SgT
+// [B,NG,H,V,K] (fp32); the reverse scan's dSp (fp32
 // [B,H,NF,K,V], gradient of the state after firing i) and dvn (fp32
 // [B,H,NF,N,V]). Workspace (fp32, [B,H,NF,N,*]): Vals, du, dxb,
 // dxg [N,K-or-V], dxw, dVals [N,V]; the parameter-gradient reduction reads
@@ -108,9 +110,11 @@ hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
 // / d_below_fin (fp32 [K][V] at strides, added) when the firing reads the
 // lower final state.
 struct ProbeBwdArgs {
-  ProbeArgs f;                // below/params as in the forward (f.A .. unused)
+  ProbeArgs f;                // gather indices, params as in the forward (f.below, f.A .. unused)
+  const float* below_kv;      // lower states as rows [K][V] (level 0: h, mode 0 layout)
+  const float* below_vk;      // and transposed [V][K] (level 0: hT)
   const void* kpT; const void* bankT; const void* bp; const void* wp; const void* gp;
-  const float* Sg; int NG;
+  const float* Sg; const float* SgT; int NG;   // this level's group states, rows and transposed
   const float* dSp; const float* dvn;
   float* wsV; float* wsdu; float* wsdxb; float* wsdxg; float* wsdxw; float* wsdV;
   float* dbank;

@@ -7,7 +7,7 @@
 //   dkeys = Q - P * b,   db = -P * keys,   dvals = dvn * w,   dw = dvn * vals
 //   dg_k  = sum_v dS'[k][v] s[k][v] - sum_n kb[n][k] P[n][k]
 // Probe (ops/probe.py:59-102; the reference differentiates it by autograd
-// replay, ops/chunk.py:339-371,486-517):
+// replay, ops/chunk.py:339-371,486-517), with u = Vals Wk^T:
 //   du    = (dkeys - keys <keys, dkeys>) / max(|u|, 1e-12)
 //   dxb   = db * b (1 - b),  dxw = dw * w (1 - w),
 //   dxg   = -(dg / N) * sigmoid(xg - 4)
@@ -21,20 +21,30 @@
 namespace ngdn {
 
 template <typename E, int K, int N, bool MERGE>
-__global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
+__global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   const ProbeArgs& a = ab.f;
   constexpr int V = K;
-  constexpr int LD = K + 4;                        // fp32 rows
+  constexpr int NW = 8;                             // waves
+  constexpr int LD = K + 4;                         // fp32 rows of K (= V) values
   constexpr int LDN = N + 4;
-  constexpr int NTK = (N / 16) * (K / 16) / 4;     // [N,K] (= [N,V]) tiles per wave
+  constexpr int CTK = K / 16;
+  constexpr int NTL = (N / 16) * CTK;               // [N,K] (= [N,V]) tiles
+  constexpr int TPW = (NTL + NW - 1) / NW;          // tiles per wave
+  constexpr int NTKV = CTK * CTK;                   // [K,V] tiles
+  constexpr int TPW2 = (NTKV + NW - 1) / NW;
   constexpr int KS = Mma<E>::KS;
   constexpr int NKS = K / KS;
-  constexpr int NR1 = V * (LD > LDN ? LD : LDN);
-  constexpr int RX = N > K ? N : K;
   typedef typename Mma<E>::SFrag SF;
-  __shared__ __attribute__((aligned(16))) float s_R1[NR1];     // S^T, then s^T, then dVals^T
-  __shared__ __attribute__((aligned(16))) float s_X[RX * LD];  // kb, then vn, then S_below
-  __shared__ float s_nrm[N], s_rd[N], s_gs[K], s_dg[K];
+  // LDS: region A holds Vals [N][LD], later dVals^T [V][LDN]; region B holds
+  // kb [N][LD], later vn [N][LD].
+  constexpr size_t SZ_A = sizeof(float) * (N * LD > V * LDN ? N * LD : V * LDN);
+  constexpr size_t SZ_B = sizeof(float) * N * LD;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_A + SZ_B];
+  __shared__ float s_nrm[N], s_rd[N], s_gs[K], s_dg[K], s_gam[K];
+  float* s_V = reinterpret_cast<float*>(smem);
+  float* s_dVT = s_V;
+  float* s_kb = reinterpret_cast<float*>(smem + SZ_A);
+  float* s_vn = s_kb;
 
   const int NF = a.NF, H = a.H;
   const int i = blockIdx.x % NF;
@@ -43,17 +53,17 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const size_t fo = (size_t)bh * NF + i;
 
-  // ---- the gathered lower state (as in probe_fwd)
+  // ---- the gathered lower state: rows (kv) and, when stored, transposed (vk)
   const int src = ((i + 1) * a.f_here) / a.f_below;
   const bool fin = src >= a.NGb;
-  const float* Sf = nullptr;    // [K][V]
-  const float* Sh = nullptr;    // [V][K] (level-0 chunk states)
-  if (fin) Sf = a.below_fin + b * a.bf_sb + h * a.bf_sh;
-  else if (a.below_mode == 1) Sf = a.below + (((size_t)b * a.NGb + src) * H + h) * K * V;
-  else Sh = a.below + (((size_t)b * H + h) * a.NGb + src) * V * K;
-  auto sbelow = [&](int k, int v) -> float { return Sh ? Sh[(size_t)v * K + k] : Sf[(size_t)k * V + v]; };
-
-  const float* Sj = ab.Sg + (((size_t)b * ab.NG + i) * H + h) * K * V;   // state before firing i
+  const size_t sbase = (a.below_mode == 0 ? ((size_t)b * H + h) * a.NGb + src
+                                          : ((size_t)b * a.NGb + src) * H + h) * K * V;
+  const float* Skv = fin ? a.below_fin + b * a.bf_sb + h * a.bf_sh : ab.below_kv + sbase;
+  const float* Svk = fin ? nullptr : ab.below_vk + sbase;
+  // this level's state before firing i, rows and transposed
+  const size_t jbase = (((size_t)b * ab.NG + i) * H + h) * K * V;
+  const float* Sj = ab.Sg + jbase;
+  const float* SjT = ab.SgT + jbase;
   const float* dSp = ab.dSp + fo * K * V;
   const float* dvn = ab.dvn + fo * N * V;
   float* wsV = ab.wsV + fo * N * V;
@@ -63,53 +73,83 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   float* wsdxw = ab.wsdxw + fo * N * V;
   float* wsdV = ab.wsdV + fo * N * V;
 
-  for (int e = tid; e < N; e += 256) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
-  for (int e = tid; e < K; e += 256) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
+  for (int e = tid; e < N; e += blockDim.x) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
+  for (int e = tid; e < K; e += blockDim.x) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
 
-  // ---- A. Vals
+  // tile t of this wave: g = wv + NW t over [N/16][K/16]
+  auto tile = [&](int t, int& rt, int& ct) -> bool {
+    const int g = wv + NW * t;
+    rt = g / CTK;
+    ct = g % CTK;
+    return g < NTL;
+  };
+
+  // ---- 1. Vals = Bank[:N] S (learned) or S (merge)
   if (!MERGE) {
-    if (Sh) {
-      stage_f32(s_R1, LD, Sh, K, V, K);
-    } else {
-      stage_state_T<K, V>(s_R1, LD, Sf);
-    }
-    __syncthreads();
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
-      f4 acc = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_R1 + ct * 16 * LD, LD, K);
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
+      const E* arow = bank + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+      const int v = ct * 16 + (lane & 15);
+      f4 acc = f4_zero();
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        wsV[(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = acc[r];
+      for (int s = 0; s < NKS; ++s) {
+        const int k0 = s * KS + kofs<E>(lane);
+        const SF fb = Svk ? Mma<E>::ld(Svk + (size_t)v * K + k0)
+                          : Mma<E>::makes([&](int e) { return Skv[(size_t)(k0 + e) * V + v]; });
+        acc = Mma<E>::mma(acc, Mma<E>::ld(arow + s * KS), fb);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = rt * 16 + acc_row(r), vv = ct * 16 + acc_col();
+        s_V[n * LD + vv] = acc[r];
+        wsV[n * V + vv] = acc[r];
+      }
     }
   } else {
-    for (int e = tid; e < K * V; e += 256) wsV[e] = sbelow(e / V, e % V);
+    for (int e = tid; e < K * V / 4; e += blockDim.x) {
+      const int k = e / (V / 4), v = (e % (V / 4)) * 4;
+      const f4 x = *reinterpret_cast<const f4*>(Skv + (size_t)k * V + v);
+      *reinterpret_cast<f4*>(s_V + k * LD + v) = x;
+      *reinterpret_cast<f4*>(wsV + (size_t)k * V + v) = x;
+    }
   }
   __syncthreads();
 
-  // projections of Vals: A rows from the workspace, B rows from global params
-  auto proj = [&](const void* P, int rt, int ct) -> f4 {
-    const E* Pt = static_cast<const E*>(P) + (size_t)h * K * V;
-    return mma_tile<E>(f4_zero(), wsV + rt * 16 * V, V, Pt + (size_t)ct * 16 * V, V, V);
-  };
-
-  // ---- B. decay and key norms
+  // ---- 2. the four projections of Vals, once: u = Vals Wk^T (learned),
+  // xb = Vals Bp, xw = Vals Wp, xg = Vals Gp; key norms and decay sums
+  const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V;
+  const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V;
+  const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V;
+  const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V;
+  f4 u[TPW], xb[TPW], xw[TPW], xg[TPW];
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    f4 x = proj(a.gpT, rt, ct);
-    float s = 0.f;
+  for (int t = 0; t < TPW; ++t) {
+    u[t] = xb[t] = xw[t] = xg[t] = f4_zero();
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
+    const float* arow = s_V + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
+    const size_t pr = (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s += softplusf_(x[r] - 4.f);
-    s += __shfl_xor(s, 16, WAVE);
-    s += __shfl_xor(s, 32, WAVE);
-    if (lane < 16) atomicAdd(&s_gs[ct * 16 + lane], s);
+    for (int s = 0; s < NKS; ++s) {
+      const SF fa = Mma<E>::ld(arow + s * KS);
+      if (!MERGE) u[t] = Mma<E>::mma(u[t], fa, Mma<E>::ld(kpH + pr + s * KS));
+      xb[t] = Mma<E>::mma(xb[t], fa, Mma<E>::ld(bpH + pr + s * KS));
+      xw[t] = Mma<E>::mma(xw[t], fa, Mma<E>::ld(wpH + pr + s * KS));
+      xg[t] = Mma<E>::mma(xg[t], fa, Mma<E>::ld(gpH + pr + s * KS));
+    }
+    float sg = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sg += softplusf_(xg[t][r] - 4.f);
+    sg += __shfl_xor(sg, 16, WAVE);
+    sg += __shfl_xor(sg, 32, WAVE);
+    if (lane < 16) atomicAdd(&s_gs[ct * 16 + lane], sg);
     if (!MERGE) {
-      f4 u = proj(a.kp, rt, ct);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float q = u[r] * u[r];
+        float q = u[t][r] * u[t][r];
         q += __shfl_xor(q, 1, WAVE);
         q += __shfl_xor(q, 2, WAVE);
         q += __shfl_xor(q, 4, WAVE);
@@ -119,92 +159,98 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     }
   }
   __syncthreads();
-  auto gam = [&](int k) { return expf(-s_gs[k] / (float)N); };
-  auto keyval = [&](const f4& u, int rt, int ct, int r) -> float {
+
+  auto keyval = [&](int t, int rt, int ct, int r) -> float {
     const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
     if (MERGE) return n == k ? 1.f : 0.f;
-    return u[r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
+    return u[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
   };
 
-  // ---- C. s^T into LDS, kb into LDS
-  for (int e = tid; e < K * V; e += 256) {
-    const int k = e / V, v = e % V;
-    s_R1[v * LD + k] = gam(k) * Sj[e];
-  }
+  // ---- 3. kb = keys * b into LDS; gam = e^g
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    f4 u = f4_zero();
-    if (!MERGE) u = proj(a.kp, rt, ct);
-    f4 xb = proj(a.bpT, rt, ct);
+  for (int t = 0; t < TPW; ++t) {
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      s_X[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] =
-          keyval(u, rt, ct, r) * sigmoidf_(xb[r] - 4.f);
+      s_kb[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] =
+          keyval(t, rt, ct, r) * sigmoidf_(xb[t][r] - 4.f);
   }
+  for (int e = tid; e < K; e += blockDim.x) s_gam[e] = expf(-s_gs[e] / (float)N);
   __syncthreads();
-  // vn = vals * w - kb s;  dw-side terms
-  f4 vnt[NTK], dvd[NTK];
+
+  // ---- 4. vn = Vals w - kb s with s = e^g S_j (s^T rows scaled per k);
+  // dw-side terms
+  f4 vnt[TPW], dvd[TPW];
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
-    f4 ks = mma_tile<E>(f4_zero(), s_X + rt * 16 * LD, LD, s_R1 + ct * 16 * LD, LD, K);
-    f4 xw = proj(a.wpT, rt, ct);
+  for (int t = 0; t < TPW; ++t) {
+    vnt[t] = dvd[t] = f4_zero();
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
+    const float* arow = s_kb + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
+    const float* brow = SjT + (size_t)(ct * 16 + (lane & 15)) * K + kofs<E>(lane);
+    f4 ks = f4_zero();
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int k0 = s * KS + kofs<E>(lane);
+      float x[Mma<E>::KPL];
+      ld_raw<Mma<E>::KPL>(brow + s * KS, x);
+      ks = Mma<E>::mma(ks, Mma<E>::ld(arow + s * KS),
+                       Mma<E>::makes([&](int e) { return x[e] * s_gam[k0 + e]; }));
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-      const float w = sigmoidf_(xw[r]);
-      const float val = wsV[n * V + v];
-      const float dv = dvn[n * V + v];
+      const float w = sigmoidf_(xw[t][r]);
+      const float val = s_V[n * LD + v];
+      const float dv = dvn[(size_t)n * V + v];
       vnt[t][r] = val * w - ks[r];
       dvd[t][r] = dv * w;
-      wsdxw[n * V + v] = dv * val * w * (1.f - w);
+      wsdxw[(size_t)n * V + v] = dv * val * w * (1.f - w);
     }
   }
-  __syncthreads();
+  __syncthreads();   // vn replaces kb
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+  for (int t = 0; t < TPW; ++t) {
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      s_X[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vnt[t][r];
+      s_vn[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vnt[t][r];
   }
   __syncthreads();
 
-  // ---- D. P = dvn s^T, Q = vn dS'^T; dkeys, db, the decay gradient
-  f4 dkt[NTK];
+  // ---- 5. P = dvn s^T, Q = vn dS'^T; dkeys, db, the decay gradient
+  f4 dkt[TPW];
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
+  for (int t = 0; t < TPW; ++t) {
+    dkt[t] = f4_zero();
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
     const int kc = ct * 16 + (lane & 15);
-    const float gk = gam(kc);
+    const float gk = s_gam[kc];
+    const float* drow = dvn + (size_t)(rt * 16 + (lane & 15)) * V + kofs<E>(lane);
+    const float* srow = Sj + (size_t)kc * V + kofs<E>(lane);
+    const float* vrow = s_vn + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
+    const float* qrow = dSp + (size_t)kc * V + kofs<E>(lane);
     f4 P = f4_zero(), Q = f4_zero();
-    const float* drow = dvn + (size_t)(rt * 16 + (lane & 15)) * V;
-    const float* srow = Sj + (size_t)kc * V;
-    const float* qrow = dSp + (size_t)kc * V;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      const int v0 = s * KS + kofs<E>(lane);
-      const SF fa = Mma<E>::ld(drow + v0);
-      const SF fs = Mma<E>::makes([&](int e) { return gk * srow[v0 + e]; });
-      const SF fv = Mma<E>::ld(s_X + (rt * 16 + (lane & 15)) * LD + v0);
-      const SF fq = Mma<E>::ld(qrow + v0);
-      P = Mma<E>::mma(P, fa, fs);
-      Q = Mma<E>::mma(Q, fv, fq);
+      float x[Mma<E>::KPL];
+      ld_raw<Mma<E>::KPL>(srow + s * KS, x);
+      P = Mma<E>::mma(P, Mma<E>::ld(drow + s * KS), Mma<E>::makes([&](int e) { return gk * x[e]; }));
+      Q = Mma<E>::mma(Q, Mma<E>::ld(vrow + s * KS), Mma<E>::ld(qrow + s * KS));
     }
-    f4 u = f4_zero();
-    if (!MERGE) u = proj(a.kp, rt, ct);
-    f4 xb = proj(a.bpT, rt, ct);
     float cs = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
-      const float key = keyval(u, rt, ct, r), bb = sigmoidf_(xb[r] - 4.f);
+      const float key = keyval(t, rt, ct, r), bb = sigmoidf_(xb[t][r] - 4.f);
       const float dkey = Q[r] - P[r] * bb;
       const float dbg = -P[r] * key;
       cs += key * bb * P[r];
       dkt[t][r] = dkey;
-      wsdxb[n * K + k] = dbg * bb * (1.f - bb);
+      wsdxb[(size_t)n * K + k] = dbg * bb * (1.f - bb);
       if (!MERGE) {
         float rd = key * dkey;
         rd += __shfl_xor(rd, 1, WAVE);
@@ -219,67 +265,66 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     if (lane < 16) atomicAdd(&s_dg[ct * 16 + lane], -cs);
   }
   // + sum_v dS'[k][v] s[k][v]
-  for (int k = wv; k < K; k += 4) {
-    float s = 0.f;
-    for (int v = lane; v < V; v += WAVE) s += dSp[(size_t)k * V + v] * Sj[(size_t)k * V + v];
-    s = wave_sum(s);
-    if (lane == 0) atomicAdd(&s_dg[k], gam(k) * s);
+  for (int k = wv; k < K; k += NW) {
+    float sum = 0.f;
+    for (int v = lane; v < V; v += WAVE) sum += dSp[(size_t)k * V + v] * Sj[(size_t)k * V + v];
+    sum = wave_sum(sum);
+    if (lane == 0) atomicAdd(&s_dg[k], s_gam[k] * sum);
   }
   __syncthreads();
 
-  // ---- D2. du and dxg
+  // ---- 6. du and dxg
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    f4 u = f4_zero();
-    if (!MERGE) u = proj(a.kp, rt, ct);
-    f4 xg = proj(a.gpT, rt, ct);
+  for (int t = 0; t < TPW; ++t) {
+    int rt, ct;
+    if (!tile(t, rt, ct)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
       if (!MERGE) {
         const float nr = sqrtf(s_nrm[n]);
-        const float key = u[r] / fmaxf(nr, 1e-12f);
+        const float key = u[t][r] / fmaxf(nr, 1e-12f);
         // F.normalize: below the clamp the denominator is the constant eps
         const float du = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) / nr : dkt[t][r] / 1e-12f;
-        wsdu[n * K + k] = du;
+        wsdu[(size_t)n * K + k] = du;
       }
-      wsdxg[n * K + k] = -(s_dg[k] / (float)N) * sigmoidf_(xg[r] - 4.f);
+      wsdxg[(size_t)n * K + k] = -(s_dg[k] / (float)N) * sigmoidf_(xg[t][r] - 4.f);
     }
   }
   __syncthreads();
 
-  // ---- E. dVals = dvn * w + du Wk + dxb Bp^T + dxw Wp^T + dxg Gp^T
+  // ---- 7. dVals = dvn * w + du Wk + dxb Bp^T + dxw Wp^T + dxg Gp^T
   {
     const E* kpT = static_cast<const E*>(ab.kpT) + (size_t)h * V * K;
     const E* bp = static_cast<const E*>(ab.bp) + (size_t)h * V * K;
     const E* wp = static_cast<const E*>(ab.wp) + (size_t)h * V * V;
     const E* gp = static_cast<const E*>(ab.gp) + (size_t)h * V * K;
-    float* s_dVT = s_R1;   // [V][LDN]
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
+      const size_t ar = (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+      const size_t br = (size_t)(ct * 16 + (lane & 15)) * K + kofs<E>(lane);
       f4 acc = dvd[t];
-      if (!MERGE) acc = mma_tile<E>(acc, wsdu + rt * 16 * K, K, kpT + (size_t)ct * 16 * K, K, K);
-      acc = mma_tile<E>(acc, wsdxb + rt * 16 * K, K, bp + (size_t)ct * 16 * K, K, K);
-      acc = mma_tile<E>(acc, wsdxw + rt * 16 * V, V, wp + (size_t)ct * 16 * V, V, V);
-      acc = mma_tile<E>(acc, wsdxg + rt * 16 * K, K, gp + (size_t)ct * 16 * K, K, K);
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        if (!MERGE) acc = Mma<E>::mma(acc, Mma<E>::ld(wsdu + ar + s * KS), Mma<E>::ld(kpT + br + s * KS));
+        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxb + ar + s * KS), Mma<E>::ld(bp + br + s * KS));
+        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxw + ar + s * KS), Mma<E>::ld(wp + br + s * KS));
+        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxg + ar + s * KS), Mma<E>::ld(gp + br + s * KS));
+      }
       dvd[t] = acc;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        wsdV[n * V + v] = acc[r];
-        s_dVT[v * LDN + n] = acc[r];
+        wsdV[(size_t)n * V + v] = acc[r];
+        if (!MERGE) s_dVT[v * LDN + n] = acc[r];
       }
-    }
-    if (!MERGE) {
-      // S_below rows k (v contiguous) for dBank
-      for (int e = tid; e < K * V; e += 256) s_X[(e / V) * LD + e % V] = sbelow(e / V, e % V);
     }
   }
   __syncthreads();
 
-  // ---- F. dS_below and dBank
+  // ---- 8. dS_below and dBank
   auto scatter = [&](int k, int v, float x) {
     if (a.f_below == 1 && a.below_mode == 0) {
       ab.inj[fo * K * V + (size_t)k * V + v] = x;
@@ -291,21 +336,24 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
   };
   if (MERGE) {
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) scatter(rt * 16 + acc_row(r), ct * 16 + acc_col(), dvd[t][r]);
     }
   } else {
+    // dS_below[k][v] = sum_n Bank[n][k] dVals[n][v]
     const E* bankT = static_cast<const E*>(ab.bankT) + (size_t)h * K * a.Nmax;
-    const float* s_dVT = s_R1;
-    constexpr int NTKV = (K / 16) * (V / 16) / 4;
-    for (int t = 0; t < NTKV; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+    constexpr int NSN = (N + KS - 1) / KS;
+#pragma unroll
+    for (int t = 0; t < TPW2; ++t) {
+      const int g = wv + NW * t;
+      if (g >= NTKV) continue;
+      const int rt = g / CTK, ct = g % CTK;
       f4 acc = f4_zero();
       const E* arow = bankT + (size_t)(rt * 16 + (lane & 15)) * a.Nmax + kofs<E>(lane);
       const float* brow = s_dVT + (ct * 16 + (lane & 15)) * LDN + kofs<E>(lane);
-      constexpr int NSN = (N + KS - 1) / KS;
 #pragma unroll
       for (int s = 0; s < NSN; ++s) {
         const bool live = s * KS + kofs<E>(lane) < N;
@@ -323,9 +371,14 @@ __global__ __launch_bounds__(256) void probe_bwd_kernel(ProbeBwdArgs ab) {
     // dBank[n][k] += sum_v dVals[n][v] S_below[k][v]
     float* dbank = ab.dbank + (size_t)h * a.Nmax * K;
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-      f4 acc = mma_tile<E>(f4_zero(), wsdV + rt * 16 * V, V, s_X + ct * 16 * LD, LD, V);
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
+      const float* arow = wsdV + (size_t)(rt * 16 + (lane & 15)) * V + kofs<E>(lane);
+      const float* brow = Skv + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
+      f4 acc = f4_zero();
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) acc = Mma<E>::mma(acc, Mma<E>::ld(arow + s * KS), Mma<E>::ld(brow + s * KS));
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()], acc[r]);
@@ -390,7 +443,7 @@ template <typename E, int K, int N, bool MERGE>
 static hipError_t launch_probe_bwd(const ProbeBwdArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.f.B * a.f.H * a.f.NF);
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((probe_bwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((probe_bwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
