@@ -70,34 +70,6 @@ struct ChunkIn {
 constexpr int GCP = 1;   // padding of gc rows
 constexpr int AT_LD = CH + 1;
 
-// Copies nrows x ncols elements of a row-major global array (row stride
-// `stride` elements) into LDS rows of stride ld, with 16-byte accesses; rows
-// at or past `nvalid` are zero. ncols, ld and stride are multiples of 16 B.
-template <typename E>
-__device__ __forceinline__ void stage_rows(E* dst, int ld, const E* src, size_t stride,
-                                           int nrows, int ncols, int nvalid) {
-  constexpr int VE = 16 / sizeof(E);
-  typedef __attribute__((__vector_size__(16))) int v4i;
-  const int segs = ncols / VE;
-  for (int e = threadIdx.x; e < nrows * segs; e += blockDim.x) {
-    const int i = e / segs, c = (e % segs) * VE;
-    v4i x = {0, 0, 0, 0};
-    if (i < nvalid) x = *reinterpret_cast<const v4i*>(src + (size_t)i * stride + c);
-    *reinterpret_cast<v4i*>(dst + i * ld + c) = x;
-  }
-}
-
-// k, b and q rows of one chunk held in LDS (stride K + 8), zero past the end;
-// the same element interface as ChunkIn.
-template <typename E, int K>
-struct ChunkLds {
-  const E* k; const E* b; const E* q;
-  float scale;
-  static constexpr int LD = K + 8;
-  __device__ __forceinline__ float K_(int i, int c) const { return to_f(k[i * LD + c]); }
-  __device__ __forceinline__ float B_(int i, int c) const { return to_f(b[i * LD + c]); }
-  __device__ __forceinline__ float Q_(int i, int c) const { return to_f(q[i * LD + c]); }
-};
 
 // gc[i][c] = sum_{s<=i} g_s[c0 + c] within the chunk (zero past the end) for
 // the NC columns from c0, into dst [64][LDG]; glast (when set) receives row

@@ -196,6 +196,42 @@ __device__ __forceinline__ void xcd_split(int x, int G, int NS, int& b, int& s) 
   s = r % NS;
 }
 
+// Copies nrows x ncols elements of a row-major global array (row stride
+// `stride` elements) into LDS rows of stride ld, with 16-byte accesses; rows
+// at or past `nvalid` are zero. ncols, ld and stride are multiples of 16 B.
+template <typename E>
+__device__ __forceinline__ void stage_rows(E* dst, int ld, const E* src, size_t stride,
+                                           int nrows, int ncols, int nvalid) {
+  constexpr int VE = 16 / sizeof(E);
+  typedef __attribute__((__vector_size__(16))) int v4i;
+  const int segs = ncols / VE;
+  for (int e = threadIdx.x; e < nrows * segs; e += blockDim.x) {
+    const int i = e / segs, c = (e % segs) * VE;
+    v4i x = {0, 0, 0, 0};
+    if (i < nvalid) x = *reinterpret_cast<const v4i*>(src + (size_t)i * stride + c);
+    *reinterpret_cast<v4i*>(dst + i * ld + c) = x;
+  }
+}
+
+// Fragments gathered down a column: KPL consecutive rows of column 0 at p
+// (row stride ld), for operands whose reduction index runs along the rows of
+// a row-major array staged in LDS. Exact (E) or derived (fp32) storage.
+template <typename E>
+__device__ __forceinline__ typename Mma<E>::Frag gather_x(const E* p, int ld) {
+  if constexpr (std::is_same<E, float>::value) {
+    return p[0];
+  } else {
+    typename Mma<E>::Frag r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = p[e * ld];
+    return r;
+  }
+}
+template <typename E>
+__device__ __forceinline__ typename Mma<E>::SFrag gather_s(const float* p, int ld) {
+  return Mma<E>::makes([&](int e) { return p[e * ld]; });
+}
+
 // Row padding (elements) that keeps rows 16-byte aligned and staggers banks.
 template <typename T> constexpr int pad16() { return 16 / (int)sizeof(T); }
 

@@ -132,54 +132,66 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a) {
   constexpr int C = CH;
-  constexpr int LDQ = C + 8;     // exact q^T rows
-  constexpr int LDD = C + 4;     // fp32 (mix do)^T rows
-  constexpr int TPW = (K / 16) * (V / 16) / 4;
-  __shared__ __attribute__((aligned(16))) E s_qT[K * LDQ];
-  __shared__ __attribute__((aligned(16))) float s_dT[V * LDD];
+  constexpr int LDQ = K + 16 / (int)sizeof(E);   // staged q rows (exact)
+  constexpr int LDD = V + 16 / (int)sizeof(E);   // staged do rows (exact)
+  constexpr int KT = K / 16, VT = V / 16;
+  constexpr int KTW = KT / 4;                   // k-tiles per wave (all v-tiles each)
+  constexpr int KS = Mma<E>::KS;
+  static_assert(KT % 4 == 0, "K must split over the 4 waves");
+  __shared__ __attribute__((aligned(16))) E s_q[C * LDQ];
+  __shared__ __attribute__((aligned(16))) E s_do[C * LDD];
+  __shared__ float s_mix[C];
 
   const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
   const int j = blockIdx.x % NG;
   const int bh = blockIdx.x / NG;
   const int h = bh % H, b = bh / H;
-  const int wv = wave_id(), tid = threadIdx.x;
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const int NT = (T + C - 1) / C;
+  const size_t rowQ = (size_t)H * L * K, rowV = (size_t)H * V;
   const E* qb = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K + (size_t)l * K;
   const E* mb = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L + l;
   const E* db = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V;
 
-  f4 acc[TPW];
+  // dS[k][v] = sum_t q[t][k] (mix[t] do[t][v]): the reduction runs down the
+  // staged rows; fragments are gathered down columns
+  f4 acc[KTW][VT];
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) acc[i] = f4_zero();
+  for (int x = 0; x < KTW; ++x)
+#pragma unroll
+    for (int y = 0; y < VT; ++y) acc[x][y] = f4_zero();
   const int n1 = min((j + 1) * a.f, NT);
   for (int n = j * a.f; n < n1; ++n) {
-    const int t0 = n * C;
-    for (int e = tid; e < C * K; e += 256) {
-      const int c = e / K, k = e % K, t = t0 + c;
-      s_qT[k * LDQ + c] = t < T ? qb[(size_t)t * H * L * K + k] : from_f<E>(0.f);
-    }
-    for (int e = tid; e < C * V; e += 256) {
-      const int c = e / V, v = e % V, t = t0 + c;
-      float x = 0.f;
-      if (t < T) x = to_f(db[(size_t)t * H * V + v]) * to_f(mb[(size_t)t * H * L]);
-      s_dT[v * LDD + c] = x;
-    }
+    const int t0 = n * C, nv = min(C, T - t0);
+    stage_rows<E>(s_q, LDQ, qb + (size_t)t0 * rowQ, rowQ, C, K, nv);
+    stage_rows<E>(s_do, LDD, db + (size_t)t0 * rowV, rowV, C, V, nv);
+    if (tid < C) s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int g = wv * TPW + i, rt = g / (V / 16), ct = g % (V / 16);
-      acc[i] = mma_tile<E>(acc[i], s_qT + rt * 16 * LDQ, LDQ, s_dT + ct * 16 * LDD, LDD, C);
+    for (int s = 0; s < C / KS; ++s) {
+      const int r0 = s * KS + kofs<E>(lane);
+      typename Mma<E>::Frag fa[KTW];
+#pragma unroll
+      for (int x = 0; x < KTW; ++x)
+        fa[x] = gather_x<E>(s_q + r0 * LDQ + (wv * KTW + x) * 16 + (lane & 15), LDQ);
+#pragma unroll
+      for (int y = 0; y < VT; ++y) {
+        const E* pd = s_do + r0 * LDD + y * 16 + (lane & 15);
+        const auto fb = Mma<E>::makes([&](int e) { return to_f(pd[e * LDD]) * s_mix[r0 + e]; });
+#pragma unroll
+        for (int x = 0; x < KTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
+      }
     }
     __syncthreads();
   }
   float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int g = wv * TPW + i, rt = g / (V / 16), ct = g % (V / 16);
+  for (int x = 0; x < KTW; ++x)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      out[(size_t)(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = acc[i][r] * a.scale;
-  }
+    for (int y = 0; y < VT; ++y)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        out[(size_t)((wv * KTW + x) * 16 + acc_row(r)) * V + y * 16 + acc_col()] = acc[x][y][r] * a.scale;
 }
 
 template <typename E, int K, int V>

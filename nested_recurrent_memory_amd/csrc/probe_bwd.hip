@@ -390,53 +390,71 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 
 template <typename E, int X, int Y>
 __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
-  constexpr int LDM = 32 + 4;
-  constexpr int TPW = (X / 16) * (Y / 16) / 4;
-  __shared__ __attribute__((aligned(16))) float s_AT[X * LDM];
-  __shared__ __attribute__((aligned(16))) float s_BT[Y * LDM];
+  constexpr int R = 32;                      // rows per staged slab
+  constexpr int LDA = X + 4, LDB = Y + 4;
+  constexpr int XT = X / 16, YT = Y / 16;
+  constexpr int XTW = XT / 4;                // x-tiles per wave (all y-tiles each)
+  constexpr int KS = Mma<E>::KS;
+  static_assert(XT % 4 == 0, "X must split over the 4 waves");
+  __shared__ __attribute__((aligned(16))) float s_A[R * LDA];
+  __shared__ __attribute__((aligned(16))) float s_B[R * LDB];
   const int H = a.H, NF = a.NF, N = a.N;
   const int part = blockIdx.x % a.split;
   const int h = blockIdx.x / a.split;
-  const int wv = wave_id(), tid = threadIdx.x;
+  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const int items = a.B * NF;
   const int per = (items + a.split - 1) / a.split;
   const int it0 = part * per, it1 = min(items, it0 + per);
-  f4 acc[TPW];
+  if (it0 >= it1) return;
+  f4 acc[XTW][YT];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) acc[t] = f4_zero();
+  for (int x = 0; x < XTW; ++x)
+#pragma unroll
+    for (int y = 0; y < YT; ++y) acc[x][y] = f4_zero();
   for (int it = it0; it < it1; ++it) {
     const int b = it / NF, i = it % NF;
     const size_t base = (((size_t)b * H + h) * NF + i) * N;
-    const float* Ap = a.A + base * X;
-    const float* Bp = a.Bm + base * Y;
-    for (int n0 = 0; n0 < N; n0 += 32) {
-      // 32 rows of the reduction, transposed into LDS (zero past N)
-      for (int e = tid; e < 32 * X; e += 256) {
-        const int n = e / X, x = e % X;
-        s_AT[x * LDM + n] = n0 + n < N ? Ap[(size_t)(n0 + n) * X + x] : 0.f;
+    for (int n0 = 0; n0 < N; n0 += R) {
+      const int nr = min(R, N - n0);
+      // rows of the reduction, zero past N
+      for (int e = tid; e < R * X / 4; e += 256) {
+        const int r = e / (X / 4), c = (e % (X / 4)) * 4;
+        f4 v = f4_zero();
+        if (r < nr) v = *reinterpret_cast<const f4*>(a.A + (base + n0 + r) * X + c);
+        *reinterpret_cast<f4*>(s_A + r * LDA + c) = v;
       }
-      for (int e = tid; e < 32 * Y; e += 256) {
-        const int n = e / Y, y = e % Y;
-        s_BT[y * LDM + n] = n0 + n < N ? Bp[(size_t)(n0 + n) * Y + y] : 0.f;
+      for (int e = tid; e < R * Y / 4; e += 256) {
+        const int r = e / (Y / 4), c = (e % (Y / 4)) * 4;
+        f4 v = f4_zero();
+        if (r < nr) v = *reinterpret_cast<const f4*>(a.Bm + (base + n0 + r) * Y + c);
+        *reinterpret_cast<f4*>(s_B + r * LDB + c) = v;
       }
       __syncthreads();
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int g = wv * TPW + t, rt = g / (Y / 16), ct = g % (Y / 16);
-        acc[t] = mma_tile<E>(acc[t], s_AT + rt * 16 * LDM, LDM, s_BT + ct * 16 * LDM, LDM, 32);
+      for (int s = 0; s < R / KS; ++s) {
+        const int r0 = s * KS + kofs<E>(lane);
+        typename Mma<E>::SFrag fa[XTW];
+#pragma unroll
+        for (int x = 0; x < XTW; ++x)
+          fa[x] = gather_s<E>(s_A + r0 * LDA + (wv * XTW + x) * 16 + (lane & 15), LDA);
+#pragma unroll
+        for (int y = 0; y < YT; ++y) {
+          const auto fb = gather_s<E>(s_B + r0 * LDB + y * 16 + (lane & 15), LDB);
+#pragma unroll
+          for (int x = 0; x < XTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
+        }
       }
       __syncthreads();
     }
   }
-  if (it0 >= it1) return;
   float* C = a.C + (size_t)h * X * Y;
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int g = wv * TPW + t, rt = g / (Y / 16), ct = g % (Y / 16);
+  for (int x = 0; x < XTW; ++x)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      atomicAdd(&C[(rt * 16 + acc_row(r)) * Y + ct * 16 + acc_col()], acc[t][r]);
-  }
+    for (int y = 0; y < YT; ++y)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        atomicAdd(&C[((wv * XTW + x) * 16 + acc_row(r)) * Y + y * 16 + acc_col()], acc[x][y][r]);
 }
 
 template <typename E, int K, int N, bool MERGE>
