@@ -27,8 +27,8 @@ __global__ __launch_bounds__(256) void output_bwd_kernel(OutputBwdArgs ab) {
   __shared__ __attribute__((aligned(16))) float s_B[ROWS * LDM];
 
   const int NT = a.NT, H = a.H, T = a.T, L = a.L;
-  const int n = blockIdx.x % NT;
-  const int bh = blockIdx.x / NT;
+  int n, bh;   // all chunks of one (batch, head) on one XCD: groups share states in its L2
+  xcd_split(blockIdx.x, gridDim.x, NT, bh, n);
   const int h = bh % H, b = bh / H;
   const int t0 = n * C;
   const int nvalid = min(C, T - t0);
