@@ -23,6 +23,10 @@ struct L0IntraArgs {
 };
 hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
+// Columns of V per scan workgroup (each step's operands are read by V / 32
+// workgroups of one (batch, head)).
+constexpr int SCAN_BV = 32;
+
 // A sequence of delta-rule steps per (b, h):
 //   Vn = U - A S;   S <- diag(gam) S + BT Vn
 // A [B*H,S,M,K], BT [B*H,S,K,M], U [B*H,S,M,V], gam [B*H,S,K], all fp32. The

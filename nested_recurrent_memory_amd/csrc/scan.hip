@@ -10,8 +10,8 @@
 // A = keys * b * e^g, BT = keys^T, U = values * w, gam = e^g, which is
 // S' = e^g S - keys^T ((keys*b)(e^g S)) + keys^T (values*w).
 //
-// Columns of V never interact, so a workgroup owns BV = 32 of them and the
-// grid is B*H*(V/32), the slices of one (batch, head) placed on one XCD so
+// Columns of V never interact, so a workgroup owns BV = SCAN_BV of them and
+// the grid is B*H*(V/BV), the slices of one (batch, head) placed on one XCD so
 // they share its L2. Per step: the state slice is written (transposed, fp32)
 // to LDS as the B operand of A S; Vn goes through LDS as the B operand of
 // BT Vn. A, BT, U and gam do not depend on the state: each wave reads the
@@ -24,7 +24,7 @@ namespace ngdn {
 
 template <typename E, int K, int M>
 __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
-  constexpr int BV = 32;
+  constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
   constexpr int TPW = RTS * CT / 4;           // state tiles per wave
@@ -205,13 +205,13 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
 
 template <typename E, int K, int M>
 static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * (a.V / 32));
+  const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
   hipLaunchKernelGGL((scan_fwd_kernel<E, K, M>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st) {
-  if (a.V % 32 != 0) return hipErrorInvalidValue;
+  if (a.V % SCAN_BV != 0) return hipErrorInvalidValue;
 #define NGDN_SC(E, KK, MM) \
   if (K == KK && a.M == MM) return launch_scan<E, KK, MM>(a, st);
 #define NGDN_SC_K(E, KK) NGDN_SC(E, KK, 16) NGDN_SC(E, KK, 32) NGDN_SC(E, KK, 64) NGDN_SC(E, KK, 128)

@@ -27,7 +27,7 @@ namespace ngdn {
 
 template <typename E, int K, int M>
 __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
-  constexpr int BV = 32;
+  constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;
   constexpr int RTS = K / 16;
   constexpr int TPW = RTS * CT / 4;
@@ -269,13 +269,13 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 
 template <typename E, int K, int M>
 static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * (a.V / 32));
+  const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
   hipLaunchKernelGGL((scan_bwd_kernel<E, K, M>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st) {
-  if (a.V % 32 != 0) return hipErrorInvalidValue;
+  if (a.V % SCAN_BV != 0) return hipErrorInvalidValue;
   if (a.QgT && a.M != CH) return hipErrorInvalidValue;
 #define NGDN_SB(E, KK, MM) \
   if (K == KK && a.M == MM) return launch_scan_bwd<E, KK, MM>(a, st);
