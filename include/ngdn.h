@@ -112,34 +112,35 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
  * o = mix_0 (Qg h + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[group].
  * statesT[l] (l = 1..L-1) is level l's transposed group states
  * [B,ng[l],H,V,K] (from ngdn_upper_scan_fwd) with firing interval f[l];
- * entries at l = 0 are ignored. o [B,T,H,V] in the working dtype. reads, when
- * not NULL, receives each level's unmixed read, fp32 [L,B,T,H,V]. */
+ * entries at l = 0 are ignored. o [B,T,H,V] in the working dtype. read0, when
+ * not NULL, receives level 0's unmixed read Qg h + Aqk Vn, fp32 [B,T,H,V]
+ * (the backward's dmix_0). */
 int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* statesT,
                         const int32_t* ng, const int32_t* f, void* o,
-                        float* reads, void* stream);
+                        float* read0, void* stream);
 
 /* ---------------------------------------------------------------- backward
  * The backward of ChunkNestedGDN2Function (ops/chunk.py:650-719,
  * chunk_nested_gdn2_bwd :374-564), one entry point per stage. */
 
-/* Output backward per chunk (ops/chunk.py:423-449): dmix for every level
- * (fp32 [B,T,H,L]) and dq[..., l, :] for l >= 1 (working dtype [B,T,H,L,K]);
- * inputs as for ngdn_output_fwd plus the untransposed group states
- * states[l] [B,ng[l],H,K,V] and do [B,T,H,V]. */
-int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
-                        const float* hT, const float* vnT, const void* q,
-                        const void* mix, const float* const* states,
-                        const float* const* statesT, const int32_t* ng,
-                        const int32_t* f, const void* dout, void* dq,
+/* dmix for level 0 (ops/chunk.py:423): dmix[..., 0] = <do, read0> per token,
+ * read0 fp32 [B,T,H,V] from ngdn_output_fwd, do [B,T,H,V]; dmix fp32
+ * [B,T,H,L] (level-0 column written). */
+int32_t ngdn_output_bwd(const ngdn_dims* d, const float* read0, const void* dout,
                         float* dmix, void* stream);
 
-/* Read gradient of level `level`'s group states (read_level_bwd,
- * ops/chunk.py:307-336): d_states fp32 [B,ng,H,K,V], written. */
+/* Backward of level `level`'s reads (read_level_bwd, ops/chunk.py:307-336,
+ * and the dq / dmix terms of :423-449), per group of f chunks: states
+ * [B,ng,H,K,V] fp32 are the level's group states. Writes d_states fp32
+ * [B,ng,H,K,V], dq[..., level, :] (working dtype [B,T,H,L,K]) and
+ * dmix[..., level] (fp32 [B,T,H,L]). */
 int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
                             int32_t ng, const void* q, const void* mix,
-                            const void* dout, float* d_states, void* stream);
+                            const void* dout, const float* states,
+                            float* d_states, void* dq, float* dmix,
+                            void* stream);
 
 /* Reverse level-0 state recurrence (the vendored fla dh kernel with dh_ext,
  * ops/_vendor/common_chunk_delta_h.py:25-380). Kt [B,H,NT,64,K],

@@ -40,8 +40,8 @@ SIGNATURES = {
                       + [P] * 11 + [P],
     "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
     "ngdn_output_fwd": [PD, P, P, P, P, P, P, P, P, P, P, P, P],
-    "ngdn_output_bwd": [PD] + [P] * 10 + [P, P, P] + [P],
-    "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P],
+    "ngdn_output_bwd": [PD, P, P, P, P],
+    "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, P],
     "ngdn_upper_scan_bwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
     "ngdn_l0_bwd_state": [PD] + [P] * 6 + [P] * 5 + [P],

@@ -142,14 +142,16 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         levels[lvl] = dict(N=N, nf=nf, ng=ng, keys=keysN, AT=AT_, gam=gm_)
 
     o = e(B, T, H, V)
+    read0 = f32(B, T, H, V) if train else None
     spT, ngs, fs = _level_arrays(statesT, NT, f, L)
     _lib.call("ngdn_output_fwd", ctypes.byref(d), P(Qg), P(Aqk), P(hT), P(vnT), P(q_),
-              P(mix_), spT, ngs, fs, P(o), None, st)
+              P(mix_), spT, ngs, fs, P(o), P(read0), st)
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
                      KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
-                     hT=hT, vnT=vnT, h=h_, vn=vn_, states=states, statesT=statesT,
+                     hT=hT, vnT=vnT, h=h_, vn=vn_, read0=read0, states=states,
+                     statesT=statesT,
                      levels=levels, final=final, par=par,
                      code=code, wd=wd)
     return o, final, saved
@@ -199,13 +201,11 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     merge = promotion == "merge"
     states, levels, par, final = sv["states"], sv["levels"], sv["par"], sv["final"]
 
-    # reads: dmix for every level, dq for levels >= 1
+    # reads: dmix for every level (level 0 from the stored read), dq and the
+    # group-state gradients for levels >= 1
     dq = e(B, T, H, L, K)
     dmix = e(B, T, H, L, dt=torch.float32)
-    sp, ngs, fs = _level_arrays(states, NT, f, L)
-    spT, _, _ = _level_arrays(sv["statesT"], NT, f, L)
-    _lib.call("ngdn_output_bwd", ctypes.byref(d), P(sv["Qg"]), P(sv["Aqk"]), P(sv["hT"]),
-              P(sv["vnT"]), P(q_), P(mix_), sp, spT, ngs, fs, P(do_), P(dq), P(dmix), st)
+    _lib.call("ngdn_output_bwd", ctypes.byref(d), P(sv["read0"]), P(do_), P(dmix), st)
 
     d_final = (dfinal.to(torch.float32).contiguous().clone() if dfinal is not None
                else z32(B, H, L, K, V))
@@ -215,7 +215,8 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         ng = n_groups(NT, f[lvl])
         d_states[lvl] = e(B, ng, H, K, V, dt=torch.float32)
         _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng, P(q_), P(mix_),
-                  P(do_), P(d_states[lvl]), st, tag=f"ngdn_read_state_bwd.{lvl}")
+                  P(do_), P(states[lvl]), P(d_states[lvl]), P(dq), P(dmix), st,
+                  tag=f"ngdn_read_state_bwd.{lvl}")
 
     dqb = dkp = dbp = dwp = dgp = None
     inj, nf1 = None, 0

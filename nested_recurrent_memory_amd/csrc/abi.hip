@@ -165,7 +165,7 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* statesT,
                         const int32_t* ng, const int32_t* f, void* o,
-                        float* reads, void* stream) {
+                        float* read0, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_output_fwd")) return r;
   if (d->K != d->V)
@@ -179,47 +179,36 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
       return fail(NGDN_EINVAL, "ngdn_output_fwd: level %d states missing", l);
     a.statesT[l] = statesT[l]; a.NGl[l] = ng[l]; a.f[l] = f[l];
   }
-  a.o = o; a.reads = reads;
+  a.o = o; a.read0 = read0;
   a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
   return launched(ngdn::output_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream), "ngdn_output_fwd");
 }
 
 
-int32_t ngdn_output_bwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
-                        const float* hT, const float* vnT, const void* q,
-                        const void* mix, const float* const* states,
-                        const float* const* statesT, const int32_t* ng,
-                        const int32_t* f, const void* dout, void* dq,
+int32_t ngdn_output_bwd(const ngdn_dims* d, const float* read0, const void* dout,
                         float* dmix, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_output_bwd")) return r;
-  if (d->K != d->V)
-    return fail(NGDN_EINVAL, "ngdn_output_bwd: K == V required, got %d, %d", d->K, d->V);
-  if (!Qg || !Aqk || !hT || !vnT || !q || !mix || !dout || !dq || !dmix)
-    return fail(NGDN_EINVAL, "ngdn_output_bwd: NULL tensor");
-  ngdn::OutputBwdArgs a{};
-  a.f.Qg = Qg; a.f.Aqk = Aqk; a.f.hT = hT; a.f.vnT = vnT; a.f.q = q; a.f.mix = mix;
-  for (int l = 1; l < d->L; ++l) {
-    if (!states || !states[l] || !statesT || !statesT[l] || !ng || !f || f[l] <= 0)
-      return fail(NGDN_EINVAL, "ngdn_output_bwd: level %d states missing", l);
-    a.f.states[l] = states[l]; a.f.statesT[l] = statesT[l]; a.f.NGl[l] = ng[l]; a.f.f[l] = f[l];
-  }
-  a.f.B = d->B; a.f.T = d->T; a.f.H = d->H; a.f.L = d->L; a.f.NT = nchunks(d); a.f.scale = d->scale;
-  a.dout = dout; a.dq = dq; a.dmix = dmix;
-  return launched(ngdn::output_bwd(a, d->dtype, d->K, d->V, (hipStream_t)stream), "ngdn_output_bwd");
+  if (!read0 || !dout || !dmix) return fail(NGDN_EINVAL, "ngdn_output_bwd: NULL tensor");
+  ngdn::Dmix0Args a{read0, dout, dmix, d->B, d->T, d->H, d->L, d->V};
+  return launched(ngdn::dmix0_bwd(a, d->dtype, (hipStream_t)stream), "ngdn_output_bwd");
 }
 
 int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
                             int32_t ng, const void* q, const void* mix,
-                            const void* dout, float* d_states, void* stream) {
+                            const void* dout, const float* states,
+                            float* d_states, void* dq, float* dmix,
+                            void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_read_state_bwd")) return r;
   if (level < 1 || level >= d->L || f <= 0 || ng != (nchunks(d) + f - 1) / f)
     return fail(NGDN_EINVAL, "ngdn_read_state_bwd: level %d / interval %d / groups %d inconsistent",
                 level, f, ng);
   if (d->K != d->V) return fail(NGDN_EINVAL, "ngdn_read_state_bwd: K == V required");
-  if (!q || !mix || !dout || !d_states) return fail(NGDN_EINVAL, "ngdn_read_state_bwd: NULL tensor");
-  ngdn::ReadStateBwdArgs a{q, mix, dout, d_states, d->B, d->T, d->H, d->L, level, f, ng, d->scale};
+  if (!q || !mix || !dout || !states || !d_states || !dq || !dmix)
+    return fail(NGDN_EINVAL, "ngdn_read_state_bwd: NULL tensor");
+  ngdn::ReadStateBwdArgs a{q, mix, dout, states, d_states, dq, dmix,
+                           d->B, d->T, d->H, d->L, level, f, ng, d->scale};
   return launched(ngdn::read_state_bwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_read_state_bwd");
 }

@@ -146,37 +146,39 @@ constexpr int MAXL = 8;
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[n / f_l]
 // Level-0 terms from the intra/scan kernels ([B,H,NT,...], fp32);
 // q [B,T,H,L,K], mix [B,T,H,L] (working dtype); upper group states fp32, as
-// S^T rows [B,NG_l,H,V,K] (statesT, the reads) and S rows [B,NG_l,H,K,V]
-// (states, the backward's dq). o [B,T,H,V] in the working dtype. When reads
-// is set, each level's unmixed read is also written, fp32 [L,B,T,H,V].
+// S^T rows [B,NG_l,H,V,K] (statesT). o [B,T,H,V] in the working dtype. When
+// read0 is set, level 0's unmixed read Qg h_n + Aqk Vn is also written, fp32
+// [B,T,H,V] (the backward's dmix_0).
 struct OutputArgs {
   const float* Qg; const float* Aqk; const float* hT; const float* vnT;
   const void* q; const void* mix;
-  const float* states[MAXL]; const float* statesT[MAXL]; int NGl[MAXL]; int f[MAXL];
-  void* o; float* reads;
+  const float* statesT[MAXL]; int NGl[MAXL]; int f[MAXL];
+  void* o; float* read0;
   int B, T, H, L, NT;
   float scale;
 };
 hipError_t output_fwd(const OutputArgs& a, int dtype, int K, int V, hipStream_t st);
 
-// Backward of the output for one chunk (ops/chunk.py:423-449):
-//   dmix_l = <do, read_l>  for every level (reads recomputed as in output_fwd)
-//   dq_l   = scale (mix_l do) S_l[group]^T   for l >= 1
-// dq [B,T,H,L,K] receives levels >= 1 (working dtype); dmix [B,T,H,L] fp32.
-struct OutputBwdArgs {
-  OutputArgs f;
-  const void* dout;
-  void* dq; float* dmix;
+// dmix_0[t] = <do[t], read0[t]> (ops/chunk.py:423), one wave per 16 tokens of
+// one head: read0 fp32 [B,T,H,V], do [B,T,H,V] (working dtype), dmix fp32
+// [B,T,H,L] (level-0 column written).
+struct Dmix0Args {
+  const float* read0; const void* dout; float* dmix;
+  int B, T, H, L, V;
 };
-hipError_t output_bwd(const OutputBwdArgs& a, int dtype, int K, int V, hipStream_t st);
+hipError_t dmix0_bwd(const Dmix0Args& a, int dtype, hipStream_t st);
 
-// Gradient of each upper level's group states from its reads
-// (read_level_bwd, ops/chunk.py:307-336):
-//   dS_l[j] = sum_{t in group j} scale q_l[t]^T (mix_l[t] do[t])
-// One workgroup per (batch, group, head); d_states fp32 [B,NG,H,K,V] written.
+// Backward of level l's reads, per (batch, group j, head), over the group's
+// chunks (read_level_bwd, ops/chunk.py:307-336, and the dq/dmix terms of
+// :423-449). With S = S_l[j] (rows [K][V] fp32, staged once) and
+// dO = mix_l do:
+//   read_l = scale q_l S,  dmix_l[t] = <do[t], read_l[t]>,
+//   dq_l   = scale dO S^T,  dS_l[j] = scale sum_t q_l[t]^T dO[t]
+// d_states fp32 [B,NG,H,K,V] written; dq [B,T,H,L,K] (level-l slice, working
+// dtype) and dmix [B,T,H,L] (level-l column) written.
 struct ReadStateBwdArgs {
-  const void* q; const void* mix; const void* dout;
-  float* d_states;
+  const void* q; const void* mix; const void* dout; const float* states;
+  float* d_states; void* dq; float* dmix;
   int B, T, H, L, level, f, NG;
   float scale;
 };

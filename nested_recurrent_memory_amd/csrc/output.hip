@@ -56,10 +56,10 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
       const float m = mixw(i, l) * sc;
 #pragma unroll
       for (int c = 0; c < CTV; ++c) out[c][r] += m * acc[c][r];
-      if (a.reads && i < nvalid) {
-        float* rp = a.reads + ((((size_t)l * a.B + b) * T + t0 + i) * H + h) * V;
+      if (l == 0 && a.read0 && i < nvalid) {
+        float* rp = a.read0 + (((size_t)b * T + t0 + i) * H + h) * V;
 #pragma unroll
-        for (int c = 0; c < CTV; ++c) rp[c * 16 + acc_col()] = acc[c][r] * sc;
+        for (int c = 0; c < CTV; ++c) rp[c * 16 + acc_col()] = acc[c][r];
       }
     }
   };
