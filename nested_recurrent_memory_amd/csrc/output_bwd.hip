@@ -30,21 +30,24 @@ __global__ __launch_bounds__(256) void dmix0_kernel(Dmix0Args a) {
 }
 
 template <typename E, int K, int V>
-__global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a) {
+__global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a) {
+  // 8 waves: for the per-chunk products wave w owns row tile w % 4 and half
+  // the columns (w / 4); the group's dS tiles are dealt round robin
+  constexpr int NW = 8;
   constexpr int C = CH;
   constexpr int LDS = V + 4;                     // staged S rows (fp32)
   constexpr int LDQ = K + 16 / (int)sizeof(E);   // staged q rows (exact)
   constexpr int LDD = V + 16 / (int)sizeof(E);   // staged do rows (exact)
   constexpr int KT = K / 16, VT = V / 16;
-  constexpr int KTW = KT / 4;                   // dS k-tiles per wave (all v-tiles each)
+  constexpr int VTH = VT / 2, KTH = KT / 2;      // column tiles per wave of read / dq
+  constexpr int NDS = KT * VT / NW;              // dS tiles per wave
   constexpr int KS = Mma<E>::KS;
-  constexpr int KPL = Mma<E>::KPL;
-  static_assert(KT % 4 == 0, "K must split over the 4 waves");
+  static_assert(KT * VT % NW == 0 && VT % 2 == 0 && KT % 2 == 0, "tiles split over 8 waves");
   typedef typename Mma<E>::SFrag SF;
   __shared__ __attribute__((aligned(16))) float s_S[K * LDS];
   __shared__ __attribute__((aligned(16))) E s_q[C * LDQ];
   __shared__ __attribute__((aligned(16))) E s_do[C * LDD];
-  __shared__ float s_mix[C];
+  __shared__ float s_mix[C], s_dm[C];
 
   const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
   const int j = blockIdx.x % NG;
@@ -61,98 +64,98 @@ __global__ __launch_bounds__(256) void read_state_bwd_kernel(ReadStateBwdArgs a)
 
   stage_f32(s_S, LDS, a.states + (((size_t)b * NG + j) * H + h) * K * V, V, K, V);
 
-  // dS[k][v] = sum_t q[t][k] dO[t][v]: the reduction runs down the staged
-  // rows; fragments are gathered down columns
-  f4 acc[KTW][VT];
+  f4 acc[NDS];
 #pragma unroll
-  for (int x = 0; x < KTW; ++x)
-#pragma unroll
-    for (int y = 0; y < VT; ++y) acc[x][y] = f4_zero();
-  const int ri = wv * 16 + (lane & 15);          // this wave's rows of the chunk
+  for (int x = 0; x < NDS; ++x) acc[x] = f4_zero();
+  const int rt = wv % 4, half = wv / 4;
+  const int ri = rt * 16 + (lane & 15);          // this wave's rows of the chunk
   const int n1 = min((j + 1) * a.f, NT);
   for (int n = j * a.f; n < n1; ++n) {
     const int t0 = n * C, nv = min(C, T - t0);
     stage_rows<E>(s_q, LDQ, qb + (size_t)t0 * rowQ, rowQ, C, K, nv);
     stage_rows<E>(s_do, LDD, db + (size_t)t0 * rowV, rowV, C, V, nv);
-    if (tid < C) s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
+    if (tid < C) {
+      s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
+      s_dm[tid] = 0.f;
+    }
     __syncthreads();
 
-    // ---- read_l = q S (this wave's 16 rows, all V) -> dmix_l
+    // ---- read_l = q S on this wave's rows and half of V -> partial dmix_l
     {
-      f4 rd[VT];
+      f4 rd[VTH];
 #pragma unroll
-      for (int y = 0; y < VT; ++y) rd[y] = f4_zero();
+      for (int y = 0; y < VTH; ++y) rd[y] = f4_zero();
 #pragma unroll
       for (int s = 0; s < K / KS; ++s) {
         const int k0 = s * KS + kofs<E>(lane);
         const auto fa = Mma<E>::ld(s_q + ri * LDQ + k0);
 #pragma unroll
-        for (int y = 0; y < VT; ++y)
-          rd[y] = Mma<E>::mma(rd[y], fa, gather_s<E>(s_S + k0 * LDS + y * 16 + (lane & 15), LDS));
+        for (int y = 0; y < VTH; ++y)
+          rd[y] = Mma<E>::mma(rd[y], fa,
+                              gather_s<E>(s_S + k0 * LDS + (half * VTH + y) * 16 + (lane & 15), LDS));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = wv * 16 + acc_row(r);
+        const int i = rt * 16 + acc_row(r);
         float sm = 0.f;
 #pragma unroll
-        for (int y = 0; y < VT; ++y) sm += to_f(s_do[i * LDD + y * 16 + acc_col()]) * rd[y][r];
+        for (int y = 0; y < VTH; ++y) sm += to_f(s_do[i * LDD + (half * VTH + y) * 16 + acc_col()]) * rd[y][r];
         sm += __shfl_xor(sm, 1, WAVE);
         sm += __shfl_xor(sm, 2, WAVE);
         sm += __shfl_xor(sm, 4, WAVE);
         sm += __shfl_xor(sm, 8, WAVE);
-        if ((lane & 15) == 0 && i < nv) dmb[(size_t)(t0 + i) * H * L] = sm * a.scale;
+        if ((lane & 15) == 0) atomicAdd(&s_dm[i], sm);
       }
     }
-    // ---- dq_l = scale dO S^T (this wave's 16 rows, all K)
+    // ---- dq_l = scale dO S^T on this wave's rows and half of K
     {
-      f4 dq[KT];
+      f4 dq[KTH];
 #pragma unroll
-      for (int x = 0; x < KT; ++x) dq[x] = f4_zero();
+      for (int x = 0; x < KTH; ++x) dq[x] = f4_zero();
       const float m = s_mix[ri];
 #pragma unroll
       for (int s = 0; s < V / KS; ++s) {
         const int v0 = s * KS + kofs<E>(lane);
         const SF fa = Mma<E>::makes([&](int e) { return to_f(s_do[ri * LDD + v0 + e]) * m; });
 #pragma unroll
-        for (int x = 0; x < KT; ++x)
-          dq[x] = Mma<E>::mma(dq[x], fa, Mma<E>::ld(s_S + (x * 16 + (lane & 15)) * LDS + v0));
+        for (int x = 0; x < KTH; ++x)
+          dq[x] = Mma<E>::mma(dq[x], fa, Mma<E>::ld(s_S + ((half * KTH + x) * 16 + (lane & 15)) * LDS + v0));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = wv * 16 + acc_row(r);
+        const int i = rt * 16 + acc_row(r);
         if (i < nv) {
 #pragma unroll
-          for (int x = 0; x < KT; ++x)
-            dqb[(size_t)(t0 + i) * rowQ + x * 16 + acc_col()] = from_f<E>(dq[x][r] * a.scale);
+          for (int x = 0; x < KTH; ++x)
+            dqb[(size_t)(t0 + i) * rowQ + (half * KTH + x) * 16 + acc_col()] = from_f<E>(dq[x][r] * a.scale);
         }
       }
     }
-    // ---- dS += q^T dO
+    // ---- dS += q^T dO: the reduction runs down the staged rows, fragments
+    // gathered down columns
 #pragma unroll
     for (int s = 0; s < C / KS; ++s) {
       const int r0 = s * KS + kofs<E>(lane);
-      typename Mma<E>::Frag fa[KTW];
 #pragma unroll
-      for (int x = 0; x < KTW; ++x)
-        fa[x] = gather_x<E>(s_q + r0 * LDQ + (wv * KTW + x) * 16 + (lane & 15), LDQ);
-#pragma unroll
-      for (int y = 0; y < VT; ++y) {
-        const E* pd = s_do + r0 * LDD + y * 16 + (lane & 15);
+      for (int x = 0; x < NDS; ++x) {
+        const int g = wv + NW * x, kt = g / VT, vt = g % VT;
+        const auto fa = gather_x<E>(s_q + r0 * LDQ + kt * 16 + (lane & 15), LDQ);
+        const E* pd = s_do + r0 * LDD + vt * 16 + (lane & 15);
         const auto fb = Mma<E>::makes([&](int e) { return to_f(pd[e * LDD]) * s_mix[r0 + e]; });
-#pragma unroll
-        for (int x = 0; x < KTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
+        acc[x] = Mma<E>::mma(acc[x], fa, fb);
       }
     }
     __syncthreads();
+    if (tid < nv) dmb[(size_t)(t0 + tid) * H * L] = s_dm[tid] * a.scale;
   }
   float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;
 #pragma unroll
-  for (int x = 0; x < KTW; ++x)
+  for (int x = 0; x < NDS; ++x) {
+    const int g = wv + NW * x, kt = g / VT, vt = g % VT;
 #pragma unroll
-    for (int y = 0; y < VT; ++y)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        out[(size_t)((wv * KTW + x) * 16 + acc_row(r)) * V + y * 16 + acc_col()] = acc[x][y][r] * a.scale;
+    for (int r = 0; r < 4; ++r)
+      out[(size_t)(kt * 16 + acc_row(r)) * V + vt * 16 + acc_col()] = acc[x][r] * a.scale;
+  }
 }
 
 template <typename E, int V>
@@ -172,7 +175,7 @@ hipError_t dmix0_bwd(const Dmix0Args& a, int dtype, hipStream_t st) {
 template <typename E, int K, int V>
 static hipError_t launch_read_state_bwd(const ReadStateBwdArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.B * a.H * a.NG);
-  hipLaunchKernelGGL((read_state_bwd_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((read_state_bwd_kernel<E, K, V>), dim3(grid), dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
