@@ -78,27 +78,27 @@ def work_model(cfg):
     wk, wv, wc = C * K * 4, C * V * 4, C * C * 4      # fp32 working tiles
     kv = K * V * 4                                    # one state
     m = {}
+    tok = B * T * H                                   # token-heads
     # level-0 intra: reads q0,k,b,v,w + g (fp32); writes W,U,KtT,Qg,Aqk,gam
     # and the backward layouts Kt, WT, QgT, AqkT, TT
     m["ngdn_l0_intra_fwd"] = (
         units * (3 * ck + 2 * cv + C * K * 4 + 4 * wk + wv + wc + K * 4 + 3 * wk + 2 * wc),
         units * (2 * 2 * C * C * K + 2 * C * C * (K + V) + C ** 3 // 3))
-    # level-0 scan: reads W, U, KtT, gam; writes hT, vnT; + final
-    m["ngdn_l0_scan_fwd"] = (units * (2 * wk + wv + K * 4 + kv + wv) + B * H * kv,
+    # level-0 scan: reads W, U, KtT, gam; writes hT, vnT and (training) h, vn; + final
+    m["ngdn_l0_scan_fwd"] = (units * (2 * wk + wv + K * 4 + 2 * kv + 2 * wv) + B * H * kv,
                              units * 2 * 2 * C * K * V)
-    # output: Qg, hT, Aqk, vnT, q of upper levels, mix; upper states once per group; o
-    up_states = sum(B * H * n_groups(NT, f[l]) * kv for l in range(1, L))
+    # output: Qg, hT, Aqk, vnT, q of upper levels, mix; upper states once per
+    # group; writes o and (training) level 0's read
+    up_states = sum(B * H * n_groups(NT, f[lvl]) * kv for lvl in range(1, L))
     m["ngdn_output_fwd"] = (
-        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv) + up_states,
+        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv + wv) + up_states,
         units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 2 * C * K * V))
-    m["ngdn_output_bwd"] = (
-        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv + (L - 1) * ck + C * L * 4)
-        + up_states,
-        units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 4 * C * K * V))
+    # dmix_0 = <do, read_0>: reads read_0 (fp32), do; writes dmix
+    m["ngdn_output_bwd"] = (tok * (V * 4 + V * es + L * 4), tok * 2 * V)
     # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
     m["ngdn_l0_scan_bwd"] = (units * (3 * wk + wc + K * 4 + cv + C * es + kv + 2 * wv),
                              units * (2 * C * K * V * 3 + 2 * C * C * V))
-    # level-0 chunk backward, state half: hT, dSp, vnT, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
+    # level-0 chunk backward, state half: h, dSp, vn, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
     m["ngdn_l0_bwd_state"] = (units * (2 * kv + 2 * wv + cv + C * es + 3 * wk + wc + K * 4),
                               units * (3 * 2 * C * K * V + 2 * C * C * V))
     # level-0 chunk backward, intra half: q0,k,b,v,w,g, W,U,TT, dQg,dWT,dKt,dAqk,dgam,dVnT
@@ -108,13 +108,28 @@ def work_model(cfg):
                  + 3 * ck + 2 * cv + C * K * 4),
         units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     for lvl in range(1, L):
-        nf = n_firings(NT, f[lvl])
+        nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         fu = B * H * nf
-        nk = N * K * 4
+        nk, nv_ = N * K * 4, N * V * 4
         m[f"ngdn_probe_fwd.{lvl}"] = (fu * (kv + 3 * nk + 4 * K) + H * (N * K + 4 * K * V) * es,
                                       fu * 5 * 2 * N * K * V)
-        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * n_groups(NT, f[lvl]) * kv,
+        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * ng * 2 * kv,
                                            fu * 2 * 2 * N * K * V)
+        # reads of level lvl, per group: q_l, do, mix, the group state ->
+        # d_states, dq_l, dmix_l (read, dq and dS products: 3 x 2 K V per token)
+        m[f"ngdn_read_state_bwd.{lvl}"] = (tok * (K * es + V * es + K * es + 2 * 4)
+                                           + B * H * ng * 2 * kv, tok * 3 * 2 * K * V)
+        # reverse firing scan: keys, A^T, gam, d_states -> dSp, dvn
+        m[f"ngdn_upper_scan_bwd.{lvl}"] = (fu * (2 * nk + K * 4 + kv + nv_) + B * H * ng * kv,
+                                           fu * 2 * 2 * N * K * V)
+        # firing backward: lower states (rows and transposed), this level's
+        # states (both), dSp, dvn, parameters -> six workspaces, the lower
+        # state's gradient; 14 N K V products
+        m[f"ngdn_probe_bwd.{lvl}"] = (fu * (4 * kv + kv + nv_ + 6 * nk + kv)
+                                      + H * (N * K + 8 * K * V) * es, fu * 14 * 2 * N * K * V)
+        # parameter gradients: four A^T B sums over every firing's N rows
+        m[f"ngdn_param_grads.{lvl}"] = (fu * 5 * nk + 4 * H * K * V * 4,
+                                        4 * fu * 2 * N * K * V)
     return m, units
 
 
