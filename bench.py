@@ -12,6 +12,9 @@ The line carries:
   roofline      the dominant kernel (entry point) of the step: its algorithmic
                 bytes or flops per launch divided by its average launch time,
                 timed with events on the launch stream over the timed region;
+                ``traffic`` is its measured HBM bytes per launch from the
+                committed counter profile of the configuration
+                (profiles/ngdn_fwd_bwd_<config>_traffic.md), null without one;
   cpu_baseline  the CPU restatement (oracle/ngdn_oracle.py, float32 PyTorch)
                 timed on a bounded sample of the same workload, extrapolated.
 """
@@ -133,6 +136,20 @@ def work_model(cfg):
     return m, units
 
 
+def profiled_traffic(config, entry):
+    """HBM bytes per launch of ``entry`` as the committed counter profile of
+    this configuration reports them (FETCH_SIZE and WRITE_SIZE, calibrated on
+    a copy kernel), or None when no profile covers it."""
+    path = os.path.join(ROOT, "profiles", f"ngdn_fwd_bwd_{config}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for row in open(path):
+        cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == entry:
+            return round(float(cells[4]) * 1e9)
+    return None
+
+
 def step_fn(inp, leaves, L, do):
     def step():
         o, _ = chunk_nested_gdn2(**{**inp, **leaves}, L=L)
@@ -227,6 +244,7 @@ def main():
     roof = None
     if dom_work is not None:
         nbytes, flops = dom_work
+        traffic = profiled_traffic(args.config, dom)
         t = ms[dom] * 1e-3
         gbs = nbytes / t / 1e9
         tfs = flops / t / 1e12
@@ -234,11 +252,11 @@ def main():
         hbm_bound = (nbytes / (HBM_PEAK_GBS * 1e9)) >= (flops / (peak_f * 1e12))
         if hbm_bound:
             roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "algorithmic_bytes": nbytes, "avg_ms": round(ms[dom], 4)}
         else:
             roof = {"kernel": dom, "bound": "mfma", "achieved": round(tfs, 2), "peak": peak_f,
-                    "unit": "TFLOP/s", "frac": round(tfs / peak_f, 4), "traffic": None,
+                    "unit": "TFLOP/s", "frac": round(tfs / peak_f, 4), "traffic": traffic,
                     "algorithmic_flops": flops, "avg_ms": round(ms[dom], 4)}
     if args.kernel_table:
         for n in sorted(per_step, key=per_step.get, reverse=True):
