@@ -225,6 +225,31 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
                          const float* ws_dxg, const float* ws_dxw, float* dkp,
                          float* dbp, float* dwp, float* dgp, void* stream);
 
+/* One decoding token: naive_step_nested_gdn2 (nested_gdn2/ops/naive.py:42-134;
+ * the layer's decode and ragged-tail path, layers/nested_gdn2.py:218-224).
+ * Level 0 writes (k, v, b, w, g), every level is read with its q slice and
+ * mixed into o, then each level whose firing this token completes promotes,
+ * bottom-up (the probe of the level below, then one firing of the update).
+ * d->T is ignored. q [B,H,L,K]; k, b [B,H,K]; v, w [B,H,V]; mix [B,H,L] in
+ * dtype; g [B,H,K] fp32; o [B,H,V] in dtype. state_in -> state_out
+ * [B,H,L,K,V] fp32: the same buffer updates in place, distinct buffers must
+ * not overlap. position: device int64 [B], each row's token index (firings
+ * decided per row on the device, no host synchronisation), or NULL to use
+ * position_all for every row (firings decided here, no launch for levels
+ * that do not fire). A token fires level l when (pos + 1) % chunk_size == 0
+ * and ((pos + 1) / chunk_size) % firing_intervals[l] == 0. firing_intervals
+ * [L] and n_queries [L-1] are host arrays; parameters as for ngdn_probe_fwd
+ * (every level's slice). ws: fp32 workspace of B*H*(3*N*K + K) floats, N the
+ * most pairs of any level (K for merge). */
+int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                  const float* g, const void* b, const void* w, const void* mix,
+                  const float* state_in, float* state_out, const int64_t* position,
+                  int64_t position_all, int32_t chunk_size,
+                  const int32_t* firing_intervals, int32_t promotion,
+                  const int32_t* n_queries, const void* query_banks, int32_t n_max,
+                  const void* key_projections, const void* bpT, const void* wpT,
+                  const void* gpT, float* ws, void* o, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,11 +1,13 @@
 """MI355X-native nested Gated DeltaNet chunkwise memory op.
 
-Drop-in for ``nested_gdn2.ops.chunk_nested_gdn2`` of awehrs/nested_recurrent_memory,
-computed by hand-written gfx950 HIP kernels (libngdn.so, C ABI in include/ngdn.h).
+Drop-in for ``nested_gdn2.ops.chunk_nested_gdn2`` of awehrs/nested_recurrent_memory
+and for its decoding step ``naive_step_nested_gdn2``, computed by hand-written
+gfx950 HIP kernels (libngdn.so, C ABI in include/ngdn.h).
 """
 
 from .chunk import PROMOTIONS, ChunkNestedGDN2Function, chunk_nested_gdn2
 from .schedule import n_firings, n_groups, source_index
+from .step import step_nested_gdn2
 
 __all__ = ["chunk_nested_gdn2", "ChunkNestedGDN2Function", "PROMOTIONS",
-           "n_firings", "n_groups", "source_index"]
+           "step_nested_gdn2", "n_firings", "n_groups", "source_index"]

@@ -27,6 +27,7 @@ class Dims(ctypes.Structure):
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
+I64 = ctypes.c_int64
 PD = ctypes.POINTER(Dims)
 
 # name -> argtypes (all return an int32 status unless listed in _RESTYPES)
@@ -49,6 +50,7 @@ SIGNATURES = {
     "ngdn_probe_bwd": [PD, I32, I32, I32, I32, I32, P, P, I32, P, P, I32, P, P, P, P,
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
+    "ngdn_step": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4 + [P, P, P],
 }
 _RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}
 

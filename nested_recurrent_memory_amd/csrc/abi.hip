@@ -395,4 +395,93 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
   return launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads");
 }
 
+int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                  const float* g, const void* b, const void* w, const void* mix,
+                  const float* state_in, float* state_out, const int64_t* position,
+                  int64_t position_all, int32_t chunk_size,
+                  const int32_t* firing_intervals, int32_t promotion,
+                  const int32_t* n_queries, const void* query_banks, int32_t n_max,
+                  const void* key_projections, const void* bpT, const void* wpT,
+                  const void* gpT, float* ws, void* o, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_step")) return r;
+  if (!q || !k || !v || !g || !b || !w || !mix || !state_in || !state_out || !o)
+    return fail(NGDN_EINVAL, "ngdn_step: NULL tensor");
+  if (chunk_size <= 0) return fail(NGDN_EINVAL, "ngdn_step: chunk_size %d", chunk_size);
+  if (!position && position_all < 0)
+    return fail(NGDN_EINVAL, "ngdn_step: position %lld is negative", (long long)position_all);
+  const int L = d->L, K = d->K, V = d->V;
+  const long long skv = (long long)K * V;
+  const long long nst = (long long)d->B * d->H * L * skv;
+  if (state_in != state_out && state_out < state_in + nst && state_in < state_out + nst)
+    return fail(NGDN_EINVAL, "ngdn_step: state_in and state_out overlap");
+  if (L > 1) {
+    if (K != V) return fail(NGDN_EINVAL, "ngdn_step: promotion needs K == V, got %d, %d", K, V);
+    if (promotion != 0 && promotion != 1)
+      return fail(NGDN_EINVAL, "ngdn_step: promotion %d unknown", promotion);
+    if (!firing_intervals || (promotion == 0 && !n_queries) || !bpT || !wpT || !gpT || !ws)
+      return fail(NGDN_EINVAL, "ngdn_step: NULL parameter");
+    for (int l = 0; l < L; ++l)
+      if (firing_intervals[l] <= 0)
+        return fail(NGDN_EINVAL, "ngdn_step: firing interval %d of level %d", firing_intervals[l], l);
+    for (int l = 1; l < L; ++l) {
+      const int N = promotion == 1 ? K : n_queries[l - 1];
+      if (!pow2_ge16(N))
+        return fail(NGDN_EINVAL, "ngdn_step: pairs per firing must be a power of two >= 16 "
+                    "(and <= 128), got %d", N);
+      if (promotion == 0 && (N > n_max || !query_banks || !key_projections))
+        return fail(NGDN_EINVAL, "ngdn_step: n_queries=%d exceeds bank rows %d", N, n_max);
+    }
+  }
+  hipStream_t st = (hipStream_t)stream;
+  ngdn::StepArgs sa{q, k, v, g, b, w, mix, state_in, state_out, o, d->B, d->H, L, d->scale};
+  if (int32_t r = launched(ngdn::step_fwd(sa, d->dtype, K, V, st), "ngdn_step")) return r;
+
+  const size_t hkv = (size_t)d->H * skv;
+  const size_t esz = d->dtype == NGDN_BF16 ? 2 : 4;
+  const size_t units = (size_t)d->B * d->H;
+  for (int l = 1; l < L; ++l) {
+    ngdn::FireGate gate{nullptr, chunk_size, firing_intervals[l]};
+    if (position) {
+      gate.pos = reinterpret_cast<const long long*>(position);
+    } else {
+      const long long end = (long long)position_all + 1;
+      if (end % chunk_size != 0 || (end / chunk_size) % firing_intervals[l] != 0) continue;
+    }
+    const int N = promotion == 1 ? K : n_queries[l - 1];
+    float* A = ws;
+    float* KT = A + units * N * K;
+    float* U = KT + units * K * N;
+    float* gam = U + units * N * V;
+    auto lvl = [&](const void* p, size_t per) -> const void* {
+      return p ? static_cast<const char*>(p) + (size_t)(l - 1) * per * esz : nullptr;
+    };
+    // probe of the level below (already updated this token), read as a
+    // "final state": one firing, source index past every stored group
+    ngdn::ProbeArgs pa{};
+    pa.below_fin = state_out + (long long)(l - 1) * skv;
+    pa.below = pa.below_fin; pa.below_mode = 1; pa.NGb = 0;
+    pa.bf_sh = L * skv; pa.bf_sb = d->H * pa.bf_sh;
+    pa.f_below = firing_intervals[l - 1]; pa.f_here = firing_intervals[l];
+    pa.bank = lvl(query_banks, (size_t)d->H * n_max * K); pa.Nmax = n_max;
+    pa.kp = lvl(key_projections, hkv);
+    pa.bpT = lvl(bpT, hkv); pa.wpT = lvl(wpT, hkv); pa.gpT = lvl(gpT, hkv);
+    pa.merge = promotion;
+    pa.A = A; pa.KT = KT; pa.U = U; pa.gam = gam;
+    pa.B = d->B; pa.H = d->H; pa.NF = 1; pa.N = N; pa.V = V;
+    pa.gate = gate;
+    if (int32_t r = launched(ngdn::probe_fwd(pa, d->dtype, K, st), "ngdn_step (probe)")) return r;
+    // one firing of this level's update, in place on state_out
+    ngdn::ScanArgs ca{};
+    ca.A = A; ca.BT = KT; ca.U = U; ca.gam = gam;
+    ca.init = state_out + (long long)l * skv; ca.init_sh = L * skv; ca.init_sb = d->H * ca.init_sh;
+    ca.state_mode = 0; ca.NG = 1;
+    ca.fin = state_out + (long long)l * skv; ca.fin_sh = ca.init_sh; ca.fin_sb = ca.init_sb;
+    ca.B = d->B; ca.H = d->H; ca.S = 1; ca.M = N; ca.V = V;
+    ca.gate = gate;
+    if (int32_t r = launched(ngdn::scan_fwd(ca, d->dtype, K, st), "ngdn_step (update)")) return r;
+  }
+  return NGDN_OK;
+}
+
 }  // extern "C"

@@ -23,6 +23,19 @@ struct L0IntraArgs {
 };
 hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
+// Per-row firing gate of the decoding step (ops/naive.py:101-113): when pos
+// is set, batch row b runs only if the token at pos[b] completes a chunk
+// (end = pos[b] + 1, end % chunk == 0) whose number end / chunk is a multiple
+// of every; other rows' workgroups return before touching memory.
+struct FireGate {
+  const long long* pos; int chunk, every;
+};
+__device__ __forceinline__ bool gated_out(const FireGate& g, int b) {
+  if (!g.pos) return false;
+  const long long end = g.pos[b] + 1;
+  return end % g.chunk != 0 || (end / g.chunk) % g.every != 0;
+}
+
 // Columns of V per scan workgroup (each step's operands are read by V / 32
 // workgroups of one (batch, head)).
 constexpr int SCAN_BV = 32;
@@ -42,6 +55,7 @@ struct ScanArgs {
   float* vnT; float* vn;
   float* fin; long long fin_sb, fin_sh;
   int B, H, S, M, V;
+  FireGate gate;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 
@@ -94,8 +108,24 @@ struct ProbeArgs {
   float* keysN; float* AT;   // optional: keys [B,H,NF,N,K], A^T [B,H,NF,K,N] for the reverse scan
   float* keys; float* vals; float* bo; float* wo; float* go;
   int B, H, NF, N, V;
+  FireGate gate;
 };
 hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
+
+// Level-0 half of one decoding token (ops/naive.py:42-100): per (b, h),
+// q [B,H,L,K], k, b [B,H,K], v, w [B,H,V], mix [B,H,L] in the working dtype,
+// g [B,H,K] fp32; state s_in -> s_out [B,H,L,K,V] fp32 (may be the same
+// buffer; level 0 updated, levels above copied when the buffers differ);
+// o [B,H,V] in the working dtype.
+struct StepArgs {
+  const void* q; const void* k; const void* v; const float* g;
+  const void* b; const void* w; const void* mix;
+  const float* s_in; float* s_out;
+  void* o;
+  int B, H, L;
+  float scale;
+};
+hipError_t step_fwd(const StepArgs& a, int dtype, int K, int V, hipStream_t st);
 
 // Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
 // the autograd replay of ops/chunk.py:339-371,486-517, derived in closed

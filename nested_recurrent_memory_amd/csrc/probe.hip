@@ -36,6 +36,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   const int bh = blockIdx.x / NF;
   const int h = bh % H, b = bh / H;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  if (gated_out(a.gate, b)) return;
 
   // ---- the gathered lower state
   const int src = ((i + 1) * a.f_here) / a.f_below;

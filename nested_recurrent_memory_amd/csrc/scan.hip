@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   const int h = bh % H, b = bh / H;
   const int v0 = vt * BV;
   const int lane = lane_id(), wv = wave_id();
+  if (gated_out(a.gate, b)) return;
 
   // state tiles of this wave: g = wv * TPW + i, rt = g / CT, ct = g % CT
   f4 st[TPW];

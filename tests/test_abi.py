@@ -8,7 +8,7 @@ import re
 import pytest
 import torch
 
-from nested_recurrent_memory_amd import _lib, chunk_nested_gdn2
+from nested_recurrent_memory_amd import _lib, chunk_nested_gdn2, step_nested_gdn2
 from nested_recurrent_memory_amd.inputs import NAMES, make_inputs
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -71,3 +71,33 @@ def test_cpu_tensors_raise_instead_of_falling_back():
     inp, L = _base()
     with pytest.raises(RuntimeError, match="GPU"):
         chunk_nested_gdn2(**inp, L=L)
+
+
+def _step_args(L=2, K=64):
+    inp = make_inputs(B=2, T=1, H=2, K=K, V=K, L=L, N=16, intervals=(1,) * L)
+    args = {n: inp[n][:, 0] for n in ("q", "k", "v", "g", "b", "w", "mix_weights")}
+    args.update({n: inp[n] for n in NAMES[7:]})
+    args["state"] = torch.zeros(2, 2, L, K, K)
+    return args, L
+
+
+def test_step_cpu_tensors_raise_instead_of_falling_back():
+    args, L = _step_args()
+    with pytest.raises(RuntimeError, match="GPU"):
+        step_nested_gdn2(**args, position=63, L=L)
+
+
+def test_step_validates_before_launch():
+    args, L = _step_args()
+    with pytest.raises(ValueError, match="chunk_size"):
+        step_nested_gdn2(**args, position=0, L=L, chunk_size=0)
+    with pytest.raises(ValueError, match="promotion"):
+        step_nested_gdn2(**args, position=0, L=L, promotion="sum")
+    args["n_queries_per_level"] = torch.tensor([24], dtype=torch.int32)
+    with pytest.raises(ValueError, match="power of two"):
+        step_nested_gdn2(**args, position=0, L=L)
+    so = _lib.lib()
+    d = _lib.dims(1, 1, 1, 2, 64, 64, _lib.NGDN_F32, 0.1)
+    rc = so.ngdn_step(ctypes.byref(d), *([None] * 9), None, -1, 64, None, 0, None, None, 16,
+                      *([None] * 7))
+    assert rc == 1 and b"NULL" in so.ngdn_last_error()

@@ -1,0 +1,127 @@
+"""Decoding step (ngdn_step) against the CPU oracle's step (float64).
+
+The oracle's step (oracle/ngdn_oracle.py:step_forward, restating
+ops/naive.py:42-134) is pinned by prefill + step == one pass in
+tests/test_oracle.py. Tolerances: fp32 inputs 1e-5; bf16 inputs
+max-abs 2e-3 / rel 1e-2, the absolute part scaled by max(1, max|ref|) for
+the state (values up to a few units).
+"""
+
+import pytest
+import torch
+
+import ngdn_oracle as ref
+from nested_recurrent_memory_amd import chunk_nested_gdn2, step_nested_gdn2
+from nested_recurrent_memory_amd.inputs import NAMES, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-5, 1e-5), torch.bfloat16: (2e-3, 1e-2)}
+STEP_IN = ("q", "k", "v", "g", "b", "w", "mix_weights")
+PARAMS = ("query_banks", "key_projections", "b_projections", "w_projections",
+          "g_projections", "n_queries_per_level", "firing_intervals")
+
+
+def _close(name, got, want, dtype):
+    atol, rtol = TOL[dtype]
+    got, want = got.double().cpu(), want.double()
+    m = max(1.0, want.abs().max().item())
+    err = (got - want).abs()
+    bad = err > atol * m + rtol * want.abs()
+    assert not bad.any(), (f"{name}: {int(bad.sum())} elements out of bound, max err "
+                           f"{err.max().item():.3e} (scale {m:.3e})")
+
+
+def _state(B, H, L, K, V, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randn(B, H, L, K, V, generator=gen) * 0.5
+
+
+def _token(inp, t):
+    return {n: inp[n][:, t] for n in STEP_IN}
+
+
+CASES = [
+    # L, K, V, N, intervals, promotion
+    (1, 64, 128, 16, (1,), "learned"),
+    (2, 64, 64, 16, (1, 1), "learned"),
+    (3, 128, 128, 64, (1, 1, 2), "learned"),
+    (3, 64, 64, 32, (1, 2, 4), "merge"),
+    (2, 128, 128, 128, (1, 1), "merge"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"L{c[0]}K{c[1]}V{c[2]}N{c[3]}{c[5][0]}")
+@pytest.mark.parametrize("position", [5, 63, 127, 255, "rows"])
+def test_step_matches_oracle(dtype, case, position):
+    L, K, V, N, f, promotion = case
+    print(f"step dtype={dtype} case={case} position={position}", flush=True)
+    B, H = 3, 2
+    inp = make_inputs(B=B, T=1, H=H, K=K, V=V, L=L, N=N, intervals=f, dtype=dtype,
+                      g_scale=0.5, seed=7)
+    state = _state(B, H, L, K, V, seed=3)
+    pos = torch.tensor([63, 64, 255]) if position == "rows" else position
+    tok = _token(inp, 0)
+    gpu_pos = pos.cuda() if torch.is_tensor(pos) else pos
+    s_dev = state.cuda()
+    o, s = step_nested_gdn2(**{n: x.cuda() for n, x in tok.items()}, state=s_dev,
+                            position=gpu_pos, **{n: inp[n].cuda() for n in PARAMS},
+                            L=L, promotion=promotion)
+    torch.cuda.synchronize()
+    assert o.dtype == dtype and s.dtype == torch.float32
+    assert torch.equal(s_dev.cpu(), state), "the state passed in must not change"
+
+    o_ref, s_ref = ref.step_forward(*[tok[n].double() for n in STEP_IN], state.double(), pos,
+                                    *[inp[n].double() for n in PARAMS[:5]],
+                                    inp["n_queries_per_level"], inp["firing_intervals"],
+                                    L=L, promotion=promotion)
+    _close("o", o, o_ref, dtype)
+    _close("state", s, s_ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("promotion", ["learned", "merge"])
+def test_prefill_then_step_handoff(dtype, promotion):
+    """The chunk op's final state feeds the step (tests/ops/test_chunk.py:161-197):
+    prefill 128 tokens, step 128 more through firings of level 1 at tokens 191
+    and 255 and of level 2 at 191; every output and the final state match one
+    oracle pass. (The sequence ends on a chunk boundary: over a ragged end the
+    chunk form counts the partial chunk as a firing, the step form does not,
+    which is why the layer chunks only whole chunks, layers/nested_gdn2.py:198-214.)"""
+    print(f"handoff dtype={dtype} promotion={promotion}", flush=True)
+    B, H, K, L, T, pre = 2, 2, 64, 3, 256, 128
+    f = (1, 1, 3)
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=K, L=L, N=16, intervals=f, dtype=dtype,
+                      g_scale=0.5, seed=11)
+    gpu = {n: inp[n].cuda() for n in NAMES}
+    with torch.no_grad():
+        o_pre, state = chunk_nested_gdn2(**{n: (gpu[n][:, :pre] if n in STEP_IN else gpu[n])
+                                            for n in NAMES}, L=L, output_final_state=True,
+                                         promotion=promotion)
+        outs = [o_pre]
+        for t in range(pre, T):
+            o_t, state = step_nested_gdn2(**{n: gpu[n][:, t] for n in STEP_IN}, state=state,
+                                          position=t, **{n: gpu[n] for n in PARAMS}, L=L,
+                                          promotion=promotion)
+            outs.append(o_t.unsqueeze(1))
+    torch.cuda.synchronize()
+    o_ref, s_ref = ref.chunk_forward(*[inp[n].double() if n not in PARAMS[5:] else inp[n]
+                                       for n in NAMES], L=L, output_final_state=True,
+                                     promotion=promotion, out_dtype=torch.float64)
+    _close("o", torch.cat(outs, 1), o_ref, dtype)
+    _close("final state", state, s_ref, dtype)
+
+
+def test_step_rows_fire_on_device():
+    """Per-row positions on the GPU: only the rows whose token ends a firing
+    promote; the others keep their upper levels bit for bit."""
+    B, H, K, L = 4, 2, 64, 2
+    inp = make_inputs(B=B, T=1, H=H, K=K, V=K, L=L, N=16, intervals=(1, 1), seed=5)
+    state = _state(B, H, L, K, K, seed=9).cuda()
+    pos = torch.tensor([63, 62, 127, 0], device="cuda")
+    o, s = step_nested_gdn2(**{n: x.cuda() for n, x in _token(inp, 0).items()}, state=state,
+                            position=pos, **{n: inp[n].cuda() for n in PARAMS}, L=L)
+    torch.cuda.synchronize()
+    up_same = (s[:, :, 1] == state[:, :, 1]).flatten(1).all(1).cpu()
+    assert up_same.tolist() == [False, True, False, True]
