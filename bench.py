@@ -189,12 +189,107 @@ def cpu_baseline(cfg, budget_s=20.0):
                       f"{t_total:.1f} s, scaled by {B * H}/{slices}"}
 
 
+# Decoding: one token for a batch of sequences, the c2 layer shape (H=16,
+# d=128, 3 levels firing every 1/4/16 chunks, 64 queries) at a serving batch.
+DECODE = dict(B=64, H=16, K=128, V=128, L=3, N=64, intervals=(1, 4, 16),
+              dtype=torch.bfloat16, g_scale=0.1)
+
+
+def decode_bench(args):
+    """Tokens/s of the decoding step (ngdn_step): one HIP graph per token
+    (the step with device-side positions, then position += 1), replayed over
+    ``steps`` tokens from position 0, so every firing of the window is
+    included. The step kernel's own duration is timed separately on tokens
+    that fire nothing."""
+    from nested_recurrent_memory_amd import prepare_step_params, step_nested_gdn2
+
+    cfg = DECODE
+    B, H, K, V, L, N = (cfg[x] for x in ("B", "H", "K", "V", "L", "N"))
+    inp = gpu_inputs(dict(cfg, T=1))
+    tok = {n: inp[n][:, 0].contiguous() for n in ("q", "k", "v", "g", "b", "w", "mix_weights")}
+    rest = {n: inp[n] for n in ("query_banks", "key_projections", "b_projections",
+                                "w_projections", "g_projections", "n_queries_per_level",
+                                "firing_intervals")}
+    par = prepare_step_params(*(rest[n] for n in list(rest)[:5]), cfg["dtype"])
+    state = torch.zeros(B, H, L, K, V, device="cuda")
+    pos = torch.zeros(B, dtype=torch.int64, device="cuda")
+
+    def token(p):
+        return step_nested_gdn2(**tok, state=state, position=p, **rest, L=L, params=par,
+                                inplace=True)
+
+    with torch.no_grad():
+        token(pos)                                   # load the library, warm the pool
+        pos.zero_()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            token(pos)
+            pos.add_(1)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            token(pos)
+            pos.add_(1)
+        for _ in range(args.warmup):
+            graph.replay()
+        pos.zero_()
+        state.zero_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+
+        # the step kernel alone: host positions that fire nothing launch only it
+        _lib.TIMING = {}
+        for i in range(20):
+            token(1 + 64 * i)
+        torch.cuda.synchronize()
+        timing, _lib.TIMING = _lib.TIMING, None
+    evs = timing["ngdn_step"]
+    k_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    es = 2
+    # reads every level's state and the token's inputs, writes level 0 and o
+    nbytes = B * H * ((L + 1) * K * V * 4 + (L * K + 3 * K + 2 * V + L) * es + K * 4 + V * es)
+    gbs = nbytes / (k_ms * 1e-3) / 1e9
+    line = {
+        "metric": "tokens/s decoding step nested GDN op (B64,H16,d128,3 lvl)",
+        "value": round(B * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode: step_nested_gdn2, one token per sequence per step, "
+                               f"positions 0..{args.steps - 1}, HIP graph per token",
+                   "B": B, "H": H, "K": K, "V": V, "L": L,
+                   "firing_intervals": list(cfg["intervals"]), "n_queries": N,
+                   "state": "fp32"},
+        "roofline": {"kernel": "ngdn_step (step_kernel)", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes, "avg_ms": round(k_ms, 4)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
+    ap.add_argument("--workload", default="train", choices=("train", "decode"),
+                    help="train: forward+backward at --config (the headline); "
+                         "decode: the decoding step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-table", action="store_true",
                     help="also print per-entry-point times to stderr")
@@ -204,6 +299,9 @@ def main():
               "(the op shards by batch or head with no communication inside it)",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "decode":
+        decode_bench(args)
+        return
 
     cfg = dict(CONFIGS[args.config])
     L = cfg["L"]

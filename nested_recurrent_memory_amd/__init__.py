@@ -7,7 +7,7 @@ gfx950 HIP kernels (libngdn.so, C ABI in include/ngdn.h).
 
 from .chunk import PROMOTIONS, ChunkNestedGDN2Function, chunk_nested_gdn2
 from .schedule import n_firings, n_groups, source_index
-from .step import step_nested_gdn2
+from .step import prepare_step_params, step_nested_gdn2
 
 __all__ = ["chunk_nested_gdn2", "ChunkNestedGDN2Function", "PROMOTIONS",
-           "step_nested_gdn2", "n_firings", "n_groups", "source_index"]
+           "step_nested_gdn2", "prepare_step_params", "n_firings", "n_groups", "source_index"]

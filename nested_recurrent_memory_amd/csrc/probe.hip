@@ -27,7 +27,9 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   // S^T (learned) and then Vals share one buffer
   constexpr int ROWS = (MERGE ? N : (V > N ? V : N));
   __shared__ __attribute__((aligned(16))) float s_buf[ROWS * LD];
-  __shared__ float s_nrm[N], s_gs[K];
+  // per-wave partial sums (each slot has one writer), added in wave order so
+  // that the result does not depend on the order in which waves finish
+  __shared__ float s_nrm[4][N], s_gs[4][K];
   float* s_S = s_buf;      // [V][LD]: S^T, k contiguous
   float* s_V = s_buf;      // [N][LD]: Vals, v contiguous
 
@@ -60,8 +62,8 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
       for (int e = tid; e < V * K; e += 256) s_buf[(e % K) * LD + e / K] = swap[e];
     }
   }
-  for (int e = tid; e < N; e += 256) s_nrm[e] = 0.f;
-  for (int e = tid; e < K; e += 256) s_gs[e] = 0.f;
+  for (int e = tid; e < 4 * N; e += 256) (&s_nrm[0][0])[e] = 0.f;
+  for (int e = tid; e < 4 * K; e += 256) (&s_gs[0][0])[e] = 0.f;
   __syncthreads();
 
   const size_t fo = ((size_t)bh * NF + i);                 // scan-ready firing index
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
       for (int r = 0; r < 4; ++r) s += softplusf_(x[r] - 4.f);
       s += __shfl_xor(s, 16, WAVE);
       s += __shfl_xor(s, 32, WAVE);
-      if (lane < 16) atomicAdd(&s_gs[ct * 16 + lane], s);
+      if (lane < 16) s_gs[wv][ct * 16 + lane] += s;
     }
     // erase gate
     {
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
         s += __shfl_xor(s, 2, WAVE);
         s += __shfl_xor(s, 4, WAVE);
         s += __shfl_xor(s, 8, WAVE);
-        if ((lane & 15) == 0) atomicAdd(&s_nrm[rt * 16 + acc_row(r)], s);
+        if ((lane & 15) == 0) s_nrm[wv][rt * 16 + acc_row(r)] += s;
       }
     }
   }
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
 
   // ---- finalize: g, keys, A = keys*b*e^g, KT = keys^T
   if (tid < K) {
-    const float g = -s_gs[tid] / (float)N;
+    const float g = -(s_gs[0][tid] + s_gs[1][tid] + s_gs[2][tid] + s_gs[3][tid]) / (float)N;
     a.gam[fo * K + tid] = expf(g);
     if (a.go) a.go[ro * K + tid] = g;
   }
@@ -163,14 +165,15 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   for (int t = 0; t < NTK; ++t) {
     const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
     const int k = ct * 16 + acc_col(), n0 = rt * 16 + acc_row(0);
-    const float gam = expf(-s_gs[k] / (float)N);
+    const float gam = expf(-(s_gs[0][k] + s_gs[1][k] + s_gs[2][k] + s_gs[3][k]) / (float)N);
     f4 kv4, av4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = n0 + r;
       float key;
       if (MERGE) key = (n == k) ? 1.f : 0.f;
-      else key = ut[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
+      else key = ut[t][r] / fmaxf(sqrtf(s_nrm[0][n] + s_nrm[1][n] + s_nrm[2][n] + s_nrm[3][n]),
+                                  1e-12f);
       kv4[r] = key;
       av4[r] = key * bt[t][r] * gam;
       Ao[n * K + k] = av4[r];

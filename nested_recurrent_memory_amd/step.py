@@ -17,7 +17,19 @@ import torch
 from . import _lib
 from .chunk import PROMOTIONS, _SUPPORTED_KV, _as_ints, _params, _working_dtype
 
-__all__ = ["step_nested_gdn2"]
+__all__ = ["step_nested_gdn2", "prepare_step_params"]
+
+
+def prepare_step_params(query_banks, key_projections, b_projections, w_projections,
+                        g_projections, dtype):
+    """The per-level parameters in the layouts the step's kernels read (the
+    bank padded to a multiple of 8 rows, the b/w/g projections transposed),
+    for inputs of ``dtype``. A decoding loop prepares them once and passes
+    them as ``params=``; they are a snapshot: prepare again after the
+    parameters change."""
+    wd, _ = _working_dtype(torch.empty(0, dtype=dtype))
+    return _params(query_banks, key_projections, b_projections, w_projections,
+                   g_projections, wd, False)
 
 
 def _validate_step(q, k, v, L, chunk_size, promotion, nq, f, query_banks):
@@ -69,6 +81,9 @@ def step_nested_gdn2(
     scale: float | None = None,
     chunk_size: int = 64,
     promotion: str = "learned",
+    *,
+    params: dict | None = None,
+    inplace: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """One token: level 0 writes, every level is read and mixed, then each
     level whose firing this token completes promotes, bottom-up
@@ -80,6 +95,12 @@ def step_nested_gdn2(
     the firing decision on the GPU: no host synchronisation). Returns o
     [B,H,V] in q's dtype and the new state [B,H,L,K,V] fp32; the state passed
     in is not modified.
+
+    Beyond the reference's arguments: ``params`` takes the output of
+    prepare_step_params (else the parameters are laid out on every call), and
+    ``inplace=True`` updates ``state`` (fp32, contiguous, on the GPU) in place
+    and returns it, which saves writing the upper levels and keeps the buffer
+    fixed for graph capture.
     """
     L = int(L)
     f = _as_ints(firing_intervals, L)
@@ -104,8 +125,13 @@ def step_nested_gdn2(
     if state.shape != (B, H, L, K, V):
         raise ValueError(f"state must be [B, H, L, K, V] = {(B, H, L, K, V)}, "
                          f"got {tuple(state.shape)}")
-    s_in = state.to(device=dev, dtype=torch.float32).contiguous()
-    s_out = torch.empty_like(s_in)
+    if inplace:
+        if state.dtype != torch.float32 or not state.is_contiguous() or state.device != dev:
+            raise ValueError("inplace=True needs a contiguous fp32 state on q's device")
+        s_in = s_out = state
+    else:
+        s_in = state.to(device=dev, dtype=torch.float32).contiguous()
+        s_out = torch.empty_like(s_in)
     o = torch.empty(B, H, V, device=dev, dtype=wd)
 
     pos_t, pos_all = None, 0
@@ -124,8 +150,11 @@ def step_nested_gdn2(
     fs = (ctypes.c_int32 * L)(*f)
     nqs = (ctypes.c_int32 * max(L - 1, 1))(*(nq or [0]))
     if L > 1:
-        par = _params(query_banks, key_projections, b_projections, w_projections,
-                      g_projections, wd, False)
+        par = params if params is not None else _params(
+            query_banks, key_projections, b_projections, w_projections, g_projections, wd,
+            False)
+        if par["qb"].dtype != wd:
+            raise ValueError(f"params were prepared for {par['qb'].dtype}, inputs are {wd}")
         n_pairs = K if merge else max(nq)
         ws = torch.empty(B * H * (3 * n_pairs * K + K), device=dev, dtype=torch.float32)
     d = _lib.dims(B, 1, H, L, K, V, code, scale)

@@ -125,3 +125,44 @@ def test_step_rows_fire_on_device():
     torch.cuda.synchronize()
     up_same = (s[:, :, 1] == state[:, :, 1]).flatten(1).all(1).cpu()
     assert up_same.tolist() == [False, True, False, True]
+
+
+def test_step_graph_replays_match_eager():
+    """One token captured in a HIP graph (in-place state, device position,
+    position += 1 inside the graph) and replayed across firings of both upper
+    levels: every replay equals the eager step bit for bit."""
+    from nested_recurrent_memory_amd import prepare_step_params
+
+    B, H, K, L, f = 2, 2, 64, 3, (1, 1, 2)
+    inp = make_inputs(B=B, T=1, H=H, K=K, V=K, L=L, N=16, intervals=f, seed=21)
+    tok = {n: x.cuda() for n, x in _token(inp, 0).items()}
+    # schedule sizes as host values, as the layer passes them (tuples): a
+    # device tensor would need a host read inside the capture
+    par_in = {n: (inp[n].cuda() if n in PARAMS[:5] else tuple(inp[n].tolist())) for n in PARAMS}
+    par = prepare_step_params(*(par_in[n] for n in PARAMS[:5]), torch.float32)
+    init = _state(B, H, L, K, K, seed=4).cuda()
+    state_g = init.clone()
+    pos = torch.full((B,), 126, dtype=torch.int64, device="cuda")
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):   # warm-up outside capture, then restore
+            step_nested_gdn2(**tok, state=state_g.clone(), position=pos.clone(), **par_in,
+                             L=L, params=par, inplace=True)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            o_g, _ = step_nested_gdn2(**tok, state=state_g, position=pos, **par_in, L=L,
+                                      params=par, inplace=True)
+            pos.add_(1)
+        state_e = init.clone()
+        for r in range(5):
+            graph.replay()
+            torch.cuda.synchronize()
+            o_e, state_e = step_nested_gdn2(**tok, state=state_e, position=126 + r, **par_in,
+                                            L=L)
+            torch.cuda.synchronize()
+            assert torch.equal(o_g, o_e), f"replay {r}: o differs"
+            assert torch.equal(state_g, state_e), f"replay {r}: state differs"
+    assert not torch.equal(state_e[:, :, 2], init[:, :, 2]), "level 2 should have fired"
