@@ -287,6 +287,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
+    ap.add_argument("--stream-groups", type=int, default=None,
+                    help="groups of batch rows run on their own streams (default: the "
+                         "package's STREAM_GROUPS)")
     ap.add_argument("--workload", default="train", choices=("train", "decode"),
                     help="train: forward+backward at --config (the headline); "
                          "decode: the decoding step")
@@ -299,6 +302,9 @@ def main():
               "(the op shards by batch or head with no communication inside it)",
               file=sys.stderr)
         sys.exit(2)
+    if args.stream_groups is not None:
+        from nested_recurrent_memory_amd import chunk as _chunk
+        _chunk.STREAM_GROUPS = args.stream_groups
     if args.workload == "decode":
         decode_bench(args)
         return
@@ -337,8 +343,13 @@ def main():
     model, units = work_model(cfg)
     # per-launch algorithmic work of each entry point; upper levels keyed by
     # level, in call order within a step
+    # the op runs each entry point once per group of batch rows (one stream
+    # per group), so a launch does 1/launches-per-step of the step's work
+    per_launch = {n: args.steps / len(evs) for n, evs in timing.items()}
     dom = max(per_step, key=per_step.get)
     dom_work = model.get(dom)
+    if dom_work is not None:
+        dom_work = tuple(x * per_launch[dom] for x in dom_work)
     roof = None
     if dom_work is not None:
         nbytes, flops = dom_work
@@ -362,6 +373,7 @@ def main():
             extra = ""
             if w:
                 t = ms[n] * 1e-3
+                w = tuple(x * per_launch[n] for x in w)
                 extra = f"  {w[0] / t / 1e9:8.1f} GB/s  {w[1] / t / 1e12:7.2f} TFLOP/s"
             print(f"{n:28s} {per_step[n]:8.3f} ms/step  {ms[n]:8.3f} ms/launch{extra}",
                   file=sys.stderr)

@@ -113,5 +113,9 @@ def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+def ptr_of_stream(st):
+    return ctypes.c_void_p(st.cuda_stream)
+
+
 def dims(B, T, H, L, K, V, dtype_code, scale):
     return Dims(B, T, H, L, K, V, dtype_code, float(scale))

@@ -77,6 +77,47 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
                 f"n_queries={n} exceeds the {query_banks.shape[2]} rows of query_banks")
 
 
+# Batch rows are independent all the way through the op, so the kernels run
+# per group of batch rows, each group on its own stream: the sequential scans
+# of one group (a few workgroups per CU, latency-bound) overlap the chunk
+# kernels of another (throughput-bound) instead of leaving most of the GPU idle.
+STREAM_GROUPS = 1
+_STREAMS = {}
+
+
+def _side_streams(dev, n):
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), n)
+    if key not in _STREAMS:
+        _STREAMS[key] = [torch.cuda.Stream(device=dev) for _ in range(n)]   # default priority
+    return _STREAMS[key]
+
+
+def _run_groups(B, dev, launch):
+    """Calls launch(b0, nb, stream) for each group of batch rows: on the
+    current stream when there is one group, else on side streams forked from
+    and joined back into the current stream."""
+    n = max(1, min(STREAM_GROUPS, B))
+    main = torch.cuda.current_stream(dev)
+    if n == 1:
+        launch(0, B, main)
+        return
+    size = -(-B // n)
+    spans = [(b0, min(size, B - b0)) for b0 in range(0, B, size)]
+    side = _side_streams(dev, len(spans))
+    fork = main.record_event()
+    for (b0, nb), st in zip(spans, side):
+        st.wait_event(fork)
+        with torch.cuda.stream(st):
+            launch(b0, nb, st)
+    for st in side[:len(spans)]:
+        main.wait_stream(st)
+
+
+def _rows(b0, nb):
+    """View of batch rows [b0, b0 + nb) of a batch-leading tensor (None stays None)."""
+    return lambda t: None if t is None else t[b0:b0 + nb]
+
+
 def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
              init, promotion, train):
     """Runs the forward kernels. Returns (o, final_state [B,H,L,K,V] fp32,
@@ -90,28 +131,20 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     q_, k_, v_, b_, w_, mix_ = (cvt(x) for x in (q, k, v, b, w, mix))
     g_ = g.to(torch.float32).contiguous()
     init_ = init.to(torch.float32).contiguous() if init is not None else None
-    d = _lib.dims(B, T, H, L, K, V, code, scale)
-    st = _lib.stream_of(q_)
-    P = _lib.ptr
     e = lambda *s, dt=wd: torch.empty(*s, device=dev, dtype=dt)  # noqa: E731
     # working tensors between the kernels are fp32 whatever the input dtype
     f32 = lambda *s: e(*s, dt=torch.float32)  # noqa: E731
     opt = lambda *s: f32(*s) if train else None  # noqa: E731
 
+    # everything is allocated here, on the current stream, before any launch
     W, U, Qg = f32(B, H, NT, 64, K), f32(B, H, NT, 64, V), f32(B, H, NT, 64, K)
     KtT, Aqk = f32(B, H, NT, K, 64), f32(B, H, NT, 64, 64)
     gam = f32(B, H, NT, K)
     Kt, WT, QgT = opt(B, H, NT, 64, K), opt(B, H, NT, K, 64), opt(B, H, NT, K, 64)
     AqkT, TT = opt(B, H, NT, 64, 64), opt(B, H, NT, 64, 64)
-    _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
-              P(W), P(U), P(KtT), P(Qg), P(Aqk), P(gam), P(Kt), P(WT), P(QgT), P(AqkT),
-              P(TT), st)
     hT, vnT = f32(B, H, NT, V, K), f32(B, H, NT, V, 64)
     h_, vn_ = opt(B, H, NT, K, V), opt(B, H, NT, 64, V)
     final = torch.empty(B, H, L, K, V, device=dev, dtype=torch.float32)
-    _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), P(W), P(U), P(KtT), P(gam), P(init_),
-              P(hT), P(vnT), P(h_), P(vn_), P(final), st)
-
     states = [None] * L       # group states as rows [B,NG,H,K,V]
     statesT = [None] * L      # and transposed [B,NG,H,V,K]
     levels = [None] * L
@@ -120,39 +153,50 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     if L > 1:
         par = _params(qb, kp, bp, wp, gp, wd, train)
     for lvl in range(1, L):
-        fh, fb = f[lvl], f[lvl - 1]
-        nf, ng = n_firings(NT, fh), n_groups(NT, fh)
+        nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         N = K if merge else nq[lvl - 1]
         nf1 = max(nf, 1)
-        A_, KT_, U_ = f32(B, H, nf1, N, K), f32(B, H, nf1, K, N), f32(B, H, nf1, N, V)
-        gm_ = f32(B, H, nf1, K)
-        keysN, AT_ = opt(B, H, nf1, N, K), opt(B, H, nf1, K, N)
-        below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
-        if nf > 0:
-            _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
-                      P(below), ngb, P(final), P(par["qb"]), par["nmax"], P(par["kp"]),
-                      P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(A_), P(KT_), P(U_),
-                      P(gm_), P(keysN), P(AT_), None, None, None, None, None, st,
-                      tag=f"ngdn_probe_fwd.{lvl}")
-        S_l, ST_l = f32(B, ng, H, K, V), f32(B, ng, H, V, K)
-        _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, N, nf, ng, P(A_), P(KT_),
-                  P(U_), P(gm_), P(init_), P(S_l), P(ST_l), P(final), st,
-                  tag=f"ngdn_upper_scan_fwd.{lvl}")
-        states[lvl], statesT[lvl] = S_l, ST_l
-        levels[lvl] = dict(N=N, nf=nf, ng=ng, keys=keysN, AT=AT_, gam=gm_)
-
+        levels[lvl] = dict(N=N, nf=nf, ng=ng, A=f32(B, H, nf1, N, K), KT=f32(B, H, nf1, K, N),
+                           U=f32(B, H, nf1, N, V), gam=f32(B, H, nf1, K),
+                           keys=opt(B, H, nf1, N, K), AT=opt(B, H, nf1, K, N))
+        states[lvl], statesT[lvl] = f32(B, ng, H, K, V), f32(B, ng, H, V, K)
     o = e(B, T, H, V)
     read0 = f32(B, T, H, V) if train else None
-    spT, ngs, fs = _level_arrays(statesT, NT, f, L)
-    _lib.call("ngdn_output_fwd", ctypes.byref(d), P(Qg), P(Aqk), P(hT), P(vnT), P(q_),
-              P(mix_), spT, ngs, fs, P(o), P(read0), st)
+    P = _lib.ptr
+
+    def launch(b0, nb, st):
+        R = _rows(b0, nb)
+        sp = _lib.ptr_of_stream(st)
+        d = _lib.dims(nb, T, H, L, K, V, code, scale)
+        _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT)), sp)
+        _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+            W, U, KtT, gam, init_, hT, vnT, h_, vn_, final)), sp)
+        for lvl in range(1, L):
+            lv = levels[lvl]
+            fh, fb = f[lvl], f[lvl - 1]
+            below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
+            if lv["nf"] > 0:
+                _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), lv["N"], fb, fh,
+                          P(R(below)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
+                          P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
+                          *(P(R(lv[x])) for x in ("A", "KT", "U", "gam", "keys", "AT")),
+                          None, None, None, None, None, sp, tag=f"ngdn_probe_fwd.{lvl}")
+            _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, lv["N"], lv["nf"], lv["ng"],
+                      *(P(R(lv[x])) for x in ("A", "KT", "U", "gam")), P(R(init_)),
+                      P(R(states[lvl])), P(R(statesT[lvl])), P(R(final)), sp,
+                      tag=f"ngdn_upper_scan_fwd.{lvl}")
+        spT, ngs, fs = _level_arrays([R(x) for x in statesT], NT, f, L)
+        _lib.call("ngdn_output_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+            Qg, Aqk, hT, vnT, q_, mix_)), spT, ngs, fs, P(R(o)), P(R(read0)), sp)
+
+    _run_groups(B, dev, launch)
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
                      KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
                      hT=hT, vnT=vnT, h=h_, vn=vn_, read0=read0, states=states,
-                     statesT=statesT,
-                     levels=levels, final=final, par=par,
+                     statesT=statesT, levels=levels, final=final, par=par,
                      code=code, wd=wd)
     return o, final, saved
 
@@ -192,85 +236,95 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     dev = q_.device
     wd, code = sv["wd"], sv["code"]
     NT = -(-T // 64)
-    d = _lib.dims(B, T, H, L, K, V, code, scale)
-    st = _lib.stream_of(q_)
     P = _lib.ptr
     e = lambda *s, dt=wd: torch.empty(*s, device=dev, dtype=dt)  # noqa: E731
+    f32 = lambda *s: e(*s, dt=torch.float32)  # noqa: E731
     z32 = lambda *s: torch.zeros(*s, device=dev, dtype=torch.float32)  # noqa: E731
     do_ = do.to(wd).contiguous()
     merge = promotion == "merge"
     states, levels, par, final = sv["states"], sv["levels"], sv["par"], sv["final"]
 
-    # reads: dmix for every level (level 0 from the stored read), dq and the
-    # group-state gradients for levels >= 1
+    # everything is allocated (and zeroed) here, on the current stream
     dq = e(B, T, H, L, K)
-    dmix = e(B, T, H, L, dt=torch.float32)
-    _lib.call("ngdn_output_bwd", ctypes.byref(d), P(sv["read0"]), P(do_), P(dmix), st)
-
+    dmix = f32(B, T, H, L)
     d_final = (dfinal.to(torch.float32).contiguous().clone() if dfinal is not None
                else z32(B, H, L, K, V))
     d_init = z32(B, H, L, K, V) if has_init else None
-    d_states = [None] * L
-    for lvl in range(1, L):
-        ng = n_groups(NT, f[lvl])
-        d_states[lvl] = e(B, ng, H, K, V, dt=torch.float32)
-        _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng, P(q_), P(mix_),
-                  P(do_), P(states[lvl]), P(d_states[lvl]), P(dq), P(dmix), st,
-                  tag=f"ngdn_read_state_bwd.{lvl}")
-
+    d_states = [None] + [f32(B, n_groups(NT, f[lvl]), H, K, V) for lvl in range(1, L)]
     dqb = dkp = dbp = dwp = dgp = None
-    inj, nf1 = None, 0
+    work = [None] * L
     if L > 1:
-        nmax8 = par["nmax"]
-        dqb = z32(L - 1, H, nmax8, K)
+        dqb = z32(L - 1, H, par["nmax"], K)
         dkp, dbp = z32(L - 1, H, K, V), z32(L - 1, H, V, K)
         dwp, dgp = z32(L - 1, H, V, V), z32(L - 1, H, V, K)
-    for lvl in range(L - 1, 0, -1):
+    for lvl in range(1, L):
         lv = levels[lvl]
-        N, nf, ng = lv["N"], lv["nf"], lv["ng"]
+        N, nf = lv["N"], lv["nf"]
         nfa = max(nf, 1)
-        dSp = e(B, H, nfa, K, V, dt=torch.float32)
-        dvn = e(B, H, nfa, N, V, dt=torch.float32)
-        _lib.call("ngdn_upper_scan_bwd", ctypes.byref(d), lvl, N, nf, ng, P(lv["keys"]),
-                  P(lv["AT"]), P(lv["gam"]), P(d_states[lvl]), P(d_final), P(dSp), P(dvn),
-                  P(d_init), st, tag=f"ngdn_upper_scan_bwd.{lvl}")
-        if nf == 0:
-            continue
-        ws = ([e(B, H, nf, N, K, dt=torch.float32) for _ in range(4)]
-              + [e(B, H, nf, N, V, dt=torch.float32) for _ in range(2)])
-        fh, fb = f[lvl], f[lvl - 1]
-        if lvl == 1:
-            inj, nf1 = e(B, H, nf, K, V, dt=torch.float32), nf
-            b_kv, b_vk, ngb, d_below = sv["h"], sv["hT"], NT, None
-        else:
-            b_kv, b_vk = states[lvl - 1], sv["statesT"][lvl - 1]
-            ngb, d_below = n_groups(NT, fb), d_states[lvl - 1]
-        _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh, P(b_kv),
-                  P(b_vk), ngb, P(final), P(par["qb"]), par["nmax"], P(par["kp"]),
-                  P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(par["kpT"]), P(par["bankT"]),
-                  P(par["bp"]), P(par["wp"]), P(par["gp"]), P(states[lvl]),
-                  P(sv["statesT"][lvl]), ng, P(dSp), P(dvn), *(P(x) for x in ws), P(dqb),
-                  P(inj if lvl == 1 else None), P(d_below), P(d_final), st,
-                  tag=f"ngdn_probe_bwd.{lvl}")
-        _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf, P(ws[0]),
-                  P(ws[1]), P(ws[2]), P(ws[3]), P(ws[4]), P(dkp), P(dbp), P(dwp), P(dgp), st,
-                  tag=f"ngdn_param_grads.{lvl}")
-
-    # level 0
-    f32 = lambda *s: e(*s, dt=torch.float32)  # noqa: E731
+        work[lvl] = dict(dSp=f32(B, H, nfa, K, V), dvn=f32(B, H, nfa, N, V),
+                         ws=[f32(B, H, nfa, N, K) for _ in range(4)]
+                         + [f32(B, H, nfa, N, V) for _ in range(2)],
+                         inj=f32(B, H, nfa, K, V) if lvl == 1 else None)
     dSp0, dVn0, dVnT0 = f32(B, H, NT, K, V), f32(B, H, NT, 64, V), f32(B, H, NT, V, 64)
-    _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), P(sv["Kt"]), P(sv["WT"]), P(sv["gam"]),
-              P(sv["AqkT"]), P(sv["QgT"]), P(do_), P(mix_), f[1] if L > 1 else 1, P(inj), nf1,
-              P(d_final), P(dSp0), P(dVn0), P(dVnT0), P(d_init), st)
     dQg, dKt, dWT = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K), f32(B, H, NT, K, 64)
     dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
-    _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(sv["h"]), P(dSp0), P(sv["vn"]), P(dVn0),
-              P(do_), P(mix_), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam), st)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
-    dg = e(B, T, H, K, dt=torch.float32)
-    _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), P(q_), P(k_), P(v_), P(g_), P(b_), P(w_),
-              P(sv["W"]), P(sv["U"]), P(sv["TT"]), P(dQg), P(dWT), P(dKt), P(dAqk), P(dgam),
-              P(dVnT0), P(dq), P(dk), P(dv), P(dg), P(db), P(dw), st)
+    dg = f32(B, T, H, K)
+
+    def launch(b0, nb, st):
+        R = _rows(b0, nb)
+        sp = _lib.ptr_of_stream(st)
+        d = _lib.dims(nb, T, H, L, K, V, code, scale)
+        # reads: dmix for every level (level 0 from the stored read), dq and the
+        # group-state gradients for levels >= 1
+        _lib.call("ngdn_output_bwd", ctypes.byref(d), P(R(sv["read0"])), P(R(do_)),
+                  P(R(dmix)), sp)
+        for lvl in range(1, L):
+            ng = n_groups(NT, f[lvl])
+            _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng,
+                      *(P(R(x)) for x in (q_, mix_, do_, states[lvl], d_states[lvl], dq, dmix)),
+                      sp, tag=f"ngdn_read_state_bwd.{lvl}")
+        inj, nf1 = None, 0
+        for lvl in range(L - 1, 0, -1):
+            lv, wk = levels[lvl], work[lvl]
+            N, nf, ng = lv["N"], lv["nf"], lv["ng"]
+            _lib.call("ngdn_upper_scan_bwd", ctypes.byref(d), lvl, N, nf, ng,
+                      *(P(R(x)) for x in (lv["keys"], lv["AT"], lv["gam"], d_states[lvl],
+                                          d_final, wk["dSp"], wk["dvn"], d_init)),
+                      sp, tag=f"ngdn_upper_scan_bwd.{lvl}")
+            if nf == 0:
+                continue
+            fh, fb = f[lvl], f[lvl - 1]
+            if lvl == 1:
+                inj, nf1 = wk["inj"], nf
+                b_kv, b_vk, ngb, d_below = sv["h"], sv["hT"], NT, None
+            else:
+                b_kv, b_vk = states[lvl - 1], sv["statesT"][lvl - 1]
+                ngb, d_below = n_groups(NT, fb), d_states[lvl - 1]
+            ws = wk["ws"]
+            _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
+                      P(R(b_kv)), P(R(b_vk)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
+                      P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
+                      P(par["kpT"]), P(par["bankT"]), P(par["bp"]), P(par["wp"]),
+                      P(par["gp"]), P(R(states[lvl])), P(R(sv["statesT"][lvl])), ng,
+                      P(R(wk["dSp"])), P(R(wk["dvn"])), *(P(R(x)) for x in ws), P(dqb),
+                      P(R(wk["inj"])), P(R(d_below)), P(R(d_final)), sp,
+                      tag=f"ngdn_probe_bwd.{lvl}")
+            _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf,
+                      *(P(R(x)) for x in ws[:5]), P(dkp), P(dbp), P(dwp), P(dgp), sp,
+                      tag=f"ngdn_param_grads.{lvl}")
+        # level 0
+        _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
+            "Kt", "WT", "gam", "AqkT", "QgT")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
+            P(R(inj)), nf1, P(R(d_final)), P(R(dSp0)), P(R(dVn0)), P(R(dVnT0)), P(R(d_init)), sp)
+        _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(R(sv["h"])), P(R(dSp0)),
+                  P(R(sv["vn"])), P(R(dVn0)), P(R(do_)), P(R(mix_)),
+                  *(P(R(x)) for x in (dQg, dWT, dKt, dAqk, dgam)), sp)
+        _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), *(P(R(x)) for x in (
+            q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], dQg, dWT, dKt, dAqk, dgam,
+            dVnT0, dq, dk, dv, dg, db, dw)), sp)
+
+    _run_groups(B, dev, launch)
     return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
 
 

@@ -20,14 +20,26 @@ namespace ngdn {
 
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
+  // Per (b, h, chunk), in halves of V: S[:, half] and dS'[:, half] are staged
+  // once as split tiles (each value split by one thread, not by every wave
+  // that reads it); every product accumulates over the halves. dgam, a plain
+  // fp32 dot product, is summed from the fp32 values while they are staged.
   constexpr int C = CH;
-  constexpr int LDV = V + 4;
+  constexpr int VH = V > 64 ? 64 : V;          // columns of V per half
+  constexpr int NHV = V / VH;
+  using ST = SplitTile<E>;
+  constexpr int LDH = VH + ST::PAD;
   constexpr int CTK = K / 16;
   constexpr int KS = Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
-  constexpr int NKV = V / KS;
+  constexpr int NKH = VH / KS;                 // k-steps per half
+  constexpr int Q4 = VH / 4;                   // 16-byte groups per staged row
+  constexpr int SIT = K * Q4 / 256;            // staged groups per thread per tensor
+  static_assert(K * Q4 % 256 == 0 && 256 % Q4 == 0, "staging covers whole rows");
   typedef typename Mma<E>::SFrag SF;
-  __shared__ __attribute__((aligned(16))) float s_S[K * LDV];   // S rows (v contiguous)
+  __shared__ __attribute__((aligned(16))) typename ST::T s_s[ST::NPLANE * K * LDH];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_d[ST::NPLANE * K * LDH];
+  const ST sS{s_s, K * LDH}, sD{s_d, K * LDH};
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -37,8 +49,8 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   const int nvalid = min(C, T - t0);
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const size_t cix = (size_t)bh * NT + n;
-
-  stage_f32(s_S, LDV, a.h + cix * K * V, V, K, V);
+  const float* Sg = a.h + cix * K * V;
+  const float* dsp = a.dSp + cix * K * V;
 
   // A fragments of this wave's 16 rows: dO (from do and mix_0), dVn, Vn
   const int ri = wv * 16 + (lane & 15);
@@ -47,66 +59,94 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   const float m0 = ri < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + ri) * H * a.L + (size_t)h * a.L]) : 0.f;
   const float* dvn = a.dVn + cix * C * V + (size_t)ri * V;
   const float* vnc = a.vn + cix * C * V;
-  SF fo[NKV], fd[NKV], fv[NKV];
+
+  f4 aq[CTK], aw[CTK], ak[CTK], adq[4];
 #pragma unroll
-  for (int s = 0; s < NKV; ++s) {
-    const int v0 = s * KS + kofs<E>(lane);
-    float x[KPL];
-    ld_vals<E>(dop + v0, x);
-    fo[s] = Mma<E>::makes([&](int e) { return x[e] * m0; });
-    fd[s] = Mma<E>::ld(dvn + v0);
-    fv[s] = Mma<E>::ld(vnc + (size_t)ri * V + v0);
+  for (int ct = 0; ct < CTK; ++ct) { aq[ct] = f4_zero(); aw[ct] = f4_zero(); ak[ct] = f4_zero(); }
+#pragma unroll
+  for (int J = 0; J < 4; ++J) adq[J] = f4_zero();
+  float dg[SIT];
+#pragma unroll
+  for (int i = 0; i < SIT; ++i) dg[i] = 0.f;
+
+#pragma unroll 1
+  for (int hv = 0; hv < NHV; ++hv) {
+    const int vb = hv * VH;
+    if (hv) __syncthreads();                   // the previous half's reads are done
+#pragma unroll
+    for (int i = 0; i < SIT; ++i) {
+      const int e = tid + 256 * i, k = e / Q4, c = (e % Q4) * 4;
+      const f4 x = *reinterpret_cast<const f4*>(Sg + (size_t)k * V + vb + c);
+      const f4 y = *reinterpret_cast<const f4*>(dsp + (size_t)k * V + vb + c);
+      dg[i] += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+      sS.put4(k * LDH + c, x);
+      sD.put4(k * LDH + c, y);
+    }
+    SF fo[NKH], fd[NKH], fv[NKH];
+#pragma unroll
+    for (int s = 0; s < NKH; ++s) {
+      const int v0 = vb + s * KS + kofs<E>(lane);
+      float x[KPL];
+      ld_vals<E>(dop + v0, x);
+      fo[s] = Mma<E>::makes([&](int e) { return x[e] * m0; });
+      fd[s] = Mma<E>::ld(dvn + v0);
+      fv[s] = Mma<E>::ld(vnc + (size_t)ri * V + v0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ct = 0; ct < CTK; ++ct) {
+      const int row = (ct * 16 + (lane & 15)) * LDH + kofs<E>(lane);
+#pragma unroll
+      for (int s = 0; s < NKH; ++s) {
+        const SF sb = sS.get(row + s * KS);
+        aq[ct] = Mma<E>::mma(aq[ct], fo[s], sb);
+        aw[ct] = Mma<E>::mma(aw[ct], fd[s], sb);
+        ak[ct] = Mma<E>::mma(ak[ct], fv[s], sD.get(row + s * KS));
+      }
+    }
+    // dAqk = dO Vn^T, lower including the diagonal (Vn rows from global)
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      if (J <= wv) {
+        const float* vrow = vnc + (size_t)(J * 16 + (lane & 15)) * V + vb + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < NKH; ++s) adq[J] = Mma<E>::mma(adq[J], fo[s], Mma<E>::ld(vrow + s * KS));
+      }
+    }
   }
-  __syncthreads();
-  const float* dsp = a.dSp + cix * K * V;
+
   float* dQg = a.dQg + cix * C * K;
   float* dWT = a.dWT + cix * K * C;
   float* dKt = a.dKt + cix * C * K;
-#pragma unroll 2
-  for (int ct = 0; ct < CTK; ++ct) {
-    f4 aq = f4_zero(), aw = f4_zero(), ak = f4_zero();
-    const float* srow = s_S + (ct * 16 + (lane & 15)) * LDV + kofs<E>(lane);
-    const float* drow = dsp + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
 #pragma unroll
-    for (int s = 0; s < NKV; ++s) {
-      const SF sb = Mma<E>::ld(srow + s * KS);
-      aq = Mma<E>::mma(aq, fo[s], sb);
-      aw = Mma<E>::mma(aw, fd[s], sb);
-      ak = Mma<E>::mma(ak, fv[s], Mma<E>::ld(drow + s * KS));
-    }
+  for (int ct = 0; ct < CTK; ++ct) {
     const int i0 = wv * 16 + acc_row(0), k = ct * 16 + acc_col();
+    f4 w;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      dQg[(i0 + r) * K + k] = aq[r];
-      dKt[(i0 + r) * K + k] = ak[r];
-      aw[r] = -aw[r];
+      dQg[(i0 + r) * K + k] = aq[ct][r];
+      dKt[(i0 + r) * K + k] = ak[ct][r];
+      w[r] = -aw[ct][r];
     }
-    *reinterpret_cast<f4*>(dWT + k * C + i0) = aw;
+    *reinterpret_cast<f4*>(dWT + k * C + i0) = w;
   }
-  // dAqk = dO Vn^T, lower including the diagonal (Vn rows from global)
   float* dAq = a.dAqk + cix * C * C;
-  for (int J = 0; J < 4; ++J) {
-    f4 acc = f4_zero();
-    if (J <= wv) {
-      const float* vrow = vnc + (size_t)(J * 16 + (lane & 15)) * V + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < NKV; ++s) acc = Mma<E>::mma(acc, fo[s], Mma<E>::ld(vrow + s * KS));
-    }
+  for (int J = 0; J < 4; ++J) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
-      dAq[i * C + j] = j <= i ? acc[r] : 0.f;
+      dAq[i * C + j] = j <= i ? adq[J][r] : 0.f;
     }
   }
-  // dgam_k = sum_v dS'[k][v] S[k][v]
-  {
-    constexpr int TPK = 256 / K;           // threads per row k
-    const int k = tid / TPK, part = tid % TPK;
-    float s = 0.f;
-    for (int v = part; v < V; v += TPK) s += dsp[(size_t)k * V + v] * s_S[k * LDV + v];
+  // dgam_k = sum_v dS'[k][v] S[k][v]: the Q4 threads of row k are adjacent lanes
 #pragma unroll
-    for (int o = 1; o < TPK; o <<= 1) s += __shfl_xor(s, o, WAVE);
-    if (part == 0) a.dgam[cix * K + k] = s;
+  for (int i = 0; i < SIT; ++i) {
+    float x = dg[i];
+#pragma unroll
+    for (int o = 1; o < Q4; o <<= 1) x += __shfl_xor(x, o, WAVE);
+    const int e = tid + 256 * i;
+    if (e % Q4 == 0) a.dgam[cix * K + e / Q4] = x;
   }
 }
 
@@ -273,7 +313,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
         for (int ct = 0; ct < CTH; ++ct) {
           const int kl = ct * 16 + (lane & 15);
-          const float fb = KV(j, kl) * expf(fminf(s_g[R0 * GH + kl] - s_g[j * GH + kl], 88.f));
+          const float fb = KV(j, kl) * fexp(fminf(s_g[R0 * GH + kl] - s_g[j * GH + kl], 88.f));
           dbk[ct] = MF::mma(dbk[ct], fa, fb);
           dqa[ct] = MF::mma(dqa[ct], fq, fb);
         }
@@ -284,11 +324,11 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = R0 + acc_row(r);
-          const float f = expf(s_g[i * GH + kl] - s_g[R0 * GH + kl]);
+          const float f = fexp(s_g[i * GH + kl] - s_g[R0 * GH + kl]);
           float xb = dbk[ct][r] * f, xq = dqa[ct][r] * f;
           if (!safe) {
             for (int j = R0; j <= i; ++j) {
-              const float d = KV(j, kl) * expf(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
+              const float d = KV(j, kl) * fexp(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
               if (j < i) xb += s_dA[i * AT_LD + j] * d;
               xq += s_dQ[i * AT_LD + j] * d;
             }
@@ -315,7 +355,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
         for (int ct = 0; ct < CTH; ++ct) {
           const int kl = ct * 16 + (lane & 15);
-          const float d = expf(fminf(s_g[i * GH + kl] - s_g[RE * GH + kl], 88.f));
+          const float d = fexp(fminf(s_g[i * GH + kl] - s_g[RE * GH + kl], 88.f));
           dka[ct] = MF::mma(dka[ct], fa, BV(i, kl) * KV(i, kl) * d);
           dka[ct] = MF::mma(dka[ct], fq, QV(i, kl) * in.scale * d);
         }
@@ -326,10 +366,10 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = R0 + acc_row(r);
-          float x = dka[ct][r] * expf(s_g[RE * GH + kl] - s_g[j * GH + kl]);
+          float x = dka[ct][r] * fexp(s_g[RE * GH + kl] - s_g[j * GH + kl]);
           if (!safe) {
             for (int i = j; i < R0 + 16; ++i) {
-              const float d = expf(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
+              const float d = fexp(fminf(s_g[i * GH + kl] - s_g[j * GH + kl], 0.f));
               x += (s_dA[i * AT_LD + j] * BV(i, kl) * KV(i, kl) +
                     s_dQ[i * AT_LD + j] * QV(i, kl) * in.scale) * d;
             }
@@ -350,7 +390,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int i = R0 + acc_row(r);
         const float gcv = s_g[i * GH + kl];
-        const float eg = expf(gcv), ekt = expf(glast - gcv);
+        const float eg = fexp(gcv), ekt = fexp(glast - gcv);
         const float bi = BV(i, kl), ki = KV(i, kl), qh = QV(i, kl) * in.scale;
         const float gq = dQg[i * K + kc], gk = dKt[i * K + kc];
         const float xw = dxw[p * CTH + ct][r];
@@ -377,7 +417,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     // every Kt and gam
     if (tid < NH) {
       const int kc = c0 + tid;
-      float run = s_col[kc] + dgam[kc] * expf(s_gl[kc]);
+      float run = s_col[kc] + dgam[kc] * fexp(s_gl[kc]);
       for (int i = C - 1; i >= 0; --i) {
         run += s_g[i * GH + tid];
         if (i < nvalid) dgo[(size_t)(t0 + i) * H * K + kc] = run;

@@ -160,19 +160,19 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
 #pragma unroll
     for (int e = 0; e < KPL; ++e) gi[e] = s_gc[ri * GL + c0 + e];
     lf[s] = Mma<E>::makes([&](int e) {
-      return bv[e] * kv[e] * expf(gi[e] - s_gc[r * GL + c0 + e]);
+      return bv[e] * kv[e] * fexp(gi[e] - s_gc[r * GL + c0 + e]);
     });
     if (want_q || ro.Qg) in.vals(in.q, in.rowQ, ri, c0, qv);
     if (want_q) {
       qf[s] = Mma<E>::makes([&](int e) {
-        return qv[e] * in.scale * expf(gi[e] - s_gc[r * GL + c0 + e]);
+        return qv[e] * in.scale * fexp(gi[e] - s_gc[r * GL + c0 + e]);
       });
     }
     if (ro.Qg) {
 #pragma unroll
       for (int e = 0; e < KPL; ++e) {
-        const float qg = qv[e] * in.scale * expf(gi[e]);
-        const float kt = kv[e] * expf(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
+        const float qg = qv[e] * in.scale * fexp(gi[e]);
+        const float kt = kv[e] * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
         ro.Qg[ri * K + c0 + e] = qg;
         if (ro.QgT) ro.QgT[(c0 + e) * CH + ri] = qg;
         if (ro.Kt) ro.Kt[ri * K + c0 + e] = kt;
@@ -191,7 +191,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
         in.vals(in.k, in.rowK, rj, c0, kv);
         const SF kf = Mma<E>::makes([&](int e) {
           const float x = s_gc[r * GL + c0 + e] - s_gc[rj * GL + c0 + e];
-          return kv[e] * expf(J < I ? x : fminf(x, 88.f));
+          return kv[e] * fexp(J < I ? x : fminf(x, 88.f));
         });
         accA = Mma<E>::mma(accA, lf[s], kf);
         if (want_q) accQ = Mma<E>::mma(accQ, qf[s], kf);
@@ -204,7 +204,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
           float sa = 0.f, sq = 0.f;
           if (j <= i) {
             for (int c = 0; c < K; ++c) {
-              const float d = expf(fminf(s_gc[i * GL + c] - s_gc[j * GL + c], 0.f));
+              const float d = fexp(fminf(s_gc[i * GL + c] - s_gc[j * GL + c], 0.f));
               const float kj = in.K_(j, c);
               sa += in.B_(i, c) * in.K_(i, c) * kj * d;
               if (want_q) sq += in.Q_(i, c) * kj * d;
@@ -284,7 +284,7 @@ __device__ __forceinline__ void l0_build_X(float* s_X, const float* s_gc, const 
   const int tid = threadIdx.x;
   for (int e = tid; e < CH * K; e += 256) {
     const int c = e / K, kk = e % K;
-    s_X[kk * LDX + c] = in.B_(c, kk) * in.K_(c, kk) * expf(s_gc[c * (K + GCP) + kk]);
+    s_X[kk * LDX + c] = in.B_(c, kk) * in.K_(c, kk) * fexp(s_gc[c * (K + GCP) + kk]);
   }
   for (int e = tid; e < CH * V; e += 256) {
     const int c = e / V, vv = e % V;

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
               a.Kt ? a.Kt + cix * C * K : nullptr, a.KtT + cix * K * C};
     l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr, ro);
   }
-  if (tid < K) a.gam[cix * K + tid] = expf(s_gc[(C - 1) * GL + tid]);
+  if (tid < K) a.gam[cix * K + tid] = fexp(s_gc[(C - 1) * GL + tid]);
   __syncthreads();
 
   // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       in.vec16(in.b, in.rowK, m, c, bv);
       in.vec16(in.k, in.rowK, m, c, kv);
 #pragma unroll
-      for (int j = 0; j < VE; ++j) s_xw[m * GL + c + j] = bv[j] * kv[j] * expf(s_xw[m * GL + c + j]);
+      for (int j = 0; j < VE; ++j) s_xw[m * GL + c + j] = bv[j] * kv[j] * fexp(s_xw[m * GL + c + j]);
     }
     for (int e = tid; e < C * V / VE; e += 256) {
       const int m = e / (V / VE), c = (e % (V / VE)) * VE;

@@ -135,6 +135,49 @@ template <> struct Mma<float> {
   __device__ __forceinline__ static float szero() { return 0.f; }
 };
 
+// An LDS tile of derived (fp32) values kept in the form the matrix core
+// reads. For bf16 MFMAs: two bf16 planes, hi then lo (plane elements apart),
+// so each value is split once by the wave that writes it rather than by every
+// wave that reads it; for fp32 MFMAs: one fp32 plane. Rows are padded by PAD
+// elements (16 bytes) so fragment reads stay 16-byte aligned.
+template <typename E> struct SplitTile;
+template <> struct SplitTile<bf16> {
+  typedef bf16 T;
+  static constexpr int NPLANE = 2, PAD = 8;
+  T* p; int plane;
+  // four consecutive values at element offset off (off % 4 == 0)
+  __device__ __forceinline__ void put4(int off, f4 x) const {
+    bf16x4 h, l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = Mma<bf16>::hi_of(x[e]);
+      l[e] = Mma<bf16>::lo_of(x[e], h[e]);
+    }
+    *reinterpret_cast<bf16x4*>(p + off) = h;
+    *reinterpret_cast<bf16x4*>(p + plane + off) = l;
+  }
+  __device__ __forceinline__ void put1(int off, float x) const {
+    const bf16 h = Mma<bf16>::hi_of(x);
+    p[off] = h;
+    p[plane + off] = Mma<bf16>::lo_of(x, h);
+  }
+  // the KPL values of one fragment from element offset off (off % 8 == 0)
+  __device__ __forceinline__ Mma<bf16>::SFrag get(int off) const {
+    return Mma<bf16>::SFrag{*reinterpret_cast<const bf16x8*>(p + off),
+                            *reinterpret_cast<const bf16x8*>(p + plane + off)};
+  }
+};
+template <> struct SplitTile<float> {
+  typedef float T;
+  static constexpr int NPLANE = 1, PAD = 4;
+  T* p; int plane;
+  __device__ __forceinline__ void put4(int off, f4 x) const {
+    *reinterpret_cast<f4*>(p + off) = x;
+  }
+  __device__ __forceinline__ void put1(int off, float x) const { p[off] = x; }
+  __device__ __forceinline__ float get(int off) const { return p[off]; }
+};
+
 template <typename E> __device__ __forceinline__ int kofs(int lane) {
   return Mma<E>::KPL * (lane >> 4);
 }
@@ -257,6 +300,15 @@ __device__ __forceinline__ void stage_state_T(float* dst, int ld, const float* S
 }
 
 // ---------------------------------------------------------------- misc
+
+// e^x on the hardware exp2 (v_exp_f32): x log2(e) rounded once, so the
+// relative error is about |x| 2^-24 ln 2 on top of exp2's own (under 1e-6
+// for the |x| < 20 of the decay factors, 5e-6 at the 88 clamp); a quarter of
+// the instructions of the library expf, which dominated the chunk kernels'
+// VALU time.
+__device__ __forceinline__ float fexp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) {

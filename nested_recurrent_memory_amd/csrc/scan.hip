@@ -20,27 +20,41 @@
 // product is three bf16 MFMAs on split operands.
 #include "ngdn_kernels.h"
 
+#ifndef SCAN_WAVES_128
+#define SCAN_WAVES_128 4
+#endif
+
 namespace ngdn {
 
-template <typename E, int K, int M>
-__global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
-  constexpr int BV = SCAN_BV;
+template <typename E, int K, int M, int BV, int NWV>
+__global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
-  constexpr int TPW = RTS * CT / 4;           // state tiles per wave
-  constexpr int TRT = TPW / CT;               // distinct state row tiles per wave
+  constexpr int TPW = RTS * CT / NWV;         // state tiles per wave
+  constexpr int TRT = (TPW + CT - 1) / CT;    // distinct state row tiles per wave
   constexpr int RTV = M / 16;                 // Vn row tiles
-  constexpr int RPW = (RTV + 3) / 4;          // Vn row tiles per wave (at most)
-  constexpr int LDS_ST = K + 4;
-  constexpr int LDS_VN = M + 4;
+  // Vn tiles of a wave, p < NVP: when the waves cover the row tiles a whole
+  // number of times (ONE_RT), tile g = wv + NWV p at rt = g % RTV, ct = g / RTV
+  // (one row tile per wave); otherwise row tiles wv + NWV q, every column.
+  constexpr int NVT = RTV * CT;
+  constexpr int NVP = (NVT + NWV - 1) / NWV;
+  constexpr bool ONE_RT = (NWV % RTV) == 0;
+  constexpr int NAR = ONE_RT ? 1 : RTV / NWV; // A row tiles held per wave
+  using ST = SplitTile<E>;
+  constexpr int LDS_ST = K + ST::PAD;
+  constexpr int LDS_VN = M + ST::PAD;
   constexpr int KS = Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
   constexpr int NSK = K / KS;                 // k-steps over K
   constexpr int NSM = (M + KS - 1) / KS;      // k-steps over M
   constexpr bool PADM = (M % KS) != 0;
-  static_assert(TPW % CT == 0, "state tiles of a wave come in whole rows");
-  __shared__ __attribute__((aligned(16))) float s_ST[BV * LDS_ST];
-  __shared__ __attribute__((aligned(16))) float s_VnT[BV * LDS_VN];
+  static_assert(TPW >= 1 && (TPW % CT == 0 || CT % TPW == 0),
+                "state tiles of a wave: whole rows, or a part of one row");
+  static_assert(ONE_RT || RTV % NWV == 0, "Vn row tiles spread evenly over the waves");
+  // S^T and Vn^T, split once by their writers
+  __shared__ __attribute__((aligned(16))) typename ST::T s_st[ST::NPLANE * BV * LDS_ST];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_vn[ST::NPLANE * BV * LDS_VN];
+  const ST sST{s_st, BV * LDS_ST}, sVn{s_vn, BV * LDS_VN};
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
@@ -70,10 +84,22 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
 
   // Operands of one step, read a step ahead: they do not depend on the state.
   struct Ops {
-    float a[RPW][NSK][KPL];     // A rows of this wave's Vn tiles
-    float u[RPW][CT][4];        // U at the Vn tiles
+    float a[NAR][NSK][KPL];     // A rows of this wave's Vn tiles
+    float u[NVP][4];            // U at the Vn tiles
     float bt[TRT][NSM][KPL];    // BT rows of this wave's state tiles
     float g[TRT][4];            // gam at the state rows
+  };
+  // p-th Vn tile of this wave: valid, row tile, column tile, A row set
+  auto vn_tile = [&](int p, int& rt, int& ct) -> bool {
+    if (ONE_RT) {
+      const int g = wv + NWV * p;
+      rt = g % RTV;
+      ct = g / RTV;
+      return g < NVT;
+    }
+    rt = wv + NWV * (p / CT);
+    ct = p % CT;
+    return true;
   };
   auto load = [&](int j, Ops& o) {
     const float* Aj = Ab + (size_t)j * M * K;
@@ -81,17 +107,17 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     const float* Bj = Bb + (size_t)j * K * M;
     const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
-    for (int p = 0; p < RPW; ++p) {
-      const int rt = wv + 4 * p;
-      if (rt < RTV) {
-        const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+    for (int p = 0; p < NVP; ++p) {
+      int rt, ct;
+      if (vn_tile(p, rt, ct)) {
+        if (ONE_RT ? p == 0 : p % CT == 0) {
+          const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < NSK; ++s) ld_raw<KPL>(arow + s * KS, o.a[p][s]);
+          for (int s = 0; s < NSK; ++s) ld_raw<KPL>(arow + s * KS, o.a[ONE_RT ? 0 : p / CT][s]);
+        }
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            o.u[p][ct][r] = Uj[(size_t)(rt * 16 + acc_row(r)) * V + v0 + ct * 16 + acc_col()];
+        for (int r = 0; r < 4; ++r)
+          o.u[p][r] = Uj[(size_t)(rt * 16 + acc_row(r)) * V + v0 + ct * 16 + acc_col()];
       }
     }
 #pragma unroll
@@ -137,35 +163,33 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-      *reinterpret_cast<f4*>(s_ST + vl * LDS_ST + k0) = st[i];
+      sST.put4(vl * LDS_ST + k0, st[i]);
     }
     __syncthreads();
 
     // ---- Vn = U - A S
 #pragma unroll
-    for (int p = 0; p < RPW; ++p) {
-      const int rt = wv + 4 * p;
-      if (rt < RTV) {
+    for (int p = 0; p < NVP; ++p) {
+      int rt, ct;
+      if (vn_tile(p, rt, ct)) {
+        f4 acc = f4_zero();
+        const int brow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          f4 acc = f4_zero();
-          const float* brow = s_ST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+        for (int s = 0; s < NSK; ++s)
+          acc = Mma<E>::mma(acc,
+                            Mma<E>::makes([&](int e) { return cur.a[ONE_RT ? 0 : p / CT][s][e]; }),
+                            sST.get(brow + s * KS));
+        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+        f4 vn;
 #pragma unroll
-          for (int s = 0; s < NSK; ++s)
-            acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.a[p][s][e]; }),
-                              Mma<E>::ld(brow + s * KS));
-          const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-          f4 vn;
+        for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][r] - acc[r];
+        sVn.put4(vl * LDS_VN + m0, vn);
+        if (a.vnT)
+          *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
+        if (a.vn) {
+          float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][ct][r] - acc[r];
-          *reinterpret_cast<f4*>(s_VnT + vl * LDS_VN + m0) = vn;
-          if (a.vnT)
-            *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
-          if (a.vn) {
-            float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
-          }
+          for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
         }
       }
     }
@@ -174,21 +198,24 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
     // ---- S <- diag(gam) S + BT Vn
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int t = i / CT, ct = i % CT;
+      // t must be a compile-time index into the operand registers
+      constexpr bool WHOLE = TPW % CT == 0;
+      const int t = WHOLE ? i / CT : 0;
+      const int ct = WHOLE ? i % CT : (wv * TPW + i) % CT;
 #pragma unroll
       for (int r = 0; r < 4; ++r) st[i][r] *= cur.g[t][r];
-      const float* brow = s_VnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+      const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
         // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
         typename Mma<E>::SFrag fb = Mma<E>::szero();
-        if (live) fb = Mma<E>::ld(brow + s * KS);
+        if (live) fb = sVn.get(brow + s * KS);
         st[i] = Mma<E>::mma(st[i], Mma<E>::makes([&](int e) { return cur.bt[t][s][e]; }), fb);
       }
     }
-    // no barrier needed here: the next writes to s_ST do not alias s_VnT, and
-    // the next writes to s_VnT follow the next step's barrier
+    // no barrier needed here: the next writes to s_st do not alias s_vn, and
+    // the next writes to s_vn follow the next step's barrier
   }
   if (a.state_mode == 1) {
     for (int j = S; j < a.NG; ++j) store_state(j);
@@ -204,10 +231,16 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(ScanArgs a) {
   }
 }
 
+// Waves per workgroup: K = 128 spreads its 16 state tiles over 8 waves (two
+// per wave), halving each wave's dependent chain per step; K = 64 keeps 4.
+template <int K> constexpr int scan_waves() { return K == 128 ? SCAN_WAVES_128 : 4; }
+
 template <typename E, int K, int M>
 static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
+  constexpr int NWV = scan_waves<K>();
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
-  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV>), dim3(grid), dim3(NWV * WAVE), 0,
+                     st, a);
   return hipGetLastError();
 }
 
