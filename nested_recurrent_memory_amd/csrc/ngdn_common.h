@@ -293,6 +293,17 @@ __device__ __forceinline__ void stage_f32(float* dst, int ld, const float* src, 
   }
 }
 
+// The same copy into a split tile: each value is split once, here.
+template <typename ST>
+__device__ __forceinline__ void stage_split(const ST& dst, int ld, const float* src, int src_ld,
+                                            int rows, int cols) {
+  const int segs = cols / 4;
+  for (int e = threadIdx.x; e < rows * segs; e += blockDim.x) {
+    const int r = e / segs, c = (e % segs) * 4;
+    dst.put4(r * ld + c, *reinterpret_cast<const f4*>(src + (size_t)r * src_ld + c));
+  }
+}
+
 // S [K][V] fp32 into LDS as S^T [V][ld] (k contiguous).
 template <int K, int V>
 __device__ __forceinline__ void stage_state_T(float* dst, int ld, const float* S) {

@@ -3,8 +3,9 @@
 // the per-token mix, written once (ops/chunk.py:129-156 read_level and the
 // accumulation at :250-251,285-286; ops/naive.py:376-390).
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l (scale q_l) S_l[group]
-// Each product runs on MFMA with the right operand staged in LDS (fp32) and the
-// left operand's rows read from global by the wave that owns them; wave w owns
+// Each product runs on MFMA with the right operand staged in LDS as a split
+// tile (each value split once, by the thread that stages it) and the left
+// operand's rows read from global by the wave that owns them; wave w owns
 // output rows 16w..16w+15.
 #include "ngdn_kernels.h"
 
@@ -13,11 +14,17 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   constexpr int C = CH;
-  constexpr int LD = K + 4;
-  constexpr int LDC = C + 4;
+  using ST = SplitTile<E>;
+  // states are staged 64 rows of K at a time: a 37 KB tile, so four
+  // workgroups fit on a CU
+  constexpr int KH = K > 64 ? 64 : K;
+  constexpr int LD = KH + ST::PAD;
+  constexpr int LDC = C + ST::PAD;
+  constexpr int LDM = LD > LDC ? LD : LDC;
   constexpr int CTV = V / 16;
   constexpr int KS = Mma<E>::KS;
-  __shared__ __attribute__((aligned(16))) float s_B[V * (LD > LDC ? LD : LDC)];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_b[ST::NPLANE * V * LDM];
+  const ST sB{s_b, V * LDM};
 
   const int NT = a.NT, H = a.H, T = a.T, L = a.L;
   int n, bh;   // all chunks of one (batch, head) on one XCD: groups share states in its L2
@@ -46,7 +53,7 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
       const auto fa = Mma<E>::ld(arow + k0);
 #pragma unroll
       for (int c = 0; c < CTV; ++c)
-        acc[c] = Mma<E>::mma(acc[c], fa, Mma<E>::ld(s_B + (c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + k0));
+        acc[c] = Mma<E>::mma(acc[c], fa, sB.get((c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + k0));
     }
   };
   auto fold = [&](int l, float sc) {
@@ -67,11 +74,13 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   // ---- level 0: Qg h + Aqk Vn
 #pragma unroll
   for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-  stage_f32(s_B, LD, a.hT + cix * V * K, K, V, K);
-  __syncthreads();
-  run(a.Qg + cix * C * K + (size_t)ri * K + kofs<E>(lane), LD, K);
-  __syncthreads();
-  stage_f32(s_B, LDC, a.vnT + cix * V * C, C, V, C);
+  for (int kb = 0; kb < K; kb += KH) {
+    stage_split(sB, LD, a.hT + cix * V * K + kb, K, V, KH);
+    __syncthreads();
+    run(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), LD, KH);
+    __syncthreads();
+  }
+  stage_split(sB, LDC, a.vnT + cix * V * C, C, V, C);
   __syncthreads();
   run(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), LDC, C);
   fold(0, 1.f);
@@ -82,13 +91,16 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
                   (size_t)(t0 + min(ri, nvalid - 1)) * H * L * K + kofs<E>(lane);
   for (int l = 1; l < L; ++l) {
     const int grp = n / a.f[l];
-    stage_f32(s_B, LD, a.statesT[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * V * K, K, V, K);
-    __syncthreads();
+    const float* Sl = a.statesT[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * V * K;
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-    run(qrow + (size_t)l * K, LD, K);   // rows past the end repeat the last row; fold drops them
-    fold(l, a.scale);
-    __syncthreads();
+    for (int kb = 0; kb < K; kb += KH) {
+      stage_split(sB, LD, Sl + kb, K, V, KH);
+      __syncthreads();
+      run(qrow + (size_t)l * K + kb, LD, KH);   // rows past the end repeat the last row
+      __syncthreads();
+    }
+    fold(l, a.scale);                           // which drops them
   }
 
   // ---- write o

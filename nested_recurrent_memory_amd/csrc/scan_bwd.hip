@@ -34,8 +34,9 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int TRT = TPW / CT;               // distinct state row tiles per wave
   constexpr int RTV = M / 16;
   constexpr int RPW = (RTV + 3) / 4;          // dVn row tiles per wave (at most)
-  constexpr int LDS_ST = K + 4;
-  constexpr int LDS_VN = M + 4;
+  using ST = SplitTile<E>;
+  constexpr int LDS_ST = K + ST::PAD;
+  constexpr int LDS_VN = M + ST::PAD;
   constexpr int KS = Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
   constexpr int NSK = K / KS;
@@ -43,9 +44,11 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr bool PADM = (M % KS) != 0;
   constexpr int DOE = M * BV / 256;           // dO elements staged per thread
   static_assert(TPW % CT == 0, "state tiles of a wave come in whole rows");
-  __shared__ __attribute__((aligned(16))) float s_dST[BV * LDS_ST];
-  __shared__ __attribute__((aligned(16))) float s_dVnT[BV * LDS_VN];
-  __shared__ __attribute__((aligned(16))) float s_dOT[BV * LDS_VN];
+  // dS'^T, dVn^T and (mix_0 dO)^T, split once by their writers
+  __shared__ __attribute__((aligned(16))) typename ST::T s_dst[ST::NPLANE * BV * LDS_ST];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_dvn[ST::NPLANE * BV * LDS_VN];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_dot[ST::NPLANE * BV * LDS_VN];
+  const ST sdS{s_dst, BV * LDS_ST}, sdV{s_dvn, BV * LDS_VN}, sdO{s_dot, BV * LDS_VN};
 
   const int V = a.V, S = a.S, H = a.H;
   const int nvt = V / BV;
@@ -180,13 +183,13 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       float* o = a.dSp + ((size_t)bh * S + j) * K * V + (size_t)k0 * V + v0 + vl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[(size_t)r * V] = ds[i][r];
-      *reinterpret_cast<f4*>(s_dST + vl * LDS_ST + k0) = ds[i];
+      sdS.put4(vl * LDS_ST + k0, ds[i]);
     }
     if (l0) {
 #pragma unroll
       for (int q = 0; q < DOE; ++q) {
         const int e = tid + q * 256, c = e / BV, vl = e % BV;
-        s_dOT[vl * LDS_VN + c] = cur.dov[q];
+        sdO.put1(vl * LDS_VN + c, cur.dov[q]);
       }
     }
     __syncthreads();
@@ -199,23 +202,23 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
           f4 acc = f4_zero();
-          const float* srow = s_dST + (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
+          const int srow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSK; ++s)
             acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.bop[p][s][e]; }),
-                              Mma<E>::ld(srow + s * KS));
+                              sdS.get(srow + s * KS));
           if (l0) {
-            const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+            const int orow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
             for (int s = 0; s < NSM; ++s)
               acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.aqk[p][s][e]; }),
-                                Mma<E>::ld(orow + s * KS));
+                                sdO.get(orow + s * KS));
           }
           const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
           float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
-          *reinterpret_cast<f4*>(s_dVnT + vl * LDS_VN + m0) = acc;
+          sdV.put4(vl * LDS_VN + m0, acc);
           if (a.dVnT)
             *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;
         }
@@ -228,21 +231,21 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     for (int i = 0; i < TPW; ++i) {
       const int t = i / CT, ct = i % CT;
       f4 acc = f4_zero();
-      const float* vrow = s_dVnT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+      const int vrow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s) {
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
         typename Mma<E>::SFrag fb = Mma<E>::szero();
-        if (live) fb = Mma<E>::ld(vrow + s * KS);
+        if (live) fb = sdV.get(vrow + s * KS);
         acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.at[t][s][e]; }), fb);
       }
       f4 qacc = f4_zero();
       if (l0) {
-        const float* orow = s_dOT + (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+        const int orow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < NSM; ++s)
           qacc = Mma<E>::mma(qacc, Mma<E>::makes([&](int e) { return cur.qg[t][s][e]; }),
-                             Mma<E>::ld(orow + s * KS));
+                             sdO.get(orow + s * KS));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) ds[i][r] = cur.g[t][r] * ds[i][r] - acc[r] + qacc[r];
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
     }
-    // s_dOT and s_dVnT are rewritten by the next step
+    // s_dot and s_dvn are rewritten by the next step
     __syncthreads();
   }
   if (a.dinit) {
