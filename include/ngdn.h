@@ -16,8 +16,11 @@
  * parameters (other than g and the states) and of its gradients: NGDN_F32 or
  * NGDN_BF16. Chunk size is 64.
  * Working tensors between the entry points ([B,H,NT,...], NT = ceil(T/64))
- * are fp32 whatever the dtype (declared float*), and are described at each
- * function.
+ * take 4 bytes per element whatever the dtype (declared float*), and are
+ * described at each function. Most hold fp32 values. Those marked "split"
+ * are read only as matrix-core operands: for NGDN_BF16 each per-unit tile
+ * [R][C] (one chunk's, or one firing's) holds two bf16 planes, hi = bf16(x)
+ * then lo = bf16(x - hi), R*C elements apart; for NGDN_F32 the fp32 values.
  */
 #ifndef NGDN_H
 #define NGDN_H
@@ -55,7 +58,8 @@ const char* ngdn_arch(void);
  * Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64] and
  * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
  * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
- * may be NULL (inference). */
+ * may be NULL (inference). W, KtT, Kt, WT, QgT and AqkT are split; U, Qg, Aqk,
+ * gam and TT fp32. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
@@ -82,9 +86,9 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
  * bpT, gpT [L-1,H,K,V] and wpT [L-1,H,V,V] are the b/g/w projections with
  * their last two axes swapped. promotion: 0 learned, 1 merge (n_queries = K).
  * Outputs for firing i in [0, NF), NF = NT / f_here, laid out [B,H,NF,...]:
- * A = keys*b*e^g [N,K], KT = keys^T [K,N], U = values*w [N,V],
+ * A = keys*b*e^g [N,K] (split), KT = keys^T [K,N] (split), U = values*w [N,V],
  * gam = e^g [K]; for the backward, keysN = keys [N,K] and AT = A^T
- * [K,N] (may be NULL). keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
+ * [K,N] (both split; may be NULL). keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
  * receive the probe outputs in the reference layout when not NULL. */
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,

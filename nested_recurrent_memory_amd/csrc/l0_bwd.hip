@@ -240,13 +240,17 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
   f4 dat[4];
   {
-    const float* Wg = a.W + cix * C * K;
+    const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);   // W in split form
     const float* Ug = a.U + cix * C * V;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
       f4 acc = f4_zero();
       if (J <= wv) {
-        acc = mma_tile<E>(acc, s_dXw + wv * 16 * LXK, LXK, Wg + (size_t)J * 16 * K, K, K);
+        const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
+        const int wr = (J * 16 + (lane & 15)) * K + kofs<E>(lane);
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += KS)
+          acc = Mma<E>::mma(acc, Mma<E>::ld(xr + k0), Ws.get(wr + k0));
         acc = mma_tile<E>(acc, s_dXu + wv * 16 * LXV, LXV, Ug + (size_t)J * 16 * V, V, V);
       }
       dat[J] = acc;

@@ -130,14 +130,15 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 
 // Per-row outputs written while the chunk's rows are in registers (forward
 // only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
-// row-major [64][K] and transposed [K][64].
+// row-major [64][K] and transposed [K][64]. Qg is fp32; Kt, Kt^T and Qg^T
+// (matrix-core operands of the scans only) are written in split form.
 struct RowOut {
   float* Qg; float* QgT; float* Kt; float* KtT;
 };
 
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
 // Aqk (lower incl. diagonal) to global fp32 [64][64]; when aqkT_out != null
-// also its transpose. Wave w computes block-row w.
+// also its transpose, in split form. Wave w computes block-row w.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
                                            const ChunkIn<E, K, V>& in, float* aqk_out,
@@ -169,14 +170,26 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       });
     }
     if (ro.Qg) {
+      const SplitTile<E> sqT = split_at<E>(ro.QgT, K * CH), skt = split_at<E>(ro.Kt, CH * K),
+                         sktT = split_at<E>(ro.KtT, K * CH);
+      float kt[KPL];
 #pragma unroll
       for (int e = 0; e < KPL; ++e) {
         const float qg = qv[e] * in.scale * fexp(gi[e]);
-        const float kt = kv[e] * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
+        kt[e] = kv[e] * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
         ro.Qg[ri * K + c0 + e] = qg;
-        if (ro.QgT) ro.QgT[(c0 + e) * CH + ri] = qg;
-        if (ro.Kt) ro.Kt[ri * K + c0 + e] = kt;
-        ro.KtT[(c0 + e) * CH + ri] = kt;
+        if (ro.QgT) sqT.put1((c0 + e) * CH + ri, qg);
+        sktT.put1((c0 + e) * CH + ri, kt[e]);
+      }
+      if (ro.Kt) {
+        if constexpr (KPL % 4 == 0) {
+#pragma unroll
+          for (int e = 0; e < KPL; e += 4)
+            skt.put4(ri * K + c0 + e, f4{kt[e], kt[e + 1], kt[e + 2], kt[e + 3]});
+        } else {
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) skt.put1(ri * K + c0 + e, kt[e]);
+        }
       }
     }
   }
@@ -223,7 +236,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       qt[rr] = (j <= i) ? accQ[rr] : 0.f;
       if (aqk_out) aqk_out[i * CH + j] = qt[rr];
     }
-    if (aqkT_out) *reinterpret_cast<f4*>(aqkT_out + (16 * J + acc_col()) * CH + r + acc_row(0)) = qt;
+    if (aqkT_out) split_at<E>(aqkT_out, CH * CH).put4((16 * J + acc_col()) * CH + r + acc_row(0), qt);
   }
 }
 

@@ -14,8 +14,9 @@
 //   gam  = e^gc_last
 // The forward consumes W, U, Kt^T, Qg, Aqk; the reverse scan consumes the
 // transposed copies Kt, W^T, Qg^T, Aqk^T, written when their pointers are set.
-// Every output is fp32; for bf16 inputs the products run on bf16 MFMA with
-// the derived operands split in two (ngdn_common.h).
+// For bf16 inputs the products run on bf16 MFMA with the derived operands
+// split in two (ngdn_common.h); the scans' operands W, Kt^T, Kt, W^T, Qg^T and
+// Aqk^T are stored split (split_at), U, Qg, Aqk, gam and T^T as fp32.
 //
 // One workgroup (4 waves) per (batch, head, chunk). Decay products are formed
 // without overflow: inside block-row I (16 rows starting at r = 16 I) every
@@ -117,9 +118,9 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w. The B fragments
   // gather KPL consecutive rows m of one column.
   {
-    float* Wo = a.W + cix * C * K;
+    const SplitTile<E> Wo = split_at<E>(a.W + cix * C * K, C * K);
     float* Uo = a.U + cix * C * V;
-    float* WTo = a.WT ? a.WT + cix * K * C : nullptr;
+    const SplitTile<E> WTo = split_at<E>(a.WT ? a.WT + cix * K * C : nullptr, K * C);
     const int i0 = R0 + acc_row(0);
     for (int tc = 0; tc < (K + V) / 16; ++tc) {
       const bool isw = tc < K / 16;
@@ -136,8 +137,8 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       }
       if (isw) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Wo[(i0 + rr) * K + col] = acc[rr];
-        if (WTo) *reinterpret_cast<f4*>(WTo + col * C + i0) = acc;
+        for (int rr = 0; rr < 4; ++rr) Wo.put1((i0 + rr) * K + col, acc[rr]);
+        if (a.WT) WTo.put4(col * C + i0, acc);
       } else {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) Uo[(i0 + rr) * V + col] = acc[rr];

@@ -178,6 +178,17 @@ template <> struct SplitTile<float> {
   __device__ __forceinline__ float get(int off) const { return p[off]; }
 };
 
+// Derived operands that only ever enter the matrix core are also kept in HBM
+// in split form: for bf16, each per-unit tile [R][C] (a chunk's or a firing's)
+// is two bf16 planes, hi then lo R*C elements apart, in the bytes of the fp32
+// tile; for fp32, the fp32 values. split_at gives the SplitTile view of one
+// unit (writes with put1 / put4, fragment reads with get), so the consumers
+// load fragments without splitting them again at every use.
+template <typename E>
+__device__ __forceinline__ SplitTile<E> split_at(const float* unit, int plane) {
+  return SplitTile<E>{reinterpret_cast<typename SplitTile<E>::T*>(const_cast<float*>(unit)), plane};
+}
+
 template <typename E> __device__ __forceinline__ int kofs(int lane) {
   return Mma<E>::KPL * (lane >> 4);
 }

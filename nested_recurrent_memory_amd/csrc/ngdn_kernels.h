@@ -8,11 +8,12 @@ namespace ngdn {
 
 // Level-0 intra-chunk forward. Inputs in the reference layout (contiguous):
 // q [B,T,H,L,K] (level-0 slice read), k, b [B,T,H,K], v, w [B,T,H,V] in the
-// working dtype, g [B,T,H,K] fp32. Outputs (fp32), per (b, h, chunk):
+// working dtype, g [B,T,H,K] fp32. Outputs, per (b, h, chunk):
 // W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64], Qg [B,H,NT,64,K],
 // Aqk [B,H,NT,64,64], gam [B,H,NT,K]. When set, the transposed copies for the
 // backward: Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64],
-// AqkT [B,H,NT,64,64], TT [B,H,NT,64,64] (= T^T).
+// AqkT [B,H,NT,64,64], TT [B,H,NT,64,64] (= T^T). W, KtT, Kt, WT, QgT and
+// AqkT are written in split form (split_at), the rest as fp32.
 struct L0IntraArgs {
   const void* q; const void* k; const void* v; const float* g;
   const void* b; const void* w;
@@ -42,7 +43,8 @@ constexpr int SCAN_BV = 32;
 
 // A sequence of delta-rule steps per (b, h):
 //   Vn = U - A S;   S <- diag(gam) S + BT Vn
-// A [B*H,S,M,K], BT [B*H,S,K,M], U [B*H,S,M,V], gam [B*H,S,K], all fp32. The
+// A [B*H,S,M,K], BT [B*H,S,K,M] in split form (split_at), U [B*H,S,M,V] and
+// gam [B*H,S,K] fp32. The
 // state entering each step is stored (fp32) as S rows (st_kv, [K][V]) and/or
 // S^T rows (st_vk, [V][K]), each optional: mode 0 per (b, h, step) at
 // [B,H,S,...] (level 0, chunk states), mode 1 per (b, group, h) at
@@ -61,7 +63,7 @@ hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 
 // Reverse of scan_fwd. Bop [B*H,S,M,K] (= BT^T: level 0 Kt, upper keys),
 // AT [B*H,S,K,M] (= A^T), gam [B*H,S,K]. Level 0 sets AqkT [B*H,S,64,64],
-// QgT [B*H,S,K,64], dout [B,T,H,V], mix [B,T,H,L] and inj (fp32
+// QgT [B*H,S,K,64] (Bop, AT, AqkT and QgT in split form), dout [B,T,H,V], mix [B,T,H,L] and inj (fp32
 // [B*H,inj_nf,K,V], added before step j when (j+1) % inj_every == 0). Upper
 // levels set d_states (fp32 [B,NG,H,K,V], added after step j, and for every
 // stored group past the last step before the first). d_final seeds the state

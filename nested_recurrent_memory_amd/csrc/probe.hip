@@ -159,8 +159,11 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
     a.gam[fo * K + tid] = expf(g);
     if (a.go) a.go[ro * K + tid] = g;
   }
-  float* Ao = a.A + fo * N * K;
-  float* KTo = a.KT + fo * K * N;
+  // the scan's operands in split form
+  const SplitTile<E> Ao = split_at<E>(a.A + fo * N * K, N * K);
+  const SplitTile<E> KTo = split_at<E>(a.KT + fo * K * N, K * N);
+  const SplitTile<E> KNo = split_at<E>(a.keysN ? a.keysN + fo * N * K : nullptr, N * K);
+  const SplitTile<E> ATo = split_at<E>(a.AT ? a.AT + fo * K * N : nullptr, K * N);
 #pragma unroll
   for (int t = 0; t < NTK; ++t) {
     const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
@@ -176,13 +179,13 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
                                   1e-12f);
       kv4[r] = key;
       av4[r] = key * bt[t][r] * gam;
-      Ao[n * K + k] = av4[r];
-      if (a.keysN) a.keysN[fo * N * K + n * K + k] = key;
+      Ao.put1(n * K + k, av4[r]);
+      if (a.keysN) KNo.put1(n * K + k, key);
       if (a.keys) a.keys[ro * N * K + n * K + k] = key;
       if (a.bo) a.bo[ro * N * K + n * K + k] = bt[t][r];
     }
-    *reinterpret_cast<f4*>(KTo + k * N + n0) = kv4;
-    if (a.AT) *reinterpret_cast<f4*>(a.AT + fo * K * N + k * N + n0) = av4;
+    KTo.put4(k * N + n0, kv4);
+    if (a.AT) ATo.put4(k * N + n0, av4);
   }
 }
 

@@ -83,10 +83,11 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   const float* Gb = a.gam + (size_t)bh * S * K;
 
   // Operands of one step, read a step ahead: they do not depend on the state.
+  typedef typename Mma<E>::SFrag SF;
   struct Ops {
-    float a[NAR][NSK][KPL];     // A rows of this wave's Vn tiles
+    SF a[NAR][NSK];             // A rows of this wave's Vn tiles
     float u[NVP][4];            // U at the Vn tiles
-    float bt[TRT][NSM][KPL];    // BT rows of this wave's state tiles
+    SF bt[TRT][NSM];            // BT rows of this wave's state tiles
     float g[TRT][4];            // gam at the state rows
   };
   // p-th Vn tile of this wave: valid, row tile, column tile, A row set
@@ -102,18 +103,18 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     return true;
   };
   auto load = [&](int j, Ops& o) {
-    const float* Aj = Ab + (size_t)j * M * K;
+    const SplitTile<E> Aj = split_at<E>(Ab + (size_t)j * M * K, M * K);
     const float* Uj = Ub + (size_t)j * M * V;
-    const float* Bj = Bb + (size_t)j * K * M;
+    const SplitTile<E> Bj = split_at<E>(Bb + (size_t)j * K * M, K * M);
     const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int p = 0; p < NVP; ++p) {
       int rt, ct;
       if (vn_tile(p, rt, ct)) {
         if (ONE_RT ? p == 0 : p % CT == 0) {
-          const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+          const int arow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSK; ++s) ld_raw<KPL>(arow + s * KS, o.a[ONE_RT ? 0 : p / CT][s]);
+          for (int s = 0; s < NSK; ++s) o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(arow + s * KS);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -123,14 +124,10 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
 #pragma unroll
     for (int t = 0; t < TRT; ++t) {
       const int rt = (wv * TPW) / CT + t;
-      const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      const int brow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < NSM; ++s) {
-        if (!PADM || s * KS + kofs<E>(lane) < M) ld_raw<KPL>(brow + s * KS, o.bt[t][s]);
-        else
-#pragma unroll
-          for (int e = 0; e < KPL; ++e) o.bt[t][s][e] = 0.f;
-      }
+      for (int s = 0; s < NSM; ++s)
+        o.bt[t][s] = (!PADM || s * KS + kofs<E>(lane) < M) ? Bj.get(brow + s * KS) : Mma<E>::szero();
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
     }
@@ -176,9 +173,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
         const int brow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < NSK; ++s)
-          acc = Mma<E>::mma(acc,
-                            Mma<E>::makes([&](int e) { return cur.a[ONE_RT ? 0 : p / CT][s][e]; }),
-                            sST.get(brow + s * KS));
+          acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], sST.get(brow + s * KS));
         const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
         f4 vn;
 #pragma unroll
@@ -211,7 +206,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
         typename Mma<E>::SFrag fb = Mma<E>::szero();
         if (live) fb = sVn.get(brow + s * KS);
-        st[i] = Mma<E>::mma(st[i], Mma<E>::makes([&](int e) { return cur.bt[t][s][e]; }), fb);
+        st[i] = Mma<E>::mma(st[i], cur.bt[t][s], fb);
       }
     }
     // no barrier needed here: the next writes to s_st do not alias s_vn, and

@@ -98,51 +98,47 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   const E* mixb = l0 ? static_cast<const E*>(a.mix) + ((size_t)b * a.T * H + h) * a.L : nullptr;
 
   // Operands of one step, read a step ahead: they do not depend on the state gradient.
+  typedef typename Mma<E>::SFrag SF;
   struct Ops {
-    float bop[RPW][NSK][KPL];   // Bop rows of this wave's dVn tiles
-    float aqk[RPW][NSM][KPL];   // Aqk^T rows (level 0)
-    float at[TRT][NSM][KPL];    // A^T rows of this wave's state tiles
-    float qg[TRT][NSM][KPL];    // Qg^T rows (level 0)
+    SF bop[RPW][NSK];           // Bop rows of this wave's dVn tiles
+    SF aqk[RPW][NSM];           // Aqk^T rows (level 0)
+    SF at[TRT][NSM];            // A^T rows of this wave's state tiles
+    SF qg[TRT][NSM];            // Qg^T rows (level 0)
     float g[TRT][4];
     float dov[DOE];             // mix_0 do at this thread's staging slots (level 0)
     f4 add[TPW];                // injection (level 0) or read gradient (upper) of the step
     bool has_add;
   };
   auto load = [&](int j, Ops& o) {
-    const float* Bj = Bb + (size_t)j * M * K;
-    const float* Aj = Ab + (size_t)j * K * M;
+    const SplitTile<E> Bj = split_at<E>(Bb + (size_t)j * M * K, M * K);
+    const SplitTile<E> Aj = split_at<E>(Ab + (size_t)j * K * M, K * M);
     const float* Gj = Gb + (size_t)j * K;
 #pragma unroll
     for (int p = 0; p < RPW; ++p) {
       const int rt = wv + 4 * p;
       if (rt < RTV) {
-        const float* brow = Bj + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
+        const int brow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < NSK; ++s) ld_raw<KPL>(brow + s * KS, o.bop[p][s]);
+        for (int s = 0; s < NSK; ++s) o.bop[p][s] = Bj.get(brow + s * KS);
         if (l0) {
-          const float* qrow = a.AqkT + ((size_t)bh * S + j) * M * M +
-                              (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+          const SplitTile<E> Qj = split_at<E>(a.AqkT + ((size_t)bh * S + j) * M * M, M * M);
+          const int qrow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSM; ++s) ld_raw<KPL>(qrow + s * KS, o.aqk[p][s]);
+          for (int s = 0; s < NSM; ++s) o.aqk[p][s] = Qj.get(qrow + s * KS);
         }
       }
     }
 #pragma unroll
     for (int t = 0; t < TRT; ++t) {
       const int rt = (wv * TPW) / CT + t;
-      const float* arow = Aj + (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+      const int arow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < NSM; ++s) {
-        if (!PADM || s * KS + kofs<E>(lane) < M) ld_raw<KPL>(arow + s * KS, o.at[t][s]);
-        else
-#pragma unroll
-          for (int e = 0; e < KPL; ++e) o.at[t][s][e] = 0.f;
-      }
+      for (int s = 0; s < NSM; ++s)
+        o.at[t][s] = (!PADM || s * KS + kofs<E>(lane) < M) ? Aj.get(arow + s * KS) : Mma<E>::szero();
       if (l0) {
-        const float* qrow = a.QgT + ((size_t)bh * S + j) * K * M +
-                            (size_t)(rt * 16 + (lane & 15)) * M + kofs<E>(lane);
+        const SplitTile<E> Gj = split_at<E>(a.QgT + ((size_t)bh * S + j) * K * M, K * M);
 #pragma unroll
-        for (int s = 0; s < NSM; ++s) ld_raw<KPL>(qrow + s * KS, o.qg[t][s]);
+        for (int s = 0; s < NSM; ++s) o.qg[t][s] = Gj.get(arow + s * KS);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
@@ -205,14 +201,12 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
           const int srow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSK; ++s)
-            acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.bop[p][s][e]; }),
-                              sdS.get(srow + s * KS));
+            acc = Mma<E>::mma(acc, cur.bop[p][s], sdS.get(srow + s * KS));
           if (l0) {
             const int orow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
             for (int s = 0; s < NSM; ++s)
-              acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.aqk[p][s][e]; }),
-                                sdO.get(orow + s * KS));
+              acc = Mma<E>::mma(acc, cur.aqk[p][s], sdO.get(orow + s * KS));
           }
           const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
           float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
@@ -237,15 +231,14 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
         const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
         typename Mma<E>::SFrag fb = Mma<E>::szero();
         if (live) fb = sdV.get(vrow + s * KS);
-        acc = Mma<E>::mma(acc, Mma<E>::makes([&](int e) { return cur.at[t][s][e]; }), fb);
+        acc = Mma<E>::mma(acc, cur.at[t][s], fb);
       }
       f4 qacc = f4_zero();
       if (l0) {
         const int orow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < NSM; ++s)
-          qacc = Mma<E>::mma(qacc, Mma<E>::makes([&](int e) { return cur.qg[t][s][e]; }),
-                             sdO.get(orow + s * KS));
+          qacc = Mma<E>::mma(qacc, cur.qg[t][s], sdO.get(orow + s * KS));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) ds[i][r] = cur.g[t][r] * ds[i][r] - acc[r] + qacc[r];
