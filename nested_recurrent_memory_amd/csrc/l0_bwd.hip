@@ -207,22 +207,13 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::ld(tt + s * KS);
     const float* dvT = a.dVnT + cix * V * C;
     const float* dwT = a.dWT + cix * K * C;
-    E* dvo = static_cast<E*>(a.dv) + ((size_t)b * T * H + h) * V;
-    E* dwo = static_cast<E*>(a.dw) + ((size_t)b * T * H + h) * V;
     for (int ct = 0; ct < CTV; ++ct) {
       f4 acc = f4_zero();
       const float* br = dvT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::ld(br + s * KS));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = wv * 16 + acc_row(r), vv = ct * 16 + acc_col();
-        s_dXu[i * LXV + vv] = acc[r];
-        if (i < nvalid) {
-          dvo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.W_(i, vv));
-          dwo[(size_t)(t0 + i) * H * V + vv] = from_f<E>(acc[r] * in.V_(i, vv));
-        }
-      }
+      for (int r = 0; r < 4; ++r) s_dXu[(wv * 16 + acc_row(r)) * LXV + ct * 16 + acc_col()] = acc[r];
     }
 #pragma unroll
     for (int ct = 0; ct < CTK; ++ct) {
@@ -236,6 +227,38 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     }
   }
   __syncthreads();
+
+  // dv = dX_u * w, dw = dX_u * v: 16-byte rows, all loads of a thread ahead of its stores
+  {
+    constexpr int VE = ChunkIn<E, K, V>::VE;
+    constexpr int PER = C * V / VE / 256;
+    static_assert(C * V / VE % 256 == 0, "whole 16-byte groups per thread");
+    E* dvo = static_cast<E*>(a.dv) + ((size_t)b * T * H + h) * V;
+    E* dwo = static_cast<E*>(a.dw) + ((size_t)b * T * H + h) * V;
+    float wx[PER][VE], vx[PER][VE];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / (V / VE), c = (e % (V / VE)) * VE;
+      in.vec16(in.w, in.rowV, i, c, wx[q]);
+      in.vec16(in.v, in.rowV, i, c, vx[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = tid + 256 * q, i = e / (V / VE), c = (e % (V / VE)) * VE;
+      if (i < nvalid) {
+        typedef E EV __attribute__((__vector_size__(16)));
+        EV dvv, dwv;
+#pragma unroll
+        for (int j = 0; j < VE; ++j) {
+          const float x = s_dXu[i * LXV + c + j];
+          dvv[j] = from_f<E>(x * wx[q][j]);
+          dwv[j] = from_f<E>(x * vx[q][j]);
+        }
+        *reinterpret_cast<EV*>(dvo + (size_t)(t0 + i) * H * V + c) = dvv;
+        *reinterpret_cast<EV*>(dwo + (size_t)(t0 + i) * H * V + c) = dwv;
+      }
+    }
+  }
 
   // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
   f4 dat[4];
@@ -384,7 +407,18 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     }
     __syncthreads();   // the cumulative-decay gradient overwrites gc in place
 
-    // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
+    // ---- 5. assemble dq, dk, db and the cumulative-decay gradient (the
+    // state half's dQg, dKt read ahead of the stores: mixed outstanding loads
+    // and stores would make every load wait for all of them)
+    float gqa[CTH][4], gka[CTH][4];
+#pragma unroll
+    for (int ct = 0; ct < CTH; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = R0 + acc_row(r), kc = c0 + ct * 16 + acc_col();
+        gqa[ct][r] = dQg[i * K + kc];
+        gka[ct][r] = dKt[i * K + kc];
+      }
 #pragma unroll
     for (int ct = 0; ct < CTH; ++ct) {
       const int kl = ct * 16 + acc_col(), kc = c0 + kl;
@@ -396,7 +430,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         const float gcv = s_g[i * GH + kl];
         const float eg = fexp(gcv), ekt = fexp(glast - gcv);
         const float bi = BV(i, kl), ki = KV(i, kl), qh = QV(i, kl) * in.scale;
-        const float gq = dQg[i * K + kc], gk = dKt[i * K + kc];
+        const float gq = gqa[ct][r], gk = gka[ct][r];
         const float xw = dxw[p * CTH + ct][r];
         const float dqh = dqa[ct][r] + gq * eg;
         const float db_ = dbk[ct][r] * ki + xw * ki * eg;
