@@ -153,8 +153,8 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
  * entering chunk (i+1)*f1, added before that chunk's step (the reference's
  * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
- * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (split), and
- * d_initial[:, :, 0] when not NULL. Kt, WT, QgT and AqkT are read split. */
+ * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64], and d_initial[:, :, 0]
+ * when not NULL. Kt, WT, QgT and AqkT are read split. */
 int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
                          const float* gam, const float* AqkT, const float* QgT,
                          const void* dout, const void* mix, int32_t f1,
@@ -175,16 +175,16 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             void* stream);
 
 /* Level-0 chunk backward, state half, from h and vn of ngdn_l0_scan_fwd:
- * dQg, dKt [B,H,NT,64,K], dWT [B,H,NT,K,64] (split), dAqk [B,H,NT,64,64],
- * dgam [B,H,NT,K]. */
+ * dQg, dKt [B,H,NT,64,K], dWT [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam
+ * [B,H,NT,K]. */
 int32_t ngdn_l0_bwd_state(const ngdn_dims* d, const float* h, const float* dSp,
                           const float* vn, const float* dVn, const void* dout,
                           const void* mix, float* dQg, float* dWT, float* dKt,
                           float* dAqk, float* dgam, void* stream);
 
 /* Level-0 chunk backward, intra half: writes dq[..., 0, :], dk, dv, db, dw
- * (working dtype) and dg (fp32 [B,T,H,K]). W, U, TT from ngdn_l0_intra_fwd;
- * W, dWT and dVnT are read split. */
+ * (working dtype) and dg (fp32 [B,T,H,K]). W (split), U, TT from
+ * ngdn_l0_intra_fwd. */
 int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, const float* W, const float* U,

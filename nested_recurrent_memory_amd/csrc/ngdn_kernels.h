@@ -68,7 +68,7 @@ hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 // levels set d_states (fp32 [B,NG,H,K,V], added after step j, and for every
 // stored group past the last step before the first). d_final seeds the state
 // gradient. Outputs (fp32): dSp [B*H,S,K,V] (gradient of the state after
-// each step), dVn [B*H,S,M,V], dVnT = dVn^T [B*H,S,V,M] (split form; when set), dinit
+// each step), dVn [B*H,S,M,V], dVnT = dVn^T [B*H,S,V,M] (when set), dinit
 // ([K][V] at strides, when set). All working tensors are fp32; dout and mix
 // are in the working dtype.
 struct ScanBwdArgs {
@@ -220,7 +220,7 @@ hipError_t read_state_bwd(const ReadStateBwdArgs& a, int dtype, int K, int V, hi
 //   dQg = dO S^T, dW = -dVn S^T, dKt = Vn dS'^T, dAqk = dO Vn^T (j <= i),
 //   dgam_k = sum_v dS'[k][v] S[k][v]
 // with S = h (rows [K][V]), Vn rows [64][V], dS' the state gradient after the
-// chunk, dO = mix_0 do. Outputs dQg, dKt [B,H,NT,64,K] (fp32), dWT (split form)
+// chunk, dO = mix_0 do. Outputs (fp32) dQg, dKt [B,H,NT,64,K], dWT
 // [B,H,NT,K,64], dAqk [B,H,NT,64,64], dgam [B,H,NT,K]; dout and mix in the
 // working dtype.
 struct L0BwdStateArgs {
@@ -235,7 +235,7 @@ hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStr
 // products and the cumulative sum), per (b, h, chunk). Reads the forward's
 // W [.,64,K], U [.,64,V] and TT = T^T [.,64,64], the state half's dQg, dKt
 // [.,64,K], dWT = dW^T [.,K,64], dAqk [.,64,64], dgam [.,K], and the scan's
-// dVnT = dVn^T [.,V,64] (dWT, dVnT in split form). Writes dq[..., 0, :], dk, dv, db, dw (working dtype)
+// dVnT = dVn^T [.,V,64] (W in split form). Writes dq[..., 0, :], dk, dv, db, dw (working dtype)
 // and dg (fp32).
 struct L0BwdIntraArgs {
   const void* q; const void* k; const void* v; const float* g; const void* b; const void* w;
