@@ -32,6 +32,8 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   constexpr int TPW = (NTL + NW - 1) / NW;          // tiles per wave
   constexpr int NTKV = CTK * CTK;                   // [K,V] tiles
   constexpr int TPW2 = (NTKV + NW - 1) / NW;
+  // hold a phase's results until its loads are done (registers permitting)
+  constexpr bool BATCH = TPW <= 4;
   constexpr int KS = Mma<E>::KS;
   constexpr int NKS = K / KS;
   typedef typename Mma<E>::SFrag SF;
@@ -87,25 +89,33 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // ---- 1. Vals = Bank[:N] S (learned) or S (merge)
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
+    // every tile computed before any store: outstanding loads and stores
+    // together would make each later load wait for all of them
+    f4 vt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
+      vt[t] = f4_zero();
       int rt, ct;
       if (!tile(t, rt, ct)) continue;
       const E* arow = bank + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
       const int v = ct * 16 + (lane & 15);
-      f4 acc = f4_zero();
 #pragma unroll
       for (int s = 0; s < NKS; ++s) {
         const int k0 = s * KS + kofs<E>(lane);
         const SF fb = Svk ? Mma<E>::ld(Svk + (size_t)v * K + k0)
                           : Mma<E>::makes([&](int e) { return Skv[(size_t)(k0 + e) * V + v]; });
-        acc = Mma<E>::mma(acc, Mma<E>::ld(arow + s * KS), fb);
+        vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fb);
       }
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = rt * 16 + acc_row(r), vv = ct * 16 + acc_col();
-        s_V[n * LD + vv] = acc[r];
-        wsV[n * V + vv] = acc[r];
+        s_V[n * LD + vv] = vt[t][r];
+        wsV[n * V + vv] = vt[t][r];
       }
     }
   } else {
@@ -181,7 +191,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 
   // ---- 4. vn = Vals w - kb s with s = e^g S_j (s^T rows scaled per k);
   // dw-side terms
-  f4 vnt[TPW], dvd[TPW];
+  f4 vnt[TPW], dvd[TPW], dxwt[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     vnt[t] = dvd[t] = f4_zero();
@@ -206,7 +216,18 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       const float dv = dvn[(size_t)n * V + v];
       vnt[t][r] = val * w - ks[r];
       dvd[t][r] = dv * w;
-      wsdxw[(size_t)n * V + v] = dv * val * w * (1.f - w);
+      if constexpr (BATCH) dxwt[t][r] = dv * val * w * (1.f - w);
+      else wsdxw[(size_t)n * V + v] = dv * val * w * (1.f - w);
+    }
+  }
+  if constexpr (BATCH) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        wsdxw[(size_t)(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = dxwt[t][r];
     }
   }
   __syncthreads();   // vn replaces kb
@@ -221,10 +242,10 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   __syncthreads();
 
   // ---- 5. P = dvn s^T, Q = vn dS'^T; dkeys, db, the decay gradient
-  f4 dkt[TPW];
+  f4 dkt[TPW], dxbt[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    dkt[t] = f4_zero();
+    dkt[t] = dxbt[t] = f4_zero();
     int rt, ct;
     if (!tile(t, rt, ct)) continue;
     const int kc = ct * 16 + (lane & 15);
@@ -250,7 +271,8 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       const float dbg = -P[r] * key;
       cs += key * bb * P[r];
       dkt[t][r] = dkey;
-      wsdxb[(size_t)n * K + k] = dbg * bb * (1.f - bb);
+      if constexpr (BATCH) dxbt[t][r] = dbg * bb * (1.f - bb);
+      else wsdxb[(size_t)n * K + k] = dbg * bb * (1.f - bb);
       if (!MERGE) {
         float rd = key * dkey;
         rd += __shfl_xor(rd, 1, WAVE);
@@ -270,6 +292,17 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     for (int v = lane; v < V; v += WAVE) sum += dSp[(size_t)k * V + v] * Sj[(size_t)k * V + v];
     sum = wave_sum(sum);
     if (lane == 0) atomicAdd(&s_dg[k], s_gam[k] * sum);
+  }
+  // the phase's stores after all of its loads
+  if constexpr (BATCH) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        wsdxb[(size_t)(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()] = dxbt[t][r];
+    }
   }
   __syncthreads();
 
@@ -314,44 +347,72 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
         acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxg + ar + s * KS), Mma<E>::ld(gp + br + s * KS));
       }
       dvd[t] = acc;
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        wsdV[(size_t)n * V + v] = acc[r];
-        if (!MERGE) s_dVT[v * LDN + n] = acc[r];
+        wsdV[(size_t)n * V + v] = dvd[t][r];
+        if (!MERGE) s_dVT[v * LDN + n] = dvd[t][r];
       }
     }
   }
   __syncthreads();
 
   // ---- 8. dS_below and dBank
-  auto scatter = [&](int k, int v, float x) {
-    if (a.f_below == 1 && a.below_mode == 0) {
-      ab.inj[fo * K * V + (size_t)k * V + v] = x;
-    } else if (fin) {
-      ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v] += x;
-    } else {
-      ab.d_below[(((size_t)b * a.NGb + src) * H + h) * K * V + (size_t)k * V + v] += x;
+  // Adds (or, for level 1, writes) the [K,V] tiles g = wv + NW t: every
+  // addend read before any store
+  auto scatter_all = [&](const f4* x) {
+    constexpr int NT2 = TPW2;
+    float prev[NT2][4];
+#pragma unroll
+    for (int t = 0; t < NT2; ++t) {
+      const int g = wv + NW * t;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        prev[t][r] = 0.f;
+        if (g >= NTKV) continue;
+        const int k = (g / CTK) * 16 + acc_row(r), v = (g % CTK) * 16 + acc_col();
+        if (a.f_below == 1 && a.below_mode == 0) continue;
+        prev[t][r] = fin ? ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v]
+                         : ab.d_below[(((size_t)b * a.NGb + src) * H + h) * K * V + (size_t)k * V + v];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT2; ++t) {
+      const int g = wv + NW * t;
+      if (g >= NTKV) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k = (g / CTK) * 16 + acc_row(r), v = (g % CTK) * 16 + acc_col();
+        if (a.f_below == 1 && a.below_mode == 0)
+          ab.inj[fo * K * V + (size_t)k * V + v] = x[t][r];
+        else if (fin)
+          ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v] = prev[t][r] + x[t][r];
+        else
+          ab.d_below[(((size_t)b * a.NGb + src) * H + h) * K * V + (size_t)k * V + v] =
+              prev[t][r] + x[t][r];
+      }
     }
   };
   if (MERGE) {
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) scatter(rt * 16 + acc_row(r), ct * 16 + acc_col(), dvd[t][r]);
-    }
+    // [N,K] tiles are the [K,V] tiles here (N = K = V): same numbering
+    static_assert(!MERGE || TPW == TPW2, "merge: one tile grid");
+    scatter_all(dvd);
   } else {
     // dS_below[k][v] = sum_n Bank[n][k] dVals[n][v]
     const E* bankT = static_cast<const E*>(ab.bankT) + (size_t)h * K * a.Nmax;
     constexpr int NSN = (N + KS - 1) / KS;
+    f4 dsb[TPW2];
 #pragma unroll
     for (int t = 0; t < TPW2; ++t) {
+      dsb[t] = f4_zero();
       const int g = wv + NW * t;
       if (g >= NTKV) continue;
       const int rt = g / CTK, ct = g % CTK;
-      f4 acc = f4_zero();
       const E* arow = bankT + (size_t)(rt * 16 + (lane & 15)) * a.Nmax + kofs<E>(lane);
       const float* brow = s_dVT + (ct * 16 + (lane & 15)) * LDN + kofs<E>(lane);
 #pragma unroll
@@ -363,25 +424,31 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
           fa = Mma<E>::ld(arow + s * KS);
           fb = Mma<E>::ld(brow + s * KS);
         }
-        acc = Mma<E>::mma(acc, fa, fb);
+        dsb[t] = Mma<E>::mma(dsb[t], fa, fb);
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) scatter(rt * 16 + acc_row(r), ct * 16 + acc_col(), acc[r]);
     }
+    scatter_all(dsb);
     // dBank[n][k] += sum_v dVals[n][v] S_below[k][v]
     float* dbank = ab.dbank + (size_t)h * a.Nmax * K;
+    f4 dbt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
+      dbt[t] = f4_zero();
       int rt, ct;
       if (!tile(t, rt, ct)) continue;
       const float* arow = wsdV + (size_t)(rt * 16 + (lane & 15)) * V + kofs<E>(lane);
       const float* brow = Skv + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
-      f4 acc = f4_zero();
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) acc = Mma<E>::mma(acc, Mma<E>::ld(arow + s * KS), Mma<E>::ld(brow + s * KS));
+      for (int s = 0; s < NKS; ++s)
+        dbt[t] = Mma<E>::mma(dbt[t], Mma<E>::ld(arow + s * KS), Mma<E>::ld(brow + s * KS));
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt, ct;
+      if (!tile(t, rt, ct)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()], acc[r]);
+        atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()], dbt[t][r]);
     }
   }
 }

@@ -67,6 +67,25 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
     part[c] += __shfl_xor(part[c], 32, WAVE);
   }
   if (lane < CQ) *reinterpret_cast<f4*>(&s_red[wv][cq * 4]) = part;
+
+  // reads of the upper levels (unchanged by this token)
+  f4 rd[MAXL];
+#pragma unroll
+  for (int l = 0; l < MAXL; ++l) rd[l] = f4_zero();
+#pragma unroll
+  for (int l = 1; l < MAXL; ++l) {
+    if (l < L) {
+      const float* Sl = Sin + (size_t)l * K * V;
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const int k = rg * RPT + r;
+        const f4 x = *reinterpret_cast<const f4*>(Sl + (size_t)k * V + col);
+        const float ql = to_f(q[(size_t)l * K + k]) * a.scale;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rd[l][c] += ql * x[c];
+      }
+    }
+  }
   __syncthreads();
   f4 u;
   {
@@ -81,10 +100,8 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
     }
   }
 
-  // ---- S0 += k u^T, written; reads of every level
-  f4 rd[MAXL];
-#pragma unroll
-  for (int l = 0; l < MAXL; ++l) rd[l] = f4_zero();
+  // ---- S0 += k u^T, written; reads of every level (the upper levels were
+  // read above, before any store)
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int k = rg * RPT + r;
@@ -94,21 +111,6 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
     const float ql = to_f(q[k]) * a.scale;
 #pragma unroll
     for (int c = 0; c < 4; ++c) rd[0][c] += ql * s0[r][c];
-  }
-#pragma unroll
-  for (int l = 1; l < MAXL; ++l) {
-    if (l < L) {
-      const float* Sl = Sin + (size_t)l * K * V;
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        const int k = rg * RPT + r;
-        const f4 x = *reinterpret_cast<const f4*>(Sl + (size_t)k * V + col);
-        if (copy_up) *reinterpret_cast<f4*>(Sout + (size_t)l * K * V + (size_t)k * V + col) = x;
-        const float ql = to_f(q[(size_t)l * K + k]) * a.scale;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) rd[l][c] += ql * x[c];
-      }
-    }
   }
 #pragma unroll
   for (int l = 0; l < MAXL; ++l) {
@@ -138,6 +140,16 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
         acc += r * to_f(mix[l]);
       }
       o[c] = from_f<E>(acc);
+    }
+  }
+  // out of place: the upper levels are copied last (after every load)
+  if (copy_up) {
+    for (int l = 1; l < L; ++l) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const size_t off = (size_t)l * K * V + (size_t)(rg * RPT + r) * V + col;
+        *reinterpret_cast<f4*>(Sout + off) = *reinterpret_cast<const f4*>(Sin + off);
+      }
     }
   }
 }
