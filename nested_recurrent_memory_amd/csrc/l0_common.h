@@ -138,11 +138,14 @@ struct RowOut {
 
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
 // Aqk (lower incl. diagonal) to global fp32 [64][64]; when aqkT_out != null
-// also its transpose, in split form. Wave w computes block-row w.
+// also its transpose, in split form. Wave w computes block-row w. With
+// per-row outputs, s_x is LDS scratch of 64 x (64 + 4) floats for the
+// transposed ones, and the call ends with a barrier.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
                                            const ChunkIn<E, K, V>& in, float* aqk_out,
-                                           float* aqkT_out, const RowOut& ro = RowOut{}) {
+                                           float* aqkT_out, const RowOut& ro = RowOut{},
+                                           float* s_x = nullptr) {
   constexpr int GL = K + GCP;
   constexpr int NKS = K / Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
@@ -163,36 +166,17 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
     lf[s] = Mma<E>::makes([&](int e) {
       return bv[e] * kv[e] * fexp(gi[e] - s_gc[r * GL + c0 + e]);
     });
-    if (want_q || ro.Qg) in.vals(in.q, in.rowQ, ri, c0, qv);
     if (want_q) {
+      in.vals(in.q, in.rowQ, ri, c0, qv);
       qf[s] = Mma<E>::makes([&](int e) {
         return qv[e] * in.scale * fexp(gi[e] - s_gc[r * GL + c0 + e]);
       });
     }
-    if (ro.Qg) {
-      const SplitTile<E> sqT = split_at<E>(ro.QgT, K * CH), skt = split_at<E>(ro.Kt, CH * K),
-                         sktT = split_at<E>(ro.KtT, K * CH);
-      float kt[KPL];
-#pragma unroll
-      for (int e = 0; e < KPL; ++e) {
-        const float qg = qv[e] * in.scale * fexp(gi[e]);
-        kt[e] = kv[e] * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi[e]);
-        ro.Qg[ri * K + c0 + e] = qg;
-        if (ro.QgT) sqT.put1((c0 + e) * CH + ri, qg);
-        sktT.put1((c0 + e) * CH + ri, kt[e]);
-      }
-      if (ro.Kt) {
-        if constexpr (KPL % 4 == 0) {
-#pragma unroll
-          for (int e = 0; e < KPL; e += 4)
-            skt.put4(ri * K + c0 + e, f4{kt[e], kt[e + 1], kt[e + 2], kt[e + 3]});
-        } else {
-#pragma unroll
-          for (int e = 0; e < KPL; ++e) skt.put1(ri * K + c0 + e, kt[e]);
-        }
-      }
-    }
   }
+  // every load of the phase (the J tiles' k rows, then the rows the per-row
+  // outputs need) before its first global store
+  f4 accAs[4], accQs[4];
+#pragma unroll
   for (int J = 0; J < 4; ++J) {
     f4 accA = f4_zero(), accQ = f4_zero();
     if (J <= I) {
@@ -228,15 +212,73 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
         }
       }
     }
+    accAs[J] = accA;
+    accQs[J] = accQ;
+  }
+  typename Mma<E>::Frag rq[NKS], rk[NKS];
+  if (ro.Qg) {
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+      const bool live = ri < in.nvalid;
+      rq[s] = live ? Mma<E>::ld(in.q + (size_t)(in.t0 + ri) * in.rowQ + c0) : Mma<E>::zero();
+      rk[s] = live ? Mma<E>::ld(in.k + (size_t)(in.t0 + ri) * in.rowK + c0) : Mma<E>::zero();
+    }
+  }
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
     f4 qt;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = r + acc_row(rr), j = 16 * J + acc_col();
-      s_A[i * AT_LD + j] = (j < i) ? accA[rr] : 0.f;
-      qt[rr] = (j <= i) ? accQ[rr] : 0.f;
+      s_A[i * AT_LD + j] = (j < i) ? accAs[J][rr] : 0.f;
+      qt[rr] = (j <= i) ? accQs[J][rr] : 0.f;
       if (aqk_out) aqk_out[i * CH + j] = qt[rr];
     }
     if (aqkT_out) split_at<E>(aqkT_out, CH * CH).put4((16 * J + acc_col()) * CH + r + acc_row(0), qt);
+  }
+  if (ro.Qg) {
+    // Kt (split) and Kt^T (split), then Qg (fp32) and Qg^T (split): each
+    // value computed once into the LDS scratch s_x [64 columns][CH + 4],
+    // then written from there row-major and transposed, 16-byte rows both
+    constexpr int LDX = CH + 4;
+    for (int which = 0; which < 2; ++which) {
+      float* tp = which ? ro.QgT : ro.KtT;
+      float* rp = which ? ro.Qg : ro.Kt;
+      const SplitTile<E> tdst = split_at<E>(tp, K * CH), rdst = split_at<E>(rp, CH * K);
+      for (int hh = 0; hh < K / 64; ++hh) {
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) {
+          if (s * Mma<E>::KS / 64 != hh) continue;
+          const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) {
+            const float gi = s_gc[ri * GL + c0 + e];
+            s_x[(c0 + e - 64 * hh) * LDX + ri] =
+                which ? to_f(Mma<E>::elem(rq[s], e)) * in.scale * fexp(gi)
+                      : to_f(Mma<E>::elem(rk[s], e)) * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi);
+          }
+        }
+        __syncthreads();
+        if (tp) {
+          for (int idx = threadIdx.x; idx < 64 * CH / 4; idx += blockDim.x) {
+            const int kl = idx / (CH / 4), m = (idx % (CH / 4)) * 4;
+            tdst.put4((64 * hh + kl) * CH + m, *reinterpret_cast<const f4*>(s_x + kl * LDX + m));
+          }
+        }
+        if (rp) {
+          for (int idx = threadIdx.x; idx < CH * 64 / 4; idx += blockDim.x) {
+            const int m = idx / 16, kl = (idx % 16) * 4;
+            f4 x;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[j] = s_x[(kl + j) * LDX + m];
+            if (which) *reinterpret_cast<f4*>(rp + m * K + 64 * hh + kl) = x;   // Qg: fp32
+            else rdst.put4(m * K + 64 * hh + kl, x);
+          }
+        }
+        __syncthreads();
+      }
+    }
   }
 }
 

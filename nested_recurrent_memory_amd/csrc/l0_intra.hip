@@ -70,7 +70,9 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   {
     RowOut ro{a.Qg + cix * C * K, a.QgT ? a.QgT + cix * K * C : nullptr,
               a.Kt ? a.Kt + cix * C * K : nullptr, a.KtT + cix * K * C};
-    l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr, ro);
+    // s_T (free until the inversion) is the scratch for the transposed rows
+    l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr, ro,
+               s_T);
   }
   if (tid < K) a.gam[cix * K + tid] = fexp(s_gc[(C - 1) * GL + tid]);
   __syncthreads();
@@ -85,10 +87,15 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
 #pragma unroll
     for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::ld(trow + s * KS);
     if (a.TT) {
-      // TT[j][i] = T[i][j] for this wave's rows i: 16 lanes per column j
+      // TT[j][i] = T[i][j]: four consecutive i of one column j per thread
       float* tt = a.TT + cix * C * C;
-      const int i = R0 + (lane & 15);
-      for (int j = lane >> 4; j < C; j += 4) tt[j * C + i] = s_T[i * LT + j];
+      for (int e = tid; e < C * C / 4; e += 256) {
+        const int j = e / (C / 4), i = (e % (C / 4)) * 4;
+        f4 x;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = s_T[(i + r) * LT + j];
+        *reinterpret_cast<f4*>(tt + j * C + i) = x;
+      }
     }
   }
   __syncthreads();
@@ -116,15 +123,17 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   __syncthreads();
 
   // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w. The B fragments
-  // gather KPL consecutive rows m of one column.
+  // gather KPL consecutive rows m of one column. All tiles stay in registers
+  // until every wave has read X_w and X_u; then W and U replace them in LDS
+  // and leave in 16-byte rows (W, W^T and U), instead of 2- and 4-byte
+  // column-strided stores.
   {
-    const SplitTile<E> Wo = split_at<E>(a.W + cix * C * K, C * K);
-    float* Uo = a.U + cix * C * V;
-    const SplitTile<E> WTo = split_at<E>(a.WT ? a.WT + cix * K * C : nullptr, K * C);
-    const int i0 = R0 + acc_row(0);
-    for (int tc = 0; tc < (K + V) / 16; ++tc) {
-      const bool isw = tc < K / 16;
-      const int col = (isw ? tc : tc - K / 16) * 16 + (lane & 15);
+    constexpr int NTW = K / 16, NTU = V / 16;
+    f4 wt[NTW], ut[NTU];
+#pragma unroll
+    for (int tc = 0; tc < NTW + NTU; ++tc) {
+      const bool isw = tc < NTW;
+      const int col = (isw ? tc : tc - NTW) * 16 + (lane & 15);
       const float* xb = isw ? s_xw + col : s_xu + col;
       const int ld = isw ? GL : LU;
       f4 acc = f4_zero();
@@ -135,13 +144,42 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
           acc = Mma<E>::mma(acc, tf[s], Mma<E>::makes([&](int e) { return xb[(m0 + e) * ld]; }));
         }
       }
-      if (isw) {
+      if (isw) wt[tc] = acc; else ut[tc - NTW] = acc;
+    }
+    __syncthreads();   // X_w and X_u are no longer read
+    constexpr int LW = K + 4, LUU = V + 4;   // fp32 rows, 16-byte aligned
+    float* s_w = reinterpret_cast<float*>(smem);    // [C][LW], then U [C][LUU]
+    float* s_u = s_w + C * LW;
+    static_assert(sizeof(float) * C * (LW + LUU) <= SZ_GC + SZ_R, "W and U fit the LDS");
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Wo.put1((i0 + rr) * K + col, acc[rr]);
-        if (a.WT) WTo.put4(col * C + i0, acc);
-      } else {
+    for (int t = 0; t < NTW; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Uo[(i0 + rr) * V + col] = acc[rr];
+      for (int r = 0; r < 4; ++r) s_w[(R0 + acc_row(r)) * LW + t * 16 + acc_col()] = wt[t][r];
+#pragma unroll
+    for (int t = 0; t < NTU; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_u[(R0 + acc_row(r)) * LUU + t * 16 + acc_col()] = ut[t][r];
+    __syncthreads();
+    // W [C][K] (split), U [C][V] (fp32): four consecutive columns per thread
+    const SplitTile<E> Wo = split_at<E>(a.W + cix * C * K, C * K);
+    for (int e = tid; e < C * K / 4; e += 256) {
+      const int i = e / (K / 4), c = (e % (K / 4)) * 4;
+      Wo.put4(i * K + c, *reinterpret_cast<const f4*>(s_w + i * LW + c));
+    }
+    float* Uo = a.U + cix * C * V;
+    for (int e = tid; e < C * V / 4; e += 256) {
+      const int i = e / (V / 4), c = (e % (V / 4)) * 4;
+      *reinterpret_cast<f4*>(Uo + i * V + c) = *reinterpret_cast<const f4*>(s_u + i * LUU + c);
+    }
+    // W^T [K][C] (split): four consecutive rows of one column per thread
+    if (a.WT) {
+      const SplitTile<E> WTo = split_at<E>(a.WT + cix * K * C, K * C);
+      for (int e = tid; e < K * C / 4; e += 256) {
+        const int c = e / (C / 4), i = (e % (C / 4)) * 4;
+        f4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = s_w[(i + j) * LW + c];
+        WTo.put4(c * C + i, x);
       }
     }
   }

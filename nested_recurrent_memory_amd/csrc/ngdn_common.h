@@ -86,6 +86,7 @@ template <> struct Mma<bf16> {
     }
     return r;
   }
+  __device__ __forceinline__ static bf16 elem(const Frag& f, int e) { return f[e]; }
   // exact values (inputs, or products known to be exact in bf16)
   template <typename F>
   __device__ __forceinline__ static Frag make(F f) {  // f(e) -> float, e < KPL
@@ -127,6 +128,7 @@ template <> struct Mma<float> {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
   }
   __device__ __forceinline__ static float ld(const float* p) { return *p; }
+  __device__ __forceinline__ static float elem(float f, int) { return f; }
   template <typename F>
   __device__ __forceinline__ static float make(F f) { return f(0); }
   template <typename F>
