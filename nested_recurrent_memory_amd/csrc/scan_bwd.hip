@@ -43,6 +43,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int NSM = (M + KS - 1) / KS;
   constexpr bool PADM = (M % KS) != 0;
   constexpr int DOE = M * BV / 256;           // dO elements staged per thread
+  static_assert(M != CH || (BV % DOE == 0 && 256 / (BV / DOE) == M && DOE % 8 == 0),
+                "level 0: one token row slice per thread");
   static_assert(TPW % CT == 0, "state tiles of a wave come in whole rows");
   // dS'^T, dVn^T and (mix_0 dO)^T, split once by their writers
   __shared__ __attribute__((aligned(16))) typename ST::T s_dst[ST::NPLANE * BV * LDS_ST];
@@ -136,18 +138,36 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       for (int s = 0; s < NSM; ++s)
         o.at[t][s] = (!PADM || s * KS + kofs<E>(lane) < M) ? Aj.get(arow + s * KS) : Mma<E>::szero();
       if (l0) {
-        const SplitTile<E> Gj = split_at<E>(a.QgT + ((size_t)bh * S + j) * K * M, K * M);
+        const SplitTile<E> QTj = split_at<E>(a.QgT + ((size_t)bh * S + j) * K * M, K * M);
 #pragma unroll
-        for (int s = 0; s < NSM; ++s) o.qg[t][s] = Gj.get(arow + s * KS);
+        for (int s = 0; s < NSM; ++s) o.qg[t][s] = QTj.get(arow + s * KS);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
     }
     if (l0) {
+      // DOE consecutive columns of one token per thread: one vector load
+      const int c = tid / (BV / DOE), vl = (tid % (BV / DOE)) * DOE, t = j * M + c;
+      if (t < a.T) {
+        const E* src = dob + (size_t)t * H * V + v0 + vl;
+        const float m = to_f(mixb[(size_t)t * H * a.L]);
+        float x[DOE];
+        if constexpr (std::is_same<E, float>::value) {
 #pragma unroll
-      for (int q = 0; q < DOE; ++q) {
-        const int e = tid + q * 256, c = e / BV, vl = e % BV, t = j * M + c;
-        o.dov[q] = t < a.T ? to_f(dob[(size_t)t * H * V + v0 + vl]) * to_f(mixb[(size_t)t * H * a.L]) : 0.f;
+          for (int q = 0; q < DOE; q += 4) {
+            const f4 y = *reinterpret_cast<const f4*>(src + q);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[q + u] = y[u];
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < DOE; q += 8) ld_vals<E>(src + q, x + q);
+        }
+#pragma unroll
+        for (int q = 0; q < DOE; ++q) o.dov[q] = x[q] * m;
+      } else {
+#pragma unroll
+        for (int q = 0; q < DOE; ++q) o.dov[q] = 0.f;
       }
     }
     // added before the step (level-0 injection) or after it (upper read gradient)
@@ -182,11 +202,9 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       sdS.put4(vl * LDS_ST + k0, ds[i]);
     }
     if (l0) {
+      const int c = tid / (BV / DOE), vl = (tid % (BV / DOE)) * DOE;
 #pragma unroll
-      for (int q = 0; q < DOE; ++q) {
-        const int e = tid + q * 256, c = e / BV, vl = e % BV;
-        sdO.put1(vl * LDS_VN + c, cur.dov[q]);
-      }
+      for (int q = 0; q < DOE; ++q) sdO.put1((vl + q) * LDS_VN + c, cur.dov[q]);
     }
     __syncthreads();
 
