@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDI : 0;
   constexpr size_t SZ_P = SZ_DA + SZ_G + SZ_IN;
   constexpr size_t SZ_R = SZ_X > SZ_P ? SZ_X : SZ_P;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * 2 * K];
+  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (2 * K + 256)];
   float* s_dXw = reinterpret_cast<float*>(smem);
   float* s_dXu = s_dXw + C * LXK;
   float* s_dA = reinterpret_cast<float*>(smem);
@@ -185,6 +185,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   E* s_q = s_b + C * LDI;
   float* s_gl = reinterpret_cast<float*>(smem + SZ_R);   // gc of the last row, per column
   float* s_col = s_gl + K;
+  float* s_part = s_col + K;                              // [256 / NH][NH] block sums of phase 6
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -197,36 +198,49 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   const int t0 = in.t0, nvalid = in.nvalid;
   for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
 
-  // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns rows 16w..16w+15
+  // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns a quarter of the
+  // columns of each and every row, so each wave splits the small T^T (all
+  // of it) and only its quarter of dVn^T and dW^T, instead of every wave
+  // splitting all of dVn^T and dW^T for its own rows
   const int ri = wv * 16 + (lane & 15);
   f4 dxw[CTK];
   {
-    SF tf[C / KS];
-    const float* tt = a.TT + cix * C * C + (size_t)ri * C + kofs<E>(lane);
+    static_assert(CTV % 4 == 0 && CTK % 4 == 0, "column tiles split over 4 waves");
+    SF tf[4][C / KS];
 #pragma unroll
-    for (int s = 0; s < C / KS; ++s) tf[s] = Mma<E>::ld(tt + s * KS);
-    const float* dvT = a.dVnT + cix * V * C;
-    const float* dwT = a.dWT + cix * K * C;
-    for (int ct = 0; ct < CTV; ++ct) {
-      f4 acc = f4_zero();
-      const float* br = dvT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+    for (int rt = 0; rt < 4; ++rt) {
+      const float* tt = a.TT + cix * C * C + (size_t)(rt * 16 + (lane & 15)) * C + kofs<E>(lane);
 #pragma unroll
-      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::ld(br + s * KS));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_dXu[(wv * 16 + acc_row(r)) * LXV + ct * 16 + acc_col()] = acc[r];
+      for (int s = 0; s < C / KS; ++s) tf[rt][s] = Mma<E>::ld(tt + s * KS);
     }
+    auto product = [&](const float* srcT, int ncols, float* dst, int ldd) {
+      const int cpw = ncols / 16 / 4;   // column tiles per wave
+#pragma unroll 1
+      for (int c = 0; c < cpw; ++c) {
+        const int ct = wv * cpw + c;
+        const float* br = srcT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+        SF fb[C / KS];
 #pragma unroll
-    for (int ct = 0; ct < CTK; ++ct) {
-      f4 acc = f4_zero();
-      const float* br = dwT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
+        for (int s = 0; s < C / KS; ++s) fb[s] = Mma<E>::ld(br + s * KS);
 #pragma unroll
-      for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[s], Mma<E>::ld(br + s * KS));
-      dxw[ct] = acc;
+        for (int rt = 0; rt < 4; ++rt) {
+          f4 acc = f4_zero();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_dXw[(wv * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()] = acc[r];
-    }
+          for (int s = 0; s < C / KS; ++s) acc = Mma<E>::mma(acc, tf[rt][s], fb[s]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(rt * 16 + acc_row(r)) * ldd + ct * 16 + acc_col()] = acc[r];
+        }
+      }
+    };
+    product(a.dVnT + cix * V * C, V, s_dXu, LXV);
+    product(a.dWT + cix * K * C, K, s_dXw, LXK);
   }
   __syncthreads();
+  // this wave's rows of dX_w, kept for phase 5 (the space is reused from phase 4)
+#pragma unroll
+  for (int ct = 0; ct < CTK; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dxw[ct][r] = s_dXw[(wv * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()];
 
   // dv = dX_u * w, dw = dX_u * v: 16-byte rows, all loads of a thread ahead of its stores
   {
@@ -452,13 +466,25 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     __syncthreads();
 
     // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
-    // every Kt and gam
-    if (tid < NH) {
-      const int kc = c0 + tid;
+    // every Kt and gam. Column col of this pass, rows in NB blocks of RB: each
+    // thread sums its block, then runs through it from the sum of the blocks
+    // after it.
+    {
+      constexpr int NB = 256 / NH, RB = C / NB;
+      static_assert(256 % NH == 0 && C % NB == 0, "whole row blocks per column");
+      const int col = tid % NH, blk = tid / NH, kc = c0 + col;
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < RB; ++i) part += s_g[(blk * RB + i) * GH + col];
+      s_part[blk * NH + col] = part;
+      __syncthreads();
       float run = s_col[kc] + dgam[kc] * fexp(s_gl[kc]);
-      for (int i = C - 1; i >= 0; --i) {
-        run += s_g[i * GH + tid];
-        if (i < nvalid) dgo[(size_t)(t0 + i) * H * K + kc] = run;
+      for (int b2 = NB - 1; b2 > blk; --b2) run += s_part[b2 * NH + col];
+#pragma unroll
+      for (int i = RB - 1; i >= 0; --i) {
+        const int row = blk * RB + i;
+        run += s_g[row * GH + col];
+        if (row < nvalid) dgo[(size_t)(t0 + row) * H * K + kc] = run;
       }
     }
     __syncthreads();   // the next pass restages gc and the inputs
