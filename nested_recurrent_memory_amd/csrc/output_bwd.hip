@@ -31,23 +31,37 @@ __global__ __launch_bounds__(256) void dmix0_kernel(Dmix0Args a) {
 
 template <typename E, int K, int V>
 __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a) {
-  // 8 waves: for the per-chunk products wave w owns row tile w % 4 and half
-  // the columns (w / 4); the group's dS tiles are dealt round robin
-  constexpr int NW = 8;
+  // Per (batch, group j, head), over the group's chunks, with S = S_l[j]:
+  //   P = do S^T                        (one product, exact do x split S)
+  //   dq_l = scale mix_l P,  dmix_l = scale rowsum(q_l * P)
+  //                                     (= <do, scale q_l S>, without forming q_l S)
+  //   dS_l += scale q_l^T (mix_l do)    (exact q^T x split (mix do)^T)
+  // S is staged once as a split tile; each chunk stages do rows (exact),
+  // q^T (exact) and (mix do)^T (split), so every fragment is a 16-byte read.
+  // 8 waves: for P, wave w owns row tile w % 4 and half the K tiles (w / 4);
+  // the group's dS tiles are dealt round robin.
+  constexpr int NW = 8, NTH = 512;
   constexpr int C = CH;
-  constexpr int LDS = V + 4;                     // staged S rows (fp32)
-  constexpr int LDQ = K + 16 / (int)sizeof(E);   // staged q rows (exact)
-  constexpr int LDD = V + 16 / (int)sizeof(E);   // staged do rows (exact)
+  using ST = SplitTile<E>;
+  constexpr int PE = 16 / (int)sizeof(E);        // exact elements per 16 bytes
+  constexpr int LDS_ = V + ST::PAD;              // S rows [K][V] (split)
+  constexpr int LDD = V + PE;                    // do rows [C][V] (exact)
+  constexpr int LDQT = C + PE;                   // q^T rows [K][C] (exact)
+  constexpr int LDDT = C + ST::PAD;              // (mix do)^T rows [V][C] (split)
   constexpr int KT = K / 16, VT = V / 16;
-  constexpr int VTH = VT / 2, KTH = KT / 2;      // column tiles per wave of read / dq
+  constexpr int KTH = KT / 2;                    // K tiles per wave of P
   constexpr int NDS = KT * VT / NW;              // dS tiles per wave
   constexpr int KS = Mma<E>::KS;
-  static_assert(KT * VT % NW == 0 && VT % 2 == 0 && KT % 2 == 0, "tiles split over 8 waves");
-  typedef typename Mma<E>::SFrag SF;
-  __shared__ __attribute__((aligned(16))) float s_S[K * LDS];
-  __shared__ __attribute__((aligned(16))) E s_q[C * LDQ];
-  __shared__ __attribute__((aligned(16))) E s_do[C * LDD];
+  static_assert(KT * VT % NW == 0 && KT % 2 == 0, "tiles split over 8 waves");
+  // fp32 inputs (a test-only path) read the do rows of P from global memory:
+  // a staged copy would not fit next to the fp32 tiles
+  constexpr bool STAGE_DO = !std::is_same<E, float>::value;
+  __shared__ __attribute__((aligned(16))) typename ST::T s_s[ST::NPLANE * K * LDS_];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_dt[ST::NPLANE * V * LDDT];
+  __shared__ __attribute__((aligned(16))) E s_do[STAGE_DO ? C * LDD : 4];
+  __shared__ __attribute__((aligned(16))) E s_qt[K * LDQT];
   __shared__ float s_mix[C], s_dm[C];
+  const ST sS{s_s, K * LDS_}, sDT{s_dt, V * LDDT};
 
   const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
   const int j = blockIdx.x % NG;
@@ -62,7 +76,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   E* dqb = static_cast<E*>(a.dq) + ((size_t)b * T * H + h) * L * K + (size_t)l * K;
   float* dmb = a.dmix + ((size_t)b * T * H + h) * L + l;
 
-  stage_f32(s_S, LDS, a.states + (((size_t)b * NG + j) * H + h) * K * V, V, K, V);
+  stage_split(sS, LDS_, a.states + (((size_t)b * NG + j) * H + h) * K * V, V, K, V);
 
   f4 acc[NDS];
 #pragma unroll
@@ -70,36 +84,79 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   const int rt = wv % 4, half = wv / 4;
   const int ri = rt * 16 + (lane & 15);          // this wave's rows of the chunk
   const int n1 = min((j + 1) * a.f, NT);
+  // The next chunk's rows are read into registers while this chunk computes
+  // (before its stores), then written to LDS at the top of the next iteration.
+  constexpr int QG = C * K / PE / NTH, DG = C * V / PE / NTH;   // 16-byte groups per thread
+  static_assert(C * K / PE % NTH == 0 && C * V / PE % NTH == 0, "whole groups per thread");
+  typedef E EV __attribute__((__vector_size__(16)));
+  EV qv[QG], dv[DG];
+  float mv[DG];
+  auto fetch = [&](int n) {
+    const int t0 = n * C, nv = min(C, T - t0);
+#pragma unroll
+    for (int u = 0; u < QG; ++u) {
+      const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+      qv[u] = i < nv ? *reinterpret_cast<const EV*>(qb + (size_t)(t0 + i) * rowQ + c) : EV{};
+    }
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+      dv[u] = i < nv ? *reinterpret_cast<const EV*>(db + (size_t)(t0 + i) * rowV + c) : EV{};
+      mv[u] = i < nv ? to_f(mb[(size_t)(t0 + i) * H * L]) : 0.f;
+    }
+  };
+  if (j * a.f < n1) fetch(j * a.f);
   for (int n = j * a.f; n < n1; ++n) {
     const int t0 = n * C, nv = min(C, T - t0);
-    stage_rows<E>(s_q, LDQ, qb + (size_t)t0 * rowQ, rowQ, C, K, nv);
-    stage_rows<E>(s_do, LDD, db + (size_t)t0 * rowV, rowV, C, V, nv);
-    if (tid < C) {
-      s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
-      s_dm[tid] = 0.f;
+    // ---- staging of the fetched rows
+    {
+#pragma unroll
+      for (int u = 0; u < QG; ++u) {
+        const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+#pragma unroll
+        for (int x = 0; x < PE; ++x) s_qt[(c + x) * LDQT + i] = qv[u][x];
+      }
+#pragma unroll
+      for (int u = 0; u < DG; ++u) {
+        const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+        if constexpr (STAGE_DO) *reinterpret_cast<EV*>(s_do + i * LDD + c) = dv[u];
+#pragma unroll
+        for (int x = 0; x < PE; ++x) sDT.put1((c + x) * LDDT + i, to_f(dv[u][x]) * mv[u]);
+      }
+      if (tid < C) {
+        s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
+        s_dm[tid] = 0.f;
+      }
     }
     __syncthreads();
+    if (n + 1 < n1) fetch(n + 1);
 
-    // ---- read_l = q S on this wave's rows and half of V -> partial dmix_l
+    // ---- P = do S^T on this wave's rows and half of K; dq and partial dmix
     {
-      f4 rd[VTH];
+      f4 pp[KTH];
 #pragma unroll
-      for (int y = 0; y < VTH; ++y) rd[y] = f4_zero();
+      for (int x = 0; x < KTH; ++x) pp[x] = f4_zero();
 #pragma unroll
-      for (int s = 0; s < K / KS; ++s) {
-        const int k0 = s * KS + kofs<E>(lane);
-        const auto fa = Mma<E>::ld(s_q + ri * LDQ + k0);
+      for (int s = 0; s < V / KS; ++s) {
+        const int v0 = s * KS + kofs<E>(lane);
+        typename Mma<E>::Frag fa;
+        if constexpr (STAGE_DO) fa = Mma<E>::ld(s_do + ri * LDD + v0);
+        else fa = ri < nv ? Mma<E>::ld(db + (size_t)(t0 + ri) * rowV + v0) : Mma<E>::zero();
 #pragma unroll
-        for (int y = 0; y < VTH; ++y)
-          rd[y] = Mma<E>::mma(rd[y], fa,
-                              gather_s<E>(s_S + k0 * LDS + (half * VTH + y) * 16 + (lane & 15), LDS));
+        for (int x = 0; x < KTH; ++x)
+          pp[x] = Mma<E>::mma(pp[x], fa, sS.get(((half * KTH + x) * 16 + (lane & 15)) * LDS_ + v0));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rt * 16 + acc_row(r);
+        const float m = s_mix[i] * a.scale;
         float sm = 0.f;
 #pragma unroll
-        for (int y = 0; y < VTH; ++y) sm += to_f(s_do[i * LDD + (half * VTH + y) * 16 + acc_col()]) * rd[y][r];
+        for (int x = 0; x < KTH; ++x) {
+          const int k = (half * KTH + x) * 16 + acc_col();
+          sm += to_f(s_qt[k * LDQT + i]) * pp[x][r];
+          if (i < nv) dqb[(size_t)(t0 + i) * rowQ + k] = from_f<E>(pp[x][r] * m);
+        }
         sm += __shfl_xor(sm, 1, WAVE);
         sm += __shfl_xor(sm, 2, WAVE);
         sm += __shfl_xor(sm, 4, WAVE);
@@ -107,42 +164,15 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         if ((lane & 15) == 0) atomicAdd(&s_dm[i], sm);
       }
     }
-    // ---- dq_l = scale dO S^T on this wave's rows and half of K
-    {
-      f4 dq[KTH];
-#pragma unroll
-      for (int x = 0; x < KTH; ++x) dq[x] = f4_zero();
-      const float m = s_mix[ri];
-#pragma unroll
-      for (int s = 0; s < V / KS; ++s) {
-        const int v0 = s * KS + kofs<E>(lane);
-        const SF fa = Mma<E>::makes([&](int e) { return to_f(s_do[ri * LDD + v0 + e]) * m; });
-#pragma unroll
-        for (int x = 0; x < KTH; ++x)
-          dq[x] = Mma<E>::mma(dq[x], fa, Mma<E>::ld(s_S + ((half * KTH + x) * 16 + (lane & 15)) * LDS + v0));
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = rt * 16 + acc_row(r);
-        if (i < nv) {
-#pragma unroll
-          for (int x = 0; x < KTH; ++x)
-            dqb[(size_t)(t0 + i) * rowQ + (half * KTH + x) * 16 + acc_col()] = from_f<E>(dq[x][r] * a.scale);
-        }
-      }
-    }
-    // ---- dS += q^T dO: the reduction runs down the staged rows, fragments
-    // gathered down columns
+    // ---- dS += q^T (mix do): q^T rows exact, (mix do)^T rows split
 #pragma unroll
     for (int s = 0; s < C / KS; ++s) {
       const int r0 = s * KS + kofs<E>(lane);
 #pragma unroll
       for (int x = 0; x < NDS; ++x) {
         const int g = wv + NW * x, kt = g / VT, vt = g % VT;
-        const auto fa = gather_x<E>(s_q + r0 * LDQ + kt * 16 + (lane & 15), LDQ);
-        const E* pd = s_do + r0 * LDD + vt * 16 + (lane & 15);
-        const auto fb = Mma<E>::makes([&](int e) { return to_f(pd[e * LDD]) * s_mix[r0 + e]; });
-        acc[x] = Mma<E>::mma(acc[x], fa, fb);
+        const auto fa = Mma<E>::ld(s_qt + (kt * 16 + (lane & 15)) * LDQT + r0);
+        acc[x] = Mma<E>::mma(acc[x], fa, sDT.get((vt * 16 + (lane & 15)) * LDDT + r0));
       }
     }
     __syncthreads();
