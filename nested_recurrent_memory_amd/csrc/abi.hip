@@ -378,7 +378,10 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
     return fail(NGDN_EINVAL, "ngdn_param_grads: NULL tensor");
   if (nf <= 0) return NGDN_OK;
   const size_t off = (size_t)(level - 1) * d->H * d->K * d->V;
-  const int split = std::max(1, std::min(32, (d->B * nf + 3) / 4));
+  // firings split over up to 16 workgroups per head, at least 4 firings
+  // each: every workgroup adds its X x Y partial with atomics, so more
+  // workgroups cost more atomics (measured best at c2 for both levels)
+  const int split = std::max(1, std::min(16, (d->B * nf + 3) / 4));
   hipStream_t st = (hipStream_t)stream;
   ngdn::AtBArgs a{};
   a.B = d->B; a.H = d->H; a.NF = nf; a.N = n_pairs; a.X = d->K; a.Y = d->V; a.split = split;

@@ -457,14 +457,21 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 
 template <typename E, int X, int Y>
 __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
+  // C[h] += sum over rows n of A[n]^T B[n]. Slabs of R rows are staged
+  // transposed as split tiles (A^T [X][R], B^T [Y][R], the reduction index
+  // contiguous), each value split once by the thread that stages it; every
+  // fragment is then a 16-byte read.
   constexpr int R = 32;                      // rows per staged slab
-  constexpr int LDA = X + 4, LDB = Y + 4;
+  using ST = SplitTile<E>;
+  constexpr int LDT = R + ST::PAD;
   constexpr int XT = X / 16, YT = Y / 16;
   constexpr int XTW = XT / 4;                // x-tiles per wave (all y-tiles each)
   constexpr int KS = Mma<E>::KS;
   static_assert(XT % 4 == 0, "X must split over the 4 waves");
-  __shared__ __attribute__((aligned(16))) float s_A[R * LDA];
-  __shared__ __attribute__((aligned(16))) float s_B[R * LDB];
+  static_assert(X * R % (256 * 4) == 0 && Y * R % (256 * 4) == 0, "whole groups of 4 rows");
+  __shared__ __attribute__((aligned(16))) typename ST::T s_at[ST::NPLANE * X * LDT];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_bt[ST::NPLANE * Y * LDT];
+  const ST sA{s_at, X * LDT}, sB{s_bt, Y * LDT};
   const int H = a.H, NF = a.NF, N = a.N;
   const int part = blockIdx.x % a.split;
   const int h = blockIdx.x / a.split;
@@ -478,41 +485,57 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
   for (int x = 0; x < XTW; ++x)
 #pragma unroll
     for (int y = 0; y < YT; ++y) acc[x][y] = f4_zero();
-  for (int it = it0; it < it1; ++it) {
-    const int b = it / NF, i = it % NF;
-    const size_t base = (((size_t)b * H + h) * NF + i) * N;
-    for (int n0 = 0; n0 < N; n0 += R) {
-      const int nr = min(R, N - n0);
-      // rows of the reduction, zero past N
-      for (int e = tid; e < R * X / 4; e += 256) {
-        const int r = e / (X / 4), c = (e % (X / 4)) * 4;
-        f4 v = f4_zero();
-        if (r < nr) v = *reinterpret_cast<const f4*>(a.A + (base + n0 + r) * X + c);
-        *reinterpret_cast<f4*>(s_A + r * LDA + c) = v;
-      }
-      for (int e = tid; e < R * Y / 4; e += 256) {
-        const int r = e / (Y / 4), c = (e % (Y / 4)) * 4;
-        f4 v = f4_zero();
-        if (r < nr) v = *reinterpret_cast<const f4*>(a.Bm + (base + n0 + r) * Y + c);
-        *reinterpret_cast<f4*>(s_B + r * LDB + c) = v;
-      }
-      __syncthreads();
+  // A thread stages 4 consecutive rows of one column (a wave reads whole
+  // rows); the next slab is read into registers while this one is multiplied.
+  constexpr int GA = X * R / 4 / 256, GB = Y * R / 4 / 256;   // 4-row groups per thread
+  f4 ra[GA], rb[GB];
+  const int slabs_per_item = (N + R - 1) / R;
+  const int nslab = (it1 - it0) * slabs_per_item;
+  auto fetch = [&](int sl) {
+    const int it = it0 + sl / slabs_per_item, n0 = (sl % slabs_per_item) * R;
+    const int b = it / NF, i = it % NF, nr = min(R, N - n0);
+    const size_t row0 = (((size_t)b * H + h) * NF + i) * N + n0;
 #pragma unroll
-      for (int s = 0; s < R / KS; ++s) {
-        const int r0 = s * KS + kofs<E>(lane);
-        typename Mma<E>::SFrag fa[XTW];
+    for (int u = 0; u < GA; ++u) {
+      const int e = tid + 256 * u, c = e % X, r4 = (e / X) * 4;
 #pragma unroll
-        for (int x = 0; x < XTW; ++x)
-          fa[x] = gather_s<E>(s_A + r0 * LDA + (wv * XTW + x) * 16 + (lane & 15), LDA);
-#pragma unroll
-        for (int y = 0; y < YT; ++y) {
-          const auto fb = gather_s<E>(s_B + r0 * LDB + y * 16 + (lane & 15), LDB);
-#pragma unroll
-          for (int x = 0; x < XTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
-        }
-      }
-      __syncthreads();
+      for (int j = 0; j < 4; ++j) ra[u][j] = r4 + j < nr ? a.A[(row0 + r4 + j) * X + c] : 0.f;
     }
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+      const int e = tid + 256 * u, c = e % Y, r4 = (e / Y) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rb[u][j] = r4 + j < nr ? a.Bm[(row0 + r4 + j) * Y + c] : 0.f;
+    }
+  };
+  fetch(0);
+  for (int sl = 0; sl < nslab; ++sl) {
+#pragma unroll
+    for (int u = 0; u < GA; ++u) {
+      const int e = tid + 256 * u;
+      sA.put4((e % X) * LDT + (e / X) * 4, ra[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+      const int e = tid + 256 * u;
+      sB.put4((e % Y) * LDT + (e / Y) * 4, rb[u]);
+    }
+    __syncthreads();
+    if (sl + 1 < nslab) fetch(sl + 1);
+#pragma unroll
+    for (int s = 0; s < R / KS; ++s) {
+      const int r0 = s * KS + kofs<E>(lane);
+      typename Mma<E>::SFrag fa[XTW];
+#pragma unroll
+      for (int x = 0; x < XTW; ++x) fa[x] = sA.get(((wv * XTW + x) * 16 + (lane & 15)) * LDT + r0);
+#pragma unroll
+      for (int y = 0; y < YT; ++y) {
+        const auto fb = sB.get((y * 16 + (lane & 15)) * LDT + r0);
+#pragma unroll
+        for (int x = 0; x < XTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
+      }
+    }
+    __syncthreads();
   }
   float* C = a.C + (size_t)h * X * Y;
 #pragma unroll
