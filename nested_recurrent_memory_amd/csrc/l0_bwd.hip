@@ -19,52 +19,61 @@
 namespace ngdn {
 
 template <typename E, int K, int V>
-__global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
-  // Per (b, h, chunk), in halves of V: S[:, half] and dS'[:, half] are staged
-  // once as split tiles (each value split by one thread, not by every wave
-  // that reads it); every product accumulates over the halves. dgam, a plain
-  // fp32 dot product, is summed from the fp32 values while they are staged.
+__global__ __launch_bounds__(256, sizeof(E) == 2 ? 3 : 2) void l0_bwd_state_kernel(L0BwdStateArgs a) {
+  // Per (b, h, chunk) and half of K: output column k of dQg, dW and dKt needs
+  // only row k of S and dS', so the two halves of K are two workgroups (on one
+  // XCD) that each read their half of the state once. Within a workgroup, in
+  // halves of V, S[khalf, vhalf] and dS'[khalf, vhalf] are staged once as
+  // split tiles (each value split by one thread, not by every wave that reads
+  // it) and every product accumulates over the halves; dgam, a plain fp32 dot
+  // product, is summed from the fp32 values while they are staged. Wave w owns
+  // rows 16 w of the chunk; the dAqk tiles J = khalf, khalf + 2 of its rows.
   constexpr int C = CH;
+  constexpr int KH = K / 2;                    // rows of K per workgroup
   constexpr int VH = V > 64 ? 64 : V;          // columns of V per half
   constexpr int NHV = V / VH;
   using ST = SplitTile<E>;
   constexpr int LDH = VH + ST::PAD;
-  constexpr int CTK = K / 16;
+  constexpr int CTW = KH / 16;                 // column tiles per wave
   constexpr int KS = Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
   constexpr int NKH = VH / KS;                 // k-steps per half
   constexpr int Q4 = VH / 4;                   // 16-byte groups per staged row
-  constexpr int SIT = K * Q4 / 256;            // staged groups per thread per tensor
-  static_assert(K * Q4 % 256 == 0 && 256 % Q4 == 0, "staging covers whole rows");
+  constexpr int SIT = KH * Q4 / 256;           // staged groups per thread per tensor
+  static_assert(KH * Q4 % 256 == 0 && WAVE % Q4 == 0, "staging covers whole rows");
   typedef typename Mma<E>::SFrag SF;
-  __shared__ __attribute__((aligned(16))) typename ST::T s_s[ST::NPLANE * K * LDH];
-  __shared__ __attribute__((aligned(16))) typename ST::T s_d[ST::NPLANE * K * LDH];
-  const ST sS{s_s, K * LDH}, sD{s_d, K * LDH};
+  __shared__ __attribute__((aligned(16))) typename ST::T s_s[ST::NPLANE * KH * LDH];
+  __shared__ __attribute__((aligned(16))) typename ST::T s_d[ST::NPLANE * KH * LDH];
+  const ST sS{s_s, KH * LDH}, sD{s_d, KH * LDH};
 
   const int NT = a.NT, H = a.H, T = a.T;
-  const int n = blockIdx.x % NT;
-  const int bh = blockIdx.x / NT;
+  int unit, kh;
+  xcd_split(blockIdx.x, gridDim.x, 2, unit, kh);
+  const int n = unit % NT;
+  const int bh = unit / NT;
   const int h = bh % H, b = bh / H;
   const int t0 = n * C;
   const int nvalid = min(C, T - t0);
-  const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const int lane = lane_id(), tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());
   const size_t cix = (size_t)bh * NT + n;
-  const float* Sg = a.h + cix * K * V;
-  const float* dsp = a.dSp + cix * K * V;
+  // uniform bases with 32-bit per-lane offsets (one address register each)
+  const float* Sg = a.h + cix * K * V + (size_t)kh * KH * V;
+  const float* dsp = a.dSp + cix * K * V + (size_t)kh * KH * V;
 
   // A fragments of this wave's 16 rows: dO (from do and mix_0), dVn, Vn
   const int ri = wv * 16 + (lane & 15);
   const int rc = min(ri, nvalid - 1);
-  const E* dop = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V + (size_t)(t0 + rc) * H * V;
+  const E* dob = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V + (size_t)t0 * H * V;
+  const unsigned dor = (unsigned)(rc * H * V);
   const float m0 = ri < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + ri) * H * a.L + (size_t)h * a.L]) : 0.f;
-  const float* dvn = a.dVn + cix * C * V + (size_t)ri * V;
+  const float* dvnb = a.dVn + cix * C * V;
   const float* vnc = a.vn + cix * C * V;
 
-  f4 aq[CTK], aw[CTK], ak[CTK], adq[4];
+  f4 aq[CTW], aw[CTW], ak[CTW], adq[2];
 #pragma unroll
-  for (int ct = 0; ct < CTK; ++ct) { aq[ct] = f4_zero(); aw[ct] = f4_zero(); ak[ct] = f4_zero(); }
-#pragma unroll
-  for (int J = 0; J < 4; ++J) adq[J] = f4_zero();
+  for (int c = 0; c < CTW; ++c) { aq[c] = f4_zero(); aw[c] = f4_zero(); ak[c] = f4_zero(); }
+  adq[0] = adq[1] = f4_zero();
   float dg[SIT];
 #pragma unroll
   for (int i = 0; i < SIT; ++i) dg[i] = 0.f;
@@ -73,44 +82,45 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   for (int hv = 0; hv < NHV; ++hv) {
     const int vb = hv * VH;
     if (hv) __syncthreads();                   // the previous half's reads are done
+    f4 xs[SIT], ys[SIT];
+#pragma unroll
+    for (int i = 0; i < SIT; ++i) {
+      const int e = tid + 256 * i;
+      const unsigned o = (unsigned)((e / Q4) * V + vb + (e % Q4) * 4);
+      xs[i] = *reinterpret_cast<const f4*>(Sg + o);
+      ys[i] = *reinterpret_cast<const f4*>(dsp + o);
+    }
 #pragma unroll
     for (int i = 0; i < SIT; ++i) {
       const int e = tid + 256 * i, k = e / Q4, c = (e % Q4) * 4;
-      const f4 x = *reinterpret_cast<const f4*>(Sg + (size_t)k * V + vb + c);
-      const f4 y = *reinterpret_cast<const f4*>(dsp + (size_t)k * V + vb + c);
-      dg[i] += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
-      sS.put4(k * LDH + c, x);
-      sD.put4(k * LDH + c, y);
+      dg[i] += xs[i][0] * ys[i][0] + xs[i][1] * ys[i][1] + xs[i][2] * ys[i][2] + xs[i][3] * ys[i][3];
+      sS.put4(k * LDH + c, xs[i]);
+      sD.put4(k * LDH + c, ys[i]);
     }
-    SF fo[NKH], fd[NKH], fv[NKH];
+    __syncthreads();
+    // one k-step of A fragments live at a time
 #pragma unroll
     for (int s = 0; s < NKH; ++s) {
       const int v0 = vb + s * KS + kofs<E>(lane);
       float x[KPL];
-      ld_vals<E>(dop + v0, x);
-      fo[s] = Mma<E>::makes([&](int e) { return x[e] * m0; });
-      fd[s] = Mma<E>::ld(dvn + v0);
-      fv[s] = Mma<E>::ld(vnc + (size_t)ri * V + v0);
-    }
-    __syncthreads();
+      ld_vals<E>(dob + (dor + (unsigned)v0), x);
+      const SF fo = Mma<E>::makes([&](int e) { return x[e] * m0; });
+      const SF fd = Mma<E>::ld(dvnb + (unsigned)(ri * V + v0));
+      const SF fv = Mma<E>::ld(vnc + (unsigned)(ri * V + v0));
 #pragma unroll
-    for (int ct = 0; ct < CTK; ++ct) {
-      const int row = (ct * 16 + (lane & 15)) * LDH + kofs<E>(lane);
-#pragma unroll
-      for (int s = 0; s < NKH; ++s) {
-        const SF sb = sS.get(row + s * KS);
-        aq[ct] = Mma<E>::mma(aq[ct], fo[s], sb);
-        aw[ct] = Mma<E>::mma(aw[ct], fd[s], sb);
-        ak[ct] = Mma<E>::mma(ak[ct], fv[s], sD.get(row + s * KS));
+      for (int c = 0; c < CTW; ++c) {
+        const int row = (c * 16 + (lane & 15)) * LDH + s * KS + kofs<E>(lane);
+        const SF sb = sS.get(row);
+        aq[c] = Mma<E>::mma(aq[c], fo, sb);
+        aw[c] = Mma<E>::mma(aw[c], fd, sb);
+        ak[c] = Mma<E>::mma(ak[c], fv, sD.get(row));
       }
-    }
-    // dAqk = dO Vn^T, lower including the diagonal (Vn rows from global)
+      // dAqk = dO Vn^T, lower including the diagonal (Vn rows from global)
 #pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      if (J <= wv) {
-        const float* vrow = vnc + (size_t)(J * 16 + (lane & 15)) * V + vb + kofs<E>(lane);
-#pragma unroll
-        for (int s = 0; s < NKH; ++s) adq[J] = Mma<E>::mma(adq[J], fo[s], Mma<E>::ld(vrow + s * KS));
+      for (int jj = 0; jj < 2; ++jj) {
+        const int J = kh + 2 * jj;
+        if (J <= wv)
+          adq[jj] = Mma<E>::mma(adq[jj], fo, Mma<E>::ld(vnc + (unsigned)((J * 16 + (lane & 15)) * V + v0)));
       }
     }
   }
@@ -119,24 +129,24 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
   float* dWT = a.dWT + cix * K * C;
   float* dKt = a.dKt + cix * C * K;
 #pragma unroll
-  for (int ct = 0; ct < CTK; ++ct) {
-    const int i0 = wv * 16 + acc_row(0), k = ct * 16 + acc_col();
+  for (int c = 0; c < CTW; ++c) {
+    const int i0 = wv * 16 + acc_row(0), k = kh * KH + c * 16 + acc_col();
     f4 w;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      dQg[(i0 + r) * K + k] = aq[ct][r];
-      dKt[(i0 + r) * K + k] = ak[ct][r];
-      w[r] = -aw[ct][r];
+      dQg[(i0 + r) * K + k] = aq[c][r];
+      dKt[(i0 + r) * K + k] = ak[c][r];
+      w[r] = -aw[c][r];
     }
     *reinterpret_cast<f4*>(dWT + k * C + i0) = w;
   }
   float* dAq = a.dAqk + cix * C * C;
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
+  for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
-      dAq[i * C + j] = j <= i ? adq[J][r] : 0.f;
+      const int i = wv * 16 + acc_row(r), j = (kh + 2 * jj) * 16 + acc_col();
+      dAq[i * C + j] = j <= i ? adq[jj][r] : 0.f;
     }
   }
   // dgam_k = sum_v dS'[k][v] S[k][v]: the Q4 threads of row k are adjacent lanes
@@ -146,7 +156,7 @@ __global__ __launch_bounds__(256) void l0_bwd_state_kernel(L0BwdStateArgs a) {
 #pragma unroll
     for (int o = 1; o < Q4; o <<= 1) x += __shfl_xor(x, o, WAVE);
     const int e = tid + 256 * i;
-    if (e % Q4 == 0) a.dgam[cix * K + e / Q4] = x;
+    if (e % Q4 == 0) a.dgam[cix * K + kh * KH + e / Q4] = x;
   }
 }
 
@@ -493,7 +503,8 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 
 template <typename E, int K, int V>
 static hipError_t launch_l0_bwd_state(const L0BwdStateArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * a.NT);
+  // two workgroups (halves of K) per chunk-head
+  const unsigned grid = (unsigned)(2 * a.B * a.H * a.NT);
   hipLaunchKernelGGL((l0_bwd_state_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
