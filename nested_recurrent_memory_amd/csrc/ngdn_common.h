@@ -25,7 +25,9 @@ constexpr int WAVE = 64;
 constexpr int CH = 64;  // tokens per chunk
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+// uniform across the wave: the compiler keeps it (and what derives from it) in
+// scalar registers
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
 
 template <typename T> __device__ __forceinline__ float to_f(T x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
@@ -236,6 +238,15 @@ __device__ __forceinline__ void ld_raw(const float* p, float* out) {
   }
 }
 
+// A workgroup barrier that orders LDS only: global stores issued before it
+// need not have completed (__syncthreads waits for every outstanding store).
+// Global data exchanged between the waves of a workgroup needs __syncthreads.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Splits a grid of G = NB * NS blocks into (b, s), b in [0, NB), s in [0, NS),
 // so that the NS slices of one b run on the same XCD (blocks are dealt to the
 // 8 XCDs round robin, block x on XCD x % 8). Falls back to b = x / NS when
@@ -250,6 +261,25 @@ __device__ __forceinline__ void xcd_split(int x, int G, int NS, int& b, int& s) 
   const int xcd = x % 8, r = x / 8;
   b = (r / NS) * 8 + xcd;
   s = r % NS;
+}
+
+// Splits a grid of B * H * NF blocks, one per (batch, head, firing), so that
+// every block of head h runs on XCD h % 8 when H is a multiple of 8: a head's
+// parameters (read by every firing) then stay in one XCD's L2 instead of
+// being fetched into all eight. Otherwise the blocks are in launch order.
+__device__ __forceinline__ void head_xcd_split(int x, int H, int NF, int& b, int& h, int& i) {
+  if (H % 8 != 0) {
+    i = x % NF;
+    const int bh = x / NF;
+    h = bh % H;
+    b = bh / H;
+    return;
+  }
+  const int xcd = x % 8, r = x / 8, H8 = H / 8;
+  i = r % NF;
+  const int t = r / NF;
+  h = (t % H8) * 8 + xcd;
+  b = t / H8;
 }
 
 // Copies nrows x ncols elements of a row-major global array (row stride

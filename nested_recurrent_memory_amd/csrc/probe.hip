@@ -34,9 +34,9 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   float* s_V = s_buf;      // [N][LD]: Vals, v contiguous
 
   const int NF = a.NF, H = a.H;
-  const int i = blockIdx.x % NF;
-  const int bh = blockIdx.x / NF;
-  const int h = bh % H, b = bh / H;
+  int b, h, i;
+  head_xcd_split(blockIdx.x, H, NF, b, h, i);
+  const int bh = b * H + h;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   if (gated_out(a.gate, b)) return;
 

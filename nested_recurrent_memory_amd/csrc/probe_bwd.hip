@@ -20,6 +20,14 @@
 
 namespace ngdn {
 
+// One workgroup (8 waves) per firing-head. The [N,K] (= [N,V]) tile grid is
+// dealt to the waves so that every wave keeps one column tile (ctw) and takes
+// the row tiles rt: the B operands of every product (the state rows, the
+// parameter rows) are then loaded once per wave and shared by its row tiles,
+// all of them issued together. A operands come from LDS: Vals, kb, vn and
+// dvn in fp32 rows, the four workspaces of the dVals product and dVals itself
+// as split tiles. Barriers that only order LDS do not wait for the
+// workspace stores (lds_barrier).
 template <typename E, int K, int N, bool MERGE>
 __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   const ProbeArgs& a = ab.f;
@@ -32,27 +40,47 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   constexpr int TPW = (NTL + NW - 1) / NW;          // tiles per wave
   constexpr int NTKV = CTK * CTK;                   // [K,V] tiles
   constexpr int TPW2 = (NTKV + NW - 1) / NW;
-  // hold a phase's results until its loads are done (registers permitting)
-  constexpr bool BATCH = TPW <= 4;
   constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
   constexpr int NKS = K / KS;
+  static_assert(NW % CTK == 0, "every wave keeps one column tile");
   typedef typename Mma<E>::SFrag SF;
-  // LDS: region A holds Vals [N][LD], later dVals^T [V][LDN]; region B holds
-  // kb [N][LD], later vn [N][LD].
-  constexpr size_t SZ_A = sizeof(float) * (N * LD > V * LDN ? N * LD : V * LDN);
-  constexpr size_t SZ_B = sizeof(float) * N * LD;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_A + SZ_B];
+  typedef typename Mma<E>::Frag FR;
+  using ST = SplitTile<E>;
+  typedef typename ST::T TT;
+  constexpr int LDT = K + ST::PAD;                  // split tile rows
+  // LDS: phases 1-5 use fp32 rows Vals, kb (later vn) and, when it fits, dvn;
+  // phases 6-7 the four workspaces as split tiles (when they fit); phase 8
+  // dVals as a split tile and dVals^T in fp32.
+  constexpr size_t BUDGET = 150 * 1024;
+  constexpr size_t SZ_F = sizeof(float) * N * LD;
+  constexpr size_t SZ_T = sizeof(TT) * ST::NPLANE * N * LDT;
+  constexpr size_t SZ_DVT = sizeof(float) * V * LDN;
+  constexpr bool DVN_LDS = 3 * SZ_F <= BUDGET;
+  constexpr bool WS_LDS = 4 * SZ_T <= BUDGET;
+  constexpr size_t SZ_A = (DVN_LDS ? 3 : 2) * SZ_F;
+  constexpr size_t SZ_B = WS_LDS ? 4 * SZ_T : 0;
+  constexpr size_t SZ_C = (MERGE ? 0 : SZ_T) + SZ_DVT;
+  constexpr size_t SZ_AB = SZ_A > SZ_B ? SZ_A : SZ_B;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_AB > SZ_C ? SZ_AB : SZ_C];
   __shared__ float s_nrm[N], s_rd[N], s_gs[K], s_dg[K], s_gam[K];
   float* s_V = reinterpret_cast<float*>(smem);
-  float* s_dVT = s_V;
-  float* s_kb = reinterpret_cast<float*>(smem + SZ_A);
+  float* s_kb = reinterpret_cast<float*>(smem + SZ_F);
   float* s_vn = s_kb;
+  float* s_dvn = reinterpret_cast<float*>(smem + 2 * SZ_F);
+  auto ws_tile = [&](int j) {
+    return ST{reinterpret_cast<TT*>(smem + j * SZ_T), N * LDT};
+  };
+  const ST sDV{reinterpret_cast<TT*>(smem), N * LDT};
+  float* s_dVT = reinterpret_cast<float*>(smem + (MERGE ? 0 : SZ_T));
 
   const int NF = a.NF, H = a.H;
-  const int i = blockIdx.x % NF;
-  const int bh = blockIdx.x / NF;
-  const int h = bh % H, b = bh / H;
+  int b, h, i;
+  head_xcd_split(blockIdx.x, H, NF, b, h, i);
+  const int bh = b * H + h;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const int rl = lane & 15, ko = kofs<E>(lane);
+  const int ctw = wv % CTK;                         // this wave's column tile
   const size_t fo = (size_t)bh * NF + i;
 
   // ---- the gathered lower state: rows (kv) and, when stored, transposed (vk)
@@ -78,42 +106,41 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   for (int e = tid; e < N; e += blockDim.x) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
   for (int e = tid; e < K; e += blockDim.x) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
 
-  // tile t of this wave: g = wv + NW t over [N/16][K/16]
-  auto tile = [&](int t, int& rt, int& ct) -> bool {
+  // row tile of this wave's t-th tile (its column tile is ctw)
+  auto tile = [&](int t, int& rt) -> bool {
     const int g = wv + NW * t;
     rt = g / CTK;
-    ct = g % CTK;
     return g < NTL;
   };
 
   // ---- 1. Vals = Bank[:N] S (learned) or S (merge)
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
-    // every tile computed before any store: outstanding loads and stores
-    // together would make each later load wait for all of them
+    const int v = ctw * 16 + rl;
+    SF fS[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int k0 = s * KS + ko;
+      fS[s] = Svk ? Mma<E>::ld(Svk + (size_t)v * K + k0)
+                  : Mma<E>::makes([&](int e) { return Skv[(size_t)(k0 + e) * V + v]; });
+    }
     f4 vt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       vt[t] = f4_zero();
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
-      const E* arow = bank + (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
-      const int v = ct * 16 + (lane & 15);
+      int rt;
+      if (!tile(t, rt)) continue;
+      const E* arow = bank + (size_t)(rt * 16 + rl) * K + ko;
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) {
-        const int k0 = s * KS + kofs<E>(lane);
-        const SF fb = Svk ? Mma<E>::ld(Svk + (size_t)v * K + k0)
-                          : Mma<E>::makes([&](int e) { return Skv[(size_t)(k0 + e) * V + v]; });
-        vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fb);
-      }
+      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fS[s]);
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
+      int rt;
+      if (!tile(t, rt)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int n = rt * 16 + acc_row(r), vv = ct * 16 + acc_col();
+        const int n = rt * 16 + acc_row(r), vv = ctw * 16 + acc_col();
         s_V[n * LD + vv] = vt[t][r];
         wsV[n * V + vv] = vt[t][r];
       }
@@ -126,52 +153,69 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       *reinterpret_cast<f4*>(wsV + (size_t)k * V + v) = x;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 2. the four projections of Vals, once: u = Vals Wk^T (learned),
   // xb = Vals Bp, xw = Vals Wp, xg = Vals Gp; key norms and decay sums
-  const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V;
-  const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V;
-  const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V;
-  const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V;
   f4 u[TPW], xb[TPW], xw[TPW], xg[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    u[t] = xb[t] = xw[t] = xg[t] = f4_zero();
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
-    const float* arow = s_V + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
-    const size_t pr = (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
+  {
+    const size_t pr = (size_t)(ctw * 16 + rl) * V + ko;
+    const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V + pr;
+    const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V + pr;
+    const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V + pr;
+    const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V + pr;
+    FR pk[NKS], pb[NKS], pw[NKS], pg[NKS];
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      const SF fa = Mma<E>::ld(arow + s * KS);
-      if (!MERGE) u[t] = Mma<E>::mma(u[t], fa, Mma<E>::ld(kpH + pr + s * KS));
-      xb[t] = Mma<E>::mma(xb[t], fa, Mma<E>::ld(bpH + pr + s * KS));
-      xw[t] = Mma<E>::mma(xw[t], fa, Mma<E>::ld(wpH + pr + s * KS));
-      xg[t] = Mma<E>::mma(xg[t], fa, Mma<E>::ld(gpH + pr + s * KS));
+      if (!MERGE) pk[s] = Mma<E>::ld(kpH + s * KS);
+      pb[s] = Mma<E>::ld(bpH + s * KS);
+      pw[s] = Mma<E>::ld(wpH + s * KS);
+      pg[s] = Mma<E>::ld(gpH + s * KS);
     }
-    float sg = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sg += softplusf_(xg[t][r] - 4.f);
-    sg += __shfl_xor(sg, 16, WAVE);
-    sg += __shfl_xor(sg, 32, WAVE);
-    if (lane < 16) atomicAdd(&s_gs[ct * 16 + lane], sg);
-    if (!MERGE) {
+    for (int t = 0; t < TPW; ++t) {
+      u[t] = xb[t] = xw[t] = xg[t] = f4_zero();
+      int rt;
+      if (!tile(t, rt)) continue;
+      const float* arow = s_V + (rt * 16 + rl) * LD + ko;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float q = u[t][r] * u[t][r];
-        q += __shfl_xor(q, 1, WAVE);
-        q += __shfl_xor(q, 2, WAVE);
-        q += __shfl_xor(q, 4, WAVE);
-        q += __shfl_xor(q, 8, WAVE);
-        if ((lane & 15) == 0) atomicAdd(&s_nrm[rt * 16 + acc_row(r)], q);
+      for (int s = 0; s < NKS; ++s) {
+        const SF fa = Mma<E>::ld(arow + s * KS);
+        if (!MERGE) u[t] = Mma<E>::mma(u[t], fa, pk[s]);
+        xb[t] = Mma<E>::mma(xb[t], fa, pb[s]);
+        xw[t] = Mma<E>::mma(xw[t], fa, pw[s]);
+        xg[t] = Mma<E>::mma(xg[t], fa, pg[s]);
+      }
+      float sg = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sg += softplusf_(xg[t][r] - 4.f);
+      sg += __shfl_xor(sg, 16, WAVE);
+      sg += __shfl_xor(sg, 32, WAVE);
+      if (lane < 16) atomicAdd(&s_gs[ctw * 16 + lane], sg);
+      if (!MERGE) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float q = u[t][r] * u[t][r];
+          q += __shfl_xor(q, 1, WAVE);
+          q += __shfl_xor(q, 2, WAVE);
+          q += __shfl_xor(q, 4, WAVE);
+          q += __shfl_xor(q, 8, WAVE);
+          if (rl == 0) atomicAdd(&s_nrm[rt * 16 + acc_row(r)], q);
+        }
       }
     }
   }
-  __syncthreads();
+  // dvn staged for phases 4-5 (loads issued before the barrier)
+  if constexpr (DVN_LDS) {
+    for (int e = tid; e < N * V / 4; e += blockDim.x) {
+      const int n = e / (V / 4), c = (e % (V / 4)) * 4;
+      *reinterpret_cast<f4*>(s_dvn + n * LD + c) = *reinterpret_cast<const f4*>(dvn + (size_t)n * V + c);
+    }
+  }
+  lds_barrier();
 
-  auto keyval = [&](int t, int rt, int ct, int r) -> float {
-    const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
+  auto keyval = [&](int t, int rt, int r) -> float {
+    const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
     if (MERGE) return n == k ? 1.f : 0.f;
     return u[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
   };
@@ -179,188 +223,234 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // ---- 3. kb = keys * b into LDS; gam = e^g
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
+    int rt;
+    if (!tile(t, rt)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      s_kb[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] =
-          keyval(t, rt, ct, r) * sigmoidf_(xb[t][r] - 4.f);
+      s_kb[(rt * 16 + acc_row(r)) * LD + ctw * 16 + acc_col()] =
+          keyval(t, rt, r) * sigmoidf_(xb[t][r] - 4.f);
   }
   for (int e = tid; e < K; e += blockDim.x) s_gam[e] = expf(-s_gs[e] / (float)N);
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. vn = Vals w - kb s with s = e^g S_j (s^T rows scaled per k);
   // dw-side terms
   f4 vnt[TPW], dvd[TPW], dxwt[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    vnt[t] = dvd[t] = f4_zero();
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
-    const float* arow = s_kb + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
-    const float* brow = SjT + (size_t)(ct * 16 + (lane & 15)) * K + kofs<E>(lane);
-    f4 ks = f4_zero();
+  {
+    SF fT[NKS];
+    const float* brow = SjT + (size_t)(ctw * 16 + rl) * K + ko;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      const int k0 = s * KS + kofs<E>(lane);
-      float x[Mma<E>::KPL];
-      ld_raw<Mma<E>::KPL>(brow + s * KS, x);
-      ks = Mma<E>::mma(ks, Mma<E>::ld(arow + s * KS),
-                       Mma<E>::makes([&](int e) { return x[e] * s_gam[k0 + e]; }));
+      const int k0 = s * KS + ko;
+      float x[KPL];
+      ld_raw<KPL>(brow + s * KS, x);
+      fT[s] = Mma<E>::makes([&](int e) { return x[e] * s_gam[k0 + e]; });
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-      const float w = sigmoidf_(xw[t][r]);
-      const float val = s_V[n * LD + v];
-      const float dv = dvn[(size_t)n * V + v];
-      vnt[t][r] = val * w - ks[r];
-      dvd[t][r] = dv * w;
-      if constexpr (BATCH) dxwt[t][r] = dv * val * w * (1.f - w);
-      else wsdxw[(size_t)n * V + v] = dv * val * w * (1.f - w);
-    }
-  }
-  if constexpr (BATCH) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
+      vnt[t] = dvd[t] = dxwt[t] = f4_zero();
+      int rt;
+      if (!tile(t, rt)) continue;
+      const float* arow = s_kb + (rt * 16 + rl) * LD + ko;
+      f4 ks = f4_zero();
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        wsdxw[(size_t)(rt * 16 + acc_row(r)) * V + ct * 16 + acc_col()] = dxwt[t][r];
+      for (int s = 0; s < NKS; ++s) ks = Mma<E>::mma(ks, Mma<E>::ld(arow + s * KS), fT[s]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = rt * 16 + acc_row(r), v = ctw * 16 + acc_col();
+        const float w = sigmoidf_(xw[t][r]);
+        const float val = s_V[n * LD + v];
+        const float dv = DVN_LDS ? s_dvn[n * LD + v] : dvn[(size_t)n * V + v];
+        vnt[t][r] = val * w - ks[r];
+        dvd[t][r] = dv * w;
+        dxwt[t][r] = dv * val * w * (1.f - w);
+      }
     }
   }
-  __syncthreads();   // vn replaces kb
+  lds_barrier();   // vn replaces kb
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
+    int rt;
+    if (!tile(t, rt)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      s_vn[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vnt[t][r];
+      s_vn[(rt * 16 + acc_row(r)) * LD + ctw * 16 + acc_col()] = vnt[t][r];
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 5. P = dvn s^T, Q = vn dS'^T; dkeys, db, the decay gradient
   f4 dkt[TPW], dxbt[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    dkt[t] = dxbt[t] = f4_zero();
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
-    const int kc = ct * 16 + (lane & 15);
+  {
+    const int kc = ctw * 16 + rl;
     const float gk = s_gam[kc];
-    const float* drow = dvn + (size_t)(rt * 16 + (lane & 15)) * V + kofs<E>(lane);
-    const float* srow = Sj + (size_t)kc * V + kofs<E>(lane);
-    const float* vrow = s_vn + (rt * 16 + (lane & 15)) * LD + kofs<E>(lane);
-    const float* qrow = dSp + (size_t)kc * V + kofs<E>(lane);
-    f4 P = f4_zero(), Q = f4_zero();
+    SF fP[NKS], fQ[NKS];
+    float dgp = 0.f;   // sum over this lane's v of dS'[kc][v] S_j[kc][v]
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      float x[Mma<E>::KPL];
-      ld_raw<Mma<E>::KPL>(srow + s * KS, x);
-      P = Mma<E>::mma(P, Mma<E>::ld(drow + s * KS), Mma<E>::makes([&](int e) { return gk * x[e]; }));
-      Q = Mma<E>::mma(Q, Mma<E>::ld(vrow + s * KS), Mma<E>::ld(qrow + s * KS));
-    }
-    float cs = 0.f;
+      const int v0 = s * KS + ko;
+      float x[KPL], y[KPL];
+      ld_raw<KPL>(Sj + (size_t)kc * V + v0, x);
+      ld_raw<KPL>(dSp + (size_t)kc * V + v0, y);
+      fP[s] = Mma<E>::makes([&](int e) { return gk * x[e]; });
+      fQ[s] = Mma<E>::makes([&](int e) { return y[e]; });
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
-      const float key = keyval(t, rt, ct, r), bb = sigmoidf_(xb[t][r] - 4.f);
-      const float dkey = Q[r] - P[r] * bb;
-      const float dbg = -P[r] * key;
-      cs += key * bb * P[r];
-      dkt[t][r] = dkey;
-      if constexpr (BATCH) dxbt[t][r] = dbg * bb * (1.f - bb);
-      else wsdxb[(size_t)n * K + k] = dbg * bb * (1.f - bb);
-      if (!MERGE) {
-        float rd = key * dkey;
-        rd += __shfl_xor(rd, 1, WAVE);
-        rd += __shfl_xor(rd, 2, WAVE);
-        rd += __shfl_xor(rd, 4, WAVE);
-        rd += __shfl_xor(rd, 8, WAVE);
-        if ((lane & 15) == 0) atomicAdd(&s_rd[n], rd);
-      }
+      for (int e = 0; e < KPL; ++e) dgp += x[e] * y[e];
     }
-    cs += __shfl_xor(cs, 16, WAVE);
-    cs += __shfl_xor(cs, 32, WAVE);
-    if (lane < 16) atomicAdd(&s_dg[ct * 16 + lane], -cs);
-  }
-  // + sum_v dS'[k][v] s[k][v]
-  for (int k = wv; k < K; k += NW) {
-    float sum = 0.f;
-    for (int v = lane; v < V; v += WAVE) sum += dSp[(size_t)k * V + v] * Sj[(size_t)k * V + v];
-    sum = wave_sum(sum);
-    if (lane == 0) atomicAdd(&s_dg[k], s_gam[k] * sum);
-  }
-  // the phase's stores after all of its loads
-  if constexpr (BATCH) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
+      dkt[t] = dxbt[t] = f4_zero();
+      int rt;
+      if (!tile(t, rt)) continue;
+      const int ar = (rt * 16 + rl) * LD + ko;
+      f4 P = f4_zero(), Q = f4_zero();
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        wsdxb[(size_t)(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()] = dxbt[t][r];
+      for (int s = 0; s < NKS; ++s) {
+        const SF fa = DVN_LDS ? Mma<E>::ld(s_dvn + ar + s * KS)
+                              : Mma<E>::ld(dvn + (size_t)(rt * 16 + rl) * V + ko + s * KS);
+        P = Mma<E>::mma(P, fa, fP[s]);
+        Q = Mma<E>::mma(Q, Mma<E>::ld(s_vn + ar + s * KS), fQ[s]);
+      }
+      float cs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = rt * 16 + acc_row(r);
+        const float key = keyval(t, rt, r), bb = sigmoidf_(xb[t][r] - 4.f);
+        const float dkey = Q[r] - P[r] * bb;
+        const float dbg = -P[r] * key;
+        cs += key * bb * P[r];
+        dkt[t][r] = dkey;
+        dxbt[t][r] = dbg * bb * (1.f - bb);
+        if (!MERGE) {
+          float rd = key * dkey;
+          rd += __shfl_xor(rd, 1, WAVE);
+          rd += __shfl_xor(rd, 2, WAVE);
+          rd += __shfl_xor(rd, 4, WAVE);
+          rd += __shfl_xor(rd, 8, WAVE);
+          if (rl == 0) atomicAdd(&s_rd[n], rd);
+        }
+      }
+      cs += __shfl_xor(cs, 16, WAVE);
+      cs += __shfl_xor(cs, 32, WAVE);
+      if (lane < 16) atomicAdd(&s_dg[ctw * 16 + lane], -cs);
     }
+    // + sum_v dS'[k][v] s[k][v] (one wave per column tile adds it)
+    dgp += __shfl_xor(dgp, 16, WAVE);
+    dgp += __shfl_xor(dgp, 32, WAVE);
+    if (wv < CTK && lane < 16) atomicAdd(&s_dg[kc], gk * dgp);
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- 6. du and dxg
+  // ---- 6. du and dxg; the dVals product's parameter rows are loaded ahead
+  // of the workspace stores
+  f4 dut[TPW], dxgt[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    int rt, ct;
-    if (!tile(t, rt, ct)) continue;
+    dut[t] = dxgt[t] = f4_zero();
+    int rt;
+    if (!tile(t, rt)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int n = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
+      const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
       if (!MERGE) {
         const float nr = sqrtf(s_nrm[n]);
         const float key = u[t][r] / fmaxf(nr, 1e-12f);
         // F.normalize: below the clamp the denominator is the constant eps
-        const float du = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) / nr : dkt[t][r] / 1e-12f;
-        wsdu[(size_t)n * K + k] = du;
+        dut[t][r] = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) / nr : dkt[t][r] / 1e-12f;
       }
-      wsdxg[(size_t)n * K + k] = -(s_dg[k] / (float)N) * sigmoidf_(xg[t][r] - 4.f);
+      dxgt[t][r] = -(s_dg[k] / (float)N) * sigmoidf_(xg[t][r] - 4.f);
     }
   }
-  __syncthreads();
+  FR qk[NKS], qb[NKS], qw[NKS], qg[NKS];
+  {
+    const size_t br = (size_t)(ctw * 16 + rl) * K + ko;
+    const E* kpT = static_cast<const E*>(ab.kpT) + (size_t)h * V * K + br;
+    const E* bp = static_cast<const E*>(ab.bp) + (size_t)h * V * K + br;
+    const E* wp = static_cast<const E*>(ab.wp) + (size_t)h * V * V + br;
+    const E* gp = static_cast<const E*>(ab.gp) + (size_t)h * V * K + br;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      if (!MERGE) qk[s] = Mma<E>::ld(kpT + s * KS);
+      qb[s] = Mma<E>::ld(bp + s * KS);
+      qw[s] = Mma<E>::ld(wp + s * KS);
+      qg[s] = Mma<E>::ld(gp + s * KS);
+    }
+  }
+  // workspaces of the parameter gradients, and (when they fit) the same
+  // values as split LDS tiles for the dVals product
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    int rt;
+    if (!tile(t, rt)) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
+      if (!MERGE) wsdu[(size_t)n * K + k] = dut[t][r];
+      wsdxb[(size_t)n * K + k] = dxbt[t][r];
+      wsdxw[(size_t)n * V + k] = dxwt[t][r];
+      wsdxg[(size_t)n * K + k] = dxgt[t][r];
+      if constexpr (WS_LDS) {
+        if (!MERGE) ws_tile(0).put1(n * LDT + k, dut[t][r]);
+        ws_tile(1).put1(n * LDT + k, dxbt[t][r]);
+        ws_tile(2).put1(n * LDT + k, dxwt[t][r]);
+        ws_tile(3).put1(n * LDT + k, dxgt[t][r]);
+      }
+    }
+  }
+  if constexpr (WS_LDS) lds_barrier();
+  else __syncthreads();   // the workspaces are read back from global memory
 
   // ---- 7. dVals = dvn * w + du Wk + dxb Bp^T + dxw Wp^T + dxg Gp^T
-  {
-    const E* kpT = static_cast<const E*>(ab.kpT) + (size_t)h * V * K;
-    const E* bp = static_cast<const E*>(ab.bp) + (size_t)h * V * K;
-    const E* wp = static_cast<const E*>(ab.wp) + (size_t)h * V * V;
-    const E* gp = static_cast<const E*>(ab.gp) + (size_t)h * V * K;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
-      const size_t ar = (size_t)(rt * 16 + (lane & 15)) * K + kofs<E>(lane);
-      const size_t br = (size_t)(ct * 16 + (lane & 15)) * K + kofs<E>(lane);
-      f4 acc = dvd[t];
+  for (int t = 0; t < TPW; ++t) {
+    int rt;
+    if (!tile(t, rt)) continue;
+    f4 acc = dvd[t];
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) {
-        if (!MERGE) acc = Mma<E>::mma(acc, Mma<E>::ld(wsdu + ar + s * KS), Mma<E>::ld(kpT + br + s * KS));
-        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxb + ar + s * KS), Mma<E>::ld(bp + br + s * KS));
-        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxw + ar + s * KS), Mma<E>::ld(wp + br + s * KS));
-        acc = Mma<E>::mma(acc, Mma<E>::ld(wsdxg + ar + s * KS), Mma<E>::ld(gp + br + s * KS));
-      }
-      dvd[t] = acc;
+    for (int s = 0; s < NKS; ++s) {
+      const int off = (rt * 16 + rl) * LDT + s * KS + ko;
+      const size_t go = (size_t)(rt * 16 + rl) * K + s * KS + ko;
+      if (!MERGE) acc = Mma<E>::mma(acc, WS_LDS ? ws_tile(0).get(off) : Mma<E>::ld(wsdu + go), qk[s]);
+      acc = Mma<E>::mma(acc, WS_LDS ? ws_tile(1).get(off) : Mma<E>::ld(wsdxb + go), qb[s]);
+      acc = Mma<E>::mma(acc, WS_LDS ? ws_tile(2).get(off) : Mma<E>::ld(wsdxw + go), qw[s]);
+      acc = Mma<E>::mma(acc, WS_LDS ? ws_tile(3).get(off) : Mma<E>::ld(wsdxg + go), qg[s]);
     }
+    dvd[t] = acc;
+  }
+  // Phase 8's operands from global memory, ahead of this phase's stores:
+  // the lower state's rows (dBank) and the bank's columns (dS_below)
+  const E* bankT = static_cast<const E*>(ab.bankT) + (size_t)h * K * a.Nmax;
+  constexpr int NSN = (N + KS - 1) / KS;
+  SF fSk[NKS];
+  FR fBt[TPW2][NSN];
+  if (!MERGE) {
+    const float* srow = Skv + (size_t)(ctw * 16 + rl) * V + ko;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
+    for (int s = 0; s < NKS; ++s) fSk[s] = Mma<E>::ld(srow + s * KS);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        wsdV[(size_t)n * V + v] = dvd[t][r];
-        if (!MERGE) s_dVT[v * LDN + n] = dvd[t][r];
+    for (int t = 0; t < TPW2; ++t) {
+      const int g = wv + NW * t;
+      const E* arow = bankT + (size_t)((g / CTK) * 16 + rl) * a.Nmax + ko;
+#pragma unroll
+      for (int s = 0; s < NSN; ++s)
+        fBt[t][s] = (g < NTKV && s * KS + ko < N) ? Mma<E>::ld(arow + s * KS) : Mma<E>::zero();
+    }
+  }
+  lds_barrier();   // dVals replaces the workspace tiles
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    int rt;
+    if (!tile(t, rt)) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = rt * 16 + acc_row(r), v = ctw * 16 + acc_col();
+      wsdV[(size_t)n * V + v] = dvd[t][r];
+      if (!MERGE) {
+        sDV.put1(n * LDT + v, dvd[t][r]);
+        s_dVT[v * LDN + n] = dvd[t][r];
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 8. dS_below and dBank
   // Adds (or, for level 1, writes) the [K,V] tiles g = wv + NW t: every
@@ -403,52 +493,40 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     static_assert(!MERGE || TPW == TPW2, "merge: one tile grid");
     scatter_all(dvd);
   } else {
-    // dS_below[k][v] = sum_n Bank[n][k] dVals[n][v]
-    const E* bankT = static_cast<const E*>(ab.bankT) + (size_t)h * K * a.Nmax;
-    constexpr int NSN = (N + KS - 1) / KS;
+    // dS_below[k][v] = sum_n Bank[n][k] dVals[n][v]: B = dVals^T rows v of
+    // this wave's column tile (the [K,V] tiles of a wave share it too)
+    SF fd[NSN];
+#pragma unroll
+    for (int s = 0; s < NSN; ++s)
+      fd[s] = s * KS + ko < N ? Mma<E>::ld(s_dVT + (ctw * 16 + rl) * LDN + s * KS + ko) : Mma<E>::szero();
     f4 dsb[TPW2];
 #pragma unroll
     for (int t = 0; t < TPW2; ++t) {
       dsb[t] = f4_zero();
-      const int g = wv + NW * t;
-      if (g >= NTKV) continue;
-      const int rt = g / CTK, ct = g % CTK;
-      const E* arow = bankT + (size_t)(rt * 16 + (lane & 15)) * a.Nmax + kofs<E>(lane);
-      const float* brow = s_dVT + (ct * 16 + (lane & 15)) * LDN + kofs<E>(lane);
+      if (wv + NW * t >= NTKV) continue;
 #pragma unroll
-      for (int s = 0; s < NSN; ++s) {
-        const bool live = s * KS + kofs<E>(lane) < N;
-        typename Mma<E>::Frag fa = Mma<E>::zero();
-        SF fb = Mma<E>::szero();
-        if (live) {
-          fa = Mma<E>::ld(arow + s * KS);
-          fb = Mma<E>::ld(brow + s * KS);
-        }
-        dsb[t] = Mma<E>::mma(dsb[t], fa, fb);
-      }
+      for (int s = 0; s < NSN; ++s) dsb[t] = Mma<E>::mma(dsb[t], fBt[t][s], fd[s]);
     }
-    scatter_all(dsb);
     // dBank[n][k] += sum_v dVals[n][v] S_below[k][v]
-    float* dbank = ab.dbank + (size_t)h * a.Nmax * K;
     f4 dbt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       dbt[t] = f4_zero();
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
-      const float* arow = wsdV + (size_t)(rt * 16 + (lane & 15)) * V + kofs<E>(lane);
-      const float* brow = Skv + (size_t)(ct * 16 + (lane & 15)) * V + kofs<E>(lane);
+      int rt;
+      if (!tile(t, rt)) continue;
 #pragma unroll
       for (int s = 0; s < NKS; ++s)
-        dbt[t] = Mma<E>::mma(dbt[t], Mma<E>::ld(arow + s * KS), Mma<E>::ld(brow + s * KS));
+        dbt[t] = Mma<E>::mma(dbt[t], sDV.get((rt * 16 + rl) * LDT + s * KS + ko), fSk[s]);
     }
+    scatter_all(dsb);
+    float* dbank = ab.dbank + (size_t)h * a.Nmax * K;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      int rt, ct;
-      if (!tile(t, rt, ct)) continue;
+      int rt;
+      if (!tile(t, rt)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ct * 16 + acc_col()], dbt[t][r]);
+        atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ctw * 16 + acc_col()], dbt[t][r]);
     }
   }
 }
