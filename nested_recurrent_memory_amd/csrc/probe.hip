@@ -12,32 +12,43 @@
 // The gathered state is the lower level's state after this level's firing
 // (ops/chunk.py:39-93). Outputs are written in the form the scan consumes:
 // A = keys*b*e^g, KT = keys^T, U = Vals*w, gam = e^g.
-// One workgroup per (batch, head, firing); the five N x K x V products run on
-// MFMA (exact bf16 parameters against the fp32 state / Vals split in two) with
-// the gates in fp32.
+// One workgroup (8 waves) per (batch, head, firing); the five N x K x V
+// products run on MFMA (exact bf16 parameters against the fp32 state / Vals
+// split in two) with the gates in fp32. Every wave keeps one column tile and
+// takes the row tiles, so the B operands of its products (state rows,
+// parameter rows) are loaded once and shared by its tiles; the A operands are
+// the bank rows and Vals in LDS.
 #include "ngdn_kernels.h"
 
 namespace ngdn {
 
 template <typename E, int K, int N, bool MERGE>
-__global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
+__global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
   constexpr int V = K;
+  constexpr int NW = 8;                                    // waves
   constexpr int LD = K + 4;                                // fp32 rows
-  constexpr int NTK = (N / 16) * (K / 16) / 4;             // [N,K] tiles per wave
-  // S^T (learned) and then Vals share one buffer
-  constexpr int ROWS = (MERGE ? N : (V > N ? V : N));
-  __shared__ __attribute__((aligned(16))) float s_buf[ROWS * LD];
+  constexpr int CTK = K / 16;
+  constexpr int NTL = (N / 16) * CTK;                      // [N,K] (= [N,V]) tiles
+  constexpr int TPW = (NTL + NW - 1) / NW;                 // tiles per wave
+  constexpr int NPW = NW / CTK;                            // waves per column tile
+  constexpr int KS = Mma<E>::KS;
+  constexpr int KPL = Mma<E>::KPL;
+  constexpr int NKS = K / KS;
+  static_assert(NW % CTK == 0, "every wave keeps one column tile");
+  typedef typename Mma<E>::SFrag SF;
+  typedef typename Mma<E>::Frag FR;
+  __shared__ __attribute__((aligned(16))) float s_V[N * LD];   // Vals, v contiguous
   // per-wave partial sums (each slot has one writer), added in wave order so
   // that the result does not depend on the order in which waves finish
-  __shared__ float s_nrm[4][N], s_gs[4][K];
-  float* s_S = s_buf;      // [V][LD]: S^T, k contiguous
-  float* s_V = s_buf;      // [N][LD]: Vals, v contiguous
+  __shared__ float s_nrm[NW][N], s_gs[NPW][K];
 
   const int NF = a.NF, H = a.H;
   int b, h, i;
   head_xcd_split(blockIdx.x, H, NF, b, h, i);
   const int bh = b * H + h;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
+  const int rl = lane & 15, ko = kofs<E>(lane);
+  const int ctw = wv % CTK;
   if (gated_out(a.gate, b)) return;
 
   // ---- the gathered lower state
@@ -48,114 +59,137 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   if (fin) Sf = a.below_fin + b * a.bf_sb + h * a.bf_sh;
   else if (a.below_mode == 1) Sf = a.below + (((size_t)b * a.NGb + src) * H + h) * K * V;
   else Sh = a.below + (((size_t)b * H + h) * a.NGb + src) * V * K;
-
-  // learned: S^T rows (k contiguous); merge: Vals = S rows (v contiguous)
-  {
-    const float* same = MERGE ? Sf : Sh;     // already in the wanted orientation
-    const float* swap = MERGE ? Sh : Sf;
-    if (same) {
-      for (int e = tid; e < V * K / 4; e += 256) {
-        const int r = e / (K / 4), c = (e % (K / 4)) * 4;
-        *reinterpret_cast<f4*>(s_buf + r * LD + c) = *reinterpret_cast<const f4*>(same + r * K + c);
-      }
-    } else {
-      for (int e = tid; e < V * K; e += 256) s_buf[(e % K) * LD + e / K] = swap[e];
-    }
-  }
-  for (int e = tid; e < 4 * N; e += 256) (&s_nrm[0][0])[e] = 0.f;
-  for (int e = tid; e < 4 * K; e += 256) (&s_gs[0][0])[e] = 0.f;
-  __syncthreads();
+  for (int e = tid; e < NW * N; e += blockDim.x) (&s_nrm[0][0])[e] = 0.f;
+  for (int e = tid; e < NPW * K; e += blockDim.x) (&s_gs[0][0])[e] = 0.f;
 
   const size_t fo = ((size_t)bh * NF + i);                 // scan-ready firing index
   const size_t ro = (((size_t)b * NF + i) * H + h);        // reference-format index
+  auto tile = [&](int t, int& rt) -> bool {
+    const int g = wv + NW * t;
+    rt = g / CTK;
+    return g < NTL;
+  };
 
-  // ---- Vals = Bank[:N] S (tiles in registers, then over S^T)
+  // ---- Vals = Bank[:N] S (learned; B = rows v of S^T) or S (merge)
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
-    f4 vt[NTK];
+    const int v = ctw * 16 + rl;
+    SF fS[NKS];
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
-      vt[t] = mma_tile<E>(f4_zero(), bank + rt * 16 * K, K, s_S + ct * 16 * LD, LD, K);
+    for (int s = 0; s < NKS; ++s) {
+      const int k0 = s * KS + ko;
+      fS[s] = Sh ? Mma<E>::ld(Sh + (size_t)v * K + k0)
+                 : Mma<E>::makes([&](int e) { return Sf[(size_t)(k0 + e) * V + v]; });
     }
-    __syncthreads();
+    f4 vt[TPW];
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-      const int g = wv + 4 * t, rt = g / (V / 16), ct = g % (V / 16);
+    for (int t = 0; t < TPW; ++t) {
+      vt[t] = f4_zero();
+      int rt;
+      if (!tile(t, rt)) continue;
+      const E* arow = bank + (size_t)(rt * 16 + rl) * K + ko;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_V[(rt * 16 + acc_row(r)) * LD + ct * 16 + acc_col()] = vt[t][r];
+      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fS[s]);
     }
-    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      int rt;
+      if (!tile(t, rt)) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_V[(rt * 16 + acc_row(r)) * LD + ctw * 16 + acc_col()] = vt[t][r];
+    }
+  } else if (Sf) {
+    for (int e = tid; e < K * V / 4; e += blockDim.x) {
+      const int r = e / (V / 4), c = (e % (V / 4)) * 4;
+      *reinterpret_cast<f4*>(s_V + r * LD + c) = *reinterpret_cast<const f4*>(Sf + (size_t)r * V + c);
+    }
+  } else {
+    for (int e = tid; e < V * K; e += blockDim.x) s_V[(e % K) * LD + e / K] = Sh[e];
   }
+  lds_barrier();
   if (a.vals) {
-    for (int e = tid; e < N * V; e += 256)
-      a.vals[ro * N * V + e] = s_V[(e / V) * LD + e % V];
-  }
-
-  // ---- projections of Vals: A operand s_V (reduce over V), B from global
-  auto proj_tile = [&](const E* Pt, int rt, int ct) -> f4 {
-    // Pt: [cols][V] with V contiguous
-    return mma_tile<E>(f4_zero(), s_V + rt * 16 * LD, LD, Pt + (size_t)ct * 16 * V, V, V);
-  };
-  const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V;
-  const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V;
-  const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V;
-  const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V;
-
-  f4 ut[NTK], bt[NTK];
-#pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    // decay logits: column sums of softplus over the N pairs
-    {
-      f4 x = proj_tile(gpH, rt, ct);
-      float s = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s += softplusf_(x[r] - 4.f);
-      s += __shfl_xor(s, 16, WAVE);
-      s += __shfl_xor(s, 32, WAVE);
-      if (lane < 16) s_gs[wv][ct * 16 + lane] += s;
-    }
-    // erase gate
-    {
-      f4 x = proj_tile(bpH, rt, ct);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bt[t][r] = sigmoidf_(x[r] - 4.f);
-    }
-    // write keys (learned)
-    if (!MERGE) {
-      ut[t] = proj_tile(kpH, rt, ct);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s = ut[t][r] * ut[t][r];
-        s += __shfl_xor(s, 1, WAVE);
-        s += __shfl_xor(s, 2, WAVE);
-        s += __shfl_xor(s, 4, WAVE);
-        s += __shfl_xor(s, 8, WAVE);
-        if ((lane & 15) == 0) s_nrm[wv][rt * 16 + acc_row(r)] += s;
-      }
+    for (int e = tid; e < N * V / 4; e += blockDim.x) {
+      const int n = e / (V / 4), c = (e % (V / 4)) * 4;
+      *reinterpret_cast<f4*>(a.vals + ro * N * V + (size_t)n * V + c) = *reinterpret_cast<const f4*>(s_V + n * LD + c);
     }
   }
-  // write gate, and U = Vals * w
+
+  // ---- projections of Vals: A = Vals rows (LDS), B = parameter rows of this
+  // wave's column tile, loaded once
+  f4 ut[TPW], bt[TPW];
   {
+    const size_t pr = (size_t)(ctw * 16 + rl) * V + ko;
+    const E* kpH = static_cast<const E*>(a.kp) + (size_t)h * K * V + pr;
+    const E* bpH = static_cast<const E*>(a.bpT) + (size_t)h * K * V + pr;
+    const E* wpH = static_cast<const E*>(a.wpT) + (size_t)h * V * V + pr;
+    const E* gpH = static_cast<const E*>(a.gpT) + (size_t)h * K * V + pr;
+    FR pk[NKS], pb[NKS], pw[NKS], pg[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      if (!MERGE) pk[s] = Mma<E>::ld(kpH + s * KS);
+      pb[s] = Mma<E>::ld(bpH + s * KS);
+      pw[s] = Mma<E>::ld(wpH + s * KS);
+      pg[s] = Mma<E>::ld(gpH + s * KS);
+    }
     float* Uo = a.U + fo * N * V;
-    for (int g = wv; g < (N / 16) * (V / 16); g += 4) {
-      const int rt = g / (V / 16), ct = g % (V / 16);
-      f4 x = proj_tile(wpH, rt, ct);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      ut[t] = bt[t] = f4_zero();
+      int rt;
+      if (!tile(t, rt)) continue;
+      const float* arow = s_V + (rt * 16 + rl) * LD + ko;
+      f4 xg = f4_zero(), xb = f4_zero(), xw = f4_zero(), xu = f4_zero();
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        const SF fa = Mma<E>::ld(arow + s * KS);
+        if (!MERGE) xu = Mma<E>::mma(xu, fa, pk[s]);
+        xb = Mma<E>::mma(xb, fa, pb[s]);
+        xw = Mma<E>::mma(xw, fa, pw[s]);
+        xg = Mma<E>::mma(xg, fa, pg[s]);
+      }
+      // decay logits: column sums of softplus over the N pairs
+      float sg = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sg += softplusf_(xg[r] - 4.f);
+      sg += __shfl_xor(sg, 16, WAVE);
+      sg += __shfl_xor(sg, 32, WAVE);
+      if (lane < 16) s_gs[wv / CTK][ctw * 16 + lane] += sg;
+      // erase gate; key norms (learned)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bt[t][r] = sigmoidf_(xb[r] - 4.f);
+      if (!MERGE) {
+        ut[t] = xu;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float q = xu[r] * xu[r];
+          q += __shfl_xor(q, 1, WAVE);
+          q += __shfl_xor(q, 2, WAVE);
+          q += __shfl_xor(q, 4, WAVE);
+          q += __shfl_xor(q, 8, WAVE);
+          if (rl == 0) s_nrm[wv][rt * 16 + acc_row(r)] += q;
+        }
+      }
+      // write gate, and U = Vals * w
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int n = rt * 16 + acc_row(r), v = ct * 16 + acc_col();
-        const float w = sigmoidf_(x[r]);
+        const int n = rt * 16 + acc_row(r), v = ctw * 16 + acc_col();
+        const float w = sigmoidf_(xw[r]);
         Uo[n * V + v] = s_V[n * LD + v] * w;
         if (a.wo) a.wo[ro * N * V + n * V + v] = w;
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- finalize: g, keys, A = keys*b*e^g, KT = keys^T
+  auto gsum = [&](int k) {
+    float x = 0.f;
+#pragma unroll
+    for (int p = 0; p < NPW; ++p) x += s_gs[p][k];
+    return x;
+  };
   if (tid < K) {
-    const float g = -(s_gs[0][tid] + s_gs[1][tid] + s_gs[2][tid] + s_gs[3][tid]) / (float)N;
+    const float g = -gsum(tid) / (float)N;
     a.gam[fo * K + tid] = expf(g);
     if (a.go) a.go[ro * K + tid] = g;
   }
@@ -164,19 +198,26 @@ __global__ __launch_bounds__(256) void probe_fwd_kernel(ProbeArgs a) {
   const SplitTile<E> KTo = split_at<E>(a.KT + fo * K * N, K * N);
   const SplitTile<E> KNo = split_at<E>(a.keysN ? a.keysN + fo * N * K : nullptr, N * K);
   const SplitTile<E> ATo = split_at<E>(a.AT ? a.AT + fo * K * N : nullptr, K * N);
+  const int k = ctw * 16 + acc_col();
+  const float gam = expf(-gsum(k) / (float)N);
 #pragma unroll
-  for (int t = 0; t < NTK; ++t) {
-    const int g = wv + 4 * t, rt = g / (K / 16), ct = g % (K / 16);
-    const int k = ct * 16 + acc_col(), n0 = rt * 16 + acc_row(0);
-    const float gam = expf(-(s_gs[0][k] + s_gs[1][k] + s_gs[2][k] + s_gs[3][k]) / (float)N);
+  for (int t = 0; t < TPW; ++t) {
+    int rt;
+    if (!tile(t, rt)) continue;
+    const int n0 = rt * 16 + acc_row(0);
     f4 kv4, av4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = n0 + r;
       float key;
-      if (MERGE) key = (n == k) ? 1.f : 0.f;
-      else key = ut[t][r] / fmaxf(sqrtf(s_nrm[0][n] + s_nrm[1][n] + s_nrm[2][n] + s_nrm[3][n]),
-                                  1e-12f);
+      if (MERGE) {
+        key = (n == k) ? 1.f : 0.f;
+      } else {
+        float nr = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) nr += s_nrm[w][n];
+        key = ut[t][r] / fmaxf(sqrtf(nr), 1e-12f);
+      }
       kv4[r] = key;
       av4[r] = key * bt[t][r] * gam;
       Ao.put1(n * K + k, av4[r]);
@@ -193,7 +234,7 @@ template <typename E, int K, int N, bool MERGE>
 static hipError_t launch_probe(const ProbeArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.B * a.H * a.NF);
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((probe_fwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((probe_fwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
