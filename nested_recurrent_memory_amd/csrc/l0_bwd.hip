@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 3 : 2) void l0_bwd_state_kern
 #pragma unroll 1
   for (int hv = 0; hv < NHV; ++hv) {
     const int vb = hv * VH;
-    if (hv) __syncthreads();                   // the previous half's reads are done
+    if (hv) lds_barrier();                   // the previous half's reads are done
     f4 xs[SIT], ys[SIT];
 #pragma unroll
     for (int i = 0; i < SIT; ++i) {
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 3 : 2) void l0_bwd_state_kern
       sS.put4(k * LDH + c, xs[i]);
       sD.put4(k * LDH + c, ys[i]);
     }
-    __syncthreads();
+    lds_barrier();
     // one k-step of A fragments live at a time
 #pragma unroll
     for (int s = 0; s < NKH; ++s) {
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     product(a.dVnT + cix * V * C, V, s_dXu, LXV);
     product(a.dWT + cix * K * C, K, s_dXw, LXK);
   }
-  __syncthreads();
+  lds_barrier();
   // this wave's rows of dX_w, kept for phase 5 (the space is reused from phase 4)
 #pragma unroll
   for (int ct = 0; ct < CTK; ++ct)
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       dat[J] = acc;
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
 #pragma unroll
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       stage_rows<E>(s_b, LDI, in.b + (size_t)t0 * in.rowK + c0, in.rowK, C, NH, nvalid);
       stage_rows<E>(s_q, LDI, in.q + (size_t)t0 * in.rowQ + c0, in.rowQ, C, NH, nvalid);
     }
-    __syncthreads();
+    lds_barrier();
     const bool safe = block_safe<NH, GH>(s_g, wv);
 
     // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         }
       }
     }
-    __syncthreads();   // the cumulative-decay gradient overwrites gc in place
+    lds_barrier();   // the cumulative-decay gradient overwrites gc in place
 
     // ---- 5. assemble dq, dk, db and the cumulative-decay gradient (the
     // state half's dQg, dKt read ahead of the stores: mixed outstanding loads
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       colsum += __shfl_xor(colsum, 32, WAVE);
       if (lane < 16) atomicAdd(&s_col[kc], colsum);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
     // every Kt and gam. Column col of this pass, rows in NB blocks of RB: each
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) part += s_g[(blk * RB + i) * GH + col];
       s_part[blk * NH + col] = part;
-      __syncthreads();
+      lds_barrier();
       float run = s_col[kc] + dgam[kc] * fexp(s_gl[kc]);
       for (int b2 = NB - 1; b2 > blk; --b2) run += s_part[b2 * NH + col];
 #pragma unroll
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
         if (row < nvalid) dgo[(size_t)(t0 + row) * H * K + kc] = run;
       }
     }
-    __syncthreads();   // the next pass restages gc and the inputs
+    lds_barrier();   // the next pass restages gc and the inputs
   }
 }
 

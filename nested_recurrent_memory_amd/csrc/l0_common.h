@@ -151,30 +151,52 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   constexpr int KPL = Mma<E>::KPL;
   typedef typename Mma<E>::SFrag SF;
   const int lane = lane_id(), I = wave_id(), r = 16 * I;
-  const bool safe = l0_block_safe<K>(s_gc, I);
   const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
-  SF lf[NKS], qf[NKS];
+  typedef typename Mma<E>::Frag FR;
   const int ri = r + (lane & 15);
+  // Every global load of the phase first, all in flight together: this
+  // wave's rows of b, k, q, and the k rows of the earlier tiles J < I (the
+  // rows of tile I are this wave's own)
+  FR bo[NKS], ko[NKS], qo[NKS], kj[3][NKS];
+  {
+    const bool live = ri < in.nvalid;
+    const size_t rowk = (size_t)(in.t0 + ri) * in.rowK, rowq = (size_t)(in.t0 + ri) * in.rowQ;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+      bo[s] = live ? Mma<E>::ld(in.b + rowk + c0) : Mma<E>::zero();
+      ko[s] = live ? Mma<E>::ld(in.k + rowk + c0) : Mma<E>::zero();
+      qo[s] = (live && (want_q || ro.Qg)) ? Mma<E>::ld(in.q + rowq + c0) : Mma<E>::zero();
+    }
+#pragma unroll
+    for (int J = 0; J < 3; ++J) {
+      const int rj = 16 * J + (lane & 15);   // below the sequence end whenever J < I
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        const int c0 = s * Mma<E>::KS + kofs<E>(lane);
+        kj[J][s] = J < I ? Mma<E>::ld(in.k + (size_t)(in.t0 + rj) * in.rowK + c0) : Mma<E>::zero();
+      }
+    }
+  }
+  const bool safe = l0_block_safe<K>(s_gc, I);
+  SF lf[NKS], qf[NKS];
 #pragma unroll
   for (int s = 0; s < NKS; ++s) {
     const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-    float bv[KPL], kv[KPL], qv[KPL], gi[KPL];
-    in.vals(in.b, in.rowK, ri, c0, bv);
-    in.vals(in.k, in.rowK, ri, c0, kv);
+    float gi[KPL];
 #pragma unroll
     for (int e = 0; e < KPL; ++e) gi[e] = s_gc[ri * GL + c0 + e];
     lf[s] = Mma<E>::makes([&](int e) {
-      return bv[e] * kv[e] * fexp(gi[e] - s_gc[r * GL + c0 + e]);
+      return to_f(Mma<E>::elem(bo[s], e)) * to_f(Mma<E>::elem(ko[s], e)) *
+             fexp(gi[e] - s_gc[r * GL + c0 + e]);
     });
     if (want_q) {
-      in.vals(in.q, in.rowQ, ri, c0, qv);
       qf[s] = Mma<E>::makes([&](int e) {
-        return qv[e] * in.scale * fexp(gi[e] - s_gc[r * GL + c0 + e]);
+        return to_f(Mma<E>::elem(qo[s], e)) * in.scale * fexp(gi[e] - s_gc[r * GL + c0 + e]);
       });
     }
   }
-  // every load of the phase (the J tiles' k rows, then the rows the per-row
-  // outputs need) before its first global store
+  // every load of the phase before its first global store
   f4 accAs[4], accQs[4];
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
@@ -184,11 +206,10 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
 #pragma unroll
       for (int s = 0; s < NKS; ++s) {
         const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-        float kv[KPL];
-        in.vals(in.k, in.rowK, rj, c0, kv);
+        const FR kr = (J == 3 || J == I) ? ko[s] : kj[J < 3 ? J : 0][s];
         const SF kf = Mma<E>::makes([&](int e) {
           const float x = s_gc[r * GL + c0 + e] - s_gc[rj * GL + c0 + e];
-          return kv[e] * fexp(J < I ? x : fminf(x, 88.f));
+          return to_f(Mma<E>::elem(kr, e)) * fexp(J < I ? x : fminf(x, 88.f));
         });
         accA = Mma<E>::mma(accA, lf[s], kf);
         if (want_q) accQ = Mma<E>::mma(accQ, qf[s], kf);
@@ -202,9 +223,9 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
           if (j <= i) {
             for (int c = 0; c < K; ++c) {
               const float d = fexp(fminf(s_gc[i * GL + c] - s_gc[j * GL + c], 0.f));
-              const float kj = in.K_(j, c);
-              sa += in.B_(i, c) * in.K_(i, c) * kj * d;
-              if (want_q) sq += in.Q_(i, c) * kj * d;
+              const float kjv = in.K_(j, c);
+              sa += in.B_(i, c) * in.K_(i, c) * kjv * d;
+              if (want_q) sq += in.Q_(i, c) * kjv * d;
             }
           }
           accA[rr] = sa;
@@ -214,16 +235,6 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
     }
     accAs[J] = accA;
     accQs[J] = accQ;
-  }
-  typename Mma<E>::Frag rq[NKS], rk[NKS];
-  if (ro.Qg) {
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-      const bool live = ri < in.nvalid;
-      rq[s] = live ? Mma<E>::ld(in.q + (size_t)(in.t0 + ri) * in.rowQ + c0) : Mma<E>::zero();
-      rk[s] = live ? Mma<E>::ld(in.k + (size_t)(in.t0 + ri) * in.rowK + c0) : Mma<E>::zero();
-    }
   }
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
@@ -255,11 +266,11 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
           for (int e = 0; e < KPL; ++e) {
             const float gi = s_gc[ri * GL + c0 + e];
             s_x[(c0 + e - 64 * hh) * LDX + ri] =
-                which ? to_f(Mma<E>::elem(rq[s], e)) * in.scale * fexp(gi)
-                      : to_f(Mma<E>::elem(rk[s], e)) * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi);
+                which ? to_f(Mma<E>::elem(qo[s], e)) * in.scale * fexp(gi)
+                      : to_f(Mma<E>::elem(ko[s], e)) * fexp(s_gc[(CH - 1) * GL + c0 + e] - gi);
           }
         }
-        __syncthreads();
+        lds_barrier();
         if (tp) {
           for (int idx = threadIdx.x; idx < 64 * CH / 4; idx += blockDim.x) {
             const int kl = idx / (CH / 4), m = (idx % (CH / 4)) * 4;
@@ -276,7 +287,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
             else rdst.put4(m * K + 64 * hh + kl, x);
           }
         }
-        __syncthreads();
+        lds_barrier();
       }
     }
   }
@@ -307,7 +318,7 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
       if ((i >> 4) != (j >> 4)) s_T[i * LDT + j] = 0.f;
     }
   }
-  __syncthreads();
+  lds_barrier();
   for (int d = 1; d < 4; ++d) {
     const int nb = 4 - d;
     for (int e = tid; e < nb * 256; e += 256) {
@@ -318,7 +329,7 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
         acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * LDT + 16 * J + j];
       s_P[blk * 272 + i * 17 + j] = acc;
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < nb * 256; e += 256) {
       const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
       const int I = d + blk, J = I - d;
@@ -328,7 +339,7 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
         acc += s_T[(16 * I + i) * LDT + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
       s_T[(16 * I + i) * LDT + 16 * J + j] = -acc;
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
 
   // ---- 1. in-chunk cumulative log decay
   l0_cumsum(s_gc, in);
-  __syncthreads();
+  lds_barrier();
 
   // ---- 2. A and Aqk; Qg, Kt and their transposes while the rows are loaded
   {
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
                s_T);
   }
   if (tid < K) a.gam[cix * K + tid] = fexp(s_gc[(C - 1) * GL + tid]);
-  __syncthreads();
+  lds_barrier();
 
   // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
   l0_invert<LT>(s_A, s_T, s_P);
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. right-hand sides: X_w = b k e^gc in place of gc, X_u = w v over A/T
   {
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       for (int j = 0; j < VE; ++j) s_xu[m * LU + c + j] = wv_[j] * vv[j];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w. The B fragments
   // gather KPL consecutive rows m of one column. All tiles stay in registers
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       }
       if (isw) wt[tc] = acc; else ut[tc - NTW] = acc;
     }
-    __syncthreads();   // X_w and X_u are no longer read
+    lds_barrier();   // X_w and X_u are no longer read
     constexpr int LW = K + 4, LUU = V + 4;   // fp32 rows, 16-byte aligned
     float* s_w = reinterpret_cast<float*>(smem);    // [C][LW], then U [C][LUU]
     float* s_u = s_w + C * LW;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
     for (int t = 0; t < NTU; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) s_u[(R0 + acc_row(r)) * LUU + t * 16 + acc_col()] = ut[t][r];
-    __syncthreads();
+    lds_barrier();
     // W [C][K] (split), U [C][V] (fp32): four consecutive columns per thread
     const SplitTile<E> Wo = split_at<E>(a.W + cix * C * K, C * K);
     for (int e = tid; e < C * K / 4; e += 256) {

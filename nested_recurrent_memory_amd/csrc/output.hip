@@ -76,15 +76,15 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
   for (int kb = 0; kb < K; kb += KH) {
     stage_split(sB, LD, a.hT + cix * V * K + kb, K, V, KH);
-    __syncthreads();
+    lds_barrier();
     run(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), LD, KH);
-    __syncthreads();
+    lds_barrier();
   }
   stage_split(sB, LDC, a.vnT + cix * V * C, C, V, C);
-  __syncthreads();
+  lds_barrier();
   run(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), LDC, C);
   fold(0, 1.f);
-  __syncthreads();
+  lds_barrier();
 
   // ---- upper levels: (scale q_l) S_l[group], q rows exact
   const E* qrow = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K +
@@ -96,9 +96,9 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
     for (int kb = 0; kb < K; kb += KH) {
       stage_split(sB, LD, Sl + kb, K, V, KH);
-      __syncthreads();
+      lds_barrier();
       run(qrow + (size_t)l * K + kb, LD, KH);   // rows past the end repeat the last row
-      __syncthreads();
+      lds_barrier();
     }
     fold(l, a.scale);                           // which drops them
   }

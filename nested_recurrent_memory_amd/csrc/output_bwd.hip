@@ -128,7 +128,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         s_dm[tid] = 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (n + 1 < n1) fetch(n + 1);
 
     // ---- P = do S^T on this wave's rows and half of K; dq and partial dmix
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         acc[x] = Mma<E>::mma(acc[x], fa, sDT.get((vt * 16 + (lane & 15)) * LDDT + r0));
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < nv) dmb[(size_t)(t0 + tid) * H * L] = s_dm[tid] * a.scale;
   }
   float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;

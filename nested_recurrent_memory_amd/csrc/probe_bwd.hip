@@ -598,7 +598,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
       const int e = tid + 256 * u;
       sB.put4((e % Y) * LDT + (e / Y) * 4, rb[u]);
     }
-    __syncthreads();
+    lds_barrier();
     if (sl + 1 < nslab) fetch(sl + 1);
 #pragma unroll
     for (int s = 0; s < R / KS; ++s) {
@@ -613,7 +613,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
         for (int x = 0; x < XTW; ++x) acc[x][y] = Mma<E>::mma(acc[x][y], fa[x], fb);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   float* C = a.C + (size_t)h * X * Y;
 #pragma unroll

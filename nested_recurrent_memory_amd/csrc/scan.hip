@@ -162,7 +162,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
       sST.put4(vl * LDS_ST + k0, st[i]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- Vn = U - A S
 #pragma unroll
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- S <- diag(gam) S + BT Vn
 #pragma unroll

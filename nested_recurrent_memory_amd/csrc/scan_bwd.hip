@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 #pragma unroll
       for (int q = 0; q < DOE; ++q) sdO.put1((vl + q) * LDS_VN + c, cur.dov[q]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- dVn = Bop dS' (+ Aqk^T dO)
 #pragma unroll
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- dS = diag(gam) dS' - A^T dVn (+ Qg^T dO)
 #pragma unroll
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
     }
     // s_dot and s_dvn are rewritten by the next step
-    __syncthreads();
+    lds_barrier();
   }
   if (a.dinit) {
 #pragma unroll

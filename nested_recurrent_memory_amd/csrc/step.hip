@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   f4 u;
   {
     const E* vv = static_cast<const E*>(a.v) + (size_t)bh * V + col;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
       if (lane < CQ) *reinterpret_cast<f4*>(&s_rd[wv][l][cq * 4]) = rd[l];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- o = sum_l mix_l read_l
   if (tid < CQ) {
