@@ -32,9 +32,8 @@ namespace ngdn {
 template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int C = CH;
-  constexpr int GL = K + GCP;                // gc rows, then X_w rows
+  constexpr int GL = K + GCP;                // gc rows
   constexpr int LT = C + 4;                  // T rows, 16-byte aligned for fragment loads
-  constexpr int LU = V + GCP;                // X_u rows
   constexpr int KS = Mma<E>::KS;
   typedef typename Mma<E>::SFrag SF;
   const int NT = a.NT, H = a.H;
@@ -43,20 +42,16 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   const int h = bh % H, b = bh / H;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
 
-  // LDS: gc (later overwritten in place by X_w = b k e^gc), and a region
-  // holding A, T and the inversion scratch, later X_u = w v. Each wave keeps
-  // its 16 rows of T in registers across the reuse.
+  // LDS: gc, and a region holding A, T and the inversion scratch, later the
+  // transposed right-hand sides X_w^T, then X_u^T. Each wave keeps its 16 rows
+  // of T in registers across the reuse.
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_ATP = sizeof(float) * (C * AT_LD + C * LT + 3 * 16 * 17);
-  constexpr size_t SZ_XU = sizeof(float) * C * LU;
-  constexpr size_t SZ_R = SZ_ATP > SZ_XU ? SZ_ATP : SZ_XU;
+  constexpr size_t SZ_R = sizeof(float) * (C * AT_LD + C * LT + 3 * 16 * 17);
   __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R];
   float* s_gc = reinterpret_cast<float*>(smem);
-  float* s_xw = s_gc;
   float* s_A = reinterpret_cast<float*>(smem + SZ_GC);
   float* s_T = s_A + C * AT_LD;
   float* s_P = s_T + C * LT;                   // [3][16][17]
-  float* s_xu = s_A;
 
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, a.T, H, a.L, a.scale);
@@ -76,6 +71,25 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   }
   if (tid < K) a.gam[cix * K + tid] = fexp(s_gc[(C - 1) * GL + tid]);
   lds_barrier();
+
+  // the right-hand sides' inputs, read now so that the loads overlap the
+  // inversion: thread e takes row m = e % C, 16 bytes from column c
+  constexpr int VE = ChunkIn<E, K, V>::VE;      // elements per 16-byte load
+  constexpr int PW = C * K / VE / 256, PU = C * V / VE / 256;
+  static_assert(C * K / VE % 256 == 0 && C * V / VE % 256 == 0, "whole 16-byte groups per thread");
+  float rb[PW][VE], rk[PW][VE], rw[PU][VE], rv[PU][VE];
+#pragma unroll
+  for (int q = 0; q < PW; ++q) {
+    const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+    in.vec16(in.b, in.rowK, m, c, rb[q]);
+    in.vec16(in.k, in.rowK, m, c, rk[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < PU; ++q) {
+    const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+    in.vec16(in.w, in.rowV, m, c, rw[q]);
+    in.vec16(in.v, in.rowV, m, c, rv[q]);
+  }
 
   // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
   l0_invert<LT>(s_A, s_T, s_P);
@@ -100,53 +114,58 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   }
   lds_barrier();
 
-  // ---- 4. right-hand sides: X_w = b k e^gc in place of gc, X_u = w v over A/T
+  // ---- 4-5. W = T X_w, U = T X_u; wave w owns block-row w. X_w^T = (b k
+  // e^gc)^T, then X_u^T = (w v)^T, take the A/T region as split tiles (rows
+  // of m, each value split once by the thread that writes it), so every B
+  // fragment is a 16-byte read. All tiles stay in registers until both
+  // products are done; then W and U replace everything in LDS and leave in
+  // 16-byte rows (W, W^T and U), instead of 2- and 4-byte column-strided
+  // stores.
   {
-    constexpr int VE = ChunkIn<E, K, V>::VE;    // elements per 16-byte load
-    for (int e = tid; e < C * K / VE; e += 256) {
-      const int m = e / (K / VE), c = (e % (K / VE)) * VE;
-      float bv[VE], kv[VE];
-      in.vec16(in.b, in.rowK, m, c, bv);
-      in.vec16(in.k, in.rowK, m, c, kv);
-#pragma unroll
-      for (int j = 0; j < VE; ++j) s_xw[m * GL + c + j] = bv[j] * kv[j] * fexp(s_xw[m * GL + c + j]);
-    }
-    for (int e = tid; e < C * V / VE; e += 256) {
-      const int m = e / (V / VE), c = (e % (V / VE)) * VE;
-      float wv_[VE], vv[VE];
-      in.vec16(in.w, in.rowV, m, c, wv_);
-      in.vec16(in.v, in.rowV, m, c, vv);
-#pragma unroll
-      for (int j = 0; j < VE; ++j) s_xu[m * LU + c + j] = wv_[j] * vv[j];
-    }
-  }
-  lds_barrier();
-
-  // ---- 5. W = T X_w, U = T X_u; wave w owns block-row w. The B fragments
-  // gather KPL consecutive rows m of one column. All tiles stay in registers
-  // until every wave has read X_w and X_u; then W and U replace them in LDS
-  // and leave in 16-byte rows (W, W^T and U), instead of 2- and 4-byte
-  // column-strided stores.
-  {
+    using ST = SplitTile<E>;
+    constexpr int LDX = C + ST::PAD;
+    static_assert(sizeof(typename ST::T) * ST::NPLANE * (K > V ? K : V) * LDX <= SZ_R,
+                  "X^T fits the A/T region");
+    const ST sX{reinterpret_cast<typename ST::T*>(s_A), (K > V ? K : V) * LDX};
     constexpr int NTW = K / 16, NTU = V / 16;
     f4 wt[NTW], ut[NTU];
 #pragma unroll
-    for (int tc = 0; tc < NTW + NTU; ++tc) {
-      const bool isw = tc < NTW;
-      const int col = (isw ? tc : tc - NTW) * 16 + (lane & 15);
-      const float* xb = isw ? s_xw + col : s_xu + col;
-      const int ld = isw ? GL : LU;
+    for (int q = 0; q < PW; ++q) {
+      const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+#pragma unroll
+      for (int j = 0; j < VE; ++j)
+        sX.put1((c + j) * LDX + m, rb[q][j] * rk[q][j] * fexp(s_gc[m * GL + c + j]));
+    }
+    lds_barrier();
+#pragma unroll
+    for (int tc = 0; tc < NTW; ++tc) {
+      const int col = tc * 16 + (lane & 15);
       f4 acc = f4_zero();
 #pragma unroll
-      for (int s = 0; s < C / KS; ++s) {
-        if (s * KS < kd) {   // T is zero past the block diagonal
-          const int m0 = s * KS + kofs<E>(lane);
-          acc = Mma<E>::mma(acc, tf[s], Mma<E>::makes([&](int e) { return xb[(m0 + e) * ld]; }));
-        }
-      }
-      if (isw) wt[tc] = acc; else ut[tc - NTW] = acc;
+      for (int s = 0; s < C / KS; ++s)
+        if (s * KS < kd)   // T is zero past the block diagonal
+          acc = Mma<E>::mma(acc, tf[s], sX.get(col * LDX + s * KS + kofs<E>(lane)));
+      wt[tc] = acc;
     }
-    lds_barrier();   // X_w and X_u are no longer read
+    lds_barrier();   // X_u^T replaces X_w^T
+#pragma unroll
+    for (int q = 0; q < PU; ++q) {
+      const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+#pragma unroll
+      for (int j = 0; j < VE; ++j) sX.put1((c + j) * LDX + m, rw[q][j] * rv[q][j]);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int tc = 0; tc < NTU; ++tc) {
+      const int col = tc * 16 + (lane & 15);
+      f4 acc = f4_zero();
+#pragma unroll
+      for (int s = 0; s < C / KS; ++s)
+        if (s * KS < kd)
+          acc = Mma<E>::mma(acc, tf[s], sX.get(col * LDX + s * KS + kofs<E>(lane)));
+      ut[tc] = acc;
+    }
+    lds_barrier();   // X_u^T is no longer read
     constexpr int LW = K + 4, LUU = V + 4;   // fp32 rows, 16-byte aligned
     float* s_w = reinterpret_cast<float*>(smem);    // [C][LW], then U [C][LUU]
     float* s_u = s_w + C * LW;
