@@ -463,7 +463,12 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
                           xw * bi * ki * eg + gq * qh * eg - gk * ki * ekt;
         colsum += gk * ki * ekt;
         s_g[i * GH + kl] = dgc;
-        if (i < nvalid) {
+        if constexpr (STAGE) {
+          // in place of this element's q, k, b (read above, by this thread only)
+          s_q[i * LDI + kl] = from_f<E>(dqh * in.scale);
+          s_k[i * LDI + kl] = from_f<E>(dk_);
+          s_b[i * LDI + kl] = from_f<E>(db_);
+        } else if (i < nvalid) {
           dqo[(size_t)(t0 + i) * H * a.L * K + kc] = from_f<E>(dqh * in.scale);
           dko[(size_t)(t0 + i) * H * K + kc] = from_f<E>(dk_);
           dbo[(size_t)(t0 + i) * H * K + kc] = from_f<E>(db_);
@@ -474,6 +479,20 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       if (lane < 16) atomicAdd(&s_col[kc], colsum);
     }
     lds_barrier();
+    if constexpr (STAGE) {
+      // dq, dk, db leave as 16-byte rows from the k, b, q columns' space
+      constexpr int VE = 16 / (int)sizeof(E), SEG = NH / VE;
+      typedef E EV __attribute__((__vector_size__(16)));
+      for (int e = tid; e < 3 * C * SEG; e += 256) {
+        const int which = e / (C * SEG), i = (e / SEG) % C, c = (e % SEG) * VE;
+        if (i < nvalid) {
+          const E* src = (which == 0 ? s_q : which == 1 ? s_k : s_b) + i * LDI + c;
+          E* dst = which == 0 ? dqo + (size_t)(t0 + i) * H * a.L * K
+                 : (which == 1 ? dko : dbo) + (size_t)(t0 + i) * H * K;
+          *reinterpret_cast<EV*>(dst + c0 + c) = *reinterpret_cast<const EV*>(src);
+        }
+      }
+    }
 
     // ---- 6. dg = reverse cumsum of dgc within the chunk; gc_last also feeds
     // every Kt and gam. Column col of this pass, rows in NB blocks of RB: each
