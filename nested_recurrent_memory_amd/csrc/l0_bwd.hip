@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 3 : 2) void l0_bwd_state_kern
 }
 
 template <typename E, int K, int V>
-__global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
+__global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr int C = CH;
   constexpr int NH = K > 64 ? 64 : K;          // columns per pass of the decay backward
   constexpr int NPASS = K / NH;
@@ -327,6 +327,65 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   float* dgo = a.dg + tok * K;
   const float* dgam = a.dgam + cix * K;
 
+  // Inputs of one pass (NH columns from c0): g for the in-chunk cumulative
+  // sum and, for bf16, the k, b, q columns. They are read into registers ahead
+  // of their pass (the first before the loop, the next one before the current
+  // pass's output stores) and written to LDS at the top of the pass.
+  constexpr int TPC = 256 / NH, SEG = C / TPC;      // cumsum: threads per column, rows each
+  constexpr int SEGS = NH * (int)sizeof(E) / 16;    // 16-byte groups per staged row
+  constexpr int SI = STAGE ? (C * SEGS + 255) / 256 : 1;
+  static_assert(!STAGE || C * SEGS % 256 == 0, "whole groups per thread");
+  typedef __attribute__((__vector_size__(16))) int v4i;
+  struct PassIn { float g[SEG]; v4i k[SI], b[SI], q[SI]; };
+  auto pass_load = [&](int p, PassIn& x) {
+    const int c0 = p * NH, col = tid / TPC, part = tid % TPC;
+#pragma unroll
+    for (int r = 0; r < SEG; ++r) {
+      const int i = part * SEG + r;
+      x.g[r] = i < nvalid ? in.g[(size_t)(t0 + i) * in.rowK + c0 + col] : 0.f;
+    }
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int u = 0; u < SI; ++u) {
+        const int e = tid + 256 * u, i = e / SEGS, c = (e % SEGS) * (16 / (int)sizeof(E));
+        const v4i z = {0, 0, 0, 0};
+        const bool live = i < nvalid;
+        x.k[u] = live ? *reinterpret_cast<const v4i*>(in.k + (size_t)(t0 + i) * in.rowK + c0 + c) : z;
+        x.b[u] = live ? *reinterpret_cast<const v4i*>(in.b + (size_t)(t0 + i) * in.rowK + c0 + c) : z;
+        x.q[u] = live ? *reinterpret_cast<const v4i*>(in.q + (size_t)(t0 + i) * in.rowQ + c0 + c) : z;
+      }
+    }
+  };
+  auto pass_store = [&](int p, const PassIn& x) {
+    const int c0 = p * NH, col = tid / TPC, part = tid % TPC;
+    float y[SEG];
+#pragma unroll
+    for (int r = 0; r < SEG; ++r) y[r] = x.g[r];
+#pragma unroll
+    for (int r = 1; r < SEG; ++r) y[r] += y[r - 1];
+    const int base = lane & ~(TPC - 1);
+    float off = 0.f;
+#pragma unroll
+    for (int q = 0; q < TPC - 1; ++q) {
+      const float t = __shfl(y[SEG - 1], base + q, WAVE);
+      if (q < part) off += t;
+    }
+#pragma unroll
+    for (int r = 0; r < SEG; ++r) s_g[(part * SEG + r) * GH + col] = y[r] + off;
+    if (part == TPC - 1) s_gl[c0 + col] = y[SEG - 1] + off;
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int u = 0; u < SI; ++u) {
+        const int e = tid + 256 * u, i = e / SEGS, c = (e % SEGS) * (16 / (int)sizeof(E));
+        *reinterpret_cast<v4i*>(s_k + i * LDI + c) = x.k[u];
+        *reinterpret_cast<v4i*>(s_b + i * LDI + c) = x.b[u];
+        *reinterpret_cast<v4i*>(s_q + i * LDI + c) = x.q[u];
+      }
+    }
+  };
+  PassIn pin;
+  pass_load(0, pin);
+
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
     const int c0 = p * NH;
@@ -341,14 +400,21 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     };
 
     // ---- 4. this pass's gc and input columns
-    cumsum_cols<NH, GH>(s_g, in, c0, s_gl + c0);
-    if constexpr (STAGE) {
-      stage_rows<E>(s_k, LDI, in.k + (size_t)t0 * in.rowK + c0, in.rowK, C, NH, nvalid);
-      stage_rows<E>(s_b, LDI, in.b + (size_t)t0 * in.rowK + c0, in.rowK, C, NH, nvalid);
-      stage_rows<E>(s_q, LDI, in.q + (size_t)t0 * in.rowQ + c0, in.rowQ, C, NH, nvalid);
-    }
+    pass_store(p, pin);
     lds_barrier();
     const bool safe = block_safe<NH, GH>(s_g, wv);
+    // the state half's dQg, dKt for phase 5, read now so that the loads overlap
+    // phases 4a-4b (and precede this pass's stores: mixed outstanding loads and
+    // stores would make every load wait for all of them)
+    float gqa[CTH][4], gka[CTH][4];
+#pragma unroll
+    for (int ct = 0; ct < CTH; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = R0 + acc_row(r), kc = c0 + ct * 16 + acc_col();
+        gqa[ct][r] = dQg[i * K + kc];
+        gka[ct][r] = dKt[i * K + kc];
+      }
 
     // ---- 4a. d(bk) and dq-hat from A and Aqk, rows of block-row I = w
     //   sum_j dA_ij k_j e^(gc_i - gc_j) = e^(gc_i - gc_r) sum_j dA_ij [k_j e^(gc_r - gc_j)]
@@ -431,18 +497,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
     }
     lds_barrier();   // the cumulative-decay gradient overwrites gc in place
 
-    // ---- 5. assemble dq, dk, db and the cumulative-decay gradient (the
-    // state half's dQg, dKt read ahead of the stores: mixed outstanding loads
-    // and stores would make every load wait for all of them)
-    float gqa[CTH][4], gka[CTH][4];
-#pragma unroll
-    for (int ct = 0; ct < CTH; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = R0 + acc_row(r), kc = c0 + ct * 16 + acc_col();
-        gqa[ct][r] = dQg[i * K + kc];
-        gka[ct][r] = dKt[i * K + kc];
-      }
+    // ---- 5. assemble dq, dk, db and the cumulative-decay gradient
 #pragma unroll
     for (int ct = 0; ct < CTH; ++ct) {
       const int kl = ct * 16 + acc_col(), kc = c0 + kl;
@@ -479,6 +534,7 @@ __global__ __launch_bounds__(256) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
       if (lane < 16) atomicAdd(&s_col[kc], colsum);
     }
     lds_barrier();
+    if (p + 1 < NPASS) pass_load(p + 1, pin);   // ahead of this pass's stores
     if constexpr (STAGE) {
       // dq, dk, db leave as 16-byte rows from the k, b, q columns' space
       constexpr int VE = 16 / (int)sizeof(E), SEG = NH / VE;
