@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     }
     auto product = [&](const float* srcT, int ncols, float* dst, int ldd) {
       const int cpw = ncols / 16 / 4;   // column tiles per wave
-#pragma unroll 1
+#pragma unroll
       for (int c = 0; c < cpw; ++c) {
         const int ct = wv * cpw + c;
         const float* br = srcT + (size_t)(ct * 16 + (lane & 15)) * C + kofs<E>(lane);
@@ -251,6 +251,31 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   for (int ct = 0; ct < CTK; ++ct)
 #pragma unroll
     for (int r = 0; r < 4; ++r) dxw[ct][r] = s_dXw[(wv * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()];
+
+  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
+  f4 dat[4];
+  {
+    const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);   // W in split form
+    const float* Ug = a.U + cix * C * V;
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      f4 acc = f4_zero();
+      if (J <= wv) {
+        const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
+        const int wr = (J * 16 + (lane & 15)) * K + kofs<E>(lane);
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += KS)
+          acc = Mma<E>::mma(acc, Mma<E>::ld(xr + k0), Ws.get(wr + k0));
+        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LXV, LXV, Ug + (size_t)J * 16 * V, V, V);
+      }
+      dat[J] = acc;
+    }
+  }
+  // dAqk, read before the dv/dw stores
+  constexpr int DQE = C * C / 256;
+  float dqv[DQE];
+#pragma unroll
+  for (int u = 0; u < DQE; ++u) dqv[u] = a.dAqk[cix * C * C + tid + 256 * u];
 
   // dv = dX_u * w, dw = dX_u * v: 16-byte rows, all loads of a thread ahead of its stores
   {
@@ -284,25 +309,6 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     }
   }
 
-  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
-  f4 dat[4];
-  {
-    const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);   // W in split form
-    const float* Ug = a.U + cix * C * V;
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      f4 acc = f4_zero();
-      if (J <= wv) {
-        const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
-        const int wr = (J * 16 + (lane & 15)) * K + kofs<E>(lane);
-#pragma unroll
-        for (int k0 = 0; k0 < K; k0 += KS)
-          acc = Mma<E>::mma(acc, Mma<E>::ld(xr + k0), Ws.get(wr + k0));
-        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LXV, LXV, Ug + (size_t)J * 16 * V, V, V);
-      }
-      dat[J] = acc;
-    }
-  }
   lds_barrier();
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
@@ -312,9 +318,10 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       s_dA[i * AT_LD + j] = (j < i) ? -dat[J][r] : 0.f;
     }
   }
-  {
-    const float* dq = a.dAqk + cix * C * C;
-    for (int e = tid; e < C * C; e += 256) s_dQ[(e / C) * AT_LD + e % C] = dq[e];
+#pragma unroll
+  for (int u = 0; u < DQE; ++u) {
+    const int e = tid + 256 * u;
+    s_dQ[(e / C) * AT_LD + e % C] = dqv[u];
   }
 
   const int R0 = 16 * wv;
