@@ -282,22 +282,6 @@ __device__ __forceinline__ void head_xcd_split(int x, int H, int NF, int& b, int
   b = t / H8;
 }
 
-// Copies nrows x ncols elements of a row-major global array (row stride
-// `stride` elements) into LDS rows of stride ld, with 16-byte accesses; rows
-// at or past `nvalid` are zero. ncols, ld and stride are multiples of 16 B.
-template <typename E>
-__device__ __forceinline__ void stage_rows(E* dst, int ld, const E* src, size_t stride,
-                                           int nrows, int ncols, int nvalid) {
-  constexpr int VE = 16 / sizeof(E);
-  typedef __attribute__((__vector_size__(16))) int v4i;
-  const int segs = ncols / VE;
-  for (int e = threadIdx.x; e < nrows * segs; e += blockDim.x) {
-    const int i = e / segs, c = (e % segs) * VE;
-    v4i x = {0, 0, 0, 0};
-    if (i < nvalid) x = *reinterpret_cast<const v4i*>(src + (size_t)i * stride + c);
-    *reinterpret_cast<v4i*>(dst + i * ld + c) = x;
-  }
-}
 
 // Fragments gathered down a column: KPL consecutive rows of column 0 at p
 // (row stride ld), for operands whose reduction index runs along the rows of
@@ -336,21 +320,25 @@ __device__ __forceinline__ void stage_f32(float* dst, int ld, const float* src, 
   }
 }
 
-// The same copy into a split tile: each value is split once, here.
-template <typename ST>
-__device__ __forceinline__ void stage_split(const ST& dst, int ld, const float* src, int src_ld,
-                                            int rows, int cols) {
-  const int segs = cols / 4;
-  for (int e = threadIdx.x; e < rows * segs; e += blockDim.x) {
-    const int r = e / segs, c = (e % segs) * 4;
-    dst.put4(r * ld + c, *reinterpret_cast<const f4*>(src + (size_t)r * src_ld + c));
+// ROWS x COLS fp32 values of a row-major global array (row stride src_ld)
+// into a split LDS tile with row stride ld, 16 bytes per access by NTH
+// threads: every load of a thread is issued before its first LDS write, so
+// the loads are in flight together rather than one round trip each.
+template <int NTH, int ROWS, int COLS, typename ST>
+__device__ __forceinline__ void stage_split(const ST& dst, int ld, const float* src, int src_ld) {
+  constexpr int SEGS = COLS / 4, NSEG = ROWS * SEGS, PER = (NSEG + NTH - 1) / NTH;
+  static_assert(COLS % 4 == 0, "whole 16-byte groups");
+  f4 x[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + NTH * u, r = e / SEGS, c = (e % SEGS) * 4;
+    if (NSEG % NTH == 0 || e < NSEG) x[u] = *reinterpret_cast<const f4*>(src + (size_t)r * src_ld + c);
   }
-}
-
-// S [K][V] fp32 into LDS as S^T [V][ld] (k contiguous).
-template <int K, int V>
-__device__ __forceinline__ void stage_state_T(float* dst, int ld, const float* S) {
-  for (int e = threadIdx.x; e < K * V; e += blockDim.x) dst[(e % V) * ld + e / V] = S[e];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + NTH * u, r = e / SEGS, c = (e % SEGS) * 4;
+    if (NSEG % NTH == 0 || e < NSEG) dst.put4(r * ld + c, x[u]);
+  }
 }
 
 // ---------------------------------------------------------------- misc

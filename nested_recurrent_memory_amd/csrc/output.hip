@@ -46,15 +46,23 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   for (int c = 0; c < CTV; ++c) out[c] = f4_zero();
   f4 acc[CTV];
 
-  // acc[c] += A[rows of this wave][0:kd] * s_B[c-th 16 rows][0:kd]^T, the A
-  // rows read from global (fp32 derived or exact inputs)
-  auto run = [&](const auto* arow, int ldb, int kd) {
-    for (int k0 = 0; k0 < kd; k0 += KS) {
-      const auto fa = Mma<E>::ld(arow + k0);
+  // One stage: this wave's A fragments (NKA k-steps from global: fp32
+  // derived rows split, or exact input rows) are read first, so their loads
+  // overlap the staging of the B operand; then acc[c] += A s_B[c-th 16 rows]^T.
+  auto stage = [&](const auto* arow, auto nka_c, const float* bsrc, int bsrc_ld, auto bcols_c, int ldb) {
+    constexpr int NKA = decltype(nka_c)::value;
+    using FA = decltype(Mma<E>::ld(arow));
+    FA fa[NKA];
+#pragma unroll
+    for (int s = 0; s < NKA; ++s) fa[s] = Mma<E>::ld(arow + s * KS);
+    stage_split<256, V, decltype(bcols_c)::value>(sB, ldb, bsrc, bsrc_ld);
+    lds_barrier();
+#pragma unroll
+    for (int s = 0; s < NKA; ++s)
 #pragma unroll
       for (int c = 0; c < CTV; ++c)
-        acc[c] = Mma<E>::mma(acc[c], fa, sB.get((c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + k0));
-    }
+        acc[c] = Mma<E>::mma(acc[c], fa[s], sB.get((c * 16 + (lane & 15)) * ldb + kofs<E>(lane) + s * KS));
+    lds_barrier();
   };
   auto fold = [&](int l, float sc) {
 #pragma unroll
@@ -63,28 +71,21 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
       const float m = mixw(i, l) * sc;
 #pragma unroll
       for (int c = 0; c < CTV; ++c) out[c][r] += m * acc[c][r];
-      if (l == 0 && a.read0 && i < nvalid) {
-        float* rp = a.read0 + (((size_t)b * T + t0 + i) * H + h) * V;
-#pragma unroll
-        for (int c = 0; c < CTV; ++c) rp[c * 16 + acc_col()] = acc[c][r];
-      }
     }
   };
 
-  // ---- level 0: Qg h + Aqk Vn
+  // ---- level 0: Qg h + Aqk Vn (its read kept for the backward, stored last)
 #pragma unroll
   for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-  for (int kb = 0; kb < K; kb += KH) {
-    stage_split(sB, LD, a.hT + cix * V * K + kb, K, V, KH);
-    lds_barrier();
-    run(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), LD, KH);
-    lds_barrier();
-  }
-  stage_split(sB, LDC, a.vnT + cix * V * C, C, V, C);
-  lds_barrier();
-  run(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), LDC, C);
+  for (int kb = 0; kb < K; kb += KH)
+    stage(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), std::integral_constant<int, KH / KS>{},
+          a.hT + cix * V * K + kb, K, std::integral_constant<int, KH>{}, LD);
+  stage(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), std::integral_constant<int, C / KS>{},
+        a.vnT + cix * V * C, C, std::integral_constant<int, C>{}, LDC);
   fold(0, 1.f);
-  lds_barrier();
+  f4 read0[CTV];
+#pragma unroll
+  for (int c = 0; c < CTV; ++c) read0[c] = acc[c];
 
   // ---- upper levels: (scale q_l) S_l[group], q rows exact
   const E* qrow = static_cast<const E*>(a.q) + ((size_t)b * T * H + h) * L * K +
@@ -94,12 +95,9 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
     const float* Sl = a.statesT[l] + (((size_t)b * a.NGl[l] + grp) * H + h) * V * K;
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-    for (int kb = 0; kb < K; kb += KH) {
-      stage_split(sB, LD, Sl + kb, K, V, KH);
-      lds_barrier();
-      run(qrow + (size_t)l * K + kb, LD, KH);   // rows past the end repeat the last row
-      lds_barrier();
-    }
+    for (int kb = 0; kb < K; kb += KH)   // rows past the end repeat the last row
+      stage(qrow + (size_t)l * K + kb, std::integral_constant<int, KH / KS>{}, Sl + kb, K,
+            std::integral_constant<int, KH>{}, LD);
     fold(l, a.scale);                           // which drops them
   }
 
@@ -112,6 +110,17 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
 #pragma unroll
       for (int c = 0; c < CTV; ++c)
         op[(size_t)(t0 + i) * H * V + c * 16 + acc_col()] = from_f<E>(out[c][r]);
+    }
+  }
+  if (a.read0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r);
+      if (i < nvalid) {
+        float* rp = a.read0 + (((size_t)b * T + t0 + i) * H + h) * V;
+#pragma unroll
+        for (int c = 0; c < CTV; ++c) rp[c * 16 + acc_col()] = read0[c][r];
+      }
     }
   }
 }

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   E* dqb = static_cast<E*>(a.dq) + ((size_t)b * T * H + h) * L * K + (size_t)l * K;
   float* dmb = a.dmix + ((size_t)b * T * H + h) * L + l;
 
-  stage_split(sS, LDS_, a.states + (((size_t)b * NG + j) * H + h) * K * V, V, K, V);
+  stage_split<NTH, K, V>(sS, LDS_, a.states + (((size_t)b * NG + j) * H + h) * K * V, V);
 
   f4 acc[NDS];
 #pragma unroll
