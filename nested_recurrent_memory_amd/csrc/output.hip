@@ -15,8 +15,7 @@ template <typename E, int K, int V>
 __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   constexpr int C = CH;
   using ST = SplitTile<E>;
-  // states are staged 64 rows of K at a time: a 37 KB tile, so four
-  // workgroups fit on a CU
+  // states are staged 64 rows of K at a time (a 37 KB tile)
   constexpr int KH = K > 64 ? 64 : K;
   constexpr int LD = KH + ST::PAD;
   constexpr int LDC = C + ST::PAD;
