@@ -385,16 +385,14 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
   hipStream_t st = (hipStream_t)stream;
   ngdn::AtBArgs a{};
   a.B = d->B; a.H = d->H; a.NF = nf; a.N = n_pairs; a.X = d->K; a.Y = d->V; a.split = split;
-  hipError_t e = hipSuccess;
-  if (promotion == 0) {
-    a.A = ws_du; a.Bm = ws_vals; a.C = dkp + off;                  // dWk = du^T Vals
-    if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
-  }
-  a.A = ws_vals; a.Bm = ws_dxb; a.C = dbp + off;                   // dBp = Vals^T dxb
-  if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
-  a.A = ws_vals; a.Bm = ws_dxw; a.C = dwp + off;                   // dWp = Vals^T dxw
-  if ((e = ngdn::atb_accumulate(a, d->dtype, st)) != hipSuccess) return launched(e, "ngdn_param_grads");
-  a.A = ws_vals; a.Bm = ws_dxg; a.C = dgp + off;                   // dGp = Vals^T dxg
+  // the (up to) four sums in one launch
+  auto add = [&](const float* A, const float* Bm, float* C) {
+    a.A[a.nprod] = A; a.Bm[a.nprod] = Bm; a.C[a.nprod] = C; ++a.nprod;
+  };
+  if (promotion == 0) add(ws_du, ws_vals, dkp + off);    // dWk = du^T Vals
+  add(ws_vals, ws_dxb, dbp + off);                       // dBp = Vals^T dxb
+  add(ws_vals, ws_dxw, dwp + off);                       // dWp = Vals^T dxw
+  add(ws_vals, ws_dxg, dgp + off);                       // dGp = Vals^T dxg
   return launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads");
 }
 

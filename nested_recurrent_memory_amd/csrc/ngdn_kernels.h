@@ -161,8 +161,11 @@ hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st);
 // C_h[X][Y] += sum over rows m = (b, i, n) of A[b,h,i,n,X] B[b,h,i,n,Y]
 // (fp32, accumulated atomically), for the per-head parameter gradients of a
 // level: one workgroup per (head, slice of items).
+// Up to four independent sums C_p[h] += sum over rows of A_p^T B_p, one
+// launch for all of them (grid nprod x H x split).
 struct AtBArgs {
-  const float* A; const float* Bm; float* C;
+  const float* A[4]; const float* Bm[4]; float* C[4];
+  int nprod;
   int B, H, NF, N, X, Y;
   int split;
 };

@@ -551,8 +551,11 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
   __shared__ __attribute__((aligned(16))) typename ST::T s_bt[ST::NPLANE * Y * LDT];
   const ST sA{s_at, X * LDT}, sB{s_bt, Y * LDT};
   const int H = a.H, NF = a.NF, N = a.N;
+  const int prod = blockIdx.x / (H * a.split);
   const int part = blockIdx.x % a.split;
-  const int h = blockIdx.x / a.split;
+  const int h = (blockIdx.x / a.split) % H;
+  const float* Ap = a.A[prod];
+  const float* Bp = a.Bm[prod];
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const int items = a.B * NF;
   const int per = (items + a.split - 1) / a.split;
@@ -577,13 +580,13 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
     for (int u = 0; u < GA; ++u) {
       const int e = tid + 256 * u, c = e % X, r4 = (e / X) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ra[u][j] = r4 + j < nr ? a.A[(row0 + r4 + j) * X + c] : 0.f;
+      for (int j = 0; j < 4; ++j) ra[u][j] = r4 + j < nr ? Ap[(row0 + r4 + j) * X + c] : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
       const int e = tid + 256 * u, c = e % Y, r4 = (e / Y) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rb[u][j] = r4 + j < nr ? a.Bm[(row0 + r4 + j) * Y + c] : 0.f;
+      for (int j = 0; j < 4; ++j) rb[u][j] = r4 + j < nr ? Bp[(row0 + r4 + j) * Y + c] : 0.f;
     }
   };
   fetch(0);
@@ -615,7 +618,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
     }
     lds_barrier();
   }
-  float* C = a.C + (size_t)h * X * Y;
+  float* C = a.C[prod] + (size_t)h * X * Y;
 #pragma unroll
   for (int x = 0; x < XTW; ++x)
 #pragma unroll
@@ -656,7 +659,7 @@ hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st) {
 
 template <typename E, int X, int Y>
 static hipError_t launch_atb(const AtBArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.H * a.split);
+  const unsigned grid = (unsigned)(a.nprod * a.H * a.split);
   if (grid == 0 || a.B * a.NF == 0) return hipSuccess;
   hipLaunchKernelGGL((atb_kernel<E, X, Y>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
