@@ -244,8 +244,11 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
  * that do not fire). A token fires level l when (pos + 1) % chunk_size == 0
  * and ((pos + 1) / chunk_size) % firing_intervals[l] == 0. firing_intervals
  * [L] and n_queries [L-1] are host arrays; parameters as for ngdn_probe_fwd
- * (every level's slice). ws: fp32 workspace of B*H*(3*N*K + K) floats, N the
- * most pairs of any level (K for merge). */
+ * (every level's slice). When no level has more than 64 pairs per firing
+ * (K for merge), the promotions of all levels run in one launch of B*H
+ * workgroups; otherwise as two launches per level (probe, then the update)
+ * through ws: fp32 workspace of B*H*(3*N*K + K) floats, N the most pairs of
+ * any level (K for merge). */
 int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* v,
                   const float* g, const void* b, const void* w, const void* mix,
                   const float* state_in, float* state_out, const int64_t* position,

@@ -441,6 +441,35 @@ int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* 
   const size_t hkv = (size_t)d->H * skv;
   const size_t esz = d->dtype == NGDN_BF16 ? 2 : 4;
   const size_t units = (size_t)d->B * d->H;
+  if (L == 1) return NGDN_OK;
+  // Every level with at most 64 pairs per firing: all promotions in one
+  // gated launch. With an int position the host skips it when no level fires.
+  bool fused = L <= ngdn::MAXL;
+  for (int l = 1; l < L; ++l)
+    if ((promotion == 1 ? K : n_queries[l - 1]) > ngdn::PROMOTE_NMAX) fused = false;
+  if (fused) {
+    if (!position) {
+      const long long end = (long long)position_all + 1;
+      bool any = false;
+      for (int l = 1; l < L; ++l)
+        any = any || (end % chunk_size == 0 && (end / chunk_size) % firing_intervals[l] == 0);
+      if (!any) return NGDN_OK;
+    }
+    ngdn::PromoteArgs pa{};
+    pa.state = state_out;
+    pa.pos = reinterpret_cast<const long long*>(position);
+    pa.pos_all = position_all;
+    pa.chunk = chunk_size;
+    for (int l = 0; l < L; ++l) {
+      pa.f[l] = firing_intervals[l];
+      pa.N[l] = l == 0 ? 0 : (promotion == 1 ? K : n_queries[l - 1]);
+    }
+    pa.bank = query_banks; pa.Nmax = n_max;
+    pa.kp = key_projections; pa.bpT = bpT; pa.wpT = wpT; pa.gpT = gpT;
+    pa.merge = promotion;
+    pa.B = d->B; pa.H = d->H; pa.L = L;
+    return launched(ngdn::promote_fwd(pa, d->dtype, K, st), "ngdn_step (promotions)");
+  }
   for (int l = 1; l < L; ++l) {
     ngdn::FireGate gate{nullptr, chunk_size, firing_intervals[l]};
     if (position) {

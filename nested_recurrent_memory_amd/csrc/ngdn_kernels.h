@@ -24,6 +24,9 @@ struct L0IntraArgs {
 };
 hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
+// Most levels any entry point handles.
+constexpr int MAXL = 8;
+
 // Per-row firing gate of the decoding step (ops/naive.py:101-113): when pos
 // is set, batch row b runs only if the token at pos[b] completes a chunk
 // (end = pos[b] + 1, end % chunk == 0) whose number end / chunk is a multiple
@@ -129,6 +132,27 @@ struct StepArgs {
 };
 hipError_t step_fwd(const StepArgs& a, int dtype, int K, int V, hipStream_t st);
 
+// The promotions that follow one decoding token (ops/naive.py:101-123),
+// bottom-up over levels 1..L-1 in one launch: for every row whose firing of
+// level l completes at this token (position + 1 a multiple of chunk f_l), the
+// probe of level l-1's state (already updated) and one firing of level l's
+// update, in place on state [B,H,L,K,V]. One workgroup of 8 waves per
+// (b, h); levels with up to 64 pairs per firing (PROMOTE_NMAX).
+constexpr int PROMOTE_NMAX = 64;
+struct PromoteArgs {
+  float* state;
+  const long long* pos;   // [B] positions, or null: pos_all for every row
+  long long pos_all;
+  int chunk;
+  int f[MAXL];       // firing intervals per level
+  int N[MAXL];       // pairs per firing per level (index l >= 1)
+  const void* bank; int Nmax;                                  // [L-1,H,Nmax,K]
+  const void* kp; const void* bpT; const void* wpT; const void* gpT;   // [L-1,H,K,V]
+  int merge;
+  int B, H, L;
+};
+hipError_t promote_fwd(const PromoteArgs& a, int dtype, int K, hipStream_t st);
+
 // Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
 // the autograd replay of ops/chunk.py:339-371,486-517, derived in closed
 // form). One workgroup of 8 waves per (batch, head, firing i). Inputs: the
@@ -174,8 +198,6 @@ hipError_t atb_accumulate(const AtBArgs& a, int dtype, hipStream_t st);
 }  // namespace ngdn
 
 namespace ngdn {
-
-constexpr int MAXL = 8;
 
 // Output of the whole op for one chunk (ops/chunk.py:250-286; ops/naive.py:376-390):
 //   o = mix_0 (Qg h_n + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[n / f_l]
