@@ -321,6 +321,26 @@ __device__ __forceinline__ void stage_f32(float* dst, int ld, const float* src, 
 }
 
 // ROWS x COLS fp32 values of a row-major global array (row stride src_ld)
+// into fp32 LDS rows of stride ld, 16 bytes per access by NTH threads, every
+// load of a thread issued before its first LDS write.
+template <int NTH, int ROWS, int COLS>
+__device__ __forceinline__ void stage_f32(float* dst, int ld, const float* src, int src_ld) {
+  constexpr int SEGS = COLS / 4, NSEG = ROWS * SEGS, PER = (NSEG + NTH - 1) / NTH;
+  static_assert(COLS % 4 == 0, "whole 16-byte groups");
+  f4 x[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + NTH * u, r = e / SEGS, c = (e % SEGS) * 4;
+    if (NSEG % NTH == 0 || e < NSEG) x[u] = *reinterpret_cast<const f4*>(src + (size_t)r * src_ld + c);
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + NTH * u, r = e / SEGS, c = (e % SEGS) * 4;
+    if (NSEG % NTH == 0 || e < NSEG) *reinterpret_cast<f4*>(dst + r * ld + c) = x[u];
+  }
+}
+
+// ROWS x COLS fp32 values of a row-major global array (row stride src_ld)
 // into a split LDS tile with row stride ld, 16 bytes per access by NTH
 // threads: every load of a thread is issued before its first LDS write, so
 // the loads are in flight together rather than one round trip each.

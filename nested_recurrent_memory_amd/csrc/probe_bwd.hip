@@ -206,12 +206,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     }
   }
   // dvn staged for phases 4-5 (loads issued before the barrier)
-  if constexpr (DVN_LDS) {
-    for (int e = tid; e < N * V / 4; e += blockDim.x) {
-      const int n = e / (V / 4), c = (e % (V / 4)) * 4;
-      *reinterpret_cast<f4*>(s_dvn + n * LD + c) = *reinterpret_cast<const f4*>(dvn + (size_t)n * V + c);
-    }
-  }
+  if constexpr (DVN_LDS) stage_f32<512, N, V>(s_dvn, LD, dvn, V);
   lds_barrier();
 
   auto keyval = [&](int t, int rt, int r) -> float {
