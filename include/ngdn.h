@@ -118,7 +118,7 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
  * [B,ng[l],H,V,K] (from ngdn_upper_scan_fwd) with firing interval f[l];
  * entries at l = 0 are ignored. o [B,T,H,V] in the working dtype. read0, when
  * not NULL, receives level 0's unmixed read Qg h + Aqk Vn, fp32 [B,T,H,V]
- * (the backward's dmix_0). */
+ * (the backward's dmix_0). K != V only with L == 1. */
 int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const float* hT, const float* vnT, const void* q,
                         const void* mix, const float* const* statesT,
@@ -257,6 +257,39 @@ int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* 
                   const int32_t* n_queries, const void* query_banks, int32_t n_max,
                   const void* key_projections, const void* bpT, const void* wpT,
                   const void* gpT, float* ws, void* o, void* stream);
+
+/* ---- The layer around the op (NestedGDN2Attention, layers/nested_gdn2.py),
+ * which takes two modules from fla; these replace them. */
+
+/* fla's ShortConvolution with activation "silu" (layers/nested_gdn2.py:57-60,
+ * 122-130): per channel d, y[b,t,d] = act(sum_{i<W} w[d][i] x[b,t-(W-1)+i,d]),
+ * act = SiLU when act != 0. x, y [B,T,D] in dtype; w [D][W] fp32 (the
+ * module's weight [D,1,W]); rows before t = 0 come from cache_in (NULL:
+ * zeros). The cache has fla's layout, [B,D,W] in dtype, the last W inputs with
+ * the newest at index W-1; cache_out (NULL: not written, must not alias
+ * cache_in) receives the last W rows of [cache_in; x], the state the next
+ * call continues from. D % 8 == 0, 1 <= W <= 8. */
+int32_t ngdn_short_conv_fwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
+                            int32_t act, const void* x, const float* w, const void* cache_in,
+                            void* y, void* cache_out, void* stream);
+/* Its backward: dx [B,T,D] (dtype) written, dw [D][W] fp32 summed into
+ * (callers zero it). The gradient into cache_in is not formed. */
+int32_t ngdn_short_conv_bwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
+                            int32_t act, const void* x, const float* w, const void* cache_in,
+                            const void* dy, void* dx, float* dw, void* stream);
+
+/* fla's FusedRMSNormGated with activation "sigmoid" (layers/nested_gdn2.py:100,
+ * 236): per row of V values, y = x rstd w sigmoid(g), rstd = 1 / sqrt(mean(x^2)
+ * + eps). x, g, y [rows,V] in dtype; w [V] fp32; rstd [rows] fp32 written for
+ * the backward (NULL: not written). V in {64, 128, 256}. */
+int32_t ngdn_rmsnorm_gated_fwd(int32_t dtype, int64_t rows, int32_t V, float eps,
+                               const void* x, const void* g, const float* w, void* y,
+                               float* rstd, void* stream);
+/* Its backward from the forward's rstd: dx, dg [rows,V] (dtype) written, dw
+ * [V] fp32 summed into (callers zero it). */
+int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const void* x,
+                               const void* g, const float* w, const float* rstd,
+                               const void* dy, void* dx, void* dg, float* dw, void* stream);
 
 #ifdef __cplusplus
 }

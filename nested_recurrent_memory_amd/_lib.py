@@ -51,6 +51,10 @@ SIGNATURES = {
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
     "ngdn_step": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4 + [P, P, P],
+    "ngdn_short_conv_fwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P],
+    "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P],
+    "ngdn_rmsnorm_gated_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P, P],
+    "ngdn_rmsnorm_gated_bwd": [I32, I64, I32, P, P, P, P, P, P, P, P, P],
 }
 _RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}
 

@@ -168,8 +168,8 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         float* read0, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_output_fwd")) return r;
-  if (d->K != d->V)
-    return fail(NGDN_EINVAL, "ngdn_output_fwd: K == V required, got %d, %d", d->K, d->V);
+  if (d->L > 1 && d->K != d->V)
+    return fail(NGDN_EINVAL, "ngdn_output_fwd: upper levels need K == V, got %d, %d", d->K, d->V);
   if (!Qg || !Aqk || !hT || !vnT || !q || !mix || !o)
     return fail(NGDN_EINVAL, "ngdn_output_fwd: NULL tensor");
   ngdn::OutputArgs a{};
@@ -512,6 +512,62 @@ int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* 
     if (int32_t r = launched(ngdn::scan_fwd(ca, d->dtype, K, st), "ngdn_step (update)")) return r;
   }
   return NGDN_OK;
+}
+
+int32_t ngdn_short_conv_fwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
+                            int32_t act, const void* x, const float* w, const void* cache_in,
+                            void* y, void* cache_out, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_short_conv_fwd: dtype %d", dtype);
+  if (B < 0 || T < 0 || D <= 0 || D % 8 != 0 || W < 1 || W > 8)
+    return fail(NGDN_EINVAL, "ngdn_short_conv_fwd: B=%d T=%d D=%d W=%d (D a multiple of 8, 1 <= W <= 8)", B, T, D, W);
+  if ((B * T > 0 && (!x || !y)) || !w) return fail(NGDN_EINVAL, "ngdn_short_conv_fwd: NULL tensor");
+  ngdn::ShortConvArgs a{};
+  a.x = x; a.w = w; a.cache_in = cache_in; a.y = y; a.cache_out = cache_out;
+  a.B = B; a.T = T; a.D = D; a.W = W; a.act = act != 0;
+  return launched(ngdn::short_conv_fwd(a, dtype, (hipStream_t)stream), "ngdn_short_conv_fwd");
+}
+
+int32_t ngdn_short_conv_bwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
+                            int32_t act, const void* x, const float* w, const void* cache_in,
+                            const void* dy, void* dx, float* dw, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: dtype %d", dtype);
+  if (B < 0 || T < 0 || D <= 0 || D % 8 != 0 || W < 1 || W > 8)
+    return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: B=%d T=%d D=%d W=%d (D a multiple of 8, 1 <= W <= 8)", B, T, D, W);
+  if ((B * T > 0 && (!x || !dy || !dx)) || !w || !dw) return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: NULL tensor");
+  ngdn::ShortConvArgs a{};
+  a.x = x; a.w = w; a.cache_in = cache_in; a.dy = dy; a.dx = dx; a.dw = dw;
+  a.B = B; a.T = T; a.D = D; a.W = W; a.act = act != 0;
+  return launched(ngdn::short_conv_bwd(a, dtype, (hipStream_t)stream), "ngdn_short_conv_bwd");
+}
+
+int32_t ngdn_rmsnorm_gated_fwd(int32_t dtype, int64_t rows, int32_t V, float eps,
+                               const void* x, const void* g, const float* w, void* y,
+                               float* rstd, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_fwd: dtype %d", dtype);
+  if (rows < 0 || (V != 64 && V != 128 && V != 256))
+    return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_fwd: rows=%lld V=%d (V in 64, 128, 256)", (long long)rows, V);
+  if (rows > 0 && (!x || !g || !w || !y)) return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_fwd: NULL tensor");
+  ngdn::NormGatedArgs a{};
+  a.x = x; a.g = g; a.w = w; a.y = y; a.rstd = rstd; a.rows = rows; a.eps = eps;
+  return launched(ngdn::rmsnorm_gated_fwd(a, dtype, V, (hipStream_t)stream), "ngdn_rmsnorm_gated_fwd");
+}
+
+int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const void* x,
+                               const void* g, const float* w, const float* rstd,
+                               const void* dy, void* dx, void* dg, float* dw, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_bwd: dtype %d", dtype);
+  if (rows < 0 || (V != 64 && V != 128 && V != 256))
+    return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_bwd: rows=%lld V=%d (V in 64, 128, 256)", (long long)rows, V);
+  if (rows > 0 && (!x || !g || !w || !rstd || !dy || !dx || !dg || !dw))
+    return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_bwd: NULL tensor");
+  ngdn::NormGatedArgs a{};
+  a.x = x; a.g = g; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dg = dg;
+  a.dw = dw; a.rows = rows;
+  return launched(ngdn::rmsnorm_gated_bwd(a, dtype, V, (hipStream_t)stream), "ngdn_rmsnorm_gated_bwd");
 }
 
 }  // extern "C"

@@ -170,11 +170,14 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
     }
 #pragma unroll
     for (int J = 0; J < 3; ++J) {
-      const int rj = 16 * J + (lane & 15);   // below the sequence end whenever J < I
+      // rows of an earlier tile can still lie past the sequence end when this
+      // wave's own rows do (a partial last chunk): those read as zero
+      const int rj = 16 * J + (lane & 15);
+      const bool in_seq = J < I && rj < in.nvalid;
 #pragma unroll
       for (int s = 0; s < NKS; ++s) {
         const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-        kj[J][s] = J < I ? Mma<E>::ld(in.k + (size_t)(in.t0 + rj) * in.rowK + c0) : Mma<E>::zero();
+        kj[J][s] = in_seq ? Mma<E>::ld(in.k + (size_t)(in.t0 + rj) * in.rowK + c0) : Mma<E>::zero();
       }
     }
   }

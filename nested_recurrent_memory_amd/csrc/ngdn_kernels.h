@@ -153,6 +153,30 @@ struct PromoteArgs {
 };
 hipError_t promote_fwd(const PromoteArgs& a, int dtype, int K, hipStream_t st);
 
+// The layer's ShortConvolution (layer_ops.hip): x, y, dy, dx [B,T,D] and the
+// caches [B,W-1,D] in the working dtype, w and dw [D][W] fp32 (dw summed
+// into), act: SiLU after the convolution.
+struct ShortConvArgs {
+  const void* x; const float* w; const void* cache_in; void* y; void* cache_out;
+  const void* dy; void* dx; float* dw;
+  int B, T, D, W, act;
+  long long rows_per_block;
+};
+hipError_t short_conv_fwd(const ShortConvArgs& a, int dtype, hipStream_t st);
+hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st);
+
+// The layer's FusedRMSNormGated (layer_ops.hip) over rows of V: x, g, y, dy,
+// dx, dg in the working dtype; w and dw [V] fp32 (dw summed into); rstd
+// [rows] fp32 written by the forward for the backward.
+struct NormGatedArgs {
+  const void* x; const void* g; const float* w; void* y; float* rstd;
+  const void* dy; void* dx; void* dg; float* dw;
+  long long rows;
+  float eps;
+};
+hipError_t rmsnorm_gated_fwd(const NormGatedArgs& a, int dtype, int V, hipStream_t st);
+hipError_t rmsnorm_gated_bwd(const NormGatedArgs& a, int dtype, int V, hipStream_t st);
+
 // Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
 // the autograd replay of ops/chunk.py:339-371,486-517, derived in closed
 // form). One workgroup of 8 waves per (batch, head, firing i). Inputs: the

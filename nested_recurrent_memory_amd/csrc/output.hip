@@ -135,9 +135,9 @@ hipError_t output_fwd(const OutputArgs& a, int dtype, int K, int V, hipStream_t 
 #define NGDN_OU(E, KK, VV) \
   if (K == KK && V == VV) return launch_output<E, KK, VV>(a, st);
   if (dtype == NGDN_BF16) {
-    NGDN_OU(bf16, 64, 64) NGDN_OU(bf16, 128, 128)
+    NGDN_OU(bf16, 64, 64) NGDN_OU(bf16, 128, 128) NGDN_OU(bf16, 64, 128) NGDN_OU(bf16, 128, 64)
   } else {
-    NGDN_OU(float, 64, 64) NGDN_OU(float, 128, 128)
+    NGDN_OU(float, 64, 64) NGDN_OU(float, 128, 128) NGDN_OU(float, 64, 128) NGDN_OU(float, 128, 64)
   }
 #undef NGDN_OU
   return hipErrorInvalidValue;

@@ -1,0 +1,170 @@
+"""The two modules NestedGDN2Attention takes from fla
+(nested_gdn2/layers/nested_gdn2.py:17-18,57-60,100), on the HIP kernels of
+libngdn.so (csrc/layer_ops.hip, entry points in include/ngdn.h):
+
+* ``ShortConvolution``: causal depthwise convolution over time with a SiLU,
+  y[b,t,d] = silu(sum_{i<W} w[d,0,i] x[b,t-(W-1)+i,d]), as fla's module with
+  activation "silu" and no bias. Its cache is fla's: the last W inputs,
+  [B,D,W] with the newest last; a cache passed in is updated in place, as
+  fla's is, and returned when ``output_final_state``.
+* ``FusedRMSNormGated``: y = x / sqrt(mean(x^2) + eps) * weight * sigmoid(g)
+  over the last dimension, as fla's module with activation "sigmoid".
+
+Inputs in bfloat16 or float32 run on the kernels as they are; float16 runs in
+float32 and returns float16. There is no fallback: without the library (or
+on tensors off the GPU) the calls raise.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+__all__ = ["ShortConvolution", "FusedRMSNormGated", "short_conv", "rmsnorm_gated"]
+
+
+def _code(t):
+    return _lib.NGDN_BF16 if t.dtype == torch.bfloat16 else _lib.NGDN_F32
+
+
+def _work(t):
+    return t if t.dtype in (torch.bfloat16, torch.float32) else t.float()
+
+
+def _on_gpu(name, *ts):
+    # the kernels take raw device pointers: a host tensor must never reach them
+    dev = ts[0].device
+    for t in ts:
+        if t is not None and (not t.is_cuda or t.device != dev):
+            raise ValueError(f"{name}: every tensor must be on one GPU (got {t.device}); "
+                             "there is no CPU path")
+
+
+class _ShortConvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, cache, act, want_cache):
+        B, T, D = x.shape
+        W = weight.shape[-1]
+        xw = _work(x).contiguous()
+        w = weight.reshape(D, W).float().contiguous()
+        # a copy: the cache is updated in place below and the backward reads the old one
+        c = cache.to(xw.dtype, copy=True).contiguous() if cache is not None else None
+        y = torch.empty_like(xw)
+        new = xw.new_empty(B, D, W) if (want_cache or cache is not None) else None
+        _lib.call("ngdn_short_conv_fwd", _code(xw), B, T, D, W, int(act), _lib.ptr(xw),
+                  _lib.ptr(w), _lib.ptr(c), _lib.ptr(y), _lib.ptr(new), _lib.stream_of(xw))
+        ctx.save_for_backward(xw, w, c)
+        ctx.act, ctx.in_dtype, ctx.w_shape, ctx.w_dtype = act, x.dtype, weight.shape, weight.dtype
+        cache_out = None
+        if new is not None:
+            if cache is not None:          # fla updates a given cache in place
+                cache.copy_(new)
+                new = cache
+            if want_cache:
+                cache_out = new
+                ctx.mark_non_differentiable(cache_out)
+        return y.to(x.dtype), cache_out
+
+    @staticmethod
+    def backward(ctx, dy, _dcache):
+        xw, w, c = ctx.saved_tensors
+        B, T, D = xw.shape
+        W = w.shape[1]
+        dyw = dy.to(xw.dtype).contiguous()
+        dx = torch.empty_like(xw)
+        dw = torch.zeros(D, W, device=xw.device, dtype=torch.float32)
+        _lib.call("ngdn_short_conv_bwd", _code(xw), B, T, D, W, int(ctx.act), _lib.ptr(xw),
+                  _lib.ptr(w), _lib.ptr(c), _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dw),
+                  _lib.stream_of(xw))
+        return dx.to(ctx.in_dtype), dw.reshape(ctx.w_shape).to(ctx.w_dtype), None, None, None
+
+
+def short_conv(x, weight, cache=None, activation=True, output_final_state=False):
+    """x [B,T,D]; weight [D,1,W] (or [D,W]); cache [B,D,W] or None (updated
+    in place). Returns (y [B,T,D], the new cache [B,D,W] or None)."""
+    if x.dim() != 3:
+        raise ValueError(f"short_conv: x must be [B,T,D], got {tuple(x.shape)}")
+    if weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"short_conv: weight {tuple(weight.shape)} does not match D={x.shape[-1]}")
+    _on_gpu("short_conv", x, weight, cache)
+    W = weight.shape[-1]
+    if cache is not None and tuple(cache.shape) != (x.shape[0], x.shape[-1], W):
+        raise ValueError(f"short_conv: cache {tuple(cache.shape)}, expected "
+                         f"{(x.shape[0], x.shape[-1], W)} ([B,D,W])")
+    return _ShortConvFn.apply(x, weight, cache, bool(activation), bool(output_final_state))
+
+
+class _NormGatedFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, g, weight, eps):
+        V = x.shape[-1]
+        xw = _work(x).contiguous()
+        gw = g.to(xw.dtype).contiguous()
+        w = weight.float().contiguous()
+        rows = xw.numel() // V
+        y = torch.empty_like(xw)
+        rstd = torch.empty(rows, device=xw.device, dtype=torch.float32)
+        _lib.call("ngdn_rmsnorm_gated_fwd", _code(xw), rows, V, float(eps), _lib.ptr(xw),
+                  _lib.ptr(gw), _lib.ptr(w), _lib.ptr(y), _lib.ptr(rstd), _lib.stream_of(xw))
+        ctx.save_for_backward(xw, gw, w, rstd)
+        ctx.dtypes = (x.dtype, g.dtype, weight.dtype)
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        xw, gw, w, rstd = ctx.saved_tensors
+        V = xw.shape[-1]
+        rows = xw.numel() // V
+        dyw = dy.to(xw.dtype).contiguous()
+        dx, dg = torch.empty_like(xw), torch.empty_like(gw)
+        dw = torch.zeros(V, device=xw.device, dtype=torch.float32)
+        _lib.call("ngdn_rmsnorm_gated_bwd", _code(xw), rows, V, _lib.ptr(xw), _lib.ptr(gw),
+                  _lib.ptr(w), _lib.ptr(rstd), _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dg),
+                  _lib.ptr(dw), _lib.stream_of(xw))
+        xd, gd, wd = ctx.dtypes
+        return dx.to(xd), dg.to(gd), dw.to(wd), None
+
+
+def rmsnorm_gated(x, g, weight, eps=1e-5):
+    """x, g [..., V]; weight [V]. y = x rstd weight sigmoid(g)."""
+    if x.shape != g.shape or weight.shape != (x.shape[-1],):
+        raise ValueError(f"rmsnorm_gated: x {tuple(x.shape)}, g {tuple(g.shape)}, "
+                         f"weight {tuple(weight.shape)}")
+    _on_gpu("rmsnorm_gated", x, g, weight)
+    return _NormGatedFn.apply(x, g, weight, eps)
+
+
+class ShortConvolution(nn.Module):
+    """fla's ``ShortConvolution(hidden_size, kernel_size, activation="silu")``
+    (no bias): parameter ``weight`` [D,1,W] as nn.Conv1d holds it."""
+
+    def __init__(self, hidden_size, kernel_size, activation="silu", bias=False):
+        super().__init__()
+        if bias:
+            raise ValueError("ShortConvolution: bias is not supported (the layer builds it without)")
+        if activation not in ("silu", "swish", None):
+            raise ValueError(f"ShortConvolution: activation {activation!r}")
+        self.hidden_size, self.kernel_size = hidden_size, kernel_size
+        self.activation = activation
+        self.weight = nn.Parameter(torch.empty(hidden_size, 1, kernel_size))
+        nn.init.kaiming_uniform_(self.weight, a=5 ** 0.5)   # nn.Conv1d's default
+
+    def forward(self, x, cache=None, output_final_state=False):
+        return short_conv(x, self.weight, cache, self.activation is not None, output_final_state)
+
+
+class FusedRMSNormGated(nn.Module):
+    """fla's ``FusedRMSNormGated(hidden_size, activation="sigmoid", eps)``:
+    parameter ``weight`` [V] (ones at init)."""
+
+    def __init__(self, hidden_size, activation="sigmoid", eps=1e-5):
+        super().__init__()
+        if activation != "sigmoid":
+            raise ValueError(f"FusedRMSNormGated: activation {activation!r} (the layer uses sigmoid)")
+        self.hidden_size, self.eps = hidden_size, eps
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+
+    def forward(self, x, g):
+        return rmsnorm_gated(x, g, self.weight, self.eps)

@@ -83,10 +83,11 @@ def _check(ours, want, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("T,K", [(128, 64), (192, 128), (100, 64)])
-def test_level0_gradients(dtype, T, K):
-    print(f"level0 grads T={T} K={K} {dtype}", flush=True)
-    inp = make_inputs(B=2, T=T, H=2, K=K, V=K, L=1, N=16, intervals=(1,), dtype=dtype,
+@pytest.mark.parametrize("T,K,V", [(128, 64, 64), (192, 128, 128), (100, 64, 64),
+                                   (128, 64, 128), (100, 128, 64)])
+def test_level0_gradients(dtype, T, K, V):
+    print(f"level0 grads T={T} K={K} V={V} {dtype}", flush=True)
+    inp = make_inputs(B=2, T=T, H=2, K=K, V=V, L=1, N=16, intervals=(1,), dtype=dtype,
                       g_scale=1.0, style="reftest")
     ours, want = _run(inp, 1, "learned", dtype, with_dfinal=True)
     _check(ours, want, dtype)

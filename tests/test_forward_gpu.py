@@ -137,6 +137,59 @@ def test_forward_matches_oracle(B, T, H, K, L, N, firing, nq, promotion, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("K,V,T", [(64, 128, 192), (128, 64, 100)])
+def test_forward_single_level_k_ne_v(dtype, K, V, T):
+    """One level with value width != key width (the layer's expand_v != 1)."""
+    print(f"forward L=1 K={K} V={V} T={T} {dtype}", flush=True)
+    inp = make_inputs(B=2, T=T, H=2, K=K, V=V, L=1, N=16, intervals=(1,), dtype=dtype,
+                      g_scale=1.0, style="reftest")
+    gen = torch.Generator().manual_seed(9)
+    init = torch.randn(2, 2, 1, K, V, generator=gen) * 0.1
+    o, s = chunk_nested_gdn2(**_gpu(inp), L=1, initial_state=init.cuda(), output_final_state=True)
+    o_ref, s_ref = _oracle(inp, 1, init=init.double())
+    torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[dtype])
+    torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[dtype])
+
+
+def _nan_tailed(x):
+    """x on the GPU at the start of a buffer whose remaining 64 KiB hold NaN:
+    a kernel that reads past the end of the sequence picks them up."""
+    n = x.numel()
+    pad = 65536 // x.element_size()
+    buf = torch.full((n + pad,), float("nan"), dtype=x.dtype, device="cuda")
+    buf[:n].copy_(x.reshape(-1).cuda())
+    return buf[:n].view(x.shape)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("T,K", [(200, 64), (100, 128), (80, 64)])
+def test_partial_last_chunk_reads_nothing_past_the_end(dtype, T, K):
+    """Every input ends exactly at the sequence end (B=1) with NaN after it:
+    the forward and backward must not read past the last token."""
+    print(f"past-the-end T={T} K={K} {dtype}", flush=True)
+    inp = make_inputs(B=1, T=T, H=2, K=K, V=K, L=3, N=16, intervals=(1, 1, 2), dtype=dtype,
+                      g_scale=1.0, style="reftest")
+    leaves = ("q", "k", "v", "g", "b", "w", "mix_weights")
+    dev = {n: (_nan_tailed(inp[n]) if n in leaves else inp[n].cuda()) for n in NAMES}
+    for n in leaves:
+        dev[n].requires_grad_(True)
+    o, s = chunk_nested_gdn2(**dev, L=3, output_final_state=True)
+    o_ref, s_ref = _oracle(inp, 3)
+    torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[dtype])
+    torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[dtype])
+    # the backward over the same buffers gives what it gives on plain copies
+    do = torch.randn(o.shape, generator=torch.Generator().manual_seed(3)).to(o.dtype).cuda()
+    (o.float() * do.float()).sum().backward()
+    plain = {n: (inp[n].cuda().requires_grad_(True) if n in leaves else inp[n].cuda())
+             for n in NAMES}
+    o2, _ = chunk_nested_gdn2(**plain, L=3, output_final_state=True)
+    (o2.float() * do.float()).sum().backward()
+    for n in leaves:
+        assert torch.isfinite(dev[n].grad).all(), n
+        torch.testing.assert_close(dev[n].grad, plain[n].grad, **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 def test_forward_with_initial_state(dtype, promotion):
     inp = make_inputs(B=2, T=256, H=2, K=64, V=64, L=3, N=16, intervals=(1, 2, 4),
