@@ -281,6 +281,93 @@ def decode_bench(args):
     print(json.dumps(line))
 
 
+# config 4: the full model, 12 layers, hidden 1024, 8 heads of 128, 3 levels
+# firing every 1/4/16 chunks with 64 queries, SwiGLU 4096, vocab 32000
+MODEL = dict(vocab_size=32000, hidden_size=1024, num_hidden_layers=12, num_heads=8, head_dim=128,
+             num_levels=3, firing_intervals=(1, 4, 16), n_queries_per_level=(64, 64),
+             intermediate_size=4096)
+MODEL_BATCH = dict(B=8, T=4096)
+
+
+def model_bench(args):
+    """Tokens/s of one training step of NestedGDN2ForCausalLM at config 4:
+    forward with the fused loss, backward, gradient clipping at 1.0 and an
+    AdamW step, fp32 parameters under bf16 autocast (the reference's
+    training loop, train/pretrain.py:208-219), on uniform random token ids.
+    The roofline is the step's model flops (the GEMMs, 6 flops per weight per
+    token, plus the op's dense tile products) over the step time, against the
+    dense bf16 peak."""
+    from nested_recurrent_memory_amd.model import NestedGDN2Config, NestedGDN2ForCausalLM
+
+    cfg = NestedGDN2Config(**MODEL)
+    B, T = MODEL_BATCH["B"], MODEL_BATCH["T"]
+    torch.manual_seed(0)
+    model = NestedGDN2ForCausalLM(cfg).cuda().train()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                            fused=True)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=g, device="cuda")
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(input_ids=ids, labels=ids, use_cache=False).loss
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.TIMING = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timing, _lib.TIMING = _lib.TIMING, None
+    ms = elapsed / args.steps * 1e3
+    ours = {n: sum(a.elapsed_time(b) for a, b in evs) / args.steps for n, evs in timing.items()}
+
+    linear = sum(m.weight.numel() for m in model.modules() if isinstance(m, torch.nn.Linear))
+    opcfg = dict(B=B, T=T, H=cfg.num_heads, K=cfg.head_dim, V=cfg.head_dim, L=cfg.num_levels,
+                 N=cfg.n_queries_per_level[0], intervals=cfg.firing_intervals, dtype=torch.bfloat16)
+    op_flops = sum(fl for _, fl in work_model(opcfg)[0].values()) * cfg.num_hidden_layers
+    flops = 6 * linear * B * T + op_flops
+    tflops = flops / (ms * 1e-3) / 1e12
+    if args.kernel_table:
+        for n, t in sorted(ours.items(), key=lambda kv: -kv[1]):
+            print(f"{n:32s} {t:8.3f} ms/step", file=sys.stderr)
+    line = {
+        "metric": "tokens/s training step NestedGDN2ForCausalLM (config 4)",
+        "value": round(B * T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "model: NestedGDN2ForCausalLM fwd (fused loss) + bwd + clip + "
+                               "AdamW, fp32 params under bf16 autocast",
+                   "B": B, "T": T, **{k: (list(v) if isinstance(v, tuple) else v)
+                                      for k, v in MODEL.items()},
+                   "params": sum(p.numel() for p in model.parameters()),
+                   "loss": round(float(loss.detach()), 4)},
+        "roofline": {"kernel": "whole step (hipBLASLt GEMMs + this library's kernels)",
+                     "bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_TFLOPS, 4),
+                     "traffic": None, "flops_per_step": flops,
+                     "library_kernels_ms": round(sum(ours.values()), 3)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -290,9 +377,10 @@ def main():
     ap.add_argument("--stream-groups", type=int, default=None,
                     help="groups of batch rows run on their own streams (default: the "
                          "package's STREAM_GROUPS)")
-    ap.add_argument("--workload", default="train", choices=("train", "decode"),
+    ap.add_argument("--workload", default="train", choices=("train", "decode", "model"),
                     help="train: forward+backward at --config (the headline); "
-                         "decode: the decoding step")
+                         "decode: the decoding step; model: a training step of the "
+                         "model at config 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-table", action="store_true",
                     help="also print per-entry-point times to stderr")
@@ -307,6 +395,9 @@ def main():
         _chunk.STREAM_GROUPS = args.stream_groups
     if args.workload == "decode":
         decode_bench(args)
+        return
+    if args.workload == "model":
+        model_bench(args)
         return
 
     cfg = dict(CONFIGS[args.config])

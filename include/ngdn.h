@@ -291,6 +291,42 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
                                const void* g, const float* w, const float* rstd,
                                const void* dy, void* dx, void* dg, float* dw, void* stream);
 
+/* ---- The model around the layer (NestedGDN2ForCausalLM,
+ * models/modeling_nested_gdn2.py), which takes three more modules from fla;
+ * these replace their kernels (the linear maps stay GEMMs of the caller). */
+
+/* fla's RMSNorm (models/modeling_nested_gdn2.py:16,46-49,97-99): per row of D
+ * values, y = x rstd w, rstd = 1 / sqrt(mean(x^2) + eps). x, y [rows,D] in
+ * dtype; w [D] fp32; rstd [rows] fp32 written for the backward (NULL: not
+ * written). D = 512 n for n in 1..6, or D in {64, 128, 256, 768}. */
+int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, const void* x,
+                         const float* w, void* y, float* rstd, void* stream);
+/* Its backward from the forward's rstd: dx [rows,D] (dtype) written, dw [D]
+ * fp32 summed into (callers zero it). */
+int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, const float* w,
+                         const float* rstd, const void* dy, void* dx, float* dw, void* stream);
+
+/* The SwiGLU of fla's GatedMLP (models/modeling_nested_gdn2.py:17,50-56):
+ * y = silu(g) u elementwise over n values (n % 8 == 0), all in dtype. */
+int32_t ngdn_swiglu_fwd(int32_t dtype, int64_t n, const void* g, const void* u, void* y, void* stream);
+/* Its backward: dg = dy u silu'(g), du = dy silu(g). */
+int32_t ngdn_swiglu_bwd(int32_t dtype, int64_t n, const void* g, const void* u, const void* dy,
+                        void* dg, void* du, void* stream);
+
+/* The cross entropy of fla's FusedLinearCrossEntropyLoss
+ * (models/modeling_nested_gdn2.py:230-239; mean over the labels that are not
+ * ignore_index): row_loss[r] = (logsumexp(logits_r) - logits_r[labels_r]) /
+ * n_valid, 0 where labels_r == ignore_index (row_loss fp32 [rows]; the loss is
+ * their sum). n_valid points to the device int64 count of labels that are not
+ * ignore_index. With grad != 0 the logits [rows,V] (dtype) are overwritten by
+ * d(loss)/d(logits) = (softmax - onehot) / n_valid, zeros on ignored rows.
+ * A label outside [0, V) that is not ignore_index gives NaN on its row, and
+ * n_valid == 0 gives NaN (the mean over no labels).
+ * V % 8 == 0, V <= 65536. */
+int32_t ngdn_cross_entropy(int32_t dtype, int64_t rows, int32_t V, int32_t ignore_index,
+                           void* logits, const int64_t* labels, const int64_t* n_valid,
+                           float* row_loss, int32_t grad, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

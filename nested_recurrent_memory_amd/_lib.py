@@ -55,6 +55,11 @@ SIGNATURES = {
     "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_bwd": [I32, I64, I32, P, P, P, P, P, P, P, P, P],
+    "ngdn_rmsnorm_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P],
+    "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 7,
+    "ngdn_swiglu_fwd": [I32, I64] + [P] * 4,
+    "ngdn_swiglu_bwd": [I32, I64] + [P] * 6,
+    "ngdn_cross_entropy": [I32, I64, I32, I32, P, P, P, P, I32, P],
 }
 _RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}
 

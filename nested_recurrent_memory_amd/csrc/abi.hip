@@ -570,4 +570,68 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
   return launched(ngdn::rmsnorm_gated_bwd(a, dtype, V, (hipStream_t)stream), "ngdn_rmsnorm_gated_bwd");
 }
 
+int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, const void* x,
+                         const float* w, void* y, float* rstd, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_fwd: dtype %d", dtype);
+  if (rows < 0 || !ngdn::rmsnorm_supported(D))
+    return fail(NGDN_EINVAL, "ngdn_rmsnorm_fwd: rows=%lld D=%d (D = 512 n for n in 1..6, or 64, 128, 256, 768)",
+                (long long)rows, D);
+  if (rows > 0 && (!x || !w || !y)) return fail(NGDN_EINVAL, "ngdn_rmsnorm_fwd: NULL tensor");
+  ngdn::RMSNormArgs a{};
+  a.x = x; a.w = w; a.y = y; a.rstd = rstd; a.rows = rows; a.D = D; a.eps = eps;
+  return launched(ngdn::rmsnorm_fwd(a, dtype, (hipStream_t)stream), "ngdn_rmsnorm_fwd");
+}
+
+int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, const float* w,
+                         const float* rstd, const void* dy, void* dx, float* dw, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_bwd: dtype %d", dtype);
+  if (rows < 0 || !ngdn::rmsnorm_supported(D))
+    return fail(NGDN_EINVAL, "ngdn_rmsnorm_bwd: rows=%lld D=%d unsupported", (long long)rows, D);
+  if (rows > 0 && (!x || !w || !rstd || !dy || !dx || !dw)) return fail(NGDN_EINVAL, "ngdn_rmsnorm_bwd: NULL tensor");
+  ngdn::RMSNormArgs a{};
+  a.x = x; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dw = dw;
+  a.rows = rows; a.D = D;
+  return launched(ngdn::rmsnorm_bwd(a, dtype, (hipStream_t)stream), "ngdn_rmsnorm_bwd");
+}
+
+int32_t ngdn_swiglu_fwd(int32_t dtype, int64_t n, const void* g, const void* u, void* y, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_swiglu_fwd: dtype %d", dtype);
+  if (n < 0 || n % 8 != 0) return fail(NGDN_EINVAL, "ngdn_swiglu_fwd: n=%lld (a multiple of 8)", (long long)n);
+  if (n > 0 && (!g || !u || !y)) return fail(NGDN_EINVAL, "ngdn_swiglu_fwd: NULL tensor");
+  ngdn::SwigluArgs a{};
+  a.g = g; a.u = u; a.y = y; a.n = n;
+  return launched(ngdn::swiglu_fwd(a, dtype, (hipStream_t)stream), "ngdn_swiglu_fwd");
+}
+
+int32_t ngdn_swiglu_bwd(int32_t dtype, int64_t n, const void* g, const void* u, const void* dy,
+                        void* dg, void* du, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_swiglu_bwd: dtype %d", dtype);
+  if (n < 0 || n % 8 != 0) return fail(NGDN_EINVAL, "ngdn_swiglu_bwd: n=%lld (a multiple of 8)", (long long)n);
+  if (n > 0 && (!g || !u || !dy || !dg || !du)) return fail(NGDN_EINVAL, "ngdn_swiglu_bwd: NULL tensor");
+  ngdn::SwigluArgs a{};
+  a.g = g; a.u = u; a.dy = dy; a.dg = dg; a.du = du; a.n = n;
+  return launched(ngdn::swiglu_bwd(a, dtype, (hipStream_t)stream), "ngdn_swiglu_bwd");
+}
+
+int32_t ngdn_cross_entropy(int32_t dtype, int64_t rows, int32_t V, int32_t ignore_index,
+                           void* logits, const int64_t* labels, const int64_t* n_valid,
+                           float* row_loss, int32_t grad, void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_cross_entropy: dtype %d", dtype);
+  if (rows < 0 || !ngdn::xent_supported(V))
+    return fail(NGDN_EINVAL, "ngdn_cross_entropy: rows=%lld V=%d (V a multiple of 8, at most 65536)",
+                (long long)rows, V);
+  if (rows > 0 && (!logits || !labels || !n_valid || !row_loss))
+    return fail(NGDN_EINVAL, "ngdn_cross_entropy: NULL tensor");
+  ngdn::XentArgs a{};
+  a.logits = logits; a.labels = reinterpret_cast<const long long*>(labels);
+  a.n_valid = reinterpret_cast<const long long*>(n_valid); a.row_loss = row_loss;
+  a.rows = rows; a.V = V; a.ignore_index = ignore_index; a.grad = grad != 0;
+  return launched(ngdn::cross_entropy(a, dtype, (hipStream_t)stream), "ngdn_cross_entropy");
+}
+
 }  // extern "C"

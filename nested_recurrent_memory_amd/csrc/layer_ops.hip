@@ -23,41 +23,12 @@ __device__ __forceinline__ float dsilu_(float a) {
   return s * (1.f + a * (1.f - s));
 }
 
-// 8 consecutive elements as floats (two 16-byte loads for fp32)
-template <typename E>
-__device__ __forceinline__ void load8(const E* p, float* out) {
-  if constexpr (std::is_same<E, float>::value) {
-    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { out[e] = a[e]; out[4 + e] = b[e]; }
-  } else {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
-  }
-}
-template <typename E>
-__device__ __forceinline__ void store8(E* p, const float* x) {
-  if constexpr (std::is_same<E, float>::value) {
-    f4 a, b;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { a[e] = x[e]; b[e] = x[4 + e]; }
-    *reinterpret_cast<f4*>(p) = a;
-    *reinterpret_cast<f4*>(p + 4) = b;
-  } else {
-    bf16x8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (bf16)x[e];
-    *reinterpret_cast<bf16x8*>(p) = v;
-  }
-}
-
 // input row s of batch b, channels d..d+7. Rows s < 0 (down to -W) come from
 // the cache, [B][D][W] with the newest input last (entry W + s), or are zero.
 template <typename E>
 __device__ __forceinline__ void conv_row(const ShortConvArgs& a, int b, int s, int d, float* out) {
   if (s >= 0) {
-    load8(static_cast<const E*>(a.x) + ((size_t)b * a.T + s) * a.D + d, out);
+    load8f(static_cast<const E*>(a.x) + ((size_t)b * a.T + s) * a.D + d, out);
   } else if (a.cache_in) {
     const E* c = static_cast<const E*>(a.cache_in) + ((size_t)b * a.D + d) * a.W + (a.W + s);
 #pragma unroll
@@ -94,7 +65,7 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(ShortConvArgs a) {
   float y[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) y[c] = a.act ? silu_(acc[c]) : acc[c];
-  store8(static_cast<E*>(a.y) + ((size_t)b * a.T + t) * a.D + d, y);
+  store8f(static_cast<E*>(a.y) + ((size_t)b * a.T + t) * a.D + d, y);
 }
 
 template <typename E>
@@ -157,7 +128,7 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvArgs a) {
       for (int u = 0; u < W; ++u) {
         if (t + u >= a.T) continue;
         float dy[8];
-        load8(static_cast<const E*>(a.dy) + ((size_t)b * a.T + t + u) * a.D + d, dy);
+        load8f(static_cast<const E*>(a.dy) + ((size_t)b * a.T + t + u) * a.D + d, dy);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           float pre = 0.f;
@@ -172,7 +143,7 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvArgs a) {
           }
         }
       }
-      store8(static_cast<E*>(a.dx) + ((size_t)b * a.T + t) * a.D + d, dx);
+      store8f(static_cast<E*>(a.dx) + ((size_t)b * a.T + t) * a.D + d, dx);
     }
   }
 #pragma unroll
@@ -245,8 +216,8 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_fwd_kernel(NormGatedArgs a)
   const bool live = row < a.rows;
   float x[8], g[8];
   if (live) {
-    load8(static_cast<const E*>(a.x) + row * V + c, x);
-    load8(static_cast<const E*>(a.g) + row * V + c, g);
+    load8f(static_cast<const E*>(a.x) + row * V + c, x);
+    load8f(static_cast<const E*>(a.g) + row * V + c, g);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
@@ -261,7 +232,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_fwd_kernel(NormGatedArgs a)
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = x[e] * rstd * a.w[c + e] / (1.f + expf(-g[e]));
-  store8(static_cast<E*>(a.y) + row * V + c, y);
+  store8f(static_cast<E*>(a.y) + row * V + c, y);
   if (a.rstd && c == 0) a.rstd[row] = rstd;
 }
 
@@ -277,9 +248,9 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_bwd_kernel(NormGatedArgs a)
   for (int e = 0; e < 8; ++e) dw[e] = 0.f;
   for (long long row = (long long)blockIdx.x * RPB + rs; row < a.rows; row += (long long)gridDim.x * RPB) {
     float x[8], g[8], dy[8];
-    load8(static_cast<const E*>(a.x) + row * V + c, x);
-    load8(static_cast<const E*>(a.g) + row * V + c, g);
-    load8(static_cast<const E*>(a.dy) + row * V + c, dy);
+    load8f(static_cast<const E*>(a.x) + row * V + c, x);
+    load8f(static_cast<const E*>(a.g) + row * V + c, g);
+    load8f(static_cast<const E*>(a.dy) + row * V + c, dy);
     const float rstd = a.rstd[row];
     float xh[8], s[8], dxh[8], dot = 0.f;
 #pragma unroll
@@ -299,8 +270,8 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_bwd_kernel(NormGatedArgs a)
       dx[e] = rstd * (dxh[e] - xh[e] * mean);
       dg[e] = dy[e] * xh[e] * a.w[c + e] * s[e] * (1.f - s[e]);
     }
-    store8(static_cast<E*>(a.dx) + row * V + c, dx);
-    store8(static_cast<E*>(a.dg) + row * V + c, dg);
+    store8f(static_cast<E*>(a.dx) + row * V + c, dx);
+    store8f(static_cast<E*>(a.dg) + row * V + c, dg);
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) s_dw[rs][c + e] = dw[e];

@@ -238,6 +238,35 @@ __device__ __forceinline__ void ld_raw(const float* p, float* out) {
   }
 }
 
+// 8 consecutive elements as floats (two 16-byte loads for fp32)
+template <typename E>
+__device__ __forceinline__ void load8f(const E* p, float* out) {
+  if constexpr (std::is_same<E, float>::value) {
+    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { out[e] = a[e]; out[4 + e] = b[e]; }
+  } else {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+  }
+}
+template <typename E>
+__device__ __forceinline__ void store8f(E* p, const float* x) {
+  if constexpr (std::is_same<E, float>::value) {
+    f4 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { a[e] = x[e]; b[e] = x[4 + e]; }
+    *reinterpret_cast<f4*>(p) = a;
+    *reinterpret_cast<f4*>(p + 4) = b;
+  } else {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)x[e];
+    *reinterpret_cast<bf16x8*>(p) = v;
+  }
+}
+
 // A workgroup barrier that orders LDS only: global stores issued before it
 // need not have completed (__syncthreads waits for every outstanding store).
 // Global data exchanged between the waves of a workgroup needs __syncthreads.

@@ -154,7 +154,7 @@ struct PromoteArgs {
 hipError_t promote_fwd(const PromoteArgs& a, int dtype, int K, hipStream_t st);
 
 // The layer's ShortConvolution (layer_ops.hip): x, y, dy, dx [B,T,D] and the
-// caches [B,W-1,D] in the working dtype, w and dw [D][W] fp32 (dw summed
+// caches [B,D,W] in the working dtype, w and dw [D][W] fp32 (dw summed
 // into), act: SiLU after the convolution.
 struct ShortConvArgs {
   const void* x; const float* w; const void* cache_in; void* y; void* cache_out;
@@ -176,6 +176,43 @@ struct NormGatedArgs {
 };
 hipError_t rmsnorm_gated_fwd(const NormGatedArgs& a, int dtype, int V, hipStream_t st);
 hipError_t rmsnorm_gated_bwd(const NormGatedArgs& a, int dtype, int V, hipStream_t st);
+
+// The model's RMSNorm (model_ops.hip) over rows of D: x, y, dy, dx in the
+// working dtype; w and dw [D] fp32 (dw summed into); rstd [rows] fp32 written
+// by the forward for the backward.
+struct RMSNormArgs {
+  const void* x; const float* w; void* y; float* rstd;
+  const void* dy; void* dx; float* dw;
+  long long rows;
+  int D;
+  float eps;
+};
+bool rmsnorm_supported(int D);
+hipError_t rmsnorm_fwd(const RMSNormArgs& a, int dtype, hipStream_t st);
+hipError_t rmsnorm_bwd(const RMSNormArgs& a, int dtype, hipStream_t st);
+
+// The MLP's SwiGLU (model_ops.hip): y = silu(g) u over n values, n % 8 == 0,
+// all in the working dtype.
+struct SwigluArgs {
+  const void* g; const void* u; void* y;
+  const void* dy; void* dg; void* du;
+  long long n;
+};
+hipError_t swiglu_fwd(const SwigluArgs& a, int dtype, hipStream_t st);
+hipError_t swiglu_bwd(const SwigluArgs& a, int dtype, hipStream_t st);
+
+// Cross entropy of rows of V logits (model_ops.hip): row_loss[r] =
+// (logsumexp(x_r) - x_r[label_r]) / n_valid, 0 for ignored labels; with grad
+// the logits are overwritten by d(sum of row_loss)/dx = (softmax - onehot) /
+// n_valid (zeros on ignored rows). n_valid: device int64, the count of labels
+// that are not ignore_index.
+struct XentArgs {
+  void* logits; const long long* labels; const long long* n_valid; float* row_loss;
+  long long rows;
+  int V, ignore_index, grad;
+};
+bool xent_supported(int V);
+hipError_t cross_entropy(const XentArgs& a, int dtype, hipStream_t st);
 
 // Backward of one level's firings (update: ops/update_bwd.py:115-158; probe:
 // the autograd replay of ops/chunk.py:339-371,486-517, derived in closed

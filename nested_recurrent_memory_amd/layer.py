@@ -158,7 +158,7 @@ class NestedGDN2Attention(nn.Module):
         mix_logits = self.mix_proj(x).reshape(B, T, H, L)
         gated = cfg.read_mix == "sigmoid"
         mix = (mix_logits.sigmoid() if gated else mix_logits.softmax(-1)).to(v.dtype)
-        keep = cfg.read_levels
+        keep = getattr(cfg, "read_levels", None)   # eval-time read ablation (not a config field)
         if keep is not None:
             masked = torch.zeros_like(mix)
             masked[..., list(keep)] = mix[..., list(keep)]
