@@ -38,6 +38,10 @@ extern "C" {
 #define NGDN_F32 0
 #define NGDN_BF16 1
 
+/* rows of per-workgroup partial sums in the ws argument of the layer/model
+ * backward entry points ([NGDN_WPARTS][n] fp32, n the weight's size) */
+#define NGDN_WPARTS 1024
+
 typedef struct ngdn_dims {
   int32_t B, T, H, L, K, V;
   int32_t dtype;
@@ -273,10 +277,13 @@ int32_t ngdn_short_conv_fwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int3
                             int32_t act, const void* x, const float* w, const void* cache_in,
                             void* y, void* cache_out, void* stream);
 /* Its backward: dx [B,T,D] (dtype) written, dw [D][W] fp32 summed into
- * (callers zero it). The gradient into cache_in is not formed. */
+ * (callers zero it). The gradient into cache_in is not formed. ws: fp32
+ * [NGDN_WPARTS][D*W] (no initial contents needed) for the per-workgroup
+ * partial sums of dw, added into dw by a second pass; or NULL to add every
+ * partial into dw with device-scope atomics (several times slower). */
 int32_t ngdn_short_conv_bwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
                             int32_t act, const void* x, const float* w, const void* cache_in,
-                            const void* dy, void* dx, float* dw, void* stream);
+                            const void* dy, void* dx, float* dw, float* ws, void* stream);
 
 /* fla's FusedRMSNormGated with activation "sigmoid" (layers/nested_gdn2.py:100,
  * 236): per row of V values, y = x rstd w sigmoid(g), rstd = 1 / sqrt(mean(x^2)
@@ -286,10 +293,12 @@ int32_t ngdn_rmsnorm_gated_fwd(int32_t dtype, int64_t rows, int32_t V, float eps
                                const void* x, const void* g, const float* w, void* y,
                                float* rstd, void* stream);
 /* Its backward from the forward's rstd: dx, dg [rows,V] (dtype) written, dw
- * [V] fp32 summed into (callers zero it). */
+ * [V] fp32 summed into (callers zero it); ws fp32 [NGDN_WPARTS][V] or NULL
+ * (as for ngdn_short_conv_bwd). */
 int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const void* x,
                                const void* g, const float* w, const float* rstd,
-                               const void* dy, void* dx, void* dg, float* dw, void* stream);
+                               const void* dy, void* dx, void* dg, float* dw, float* ws,
+                               void* stream);
 
 /* ---- The model around the layer (NestedGDN2ForCausalLM,
  * models/modeling_nested_gdn2.py), which takes three more modules from fla;
@@ -302,9 +311,11 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
 int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, const void* x,
                          const float* w, void* y, float* rstd, void* stream);
 /* Its backward from the forward's rstd: dx [rows,D] (dtype) written, dw [D]
- * fp32 summed into (callers zero it). */
+ * fp32 summed into (callers zero it); ws fp32 [NGDN_WPARTS][D] or NULL (as
+ * for ngdn_short_conv_bwd). */
 int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, const float* w,
-                         const float* rstd, const void* dy, void* dx, float* dw, void* stream);
+                         const float* rstd, const void* dy, void* dx, float* dw, float* ws,
+                         void* stream);
 
 /* The SwiGLU of fla's GatedMLP (models/modeling_nested_gdn2.py:17,50-56):
  * y = silu(g) u elementwise over n values (n % 8 == 0), all in dtype. */

@@ -28,6 +28,7 @@ class Dims(ctypes.Structure):
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
 I64 = ctypes.c_int64
+WPARTS = 1024         # NGDN_WPARTS: rows of partial weight-gradient sums in the ws arguments
 PD = ctypes.POINTER(Dims)
 
 # name -> argtypes (all return an int32 status unless listed in _RESTYPES)
@@ -52,11 +53,11 @@ SIGNATURES = {
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
     "ngdn_step": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4 + [P, P, P],
     "ngdn_short_conv_fwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P],
-    "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P],
+    "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P, P],
-    "ngdn_rmsnorm_gated_bwd": [I32, I64, I32, P, P, P, P, P, P, P, P, P],
+    "ngdn_rmsnorm_gated_bwd": [I32, I64, I32, P, P, P, P, P, P, P, P, P, P],
     "ngdn_rmsnorm_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P],
-    "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 7,
+    "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 8,
     "ngdn_swiglu_fwd": [I32, I64] + [P] * 4,
     "ngdn_swiglu_bwd": [I32, I64] + [P] * 6,
     "ngdn_cross_entropy": [I32, I64, I32, I32, P, P, P, P, I32, P],

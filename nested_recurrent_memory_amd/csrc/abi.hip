@@ -530,14 +530,14 @@ int32_t ngdn_short_conv_fwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int3
 
 int32_t ngdn_short_conv_bwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,
                             int32_t act, const void* x, const float* w, const void* cache_in,
-                            const void* dy, void* dx, float* dw, void* stream) {
+                            const void* dy, void* dx, float* dw, float* ws, void* stream) {
   g_err[0] = 0;
   if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: dtype %d", dtype);
   if (B < 0 || T < 0 || D <= 0 || D % 8 != 0 || W < 1 || W > 8)
     return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: B=%d T=%d D=%d W=%d (D a multiple of 8, 1 <= W <= 8)", B, T, D, W);
   if ((B * T > 0 && (!x || !dy || !dx)) || !w || !dw) return fail(NGDN_EINVAL, "ngdn_short_conv_bwd: NULL tensor");
   ngdn::ShortConvArgs a{};
-  a.x = x; a.w = w; a.cache_in = cache_in; a.dy = dy; a.dx = dx; a.dw = dw;
+  a.x = x; a.w = w; a.cache_in = cache_in; a.dy = dy; a.dx = dx; a.dw = dw; a.ws = ws;
   a.B = B; a.T = T; a.D = D; a.W = W; a.act = act != 0;
   return launched(ngdn::short_conv_bwd(a, dtype, (hipStream_t)stream), "ngdn_short_conv_bwd");
 }
@@ -557,7 +557,8 @@ int32_t ngdn_rmsnorm_gated_fwd(int32_t dtype, int64_t rows, int32_t V, float eps
 
 int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const void* x,
                                const void* g, const float* w, const float* rstd,
-                               const void* dy, void* dx, void* dg, float* dw, void* stream) {
+                               const void* dy, void* dx, void* dg, float* dw, float* ws,
+                               void* stream) {
   g_err[0] = 0;
   if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_bwd: dtype %d", dtype);
   if (rows < 0 || (V != 64 && V != 128 && V != 256))
@@ -566,7 +567,7 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
     return fail(NGDN_EINVAL, "ngdn_rmsnorm_gated_bwd: NULL tensor");
   ngdn::NormGatedArgs a{};
   a.x = x; a.g = g; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dg = dg;
-  a.dw = dw; a.rows = rows;
+  a.dw = dw; a.ws = ws; a.rows = rows;
   return launched(ngdn::rmsnorm_gated_bwd(a, dtype, V, (hipStream_t)stream), "ngdn_rmsnorm_gated_bwd");
 }
 
@@ -584,7 +585,8 @@ int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, cons
 }
 
 int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, const float* w,
-                         const float* rstd, const void* dy, void* dx, float* dw, void* stream) {
+                         const float* rstd, const void* dy, void* dx, float* dw, float* ws,
+                         void* stream) {
   g_err[0] = 0;
   if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_rmsnorm_bwd: dtype %d", dtype);
   if (rows < 0 || !ngdn::rmsnorm_supported(D))
@@ -592,7 +594,7 @@ int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, 
   if (rows > 0 && (!x || !w || !rstd || !dy || !dx || !dw)) return fail(NGDN_EINVAL, "ngdn_rmsnorm_bwd: NULL tensor");
   ngdn::RMSNormArgs a{};
   a.x = x; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dw = dw;
-  a.rows = rows; a.D = D;
+  a.ws = ws; a.rows = rows; a.D = D;
   return launched(ngdn::rmsnorm_bwd(a, dtype, (hipStream_t)stream), "ngdn_rmsnorm_bwd");
 }
 

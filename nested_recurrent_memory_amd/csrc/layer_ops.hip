@@ -17,9 +17,9 @@ namespace ngdn {
 
 namespace {
 
-__device__ __forceinline__ float silu_(float a) { return a / (1.f + expf(-a)); }
+__device__ __forceinline__ float silu_(float a) { return a * sigmoid_fast(a); }
 __device__ __forceinline__ float dsilu_(float a) {
-  const float s = 1.f / (1.f + expf(-a));
+  const float s = sigmoid_fast(a);
   return s * (1.f + a * (1.f - s));
 }
 
@@ -39,33 +39,107 @@ __device__ __forceinline__ void conv_row(const ShortConvArgs& a, int b, int s, i
   }
 }
 
+// N (4 or 8) consecutive values of a row as loaded (bf16: 8 or 16 bytes in
+// 2 or 4 registers; fp32: one or two 16-byte quads), converted to float where
+// used, so that rows held for a whole time block cost half the registers in
+// bf16
+template <typename E, int N> struct Raw;
+template <int N> struct Raw<bf16, N> {
+  typedef __attribute__((__vector_size__(N * sizeof(bf16)))) bf16 V;
+  V v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const V*>(p); }
+  __device__ __forceinline__ float operator[](int e) const { return (float)v[e]; }
+  __device__ __forceinline__ void set(int e, float x) { v[e] = (bf16)x; }
+  __device__ __forceinline__ void store(bf16* p) const { *reinterpret_cast<V*>(p) = v; }
+};
+template <int N> struct Raw<float, N> {
+  f4 q[N / 4];
+  __device__ __forceinline__ void load(const float* p) {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) q[j] = *reinterpret_cast<const f4*>(p + 4 * j);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return q[e / 4][e % 4]; }
+  __device__ __forceinline__ void set(int e, float x) { q[e / 4][e % 4] = x; }
+  __device__ __forceinline__ void store(float* p) const {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) *reinterpret_cast<f4*>(p + 4 * j) = q[j];
+  }
+};
+
+// input row s of batch b, channels d..d+N-1, into a raw row: rows s < 0 (down
+// to -W) from the cache ([B][D][W], entry W + s) or zeros, rows past the end
+// of the sequence zeros
+template <typename E, int N>
+__device__ __forceinline__ void conv_raw(const ShortConvArgs& a, int b, int s, int d, Raw<E, N>& out) {
+  if (s >= 0 && s < a.T) {
+    out.load(static_cast<const E*>(a.x) + ((size_t)b * a.T + s) * a.D + d);
+  } else if (s < 0 && a.cache_in) {
+    const E* c = static_cast<const E*>(a.cache_in) + ((size_t)b * a.D + d) * a.W + (a.W + s);
+#pragma unroll
+    for (int e = 0; e < N; ++e) out.set(e, (float)c[(size_t)e * a.W]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out.set(e, 0.f);
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- ShortConvolution
 
+// Work split of both kernels: a thread owns one group of CPT channels over
+// RT consecutive time steps of one sequence (a "time block"); a workgroup is
+// 64 channel groups (consecutive threads, so each row access of a wave is
+// contiguous) by 4 time-block slots. The taps of the thread's channels are
+// loaded once (CPT W fp32, contiguous) and the W - 1 rows before the block
+// are the only rows read twice. The forward holds 8 channels, the backward
+// (which keeps more rows live) 4.
+constexpr int SC_CG = 64, SC_SLOTS = 4;
+
+template <typename E> struct ScRT { static constexpr int f = sizeof(E) == 2 ? 8 : 4, b = sizeof(E) == 2 ? 8 : 4; };
+constexpr int SC_CPT_F = 8, SC_CPT_B = 4;
+
+template <int CPT, int W>
+__device__ __forceinline__ void load_taps(const float* w, int d, float (&tw)[CPT][W]) {
+  const f4* p = reinterpret_cast<const f4*>(w + (size_t)d * W);   // 4 CPT W bytes, 16-byte aligned
+#pragma unroll
+  for (int j = 0; j < CPT * W / 4; ++j) {
+    const f4 v = p[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int f = 4 * j + e;
+      tw[f / W][f % W] = v[e];
+    }
+  }
+}
+
 template <typename E, int W>
 __global__ __launch_bounds__(256) void short_conv_fwd_kernel(ShortConvArgs a) {
-  // thread: 8 channels of one (b, t); the W input rows are 16-byte loads
-  const int D8 = a.D / 8;
-  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (e >= (long long)a.B * a.T * D8) return;
-  const int d = (int)(e % D8) * 8;
-  const long long bt = e / D8;
-  const int t = (int)(bt % a.T), b = (int)(bt / a.T);
-  float acc[8];
+  constexpr int RT = ScRT<E>::f, CPT = SC_CPT_F;
+  const int DG = a.D / CPT, NTB = (a.T + RT - 1) / RT;
+  const int ctiles = (DG + SC_CG - 1) / SC_CG;
+  const int cg = (blockIdx.x % ctiles) * SC_CG + threadIdx.x % SC_CG;
+  const long long q = (long long)(blockIdx.x / ctiles) * SC_SLOTS + threadIdx.x / SC_CG;
+  if (cg >= DG || q >= (long long)a.B * NTB) return;
+  const int d = cg * CPT, b = (int)(q / NTB), t0 = (int)(q % NTB) * RT;
+  Raw<E, CPT> x[RT + W - 1];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+  for (int r = 0; r < RT + W - 1; ++r) conv_raw<E, CPT>(a, b, t0 - (W - 1) + r, d, x[r]);
+  float tw[CPT][W];
+  load_taps<CPT, W>(a.w, d, tw);
 #pragma unroll
-  for (int i = 0; i < W; ++i) {
-    float x[8];
-    conv_row<E>(a, b, t - (W - 1) + i, d, x);
+  for (int r = 0; r < RT; ++r) {
+    if (t0 + r >= a.T) break;
+    Raw<E, CPT> y;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] += a.w[(size_t)(d + c) * W + i] * x[c];
+    for (int c = 0; c < CPT; ++c) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < W; ++i) acc += tw[c][i] * x[r + i][c];
+      y.set(c, a.act ? silu_(acc) : acc);
+    }
+    y.store(static_cast<E*>(a.y) + ((size_t)b * a.T + t0 + r) * a.D + d);
   }
-  float y[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) y[c] = a.act ? silu_(acc[c]) : acc[c];
-  store8f(static_cast<E*>(a.y) + ((size_t)b * a.T + t) * a.D + d, y);
 }
 
 template <typename E>
@@ -84,89 +158,106 @@ __global__ __launch_bounds__(256) void short_conv_cache_kernel(ShortConvArgs a) 
   for (int k = 0; k < 8; ++k) c[(size_t)k * a.W] = (E)x[k];
 }
 
-// dx and dw. A workgroup owns 32 groups of 8 channels and a block of rows;
-// each thread walks rows r = lane-row, lane-row + 8, ...: it recomputes the
-// pre-activation a[s] of the rows s = t .. t+W-1 its dx needs and adds
-// da[t] x[t-(W-1)+i] to its dw partials; the 8 row lanes of a channel group
-// are summed in LDS and added to dw with one atomic per weight.
+// dx and dw, time blocks as in the forward. For the block's rows t0..t0+RT-1
+// a thread forms the pre-activations a[s], s in t0 .. t0+RT+W-2 (the rows
+// whose da its dx needs), da = dy silu'(a); then dx[t] = sum_u w[W-1-u]
+// da[t+u] and dw[i] += da[t] x[t-(W-1)+i]. Each workgroup walks a range of
+// time blocks (its 4 slots interleaved), keeps dw in registers, sums its
+// slots in LDS and adds to dw with one atomic per weight.
 template <typename E, int W>
 __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvArgs a) {
-  constexpr int CG = 32, RL = 8, MAXW = W;
-  __shared__ float s_dw[RL][CG][8 * MAXW];
-  const int D8 = a.D / 8;
-  const int cg = threadIdx.x % CG, rl = threadIdx.x / CG;
-  const int dgrp = blockIdx.x % ((D8 + CG - 1) / CG) * CG + cg;
-  const int rb = blockIdx.x / ((D8 + CG - 1) / CG);
-  const int d = dgrp * 8;
-  const bool live = dgrp < D8;
-  float dw[8 * MAXW];
+  constexpr int RT = ScRT<E>::b, CPT = SC_CPT_B;
+  __shared__ float s_dw[SC_SLOTS][SC_CG][CPT * W + 1];
+  const int DG = a.D / CPT, NTB = (a.T + RT - 1) / RT;
+  const int ctiles = (DG + SC_CG - 1) / SC_CG;
+  const int cl = threadIdx.x % SC_CG, slot = threadIdx.x / SC_CG;
+  const int cg = (blockIdx.x % ctiles) * SC_CG + cl;
+  const long long nq = (long long)a.B * NTB;
+  const long long rg = blockIdx.x / ctiles, nrg = gridDim.x / ctiles;
+  const bool live = cg < DG;
+  const int d = cg * CPT;
+  float dw[CPT][W];
 #pragma unroll
-  for (int k = 0; k < 8 * MAXW; ++k) dw[k] = 0.f;
-  const long long rows = (long long)a.B * a.T;
-  const long long r0 = (long long)rb * a.rows_per_block;
-  const long long r1 = min(rows, r0 + a.rows_per_block);
+  for (int c = 0; c < CPT; ++c)
+#pragma unroll
+    for (int i = 0; i < W; ++i) dw[c][i] = 0.f;
   if (live) {
-    for (long long r = r0 + rl; r < r1; r += RL) {
-      const int t = (int)(r % a.T), b = (int)(r / a.T);
-      // inputs x[t - (W-1) .. t + W-1]: 2W - 1 rows
-      float xs[2 * MAXW - 1][8];
+    float tw[CPT][W];
+    load_taps<CPT, W>(a.w, d, tw);
+    for (long long q = rg * SC_SLOTS + slot; q < nq; q += nrg * SC_SLOTS) {
+      const int b = (int)(q / NTB), t0 = (int)(q % NTB) * RT;
+      // every load of the block first: input rows t0-(W-1) .. t0+RT+W-2 and
+      // output-gradient rows t0 .. t0+RT+W-2 (zeros past the end)
+      Raw<E, CPT> x[RT + 2 * W - 2], dyr[RT + W - 1];
 #pragma unroll
-      for (int q = 0; q < 2 * W - 1; ++q) {
-        const int s = t - (W - 1) + q;
-        if (s < a.T) {
-          conv_row<E>(a, b, s, d, xs[q]);
+      for (int r = 0; r < RT + 2 * W - 2; ++r) conv_raw<E, CPT>(a, b, t0 - (W - 1) + r, d, x[r]);
+#pragma unroll
+      for (int u = 0; u < RT + W - 1; ++u) {
+        if (t0 + u < a.T) {
+          dyr[u].load(static_cast<const E*>(a.dy) + ((size_t)b * a.T + t0 + u) * a.D + d);
         } else {
 #pragma unroll
-          for (int c = 0; c < 8; ++c) xs[q][c] = 0.f;
+          for (int c = 0; c < CPT; ++c) dyr[u].set(c, 0.f);
         }
       }
-      float dx[8];
+      // da[u] at s = t0 + u, formed in order; dx of row r = u - (W-1) once
+      // da[r .. r+W-1] exist, so only a window of W rows of da is live
+      float da[RT + W - 1][CPT];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) dx[c] = 0.f;
-      // da at s = t + u (u < W), each a pre-activation over xs[u .. u+W-1]
+      for (int u = 0; u < RT + W - 1; ++u) {
 #pragma unroll
-      for (int u = 0; u < W; ++u) {
-        if (t + u >= a.T) continue;
-        float dy[8];
-        load8f(static_cast<const E*>(a.dy) + ((size_t)b * a.T + t + u) * a.D + d, dy);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < CPT; ++c) {
           float pre = 0.f;
 #pragma unroll
-          for (int i = 0; i < W; ++i) pre += a.w[(size_t)(d + c) * W + i] * xs[u + i][c];
-          const float da = a.act ? dy[c] * dsilu_(pre) : dy[c];
-          // x[t] enters a[t + u] through tap W-1-u
-          dx[c] += a.w[(size_t)(d + c) * W + (W - 1 - u)] * da;
-          if (u == 0) {
+          for (int i = 0; i < W; ++i) pre += tw[c][i] * x[u + i][c];
+          da[u][c] = a.act ? dyr[u][c] * dsilu_(pre) : dyr[u][c];
+        }
+        if (u < RT) {
 #pragma unroll
-            for (int i = 0; i < W; ++i) dw[c * MAXW + i] += da * xs[i][c];
+          for (int c = 0; c < CPT; ++c)
+#pragma unroll
+            for (int i = 0; i < W; ++i) dw[c][i] += da[u][c] * x[u + i][c];
+        }
+        const int r = u - (W - 1);
+        if (r >= 0 && r < RT && t0 + r < a.T) {
+          Raw<E, CPT> dx;
+#pragma unroll
+          for (int c = 0; c < CPT; ++c) {
+            float acc = 0.f;
+#pragma unroll
+            for (int v = 0; v < W; ++v) acc += tw[c][W - 1 - v] * da[r + v][c];
+            dx.set(c, acc);
           }
+          dx.store(static_cast<E*>(a.dx) + ((size_t)b * a.T + t0 + r) * a.D + d);
         }
       }
-      store8f(static_cast<E*>(a.dx) + ((size_t)b * a.T + t) * a.D + d, dx);
     }
   }
 #pragma unroll
-  for (int k = 0; k < 8 * MAXW; ++k) s_dw[rl][cg][k] = dw[k];
+  for (int c = 0; c < CPT; ++c)
+#pragma unroll
+    for (int i = 0; i < W; ++i) s_dw[slot][cl][c * W + i] = dw[c][i];
   __syncthreads();
-  if (rl == 0 && live) {
+  if (slot == 0 && live) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int k = 0; k < CPT * W; ++k) {
+      float sum = 0.f;
 #pragma unroll
-      for (int i = 0; i < W; ++i) {
-        float s = 0.f;
-#pragma unroll
-        for (int q = 0; q < RL; ++q) s += s_dw[q][cg][c * MAXW + i];
-        atomicAdd(&a.dw[(size_t)(d + c) * W + i], s);
-      }
+      for (int sl = 0; sl < SC_SLOTS; ++sl) sum += s_dw[sl][cl][k];
+      if (a.ws) a.ws[(size_t)rg * a.D * W + (size_t)d * W + k] = sum;
+      else atomicAdd(&a.dw[(size_t)d * W + k], sum);
+    }
   }
 }
 
+static unsigned sc_ctiles(const ShortConvArgs& a, int cpt) { return (unsigned)((a.D / cpt + SC_CG - 1) / SC_CG); }
+
 hipError_t short_conv_fwd(const ShortConvArgs& a, int dtype, hipStream_t st) {
   if (a.D % 8 != 0 || a.W < 1 || a.W > 8) return hipErrorInvalidValue;
-  const long long n = (long long)a.B * a.T * (a.D / 8);
-  if (n > 0) {
-    const unsigned grid = (unsigned)((n + 255) / 256);
+  if ((long long)a.B * a.T > 0) {
+    const int RT = dtype == NGDN_BF16 ? ScRT<bf16>::f : ScRT<float>::f;
+    const long long nq = (long long)a.B * ((a.T + RT - 1) / RT);
+    const unsigned grid = sc_ctiles(a, SC_CPT_F) * (unsigned)((nq + SC_SLOTS - 1) / SC_SLOTS);
 #define NGDN_CF(WW)                                                                              \
     if (a.W == WW) {                                                                             \
       if (dtype == NGDN_BF16) hipLaunchKernelGGL((short_conv_fwd_kernel<bf16, WW>), dim3(grid), dim3(256), 0, st, a); \
@@ -188,12 +279,17 @@ hipError_t short_conv_fwd(const ShortConvArgs& a, int dtype, hipStream_t st) {
 
 hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st) {
   if (a.D % 8 != 0 || a.W < 1 || a.W > 8) return hipErrorInvalidValue;
-  const long long rows = (long long)a.B * a.T;
-  if (rows == 0) return hipSuccess;
-  a.rows_per_block = 256;
-  const int cblocks = (a.D / 8 + 31) / 32;
-  const long long rblocks = (rows + a.rows_per_block - 1) / a.rows_per_block;
-  const unsigned grid = (unsigned)(cblocks * rblocks);
+  if ((long long)a.B * a.T == 0) return hipSuccess;
+  const int RT = dtype == NGDN_BF16 ? ScRT<bf16>::b : ScRT<float>::b;
+  const long long nq = (long long)a.B * ((a.T + RT - 1) / RT);
+  const unsigned ct = sc_ctiles(a, SC_CPT_B);
+  // about 2048 workgroups, each walking its share of the time blocks; at
+  // most NGDN_WPARTS rows of partial sums
+  long long rgs = 2048 / ct;
+  const long long most = (nq + SC_SLOTS - 1) / SC_SLOTS;
+  rgs = rgs < 1 ? 1 : (rgs > most ? most : rgs);
+  if (rgs > NGDN_WPARTS) rgs = NGDN_WPARTS;
+  const unsigned grid = ct * (unsigned)rgs;
 #define NGDN_CB(WW)                                                                              \
   if (a.W == WW) {                                                                               \
     if (dtype == NGDN_BF16) hipLaunchKernelGGL((short_conv_bwd_kernel<bf16, WW>), dim3(grid), dim3(256), 0, st, a); \
@@ -201,7 +297,8 @@ hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st) {
   }
   NGDN_CB(1) NGDN_CB(2) NGDN_CB(3) NGDN_CB(4) NGDN_CB(5) NGDN_CB(6) NGDN_CB(7) NGDN_CB(8)
 #undef NGDN_CB
-  return hipGetLastError();
+  if (hipError_t e = hipGetLastError()) return e;
+  return a.ws ? sum_parts(a.ws, rgs, (long long)a.D * a.W, a.dw, st) : hipSuccess;
 }
 
 // ---------------------------------------------------------------- FusedRMSNormGated
@@ -231,7 +328,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_fwd_kernel(NormGatedArgs a)
   if (!live) return;
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = x[e] * rstd * a.w[c + e] / (1.f + expf(-g[e]));
+  for (int e = 0; e < 8; ++e) y[e] = x[e] * rstd * a.w[c + e] * sigmoid_fast(g[e]);
   store8f(static_cast<E*>(a.y) + row * V + c, y);
   if (a.rstd && c == 0) a.rstd[row] = rstd;
 }
@@ -256,7 +353,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_bwd_kernel(NormGatedArgs a)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       xh[e] = x[e] * rstd;
-      s[e] = 1.f / (1.f + expf(-g[e]));
+      s[e] = sigmoid_fast(g[e]);
       dxh[e] = dy[e] * a.w[c + e] * s[e];
       dot += dxh[e] * xh[e];
       dw[e] += dy[e] * xh[e] * s[e];
@@ -279,7 +376,8 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_bwd_kernel(NormGatedArgs a)
   for (int v = threadIdx.x; v < V; v += 256) {
     float sum = 0.f;
     for (int r = 0; r < RPB; ++r) sum += s_dw[r][v];
-    atomicAdd(&a.dw[v], sum);
+    if (a.ws) a.ws[(size_t)blockIdx.x * V + v] = sum;
+    else atomicAdd(&a.dw[v], sum);
   }
 }
 
@@ -305,12 +403,13 @@ hipError_t rmsnorm_gated_bwd(const NormGatedArgs& a, int dtype, int V, hipStream
   if (V == VV) {                                                                            \
     constexpr int RPB = 256 / (VV / 8);                                                     \
     const long long want = (a.rows + RPB * 16 - 1) / (RPB * 16);   /* ~16 rows per thread */ \
-    const unsigned grid = (unsigned)(want < 2048 ? (want > 0 ? want : 1) : 2048);           \
+    const unsigned grid = (unsigned)(want < NGDN_WPARTS ? (want > 0 ? want : 1) : NGDN_WPARTS); \
     if (dtype == NGDN_BF16)                                                                 \
       hipLaunchKernelGGL((rmsnorm_gated_bwd_kernel<bf16, VV>), dim3(grid), dim3(256), 0, st, a); \
     else                                                                                    \
       hipLaunchKernelGGL((rmsnorm_gated_bwd_kernel<float, VV>), dim3(grid), dim3(256), 0, st, a); \
-    return hipGetLastError();                                                               \
+    if (hipError_t e = hipGetLastError()) return e;                                         \
+    return a.ws ? sum_parts(a.ws, grid, VV, a.dw, st) : hipSuccess;                         \
   }
   NGDN_NG(64) NGDN_NG(128) NGDN_NG(256)
 #undef NGDN_NG

@@ -16,7 +16,7 @@ namespace ngdn {
 
 namespace {
 
-__device__ __forceinline__ float sigm(float a) { return 1.f / (1.f + __expf(-a)); }
+__device__ __forceinline__ float sigm(float a) { return sigmoid_fast(a); }
 
 // sum over the G lanes of a row group (G a power of two <= 64, groups aligned)
 template <int G>
@@ -125,7 +125,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RMSNormArgs a) {
     float sum = 0.f;
 #pragma unroll
     for (int r = 0; r < RPB; ++r) sum += s_dw[r][c];
-    atomicAdd(&a.dw[c], sum);
+    if (a.ws) a.ws[(size_t)blockIdx.x * D + c] = sum;
+    else atomicAdd(&a.dw[c], sum);
   }
 }
 
@@ -163,16 +164,52 @@ hipError_t rmsnorm_bwd(const RMSNormArgs& a, int dtype, hipStream_t st) {
   if (a.D == 8 * GG * VV) {                                                                  \
     constexpr long long RPB = 256 / GG;                                                      \
     const long long want = (a.rows + RPB * 16 - 1) / (RPB * 16);   /* ~16 rows per slot */   \
-    const unsigned grid = (unsigned)(want < 1024 ? want : 1024);                             \
+    const unsigned grid = (unsigned)(want < NGDN_WPARTS ? want : NGDN_WPARTS);               \
     if (dtype == NGDN_BF16)                                                                  \
       hipLaunchKernelGGL((rmsnorm_bwd_kernel<bf16, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
     else                                                                                     \
       hipLaunchKernelGGL((rmsnorm_bwd_kernel<float, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
-    return hipGetLastError();                                                                \
+    if (hipError_t e = hipGetLastError()) return e;                                          \
+    return a.ws ? sum_parts(a.ws, grid, a.D, a.dw, st) : hipSuccess;                         \
   }
   NGDN_RMS_SHAPES(NGDN_RMS_B)
 #undef NGDN_RMS_B
   return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------- partial sums
+
+// out[j] += sum_p ws[p][j]: a workgroup takes 64 columns and a range of at
+// most 64 rows (4 slices of 16), sums in LDS and adds with one atomic per
+// column, so no address sees more than nparts / 64 atomics
+constexpr int SP_COLS = 64, SP_ROWS = 64;
+
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float* ws, long long nparts, long long n,
+                                                        float* out) {
+  __shared__ float s_part[4][SP_COLS];
+  const long long j = (long long)blockIdx.x * SP_COLS + threadIdx.x % SP_COLS;
+  const int slice = threadIdx.x / SP_COLS;
+  const long long p0 = (long long)blockIdx.y * SP_ROWS + slice * (SP_ROWS / 4);
+  float acc = 0.f;
+  if (j < n) {
+#pragma unroll
+    for (int r = 0; r < SP_ROWS / 4; ++r) {
+      const long long p = p0 + r;
+      if (p < nparts) acc += ws[(size_t)p * n + j];
+    }
+  }
+  s_part[slice][threadIdx.x % SP_COLS] = acc;
+  __syncthreads();
+  if (slice == 0 && j < n)
+    atomicAdd(&out[j], s_part[0][threadIdx.x] + s_part[1][threadIdx.x] + s_part[2][threadIdx.x] +
+                       s_part[3][threadIdx.x]);
+}
+
+hipError_t sum_parts(const float* ws, long long nparts, long long n, float* out, hipStream_t st) {
+  if (n == 0 || nparts == 0) return hipSuccess;
+  const dim3 grid((unsigned)((n + SP_COLS - 1) / SP_COLS), (unsigned)((nparts + SP_ROWS - 1) / SP_ROWS));
+  hipLaunchKernelGGL(sum_parts_kernel, grid, dim3(256), 0, st, ws, nparts, n, out);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- SwiGLU

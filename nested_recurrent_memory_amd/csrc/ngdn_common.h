@@ -32,6 +32,12 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 template <typename T> __device__ __forceinline__ float to_f(T x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
 
+// logistic function from the hardware exp and reciprocal (about 2 ulp; the
+// exact-division form costs several times the instructions in the
+// elementwise kernels, where it dominates)
+__device__ __forceinline__ float sigmoid_fast(float a) {
+  return __builtin_amdgcn_rcpf(1.f + __expf(-a));
+}
 __device__ __forceinline__ f4 f4_zero() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // ---------------------------------------------------------------- MFMA

@@ -159,9 +159,16 @@ hipError_t promote_fwd(const PromoteArgs& a, int dtype, int K, hipStream_t st);
 struct ShortConvArgs {
   const void* x; const float* w; const void* cache_in; void* y; void* cache_out;
   const void* dy; void* dx; float* dw;
+  float* ws;    // backward: per-workgroup partial dw [NGDN_WPARTS][D*W], or NULL
   int B, T, D, W, act;
-  long long rows_per_block;
 };
+
+// Weight gradients summed over many workgroups: each workgroup stores its
+// partial sum in row p of a workspace [NGDN_WPARTS][n] (plain stores), then
+// sum_parts adds the rows into the gradient with a few atomics per element.
+// Device-scope float atomics are performed past the per-XCD L2s, a few
+// million of them (one per workgroup and weight) cost more than the kernel.
+hipError_t sum_parts(const float* ws, long long nparts, long long n, float* out, hipStream_t st);
 hipError_t short_conv_fwd(const ShortConvArgs& a, int dtype, hipStream_t st);
 hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st);
 
@@ -171,6 +178,7 @@ hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st);
 struct NormGatedArgs {
   const void* x; const void* g; const float* w; void* y; float* rstd;
   const void* dy; void* dx; void* dg; float* dw;
+  float* ws;    // backward: per-workgroup partial dw [NGDN_WPARTS][n], or NULL
   long long rows;
   float eps;
 };
@@ -183,6 +191,7 @@ hipError_t rmsnorm_gated_bwd(const NormGatedArgs& a, int dtype, int V, hipStream
 struct RMSNormArgs {
   const void* x; const float* w; void* y; float* rstd;
   const void* dy; void* dx; float* dw;
+  float* ws;    // backward: per-workgroup partial dw [NGDN_WPARTS][n], or NULL
   long long rows;
   int D;
   float eps;

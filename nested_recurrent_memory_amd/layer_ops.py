@@ -75,9 +75,10 @@ class _ShortConvFn(torch.autograd.Function):
         dyw = dy.to(xw.dtype).contiguous()
         dx = torch.empty_like(xw)
         dw = torch.zeros(D, W, device=xw.device, dtype=torch.float32)
+        ws = torch.empty(_lib.WPARTS, D * W, device=xw.device, dtype=torch.float32)
         _lib.call("ngdn_short_conv_bwd", _code(xw), B, T, D, W, int(ctx.act), _lib.ptr(xw),
                   _lib.ptr(w), _lib.ptr(c), _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dw),
-                  _lib.stream_of(xw))
+                  _lib.ptr(ws), _lib.stream_of(xw))
         return dx.to(ctx.in_dtype), dw.reshape(ctx.w_shape).to(ctx.w_dtype), None, None, None
 
 
@@ -120,9 +121,10 @@ class _NormGatedFn(torch.autograd.Function):
         dyw = dy.to(xw.dtype).contiguous()
         dx, dg = torch.empty_like(xw), torch.empty_like(gw)
         dw = torch.zeros(V, device=xw.device, dtype=torch.float32)
+        ws = torch.empty(_lib.WPARTS, V, device=xw.device, dtype=torch.float32)
         _lib.call("ngdn_rmsnorm_gated_bwd", _code(xw), rows, V, _lib.ptr(xw), _lib.ptr(gw),
                   _lib.ptr(w), _lib.ptr(rstd), _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dg),
-                  _lib.ptr(dw), _lib.stream_of(xw))
+                  _lib.ptr(dw), _lib.ptr(ws), _lib.stream_of(xw))
         xd, gd, wd = ctx.dtypes
         return dx.to(xd), dg.to(gd), dw.to(wd), None
 

@@ -75,8 +75,9 @@ class _RMSNormFn(torch.autograd.Function):
         dyw = dy.to(xw.dtype).contiguous()
         dx = torch.empty_like(xw)
         dw = torch.zeros(D, device=xw.device, dtype=torch.float32)
+        ws = torch.empty(_lib.WPARTS, D, device=xw.device, dtype=torch.float32)
         _lib.call("ngdn_rmsnorm_bwd", _code(xw), rows, D, _lib.ptr(xw), _lib.ptr(w), _lib.ptr(rstd),
-                  _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dw), _lib.stream_of(xw))
+                  _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(ws), _lib.stream_of(xw))
         return dx.to(ctx.dtypes[0]), dw.to(ctx.dtypes[1]), None
 
 

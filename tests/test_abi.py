@@ -108,9 +108,9 @@ def test_layer_op_entry_points_validate_before_launch():
     # W=9 is beyond the unrolled tap counts; D must be a multiple of 8
     assert so.ngdn_short_conv_fwd(_lib.NGDN_BF16, 1, 4, 64, 9, 1, *([None] * 6)) == 1
     assert b"W=9" in so.ngdn_last_error()
-    assert so.ngdn_short_conv_bwd(_lib.NGDN_F32, 1, 4, 60, 4, 1, *([None] * 7)) == 1
+    assert so.ngdn_short_conv_bwd(_lib.NGDN_F32, 1, 4, 60, 4, 1, *([None] * 8)) == 1
     assert b"D=60" in so.ngdn_last_error()
     assert so.ngdn_rmsnorm_gated_fwd(_lib.NGDN_F32, 4, 96, 1e-5, *([None] * 6)) == 1
     assert b"V=96" in so.ngdn_last_error()
-    assert so.ngdn_rmsnorm_gated_bwd(_lib.NGDN_BF16, 4, 64, *([None] * 9)) == 1
+    assert so.ngdn_rmsnorm_gated_bwd(_lib.NGDN_BF16, 4, 64, *([None] * 10)) == 1
     assert b"NULL" in so.ngdn_last_error()
