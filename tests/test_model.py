@@ -125,3 +125,26 @@ def test_model_ops_refuse_host_tensors():
     with pytest.raises(ValueError, match="no CPU path"):
         fused_linear_cross_entropy(torch.randn(4, 8), torch.zeros(4, dtype=torch.long),
                                    torch.randn(16, 8))
+
+
+def test_save_pretrained_round_trip(tmp_path):
+    """save_pretrained / from_pretrained and AutoModelForCausalLM give back the
+    same config and parameters (the checkpoint format of the reference:
+    config.json with model_type nested_gdn2 + safetensors weights)."""
+    import json
+
+    from transformers import AutoModelForCausalLM
+    cfg = _tiny(num_levels=3, firing_intervals=(1, 2, 4), n_queries_per_level=(16, 32))
+    torch.manual_seed(3)
+    m = NestedGDN2ForCausalLM(cfg)
+    m.save_pretrained(tmp_path)
+    meta = json.loads((tmp_path / "config.json").read_text())
+    assert meta["model_type"] == "nested_gdn2" and meta["firing_intervals"] == [1, 2, 4]
+    for loaded in (NestedGDN2ForCausalLM.from_pretrained(tmp_path),
+                   AutoModelForCausalLM.from_pretrained(tmp_path)):
+        assert isinstance(loaded, NestedGDN2ForCausalLM)
+        assert loaded.config.firing_intervals == (1, 2, 4)
+        sd, sd2 = m.state_dict(), loaded.state_dict()
+        assert set(sd) == set(sd2)
+        for k in sd:
+            assert torch.equal(sd[k], sd2[k]), k
