@@ -300,6 +300,39 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
                                const void* dy, void* dx, void* dg, float* dw, float* ws,
                                void* stream);
 
+/* The layer's gate prologue (layers/nested_gdn2.py:134-166), from the
+ * convolved projections to the op's inputs, per token t and head h:
+ *   qn[t,h,l,:] = normalize(q[t, l*H*K + h*K + :])   (q in "b t (l h d)" order)
+ *   kn[t,h,:]   = normalize(k[t, h*K + :])
+ *   g0[t,h,:]   = min(-exp(A_log[h]) softplus(f[t, h*K + :] + dt_bias[h*K + :]), cap)
+ *   b0 = sigmoid(bz), w0 = sigmoid(wz), mix[t,h,:] = softmax (or sigmoid) of ml[t, h*L + :]
+ * normalize(x) = x / max(|x|, 1e-12) (F.normalize), softplus with torch's
+ * threshold 20. BT = B*T tokens; q, k, f, bz, wz, ml, qn, kn, b0, w0, mix in
+ * dtype; g0 fp32 [BT,H,K]; A_log [H] and dt_bias [H*K] in param_dtype.
+ * cap = -1/max_horizon, or +inf. K, V in {64, 128}, 1 <= L <= 8. The
+ * backward reads the forward inputs and the gradients dqn, dkn, dg0 (fp32),
+ * db0, dw0, dmix of the six outputs, writes dq, dk, df, dbz, dwz, dml, and
+ * adds the decay parameters' gradients into dpar (fp32 [H*K + H]: dt_bias,
+ * then A_log; callers zero it) through ws (fp32 [NGDN_WPARTS][H*K + H], or
+ * NULL: device-scope atomics). */
+typedef struct ngdn_gate_args {
+  int64_t BT;
+  int32_t H, L, K, V;
+  int32_t param_dtype, sigmoid_mix;
+  float cap;
+  const void *q, *k, *f, *bz, *wz, *ml, *A_log, *dt_bias;
+  void *qn, *kn;
+  float* g0;
+  void *b0, *w0, *mix;
+  const void *dqn, *dkn;
+  const float* dg0;
+  const void *db0, *dw0, *dmix;
+  void *dq, *dk, *df, *dbz, *dwz, *dml;
+  float *dpar, *ws;
+} ngdn_gate_args;
+int32_t ngdn_gate_prep_fwd(int32_t dtype, const ngdn_gate_args* g, void* stream);
+int32_t ngdn_gate_prep_bwd(int32_t dtype, const ngdn_gate_args* g, void* stream);
+
 /* ---- The model around the layer (NestedGDN2ForCausalLM,
  * models/modeling_nested_gdn2.py), which takes three more modules from fla;
  * these replace their kernels (the linear maps stay GEMMs of the caller). */

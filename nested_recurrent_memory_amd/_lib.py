@@ -56,6 +56,8 @@ SIGNATURES = {
     "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_bwd": [I32, I64, I32, P, P, P, P, P, P, P, P, P, P],
+    "ngdn_gate_prep_fwd": [I32, P, P],
+    "ngdn_gate_prep_bwd": [I32, P, P],
     "ngdn_rmsnorm_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P],
     "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 8,
     "ngdn_swiglu_fwd": [I32, I64] + [P] * 4,
@@ -125,6 +127,16 @@ def stream_of(t):
 
 def ptr_of_stream(st):
     return ctypes.c_void_p(st.cuda_stream)
+
+
+class GateArgs(ctypes.Structure):
+    """ngdn_gate_args (include/ngdn.h)."""
+    _fields_ = ([("BT", ctypes.c_int64)] + [(n, ctypes.c_int32) for n in
+                ("H", "L", "K", "V", "param_dtype", "sigmoid_mix")] + [("cap", ctypes.c_float)] +
+                [(n, ctypes.c_void_p) for n in (
+                    "q", "k", "f", "bz", "wz", "ml", "A_log", "dt_bias", "qn", "kn", "g0", "b0",
+                    "w0", "mix", "dqn", "dkn", "dg0", "db0", "dw0", "dmix", "dq", "dk", "df",
+                    "dbz", "dwz", "dml", "dpar", "ws")])
 
 
 def dims(B, T, H, L, K, V, dtype_code, scale):

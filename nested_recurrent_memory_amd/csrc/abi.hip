@@ -571,6 +571,46 @@ int32_t ngdn_rmsnorm_gated_bwd(int32_t dtype, int64_t rows, int32_t V, const voi
   return launched(ngdn::rmsnorm_gated_bwd(a, dtype, V, (hipStream_t)stream), "ngdn_rmsnorm_gated_bwd");
 }
 
+static int32_t gate_args(int32_t dtype, const ngdn_gate_args* g, ngdn::GatePrepArgs& a, const char* who) {
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "%s: dtype %d", who, dtype);
+  if (!g) return fail(NGDN_EINVAL, "%s: NULL arguments", who);
+  if (g->BT < 0 || g->H <= 0 || g->L < 1 || g->L > 8 || (g->K != 64 && g->K != 128) ||
+      (g->V != 64 && g->V != 128) || (g->param_dtype != NGDN_F32 && g->param_dtype != NGDN_BF16))
+    return fail(NGDN_EINVAL, "%s: BT=%lld H=%d L=%d K=%d V=%d param_dtype=%d (K, V in 64, 128; 1 <= L <= 8)",
+                who, (long long)g->BT, g->H, g->L, g->K, g->V, g->param_dtype);
+  a = ngdn::GatePrepArgs{};
+  a.q = g->q; a.k = g->k; a.f = g->f; a.bz = g->bz; a.wz = g->wz; a.ml = g->ml;
+  a.A_log = g->A_log; a.dt_bias = g->dt_bias;
+  a.qn = g->qn; a.kn = g->kn; a.g0 = g->g0; a.b0 = g->b0; a.w0 = g->w0; a.mix = g->mix;
+  a.dqn = g->dqn; a.dkn = g->dkn; a.dg0 = g->dg0; a.db0 = g->db0; a.dw0 = g->dw0; a.dmix = g->dmix;
+  a.dq = g->dq; a.dk = g->dk; a.df = g->df; a.dbz = g->dbz; a.dwz = g->dwz; a.dml = g->dml;
+  a.dpar = g->dpar; a.ws = g->ws;
+  a.BT = g->BT; a.H = g->H; a.L = g->L; a.K = g->K; a.V = g->V;
+  a.pdtype = g->param_dtype; a.sigmoid_mix = g->sigmoid_mix != 0; a.cap = g->cap;
+  return 0;
+}
+
+int32_t ngdn_gate_prep_fwd(int32_t dtype, const ngdn_gate_args* g, void* stream) {
+  g_err[0] = 0;
+  ngdn::GatePrepArgs a;
+  if (int32_t r = gate_args(dtype, g, a, "ngdn_gate_prep_fwd")) return r;
+  if (a.BT > 0 && (!a.q || !a.k || !a.f || !a.bz || !a.wz || !a.ml || !a.A_log || !a.dt_bias ||
+                   !a.qn || !a.kn || !a.g0 || !a.b0 || !a.w0 || !a.mix))
+    return fail(NGDN_EINVAL, "ngdn_gate_prep_fwd: NULL tensor");
+  return launched(ngdn::gate_prep_fwd(a, dtype, (hipStream_t)stream), "ngdn_gate_prep_fwd");
+}
+
+int32_t ngdn_gate_prep_bwd(int32_t dtype, const ngdn_gate_args* g, void* stream) {
+  g_err[0] = 0;
+  ngdn::GatePrepArgs a;
+  if (int32_t r = gate_args(dtype, g, a, "ngdn_gate_prep_bwd")) return r;
+  if (a.BT > 0 && (!a.q || !a.k || !a.f || !a.bz || !a.wz || !a.ml || !a.A_log || !a.dt_bias ||
+                   !a.dqn || !a.dkn || !a.dg0 || !a.db0 || !a.dw0 || !a.dmix || !a.dq || !a.dk ||
+                   !a.df || !a.dbz || !a.dwz || !a.dml || !a.dpar))
+    return fail(NGDN_EINVAL, "ngdn_gate_prep_bwd: NULL tensor");
+  return launched(ngdn::gate_prep_bwd(a, dtype, (hipStream_t)stream), "ngdn_gate_prep_bwd");
+}
+
 int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, const void* x,
                          const float* w, void* y, float* rstd, void* stream) {
   g_err[0] = 0;

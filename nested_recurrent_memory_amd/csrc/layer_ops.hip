@@ -301,6 +301,209 @@ hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st) {
   return a.ws ? sum_parts(a.ws, rgs, (long long)a.D * a.W, a.dw, st) : hipSuccess;
 }
 
+// ---------------------------------------------------------------- gate prologue
+
+namespace {
+
+// max and sum over the first 8 lanes (the mix weights of one head, L <= 8)
+__device__ __forceinline__ float max8(float v) {
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+__device__ __forceinline__ float sum8(float v) {
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+template <typename P> __device__ __forceinline__ float ldp(const void* p, size_t i) {
+  return to_f(static_cast<const P*>(p)[i]);
+}
+// torch's softplus (beta 1, threshold 20) and its derivative
+__device__ __forceinline__ float softplus20(float z) { return z > 20.f ? z : log1pf(__expf(z)); }
+__device__ __forceinline__ float dsoftplus20(float z) { return z > 20.f ? 1.f : sigmoid_fast(z); }
+
+}  // namespace
+
+// One wave per (b, t, h), lane j holding elements j*KPL .. j*KPL+KPL-1 of a
+// K row (V row: VPL); blockIdx.y is the head, so a workgroup's 4 waves are 4
+// consecutive tokens of one head.
+template <typename E, typename P, int K, int V>
+__global__ __launch_bounds__(256) void gate_prep_fwd_kernel(GatePrepArgs a) {
+  constexpr int KPL = K / WAVE, VPL = V / WAVE;
+  const int h = blockIdx.y, H = a.H, L = a.L, lane = lane_id();
+  const long long bt = (long long)blockIdx.x * 4 + wave_id();
+  if (bt >= a.BT) return;
+  const long long th = bt * H + h;                 // token-head
+  // q: L rows, transposed from (l h) to (h l); k: one row
+  for (int l = 0; l <= L; ++l) {
+    const E* src = l < L ? static_cast<const E*>(a.q) + (bt * L + l) * H * K + (size_t)h * K
+                         : static_cast<const E*>(a.k) + th * K;
+    E* dst = l < L ? static_cast<E*>(a.qn) + (th * L + l) * K : static_cast<E*>(a.kn) + th * K;
+    float x[KPL], ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) { x[j] = to_f(src[lane * KPL + j]); ss += x[j] * x[j]; }
+    const float inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) dst[lane * KPL + j] = from_f<E>(x[j] * inv);
+  }
+  // decay and gates
+  const float A = __expf(ldp<P>(a.A_log, h));
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int c = lane * KPL + j;
+    const float z = to_f(static_cast<const E*>(a.f)[th * K + c]) + ldp<P>(a.dt_bias, (size_t)h * K + c);
+    a.g0[th * K + c] = fminf(-A * softplus20(z), a.cap);
+    static_cast<E*>(a.b0)[th * K + c] = from_f<E>(sigmoid_fast(to_f(static_cast<const E*>(a.bz)[th * K + c])));
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane * VPL + j;
+    static_cast<E*>(a.w0)[th * V + c] = from_f<E>(sigmoid_fast(to_f(static_cast<const E*>(a.wz)[th * V + c])));
+  }
+  // mix over the L levels in lanes 0..L-1
+  if (lane < 8) {
+    const float z = lane < L ? to_f(static_cast<const E*>(a.ml)[th * L + lane]) : -INFINITY;
+    // every one of the 8 lanes takes part in the shuffles (a shuffle reads
+    // the source lane's register, which must be active)
+    const float mx = max8(z);
+    const float e = lane < L ? __expf(z - mx) : 0.f;
+    const float den = sum8(e);
+    const float m = a.sigmoid_mix ? sigmoid_fast(z) : e / den;
+    if (lane < L) static_cast<E*>(a.mix)[th * L + lane] = from_f<E>(m);
+  }
+}
+
+// Backward, same mapping; waves walk tokens grid-stride so the decay
+// parameters' gradients collect in registers, then one partial row per
+// workgroup.
+template <typename E, typename P, int K, int V>
+__global__ __launch_bounds__(256) void gate_prep_bwd_kernel(GatePrepArgs a) {
+  constexpr int KPL = K / WAVE, VPL = V / WAVE;
+  __shared__ float s_dt[4][K], s_da[4];
+  const int h = blockIdx.y, H = a.H, L = a.L, lane = lane_id(), wv = wave_id();
+  const float A = __expf(ldp<P>(a.A_log, h));
+  float ddt[KPL], dA = 0.f;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) ddt[j] = 0.f;
+  for (long long bt = (long long)blockIdx.x * 4 + wv; bt < a.BT; bt += (long long)gridDim.x * 4) {
+    const long long th = bt * H + h;
+    for (int l = 0; l <= L; ++l) {
+      const size_t xo = l < L ? (bt * L + l) * H * K + (size_t)h * K : th * K;
+      const size_t yo = l < L ? (th * L + l) * K : th * K;
+      const E* src = static_cast<const E*>(l < L ? a.q : a.k) + xo;
+      const E* dy = static_cast<const E*>(l < L ? a.dqn : a.dkn) + yo;
+      E* dx = static_cast<E*>(l < L ? a.dq : a.dk) + xo;
+      float x[KPL], g[KPL], ss = 0.f, xg = 0.f;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        x[j] = to_f(src[lane * KPL + j]);
+        g[j] = to_f(dy[lane * KPL + j]);
+        ss += x[j] * x[j];
+        xg += x[j] * g[j];
+      }
+      const float n = sqrtf(wave_sum(ss));
+      xg = wave_sum(xg);
+      // y = x / max(n, eps): dx = dy / n - x <x, dy> / n^3 above eps, dy / eps below
+      const float inv = 1.f / fmaxf(n, 1e-12f);
+      const float c = n > 1e-12f ? xg * inv * inv * inv : 0.f;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) dx[lane * KPL + j] = from_f<E>(g[j] * inv - x[j] * c);
+    }
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int c = lane * KPL + j;
+      const float z = to_f(static_cast<const E*>(a.f)[th * K + c]) + ldp<P>(a.dt_bias, (size_t)h * K + c);
+      const float gu = -A * softplus20(z);
+      const float dg = gu <= a.cap ? a.dg0[th * K + c] : 0.f;   // clamp(max=cap) passes at equality
+      dA += dg * gu;
+      const float dz = -A * dg * dsoftplus20(z);
+      static_cast<E*>(a.df)[th * K + c] = from_f<E>(dz);
+      ddt[j] += dz;
+      const float s = sigmoid_fast(to_f(static_cast<const E*>(a.bz)[th * K + c]));
+      static_cast<E*>(a.dbz)[th * K + c] = from_f<E>(to_f(static_cast<const E*>(a.db0)[th * K + c]) * s * (1.f - s));
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int c = lane * VPL + j;
+      const float s = sigmoid_fast(to_f(static_cast<const E*>(a.wz)[th * V + c]));
+      static_cast<E*>(a.dwz)[th * V + c] = from_f<E>(to_f(static_cast<const E*>(a.dw0)[th * V + c]) * s * (1.f - s));
+    }
+    if (lane < 8) {
+      const float z = lane < L ? to_f(static_cast<const E*>(a.ml)[th * L + lane]) : -INFINITY;
+      const float dm = lane < L ? to_f(static_cast<const E*>(a.dmix)[th * L + lane]) : 0.f;
+      const float mx = max8(z);
+      const float e = lane < L ? __expf(z - mx) : 0.f;
+      const float ms = e / sum8(e);
+      const float dot = sum8(ms * dm);
+      const float sg = sigmoid_fast(z);
+      const float dz = a.sigmoid_mix ? dm * sg * (1.f - sg) : ms * (dm - dot);
+      if (lane < L) static_cast<E*>(a.dml)[th * L + lane] = from_f<E>(dz);
+    }
+  }
+  // the decay parameters: waves -> LDS -> one partial row per workgroup
+  dA = wave_sum(dA);
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) s_dt[wv][lane * KPL + j] = ddt[j];
+  if (lane == 0) s_da[wv] = dA;
+  __syncthreads();
+  const int n = H * K + H;
+  float* row = a.ws ? a.ws + (size_t)blockIdx.x * n : nullptr;
+  for (int c = threadIdx.x; c < K; c += 256) {
+    const float v = s_dt[0][c] + s_dt[1][c] + s_dt[2][c] + s_dt[3][c];
+    if (row) row[(size_t)h * K + c] = v;
+    else atomicAdd(&a.dpar[(size_t)h * K + c], v);
+  }
+  if (threadIdx.x == 0) {
+    const float v = s_da[0] + s_da[1] + s_da[2] + s_da[3];
+    if (row) row[(size_t)H * K + h] = v;
+    else atomicAdd(&a.dpar[(size_t)H * K + h], v);
+  }
+}
+
+#define NGDN_GP_DISPATCH(KERNEL, GRID)                                                         \
+  do {                                                                                         \
+    const dim3 grid_ = (GRID);                                                                 \
+    auto go = [&](auto e, auto p, auto kk, auto vv) {                                          \
+      hipLaunchKernelGGL((KERNEL<decltype(e), decltype(p), decltype(kk)::value,                \
+                                 decltype(vv)::value>), grid_, dim3(256), 0, st, a);           \
+    };                                                                                         \
+    using I64 = std::integral_constant<int, 64>;                                               \
+    using I128 = std::integral_constant<int, 128>;                                             \
+    auto pick_kv = [&](auto e, auto p) {                                                       \
+      if (a.K == 64 && a.V == 64) go(e, p, I64{}, I64{});                                      \
+      else if (a.K == 64 && a.V == 128) go(e, p, I64{}, I128{});                               \
+      else if (a.K == 128 && a.V == 64) go(e, p, I128{}, I64{});                               \
+      else go(e, p, I128{}, I128{});                                                           \
+    };                                                                                         \
+    auto pick_p = [&](auto e) {                                                                \
+      if (a.pdtype == NGDN_BF16) pick_kv(e, bf16{}); else pick_kv(e, float{});                 \
+    };                                                                                         \
+    if (dtype == NGDN_BF16) pick_p(bf16{}); else pick_p(float{});                              \
+  } while (0)
+
+static bool gate_prep_ok(const GatePrepArgs& a) {
+  return (a.K == 64 || a.K == 128) && (a.V == 64 || a.V == 128) && a.L >= 1 && a.L <= 8 && a.H > 0;
+}
+
+hipError_t gate_prep_fwd(const GatePrepArgs& a, int dtype, hipStream_t st) {
+  if (!gate_prep_ok(a)) return hipErrorInvalidValue;
+  if (a.BT == 0) return hipSuccess;
+  NGDN_GP_DISPATCH(gate_prep_fwd_kernel, dim3((unsigned)((a.BT + 3) / 4), (unsigned)a.H));
+  return hipGetLastError();
+}
+
+hipError_t gate_prep_bwd(const GatePrepArgs& a, int dtype, hipStream_t st) {
+  if (!gate_prep_ok(a)) return hipErrorInvalidValue;
+  if (a.BT == 0) return hipSuccess;
+  // about 8 tokens per wave, at most NGDN_WPARTS partial rows
+  long long nb = (a.BT + 31) / 32;
+  if (nb > NGDN_WPARTS) nb = NGDN_WPARTS;
+  NGDN_GP_DISPATCH(gate_prep_bwd_kernel, dim3((unsigned)nb, (unsigned)a.H));
+  if (hipError_t e = hipGetLastError()) return e;
+  return a.ws ? sum_parts(a.ws, nb, (long long)a.H * a.K + a.H, a.dpar, st) : hipSuccess;
+}
+
 // ---------------------------------------------------------------- FusedRMSNormGated
 
 // 16 lanes per row (8 values each), four rows per wave, 16 rows per workgroup

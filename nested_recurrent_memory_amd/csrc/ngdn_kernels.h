@@ -172,6 +172,32 @@ hipError_t sum_parts(const float* ws, long long nparts, long long n, float* out,
 hipError_t short_conv_fwd(const ShortConvArgs& a, int dtype, hipStream_t st);
 hipError_t short_conv_bwd(ShortConvArgs a, int dtype, hipStream_t st);
 
+// The layer's gate prologue (layer_ops.hip, layers/nested_gdn2.py:134-166):
+// from the convolved projections to the op's inputs, per (b, t, h):
+//   qn[b,t,h,l,:] = normalize(q[b,t, l*H*K + h*K + :])    (q "b t (l h d)")
+//   kn[b,t,h,:]   = normalize(k[b,t, h*K + :])
+//   g0[b,t,h,:]   = min(-exp(A_log[h]) softplus(f[b,t,h*K+:] + dt_bias[h*K+:]), cap)
+//   b0 = sigmoid(bz), w0 = sigmoid(wz), mix = softmax_l (or sigmoid) of ml[b,t,h*L+:]
+// normalize(x) = x / max(|x|, 1e-12) as F.normalize. Raw inputs, qn, kn, b0,
+// w0, mix in the working dtype; g0 fp32; A_log [H], dt_bias [H*K] in
+// pdtype (0 fp32, 1 bf16). cap = -1/max_horizon, or +inf. The backward takes
+// the gradients of the six outputs and writes those of the six raw inputs;
+// dpar (fp32 [H*K + H]: ddt_bias, then dA_log) is summed into through ws
+// partial rows [NGDN_WPARTS][H*K + H].
+struct GatePrepArgs {
+  const void* q; const void* k; const void* f; const void* bz; const void* wz; const void* ml;
+  const void* A_log; const void* dt_bias;
+  void* qn; void* kn; float* g0; void* b0; void* w0; void* mix;
+  const void* dqn; const void* dkn; const float* dg0; const void* db0; const void* dw0; const void* dmix;
+  void* dq; void* dk; void* df; void* dbz; void* dwz; void* dml;
+  float* dpar; float* ws;
+  long long BT;
+  int H, L, K, V, pdtype, sigmoid_mix;
+  float cap;
+};
+hipError_t gate_prep_fwd(const GatePrepArgs& a, int dtype, hipStream_t st);
+hipError_t gate_prep_bwd(const GatePrepArgs& a, int dtype, hipStream_t st);
+
 // The layer's FusedRMSNormGated (layer_ops.hip) over rows of V: x, g, y, dy,
 // dx, dg in the working dtype; w and dw [V] fp32 (dw summed into); rstd
 // [rows] fp32 written by the forward for the backward.

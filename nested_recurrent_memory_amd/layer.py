@@ -12,9 +12,9 @@ over whole chunks from an aligned position and the decoding step for the rest
 -> FusedRMSNormGated(o, g_proj x) -> o_proj.
 
 The matrix products of the projections are torch.nn.Linear (hipBLASLt); the
-convolution, the gated norm, the op and the step are HIP kernels of
-libngdn.so. The softplus/sigmoid/softmax/normalise elementwise steps are the
-reference's own torch expressions.
+convolution, the prologue from the normalisation to the mix (one kernel
+forward, one backward), the gated norm, the op and the step are HIP kernels
+of libngdn.so.
 
 Cache (``past_key_values``): a dict keyed by ``layer_idx`` whose entries hold
 ``"recurrent_state": (state [B,H,L,K,V] fp32, position [B] int64)`` (the
@@ -34,7 +34,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .chunk import chunk_nested_gdn2
-from .layer_ops import FusedRMSNormGated, ShortConvolution
+from .layer_ops import FusedRMSNormGated, ShortConvolution, gate_prep
 from .step import step_nested_gdn2
 
 __all__ = ["NestedGDN2LayerConfig", "NestedGDN2Attention"]
@@ -142,22 +142,15 @@ class NestedGDN2Attention(nn.Module):
             v, conv_v = self.v_conv1d(self.v_proj(x), cache=conv_v, output_final_state=use_cache)
         else:
             q, k, v = (F.silu(p(x)) for p in (self.q_proj, self.k_proj, self.v_proj))
-        q = q.reshape(B, T, L, H, K).transpose(2, 3)          # b t (l h d) -> b t h l d
-        k = k.reshape(B, T, H, K)
         v = v.reshape(B, T, H, V)
-        q = F.normalize(q, dim=-1).to(v.dtype)
-        k = F.normalize(k, dim=-1).to(v.dtype)
-
-        g0 = F.softplus(self.f_proj(x).float() + self.dt_bias).reshape(B, T, H, K)
-        g0 = -self.A_log.float().exp().unsqueeze(-1) * g0
-        if cfg.max_horizon:
-            g0 = g0.clamp(max=-1.0 / cfg.max_horizon)
-        b0 = self.b_proj(x).sigmoid().reshape(B, T, H, K)
-        w0 = self.w_proj(x).sigmoid().reshape(B, T, H, V)
-
-        mix_logits = self.mix_proj(x).reshape(B, T, H, L)
+        # q -> [B,T,H,L,K] and k L2-normalised, the decay g0 (fp32), gates b0,
+        # w0 and the level mix, in one kernel (layers/nested_gdn2.py:134-166)
         gated = cfg.read_mix == "sigmoid"
-        mix = (mix_logits.sigmoid() if gated else mix_logits.softmax(-1)).to(v.dtype)
+        wd = v.dtype
+        q, k, g0, b0, w0, mix = gate_prep(
+            q.to(wd), k.to(wd), self.f_proj(x).to(wd), self.b_proj(x).to(wd),
+            self.w_proj(x).to(wd), self.mix_proj(x).to(wd), self.A_log, self.dt_bias,
+            L, H, K, V, max_horizon=cfg.max_horizon, sigmoid_mix=gated)
         keep = getattr(cfg, "read_levels", None)   # eval-time read ablation (not a config field)
         if keep is not None:
             masked = torch.zeros_like(mix)

@@ -17,12 +17,14 @@ on tensors off the GPU) the calls raise.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn as nn
 
 from . import _lib
 
-__all__ = ["ShortConvolution", "FusedRMSNormGated", "short_conv", "rmsnorm_gated"]
+__all__ = ["ShortConvolution", "FusedRMSNormGated", "short_conv", "rmsnorm_gated", "gate_prep"]
 
 
 def _code(t):
@@ -136,6 +138,91 @@ def rmsnorm_gated(x, g, weight, eps=1e-5):
                          f"weight {tuple(weight.shape)}")
     _on_gpu("rmsnorm_gated", x, g, weight)
     return _NormGatedFn.apply(x, g, weight, eps)
+
+
+class _GatePrepFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, f, bz, wz, ml, A_log, dt_bias, L, H, K, V, cap, sigmoid_mix):
+        B, T = q.shape[:2]
+        wd = q.dtype if q.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        ins = [t.to(wd).contiguous() for t in (q, k, f, bz, wz, ml)]
+        pd = A_log.dtype if A_log.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        A, dt = A_log.to(pd).contiguous(), dt_bias.to(pd).contiguous()
+        dev = q.device
+        qn = torch.empty(B, T, H, L, K, device=dev, dtype=wd)
+        kn = torch.empty(B, T, H, K, device=dev, dtype=wd)
+        g0 = torch.empty(B, T, H, K, device=dev, dtype=torch.float32)
+        b0 = torch.empty(B, T, H, K, device=dev, dtype=wd)
+        w0 = torch.empty(B, T, H, V, device=dev, dtype=wd)
+        mix = torch.empty(B, T, H, L, device=dev, dtype=wd)
+        ga = _gate_args(B * T, H, L, K, V, pd, sigmoid_mix, cap, ins, A, dt)
+        for n, t in zip(("qn", "kn", "g0", "b0", "w0", "mix"), (qn, kn, g0, b0, w0, mix)):
+            setattr(ga, n, t.data_ptr())
+        _lib.call("ngdn_gate_prep_fwd", _code(qn), ctypes.byref(ga), _lib.stream_of(qn))
+        ctx.save_for_backward(*ins, A, dt)
+        ctx.cfg = (L, H, K, V, cap, sigmoid_mix)
+        ctx.dtypes = [t.dtype for t in (q, k, f, bz, wz, ml, A_log, dt_bias)]
+        return qn, kn, g0, b0, w0, mix
+
+    @staticmethod
+    def backward(ctx, dqn, dkn, dg0, db0, dw0, dmix):
+        *ins, A, dt = ctx.saved_tensors
+        L, H, K, V, cap, sigmoid_mix = ctx.cfg
+        q = ins[0]
+        B, T = q.shape[:2]
+        wd, dev = q.dtype, q.device
+
+        def grad(g, shape, dtype):
+            return (g.to(dtype).contiguous() if g is not None
+                    else torch.zeros(shape, device=dev, dtype=dtype))
+        outs = [grad(dqn, (B, T, H, L, K), wd), grad(dkn, (B, T, H, K), wd),
+                grad(dg0, (B, T, H, K), torch.float32), grad(db0, (B, T, H, K), wd),
+                grad(dw0, (B, T, H, V), wd), grad(dmix, (B, T, H, L), wd)]
+        dins = [torch.empty_like(t) for t in ins]
+        dpar = torch.zeros(H * K + H, device=dev, dtype=torch.float32)
+        ws = torch.empty(_lib.WPARTS, H * K + H, device=dev, dtype=torch.float32)
+        ga = _gate_args(B * T, H, L, K, V, A.dtype, sigmoid_mix, cap, ins, A, dt)
+        for n, t in zip(("dqn", "dkn", "dg0", "db0", "dw0", "dmix"), outs):
+            setattr(ga, n, t.data_ptr())
+        for n, t in zip(("dq", "dk", "df", "dbz", "dwz", "dml"), dins):
+            setattr(ga, n, t.data_ptr())
+        ga.dpar, ga.ws = dpar.data_ptr(), ws.data_ptr()
+        _lib.call("ngdn_gate_prep_bwd", _code(q), ctypes.byref(ga), _lib.stream_of(q))
+        dt_d, A_d = ctx.dtypes[7], ctx.dtypes[6]
+        res = [d.to(t) for d, t in zip(dins, ctx.dtypes[:6])]
+        return (*res, dpar[H * K:].to(A_d), dpar[:H * K].to(dt_d),
+                None, None, None, None, None, None)
+
+
+def _gate_args(BT, H, L, K, V, pd, sigmoid_mix, cap, ins, A, dt):
+    ga = _lib.GateArgs()
+    ga.BT, ga.H, ga.L, ga.K, ga.V = BT, H, L, K, V
+    ga.param_dtype = _lib.NGDN_BF16 if pd == torch.bfloat16 else _lib.NGDN_F32
+    ga.sigmoid_mix, ga.cap = int(sigmoid_mix), float(cap)
+    for n, t in zip(("q", "k", "f", "bz", "wz", "ml"), ins):
+        setattr(ga, n, t.data_ptr())
+    ga.A_log, ga.dt_bias = A.data_ptr(), dt.data_ptr()
+    return ga
+
+
+def gate_prep(q, k, f, bz, wz, ml, A_log, dt_bias, L, H, K, V, max_horizon=None,
+              sigmoid_mix=False):
+    """The layer's prologue (layers/nested_gdn2.py:134-166) in one kernel:
+    q [B,T,L*H*K] and k [B,T,H*K] (after the convolution), f = f_proj x
+    [B,T,H*K], bz = b_proj x, wz = w_proj x, ml = mix_proj x [B,T,H*L].
+    Returns qn [B,T,H,L,K], kn [B,T,H,K] (L2-normalised), g0 [B,T,H,K] fp32
+    (-exp(A_log) softplus(f + dt_bias), clamped at -1/max_horizon), b0, w0
+    (sigmoid) and mix [B,T,H,L] (softmax over levels, or sigmoid)."""
+    _on_gpu("gate_prep", q, k, f, bz, wz, ml, A_log, dt_bias)
+    B, T = q.shape[:2]
+    want = {"q": (B, T, L * H * K), "k": (B, T, H * K), "f": (B, T, H * K),
+            "bz": (B, T, H * K), "wz": (B, T, H * V), "ml": (B, T, H * L)}
+    for (n, shape), t in zip(want.items(), (q, k, f, bz, wz, ml)):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"gate_prep: {n} {tuple(t.shape)}, expected {shape}")
+    cap = -1.0 / max_horizon if max_horizon else float("inf")
+    return _GatePrepFn.apply(q, k, f, bz, wz, ml, A_log, dt_bias, L, H, K, V, cap,
+                             bool(sigmoid_mix))
 
 
 class ShortConvolution(nn.Module):

@@ -18,6 +18,7 @@
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 import ngdn_layer_oracle as lref
 from nested_recurrent_memory_amd.layer import NestedGDN2Attention, NestedGDN2LayerConfig
@@ -126,6 +127,60 @@ def test_rmsnorm_gated_matches_oracle(dtype, V, rows):
     _close("dg", gd.grad, g64.grad, dtype)
     # dw sums over every row in fp32
     _close("dw", wd.grad, w64.grad, torch.float32 if rows < 10000 else torch.bfloat16)
+
+
+# ----------------------------------------------------------------- gate prologue
+
+def _prologue_ref(q, k, f, bz, wz, ml, A_log, dt_bias, L, H, K, V, max_horizon, gated):
+    """The reference's expressions (layers/nested_gdn2.py:134-166) in float64."""
+    B, T = q.shape[:2]
+    qn = F.normalize(q.reshape(B, T, L, H, K).transpose(2, 3), dim=-1)
+    kn = F.normalize(k.reshape(B, T, H, K), dim=-1)
+    g0 = F.softplus(f + dt_bias).reshape(B, T, H, K)
+    g0 = -A_log.exp().unsqueeze(-1) * g0
+    if max_horizon:
+        g0 = g0.clamp(max=-1.0 / max_horizon)
+    b0 = bz.sigmoid().reshape(B, T, H, K)
+    w0 = wz.sigmoid().reshape(B, T, H, V)
+    lg = ml.reshape(B, T, H, L)
+    mix = lg.sigmoid() if gated else lg.softmax(-1)
+    return qn, kn, g0, b0, w0, mix
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("L,K,V,horizon,gated", [(3, 128, 128, None, False), (2, 64, 64, 16, True),
+                                                 (1, 64, 128, None, False), (4, 128, 64, 8, False)])
+def test_gate_prologue_matches_torch(dtype, L, K, V, horizon, gated):
+    from nested_recurrent_memory_amd.layer_ops import gate_prep
+    print(f"gate_prep dtype={dtype} L={L} K={K} V={V} horizon={horizon} gated={gated}", flush=True)
+    g = _gen(L * K + V)
+    B, T, H = 2, 37, 3
+    raw = [torch.randn(B, T, n, generator=g).to(dtype) for n in
+           (L * H * K, H * K, H * K, H * K, H * V, H * L)]
+    raw[2] = raw[2] * 3                     # f: reach both softplus branches and the cap
+    raw[2][0, 0, :5] = 25.0
+    A_log = torch.log(torch.empty(H).uniform_(1, 16, generator=g))
+    dt_bias = torch.randn(H * K, generator=g) * 0.5
+    cots = [torch.randn(s, generator=g) for s in
+            ((B, T, H, L, K), (B, T, H, K), (B, T, H, K), (B, T, H, K), (B, T, H, V), (B, T, H, L))]
+
+    r64 = [t.double().requires_grad_() for t in raw]
+    p64 = [A_log.double().requires_grad_(), dt_bias.double().requires_grad_()]
+    outs64 = _prologue_ref(*r64, *p64, L, H, K, V, horizon, gated)
+    sum((o * c.double()).sum() for o, c in zip(outs64, cots)).backward()
+
+    rd = [t.to(DEV).requires_grad_() for t in raw]
+    pd = [A_log.to(DEV).requires_grad_(), dt_bias.to(DEV).requires_grad_()]
+    outs = gate_prep(*rd, *pd, L, H, K, V, max_horizon=horizon, sigmoid_mix=gated)
+    sum((o.float() * c.to(DEV)).sum() for o, c in zip(outs, cots)).backward()
+    torch.cuda.synchronize()
+    names = ("qn", "kn", "g0", "b0", "w0", "mix")
+    for n, o, o64 in zip(names, outs, outs64):
+        _close(n, o, o64, dtype if n != "g0" else torch.float32)
+    for n, t, t64 in zip(("dq", "dk", "df", "dbz", "dwz", "dml"), rd, r64):
+        _close(n, t.grad, t64.grad, dtype)
+    _close("dA_log", pd[0].grad, p64[0].grad, torch.float32)
+    _close("ddt_bias", pd[1].grad, p64[1].grad, torch.float32)
 
 
 # ----------------------------------------------------------------- the layer
