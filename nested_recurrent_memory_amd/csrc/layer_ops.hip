@@ -11,6 +11,8 @@
 // call with a cache output writes the last W inputs of [cache; x] there.
 // FusedRMSNormGated, per row of V values:
 //   y = x rstd w sigmoid(g),   rstd = 1 / sqrt(mean(x^2) + eps)
+#include <numeric>
+
 #include "ngdn_kernels.h"
 
 namespace ngdn {
@@ -325,109 +327,182 @@ __device__ __forceinline__ float dsoftplus20(float z) { return z > 20.f ? 1.f : 
 
 }  // namespace
 
-// One wave per (b, t, h), lane j holding elements j*KPL .. j*KPL+KPL-1 of a
-// K row (V row: VPL); blockIdx.y is the head, so a workgroup's 4 waves are 4
-// consecutive tokens of one head.
-template <typename E, typename P, int K, int V>
+// One wave per (b, t, h), heads fastest, so a workgroup's 4 waves read
+// neighbouring parts of the same token's rows. Every access is 16 bytes: a K row is
+// VK = K/8 lanes, so the L + 1 rows to normalise (q's levels, then k) take
+// (L+1) VK lanes (one pass for L = 3, K = 128), and the f, bz, wz rows sit
+// side by side in lanes [0, VK), [VK, 2 VK), [2 VK, 2 VK + V/8).
+template <int G>
+__device__ __forceinline__ float gsum(float v) {   // sum over aligned groups of G lanes
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+// A wave takes GP_TPW consecutive token-heads and issues every load of all
+// of them before the first use (each lane's row vectors to normalise, NP
+// passes of 64 vectors; its gate vector; its mix logit): one token-head per
+// wave left each wave two dependent memory round trips for 4 KB and ran at
+// under half the copy rate.
+constexpr int GP_TPW = 4;
+
+template <typename E, typename P, int K, int V, int NP>
 __global__ __launch_bounds__(256) void gate_prep_fwd_kernel(GatePrepArgs a) {
-  constexpr int KPL = K / WAVE, VPL = V / WAVE;
-  const int h = blockIdx.y, H = a.H, L = a.L, lane = lane_id();
-  const long long bt = (long long)blockIdx.x * 4 + wave_id();
-  if (bt >= a.BT) return;
-  const long long th = bt * H + h;                 // token-head
-  // q: L rows, transposed from (l h) to (h l); k: one row
-  for (int l = 0; l <= L; ++l) {
-    const E* src = l < L ? static_cast<const E*>(a.q) + (bt * L + l) * H * K + (size_t)h * K
-                         : static_cast<const E*>(a.k) + th * K;
-    E* dst = l < L ? static_cast<E*>(a.qn) + (th * L + l) * K : static_cast<E*>(a.kn) + th * K;
-    float x[KPL], ss = 0.f;
+  constexpr int VK = K / 8, VV = V / 8;
+  const int H = a.H, L = a.L, lane = lane_id();
+  const long long th0 = ((long long)blockIdx.x * 4 + wave_id()) * GP_TPW, nth = a.BT * H;
+  if (th0 >= nth) return;
+  const bool isf = lane < VK, isb = !isf && lane < 2 * VK, isw = !isf && !isb && lane < 2 * VK + VV;
+  float x[GP_TPW][NP][8], z[GP_TPW][8], zm[GP_TPW];
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) { x[j] = to_f(src[lane * KPL + j]); ss += x[j] * x[j]; }
-    const float inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
+  for (int j = 0; j < GP_TPW; ++j) {
+    const long long th = th0 + j, bt = th / H;
+    const int h = (int)(th % H);
+    const bool live = th < nth;
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) dst[lane * KPL + j] = from_f<E>(x[j] * inv);
+    for (int p = 0; p < NP; ++p) {
+      const int r = (p * WAVE + lane) / VK, c = (p * WAVE + lane) % VK * 8;
+      if (live && r <= L) {
+        const E* src = r < L ? static_cast<const E*>(a.q) + (bt * L + r) * H * K + (size_t)h * K
+                             : static_cast<const E*>(a.k) + th * K;
+        load8f(src + c, x[j][p]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][p][e] = 0.f;
+      }
+    }
+    const size_t go = isf ? th * K + (size_t)lane * 8
+                    : isb ? th * K + (size_t)(lane - VK) * 8 : th * V + (size_t)(lane - 2 * VK) * 8;
+    if (live && (isf || isb || isw)) {
+      load8f(static_cast<const E*>(isf ? a.f : isb ? a.bz : a.wz) + go, z[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[j][e] = 0.f;
+    }
+    zm[j] = live && lane < L ? to_f(static_cast<const E*>(a.ml)[th * L + lane]) : -INFINITY;
   }
-  // decay and gates
-  const float A = __expf(ldp<P>(a.A_log, h));
 #pragma unroll
-  for (int j = 0; j < KPL; ++j) {
-    const int c = lane * KPL + j;
-    const float z = to_f(static_cast<const E*>(a.f)[th * K + c]) + ldp<P>(a.dt_bias, (size_t)h * K + c);
-    a.g0[th * K + c] = fminf(-A * softplus20(z), a.cap);
-    static_cast<E*>(a.b0)[th * K + c] = from_f<E>(sigmoid_fast(to_f(static_cast<const E*>(a.bz)[th * K + c])));
-  }
+  for (int j = 0; j < GP_TPW; ++j) {
+    const long long th = th0 + j;
+    if (th >= nth) break;
+    const int h = (int)(th % H);
+    // q's L rows, transposed from (l h) to (h l), and k: x / max(|x|, eps)
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int c = lane * VPL + j;
-    static_cast<E*>(a.w0)[th * V + c] = from_f<E>(sigmoid_fast(to_f(static_cast<const E*>(a.wz)[th * V + c])));
-  }
-  // mix over the L levels in lanes 0..L-1
-  if (lane < 8) {
-    const float z = lane < L ? to_f(static_cast<const E*>(a.ml)[th * L + lane]) : -INFINITY;
-    // every one of the 8 lanes takes part in the shuffles (a shuffle reads
-    // the source lane's register, which must be active)
-    const float mx = max8(z);
-    const float e = lane < L ? __expf(z - mx) : 0.f;
-    const float den = sum8(e);
-    const float m = a.sigmoid_mix ? sigmoid_fast(z) : e / den;
-    if (lane < L) static_cast<E*>(a.mix)[th * L + lane] = from_f<E>(m);
+    for (int p = 0; p < NP; ++p) {
+      const int r = (p * WAVE + lane) / VK, c = (p * WAVE + lane) % VK * 8;
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[j][p][e] * x[j][p][e];
+      const float inv = 1.f / fmaxf(sqrtf(gsum<VK>(ss)), 1e-12f);
+      if (r <= L) {
+        E* dst = r < L ? static_cast<E*>(a.qn) + (th * L + r) * K : static_cast<E*>(a.kn) + th * K;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][p][e] *= inv;
+        store8f(dst + c, x[j][p]);
+      }
+    }
+    // decay (lanes [0, VK)), b gate ([VK, 2 VK)), w gate ([2 VK, 2 VK + VV))
+    const size_t go = isf ? th * K + (size_t)lane * 8
+                    : isb ? th * K + (size_t)(lane - VK) * 8 : th * V + (size_t)(lane - 2 * VK) * 8;
+    if (isf) {
+      const int c = lane * 8;
+      const float A = __expf(ldp<P>(a.A_log, h));
+      f4 g[2];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        g[e / 4][e % 4] = fminf(-A * softplus20(z[j][e] + ldp<P>(a.dt_bias, (size_t)h * K + c + e)), a.cap);
+      *reinterpret_cast<f4*>(a.g0 + go) = g[0];
+      *reinterpret_cast<f4*>(a.g0 + go + 4) = g[1];
+    } else if (isb || isw) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[j][e] = sigmoid_fast(z[j][e]);
+      store8f(static_cast<E*>(isb ? a.b0 : a.w0) + go, z[j]);
+    }
+    // mix over the L levels in lanes 0..7 (all 8 take part in the shuffles)
+    if (lane < 8) {
+      const float mx = max8(zm[j]);
+      const float e = lane < L ? __expf(zm[j] - mx) : 0.f;
+      const float den = sum8(e);
+      const float m = a.sigmoid_mix ? sigmoid_fast(zm[j]) : e / den;
+      if (lane < L) static_cast<E*>(a.mix)[th * L + lane] = from_f<E>(m);
+    }
   }
 }
 
-// Backward, same mapping; waves walk tokens grid-stride so the decay
-// parameters' gradients collect in registers, then one partial row per
-// workgroup.
+// Backward, same mapping; waves walk token-heads grid-stride with a stride
+// that is a multiple of H, so each wave keeps one head and its decay
+// parameters' gradients collect in registers; then one partial row per
+// workgroup (zeros for the heads none of its waves had).
 template <typename E, typename P, int K, int V>
 __global__ __launch_bounds__(256) void gate_prep_bwd_kernel(GatePrepArgs a) {
-  constexpr int KPL = K / WAVE, VPL = V / WAVE;
+  constexpr int VK = K / 8, VV = V / 8;
   __shared__ float s_dt[4][K], s_da[4];
-  const int h = blockIdx.y, H = a.H, L = a.L, lane = lane_id(), wv = wave_id();
+  const int H = a.H, L = a.L, lane = lane_id(), wv = wave_id();
+  const long long th0 = (long long)blockIdx.x * 4 + wv, stride = (long long)gridDim.x * 4;
+  const int h = (int)(th0 % H);
   const float A = __expf(ldp<P>(a.A_log, h));
-  float ddt[KPL], dA = 0.f;
+  float ddt[8], dA = 0.f, dtb[8];
 #pragma unroll
-  for (int j = 0; j < KPL; ++j) ddt[j] = 0.f;
-  for (long long bt = (long long)blockIdx.x * 4 + wv; bt < a.BT; bt += (long long)gridDim.x * 4) {
-    const long long th = bt * H + h;
-    for (int l = 0; l <= L; ++l) {
-      const size_t xo = l < L ? (bt * L + l) * H * K + (size_t)h * K : th * K;
-      const size_t yo = l < L ? (th * L + l) * K : th * K;
-      const E* src = static_cast<const E*>(l < L ? a.q : a.k) + xo;
-      const E* dy = static_cast<const E*>(l < L ? a.dqn : a.dkn) + yo;
-      E* dx = static_cast<E*>(l < L ? a.dq : a.dk) + xo;
-      float x[KPL], g[KPL], ss = 0.f, xg = 0.f;
+  for (int e = 0; e < 8; ++e) {
+    ddt[e] = 0.f;
+    dtb[e] = lane < VK ? ldp<P>(a.dt_bias, (size_t)h * K + lane * 8 + e) : 0.f;
+  }
+  for (long long th = th0; th < a.BT * H; th += stride) {
+    const long long bt = th / H;
+    for (int base = 0; base < (L + 1) * VK; base += WAVE) {
+      const int r = (base + lane) / VK, c = (base + lane) % VK * 8;
+      const bool live = r <= L;
+      const size_t xo = r < L ? (bt * L + r) * H * K + (size_t)h * K : th * K;
+      const size_t yo = r < L ? (th * L + r) * K : th * K;
+      float x[8], g[8], ss = 0.f, xg = 0.f;
+      if (live) {
+        load8f(static_cast<const E*>(r < L ? a.q : a.k) + xo + c, x);
+        load8f(static_cast<const E*>(r < L ? a.dqn : a.dkn) + yo + c, g);
+      } else {
 #pragma unroll
-      for (int j = 0; j < KPL; ++j) {
-        x[j] = to_f(src[lane * KPL + j]);
-        g[j] = to_f(dy[lane * KPL + j]);
-        ss += x[j] * x[j];
-        xg += x[j] * g[j];
+        for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
       }
-      const float n = sqrtf(wave_sum(ss));
-      xg = wave_sum(xg);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { ss += x[e] * x[e]; xg += x[e] * g[e]; }
+      const float n = sqrtf(gsum<VK>(ss));
+      xg = gsum<VK>(xg);
       // y = x / max(n, eps): dx = dy / n - x <x, dy> / n^3 above eps, dy / eps below
       const float inv = 1.f / fmaxf(n, 1e-12f);
-      const float c = n > 1e-12f ? xg * inv * inv * inv : 0.f;
+      const float cc = n > 1e-12f ? xg * inv * inv * inv : 0.f;
+      if (live) {
 #pragma unroll
-      for (int j = 0; j < KPL; ++j) dx[lane * KPL + j] = from_f<E>(g[j] * inv - x[j] * c);
+        for (int e = 0; e < 8; ++e) g[e] = g[e] * inv - x[e] * cc;
+        store8f(static_cast<E*>(r < L ? a.dq : a.dk) + xo + c, g);
+      }
     }
+    if (lane < VK) {
+      const int c = lane * 8;
+      float f[8], df[8];
+      load8f(static_cast<const E*>(a.f) + th * K + c, f);
+      const f4 d0 = *reinterpret_cast<const f4*>(a.dg0 + th * K + c);
+      const f4 d1 = *reinterpret_cast<const f4*>(a.dg0 + th * K + c + 4);
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-      const int c = lane * KPL + j;
-      const float z = to_f(static_cast<const E*>(a.f)[th * K + c]) + ldp<P>(a.dt_bias, (size_t)h * K + c);
-      const float gu = -A * softplus20(z);
-      const float dg = gu <= a.cap ? a.dg0[th * K + c] : 0.f;   // clamp(max=cap) passes at equality
-      dA += dg * gu;
-      const float dz = -A * dg * dsoftplus20(z);
-      static_cast<E*>(a.df)[th * K + c] = from_f<E>(dz);
-      ddt[j] += dz;
-      const float s = sigmoid_fast(to_f(static_cast<const E*>(a.bz)[th * K + c]));
-      static_cast<E*>(a.dbz)[th * K + c] = from_f<E>(to_f(static_cast<const E*>(a.db0)[th * K + c]) * s * (1.f - s));
-    }
+      for (int e = 0; e < 8; ++e) {
+        const float z = f[e] + dtb[e];
+        const float gu = -A * softplus20(z);
+        const float dg = gu <= a.cap ? (e < 4 ? d0[e] : d1[e - 4]) : 0.f;   // clamp(max) passes at equality
+        dA += dg * gu;
+        df[e] = -A * dg * dsoftplus20(z);
+        ddt[e] += df[e];
+      }
+      store8f(static_cast<E*>(a.df) + th * K + c, df);
+    } else if (lane < 2 * VK + VV) {
+      const bool isb = lane < 2 * VK;
+      const size_t o = isb ? th * K + (size_t)(lane - VK) * 8 : th * V + (size_t)(lane - 2 * VK) * 8;
+      float z[8], d[8];
+      load8f(static_cast<const E*>(isb ? a.bz : a.wz) + o, z);
+      load8f(static_cast<const E*>(isb ? a.db0 : a.dw0) + o, d);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int c = lane * VPL + j;
-      const float s = sigmoid_fast(to_f(static_cast<const E*>(a.wz)[th * V + c]));
-      static_cast<E*>(a.dwz)[th * V + c] = from_f<E>(to_f(static_cast<const E*>(a.dw0)[th * V + c]) * s * (1.f - s));
+      for (int e = 0; e < 8; ++e) {
+        const float sg = sigmoid_fast(z[e]);
+        d[e] *= sg * (1.f - sg);
+      }
+      store8f(static_cast<E*>(isb ? a.dbz : a.dwz) + o, d);
     }
     if (lane < 8) {
       const float z = lane < L ? to_f(static_cast<const E*>(a.ml)[th * L + lane]) : -INFINITY;
@@ -443,21 +518,29 @@ __global__ __launch_bounds__(256) void gate_prep_bwd_kernel(GatePrepArgs a) {
   }
   // the decay parameters: waves -> LDS -> one partial row per workgroup
   dA = wave_sum(dA);
+  if (lane < VK) {
 #pragma unroll
-  for (int j = 0; j < KPL; ++j) s_dt[wv][lane * KPL + j] = ddt[j];
+    for (int e = 0; e < 8; ++e) s_dt[wv][lane * 8 + e] = ddt[e];
+  }
   if (lane == 0) s_da[wv] = dA;
   __syncthreads();
   const int n = H * K + H;
+  int hw[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) hw[w] = (int)(((long long)blockIdx.x * 4 + w) % H);
   float* row = a.ws ? a.ws + (size_t)blockIdx.x * n : nullptr;
-  for (int c = threadIdx.x; c < K; c += 256) {
-    const float v = s_dt[0][c] + s_dt[1][c] + s_dt[2][c] + s_dt[3][c];
-    if (row) row[(size_t)h * K + c] = v;
-    else atomicAdd(&a.dpar[(size_t)h * K + c], v);
-  }
-  if (threadIdx.x == 0) {
-    const float v = s_da[0] + s_da[1] + s_da[2] + s_da[3];
-    if (row) row[(size_t)H * K + h] = v;
-    else atomicAdd(&a.dpar[(size_t)H * K + h], v);
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const int hh = j < H * K ? j / K : j - H * K;
+    float v = 0.f;
+    bool any = false;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (hw[w] != hh) continue;
+      v += j < H * K ? s_dt[w][j % K] : s_da[w];
+      any = true;
+    }
+    if (row) row[j] = v;
+    else if (any) atomicAdd(&a.dpar[j], v);
   }
 }
 
@@ -489,17 +572,45 @@ static bool gate_prep_ok(const GatePrepArgs& a) {
 hipError_t gate_prep_fwd(const GatePrepArgs& a, int dtype, hipStream_t st) {
   if (!gate_prep_ok(a)) return hipErrorInvalidValue;
   if (a.BT == 0) return hipSuccess;
-  NGDN_GP_DISPATCH(gate_prep_fwd_kernel, dim3((unsigned)((a.BT + 3) / 4), (unsigned)a.H));
+  const dim3 grid((unsigned)((a.BT * a.H + 4 * GP_TPW - 1) / (4 * GP_TPW)));
+  const int np = ((a.L + 1) * (a.K / 8) + WAVE - 1) / WAVE;
+  auto go = [&](auto e, auto p, auto kk, auto vv, auto npc) {
+    hipLaunchKernelGGL((gate_prep_fwd_kernel<decltype(e), decltype(p), decltype(kk)::value,
+                                             decltype(vv)::value, decltype(npc)::value>),
+                       grid, dim3(256), 0, st, a);
+  };
+  using I64 = std::integral_constant<int, 64>;
+  using I128 = std::integral_constant<int, 128>;
+  auto pick_np = [&](auto e, auto p, auto kk, auto vv) {
+    if (np == 1) go(e, p, kk, vv, std::integral_constant<int, 1>{});
+    else if (np == 2) go(e, p, kk, vv, std::integral_constant<int, 2>{});
+    else go(e, p, kk, vv, std::integral_constant<int, 3>{});
+  };
+  auto pick_kv = [&](auto e, auto p) {
+    if (a.K == 64 && a.V == 64) pick_np(e, p, I64{}, I64{});
+    else if (a.K == 64 && a.V == 128) pick_np(e, p, I64{}, I128{});
+    else if (a.K == 128 && a.V == 64) pick_np(e, p, I128{}, I64{});
+    else pick_np(e, p, I128{}, I128{});
+  };
+  auto pick_p = [&](auto e) {
+    if (a.pdtype == NGDN_BF16) pick_kv(e, bf16{}); else pick_kv(e, float{});
+  };
+  if (dtype == NGDN_BF16) pick_p(bf16{}); else pick_p(float{});
   return hipGetLastError();
 }
 
 hipError_t gate_prep_bwd(const GatePrepArgs& a, int dtype, hipStream_t st) {
   if (!gate_prep_ok(a)) return hipErrorInvalidValue;
   if (a.BT == 0) return hipSuccess;
-  // about 8 tokens per wave, at most NGDN_WPARTS partial rows
-  long long nb = (a.BT + 31) / 32;
+  // about 8 token-heads per wave, at most NGDN_WPARTS partial rows, and a
+  // wave stride (4 nb) that is a multiple of H
+  const long long m = a.H / std::gcd(a.H, 4);
+  long long nb = (a.BT * a.H + 31) / 32;
   if (nb > NGDN_WPARTS) nb = NGDN_WPARTS;
-  NGDN_GP_DISPATCH(gate_prep_bwd_kernel, dim3((unsigned)nb, (unsigned)a.H));
+  nb = (nb + m - 1) / m * m;
+  if (nb > NGDN_WPARTS) nb -= m;
+  if (nb < m) return hipErrorInvalidValue;    // H beyond 4 NGDN_WPARTS
+  NGDN_GP_DISPATCH(gate_prep_bwd_kernel, dim3((unsigned)nb));
   if (hipError_t e = hipGetLastError()) return e;
   return a.ws ? sum_parts(a.ws, nb, (long long)a.H * a.K + a.H, a.dpar, st) : hipSuccess;
 }

@@ -149,7 +149,8 @@ def _prologue_ref(q, k, f, bz, wz, ml, A_log, dt_bias, L, H, K, V, max_horizon, 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("L,K,V,horizon,gated", [(3, 128, 128, None, False), (2, 64, 64, 16, True),
-                                                 (1, 64, 128, None, False), (4, 128, 64, 8, False)])
+                                                 (1, 64, 128, None, False), (4, 128, 64, 8, False),
+                                                 (8, 128, 128, 32, True), (7, 64, 64, None, False)])
 def test_gate_prologue_matches_torch(dtype, L, K, V, horizon, gated):
     from nested_recurrent_memory_amd.layer_ops import gate_prep
     print(f"gate_prep dtype={dtype} L={L} K={K} V={V} horizon={horizon} gated={gated}", flush=True)
