@@ -407,10 +407,12 @@ __global__ __launch_bounds__(256) void gate_prep_fwd_kernel(GatePrepArgs a) {
     if (isf) {
       const int c = lane * 8;
       const float A = __expf(ldp<P>(a.A_log, h));
+      float dtv[8];
+      load8f(static_cast<const P*>(a.dt_bias) + (size_t)h * K + c, dtv);
       f4 g[2];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        g[e / 4][e % 4] = fminf(-A * softplus20(z[j][e] + ldp<P>(a.dt_bias, (size_t)h * K + c + e)), a.cap);
+        g[e / 4][e % 4] = fminf(-A * softplus20(z[j][e] + dtv[e]), a.cap);
       *reinterpret_cast<f4*>(a.g0 + go) = g[0];
       *reinterpret_cast<f4*>(a.g0 + go + 4) = g[1];
     } else if (isb || isw) {
@@ -443,10 +445,8 @@ __global__ __launch_bounds__(256) void gate_prep_bwd_kernel(GatePrepArgs a) {
   const float A = __expf(ldp<P>(a.A_log, h));
   float ddt[8], dA = 0.f, dtb[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    ddt[e] = 0.f;
-    dtb[e] = lane < VK ? ldp<P>(a.dt_bias, (size_t)h * K + lane * 8 + e) : 0.f;
-  }
+  for (int e = 0; e < 8; ++e) ddt[e] = dtb[e] = 0.f;
+  if (lane < VK) load8f(static_cast<const P*>(a.dt_bias) + (size_t)h * K + lane * 8, dtb);
   for (long long th = th0; th < a.BT * H; th += stride) {
     const long long bt = th / H;
     for (int base = 0; base < (L + 1) * VK; base += WAVE) {
