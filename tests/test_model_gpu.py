@@ -186,6 +186,25 @@ def test_model_training_step_matches_oracle(mode, promotion):
         _near(f"d{name}", p.grad, p64[name].grad, 0.15 if decay else gtol)
 
 
+def test_model_options_match_oracle():
+    """No short convolution, sigmoid level mix, a decay horizon, tied
+    embeddings off, 2 levels firing every other chunk: fp32 loss and every
+    gradient."""
+    cfg = _cfg(num_levels=2, firing_intervals=(1, 2), n_queries_per_level=(32,),
+               use_short_conv=False, read_mix="sigmoid", max_horizon=64, promotion="merge")
+    m, p64 = _model(cfg, 13)
+    m.train()
+    ids = torch.randint(0, cfg.vocab_size, (2, 256), generator=_gen(14))
+    _, loss64, _ = mref.model_forward(p64, ids, cfg, labels=ids)
+    loss64.backward()
+    out = m(input_ids=ids.to(DEV), labels=ids.to(DEV))
+    out.loss.backward()
+    torch.cuda.synchronize()
+    _near("loss", out.loss, loss64, 1e-4)
+    for name, p in m.named_parameters():
+        _near(f"d{name}", p.grad, p64[name].grad, 1e-4)
+
+
 def test_model_eval_logits_and_loss_path():
     cfg = _cfg(num_levels=2, firing_intervals=(1, 2), n_queries_per_level=(16,))
     m, p64 = _model(cfg, 5)
