@@ -97,15 +97,17 @@ def lib():
 TIMING = None
 
 
-def call(name, *args, tag=None):
+def call(name, *args, tag=None, stream=None):
     """Calls entry point ``name``; raises NgdnError on a nonzero status.
-    ``tag`` names the call in TIMING (default: the entry point)."""
+    ``tag`` names the call in TIMING (default: the entry point); ``stream``
+    is the torch stream the call launches on when it is not the current one
+    (the timing events go on that stream)."""
     if TIMING is not None:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        start.record()
+        start.record(stream)
         rc = getattr(lib(), name)(*args)
-        end.record()
+        end.record(stream)
         TIMING.setdefault(tag or name, []).append((start, end))
     else:
         rc = getattr(lib(), name)(*args)

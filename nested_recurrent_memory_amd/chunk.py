@@ -92,6 +92,16 @@ def _side_streams(dev, n):
     return _STREAMS[key]
 
 
+def _aux_streams(dev):
+    """Two streams (default priority) for independent launches inside one
+    backward: the reads' backward next to the top level's scan, and the
+    parameter-gradient sums next to the rest of the chain."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), "aux")
+    if key not in _STREAMS:
+        _STREAMS[key] = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    return _STREAMS[key]
+
+
 def _run_groups(B, dev, launch):
     """Calls launch(b0, nb, stream) for each group of batch rows: on the
     current stream when there is one group, else on side streams forked from
@@ -275,15 +285,31 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         R = _rows(b0, nb)
         sp = _lib.ptr_of_stream(st)
         d = _lib.dims(nb, T, H, L, K, V, code, scale)
+        # With one group of rows, independent launches go to two side streams:
+        # (a) dmix_0 and the reads' backward of the levels below the top one
+        # (each writes its own columns of dmix and dq and its own d_states)
+        # beside the top level's read and reverse scan, joined before the top
+        # level's probe backward adds into the level below's d_states; (b) each
+        # level's parameter-gradient sums (reading only that level's
+        # workspaces) beside the rest of the chain, joined at the end.
+        aux = _aux_streams(dev) if (L > 1 and nb == B) else None
+        if aux is not None:
+            fork = st.record_event()
+            for a in aux:
+                a.wait_event(fork)
+        ta, tb = (aux[0], aux[1]) if aux else (st, st)
+        sa, sb = _lib.ptr_of_stream(ta), _lib.ptr_of_stream(tb)
         # reads: dmix for every level (level 0 from the stored read), dq and the
         # group-state gradients for levels >= 1
         _lib.call("ngdn_output_bwd", ctypes.byref(d), P(R(sv["read0"])), P(R(do_)),
-                  P(R(dmix)), sp)
+                  P(R(dmix)), sa, stream=ta)
         for lvl in range(1, L):
             ng = n_groups(NT, f[lvl])
+            top = lvl == L - 1
             _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng,
                       *(P(R(x)) for x in (q_, mix_, do_, states[lvl], d_states[lvl], dq, dmix)),
-                      sp, tag=f"ngdn_read_state_bwd.{lvl}")
+                      sp if top else sa, tag=f"ngdn_read_state_bwd.{lvl}", stream=st if top else ta)
+        joined = aux is None
         inj, nf1 = None, 0
         for lvl in range(L - 1, 0, -1):
             lv, wk = levels[lvl], work[lvl]
@@ -302,6 +328,9 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                 b_kv, b_vk = states[lvl - 1], sv["statesT"][lvl - 1]
                 ngb, d_below = n_groups(NT, fb), d_states[lvl - 1]
             ws = wk["ws"]
+            if not joined:
+                st.wait_stream(aux[0])
+                joined = True
             _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
                       P(R(b_kv)), P(R(b_vk)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
                       P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
@@ -310,9 +339,13 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                       P(R(wk["dSp"])), P(R(wk["dvn"])), *(P(R(x)) for x in ws), P(dqb),
                       P(R(wk["inj"])), P(R(d_below)), P(R(d_final)), sp,
                       tag=f"ngdn_probe_bwd.{lvl}")
+            if aux is not None:
+                aux[1].wait_stream(st)
             _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf,
-                      *(P(R(x)) for x in ws[:5]), P(dkp), P(dbp), P(dwp), P(dgp), sp,
-                      tag=f"ngdn_param_grads.{lvl}")
+                      *(P(R(x)) for x in ws[:5]), P(dkp), P(dbp), P(dwp), P(dgp), sb,
+                      tag=f"ngdn_param_grads.{lvl}", stream=tb)
+        if not joined:
+            st.wait_stream(aux[0])
         # level 0
         _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
             "Kt", "WT", "gam", "AqkT", "QgT")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
@@ -323,6 +356,8 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), *(P(R(x)) for x in (
             q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], dQg, dWT, dKt, dAqk, dgam,
             dVnT0, dq, dk, dv, dg, db, dw)), sp)
+        if aux is not None:
+            st.wait_stream(aux[1])
 
     _run_groups(B, dev, launch)
     return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
