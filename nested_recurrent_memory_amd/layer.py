@@ -163,10 +163,12 @@ class NestedGDN2Attention(nn.Module):
                            else (None, x.new_zeros(B, dtype=torch.long)))
         BT = cfg.op_chunk_size
         # whole chunks from an aligned position run chunkwise, the rest steps
-        # (the chunk form fires on a partial last chunk, the step form does not).
-        # Without a cache the position is 0: no device read (a host
-        # synchronisation per layer would stall the launch queue in training)
-        aligned = last is None or bool((position % BT == 0).all())
+        # (the chunk form fires on a partial last chunk, the step form does
+        # not). The position is read back to the host only when it matters:
+        # without a cache it is 0, and a call shorter than a chunk (a decoding
+        # step) steps whatever it is; a host synchronisation per layer would
+        # stall the launch queue
+        aligned = T >= BT and (last is None or bool((position % BT == 0).all()))
         n_chunked = (T // BT) * BT if aligned else 0
         parts = []
         if n_chunked:
