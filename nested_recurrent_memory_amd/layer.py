@@ -34,7 +34,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .chunk import chunk_nested_gdn2
-from .layer_ops import FusedRMSNormGated, ShortConvolution, gate_prep
+from .layer_ops import FusedRMSNormGated, ShortConvolution, fanout, gate_prep
 from .step import step_nested_gdn2
 
 __all__ = ["NestedGDN2LayerConfig", "NestedGDN2Attention"]
@@ -136,20 +136,23 @@ class NestedGDN2Attention(nn.Module):
         last = past_key_values.get(self.layer_idx) if past_key_values is not None else None
         conv = last.get("conv_state") if last is not None else None
         conv_q, conv_k, conv_v = conv if conv is not None else (None, None, None)
+        # x feeds eight linear maps: one autocast cast of it for all of them
+        xq, xk, xv, xf, xb, xw, xm, xg = fanout(x, 8)
         if cfg.use_short_conv:
-            q, conv_q = self.q_conv1d(self.q_proj(x), cache=conv_q, output_final_state=use_cache)
-            k, conv_k = self.k_conv1d(self.k_proj(x), cache=conv_k, output_final_state=use_cache)
-            v, conv_v = self.v_conv1d(self.v_proj(x), cache=conv_v, output_final_state=use_cache)
+            q, conv_q = self.q_conv1d(self.q_proj(xq), cache=conv_q, output_final_state=use_cache)
+            k, conv_k = self.k_conv1d(self.k_proj(xk), cache=conv_k, output_final_state=use_cache)
+            v, conv_v = self.v_conv1d(self.v_proj(xv), cache=conv_v, output_final_state=use_cache)
         else:
-            q, k, v = (F.silu(p(x)) for p in (self.q_proj, self.k_proj, self.v_proj))
+            q, k, v = (F.silu(p(xi)) for p, xi in ((self.q_proj, xq), (self.k_proj, xk),
+                                                    (self.v_proj, xv)))
         v = v.reshape(B, T, H, V)
         # q -> [B,T,H,L,K] and k L2-normalised, the decay g0 (fp32), gates b0,
         # w0 and the level mix, in one kernel (layers/nested_gdn2.py:134-166)
         gated = cfg.read_mix == "sigmoid"
         wd = v.dtype
         q, k, g0, b0, w0, mix = gate_prep(
-            q.to(wd), k.to(wd), self.f_proj(x).to(wd), self.b_proj(x).to(wd),
-            self.w_proj(x).to(wd), self.mix_proj(x).to(wd), self.A_log, self.dt_bias,
+            q.to(wd), k.to(wd), self.f_proj(xf).to(wd), self.b_proj(xb).to(wd),
+            self.w_proj(xw).to(wd), self.mix_proj(xm).to(wd), self.A_log, self.dt_bias,
             L, H, K, V, max_horizon=cfg.max_horizon, sigmoid_mix=gated)
         keep = getattr(cfg, "read_levels", None)   # eval-time read ablation (not a config field)
         if keep is not None:
@@ -197,5 +200,5 @@ class NestedGDN2Attention(nn.Module):
                 "recurrent_state": (state, position),
                 "conv_state": (conv_q, conv_k, conv_v) if cfg.use_short_conv else None,
             }
-        o = self.o_norm(o, self.g_proj(x).reshape(B, T, H, V))
+        o = self.o_norm(o, self.g_proj(xg).reshape(B, T, H, V))
         return self.o_proj(o.reshape(B, T, H * V)), None, past_key_values

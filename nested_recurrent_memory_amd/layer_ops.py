@@ -24,7 +24,8 @@ import torch.nn as nn
 
 from . import _lib
 
-__all__ = ["ShortConvolution", "FusedRMSNormGated", "short_conv", "rmsnorm_gated", "gate_prep"]
+__all__ = ["ShortConvolution", "FusedRMSNormGated", "short_conv", "rmsnorm_gated", "gate_prep",
+           "fanout"]
 
 
 def _code(t):
@@ -192,6 +193,37 @@ class _GatePrepFn(torch.autograd.Function):
         res = [d.to(t) for d, t in zip(dins, ctx.dtypes[:6])]
         return (*res, dpar[H * K:].to(A_d), dpar[:H * K].to(dt_d),
                 None, None, None, None, None, None)
+
+
+class _Fanout(torch.autograd.Function):
+    """x cast once to the autocast dtype for n consumers (aliases of one
+    tensor); their gradients summed in fp32 and returned in x's dtype. The
+    same values and the same fp32 sum as n autocast casts of x, without the
+    n casts forward, n casts back and n - 1 separate additions."""
+
+    @staticmethod
+    def forward(ctx, x, n, dtype):
+        ctx.xdtype = x.dtype
+        y = x.to(dtype)
+        return tuple(y.view_as(y) for _ in range(n))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        acc = None
+        for g in grads:
+            if g is None:
+                continue
+            acc = g.float() if acc is None else acc.add_(g)
+        return (acc.to(ctx.xdtype) if acc is not None else None), None, None
+
+
+def fanout(x, n):
+    """n inputs for n linear maps of x: under autocast with x in fp32, one
+    cast shared (see _Fanout); otherwise x itself, n times."""
+    if (x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") != torch.float32):
+        return _Fanout.apply(x, n, torch.get_autocast_dtype("cuda"))
+    return (x,) * n
 
 
 def _gate_args(BT, H, L, K, V, pd, sigmoid_mix, cap, ins, A, dt):

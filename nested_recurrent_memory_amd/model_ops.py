@@ -23,6 +23,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from .layer_ops import fanout
 
 __all__ = ["RMSNorm", "GatedMLP", "FusedLinearCrossEntropyLoss", "rms_norm", "swiglu",
            "fused_linear_cross_entropy"]
@@ -158,7 +159,8 @@ class GatedMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x):
-        return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
+        xg, xu = fanout(x, 2)      # one autocast cast of x for both maps
+        return self.down_proj(swiglu(self.gate_proj(xg), self.up_proj(xu)))
 
 
 # ---------------------------------------------------------------- linear + cross entropy
