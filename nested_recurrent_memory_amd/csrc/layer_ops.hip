@@ -321,8 +321,19 @@ __device__ __forceinline__ float sum8(float v) {
 template <typename P> __device__ __forceinline__ float ldp(const void* p, size_t i) {
   return to_f(static_cast<const P*>(p)[i]);
 }
-// torch's softplus (beta 1, threshold 20) and its derivative
-__device__ __forceinline__ float softplus20(float z) { return z > 20.f ? z : log1pf(__expf(z)); }
+// torch's softplus (beta 1, threshold 20) and its derivative. log1p(e^z) as
+// max(z, 0) + log1p(t), t = e^-|z| in (0, 1], from the hardware exp and log;
+// log1p(t) = log(u) t / (u - 1) with u = 1 + t rounded (the quotient undoes
+// the rounding of u; Goldberg, "What every computer scientist should know
+// about floating-point arithmetic", 1991, theorem 4), a few ulp. The library
+// log1pf was several times the instructions of the rest of the prologue.
+__device__ __forceinline__ float softplus20(float z) {
+  if (z > 20.f) return z;
+  const float t = __expf(-fabsf(z));
+  const float u = 1.f + t;
+  const float l = u == 1.f ? t : __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.f));
+  return fmaxf(z, 0.f) + l;
+}
 __device__ __forceinline__ float dsoftplus20(float z) { return z > 20.f ? 1.f : sigmoid_fast(z); }
 
 }  // namespace
