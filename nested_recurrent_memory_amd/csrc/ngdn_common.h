@@ -407,10 +407,21 @@ __device__ __forceinline__ float fexp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+// The probes' gates, evaluated N K (or N V) times per firing: from the
+// hardware exp, log and reciprocal (a few ulp) rather than the library expf,
+// log1pf and an IEEE division, which cost several times the instructions.
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.f + fexp(-x));
+}
+// log(1 + e^x) with torch's threshold 20: max(x, 0) + log1p(t), t = e^-|x|;
+// log1p(t) = log(u) t / (u - 1) with u = 1 + t rounded (the quotient undoes
+// the rounding of u; Goldberg 1991, theorem 4)
 __device__ __forceinline__ float softplusf_(float x) {
-  // log(1 + e^x), stable on both tails
-  return x > 20.f ? x : log1pf(expf(x));
+  if (x > 20.f) return x;
+  const float t = fexp(-fabsf(x));
+  const float u = 1.f + t;
+  const float l = u == 1.f ? t : __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.f));
+  return fmaxf(x, 0.f) + l;
 }
 
 // Bounded per-block LDS reductions are written inline in the kernels; this is
