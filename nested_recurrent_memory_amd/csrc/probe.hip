@@ -216,7 +216,7 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
         float nr = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) nr += s_nrm[w][n];
-        key = ut[t][r] / fmaxf(sqrtf(nr), 1e-12f);
+        key = ut[t][r] * __builtin_amdgcn_rcpf(fmaxf(sqrtf(nr), 1e-12f));
       }
       kv4[r] = key;
       av4[r] = key * bt[t][r] * gam;

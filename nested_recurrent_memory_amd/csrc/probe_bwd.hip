@@ -212,7 +212,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   auto keyval = [&](int t, int rt, int r) -> float {
     const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
     if (MERGE) return n == k ? 1.f : 0.f;
-    return u[t][r] / fmaxf(sqrtf(s_nrm[n]), 1e-12f);
+    return u[t][r] * __builtin_amdgcn_rcpf(fmaxf(sqrtf(s_nrm[n]), 1e-12f));
   };
 
   // ---- 3. kb = keys * b into LDS; gam = e^g
@@ -348,11 +348,12 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
       if (!MERGE) {
         const float nr = sqrtf(s_nrm[n]);
-        const float key = u[t][r] / fmaxf(nr, 1e-12f);
+        const float rn = __builtin_amdgcn_rcpf(fmaxf(nr, 1e-12f));
+        const float key = u[t][r] * rn;
         // F.normalize: below the clamp the denominator is the constant eps
-        dut[t][r] = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) / nr : dkt[t][r] / 1e-12f;
+        dut[t][r] = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) * rn : dkt[t][r] * 1e12f;
       }
-      dxgt[t][r] = -(s_dg[k] / (float)N) * sigmoidf_(xg[t][r] - 4.f);
+      dxgt[t][r] = -(s_dg[k] * (1.f / (float)N)) * sigmoidf_(xg[t][r] - 4.f);
     }
   }
   FR qk[NKS], qb[NKS], qw[NKS], qg[NKS];

@@ -337,7 +337,7 @@ __device__ __forceinline__ void promote_level(const PromoteArgs& a, char* smem, 
         float nr = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) nr += s_nrm[w * N + n];
-        key = ut[t][r] / fmaxf(sqrtf(nr), 1e-12f);
+        key = ut[t][r] * __builtin_amdgcn_rcpf(fmaxf(sqrtf(nr), 1e-12f));
       }
       kv4[r] = key;
       sKB.put1(n * LDKB + k, key * bt[t][r]);
