@@ -357,6 +357,14 @@ int32_t ngdn_swiglu_fwd(int32_t dtype, int64_t n, const void* g, const void* u, 
 int32_t ngdn_swiglu_bwd(int32_t dtype, int64_t n, const void* g, const void* u, const void* dy,
                         void* dg, void* du, void* stream);
 
+/* out[i] = sum_{j < count} xs[j][i] in fp32, xs[j] in dtype, n % 8 == 0,
+ * 1 <= count <= 8 (xs a host array of device pointers). The gradient of a
+ * tensor that feeds several linear maps under autocast (the layer's eight
+ * projections of x): one pass instead of a cast and an addition per
+ * consumer. No counterpart in fla; it replaces autograd's accumulation. */
+int32_t ngdn_sum_f32(int32_t dtype, int32_t count, const void* const* xs, int64_t n, float* out,
+                     void* stream);
+
 /* The cross entropy of fla's FusedLinearCrossEntropyLoss
  * (models/modeling_nested_gdn2.py:230-239; mean over the labels that are not
  * ignore_index): row_loss[r] = (logsumexp(logits_r) - logits_r[labels_r]) /

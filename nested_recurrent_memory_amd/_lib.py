@@ -62,6 +62,7 @@ SIGNATURES = {
     "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 8,
     "ngdn_swiglu_fwd": [I32, I64] + [P] * 4,
     "ngdn_swiglu_bwd": [I32, I64] + [P] * 6,
+    "ngdn_sum_f32": [I32, I32, P, I64, P, P],
     "ngdn_cross_entropy": [I32, I64, I32, I32, P, P, P, P, I32, P],
 }
 _RESTYPES = {"ngdn_last_error": ctypes.c_char_p, "ngdn_arch": ctypes.c_char_p}

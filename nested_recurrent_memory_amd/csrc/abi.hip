@@ -659,6 +659,23 @@ int32_t ngdn_swiglu_bwd(int32_t dtype, int64_t n, const void* g, const void* u, 
   return launched(ngdn::swiglu_bwd(a, dtype, (hipStream_t)stream), "ngdn_swiglu_bwd");
 }
 
+int32_t ngdn_sum_f32(int32_t dtype, int32_t count, const void* const* xs, int64_t n, float* out,
+                     void* stream) {
+  g_err[0] = 0;
+  if (dtype != NGDN_F32 && dtype != NGDN_BF16) return fail(NGDN_EINVAL, "ngdn_sum_f32: dtype %d", dtype);
+  if (count < 1 || count > ngdn::SUM_MAX || n < 0 || n % 8 != 0)
+    return fail(NGDN_EINVAL, "ngdn_sum_f32: count=%d n=%lld (1 <= count <= 8, n a multiple of 8)",
+                count, (long long)n);
+  if (n > 0 && (!xs || !out)) return fail(NGDN_EINVAL, "ngdn_sum_f32: NULL tensor");
+  ngdn::SumArgs a{};
+  for (int j = 0; j < count; ++j) {
+    if (n > 0 && !xs[j]) return fail(NGDN_EINVAL, "ngdn_sum_f32: NULL input %d", j);
+    a.x[j] = xs[j];
+  }
+  a.out = out; a.n = n; a.count = count;
+  return launched(ngdn::sum_into_f32(a, dtype, (hipStream_t)stream), "ngdn_sum_f32");
+}
+
 int32_t ngdn_cross_entropy(int32_t dtype, int64_t rows, int32_t V, int32_t ignore_index,
                            void* logits, const int64_t* labels, const int64_t* n_valid,
                            float* row_loss, int32_t grad, void* stream) {

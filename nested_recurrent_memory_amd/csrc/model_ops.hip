@@ -269,6 +269,45 @@ hipError_t swiglu_bwd(const SwigluArgs& a, int dtype, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- sum into fp32
+
+template <typename E, int C>
+__global__ __launch_bounds__(256) void sum_f32_kernel(SumArgs a) {
+  const long long n8 = a.n / 8;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n8;
+       i += (long long)gridDim.x * 256) {
+    float v[C][8];
+#pragma unroll
+    for (int j = 0; j < C; ++j) load8f(static_cast<const E*>(a.x[j]) + i * 8, v[j]);
+    f4 o[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < C; ++j) acc += v[j][e];
+      o[e / 4][e % 4] = acc;
+    }
+    *reinterpret_cast<f4*>(a.out + i * 8) = o[0];
+    *reinterpret_cast<f4*>(a.out + i * 8 + 4) = o[1];
+  }
+}
+
+hipError_t sum_into_f32(const SumArgs& a, int dtype, hipStream_t st) {
+  if (a.n == 0) return hipSuccess;
+  if (a.count < 1 || a.count > SUM_MAX || a.n % 8 != 0) return hipErrorInvalidValue;
+  const long long want = (a.n / 8 + 255) / 256;
+  const dim3 grid((unsigned)(want < 8192 ? want : 8192));
+#define NGDN_SUM(CC)                                                                           \
+  if (a.count == CC) {                                                                         \
+    if (dtype == NGDN_BF16) hipLaunchKernelGGL((sum_f32_kernel<bf16, CC>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((sum_f32_kernel<float, CC>), grid, dim3(256), 0, st, a);         \
+    return hipGetLastError();                                                                  \
+  }
+  NGDN_SUM(1) NGDN_SUM(2) NGDN_SUM(3) NGDN_SUM(4) NGDN_SUM(5) NGDN_SUM(6) NGDN_SUM(7) NGDN_SUM(8)
+#undef NGDN_SUM
+  return hipErrorInvalidValue;
+}
+
 // ---------------------------------------------------------------- cross entropy
 
 // One workgroup of NTH threads per row; thread t holds the row's runs of 8

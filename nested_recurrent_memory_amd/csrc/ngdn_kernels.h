@@ -236,6 +236,17 @@ struct SwigluArgs {
 hipError_t swiglu_fwd(const SwigluArgs& a, int dtype, hipStream_t st);
 hipError_t swiglu_bwd(const SwigluArgs& a, int dtype, hipStream_t st);
 
+// Sum of up to 8 same-shaped tensors in the working dtype into fp32
+// (model_ops.hip): out[i] = sum_j x_j[i], n % 8 == 0.
+constexpr int SUM_MAX = 8;
+struct SumArgs {
+  const void* x[SUM_MAX];
+  float* out;
+  long long n;
+  int count;
+};
+hipError_t sum_into_f32(const SumArgs& a, int dtype, hipStream_t st);
+
 // Cross entropy of rows of V logits (model_ops.hip): row_loss[r] =
 // (logsumexp(x_r) - x_r[label_r]) / n_valid, 0 for ignored labels; with grad
 // the logits are overwritten by d(sum of row_loss)/dx = (softmax - onehot) /

@@ -209,12 +209,21 @@ class _Fanout(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
-        acc = None
-        for g in grads:
-            if g is None:
-                continue
-            acc = g.float() if acc is None else acc.add_(g)
-        return (acc.to(ctx.xdtype) if acc is not None else None), None, None
+        gs = [g.contiguous() for g in grads if g is not None]
+        if not gs:
+            return None, None, None
+        dt = gs[0].dtype
+        if (len(gs) > 8 or any(g.dtype != dt for g in gs) or dt not in (torch.bfloat16, torch.float32)
+                or gs[0].numel() % 8):
+            acc = gs[0].float()
+            for g in gs[1:]:
+                acc.add_(g)
+        else:       # one pass over every gradient (ngdn_sum_f32)
+            acc = torch.empty(gs[0].shape, device=gs[0].device, dtype=torch.float32)
+            ptrs = (ctypes.c_void_p * len(gs))(*[g.data_ptr() for g in gs])
+            _lib.call("ngdn_sum_f32", _code(gs[0]), len(gs), ptrs, acc.numel(), _lib.ptr(acc),
+                      _lib.stream_of(acc))
+        return acc.to(ctx.xdtype), None, None
 
 
 def fanout(x, n):

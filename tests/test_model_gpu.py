@@ -266,3 +266,24 @@ def test_model_refuses_padded_batches():
     mask[0, :3] = 0
     with pytest.raises(ValueError, match="padded batches"):
         m(input_ids=ids, attention_mask=mask)
+
+
+@pytest.mark.parametrize("n", [2, 8])
+def test_fanout_gradient_sum(n):
+    """x shared by n linear maps under autocast: one cast forward, the input
+    gradient summed in fp32 in one pass (ngdn_sum_f32); equals the fp64 sum of
+    the per-map gradients (each a bf16 GEMM output, rounded once)."""
+    from nested_recurrent_memory_amd.layer_ops import fanout
+    g = _gen(n)
+    x = torch.randn(3, 50, 64, generator=g).to(DEV).requires_grad_()
+    ws = [torch.randn(32, 64, generator=g).to(DEV) for _ in range(n)]
+    cots = [torch.randn(3, 50, 32, generator=g).to(DEV) for _ in range(n)]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        xs = fanout(x, n)
+        assert all(t.dtype == torch.bfloat16 for t in xs)
+        ys = [torch.nn.functional.linear(xi, w) for xi, w in zip(xs, ws)]
+    sum((y.float() * c).sum() for y, c in zip(ys, cots)).backward()
+    # each map's input gradient is the bf16 product c_j W_j; their sum in fp64
+    want = sum((c.to(torch.bfloat16) @ w.to(torch.bfloat16)).double() for c, w in zip(cots, ws))
+    assert x.grad.dtype == torch.float32
+    _near("dx", x.grad, want.cpu(), 1e-2)
