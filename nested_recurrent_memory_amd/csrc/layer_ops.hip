@@ -364,11 +364,17 @@ __global__ __launch_bounds__(256) void gate_prep_fwd_kernel(GatePrepArgs a) {
   const long long th0 = ((long long)blockIdx.x * 4 + wave_id()) * GP_TPW, nth = a.BT * H;
   if (th0 >= nth) return;
   const bool isf = lane < VK, isb = !isf && lane < 2 * VK, isw = !isf && !isb && lane < 2 * VK + VV;
+  // token and head of the wave's first token-head (one division), then by
+  // steps: a 64-bit division per token-head was most of the scalar work
+  const long long bt0 = th0 / H;
+  const int h0 = (int)(th0 - bt0 * H);
   float x[GP_TPW][NP][8], z[GP_TPW][8], zm[GP_TPW];
 #pragma unroll
   for (int j = 0; j < GP_TPW; ++j) {
-    const long long th = th0 + j, bt = th / H;
-    const int h = (int)(th % H);
+    const long long th = th0 + j;
+    const int hj = h0 + j;
+    const long long bt = bt0 + hj / H;
+    const int h = hj % H;
     const bool live = th < nth;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(256) void gate_prep_fwd_kernel(GatePrepArgs a) {
   for (int j = 0; j < GP_TPW; ++j) {
     const long long th = th0 + j;
     if (th >= nth) break;
-    const int h = (int)(th % H);
+    const int h = (h0 + j) % H;
     // q's L rows, transposed from (l h) to (h l), and k: x / max(|x|, eps)
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -458,8 +464,9 @@ __global__ __launch_bounds__(256) void gate_prep_bwd_kernel(GatePrepArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) ddt[e] = dtb[e] = 0.f;
   if (lane < VK) load8f(static_cast<const P*>(a.dt_bias) + (size_t)h * K + lane * 8, dtb);
-  for (long long th = th0; th < a.BT * H; th += stride) {
-    const long long bt = th / H;
+  const long long bstep = stride / H;          // the stride is a multiple of H
+  long long bt = th0 / H;
+  for (long long th = th0; th < a.BT * H; th += stride, bt += bstep) {
     for (int base = 0; base < (L + 1) * VK; base += WAVE) {
       const int r = (base + lane) / VK, c = (base + lane) % VK * 8;
       const bool live = r <= L;
