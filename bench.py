@@ -437,7 +437,9 @@ def main():
     # the op runs each entry point once per group of batch rows (one stream
     # per group), so a launch does 1/launches-per-step of the step's work
     per_launch = {n: args.steps / len(evs) for n, evs in timing.items()}
-    dom = max(per_step, key=per_step.get)
+    # the dominant kernel among those on the launch stream (side-stream
+    # intervals include the time they share the GPU with it)
+    dom = max((n for n in per_step if n not in _lib.SIDE), key=per_step.get)
     dom_work = model.get(dom)
     if dom_work is not None:
         dom_work = tuple(x * per_launch[dom] for x in dom_work)
@@ -466,7 +468,8 @@ def main():
                 t = ms[n] * 1e-3
                 w = tuple(x * per_launch[n] for x in w)
                 extra = f"  {w[0] / t / 1e9:8.1f} GB/s  {w[1] / t / 1e12:7.2f} TFLOP/s"
-            print(f"{n:28s} {per_step[n]:8.3f} ms/step  {ms[n]:8.3f} ms/launch{extra}",
+            side = "  (side stream)" if n in _lib.SIDE else ""
+            print(f"{n:28s} {per_step[n]:8.3f} ms/step  {ms[n]:8.3f} ms/launch{extra}{side}",
                   file=sys.stderr)
 
     ms_step = elapsed / args.steps * 1e3

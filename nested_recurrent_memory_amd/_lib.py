@@ -93,9 +93,11 @@ def lib():
 
 
 # When set to a dict, every entry point call is bracketed by two timing events
-# recorded on torch's current stream (the stream the kernels are launched on):
-# TIMING[name] collects (start, end) event pairs.
+# recorded on the stream it launches on: TIMING[name] collects (start, end)
+# event pairs. SIDE collects the names launched on a side stream (their
+# intervals overlap the main stream's kernels).
 TIMING = None
+SIDE = set()
 
 
 def call(name, *args, tag=None, stream=None):
@@ -109,6 +111,8 @@ def call(name, *args, tag=None, stream=None):
         start.record(stream)
         rc = getattr(lib(), name)(*args)
         end.record(stream)
+        if stream is not None and stream != torch.cuda.current_stream():
+            SIDE.add(tag or name)
         TIMING.setdefault(tag or name, []).append((start, end))
     else:
         rc = getattr(lib(), name)(*args)
