@@ -254,19 +254,29 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     merge = promotion == "merge"
     states, levels, par, final = sv["states"], sv["levels"], sv["par"], sv["final"]
 
-    # everything is allocated (and zeroed) here, on the current stream
+    # everything is allocated (and zeroed) here, on the current stream; the
+    # buffers that start at zero share one allocation and one fill
+    zshapes = ([] if dfinal is not None else [(B, H, L, K, V)]) + \
+        ([(B, H, L, K, V)] if has_init else []) + \
+        ([(L - 1, H, par["nmax"], K), (L - 1, H, K, V), (L - 1, H, V, K), (L - 1, H, V, V),
+          (L - 1, H, V, K)] if L > 1 else [])
+    zsizes = [math.prod(sh) for sh in zshapes]
+    zbuf = z32(sum(zsizes)) if zshapes else None
+    zviews, off = [], 0
+    for sh, n in zip(zshapes, zsizes):
+        zviews.append(zbuf[off:off + n].view(sh))
+        off += n
+    zit = iter(zviews)
     dq = e(B, T, H, L, K)
     dmix = f32(B, T, H, L)
     d_final = (dfinal.to(torch.float32).contiguous().clone() if dfinal is not None
-               else z32(B, H, L, K, V))
-    d_init = z32(B, H, L, K, V) if has_init else None
+               else next(zit))
+    d_init = next(zit) if has_init else None
     d_states = [None] + [f32(B, n_groups(NT, f[lvl]), H, K, V) for lvl in range(1, L)]
     dqb = dkp = dbp = dwp = dgp = None
     work = [None] * L
     if L > 1:
-        dqb = z32(L - 1, H, par["nmax"], K)
-        dkp, dbp = z32(L - 1, H, K, V), z32(L - 1, H, V, K)
-        dwp, dgp = z32(L - 1, H, V, V), z32(L - 1, H, V, K)
+        dqb, dkp, dbp, dwp, dgp = (next(zit) for _ in range(5))
     for lvl in range(1, L):
         lv = levels[lvl]
         N, nf = lv["N"], lv["nf"]
