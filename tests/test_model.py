@@ -148,3 +148,12 @@ def test_save_pretrained_round_trip(tmp_path):
         assert set(sd) == set(sd2)
         for k in sd:
             assert torch.equal(sd[k], sd2[k]), k
+
+
+def test_tied_embeddings():
+    """tie_word_embeddings shares the embedding matrix with the LM head, as
+    the reference declares (_tied_weights_keys, modeling_nested_gdn2.py:165)."""
+    m = NestedGDN2ForCausalLM(_tiny(tie_word_embeddings=True))
+    assert m.lm_head.weight.data_ptr() == m.model.embeddings.weight.data_ptr()
+    untied = NestedGDN2ForCausalLM(_tiny())
+    assert untied.lm_head.weight.data_ptr() != untied.model.embeddings.weight.data_ptr()
