@@ -350,6 +350,27 @@ int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, 
                          const float* rstd, const void* dy, void* dx, float* dw, float* ws,
                          void* stream);
 
+/* The block's residual add fused into the RMSNorm after it (no counterpart
+ * entry point: the reference adds in Python, models/modeling_nested_gdn2.py:
+ * 59-67, then calls fla's RMSNorm; the results are the same). With r set:
+ * h = x + r rounded to x's dtype (written, [rows,D]) and y = RMSNorm(h) as
+ * ngdn_rmsnorm_fwd; r NULL: y = RMSNorm(x), h untouched. y in y_dtype, so a
+ * norm whose consumer computes in bf16 (autocast) writes bf16 directly.
+ * Dtype combinations (x, r, y): all NGDN_F32, all NGDN_BF16, or NGDN_F32 x
+ * with NGDN_BF16 r and y (r's code also selects the combination when r is
+ * NULL). D as for ngdn_rmsnorm_fwd. */
+int32_t ngdn_add_rmsnorm_fwd(int32_t x_dtype, int32_t r_dtype, int32_t y_dtype, int64_t rows,
+                             int32_t D, float eps, const void* x, const void* r, const float* w,
+                             void* h, void* y, float* rstd, void* stream);
+/* Its backward from h (x when r was NULL) and the forward's rstd: dx = the
+ * norm's input gradient plus dh (the gradient h receives from elsewhere, the
+ * residual path; NULL: none), in x_dtype; dr (NULL: not written) the same
+ * values in r_dtype; dy in y_dtype; dw and ws as for ngdn_rmsnorm_bwd. */
+int32_t ngdn_add_rmsnorm_bwd(int32_t x_dtype, int32_t r_dtype, int32_t y_dtype, int64_t rows,
+                             int32_t D, const void* h, const float* w, const float* rstd,
+                             const void* dy, const void* dh, void* dx, void* dr, float* dw,
+                             float* ws, void* stream);
+
 /* The SwiGLU of fla's GatedMLP (models/modeling_nested_gdn2.py:17,50-56):
  * y = silu(g) u elementwise over n values (n % 8 == 0), all in dtype. */
 int32_t ngdn_swiglu_fwd(int32_t dtype, int64_t n, const void* g, const void* u, void* y, void* stream);

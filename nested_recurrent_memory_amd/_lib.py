@@ -60,6 +60,8 @@ SIGNATURES = {
     "ngdn_gate_prep_bwd": [I32, P, P],
     "ngdn_rmsnorm_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P],
     "ngdn_rmsnorm_bwd": [I32, I64, I32] + [P] * 8,
+    "ngdn_add_rmsnorm_fwd": [I32, I32, I32, I64, I32, ctypes.c_float] + [P] * 7,
+    "ngdn_add_rmsnorm_bwd": [I32, I32, I32, I64, I32] + [P] * 10,
     "ngdn_swiglu_fwd": [I32, I64] + [P] * 4,
     "ngdn_swiglu_bwd": [I32, I64] + [P] * 6,
     "ngdn_sum_f32": [I32, I32, P, I64, P, P],

@@ -621,7 +621,7 @@ int32_t ngdn_rmsnorm_fwd(int32_t dtype, int64_t rows, int32_t D, float eps, cons
   if (rows > 0 && (!x || !w || !y)) return fail(NGDN_EINVAL, "ngdn_rmsnorm_fwd: NULL tensor");
   ngdn::RMSNormArgs a{};
   a.x = x; a.w = w; a.y = y; a.rstd = rstd; a.rows = rows; a.D = D; a.eps = eps;
-  return launched(ngdn::rmsnorm_fwd(a, dtype, (hipStream_t)stream), "ngdn_rmsnorm_fwd");
+  return launched(ngdn::rmsnorm_fwd(a, dtype, dtype, dtype, (hipStream_t)stream), "ngdn_rmsnorm_fwd");
 }
 
 int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, const float* w,
@@ -635,7 +635,44 @@ int32_t ngdn_rmsnorm_bwd(int32_t dtype, int64_t rows, int32_t D, const void* x, 
   ngdn::RMSNormArgs a{};
   a.x = x; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dx = dx; a.dw = dw;
   a.ws = ws; a.rows = rows; a.D = D;
-  return launched(ngdn::rmsnorm_bwd(a, dtype, (hipStream_t)stream), "ngdn_rmsnorm_bwd");
+  return launched(ngdn::rmsnorm_bwd(a, dtype, dtype, dtype, (hipStream_t)stream), "ngdn_rmsnorm_bwd");
+}
+
+int32_t ngdn_add_rmsnorm_fwd(int32_t x_dtype, int32_t r_dtype, int32_t y_dtype, int64_t rows,
+                             int32_t D, float eps, const void* x, const void* r, const float* w,
+                             void* h, void* y, float* rstd, void* stream) {
+  g_err[0] = 0;
+  if (!ngdn::rmsnorm_types_supported(x_dtype, r_dtype, y_dtype))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_fwd: dtypes x=%d r=%d y=%d (all fp32, all bf16, or "
+                "fp32 x with bf16 r and y)", x_dtype, r_dtype, y_dtype);
+  if (rows < 0 || !ngdn::rmsnorm_supported(D))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_fwd: rows=%lld D=%d unsupported", (long long)rows, D);
+  if (rows > 0 && (!x || !w || !y || (r && !h)))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_fwd: NULL tensor");
+  ngdn::RMSNormArgs a{};
+  a.x = x; a.r = r; a.h = r ? h : nullptr; a.w = w; a.y = y; a.rstd = rstd;
+  a.rows = rows; a.D = D; a.eps = eps;
+  return launched(ngdn::rmsnorm_fwd(a, x_dtype, r_dtype, y_dtype, (hipStream_t)stream),
+                  "ngdn_add_rmsnorm_fwd");
+}
+
+int32_t ngdn_add_rmsnorm_bwd(int32_t x_dtype, int32_t r_dtype, int32_t y_dtype, int64_t rows,
+                             int32_t D, const void* h, const float* w, const float* rstd,
+                             const void* dy, const void* dh, void* dx, void* dr, float* dw,
+                             float* ws, void* stream) {
+  g_err[0] = 0;
+  if (!ngdn::rmsnorm_types_supported(x_dtype, r_dtype, y_dtype))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_bwd: dtypes x=%d r=%d y=%d (all fp32, all bf16, or "
+                "fp32 x with bf16 r and y)", x_dtype, r_dtype, y_dtype);
+  if (rows < 0 || !ngdn::rmsnorm_supported(D))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_bwd: rows=%lld D=%d unsupported", (long long)rows, D);
+  if (rows > 0 && (!h || !w || !rstd || !dy || !dx || !dw))
+    return fail(NGDN_EINVAL, "ngdn_add_rmsnorm_bwd: NULL tensor");
+  ngdn::RMSNormArgs a{};
+  a.x = h; a.w = w; a.rstd = const_cast<float*>(rstd); a.dy = dy; a.dh = dh; a.dx = dx; a.dr = dr;
+  a.dw = dw; a.ws = ws; a.rows = rows; a.D = D;
+  return launched(ngdn::rmsnorm_bwd(a, x_dtype, r_dtype, y_dtype, (hipStream_t)stream),
+                  "ngdn_add_rmsnorm_bwd");
 }
 
 int32_t ngdn_swiglu_fwd(int32_t dtype, int64_t n, const void* g, const void* u, void* y, void* stream) {

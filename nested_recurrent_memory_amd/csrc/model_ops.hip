@@ -32,22 +32,35 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // G lanes per row, each holding VPL runs of 8 values: D = 8 G VPL. Lane l of
 // a row owns columns (v G + l) 8 .. +7, so a wave's 16-byte accesses are
-// contiguous.
-template <typename E, int G, int VPL>
+// contiguous. X is the dtype of x (and of h), R of the residual r, Y of y.
+// With r set the row is first h = x + r, rounded to X and written to a.h,
+// and normalised from that rounded value (as a separate add would store it).
+template <typename X, typename R, typename Y, int G, int VPL>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RMSNormArgs a) {
   constexpr int D = 8 * G * VPL;
   const long long row = ((long long)blockIdx.x * 256 + threadIdx.x) / G;
   const int li = threadIdx.x % G;
   const bool live = row < a.rows;
-  const E* xr = static_cast<const E*>(a.x) + row * D;
-  float x[VPL][8];
+  const bool add = a.r != nullptr;
+  const X* xr = static_cast<const X*>(a.x) + row * D;
+  const R* rr = static_cast<const R*>(a.r) + row * D;
+  float x[VPL][8], t[VPL][8];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     if (live) {
       load8f(xr + (v * G + li) * 8, x[v]);
+      if (add) load8f(rr + (v * G + li) * 8, t[v]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[v][e] = 0.f;
+      for (int e = 0; e < 8; ++e) x[v][e] = t[v][e] = 0.f;
+    }
+  }
+  if (add) {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[v][e] = to_f(from_f<X>(x[v][e] + t[v][e]));
+      if (live) store8f(static_cast<X*>(a.h) + row * D + (v * G + li) * 8, x[v]);
     }
   }
   float ss = 0.f;
@@ -58,7 +71,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RMSNormArgs a) {
   ss = group_sum<G>(ss);
   const float rstd = 1.f / sqrtf(ss / (float)D + a.eps);
   if (!live) return;
-  E* yr = static_cast<E*>(a.y) + row * D;
+  Y* yr = static_cast<Y*>(a.y) + row * D;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * G + li) * 8;
@@ -70,14 +83,18 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RMSNormArgs a) {
   if (a.rstd && li == 0) a.rstd[row] = rstd;
 }
 
-// dx = rstd (dy w - xh mean(dy w xh)), dw += dy xh with xh = x rstd. Rows are
-// visited grid-stride; a thread's dw partials are summed over the workgroup's
-// row slots in LDS, then added to dw with one atomic per column and workgroup.
-template <typename E, int G, int VPL>
+// dx = rstd (dy w - xh mean(dy w xh)) (+ dh, the gradient h receives besides
+// the norm, when set), dw += dy xh with xh = x rstd; with dr set, dx is also
+// written in R's dtype (the residual's gradient). x is h when the forward
+// added a residual. Rows are visited grid-stride; a thread's dw partials are
+// summed over the workgroup's row slots in LDS, then written as the
+// workgroup's partial row (or added to dw with one atomic per column).
+template <typename X, typename R, typename Y, int G, int VPL>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RMSNormArgs a) {
   constexpr int D = 8 * G * VPL, RPB = 256 / G;
   __shared__ float s_dw[RPB][D];
   const int li = threadIdx.x % G, rs = threadIdx.x / G;
+  const bool res = a.dh != nullptr;
   float dw[VPL][8];
 #pragma unroll
   for (int v = 0; v < VPL; ++v)
@@ -85,13 +102,15 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RMSNormArgs a) {
     for (int e = 0; e < 8; ++e) dw[v][e] = 0.f;
   for (long long row = (long long)blockIdx.x * RPB + rs; row < a.rows;
        row += (long long)gridDim.x * RPB) {
-    const E* xr = static_cast<const E*>(a.x) + row * D;
-    const E* dyr = static_cast<const E*>(a.dy) + row * D;
-    float x[VPL][8], dy[VPL][8];
+    const X* xr = static_cast<const X*>(a.x) + row * D;
+    const Y* dyr = static_cast<const Y*>(a.dy) + row * D;
+    const X* dhr = static_cast<const X*>(a.dh) + row * D;
+    float x[VPL][8], dy[VPL][8], dh[VPL][8];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       load8f(xr + (v * G + li) * 8, x[v]);
       load8f(dyr + (v * G + li) * 8, dy[v]);
+      if (res) load8f(dhr + (v * G + li) * 8, dh[v]);
     }
     const float rstd = a.rstd[row];
     float dot = 0.f;
@@ -107,13 +126,15 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RMSNormArgs a) {
       }
     }
     const float mean = group_sum<G>(dot) / (float)D;
-    E* dxr = static_cast<E*>(a.dx) + row * D;
+    X* dxr = static_cast<X*>(a.dx) + row * D;
+    R* drr = static_cast<R*>(a.dr) + row * D;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       float dx[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dx[e] = rstd * (dy[v][e] - x[v][e] * mean);
+      for (int e = 0; e < 8; ++e) dx[e] = rstd * (dy[v][e] - x[v][e] * mean) + (res ? dh[v][e] : 0.f);
       store8f(dxr + (v * G + li) * 8, dx);
+      if (a.dr) store8f(drr + (v * G + li) * 8, dx);
     }
   }
 #pragma unroll
@@ -142,33 +163,44 @@ bool rmsnorm_supported(int D) {
   return false;
 }
 
-hipError_t rmsnorm_fwd(const RMSNormArgs& a, int dtype, hipStream_t st) {
+// dtype combinations (x, r, y): all fp32, all bf16, or fp32 x with bf16 r and
+// y (an fp32 residual stream under bf16 autocast)
+bool rmsnorm_types_supported(int xd, int rd, int yd) {
+  return (xd == rd && rd == yd && (xd == NGDN_F32 || xd == NGDN_BF16)) ||
+         (xd == NGDN_F32 && rd == NGDN_BF16 && yd == NGDN_BF16);
+}
+
+#define NGDN_RMS_TYPED(KERNEL, GG, VV, grid, xd, rd)                                          \
+  if (xd == NGDN_BF16)                                                                        \
+    hipLaunchKernelGGL((KERNEL<bf16, bf16, bf16, GG, VV>), dim3(grid), dim3(256), 0, st, a);  \
+  else if (rd == NGDN_BF16)                                                                   \
+    hipLaunchKernelGGL((KERNEL<float, bf16, bf16, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
+  else                                                                                        \
+    hipLaunchKernelGGL((KERNEL<float, float, float, GG, VV>), dim3(grid), dim3(256), 0, st, a);
+
+hipError_t rmsnorm_fwd(const RMSNormArgs& a, int xd, int rd, int yd, hipStream_t st) {
+  if (!rmsnorm_types_supported(xd, rd, yd)) return hipErrorInvalidValue;
   if (a.rows == 0) return hipSuccess;
-#define NGDN_RMS_F(GG, VV)                                                                   \
-  if (a.D == 8 * GG * VV) {                                                                  \
-    const unsigned grid = (unsigned)((a.rows * GG + 255) / 256);                             \
-    if (dtype == NGDN_BF16)                                                                  \
-      hipLaunchKernelGGL((rmsnorm_fwd_kernel<bf16, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
-    else                                                                                     \
-      hipLaunchKernelGGL((rmsnorm_fwd_kernel<float, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
-    return hipGetLastError();                                                                \
+#define NGDN_RMS_F(GG, VV)                                                   \
+  if (a.D == 8 * GG * VV) {                                                  \
+    const unsigned grid = (unsigned)((a.rows * GG + 255) / 256);             \
+    NGDN_RMS_TYPED(rmsnorm_fwd_kernel, GG, VV, grid, xd, rd)                 \
+    return hipGetLastError();                                                \
   }
   NGDN_RMS_SHAPES(NGDN_RMS_F)
 #undef NGDN_RMS_F
   return hipErrorInvalidValue;
 }
 
-hipError_t rmsnorm_bwd(const RMSNormArgs& a, int dtype, hipStream_t st) {
+hipError_t rmsnorm_bwd(const RMSNormArgs& a, int xd, int rd, int yd, hipStream_t st) {
+  if (!rmsnorm_types_supported(xd, rd, yd)) return hipErrorInvalidValue;
   if (a.rows == 0) return hipSuccess;
 #define NGDN_RMS_B(GG, VV)                                                                   \
   if (a.D == 8 * GG * VV) {                                                                  \
     constexpr long long RPB = 256 / GG;                                                      \
     const long long want = (a.rows + RPB * 16 - 1) / (RPB * 16);   /* ~16 rows per slot */   \
     const unsigned grid = (unsigned)(want < NGDN_WPARTS ? want : NGDN_WPARTS);               \
-    if (dtype == NGDN_BF16)                                                                  \
-      hipLaunchKernelGGL((rmsnorm_bwd_kernel<bf16, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
-    else                                                                                     \
-      hipLaunchKernelGGL((rmsnorm_bwd_kernel<float, GG, VV>), dim3(grid), dim3(256), 0, st, a); \
+    NGDN_RMS_TYPED(rmsnorm_bwd_kernel, GG, VV, grid, xd, rd)                                 \
     if (hipError_t e = hipGetLastError()) return e;                                          \
     return a.ws ? sum_parts(a.ws, grid, a.D, a.dw, st) : hipSuccess;                         \
   }
@@ -176,6 +208,7 @@ hipError_t rmsnorm_bwd(const RMSNormArgs& a, int dtype, hipStream_t st) {
 #undef NGDN_RMS_B
   return hipErrorInvalidValue;
 }
+#undef NGDN_RMS_TYPED
 
 // ---------------------------------------------------------------- partial sums
 

@@ -216,15 +216,18 @@ hipError_t rmsnorm_gated_bwd(const NormGatedArgs& a, int dtype, int V, hipStream
 // by the forward for the backward.
 struct RMSNormArgs {
   const void* x; const float* w; void* y; float* rstd;
+  const void* r; void* h;        // forward: residual added first (h = x + r), or NULL
   const void* dy; void* dx; float* dw;
+  const void* dh; void* dr;      // backward: gradient of h besides the norm, residual's copy
   float* ws;    // backward: per-workgroup partial dw [NGDN_WPARTS][n], or NULL
   long long rows;
   int D;
   float eps;
 };
 bool rmsnorm_supported(int D);
-hipError_t rmsnorm_fwd(const RMSNormArgs& a, int dtype, hipStream_t st);
-hipError_t rmsnorm_bwd(const RMSNormArgs& a, int dtype, hipStream_t st);
+bool rmsnorm_types_supported(int xd, int rd, int yd);
+hipError_t rmsnorm_fwd(const RMSNormArgs& a, int xd, int rd, int yd, hipStream_t st);
+hipError_t rmsnorm_bwd(const RMSNormArgs& a, int xd, int rd, int yd, hipStream_t st);
 
 // The MLP's SwiGLU (model_ops.hip): y = silu(g) u over n values, n % 8 == 0,
 // all in the working dtype.

@@ -27,7 +27,7 @@ from transformers.modeling_utils import PreTrainedModel
 
 from .layer import NestedGDN2Attention
 from .layer_ops import FusedRMSNormGated, ShortConvolution
-from .model_ops import FusedLinearCrossEntropyLoss, GatedMLP, RMSNorm
+from .model_ops import FusedLinearCrossEntropyLoss, GatedMLP, RMSNorm, add_rms_norm, rms_norm
 
 __all__ = ["NestedGDN2Config", "NestedGDN2Cache", "NestedGDN2Block", "NestedGDN2Model",
            "NestedGDN2ForCausalLM", "NestedGDN2PreTrainedModel"]
@@ -131,11 +131,18 @@ class NestedGDN2Block(nn.Module):
                             hidden_act=config.hidden_act, fuse_swiglu=config.fuse_swiglu)
 
     def forward(self, hidden_states, past_key_values=None, use_cache=False):
-        attn_out, _, past_key_values = self.attn(self.attn_norm(hidden_states),
+        # The norms write the dtype their consumers compute in (bf16 under
+        # autocast: the cast the projections would make), and the attention's
+        # residual add runs inside the second norm's kernel. Same values as
+        # norm -> attn -> add -> norm -> mlp -> add.
+        cdt = (torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda")
+               else hidden_states.dtype)
+        an, mn = self.attn_norm, self.mlp_norm
+        attn_out, _, past_key_values = self.attn(rms_norm(hidden_states, an.weight, an.eps, cdt),
                                                  past_key_values=past_key_values,
                                                  use_cache=use_cache)
-        hidden_states = hidden_states + attn_out
-        hidden_states = hidden_states + self.mlp(self.mlp_norm(hidden_states))
+        hidden_states, y = add_rms_norm(hidden_states, attn_out, mn.weight, mn.eps, cdt)
+        hidden_states = hidden_states + self.mlp(y)
         return hidden_states, past_key_values
 
 

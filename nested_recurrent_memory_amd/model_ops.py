@@ -25,8 +25,8 @@ import torch.nn as nn
 from . import _lib
 from .layer_ops import fanout
 
-__all__ = ["RMSNorm", "GatedMLP", "FusedLinearCrossEntropyLoss", "rms_norm", "swiglu",
-           "fused_linear_cross_entropy"]
+__all__ = ["RMSNorm", "GatedMLP", "FusedLinearCrossEntropyLoss", "rms_norm", "add_rms_norm",
+           "swiglu", "fused_linear_cross_entropy"]
 
 
 def _code(t):
@@ -54,40 +54,88 @@ def _compute_dtype(x):
 # ---------------------------------------------------------------- RMSNorm
 
 class _RMSNormFn(torch.autograd.Function):
+    """y = RMSNorm(x + r) (r optional) in y's dtype; with r also h = x + r.
+    Dtype combinations (x, r, y) run on the kernel: all fp32, all bf16, or
+    an fp32 x (a residual stream) with bf16 r and y (bf16 autocast)."""
+
     @staticmethod
-    def forward(ctx, x, weight, eps):
+    def forward(ctx, x, r, weight, eps, ydt):
         D = x.shape[-1]
         xw = _work(x).contiguous()
+        want = torch.bfloat16 if ydt == torch.bfloat16 else x.dtype
+        if xw.dtype == torch.bfloat16:
+            rdt = torch.bfloat16                      # all bf16 (r is bf16: add_rms_norm)
+        elif want == torch.bfloat16 and (r is None or r.dtype == torch.bfloat16):
+            rdt = torch.bfloat16                      # fp32 x, bf16 r and y
+        else:
+            rdt = torch.float32                       # all fp32 (a bf16 r widens exactly)
+        ydt = rdt
+        rw = r.to(rdt).contiguous() if r is not None else None
         w = weight.float().contiguous()
         rows = xw.numel() // D
-        y = torch.empty_like(xw)
+        y = torch.empty(xw.shape, device=xw.device, dtype=ydt)
+        h = torch.empty_like(xw) if r is not None else None
         rstd = torch.empty(rows, device=xw.device, dtype=torch.float32)
-        _lib.call("ngdn_rmsnorm_fwd", _code(xw), rows, D, float(eps), _lib.ptr(xw), _lib.ptr(w),
-                  _lib.ptr(y), _lib.ptr(rstd), _lib.stream_of(xw))
-        ctx.save_for_backward(xw, w, rstd)
-        ctx.dtypes = (x.dtype, weight.dtype)
-        return y.to(x.dtype)
+        c = _lib.NGDN_BF16 if rdt == torch.bfloat16 else _lib.NGDN_F32
+        _lib.call("ngdn_add_rmsnorm_fwd", _code(xw), c, c, rows, D, float(eps), _lib.ptr(xw),
+                  _lib.ptr(rw), _lib.ptr(w), _lib.ptr(h), _lib.ptr(y), _lib.ptr(rstd),
+                  _lib.stream_of(xw))
+        ctx.save_for_backward(h if r is not None else xw, w, rstd)
+        ctx.codes = (_code(xw), c)
+        ctx.dtypes = (x.dtype, r.dtype if r is not None else None, weight.dtype, rdt)
+        y = y.to(want)
+        if r is None:
+            return y
+        return h.to(x.dtype), y
 
     @staticmethod
-    def backward(ctx, dy):
-        xw, w, rstd = ctx.saved_tensors
-        D = xw.shape[-1]
-        rows = xw.numel() // D
-        dyw = dy.to(xw.dtype).contiguous()
-        dx = torch.empty_like(xw)
-        dw = torch.zeros(D, device=xw.device, dtype=torch.float32)
-        ws = torch.empty(_lib.WPARTS, D, device=xw.device, dtype=torch.float32)
-        _lib.call("ngdn_rmsnorm_bwd", _code(xw), rows, D, _lib.ptr(xw), _lib.ptr(w), _lib.ptr(rstd),
-                  _lib.ptr(dyw), _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(ws), _lib.stream_of(xw))
-        return dx.to(ctx.dtypes[0]), dw.to(ctx.dtypes[1]), None
+    def backward(ctx, *grads):
+        hx, w, rstd = ctx.saved_tensors
+        xd, rd, wd, rdt = ctx.dtypes
+        if rd is None:
+            dy, dh = grads[0], None
+        else:
+            dh, dy = grads
+        D = hx.shape[-1]
+        rows = hx.numel() // D
+        dyw = (dy.to(rdt) if dy is not None else torch.zeros(hx.shape, device=hx.device, dtype=rdt)).contiguous()
+        dhw = dh.to(hx.dtype).contiguous() if dh is not None else None
+        dx = torch.empty_like(hx)
+        dr = torch.empty(hx.shape, device=hx.device, dtype=rdt) if (rd is not None and ctx.needs_input_grad[1]) else None
+        dw = torch.zeros(D, device=hx.device, dtype=torch.float32)
+        ws = torch.empty(_lib.WPARTS, D, device=hx.device, dtype=torch.float32)
+        xc, c = ctx.codes
+        _lib.call("ngdn_add_rmsnorm_bwd", xc, c, c, rows, D, _lib.ptr(hx), _lib.ptr(w),
+                  _lib.ptr(rstd), _lib.ptr(dyw), _lib.ptr(dhw), _lib.ptr(dx), _lib.ptr(dr),
+                  _lib.ptr(dw), _lib.ptr(ws), _lib.stream_of(hx))
+        return (dx.to(xd), dr.to(rd) if dr is not None else None, dw.to(wd), None, None)
 
 
-def rms_norm(x, weight, eps=1e-5):
-    """x [..., D]; weight [D]. y = x rstd weight, in x's dtype."""
+def rms_norm(x, weight, eps=1e-5, out_dtype=None):
+    """x [..., D]; weight [D]. y = x rstd weight, in x's dtype, or bf16 when
+    out_dtype is bf16 and x fp32 (the cast a bf16 consumer would make)."""
     if weight.shape != (x.shape[-1],):
         raise ValueError(f"rms_norm: x {tuple(x.shape)}, weight {tuple(weight.shape)}")
     _on_gpu("rms_norm", x, weight)
-    return _RMSNormFn.apply(x, weight, eps)
+    return _RMSNormFn.apply(x, None, weight, eps, out_dtype)
+
+
+def add_rms_norm(x, r, weight, eps=1e-5, out_dtype=None):
+    """h = x + r and y = RMSNorm(h) weight in one pass: returns (h, y), h in
+    x's dtype (a pre-norm block's residual stream: x + sublayer(x) followed
+    by the next norm), y as for rms_norm."""
+    if weight.shape != (x.shape[-1],) or r.shape != x.shape:
+        raise ValueError(f"add_rms_norm: x {tuple(x.shape)}, r {tuple(r.shape)}, weight {tuple(weight.shape)}")
+    _on_gpu("add_rms_norm", x, r, weight)
+    if (x.dtype, r.dtype) not in _ADD_FORMS:
+        h = x + r                  # other dtype pairs: the add on its own, then the norm
+        return h, rms_norm(h, weight, eps, out_dtype)
+    return _RMSNormFn.apply(x, r, weight, eps, out_dtype)
+
+
+# (x, r) dtype pairs whose sum keeps x's dtype and runs inside the norm kernel
+_ADD_FORMS = {(torch.float32, torch.float32), (torch.float32, torch.bfloat16),
+              (torch.bfloat16, torch.bfloat16)}
 
 
 class RMSNorm(nn.Module):

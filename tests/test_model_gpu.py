@@ -23,7 +23,8 @@ import torch.nn.functional as F
 
 import ngdn_model_oracle as mref
 from nested_recurrent_memory_amd.model import NestedGDN2Config, NestedGDN2ForCausalLM
-from nested_recurrent_memory_amd.model_ops import fused_linear_cross_entropy, rms_norm, swiglu
+from nested_recurrent_memory_amd.model_ops import (add_rms_norm, fused_linear_cross_entropy,
+                                                   rms_norm, swiglu)
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +73,55 @@ def test_rms_norm_matches_torch(dtype, D, rows):
     _close("y", y, y64, dtype)
     _close("dx", xd.grad, x64.grad, dtype)
     _close("dw", wd.grad, w64.grad, torch.float32 if rows < 10000 else torch.bfloat16)
+
+
+@pytest.mark.parametrize("xdt,rdt,ydt", [
+    (torch.float32, torch.bfloat16, torch.bfloat16),     # fp32 residual stream, bf16 autocast
+    (torch.float32, torch.float32, None),
+    (torch.bfloat16, torch.bfloat16, None),
+    (torch.float32, torch.bfloat16, None),               # bf16 r widened, fp32 y
+    (torch.float32, torch.float32, torch.bfloat16),      # fp32 r, y cast to bf16
+], ids=["f32-bf16-bf16", "f32", "bf16", "f32-bf16-f32", "f32-f32-bf16"])
+@pytest.mark.parametrize("D,rows", [(256, 1000), (1024, 40000)])
+def test_add_rms_norm_matches_torch(xdt, rdt, ydt, D, rows):
+    """h = x + r and y = RMSNorm(h) w in one kernel against the separate add
+    and norm in float64: h, y, and the gradients of x (the residual path's dh
+    plus the norm's), r and w."""
+    print(f"add_rms_norm x={xdt} r={rdt} y={ydt} D={D} rows={rows}", flush=True)
+    g = _gen(3 * D + rows)
+    x = (torch.randn(rows, D, generator=g) * 2).to(xdt)
+    r = torch.randn(rows, D, generator=g).to(rdt)
+    w = 1 + 0.3 * torch.randn(D, generator=g)
+    ydt_eff = ydt if ydt is not None else xdt
+    dy = torch.randn(rows, D, generator=g).to(ydt_eff)
+    dh = torch.randn(rows, D, generator=g).to(xdt)
+    x64, r64, w64 = (t.double().requires_grad_() for t in (x, r, w))
+    h64 = x64 + r64
+    # the sum as stored in x's dtype is what gets normalised (as after a separate add)
+    hs = h64 + (h64.detach().to(xdt).double() - h64.detach())
+    y64 = F.rms_norm(hs, (D,), w64, 1e-5)
+    ((y64 * dy.double()).sum() + (h64 * dh.double()).sum()).backward()
+    xd, rd, wd = (t.to(DEV).requires_grad_() for t in (x, r, w))
+    h, y = add_rms_norm(xd, rd, wd, 1e-5, ydt)
+    assert h.dtype == xdt and y.dtype == ydt_eff
+    torch.autograd.backward([h, y], [dh.to(DEV), dy.to(DEV)])
+    torch.cuda.synchronize()
+    _close("h", h, h64, xdt)
+    _close("y", y, y64, torch.bfloat16 if torch.bfloat16 in (xdt, ydt_eff) else torch.float32)
+    _close("dx", xd.grad, x64.grad, xdt)
+    _close("dr", rd.grad, r64.grad, rdt)
+    _close("dw", wd.grad, w64.grad, torch.float32 if rows < 10000 else torch.bfloat16)
+
+
+def test_rms_norm_bf16_output_from_fp32():
+    """The block's first norm: fp32 x, bf16 y equal to the fp32 norm cast."""
+    g = _gen(7)
+    x = torch.randn(300, 1024, generator=g).to(DEV)
+    w = (1 + 0.3 * torch.randn(1024, generator=g)).to(DEV)
+    y32 = rms_norm(x, w, 1e-5)
+    y16 = rms_norm(x, w, 1e-5, torch.bfloat16)
+    assert y16.dtype == torch.bfloat16
+    assert torch.equal(y16, y32.to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
