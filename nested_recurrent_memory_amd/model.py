@@ -130,20 +130,30 @@ class NestedGDN2Block(nn.Module):
                             intermediate_size=config.intermediate_size,
                             hidden_act=config.hidden_act, fuse_swiglu=config.fuse_swiglu)
 
-    def forward(self, hidden_states, past_key_values=None, use_cache=False):
-        # The norms write the dtype their consumers compute in (bf16 under
-        # autocast: the cast the projections would make), and the attention's
-        # residual add runs inside the second norm's kernel. Same values as
-        # norm -> attn -> add -> norm -> mlp -> add.
+    def forward(self, hidden_states, past_key_values=None, use_cache=False, residual=None,
+                defer_residual=False):
+        """Same values as norm -> attn -> add -> norm -> mlp -> add. The norms
+        write the dtype their consumers compute in (bf16 under autocast: the
+        cast the projections would make) and each residual add runs inside
+        the norm after it: the attention's in the second norm; with
+        ``residual`` (the previous block's deferred MLP output) the input is
+        hidden_states + residual, added inside the first norm; with
+        ``defer_residual`` the block returns (h, mlp_out, cache) for the next
+        norm to add instead of h + mlp_out."""
         cdt = (torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda")
                else hidden_states.dtype)
         an, mn = self.attn_norm, self.mlp_norm
-        attn_out, _, past_key_values = self.attn(rms_norm(hidden_states, an.weight, an.eps, cdt),
-                                                 past_key_values=past_key_values,
+        if residual is None:
+            y = rms_norm(hidden_states, an.weight, an.eps, cdt)
+        else:
+            hidden_states, y = add_rms_norm(hidden_states, residual, an.weight, an.eps, cdt)
+        attn_out, _, past_key_values = self.attn(y, past_key_values=past_key_values,
                                                  use_cache=use_cache)
         hidden_states, y = add_rms_norm(hidden_states, attn_out, mn.weight, mn.eps, cdt)
-        hidden_states = hidden_states + self.mlp(y)
-        return hidden_states, past_key_values
+        mlp_out = self.mlp(y)
+        if defer_residual:
+            return hidden_states, mlp_out, past_key_values
+        return hidden_states + mlp_out, past_key_values
 
 
 class NestedGDN2PreTrainedModel(PreTrainedModel):
@@ -199,14 +209,21 @@ class NestedGDN2Model(NestedGDN2PreTrainedModel):
         if use_cache and not isinstance(past_key_values, NestedGDN2Cache):
             past_key_values = NestedGDN2Cache.from_legacy_cache(past_key_values)
         all_hidden_states = () if output_hidden_states else None
+        residual = None     # each block's MLP output, added inside the next norm
         for layer in self.layers:
             if output_hidden_states:
+                if residual is not None:
+                    hidden_states, residual = hidden_states + residual, None
                 all_hidden_states += (hidden_states,)
-            hidden_states, past_key_values = layer(hidden_states, past_key_values=past_key_values,
-                                                   use_cache=use_cache)
+            hidden_states, residual, past_key_values = layer(
+                hidden_states, past_key_values=past_key_values, use_cache=use_cache,
+                residual=residual, defer_residual=True)
         if use_cache:
             past_key_values.seen_tokens += hidden_states.shape[1]
-        hidden_states = self.norm(hidden_states)
+        if residual is not None:
+            _, hidden_states = add_rms_norm(hidden_states, residual, self.norm.weight, self.norm.eps)
+        else:
+            hidden_states = self.norm(hidden_states)
         if output_hidden_states:
             all_hidden_states += (hidden_states,)
         if not return_dict:
