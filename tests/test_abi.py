@@ -114,3 +114,20 @@ def test_layer_op_entry_points_validate_before_launch():
     assert b"V=96" in so.ngdn_last_error()
     assert so.ngdn_rmsnorm_gated_bwd(_lib.NGDN_BF16, 4, 64, *([None] * 10)) == 1
     assert b"NULL" in so.ngdn_last_error()
+
+
+def test_add_rmsnorm_entry_points_validate_before_launch():
+    so = _lib.lib()
+    F32, BF16 = _lib.NGDN_F32, _lib.NGDN_BF16
+    # bf16 x with an fp32 residual is not one of the kernel's dtype combinations
+    assert so.ngdn_add_rmsnorm_fwd(BF16, F32, BF16, 4, 1024, 1e-5, *([None] * 7)) == 1
+    assert b"dtypes" in so.ngdn_last_error()
+    assert so.ngdn_add_rmsnorm_bwd(F32, F32, BF16, 4, 1024, *([None] * 10)) == 1
+    assert b"dtypes" in so.ngdn_last_error()
+    # unsupported width, then a residual without the buffer for h
+    assert so.ngdn_add_rmsnorm_fwd(F32, BF16, BF16, 4, 1000, 1e-5, *([None] * 7)) == 1
+    assert b"D=1000" in so.ngdn_last_error()
+    assert so.ngdn_add_rmsnorm_fwd(F32, BF16, BF16, 4, 1024, 1e-5, 8, 8, 8, None, 8, None, None) == 1
+    assert b"NULL" in so.ngdn_last_error()
+    # zero rows: nothing to do, nothing launched
+    assert so.ngdn_add_rmsnorm_fwd(F32, F32, F32, 0, 1024, 1e-5, *([None] * 7)) == 0
