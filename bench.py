@@ -68,9 +68,18 @@ def gpu_inputs(cfg, seed=0):
 
 
 def work_model(cfg):
-    """Algorithmic bytes and flops per launch of each entry point at cfg (one
-    fwd+bwd step), from the tensors each reads and writes once and its dense
-    tile products (2 m n k). Units: bytes, flop."""
+    """Work per launch of each entry point at cfg (one fwd+bwd step), as
+    (algorithmic bytes, design bytes, flops).
+
+    Algorithmic bytes count only op-level tensors, each once at its op-level
+    size: the op's inputs and parameters, its outputs (o, final state), the
+    output gradient do, the gradients it returns, and the state sequences
+    the op saves for its backward (level-0 chunk states h and upper group
+    states, fp32) with their gradients (dh, d_states). Tensors that exist only
+    between this build's kernels (W, U, T, Qg, Aqk, Kt, Vn and their
+    gradients, transposed copies, per-firing pairs) are not counted there.
+    Design bytes count every tensor the kernel reads and writes once, as this
+    kernel split lays it out. Flops are dense tile products, 2 m n k."""
     B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
     f = cfg["intervals"]
     es = 2 if cfg["dtype"] == torch.bfloat16 else 4   # inputs, parameters, gradients
@@ -78,62 +87,115 @@ def work_model(cfg):
     NT = -(-T // C)
     units = B * H * NT                       # chunk-heads
     ck, cv, cc = C * K * es, C * V * es, C * C * es   # input tiles of one chunk
+    gk = C * K * 4                                    # g and dg (fp32) of one chunk
     wk, wv, wc = C * K * 4, C * V * 4, C * C * 4      # fp32 working tiles
     kv = K * V * 4                                    # one state
+    cm = C * L * es                                   # mix of one chunk
     m = {}
     tok = B * T * H                                   # token-heads
+    fin0 = B * H * kv                                 # one level's final state
     # level-0 intra: reads q0,k,b,v,w + g (fp32); writes W,U,KtT,Qg,Aqk,gam
     # and the backward layouts Kt, WT, QgT, AqkT, TT
     m["ngdn_l0_intra_fwd"] = (
-        units * (3 * ck + 2 * cv + C * K * 4 + 4 * wk + wv + wc + K * 4 + 3 * wk + 2 * wc),
+        units * (3 * ck + 2 * cv + gk),
+        units * (3 * ck + 2 * cv + gk + 4 * wk + wv + wc + K * 4 + 3 * wk + 2 * wc),
         units * (2 * 2 * C * C * K + 2 * C * C * (K + V) + C ** 3 // 3))
     # level-0 scan: reads W, U, KtT, gam; writes hT, vnT and (training) h, vn; + final
-    m["ngdn_l0_scan_fwd"] = (units * (2 * wk + wv + K * 4 + 2 * kv + 2 * wv) + B * H * kv,
+    m["ngdn_l0_scan_fwd"] = (units * kv + fin0,
+                             units * (2 * wk + wv + K * 4 + 2 * kv + 2 * wv) + fin0,
                              units * 2 * 2 * C * K * V)
     # output: Qg, hT, Aqk, vnT, q of upper levels, mix; upper states once per
     # group; writes o and (training) level 0's read
     up_states = sum(B * H * n_groups(NT, f[lvl]) * kv for lvl in range(1, L))
     m["ngdn_output_fwd"] = (
-        units * (wk + kv + wc + wv + (L - 1) * ck + C * L * es + cv + wv) + up_states,
+        units * (L * ck + cm + kv + cv) + up_states,
+        units * (wk + kv + wc + wv + (L - 1) * ck + cm + cv + wv) + up_states,
         units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 2 * C * K * V))
     # dmix_0 = <do, read_0>: reads read_0 (fp32), do; writes dmix
-    m["ngdn_output_bwd"] = (tok * (V * 4 + V * es + L * 4), tok * 2 * V)
+    m["ngdn_output_bwd"] = (tok * (V * es + 4), tok * (V * 4 + V * es + L * 4), tok * 2 * V)
     # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
-    m["ngdn_l0_scan_bwd"] = (units * (3 * wk + wc + K * 4 + cv + C * es + kv + 2 * wv),
+    m["ngdn_l0_scan_bwd"] = (units * (cv + cm + kv),
+                             units * (3 * wk + wc + K * 4 + cv + C * es + kv + 2 * wv),
                              units * (2 * C * K * V * 3 + 2 * C * C * V))
     # level-0 chunk backward, state half: h, dSp, vn, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
-    m["ngdn_l0_bwd_state"] = (units * (2 * kv + 2 * wv + cv + C * es + 3 * wk + wc + K * 4),
+    m["ngdn_l0_bwd_state"] = (units * (2 * kv + cv + cm),
+                              units * (2 * kv + 2 * wv + cv + C * es + 3 * wk + wc + K * 4),
                               units * (3 * 2 * C * K * V + 2 * C * C * V))
     # level-0 chunk backward, intra half: q0,k,b,v,w,g, W,U,TT, dQg,dWT,dKt,dAqk,dgam,dVnT
     # -> dq0,dk,dv,dg,db,dw
     m["ngdn_l0_bwd_intra"] = (
-        units * (3 * ck + 2 * cv + C * K * 4 + wk + wv + wc + 3 * wk + wc + K * 4 + wv
-                 + 3 * ck + 2 * cv + C * K * 4),
+        units * 2 * (3 * ck + 2 * cv + gk),
+        units * (3 * ck + 2 * cv + gk + wk + wv + wc + 3 * wk + wc + K * 4 + wv
+                 + 3 * ck + 2 * cv + gk),
         units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     for lvl in range(1, L):
         nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         fu = B * H * nf
         nk, nv_ = N * K * 4, N * V * 4
-        m[f"ngdn_probe_fwd.{lvl}"] = (fu * (kv + 3 * nk + 4 * K) + H * (N * K + 4 * K * V) * es,
+        par_f = H * (N * K + 4 * K * V) * es          # the level's bank and projections
+        m[f"ngdn_probe_fwd.{lvl}"] = (fu * kv + par_f,
+                                      fu * (kv + 3 * nk + 4 * K) + par_f,
                                       fu * 5 * 2 * N * K * V)
-        m[f"ngdn_upper_scan_fwd.{lvl}"] = (fu * 3 * nk + B * H * ng * 2 * kv,
+        m[f"ngdn_upper_scan_fwd.{lvl}"] = (B * H * ng * kv + fin0,
+                                           fu * 3 * nk + B * H * ng * 2 * kv,
                                            fu * 2 * 2 * N * K * V)
         # reads of level lvl, per group: q_l, do, mix, the group state ->
         # d_states, dq_l, dmix_l (read, dq and dS products: 3 x 2 K V per token)
-        m[f"ngdn_read_state_bwd.{lvl}"] = (tok * (K * es + V * es + K * es + 2 * 4)
+        m[f"ngdn_read_state_bwd.{lvl}"] = (tok * (K * es + V * es + es + K * es + 4)
+                                           + B * H * ng * 2 * kv,
+                                           tok * (K * es + V * es + K * es + 2 * 4)
                                            + B * H * ng * 2 * kv, tok * 3 * 2 * K * V)
         # reverse firing scan: keys, A^T, gam, d_states -> dSp, dvn
-        m[f"ngdn_upper_scan_bwd.{lvl}"] = (fu * (2 * nk + K * 4 + kv + nv_) + B * H * ng * kv,
+        m[f"ngdn_upper_scan_bwd.{lvl}"] = (B * H * ng * kv,
+                                           fu * (2 * nk + K * 4 + kv + nv_) + B * H * ng * kv,
                                            fu * 2 * 2 * N * K * V)
         # firing backward: lower states (rows and transposed), this level's
         # states (both), dSp, dvn, parameters -> six workspaces, the lower
         # state's gradient; 14 N K V products
-        m[f"ngdn_probe_bwd.{lvl}"] = (fu * (4 * kv + kv + nv_ + 6 * nk + kv)
+        m[f"ngdn_probe_bwd.{lvl}"] = (fu * 3 * kv + H * (N * K + 8 * K * V) * es,
+                                      fu * (4 * kv + kv + nv_ + 6 * nk + kv)
                                       + H * (N * K + 8 * K * V) * es, fu * 14 * 2 * N * K * V)
         # parameter gradients: four A^T B sums over every firing's N rows
-        m[f"ngdn_param_grads.{lvl}"] = (fu * 5 * nk + 4 * H * K * V * 4,
+        m[f"ngdn_param_grads.{lvl}"] = (4 * H * K * V * 4, fu * 5 * nk + 4 * H * K * V * 4,
                                         4 * fu * 2 * N * K * V)
     return m, units
+
+
+# entry points whose work is matrix products (intra-chunk, output, probe):
+# the benchmark reports their achieved fraction of the dense MFMA peak
+MFMA_KERNELS = ("ngdn_l0_intra_fwd", "ngdn_output_fwd", "ngdn_l0_bwd_state", "ngdn_l0_bwd_intra",
+                "ngdn_probe_fwd", "ngdn_probe_bwd")
+
+
+def step_totals(cfg):
+    """Algorithmic HBM bytes and flops of one fwd+bwd step of the op as a
+    whole. Flops are the dense tile products of the op's mathematics with
+    C = 64: forward, per chunk-head 2C^2(3K+2V) + 6CKV + C^3/3 for level 0,
+    per token-head and upper level 2KV for its read, per firing-head 14NKV
+    for a promotion; backward 2C^2(6K+4V) + 12CKV + 4C^3, 4KV and 28NKV.
+    Bytes are the op-level tensors once: the
+    forward reads the inputs and parameters and writes o, the final state and
+    the fp32 state sequences it saves; the backward reads the inputs,
+    parameters, saved states and do and writes every gradient."""
+    B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
+    f = cfg["intervals"]
+    es = 2 if cfg["dtype"] == torch.bfloat16 else 4
+    NT = -(-T // 64)
+    tok = B * T * H
+    kv = K * V * 4
+    inputs = tok * ((L + 2) * K * es + 2 * V * es + K * 4 + L * es)
+    params = (L - 1) * H * (N * K + 4 * K * V) * es
+    states = B * H * (NT + sum(n_groups(NT, f[l]) for l in range(1, L))) * kv
+    fwd = inputs + params + tok * V * es + B * H * L * kv + states
+    bwd = inputs + params + states + tok * V * es + (inputs + params)
+    C = 64
+    units = B * H * NT
+    fires = sum(B * H * n_firings(NT, f[l]) for l in range(1, L))
+    flops = (units * (2 * C * C * (3 * K + 2 * V) + 6 * C * K * V + C ** 3 // 3)
+             + tok * (L - 1) * 2 * K * V + fires * 14 * N * K * V
+             + units * (2 * C * C * (6 * K + 4 * V) + 12 * C * K * V + 4 * C ** 3)
+             + tok * (L - 1) * 4 * K * V + fires * 28 * N * K * V)
+    return fwd + bwd, flops
 
 
 def profiled_traffic(config, entry):
@@ -333,7 +395,7 @@ def model_bench(args):
     linear = sum(m.weight.numel() for m in model.modules() if isinstance(m, torch.nn.Linear))
     opcfg = dict(B=B, T=T, H=cfg.num_heads, K=cfg.head_dim, V=cfg.head_dim, L=cfg.num_levels,
                  N=cfg.n_queries_per_level[0], intervals=cfg.firing_intervals, dtype=torch.bfloat16)
-    op_flops = sum(fl for _, fl in work_model(opcfg)[0].values()) * cfg.num_hidden_layers
+    op_flops = sum(w[2] for w in work_model(opcfg)[0].values()) * cfg.num_hidden_layers
     flops = 6 * linear * B * T + op_flops
     tflops = flops / (ms * 1e-3) / 1e12
     if args.kernel_table:
@@ -440,34 +502,48 @@ def main():
     # the dominant kernel among those on the launch stream (side-stream
     # intervals include the time they share the GPU with it)
     dom = max((n for n in per_step if n not in _lib.SIDE), key=per_step.get)
-    dom_work = model.get(dom)
-    if dom_work is not None:
-        dom_work = tuple(x * per_launch[dom] for x in dom_work)
+    peak_f = MFMA_BF16_TFLOPS if cfg["dtype"] == torch.bfloat16 else MFMA_FP32_TFLOPS
+
+    def launch_work(n):
+        return tuple(x * per_launch[n] for x in model[n])
+
     roof = None
-    if dom_work is not None:
-        nbytes, flops = dom_work
-        traffic = profiled_traffic(args.config, dom)
+    if dom in model:
+        nbytes, dbytes, flops = launch_work(dom)
         t = ms[dom] * 1e-3
-        gbs = nbytes / t / 1e9
-        tfs = flops / t / 1e12
-        peak_f = MFMA_BF16_TFLOPS if cfg["dtype"] == torch.bfloat16 else MFMA_FP32_TFLOPS
+        gbs, dgbs, tfs = nbytes / t / 1e9, dbytes / t / 1e9, flops / t / 1e12
         hbm_bound = (nbytes / (HBM_PEAK_GBS * 1e9)) >= (flops / (peak_f * 1e12))
-        if hbm_bound:
-            roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "algorithmic_bytes": nbytes, "avg_ms": round(ms[dom], 4)}
-        else:
-            roof = {"kernel": dom, "bound": "mfma", "achieved": round(tfs, 2), "peak": peak_f,
-                    "unit": "TFLOP/s", "frac": round(tfs / peak_f, 4), "traffic": traffic,
-                    "algorithmic_flops": flops, "avg_ms": round(ms[dom], 4)}
+        roof = {"kernel": dom, "bound": "hbm" if hbm_bound else "mfma",
+                "achieved": round(gbs if hbm_bound else tfs, 2),
+                "peak": HBM_PEAK_GBS if hbm_bound else peak_f,
+                "unit": "GB/s" if hbm_bound else "TFLOP/s",
+                "frac": round((gbs / HBM_PEAK_GBS) if hbm_bound else (tfs / peak_f), 4),
+                "traffic": profiled_traffic(args.config, dom),
+                "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                "design_bytes": dbytes, "design_frac": round(dgbs / HBM_PEAK_GBS, 4),
+                "avg_ms": round(ms[dom], 4)}
+        # the matrix-product kernels' achieved fraction of the dense MFMA peak
+        mf = {}
+        for n in sorted(per_step, key=per_step.get, reverse=True):
+            if n.split(".")[0] in MFMA_KERNELS and n in model:
+                fl = launch_work(n)[2]
+                tf = fl / (ms[n] * 1e-3) / 1e12
+                mf[n] = {"tflops": round(tf, 2), "frac": round(tf / peak_f, 4),
+                         "avg_ms": round(ms[n], 4)}
+        roof["mfma_kernels"] = mf
+        sb, sf = step_totals(cfg)
+        st = elapsed / args.steps
+        roof["step"] = {"algorithmic_bytes": sb, "hbm_frac": round(sb / st / 1e9 / HBM_PEAK_GBS, 4),
+                        "algorithmic_flops": sf,
+                        "mfma_frac": round(sf / st / 1e12 / peak_f, 4)}
     if args.kernel_table:
         for n in sorted(per_step, key=per_step.get, reverse=True):
-            w = model.get(n)
             extra = ""
-            if w:
+            if n in model:
                 t = ms[n] * 1e-3
-                w = tuple(x * per_launch[n] for x in w)
-                extra = f"  {w[0] / t / 1e9:8.1f} GB/s  {w[1] / t / 1e12:7.2f} TFLOP/s"
+                a, d, fl = launch_work(n)
+                extra = (f"  alg {a / t / 1e9:7.1f} GB/s  design {d / t / 1e9:7.1f} GB/s"
+                         f"  {fl / t / 1e12:7.2f} TFLOP/s")
             side = "  (side stream)" if n in _lib.SIDE else ""
             print(f"{n:28s} {per_step[n]:8.3f} ms/step  {ms[n]:8.3f} ms/launch{extra}{side}",
                   file=sys.stderr)

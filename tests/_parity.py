@@ -1,0 +1,90 @@
+"""The parity bar shared by the GPU tests, with the errors it measured.
+
+The bar: against the float64 oracle on identical
+inputs, elementwise
+    |got - ref| <= atol + rtol |ref|
+with (atol, rtol) = (2e-3, 1e-2) for bf16 inputs and (1e-5, 1e-5) for fp32
+inputs. This unscaled form is asserted for the forward outputs, the final
+state and every per-token gradient (q, k, v, g, b, w, mix, initial state).
+
+The per-head parameter gradients (query banks and the four projections) are
+sums over every firing and batch row: their values reach tens, where a
+single bf16 rounding of one summand is already above 2e-3. For them the
+absolute part is scaled by m = max(1, max|ref|):
+    |got - ref| <= atol m + rtol |ref|
+and the unscaled figures are still measured and reported.
+
+Every comparison prints one line (name, max-abs error, max |ref|, and the
+largest ratio of the error to the unscaled and to the scaled bound; <= 1
+passes) and, when the environment variable NGDN_PARITY_LOG names a file,
+appends the same figures to it as a JSON line.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import torch
+
+TOL = {torch.float32: (1e-5, 1e-5), torch.float64: (1e-5, 1e-5),
+       torch.bfloat16: (2e-3, 1e-2), torch.float16: (2e-3, 1e-2)}
+
+# gradients that sum over firings and batch rows: scaled absolute part
+PARAM_GRADS = ("query_banks", "key_projections", "b_projections", "w_projections",
+               "g_projections")
+
+
+def is_param_grad(name: str) -> bool:
+    return any(p in name for p in PARAM_GRADS)
+
+
+def check(name, got, want, dtype, *, scaled=None, test=""):
+    """Asserts the bar for ``got`` against ``want``; returns the figures.
+
+    ``scaled``: None picks by name (parameter gradients scaled, everything
+    else unscaled); True / False force it."""
+    atol, rtol = TOL[dtype]
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    assert got.shape == want.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(want.shape)}"
+    if scaled is None:
+        scaled = is_param_grad(name)
+    err = (got - want).abs()
+    if not torch.isfinite(got).all():
+        raise AssertionError(f"{name}: non-finite values")
+    m = max(1.0, want.abs().max().item()) if want.numel() else 1.0
+    b_u = atol + rtol * want.abs()
+    b_s = atol * m + rtol * want.abs()
+    r_u = (err / b_u).max().item() if want.numel() else 0.0
+    r_s = (err / b_s).max().item() if want.numel() else 0.0
+    fig = dict(test=test, name=name, dtype=str(dtype).replace("torch.", ""),
+               max_abs=err.max().item() if want.numel() else 0.0,
+               max_ref=want.abs().max().item() if want.numel() else 0.0,
+               unscaled_ratio=r_u, scaled_ratio=r_s, bar="scaled" if scaled else "unscaled")
+    print(f"  {name:>16}: max_abs {fig['max_abs']:.3e}  max|ref| {fig['max_ref']:.3e}  "
+          f"err/bound unscaled {r_u:.3f} scaled {r_s:.3f} [{fig['bar']}]", flush=True)
+    path = os.environ.get("NGDN_PARITY_LOG")
+    if path:
+        with open(path, "a") as fh:
+            fh.write(json.dumps(fig) + "\n")
+    bad = err > (b_s if scaled else b_u)
+    if bad.any():
+        i = tuple(torch.nonzero(bad)[0].tolist())
+        raise AssertionError(
+            f"{name}: {int(bad.sum())}/{want.numel()} outside the {fig['bar']} bound "
+            f"(atol {atol}, rtol {rtol}); max err {fig['max_abs']:.3e}, max|ref| "
+            f"{fig['max_ref']:.3e}; first at {list(i)}: got {got[i].item():.6e} "
+            f"want {want[i].item():.6e}")
+    return fig
+
+
+def check_all(pairs, dtype, test=""):
+    """check() over (name, got, want) triples; reports every failure at once."""
+    errors = []
+    for name, got, want in pairs:
+        try:
+            check(name, got, want, dtype, test=test)
+        except AssertionError as e:
+            errors.append(str(e))
+    assert not errors, "\n".join(errors)

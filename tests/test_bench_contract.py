@@ -25,5 +25,20 @@ def test_work_model_covers_every_headline_entry_point():
     for name in ("ngdn_l0_intra_fwd", "ngdn_l0_scan_fwd", "ngdn_output_fwd", "ngdn_l0_bwd_intra",
                  "ngdn_l0_bwd_state", "ngdn_l0_scan_bwd", "ngdn_probe_fwd.1", "ngdn_probe_bwd.2",
                  "ngdn_param_grads.1", "ngdn_read_state_bwd.2", "ngdn_output_bwd"):
-        nbytes, flops = model[name]
-        assert nbytes > 0 and flops > 0, name
+        nbytes, design, flops = model[name]
+        assert 0 < nbytes <= design and flops > 0, name
+    # the level-0 intra backward's algorithmic bytes are the op's tensors it
+    # touches: reads q0, k, b, v, w (bf16) and g (fp32), writes their
+    # gradients: 224 KiB per chunk-head
+    assert model["ngdn_l0_bwd_intra"][0] == units * 2 * (5 * 64 * 128 * 2 + 64 * 128 * 4)
+
+
+def test_step_totals_at_the_headline():
+    sys.path.insert(0, ROOT)
+    import bench
+    from nested_recurrent_memory_amd.inputs import CONFIGS
+    nbytes, flops = bench.step_totals(CONFIGS["c2"])
+    # op-level tensors once per direction, with fp32 decay and saved states
+    assert 5.0e9 < nbytes < 5.6e9
+    # dense tile products of the forward and backward
+    assert 4.5e11 < flops < 5.5e11

@@ -281,3 +281,32 @@ def test_layer_tail_with_grad_raises():
     x = torch.randn(1, 70, cfg.hidden_size, device=DEV, requires_grad=True)
     with pytest.raises(ValueError, match="no backward"):
         layer(x)
+
+
+def test_layer_at_model_config_shape_matches_oracle():
+    """One layer at config 4's shape (hidden 1024, 8 heads of 128, three
+    levels at 1/4/16 chunks with 64 queries each), bf16, T = 2048 so that
+    level 2 fires twice: output and every gradient against the oracle layer."""
+    dtype = torch.bfloat16
+    print("layer at the model config's shape, bf16, T=2048", flush=True)
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    cfg, layer, p64 = _layer(dtype, 41, hidden_size=1024, num_heads=8, head_dim=128,
+                             num_levels=3, firing_intervals=(1, 4, 16),
+                             n_queries_per_level=(64, 64))
+    g = _gen(42)
+    x = torch.randn(1, 2048, cfg.hidden_size, generator=g).to(dtype)
+    dy = torch.randn(1, 2048, cfg.hidden_size, generator=g).to(dtype)
+
+    x64 = x.double().requires_grad_()
+    o64, _ = lref.layer_forward(p64, x64, cfg)
+    (o64 * dy.double()).sum().backward()
+
+    xd = x.to(DEV).requires_grad_()
+    o, _, _ = layer(xd)
+    o.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    _near("o", o, o64, dtype)
+    _near("dx", xd.grad, x64.grad, dtype)
+    for pname, p in layer.named_parameters():
+        wide = pname in ("A_log", "dt_bias")
+        _near(f"d{pname}", p.grad, p64[pname].grad, dtype, DECAY_BF16_TOL if wide else None)

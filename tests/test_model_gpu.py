@@ -236,6 +236,33 @@ def test_model_training_step_matches_oracle(mode, promotion):
         _near(f"d{name}", p.grad, p64[name].grad, 0.15 if decay else gtol)
 
 
+@pytest.mark.parametrize("mode", ["f32", "bf16_autocast"])
+def test_model_at_config4_shapes_matches_oracle(mode):
+    """Two layers of config 4 (hidden 1024, 8 heads of 128, three levels at
+    1/4/16 chunks with 64 queries each, SwiGLU 4096, vocab 32000), B=1,
+    T=1024 so that level 2 fires: loss and every parameter gradient."""
+    print(f"model at config 4 shapes {mode}", flush=True)
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    cfg = _cfg(vocab_size=32000, hidden_size=1024, num_heads=8, head_dim=128,
+               firing_intervals=(1, 4, 16), n_queries_per_level=(64, 64),
+               intermediate_size=4096)
+    m, p64 = _model(cfg, 31)
+    m.train()
+    ids = torch.randint(0, cfg.vocab_size, (1, 1024), generator=_gen(32))
+    _, loss64, _ = mref.model_forward(p64, ids, cfg, labels=ids)
+    loss64.backward()
+    tol = NORM_TOL[torch.float32 if mode == "f32" else torch.bfloat16]
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=mode != "f32"):
+        out = m(input_ids=ids.to(DEV), labels=ids.to(DEV))
+    out.loss.backward()
+    torch.cuda.synchronize()
+    _near("loss", out.loss, loss64, tol)
+    for name, p in m.named_parameters():
+        decay = mode != "f32" and name.endswith(("attn.A_log", "attn.dt_bias"))
+        gtol = tol if mode == "f32" else 5e-2
+        _near(f"d{name}", p.grad, p64[name].grad, 0.15 if decay else gtol)
+
+
 def test_model_options_match_oracle():
     """No short convolution, sigmoid level mix, a decay horizon, tied
     embeddings off, 2 levels firing every other chunk: fp32 loss and every

@@ -2,34 +2,28 @@
 
 The oracle's step (oracle/ngdn_oracle.py:step_forward, restating
 ops/naive.py:42-134) is pinned by prefill + step == one pass in
-tests/test_oracle.py. Tolerances: fp32 inputs 1e-5; bf16 inputs
-max-abs 2e-3 / rel 1e-2, the absolute part scaled by max(1, max|ref|) for
-the state (values up to a few units).
+tests/test_oracle.py. Bar (tests/_parity.py), elementwise and unscaled:
+fp32 inputs |err| <= 1e-5 + 1e-5 |ref|; bf16 inputs |err| <= 2e-3 +
+1e-2 |ref|, for the output and every level's state.
 """
 
 import pytest
 import torch
 
+import _parity
 import ngdn_oracle as ref
 from nested_recurrent_memory_amd import chunk_nested_gdn2, step_nested_gdn2
 from nested_recurrent_memory_amd.inputs import NAMES, make_inputs
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: (1e-5, 1e-5), torch.bfloat16: (2e-3, 1e-2)}
 STEP_IN = ("q", "k", "v", "g", "b", "w", "mix_weights")
 PARAMS = ("query_banks", "key_projections", "b_projections", "w_projections",
           "g_projections", "n_queries_per_level", "firing_intervals")
 
 
 def _close(name, got, want, dtype):
-    atol, rtol = TOL[dtype]
-    got, want = got.double().cpu(), want.double()
-    m = max(1.0, want.abs().max().item())
-    err = (got - want).abs()
-    bad = err > atol * m + rtol * want.abs()
-    assert not bad.any(), (f"{name}: {int(bad.sum())} elements out of bound, max err "
-                           f"{err.max().item():.3e} (scale {m:.3e})")
+    _parity.check(name, got, want, dtype, scaled=False, test="step")
 
 
 def _state(B, H, L, K, V, seed):
