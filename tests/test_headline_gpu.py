@@ -16,8 +16,7 @@ benchmark's inputs), through the same launch the benchmark times.
   completes a firing of every level).
 
 Bar (tests/_parity.py): bf16 |err| <= 2e-3 + 1e-2 |ref| elementwise for
-outputs, states and per-token gradients; parameter gradients with the
-absolute part scaled by max(1, max|ref|).
+every tensor (outputs, states and every gradient).
 """
 
 import pytest

@@ -12,8 +12,7 @@
   the full pass).
 
 Bar as everywhere (tests/_parity.py): bf16 |err| <= 2e-3 + 1e-2 |ref|
-elementwise for outputs, states and per-token gradients; the per-head
-parameter gradients take the absolute part scaled by max(1, max|ref|).
+elementwise for every tensor (outputs, states and every gradient).
 """
 
 import pytest
