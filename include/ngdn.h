@@ -262,6 +262,33 @@ int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* 
                   const void* key_projections, const void* bpT, const void* wpT,
                   const void* gpT, float* ws, void* o, void* stream);
 
+/* Bytes of the device scratch that ngdn_step_noalloc uses (one copy per GPU,
+ * held from the library's load until the process ends). */
+#define NGDN_STEP_SCRATCH_BYTES (32u << 20)
+
+/* ngdn_step without a workspace argument, and without allocating anything:
+ * no counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight decoding loops, harnesses that
+ * forbid hipMalloc). Same arguments, results and errors as ngdn_step, minus
+ * ws; the caller still passes every input and output. The levels with more
+ * than 64 pairs per firing (K for merge), which ngdn_step runs through ws,
+ * run through a file-scope device array of NGDN_STEP_SCRATCH_BYTES, a slice
+ * of batch rows at a time; one batch row needs H * (3 N K + K) * 4 bytes, N
+ * the most pairs of any level, and a call whose one row needs more than the
+ * scratch holds fails with NGDN_EINVAL. Nothing in the scratch needs initial
+ * contents. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (on different streams, or from different threads) race.
+ * The current device must be the stream's device; the first call on a device
+ * looks the scratch's address up (hipGetSymbolAddress) and keeps it. */
+int32_t ngdn_step_noalloc(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                          const float* g, const void* b, const void* w, const void* mix,
+                          const float* state_in, float* state_out, const int64_t* position,
+                          int64_t position_all, int32_t chunk_size,
+                          const int32_t* firing_intervals, int32_t promotion,
+                          const int32_t* n_queries, const void* query_banks, int32_t n_max,
+                          const void* key_projections, const void* bpT, const void* wpT,
+                          const void* gpT, void* o, void* stream);
+
 /* ---- The layer around the op (NestedGDN2Attention, layers/nested_gdn2.py),
  * which takes two modules from fla; these replace them. */
 

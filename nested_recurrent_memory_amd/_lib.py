@@ -52,6 +52,8 @@ SIGNATURES = {
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
     "ngdn_step": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4 + [P, P, P],
+    "ngdn_step_noalloc": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4
+                         + [P, P],
     "ngdn_short_conv_fwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P],
     "ngdn_short_conv_bwd": [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_rmsnorm_gated_fwd": [I32, I64, I32, ctypes.c_float, P, P, P, P, P, P],

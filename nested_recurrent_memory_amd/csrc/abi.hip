@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "ngdn_kernels.h"
 
@@ -396,57 +397,70 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
   return launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads");
 }
 
-int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* v,
-                  const float* g, const void* b, const void* w, const void* mix,
-                  const float* state_in, float* state_out, const int64_t* position,
-                  int64_t position_all, int32_t chunk_size,
-                  const int32_t* firing_intervals, int32_t promotion,
-                  const int32_t* n_queries, const void* query_banks, int32_t n_max,
-                  const void* key_projections, const void* bpT, const void* wpT,
-                  const void* gpT, float* ws, void* o, void* stream) {
-  g_err[0] = 0;
-  if (int32_t r = check_dims(d, "ngdn_step")) return r;
-  if (!q || !k || !v || !g || !b || !w || !mix || !state_in || !state_out || !o)
-    return fail(NGDN_EINVAL, "ngdn_step: NULL tensor");
-  if (chunk_size <= 0) return fail(NGDN_EINVAL, "ngdn_step: chunk_size %d", chunk_size);
-  if (!position && position_all < 0)
-    return fail(NGDN_EINVAL, "ngdn_step: position %lld is negative", (long long)position_all);
+}  // extern "C"
+
+namespace {
+
+// Scratch of ngdn_step_noalloc: the per-level pairs (A, KT, U, gam) of the
+// promotions whose levels take more than PROMOTE_NMAX pairs per firing. Each
+// GPU holds its own copy for the life of the process; host code uses only the
+// per-device address from hipGetSymbolAddress, never the array's name.
+static __device__ __align__(256) float scratch[NGDN_STEP_SCRATCH_BYTES / sizeof(float)];
+constexpr long long kScratchFloats = NGDN_STEP_SCRATCH_BYTES / sizeof(float);
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices];
+
+// The current device's address of `scratch`, looked up once per device.
+int32_t scratch_of_current_device(float** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NGDN_ELAUNCH, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(NGDN_EINVAL, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(NGDN_ELAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return NGDN_OK;
+}
+
+// Pairs per firing of level l (K for merge).
+inline int step_pairs(int promotion, const int32_t* n_queries, int K, int l) {
+  return promotion == 1 ? K : n_queries[l - 1];
+}
+
+// The body of ngdn_step and ngdn_step_noalloc. Levels with more than
+// PROMOTE_NMAX pairs per firing go through ws, rows_per_slice batch rows at a
+// time (probe, then one firing of the update, per slice); ws must hold
+// rows_per_slice * H * (3 N K + K) floats, N the most pairs of any level.
+int32_t step_run(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                 const float* g, const void* b, const void* w, const void* mix,
+                 const float* state_in, float* state_out, const int64_t* position,
+                 int64_t position_all, int32_t chunk_size, const int32_t* firing_intervals,
+                 int32_t promotion, const int32_t* n_queries, const void* query_banks,
+                 int32_t n_max, const void* key_projections, const void* bpT, const void* wpT,
+                 const void* gpT, float* ws, int rows_per_slice, void* o, void* stream,
+                 const char* what) {
   const int L = d->L, K = d->K, V = d->V;
   const long long skv = (long long)K * V;
-  const long long nst = (long long)d->B * d->H * L * skv;
-  if (state_in != state_out && state_out < state_in + nst && state_in < state_out + nst)
-    return fail(NGDN_EINVAL, "ngdn_step: state_in and state_out overlap");
-  if (L > 1) {
-    if (K != V) return fail(NGDN_EINVAL, "ngdn_step: promotion needs K == V, got %d, %d", K, V);
-    if (promotion != 0 && promotion != 1)
-      return fail(NGDN_EINVAL, "ngdn_step: promotion %d unknown", promotion);
-    if (!firing_intervals || (promotion == 0 && !n_queries) || !bpT || !wpT || !gpT || !ws)
-      return fail(NGDN_EINVAL, "ngdn_step: NULL parameter");
-    for (int l = 0; l < L; ++l)
-      if (firing_intervals[l] <= 0)
-        return fail(NGDN_EINVAL, "ngdn_step: firing interval %d of level %d", firing_intervals[l], l);
-    for (int l = 1; l < L; ++l) {
-      const int N = promotion == 1 ? K : n_queries[l - 1];
-      if (!pow2_ge16(N))
-        return fail(NGDN_EINVAL, "ngdn_step: pairs per firing must be a power of two >= 16 "
-                    "(and <= 128), got %d", N);
-      if (promotion == 0 && (N > n_max || !query_banks || !key_projections))
-        return fail(NGDN_EINVAL, "ngdn_step: n_queries=%d exceeds bank rows %d", N, n_max);
-    }
-  }
   hipStream_t st = (hipStream_t)stream;
   ngdn::StepArgs sa{q, k, v, g, b, w, mix, state_in, state_out, o, d->B, d->H, L, d->scale};
-  if (int32_t r = launched(ngdn::step_fwd(sa, d->dtype, K, V, st), "ngdn_step")) return r;
+  if (int32_t r = launched(ngdn::step_fwd(sa, d->dtype, K, V, st), what)) return r;
 
   const size_t hkv = (size_t)d->H * skv;
   const size_t esz = d->dtype == NGDN_BF16 ? 2 : 4;
-  const size_t units = (size_t)d->B * d->H;
   if (L == 1) return NGDN_OK;
   // Every level with at most 64 pairs per firing: all promotions in one
   // gated launch. With an int position the host skips it when no level fires.
   bool fused = L <= ngdn::MAXL;
   for (int l = 1; l < L; ++l)
-    if ((promotion == 1 ? K : n_queries[l - 1]) > ngdn::PROMOTE_NMAX) fused = false;
+    if (step_pairs(promotion, n_queries, K, l) > ngdn::PROMOTE_NMAX) fused = false;
   if (fused) {
     if (!position) {
       const long long end = (long long)position_all + 1;
@@ -462,56 +476,158 @@ int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* 
     pa.chunk = chunk_size;
     for (int l = 0; l < L; ++l) {
       pa.f[l] = firing_intervals[l];
-      pa.N[l] = l == 0 ? 0 : (promotion == 1 ? K : n_queries[l - 1]);
+      pa.N[l] = l == 0 ? 0 : step_pairs(promotion, n_queries, K, l);
     }
     pa.bank = query_banks; pa.Nmax = n_max;
     pa.kp = key_projections; pa.bpT = bpT; pa.wpT = wpT; pa.gpT = gpT;
     pa.merge = promotion;
     pa.B = d->B; pa.H = d->H; pa.L = L;
-    return launched(ngdn::promote_fwd(pa, d->dtype, K, st), "ngdn_step (promotions)");
+    return launched(ngdn::promote_fwd(pa, d->dtype, K, st), what);
   }
+  const long long row = (long long)d->H * L * skv;    // one batch row of the state
   for (int l = 1; l < L; ++l) {
-    ngdn::FireGate gate{nullptr, chunk_size, firing_intervals[l]};
-    if (position) {
-      gate.pos = reinterpret_cast<const long long*>(position);
-    } else {
+    if (!position) {
       const long long end = (long long)position_all + 1;
       if (end % chunk_size != 0 || (end / chunk_size) % firing_intervals[l] != 0) continue;
     }
-    const int N = promotion == 1 ? K : n_queries[l - 1];
-    float* A = ws;
-    float* KT = A + units * N * K;
-    float* U = KT + units * K * N;
-    float* gam = U + units * N * V;
+    const int N = step_pairs(promotion, n_queries, K, l);
     auto lvl = [&](const void* p, size_t per) -> const void* {
       return p ? static_cast<const char*>(p) + (size_t)(l - 1) * per * esz : nullptr;
     };
-    // probe of the level below (already updated this token), read as a
-    // "final state": one firing, source index past every stored group
-    ngdn::ProbeArgs pa{};
-    pa.below_fin = state_out + (long long)(l - 1) * skv;
-    pa.below = pa.below_fin; pa.below_mode = 1; pa.NGb = 0;
-    pa.bf_sh = L * skv; pa.bf_sb = d->H * pa.bf_sh;
-    pa.f_below = firing_intervals[l - 1]; pa.f_here = firing_intervals[l];
-    pa.bank = lvl(query_banks, (size_t)d->H * n_max * K); pa.Nmax = n_max;
-    pa.kp = lvl(key_projections, hkv);
-    pa.bpT = lvl(bpT, hkv); pa.wpT = lvl(wpT, hkv); pa.gpT = lvl(gpT, hkv);
-    pa.merge = promotion;
-    pa.A = A; pa.KT = KT; pa.U = U; pa.gam = gam;
-    pa.B = d->B; pa.H = d->H; pa.NF = 1; pa.N = N; pa.V = V;
-    pa.gate = gate;
-    if (int32_t r = launched(ngdn::probe_fwd(pa, d->dtype, K, st), "ngdn_step (probe)")) return r;
-    // one firing of this level's update, in place on state_out
-    ngdn::ScanArgs ca{};
-    ca.A = A; ca.BT = KT; ca.U = U; ca.gam = gam;
-    ca.init = state_out + (long long)l * skv; ca.init_sh = L * skv; ca.init_sb = d->H * ca.init_sh;
-    ca.state_mode = 0; ca.NG = 1;
-    ca.fin = state_out + (long long)l * skv; ca.fin_sh = ca.init_sh; ca.fin_sb = ca.init_sb;
-    ca.B = d->B; ca.H = d->H; ca.S = 1; ca.M = N; ca.V = V;
-    ca.gate = gate;
-    if (int32_t r = launched(ngdn::scan_fwd(ca, d->dtype, K, st), "ngdn_step (update)")) return r;
+    for (int b0 = 0; b0 < d->B; b0 += rows_per_slice) {
+      const int nb = std::min(rows_per_slice, d->B - b0);
+      const size_t units = (size_t)nb * d->H;
+      float* A = ws;
+      float* KT = A + units * N * K;
+      float* U = KT + units * K * N;
+      float* gam = U + units * N * V;
+      float* srow = state_out + (long long)b0 * row;
+      ngdn::FireGate gate{position ? reinterpret_cast<const long long*>(position) + b0 : nullptr,
+                          chunk_size, firing_intervals[l]};
+      // probe of the level below (already updated this token), read as a
+      // "final state": one firing, source index past every stored group
+      ngdn::ProbeArgs pa{};
+      pa.below_fin = srow + (long long)(l - 1) * skv;
+      pa.below = pa.below_fin; pa.below_mode = 1; pa.NGb = 0;
+      pa.bf_sh = L * skv; pa.bf_sb = d->H * pa.bf_sh;
+      pa.f_below = firing_intervals[l - 1]; pa.f_here = firing_intervals[l];
+      pa.bank = lvl(query_banks, (size_t)d->H * n_max * K); pa.Nmax = n_max;
+      pa.kp = lvl(key_projections, hkv);
+      pa.bpT = lvl(bpT, hkv); pa.wpT = lvl(wpT, hkv); pa.gpT = lvl(gpT, hkv);
+      pa.merge = promotion;
+      pa.A = A; pa.KT = KT; pa.U = U; pa.gam = gam;
+      pa.B = nb; pa.H = d->H; pa.NF = 1; pa.N = N; pa.V = V;
+      pa.gate = gate;
+      if (int32_t r = launched(ngdn::probe_fwd(pa, d->dtype, K, st), what)) return r;
+      // one firing of this level's update, in place on state_out
+      ngdn::ScanArgs ca{};
+      ca.A = A; ca.BT = KT; ca.U = U; ca.gam = gam;
+      ca.init = srow + (long long)l * skv; ca.init_sh = L * skv; ca.init_sb = d->H * ca.init_sh;
+      ca.state_mode = 0; ca.NG = 1;
+      ca.fin = srow + (long long)l * skv; ca.fin_sh = ca.init_sh; ca.fin_sb = ca.init_sb;
+      ca.B = nb; ca.H = d->H; ca.S = 1; ca.M = N; ca.V = V;
+      ca.gate = gate;
+      if (int32_t r = launched(ngdn::scan_fwd(ca, d->dtype, K, st), what)) return r;
+    }
   }
   return NGDN_OK;
+}
+
+// Checks shared by ngdn_step and ngdn_step_noalloc (not the workspace).
+int32_t step_check(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                   const float* g, const void* b, const void* w, const void* mix,
+                   const float* state_in, float* state_out, const int64_t* position,
+                   int64_t position_all, int32_t chunk_size, const int32_t* firing_intervals,
+                   int32_t promotion, const int32_t* n_queries, const void* query_banks,
+                   int32_t n_max, const void* key_projections, const void* bpT, const void* wpT,
+                   const void* gpT, void* o, const char* what) {
+  if (int32_t r = check_dims(d, what)) return r;
+  if (!q || !k || !v || !g || !b || !w || !mix || !state_in || !state_out || !o)
+    return fail(NGDN_EINVAL, "%s: NULL tensor", what);
+  if (chunk_size <= 0) return fail(NGDN_EINVAL, "%s: chunk_size %d", what, chunk_size);
+  if (!position && position_all < 0)
+    return fail(NGDN_EINVAL, "%s: position %lld is negative", what, (long long)position_all);
+  const int L = d->L, K = d->K, V = d->V;
+  const long long skv = (long long)K * V;
+  const long long nst = (long long)d->B * d->H * L * skv;
+  if (state_in != state_out && state_out < state_in + nst && state_in < state_out + nst)
+    return fail(NGDN_EINVAL, "%s: state_in and state_out overlap", what);
+  if (L > 1) {
+    if (K != V) return fail(NGDN_EINVAL, "%s: promotion needs K == V, got %d, %d", what, K, V);
+    if (promotion != 0 && promotion != 1)
+      return fail(NGDN_EINVAL, "%s: promotion %d unknown", what, promotion);
+    if (!firing_intervals || (promotion == 0 && !n_queries) || !bpT || !wpT || !gpT)
+      return fail(NGDN_EINVAL, "%s: NULL parameter", what);
+    for (int l = 0; l < L; ++l)
+      if (firing_intervals[l] <= 0)
+        return fail(NGDN_EINVAL, "%s: firing interval %d of level %d", what, firing_intervals[l], l);
+    for (int l = 1; l < L; ++l) {
+      const int N = step_pairs(promotion, n_queries, K, l);
+      if (!pow2_ge16(N))
+        return fail(NGDN_EINVAL, "%s: pairs per firing must be a power of two >= 16 "
+                    "(and <= 128), got %d", what, N);
+      if (promotion == 0 && (N > n_max || !query_banks || !key_projections))
+        return fail(NGDN_EINVAL, "%s: n_queries=%d exceeds bank rows %d", what, N, n_max);
+    }
+  }
+  return NGDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t ngdn_step(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                  const float* g, const void* b, const void* w, const void* mix,
+                  const float* state_in, float* state_out, const int64_t* position,
+                  int64_t position_all, int32_t chunk_size,
+                  const int32_t* firing_intervals, int32_t promotion,
+                  const int32_t* n_queries, const void* query_banks, int32_t n_max,
+                  const void* key_projections, const void* bpT, const void* wpT,
+                  const void* gpT, float* ws, void* o, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = step_check(d, q, k, v, g, b, w, mix, state_in, state_out, position,
+                             position_all, chunk_size, firing_intervals, promotion, n_queries,
+                             query_banks, n_max, key_projections, bpT, wpT, gpT, o, "ngdn_step"))
+    return r;
+  if (d->L > 1 && !ws) return fail(NGDN_EINVAL, "ngdn_step: NULL parameter");
+  return step_run(d, q, k, v, g, b, w, mix, state_in, state_out, position, position_all,
+                  chunk_size, firing_intervals, promotion, n_queries, query_banks, n_max,
+                  key_projections, bpT, wpT, gpT, ws, d->B, o, stream, "ngdn_step");
+}
+
+int32_t ngdn_step_noalloc(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                          const float* g, const void* b, const void* w, const void* mix,
+                          const float* state_in, float* state_out, const int64_t* position,
+                          int64_t position_all, int32_t chunk_size,
+                          const int32_t* firing_intervals, int32_t promotion,
+                          const int32_t* n_queries, const void* query_banks, int32_t n_max,
+                          const void* key_projections, const void* bpT, const void* wpT,
+                          const void* gpT, void* o, void* stream) {
+  g_err[0] = 0;
+  const char* what = "ngdn_step_noalloc";
+  if (int32_t r = step_check(d, q, k, v, g, b, w, mix, state_in, state_out, position,
+                             position_all, chunk_size, firing_intervals, promotion, n_queries,
+                             query_banks, n_max, key_projections, bpT, wpT, gpT, o, what))
+    return r;
+  // the most pairs of any level decides the scratch taken per (row, head)
+  int nmax_pairs = 0;
+  for (int l = 1; l < d->L; ++l)
+    nmax_pairs = std::max(nmax_pairs, step_pairs(promotion, n_queries, d->K, l));
+  float* ws = nullptr;
+  int rows = d->B;
+  if (nmax_pairs > ngdn::PROMOTE_NMAX) {
+    const long long per_row = (long long)d->H * (3LL * nmax_pairs * d->K + d->K);
+    if (per_row > kScratchFloats)
+      return fail(NGDN_EINVAL, "%s: one batch row needs %lld bytes of scratch (H=%d, %d pairs, "
+                  "K=%d); the scratch holds %lld bytes", what, per_row * 4, d->H, nmax_pairs,
+                  d->K, (long long)NGDN_STEP_SCRATCH_BYTES);
+    rows = (int)std::min<long long>(d->B, kScratchFloats / per_row);
+    if (int32_t r = scratch_of_current_device(&ws, what)) return r;
+  }
+  return step_run(d, q, k, v, g, b, w, mix, state_in, state_out, position, position_all,
+                  chunk_size, firing_intervals, promotion, n_queries, query_banks, n_max,
+                  key_projections, bpT, wpT, gpT, ws, rows, o, stream, what);
 }
 
 int32_t ngdn_short_conv_fwd(int32_t dtype, int32_t B, int32_t T, int32_t D, int32_t W,

@@ -46,6 +46,27 @@ def test_invalid_arguments_return_error_without_launch():
     assert rc == 1 and b"power of two" in so.ngdn_last_error()
 
 
+def test_step_noalloc_validates_before_any_hip_call():
+    """Shape errors, and a batch row larger than the scratch, are refused
+    before the entry point touches the GPU (the pointers here are never
+    dereferenced)."""
+    so = _lib.lib()
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(12)]
+    fs = (ctypes.c_int32 * 2)(1, 1)
+    nqs = (ctypes.c_int32 * 1)(128)
+    d = _lib.dims(1, 1, 2, 2, 96, 96, _lib.NGDN_F32, 0.1)      # K=96 unsupported
+    rc = so.ngdn_step_noalloc(ctypes.byref(d), *fake[:7], fake[7], fake[7], None, 63, 64, fs, 0,
+                              nqs, fake[8], 128, fake[9], fake[10], fake[11], fake[11],
+                              fake[11], None)
+    assert rc == 1 and b"K=96" in so.ngdn_last_error()
+    # one row of 200 heads at 128 pairs and K=128 needs 39.4 MB > 32 MiB
+    d = _lib.dims(1, 1, 200, 2, 128, 128, _lib.NGDN_F32, 0.1)
+    rc = so.ngdn_step_noalloc(ctypes.byref(d), *fake[:7], fake[7], fake[7], None, 63, 64, fs, 0,
+                              nqs, fake[8], 128, fake[9], fake[10], fake[11], fake[11],
+                              fake[11], None)
+    assert rc == 1 and b"scratch" in so.ngdn_last_error()
+
+
 def _base(**kw):
     cfg = dict(B=1, T=256, H=2, K=64, V=64, L=2, N=32, intervals=(1, 2))
     cfg.update(kw)
