@@ -116,6 +116,32 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             const float* initial_state, float* states,
                             float* statesT, float* final_state, void* stream);
 
+/* The promotions of level `level` >= 1, fused: the reference's per-level
+ * chain gather_source -> probe_learned / probe_merge -> update_state
+ * (nested_gdn2/ops/chunk.py:257-290 with ops/probe.py:34-136 and
+ * ops/update_fwd.py:131-204) in one launch of B*H workgroups, each running
+ * its (b, h)'s NF = NT / f_here firings in order with the level's state on
+ * chip: the lower snapshot, the probe's pairs and gates and the state never
+ * go to HBM between the probe's read and the update's write. below: the lower
+ * level's stored states transposed, level 1 the level-0 chunk states hT
+ * [B,H,NT,V,K], level >= 2 the lower statesT [B,ng_below,H,V,K]; a firing
+ * whose source index is ng_below reads final_state[:, :, level-1].
+ * Parameters as for ngdn_probe_fwd. Writes states [B,NG,H,K,V] and statesT
+ * [B,NG,H,V,K] (NG = ceil(NT / f_here); the state entering each group,
+ * groups past the last firing hold the final state) and
+ * final_state[:, :, level]. For the backward (all three or none): keysN
+ * [B,H,NF,N,K] and AT = (keys b e^g)^T [B,H,NF,K,N] (split), gam = e^g
+ * [B,H,NF,K] fp32, as ngdn_probe_fwd writes them. Up to 64 pairs per firing
+ * (merge: K = 64); other levels use ngdn_probe_fwd + ngdn_upper_scan_fwd. */
+int32_t ngdn_promote_chain_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
+                               int32_t n_queries, int32_t f_below, int32_t f_here,
+                               const float* below, int32_t ng_below,
+                               float* final_state, const void* query_banks,
+                               int32_t n_max, const void* key_projections,
+                               const void* bpT, const void* wpT, const void* gpT,
+                               const float* initial_state, float* states, float* statesT,
+                               float* keysN, float* AT, float* gam, void* stream);
+
 /* Output for every token (ops/chunk.py:129-156, 250-251, 285-286):
  * o = mix_0 (Qg h + Aqk Vn) + sum_{l>=1} mix_l scale q_l S_l[group].
  * statesT[l] (l = 1..L-1) is level l's transposed group states
@@ -128,6 +154,18 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
                         const void* mix, const float* const* statesT,
                         const int32_t* ng, const int32_t* f, void* o,
                         float* read0, void* stream);
+
+/* ngdn_output_fwd in two passes, so that the first can run beside the upper
+ * levels' promotions (it reads level 0 only): ngdn_output_l0_fwd writes
+ * level 0's read Qg h + Aqk Vn into read0 (fp32 [B,T,H,V]); then
+ * ngdn_output_upper_fwd forms o = mix_0 read0 + sum_{l>=1} mix_l scale q_l
+ * S_l[group] with the same arguments as ngdn_output_fwd. Same results as the
+ * one-pass entry point. */
+int32_t ngdn_output_l0_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                           const float* hT, const float* vnT, float* read0, void* stream);
+int32_t ngdn_output_upper_fwd(const ngdn_dims* d, const float* read0, const void* q,
+                              const void* mix, const float* const* statesT,
+                              const int32_t* ng, const int32_t* f, void* o, void* stream);
 
 /* ---------------------------------------------------------------- backward
  * The backward of ChunkNestedGDN2Function (ops/chunk.py:650-719,

@@ -41,7 +41,11 @@ SIGNATURES = {
     "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
                       + [P] * 11 + [P],
     "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
+    "ngdn_promote_chain_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
+                              + [P] * 6 + [P],
     "ngdn_output_fwd": [PD, P, P, P, P, P, P, P, P, P, P, P, P],
+    "ngdn_output_l0_fwd": [PD, P, P, P, P, P, P],
+    "ngdn_output_upper_fwd": [PD, P, P, P, P, P, P, P, P],
     "ngdn_output_bwd": [PD, P, P, P, P],
     "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, P],

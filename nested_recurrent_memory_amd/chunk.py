@@ -12,9 +12,14 @@ Forward, per call (reference composition ops/chunk.py:159-304):
   ngdn_l0_intra_fwd    per-chunk level-0 terms, all chunks in parallel
   ngdn_l0_scan_fwd     level-0 state recurrence, states h per chunk
   for each level l >= 1:
-    ngdn_probe_fwd       probe the level below at this level's firings
-    ngdn_upper_scan_fwd  this level's write scan, one state per group
+    ngdn_promote_chain_fwd  the level's firings in order per (batch, head):
+                            gather, probe and update on chip, one state per
+                            group stored (up to 64 pairs per firing), or
+    ngdn_probe_fwd          probe the level below at this level's firings,
+    ngdn_upper_scan_fwd     then this level's write scan (128 pairs)
   ngdn_output_fwd      level-0 read + every upper read + mix, o written once
+                       (with a fused ladder: ngdn_output_l0_fwd beside it on a
+                       side stream, then ngdn_output_upper_fwd)
 """
 
 from __future__ import annotations
@@ -75,6 +80,18 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
         if promotion == "learned" and n > query_banks.shape[2]:
             raise ValueError(
                 f"n_queries={n} exceeds the {query_banks.shape[2]} rows of query_banks")
+
+
+# The promotions of a level with at most 64 pairs per firing (merge: K = 64)
+# run fused, one launch per level (ngdn_promote_chain_fwd); others as a probe
+# launch and a scan launch. False forces the two-launch path everywhere.
+FUSED_PROMOTION = True
+
+
+def _chain_ok(K, N, merge):
+    if merge:
+        return K == 64 and N == 64
+    return K in (64, 128) and N in (16, 32, 64)
 
 
 # Batch rows are independent all the way through the op, so the kernels run
@@ -166,12 +183,23 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         N = K if merge else nq[lvl - 1]
         nf1 = max(nf, 1)
-        levels[lvl] = dict(N=N, nf=nf, ng=ng, A=f32(B, H, nf1, N, K), KT=f32(B, H, nf1, K, N),
-                           U=f32(B, H, nf1, N, V), gam=f32(B, H, nf1, K),
-                           keys=opt(B, H, nf1, N, K), AT=opt(B, H, nf1, K, N))
+        if FUSED_PROMOTION and _chain_ok(K, N, merge):
+            # one launch: probes and updates on chip; the backward's keys,
+            # (keys b e^g)^T and e^g only when training
+            levels[lvl] = dict(N=N, nf=nf, ng=ng, chain=True, gam=opt(B, H, nf1, K),
+                               keys=opt(B, H, nf1, N, K), AT=opt(B, H, nf1, K, N))
+        else:
+            levels[lvl] = dict(N=N, nf=nf, ng=ng, chain=False, A=f32(B, H, nf1, N, K),
+                               KT=f32(B, H, nf1, K, N), U=f32(B, H, nf1, N, V),
+                               gam=f32(B, H, nf1, K), keys=opt(B, H, nf1, N, K),
+                               AT=opt(B, H, nf1, K, N))
         states[lvl], statesT[lvl] = f32(B, ng, H, K, V), f32(B, ng, H, V, K)
     o = e(B, T, H, V)
-    read0 = f32(B, T, H, V) if train else None
+    # With a fused promotion ladder (one workgroup per (batch, head), a
+    # fraction of the GPU) level 0's share of the output runs beside it on a
+    # side stream, writing its read; a second pass adds the upper levels'.
+    chains = any(levels[lvl]["chain"] for lvl in range(1, L))
+    read0 = f32(B, T, H, V) if (train or chains) else None
     P = _lib.ptr
 
     def launch(b0, nb, st):
@@ -182,9 +210,24 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
             q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT)), sp)
         _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
             W, U, KtT, gam, init_, hT, vnT, h_, vn_, final)), sp)
+        split = chains and nb == B
+        if split:
+            side = _aux_streams(dev)[0]
+            side.wait_event(st.record_event())
+            _lib.call("ngdn_output_l0_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+                Qg, Aqk, hT, vnT, read0)), _lib.ptr_of_stream(side), stream=side)
         for lvl in range(1, L):
             lv = levels[lvl]
             fh, fb = f[lvl], f[lvl - 1]
+            if lv["chain"]:
+                belowT, ngb = (hT, NT) if lvl == 1 else (statesT[lvl - 1], n_groups(NT, fb))
+                _lib.call("ngdn_promote_chain_fwd", ctypes.byref(d), lvl, int(merge), lv["N"], fb,
+                          fh, P(R(belowT)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
+                          P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]), P(R(init_)),
+                          P(R(states[lvl])), P(R(statesT[lvl])),
+                          *(P(R(lv[x])) for x in ("keys", "AT", "gam")), sp,
+                          tag=f"ngdn_promote_chain_fwd.{lvl}")
+                continue
             below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
             if lv["nf"] > 0:
                 _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), lv["N"], fb, fh,
@@ -197,8 +240,13 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                       P(R(states[lvl])), P(R(statesT[lvl])), P(R(final)), sp,
                       tag=f"ngdn_upper_scan_fwd.{lvl}")
         spT, ngs, fs = _level_arrays([R(x) for x in statesT], NT, f, L)
-        _lib.call("ngdn_output_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-            Qg, Aqk, hT, vnT, q_, mix_)), spT, ngs, fs, P(R(o)), P(R(read0)), sp)
+        if split:
+            st.wait_stream(side)
+            _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(R(read0)), P(R(q_)),
+                      P(R(mix_)), spT, ngs, fs, P(R(o)), sp)
+        else:
+            _lib.call("ngdn_output_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+                Qg, Aqk, hT, vnT, q_, mix_)), spT, ngs, fs, P(R(o)), P(R(read0)), sp)
 
     _run_groups(B, dev, launch)
     saved = None

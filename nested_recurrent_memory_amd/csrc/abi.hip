@@ -134,6 +134,64 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   return launched(ngdn::probe_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_probe_fwd");
 }
 
+int32_t ngdn_promote_chain_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
+                               int32_t n_queries, int32_t f_below, int32_t f_here,
+                               const float* below, int32_t ng_below,
+                               float* final_state, const void* query_banks,
+                               int32_t n_max, const void* key_projections,
+                               const void* bpT, const void* wpT, const void* gpT,
+                               const float* initial_state, float* states, float* statesT,
+                               float* keysN, float* AT, float* gam, void* stream) {
+  g_err[0] = 0;
+  const char* what = "ngdn_promote_chain_fwd";
+  if (int32_t r = check_dims(d, what)) return r;
+  if (level < 1 || level >= d->L)
+    return fail(NGDN_EINVAL, "%s: level %d outside [1, L=%d)", what, level, d->L);
+  if (d->K != d->V)
+    return fail(NGDN_EINVAL, "%s: promotion needs K == V, got %d, %d", what, d->K, d->V);
+  if (promotion != 0 && promotion != 1)
+    return fail(NGDN_EINVAL, "%s: promotion %d unknown", what, promotion);
+  const int N = promotion == 1 ? d->K : n_queries;
+  if (!pow2_ge16(N))
+    return fail(NGDN_EINVAL, "%s: pairs per firing must be a power of two >= 16 "
+                "(and <= 128), got %d", what, N);
+  if (!ngdn::promote_chain_supported(d->K, N, promotion == 1))
+    return fail(NGDN_EINVAL, "%s: %d pairs per firing at K=%d (%s) need the two-launch path "
+                "(ngdn_probe_fwd, ngdn_upper_scan_fwd)", what, N, d->K,
+                promotion == 1 ? "merge" : "learned");
+  if (promotion == 0 && (n_queries > n_max || !query_banks || !key_projections))
+    return fail(NGDN_EINVAL, "%s: n_queries=%d exceeds bank rows %d", what, n_queries, n_max);
+  if (f_below <= 0 || f_here <= 0)
+    return fail(NGDN_EINVAL, "%s: firing intervals must be positive", what);
+  if (!below || !final_state || !bpT || !wpT || !gpT || !states || !statesT)
+    return fail(NGDN_EINVAL, "%s: NULL tensor", what);
+  if ((keysN || AT || gam) && !(keysN && AT && gam))
+    return fail(NGDN_EINVAL, "%s: keys, AT and gam are written together", what);
+  const int NT = nchunks(d);
+  const long long skv = (long long)d->K * d->V;
+  ngdn::PromoteChainArgs a{};
+  a.below = below; a.below_mode = level == 1 ? 0 : 1; a.NGb = ng_below;
+  a.below_fin = final_state + (long long)(level - 1) * skv;
+  a.bf_sh = d->L * skv; a.bf_sb = d->H * a.bf_sh;
+  a.f_below = f_below; a.f_here = f_here;
+  const size_t hkv = (size_t)d->H * skv;
+  const size_t esz = d->dtype == NGDN_BF16 ? 2 : 4;
+  auto lvl = [&](const void* p, size_t per) -> const void* {
+    return p ? static_cast<const char*>(p) + (size_t)(level - 1) * per * esz : nullptr;
+  };
+  a.bank = lvl(query_banks, (size_t)d->H * n_max * d->K); a.Nmax = n_max;
+  a.kp = lvl(key_projections, hkv);
+  a.bpT = lvl(bpT, hkv); a.wpT = lvl(wpT, hkv); a.gpT = lvl(gpT, hkv);
+  a.init = initial_state ? initial_state + (long long)level * skv : nullptr;
+  a.init_sh = d->L * skv; a.init_sb = d->H * a.init_sh;
+  a.st_kv = states; a.st_vk = statesT;
+  a.fin = final_state + (long long)level * skv; a.fin_sh = a.init_sh; a.fin_sb = a.init_sb;
+  a.keysN = keysN; a.AT = AT; a.gam = gam;
+  a.B = d->B; a.H = d->H; a.NF = NT / f_here; a.NG = (NT + f_here - 1) / f_here;
+  return launched(ngdn::promote_chain_fwd(a, d->dtype, d->K, N, promotion == 1,
+                                          (hipStream_t)stream), what);
+}
+
 int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* A,
                             const float* KT, const float* U, const float* gam,
@@ -185,6 +243,41 @@ int32_t ngdn_output_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
   return launched(ngdn::output_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream), "ngdn_output_fwd");
 }
 
+
+int32_t ngdn_output_l0_fwd(const ngdn_dims* d, const float* Qg, const float* Aqk,
+                           const float* hT, const float* vnT, float* read0, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_output_l0_fwd")) return r;
+  if (!Qg || !Aqk || !hT || !vnT || !read0)
+    return fail(NGDN_EINVAL, "ngdn_output_l0_fwd: NULL tensor");
+  ngdn::OutputArgs a{};
+  a.Qg = Qg; a.Aqk = Aqk; a.hT = hT; a.vnT = vnT; a.read0 = read0; a.l0_only = 1;
+  a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
+  return launched(ngdn::output_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
+                  "ngdn_output_l0_fwd");
+}
+
+int32_t ngdn_output_upper_fwd(const ngdn_dims* d, const float* read0, const void* q,
+                              const void* mix, const float* const* statesT,
+                              const int32_t* ng, const int32_t* f, void* o, void* stream) {
+  g_err[0] = 0;
+  if (int32_t r = check_dims(d, "ngdn_output_upper_fwd")) return r;
+  if (d->L > 1 && d->K != d->V)
+    return fail(NGDN_EINVAL, "ngdn_output_upper_fwd: upper levels need K == V, got %d, %d",
+                d->K, d->V);
+  if (!read0 || !q || !mix || !o) return fail(NGDN_EINVAL, "ngdn_output_upper_fwd: NULL tensor");
+  ngdn::OutputArgs a{};
+  a.q = q; a.mix = mix; a.read0_in = read0;
+  for (int l = 1; l < d->L; ++l) {
+    if (!statesT || !statesT[l] || !ng || !f || f[l] <= 0)
+      return fail(NGDN_EINVAL, "ngdn_output_upper_fwd: level %d states missing", l);
+    a.statesT[l] = statesT[l]; a.NGl[l] = ng[l]; a.f[l] = f[l];
+  }
+  a.o = o;
+  a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
+  return launched(ngdn::output_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
+                  "ngdn_output_upper_fwd");
+}
 
 int32_t ngdn_output_bwd(const ngdn_dims* d, const float* read0, const void* dout,
                         float* dmix, void* stream) {

@@ -153,6 +153,36 @@ struct PromoteArgs {
 };
 hipError_t promote_fwd(const PromoteArgs& a, int dtype, int K, hipStream_t st);
 
+// One level's promotions in the chunk op, fused (promote_chunk.hip): one
+// workgroup of 8 waves per (b, h) runs the level's firings in order with the
+// level's state in registers: per firing the gather of the lower snapshot,
+// the probe (as probe_fwd) and the update (as one scan_fwd step), and the
+// group states stored before each firing (store-then-fire; groups past the
+// last firing hold the final state). below: the lower level's stored states
+// as [V][K] rows, mode 0 [B,H,NGb,V,K] (level-0 chunk states) or mode 1
+// [B,NGb,H,V,K] (upper group states); below_fin: the lower final state
+// ([K][V] rows at strides). Parameters: this level's slices in the working
+// dtype, as for probe_fwd. init: [K][V] at strides, or null (zeros).
+// st_kv [B,NG,H,K,V] and st_vk [B,NG,H,V,K] fp32; fin [K][V] at strides.
+// For the backward (null for inference): keysN [B,H,NF,N,K] and
+// AT = (keys b e^g)^T [B,H,NF,K,N] in split form, gam = e^g [B,H,NF,K].
+// Up to PROMOTE_NMAX pairs per firing; merge at K = 64 only.
+struct PromoteChainArgs {
+  const float* below; int below_mode; int NGb;
+  const float* below_fin; long long bf_sb, bf_sh;
+  int f_below, f_here;
+  const void* bank; int Nmax;
+  const void* kp; const void* bpT; const void* wpT; const void* gpT;
+  const float* init; long long init_sb, init_sh;
+  float* st_kv; float* st_vk;
+  float* fin; long long fin_sb, fin_sh;
+  float* keysN; float* AT; float* gam;
+  int B, H, NF, NG;
+};
+bool promote_chain_supported(int K, int N, bool merge);
+hipError_t promote_chain_fwd(const PromoteChainArgs& a, int dtype, int K, int N, bool merge,
+                             hipStream_t st);
+
 // The layer's ShortConvolution (layer_ops.hip): x, y, dy, dx [B,T,D] and the
 // caches [B,D,W] in the working dtype, w and dw [D][W] fp32 (dw summed
 // into), act: SiLU after the convolution.
@@ -316,11 +346,15 @@ namespace ngdn {
 // S^T rows [B,NG_l,H,V,K] (statesT). o [B,T,H,V] in the working dtype. When
 // read0 is set, level 0's unmixed read Qg h_n + Aqk Vn is also written, fp32
 // [B,T,H,V] (the backward's dmix_0).
+// Split in two passes (the first can run beside the upper levels' promotions):
+// l0_only computes level 0's read into read0 and writes nothing else;
+// read0_in takes that read instead of computing it and forms o.
 struct OutputArgs {
   const float* Qg; const float* Aqk; const float* hT; const float* vnT;
   const void* q; const void* mix;
   const float* statesT[MAXL]; int NGl[MAXL]; int f[MAXL];
   void* o; float* read0;
+  const float* read0_in; int l0_only;
   int B, T, H, L, NT;
   float scale;
 };

@@ -73,14 +73,37 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
     }
   };
 
-  // ---- level 0: Qg h + Aqk Vn (its read kept for the backward, stored last)
+  // ---- level 0: Qg h + Aqk Vn (its read kept for the backward, stored
+  // last), or the read a level-0 pass stored
+  if (a.read0_in) {
 #pragma unroll
-  for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
-  for (int kb = 0; kb < K; kb += KH)
-    stage(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), std::integral_constant<int, KH / KS>{},
-          a.hT + cix * V * K + kb, K, std::integral_constant<int, KH>{}, LD);
-  stage(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), std::integral_constant<int, C / KS>{},
-        a.vnT + cix * V * C, C, std::integral_constant<int, C>{}, LDC);
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r);
+      const float* rp = a.read0_in + (((size_t)b * T + t0 + min(i, nvalid - 1)) * H + h) * V;
+#pragma unroll
+      for (int c = 0; c < CTV; ++c) acc[c][r] = rp[c * 16 + acc_col()];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
+    for (int kb = 0; kb < K; kb += KH)
+      stage(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), std::integral_constant<int, KH / KS>{},
+            a.hT + cix * V * K + kb, K, std::integral_constant<int, KH>{}, LD);
+    stage(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), std::integral_constant<int, C / KS>{},
+          a.vnT + cix * V * C, C, std::integral_constant<int, C>{}, LDC);
+  }
+  if (a.l0_only) {   // level 0's read only: no mix, no upper levels, no o
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r);
+      if (i < nvalid) {
+        float* rp = a.read0 + (((size_t)b * T + t0 + i) * H + h) * V;
+#pragma unroll
+        for (int c = 0; c < CTV; ++c) rp[c * 16 + acc_col()] = acc[c][r];
+      }
+    }
+    return;
+  }
   fold(0, 1.f);
   f4 read0[CTV];
 #pragma unroll
@@ -111,7 +134,7 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
         op[(size_t)(t0 + i) * H * V + c * 16 + acc_col()] = from_f<E>(out[c][r]);
     }
   }
-  if (a.read0) {
+  if (a.read0 && !a.read0_in) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = wv * 16 + acc_row(r);

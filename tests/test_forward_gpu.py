@@ -229,3 +229,63 @@ def test_l1_config0_and_large_decay():
         assert torch.isfinite(o).all() and torch.isfinite(s).all()
         torch.testing.assert_close(o.double().cpu(), o_ref, **TOL[torch.float32])
         torch.testing.assert_close(s.double().cpu(), s_ref, **TOL[torch.float32])
+
+
+# ------------------------------------------------------------- fused promotion
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("K,L,N,firing,promotion,T", [
+    (64, 3, 16, (1, 2, 4), "learned", 320), (128, 3, 64, (1, 4, 16), "learned", 1100),
+    (64, 2, 32, (1, 1), "learned", 200), (64, 3, 64, (1, 2, 3), "merge", 450),
+    (128, 2, 32, (1, 3), "learned", 512)])
+def test_fused_promotion_matches_two_launch_path(dtype, K, L, N, firing, promotion, T):
+    """ngdn_promote_chain_fwd (the level's firings in one launch, on chip)
+    against ngdn_probe_fwd + ngdn_upper_scan_fwd on the same inputs, with an
+    initial state: outputs and final state within the op's bar (the two
+    paths round differently: the fused one scales the state by e^g first)."""
+    from nested_recurrent_memory_amd import chunk as chunk_mod
+    print(f"fused promotion K={K} L={L} N={N} f={firing} {promotion} T={T} {dtype}", flush=True)
+    inp = make_inputs(B=2, T=T, H=2, K=K, V=K, L=L, N=N, intervals=firing, dtype=dtype,
+                      g_scale=0.5)
+    gen = torch.Generator().manual_seed(3)
+    init = (torch.randn(2, 2, L, K, K, generator=gen) * 0.2).cuda()
+    g = _gpu(inp)
+    outs = {}
+    try:
+        for fused in (True, False):
+            chunk_mod.FUSED_PROMOTION = fused
+            with torch.no_grad():
+                outs[fused] = chunk_nested_gdn2(**g, L=L, initial_state=init,
+                                                output_final_state=True, promotion=promotion)
+    finally:
+        chunk_mod.FUSED_PROMOTION = True
+    torch.cuda.synchronize()
+    tol = TOL[dtype]
+    torch.testing.assert_close(outs[True][0].float(), outs[False][0].float(), **tol)
+    torch.testing.assert_close(outs[True][1], outs[False][1], **tol)
+    o_ref, s_ref = _oracle(inp, L, promotion, init=init.double().cpu())
+    torch.testing.assert_close(outs[True][0].double().cpu(), o_ref, **tol)
+    torch.testing.assert_close(outs[True][1].double().cpu(), s_ref, **tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_two_pass_output_equals_one_pass(dtype):
+    """With the fused promotion ladder the output runs in two passes
+    (ngdn_output_l0_fwd beside the ladder, then ngdn_output_upper_fwd); with
+    two stream groups it runs in one (ngdn_output_fwd). Same arithmetic:
+    equal bit for bit."""
+    from nested_recurrent_memory_amd import chunk as chunk_mod
+    inp = make_inputs(B=2, T=700, H=2, K=128, V=128, L=3, N=64, intervals=(1, 2, 4),
+                      dtype=dtype, g_scale=0.5)
+    g = _gpu(inp)
+    outs = []
+    try:
+        for groups in (1, 2):
+            chunk_mod.STREAM_GROUPS = groups
+            with torch.no_grad():
+                outs.append(chunk_nested_gdn2(**g, L=3, output_final_state=True))
+    finally:
+        chunk_mod.STREAM_GROUPS = 1
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
