@@ -244,7 +244,8 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
  * [L-1,H,V,K], wp [L-1,H,V,V]. states [B,ng,H,K,V] and statesT [B,ng,H,V,K]
  * are this level's group states; dSp, dvn from ngdn_upper_scan_bwd.
  * Workspace (fp32): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K], ws_dxw,
- * ws_dvals [B,H,NF,N,V]. dbank fp32 [L-1,H,n_max,K] accumulates. The gradient
+ * ws_dvals [B,H,NF,N,V], and ws_dbank [B,H,NF,N,K] (learned only): each
+ * firing's bank-gradient partial, summed by ngdn_param_grads. The gradient
  * of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is added to
  * d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
@@ -259,18 +260,27 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* statesT, int32_t ng, const float* dSp,
                        const float* dvn, float* ws_vals, float* ws_du,
                        float* ws_dxb, float* ws_dxg, float* ws_dxw,
-                       float* ws_dvals, float* dbank, float* inj,
+                       float* ws_dvals, float* ws_dbank, float* inj,
                        float* d_below, float* d_final, void* stream);
+
+/* Slices of firings per head in the parameter-gradient sums (the first
+ * dimension of ws_parts' slices). */
+#define NGDN_PARAM_SPLIT 16
 
 /* Per-head parameter gradients of level `level` summed over all its firings
  * (the leaf gradients of the probe replay, ops/chunk.py:502-517), from the
  * workspace of ngdn_probe_bwd; accumulated into fp32 dkp [L-1,H,K,V] (learned
- * only), dbp [L-1,H,V,K], dwp [L-1,H,V,V], dgp [L-1,H,V,K]. */
+ * only), dbp [L-1,H,V,K], dwp [L-1,H,V,V], dgp [L-1,H,V,K], and dbank
+ * [L-1,H,n_max,K] (learned only, from ws_dbank). Deterministic: every sum
+ * runs in a fixed order (partials per slice of firings in ws_parts, fp32
+ * [4][H][NGDN_PARAM_SPLIT][K][V], no initial contents needed, then added
+ * slice by slice), so repeated calls on the same inputs give the same bits. */
 int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
                          int32_t n_pairs, int32_t nf, const float* ws_vals,
                          const float* ws_du, const float* ws_dxb,
-                         const float* ws_dxg, const float* ws_dxw, float* dkp,
-                         float* dbp, float* dwp, float* dgp, void* stream);
+                         const float* ws_dxg, const float* ws_dxw,
+                         const float* ws_dbank, int32_t n_max, float* dbank, float* dkp,
+                         float* dbp, float* dwp, float* dgp, float* ws_parts, void* stream);
 
 /* One decoding token: naive_step_nested_gdn2 (nested_gdn2/ops/naive.py:42-134;
  * the layer's decode and ragged-tail path, layers/nested_gdn2.py:218-224).

@@ -29,6 +29,7 @@ P = ctypes.c_void_p
 I32 = ctypes.c_int32
 I64 = ctypes.c_int64
 WPARTS = 1024         # NGDN_WPARTS: rows of partial weight-gradient sums in the ws arguments
+PARAM_SPLIT = 16      # NGDN_PARAM_SPLIT: slices of firings per head in ngdn_param_grads
 PD = ctypes.POINTER(Dims)
 
 # name -> argtypes (all return an int32 status unless listed in _RESTYPES)
@@ -54,7 +55,7 @@ SIGNATURES = {
     "ngdn_l0_bwd_intra": [PD] + [P] * 6 + [P] * 3 + [P] * 6 + [P] * 6 + [P],
     "ngdn_probe_bwd": [PD, I32, I32, I32, I32, I32, P, P, I32, P, P, I32, P, P, P, P,
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
-    "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P, P],
+    "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, I32, P, P, P, P, P, P, P],
     "ngdn_step": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4 + [P, P, P],
     "ngdn_step_noalloc": [PD] + [P] * 7 + [P, P, P, I64, I32, P, I32, P, P, I32] + [P] * 4
                          + [P, P],

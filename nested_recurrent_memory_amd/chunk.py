@@ -122,12 +122,12 @@ def _aux_streams(dev):
 def _run_groups(B, dev, launch):
     """Calls launch(b0, nb, stream) for each group of batch rows: on the
     current stream when there is one group, else on side streams forked from
-    and joined back into the current stream."""
+    and joined back into the current stream. Returns the number of groups."""
     n = max(1, min(STREAM_GROUPS, B))
     main = torch.cuda.current_stream(dev)
     if n == 1:
         launch(0, B, main)
-        return
+        return 1
     size = -(-B // n)
     spans = [(b0, min(size, B - b0)) for b0 in range(0, B, size)]
     side = _side_streams(dev, len(spans))
@@ -138,6 +138,7 @@ def _run_groups(B, dev, launch):
             launch(b0, nb, st)
     for st in side[:len(spans)]:
         main.wait_stream(st)
+    return len(spans)
 
 
 def _rows(b0, nb):
@@ -201,6 +202,14 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     chains = any(levels[lvl]["chain"] for lvl in range(1, L))
     read0 = f32(B, T, H, V) if (train or chains) else None
     P = _lib.ptr
+
+    def param_grads(d, lvl, sp, st):
+        lv, wk = levels[lvl], work[lvl]
+        ws = wk["ws"]
+        _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), lv["N"], lv["nf"],
+                  *(P(x) for x in ws[:5]), P(wk["dbank"]), par["nmax"], P(dqb), P(dkp),
+                  P(dbp), P(dwp), P(dgp), P(parts), sp, tag=f"ngdn_param_grads.{lvl}",
+                  stream=st)
 
     def launch(b0, nb, st):
         R = _rows(b0, nb)
@@ -332,12 +341,24 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         work[lvl] = dict(dSp=f32(B, H, nfa, K, V), dvn=f32(B, H, nfa, N, V),
                          ws=[f32(B, H, nfa, N, K) for _ in range(4)]
                          + [f32(B, H, nfa, N, V) for _ in range(2)],
+                         dbank=None if merge else f32(B, H, nfa, N, K),
                          inj=f32(B, H, nfa, K, V) if lvl == 1 else None)
+    # per-slice partials of the parameter-gradient sums, shared by the levels
+    # (their sums run one after another on one stream)
+    parts = f32(4, H, _lib.PARAM_SPLIT, K, V) if L > 1 else None
     dSp0, dVn0, dVnT0 = f32(B, H, NT, K, V), f32(B, H, NT, 64, V), f32(B, H, NT, V, 64)
     dQg, dKt, dWT = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K), f32(B, H, NT, K, 64)
     dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
     dg = f32(B, T, H, K)
+
+    def param_grads(d, lvl, sp, st):
+        lv, wk = levels[lvl], work[lvl]
+        ws = wk["ws"]
+        _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), lv["N"], lv["nf"],
+                  *(P(x) for x in ws[:5]), P(wk["dbank"]), par["nmax"], P(dqb), P(dkp),
+                  P(dbp), P(dwp), P(dgp), P(parts), sp, tag=f"ngdn_param_grads.{lvl}",
+                  stream=st)
 
     def launch(b0, nb, st):
         R = _rows(b0, nb)
@@ -349,7 +370,10 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         # beside the top level's read and reverse scan, joined before the top
         # level's probe backward adds into the level below's d_states; (b) each
         # level's parameter-gradient sums (reading only that level's
-        # workspaces) beside the rest of the chain, joined at the end.
+        # workspaces) beside the rest of the chain, joined at the end. With
+        # several groups of rows the sums run once over all rows after the
+        # groups join, so every row group's partials are in place and the
+        # result does not depend on the grouping.
         aux = _aux_streams(dev) if (L > 1 and nb == B) else None
         if aux is not None:
             fork = st.record_event()
@@ -394,14 +418,13 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                       P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
                       P(par["kpT"]), P(par["bankT"]), P(par["bp"]), P(par["wp"]),
                       P(par["gp"]), P(R(states[lvl])), P(R(sv["statesT"][lvl])), ng,
-                      P(R(wk["dSp"])), P(R(wk["dvn"])), *(P(R(x)) for x in ws), P(dqb),
-                      P(R(wk["inj"])), P(R(d_below)), P(R(d_final)), sp,
+                      P(R(wk["dSp"])), P(R(wk["dvn"])), *(P(R(x)) for x in ws),
+                      P(R(wk["dbank"])), P(R(wk["inj"])), P(R(d_below)), P(R(d_final)), sp,
                       tag=f"ngdn_probe_bwd.{lvl}")
-            if aux is not None:
-                aux[1].wait_stream(st)
-            _lib.call("ngdn_param_grads", ctypes.byref(d), lvl, int(merge), N, nf,
-                      *(P(R(x)) for x in ws[:5]), P(dkp), P(dbp), P(dwp), P(dgp), sb,
-                      tag=f"ngdn_param_grads.{lvl}", stream=tb)
+            if nb == B:
+                if aux is not None:
+                    aux[1].wait_stream(st)
+                param_grads(d, lvl, sb, tb)
         if not joined:
             st.wait_stream(aux[0])
         # level 0
@@ -417,7 +440,13 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         if aux is not None:
             st.wait_stream(aux[1])
 
-    _run_groups(B, dev, launch)
+    groups = _run_groups(B, dev, launch)
+    if groups > 1:
+        st = torch.cuda.current_stream(dev)
+        d = _lib.dims(B, T, H, L, K, V, code, scale)
+        for lvl in range(L - 1, 0, -1):
+            if levels[lvl]["nf"] > 0:
+                param_grads(d, lvl, _lib.ptr_of_stream(st), st)
     return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
 
 

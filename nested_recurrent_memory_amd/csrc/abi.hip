@@ -407,7 +407,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* statesT, int32_t ng, const float* dSp,
                        const float* dvn, float* ws_vals, float* ws_du,
                        float* ws_dxb, float* ws_dxg, float* ws_dxw,
-                       float* ws_dvals, float* dbank, float* inj,
+                       float* ws_dvals, float* ws_dbank, float* inj,
                        float* d_below, float* d_final, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_bwd")) return r;
@@ -417,7 +417,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   if (!pow2_ge16(N))
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: pairs per firing must be a power of two >= 16, got %d", N);
   if (promotion == 0 && (n_queries > n_max || n_max % 8 != 0 || !query_banks || !key_projections ||
-                         !kpT || !bankT || !dbank))
+                         !kpT || !bankT || !ws_dbank))
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: bank of %d rows (a multiple of 8 >= n_queries=%d) "
                 "and its transposes are required", n_max, n_queries);
   if (f_below <= 0 || f_here <= 0) return fail(NGDN_EINVAL, "ngdn_probe_bwd: bad intervals");
@@ -451,7 +451,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.dSp = dSp; a.dvn = dvn;
   a.wsV = ws_vals; a.wsdu = ws_du; a.wsdxb = ws_dxb; a.wsdxg = ws_dxg; a.wsdxw = ws_dxw;
   a.wsdV = ws_dvals;
-  a.dbank = dbank ? dbank + (size_t)(level - 1) * d->H * n_max * d->K : nullptr;
+  a.dbank = ws_dbank;   // [B,H,NF,N,K], summed by ngdn_param_grads
   a.inj = inj; a.d_below = d_below;
   a.d_below_fin = d_final ? d_final + (long long)(level - 1) * skv : nullptr;
   if (a.f.NF == 0) return NGDN_OK;
@@ -461,24 +461,29 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
 int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
                          int32_t n_pairs, int32_t nf, const float* ws_vals,
                          const float* ws_du, const float* ws_dxb,
-                         const float* ws_dxg, const float* ws_dxw, float* dkp,
-                         float* dbp, float* dwp, float* dgp, void* stream) {
+                         const float* ws_dxg, const float* ws_dxw,
+                         const float* ws_dbank, int32_t n_max, float* dbank, float* dkp,
+                         float* dbp, float* dwp, float* dgp, float* ws_parts, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_param_grads")) return r;
   if (level < 1 || level >= d->L || d->K != d->V)
     return fail(NGDN_EINVAL, "ngdn_param_grads: bad level %d or K != V", level);
-  if (!ws_vals || !ws_dxb || !ws_dxg || !ws_dxw || !dbp || !dwp || !dgp ||
-      (promotion == 0 && (!ws_du || !dkp)))
+  if (!ws_vals || !ws_dxb || !ws_dxg || !ws_dxw || !dbp || !dwp || !dgp || !ws_parts ||
+      (promotion == 0 && (!ws_du || !dkp || !ws_dbank || !dbank)))
     return fail(NGDN_EINVAL, "ngdn_param_grads: NULL tensor");
+  if (promotion == 0 && (n_max < n_pairs || n_max % 8 != 0))
+    return fail(NGDN_EINVAL, "ngdn_param_grads: bank rows %d (a multiple of 8 >= %d)", n_max,
+                n_pairs);
   if (nf <= 0) return NGDN_OK;
-  const size_t off = (size_t)(level - 1) * d->H * d->K * d->V;
-  // firings split over up to 16 workgroups per head, at least 4 firings
-  // each: every workgroup adds its X x Y partial with atomics, so more
-  // workgroups cost more atomics (measured best at c2 for both levels)
-  const int split = std::max(1, std::min(16, (d->B * nf + 3) / 4));
+  const int H = d->H, K = d->K, V = d->V;
+  const size_t off = (size_t)(level - 1) * H * K * V;
+  // firings split over up to NGDN_PARAM_SPLIT workgroups per head and
+  // product, at least 4 firings each; each writes its partial
+  const int split = std::max(1, std::min(NGDN_PARAM_SPLIT, (d->B * nf + 3) / 4));
   hipStream_t st = (hipStream_t)stream;
   ngdn::AtBArgs a{};
-  a.B = d->B; a.H = d->H; a.NF = nf; a.N = n_pairs; a.X = d->K; a.Y = d->V; a.split = split;
+  a.parts = ws_parts;
+  a.B = d->B; a.H = H; a.NF = nf; a.N = n_pairs; a.X = K; a.Y = V; a.split = split;
   // the (up to) four sums in one launch
   auto add = [&](const float* A, const float* Bm, float* C) {
     a.A[a.nprod] = A; a.Bm[a.nprod] = Bm; a.C[a.nprod] = C; ++a.nprod;
@@ -487,7 +492,31 @@ int32_t ngdn_param_grads(const ngdn_dims* d, int32_t level, int32_t promotion,
   add(ws_vals, ws_dxb, dbp + off);                       // dBp = Vals^T dxb
   add(ws_vals, ws_dxw, dwp + off);                       // dWp = Vals^T dxw
   add(ws_vals, ws_dxg, dgp + off);                       // dGp = Vals^T dxg
-  return launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads");
+  if (int32_t r = launched(ngdn::atb_accumulate(a, d->dtype, st), "ngdn_param_grads")) return r;
+  // the slices added in order, and the bank gradient's per-firing partials
+  // in (batch row, firing) order
+  ngdn::OrderedSumArgs o{};
+  o.ng = H;
+  const long long kv = (long long)K * V;
+  for (int p = 0; p < a.nprod; ++p) {
+    o.parts[o.nsum] = ws_parts + (long long)p * H * split * kv;   // as atb writes them
+    o.out[o.nsum] = a.C[p];
+    o.pg[o.nsum] = (long long)split * kv; o.og[o.nsum] = kv;
+    o.s1[o.nsum] = kv; o.n1[o.nsum] = split; o.s2[o.nsum] = 0; o.n2[o.nsum] = 1;
+    o.n[o.nsum] = kv;
+    ++o.nsum;
+  }
+  if (promotion == 0) {
+    const long long nk = (long long)n_pairs * K;
+    o.parts[o.nsum] = ws_dbank;
+    o.out[o.nsum] = dbank + (size_t)(level - 1) * H * n_max * K;
+    o.pg[o.nsum] = (long long)nf * nk; o.og[o.nsum] = (long long)n_max * K;
+    o.s1[o.nsum] = (long long)H * nf * nk; o.n1[o.nsum] = d->B;
+    o.s2[o.nsum] = nk; o.n2[o.nsum] = nf;
+    o.n[o.nsum] = nk;
+    ++o.nsum;
+  }
+  return launched(ngdn::ordered_sum(o, st), "ngdn_param_grads (sums)");
 }
 
 }  // extern "C"

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDI : 0;
   constexpr size_t SZ_P = SZ_DA + SZ_G + SZ_IN;
   constexpr size_t SZ_R = SZ_X > SZ_P ? SZ_X : SZ_P;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (2 * K + 256)];
+  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (5 * K + 256)];
   float* s_dXw = reinterpret_cast<float*>(smem);
   float* s_dXu = s_dXw + C * LXK;
   float* s_dA = reinterpret_cast<float*>(smem);
@@ -194,8 +194,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   E* s_b = s_k + C * LDI;
   E* s_q = s_b + C * LDI;
   float* s_gl = reinterpret_cast<float*>(smem + SZ_R);   // gc of the last row, per column
-  float* s_col = s_gl + K;
-  float* s_part = s_col + K;                              // [256 / NH][NH] block sums of phase 6
+  float* s_col = s_gl + K;                                // [4 waves][K] column sums of phase 5
+  float* s_part = s_col + 4 * K;                          // [256 / NH][NH] block sums of phase 6
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, T, H, a.L, a.scale);
   const int t0 = in.t0, nvalid = in.nvalid;
-  for (int e = tid; e < K; e += 256) s_col[e] = 0.f;
+  for (int e = tid; e < 4 * K; e += 256) s_col[e] = 0.f;
 
   // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns a quarter of the
   // columns of each and every row, so each wave splits the small T^T (all
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       }
       colsum += __shfl_xor(colsum, 16, WAVE);
       colsum += __shfl_xor(colsum, 32, WAVE);
-      if (lane < 16) atomicAdd(&s_col[kc], colsum);
+      if (lane < 16) s_col[wv * K + kc] = colsum;   // one slot per wave, added in wave order
     }
     lds_barrier();
     if (p + 1 < NPASS) pass_load(p + 1, pin);   // ahead of this pass's stores
@@ -570,7 +570,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       for (int i = 0; i < RB; ++i) part += s_g[(blk * RB + i) * GH + col];
       s_part[blk * NH + col] = part;
       lds_barrier();
-      float run = s_col[kc] + dgam[kc] * fexp(s_gl[kc]);
+      float run = ((s_col[kc] + s_col[K + kc]) + s_col[2 * K + kc]) + s_col[3 * K + kc];
+      run += dgam[kc] * fexp(s_gl[kc]);
       for (int b2 = NB - 1; b2 > blk; --b2) run += s_part[b2 * NH + col];
 #pragma unroll
       for (int i = RB - 1; i >= 0; --i) {

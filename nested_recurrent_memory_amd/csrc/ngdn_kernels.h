@@ -304,7 +304,8 @@ hipError_t cross_entropy(const XentArgs& a, int dtype, hipStream_t st);
 // [B,H,NF,K,V], gradient of the state after firing i) and dvn (fp32
 // [B,H,NF,N,V]). Workspace (fp32, [B,H,NF,N,*]): Vals, du, dxb,
 // dxg [N,K-or-V], dxw, dVals [N,V]; the parameter-gradient reduction reads
-// them. dbank (fp32 [H,Nmax,K]) is accumulated atomically.
+// them. dbank: this firing's bank-gradient partial (fp32 [B,H,NF,N,K],
+// written), summed per head in a fixed order by the parameter-gradient pass.
 // The gradient of the gathered lower state goes to: inj (level 1; fp32
 // [B,H,NF,K,V], written) or d_below (level >= 2; fp32 [B,NGb,H,K,V], added)
 // / d_below_fin (fp32 [K][V] at strides, added) when the firing reads the
@@ -322,18 +323,31 @@ struct ProbeBwdArgs {
 };
 hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st);
 
-// C_h[X][Y] += sum over rows m = (b, i, n) of A[b,h,i,n,X] B[b,h,i,n,Y]
-// (fp32, accumulated atomically), for the per-head parameter gradients of a
-// level: one workgroup per (head, slice of items).
-// Up to four independent sums C_p[h] += sum over rows of A_p^T B_p, one
-// launch for all of them (grid nprod x H x split).
+// Partial sums over rows m = (b, i, n) of A[b,h,i,n,X] B[b,h,i,n,Y] for the
+// per-head parameter gradients of a level: one workgroup per (product, head,
+// slice of items) writes its X x Y partial to parts [nprod][H][split][X][Y]
+// (fp32; slices without items write zeros). ordered_sum then adds the slices
+// into C_p[h] in a fixed order. Up to four sums in one launch.
 struct AtBArgs {
   const float* A[4]; const float* Bm[4]; float* C[4];
+  float* parts;
   int nprod;
   int B, H, NF, N, X, Y;
   int split;
 };
 hipError_t atb_accumulate(const AtBArgs& a, int dtype, hipStream_t st);
+
+// Fixed-order sums of partials (deterministic reductions): for w < nsum,
+// g < ng, x < n[w]: out[w][g og + x] += sum_{j1 < n1, j2 < n2} (in that order)
+// parts[w][g pg + j1 s1 + j2 s2 + x].
+constexpr int OSUM_MAX = 5;
+struct OrderedSumArgs {
+  const float* parts[OSUM_MAX]; float* out[OSUM_MAX];
+  long long pg[OSUM_MAX], og[OSUM_MAX], s1[OSUM_MAX], s2[OSUM_MAX], n[OSUM_MAX];
+  int n1[OSUM_MAX], n2[OSUM_MAX];
+  int nsum, ng;
+};
+hipError_t ordered_sum(const OrderedSumArgs& a, hipStream_t st);
 
 }  // namespace ngdn
 

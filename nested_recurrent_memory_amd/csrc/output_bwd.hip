@@ -60,7 +60,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   __shared__ __attribute__((aligned(16))) typename ST::T s_dt[ST::NPLANE * V * LDDT];
   __shared__ __attribute__((aligned(16))) E s_do[STAGE_DO ? C * LDD : 4];
   __shared__ __attribute__((aligned(16))) E s_qt[K * LDQT];
-  __shared__ float s_mix[C], s_dm[C];
+  __shared__ float s_mix[C], s_dm[2 * C];   // dmix partials of the two halves of K
   const ST sS{s_s, K * LDS_}, sDT{s_dt, V * LDDT};
 
   const int NG = a.NG, H = a.H, T = a.T, L = a.L, l = a.level;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
       }
       if (tid < C) {
         s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
-        s_dm[tid] = 0.f;
+        s_dm[tid] = s_dm[C + tid] = 0.f;
       }
     }
     lds_barrier();
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         sm += __shfl_xor(sm, 2, WAVE);
         sm += __shfl_xor(sm, 4, WAVE);
         sm += __shfl_xor(sm, 8, WAVE);
-        if ((lane & 15) == 0) atomicAdd(&s_dm[i], sm);
+        if ((lane & 15) == 0) s_dm[half * C + i] = sm;   // each slot has one writer
       }
     }
     // ---- dS += q^T (mix do): q^T rows exact, (mix do)^T rows split
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
       }
     }
     lds_barrier();
-    if (tid < nv) dmb[(size_t)(t0 + tid) * H * L] = s_dm[tid] * a.scale;
+    if (tid < nv) dmb[(size_t)(t0 + tid) * H * L] = (s_dm[tid] + s_dm[C + tid]) * a.scale;
   }
   float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;
 #pragma unroll

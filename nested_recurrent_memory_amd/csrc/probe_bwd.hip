@@ -63,7 +63,12 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   constexpr size_t SZ_C = (MERGE ? 0 : SZ_T) + SZ_DVT;
   constexpr size_t SZ_AB = SZ_A > SZ_B ? SZ_A : SZ_B;
   __shared__ __attribute__((aligned(16))) char smem[SZ_AB > SZ_C ? SZ_AB : SZ_C];
-  __shared__ float s_nrm[N], s_rd[N], s_gs[K], s_dg[K], s_gam[K];
+  // Sums across waves go through one slot per contributing wave (column tile
+  // or wave group), added in a fixed order: the results do not depend on the
+  // order in which the waves finish.
+  constexpr int NPW = NW / CTK;                     // waves per column tile
+  __shared__ float s_nrm[CTK * N], s_rd[CTK * N], s_gs[NPW * K], s_dg[NPW * K];
+  __shared__ float s_gam[K], s_nsum[N], s_rdt[N], s_dgt[K];
   float* s_V = reinterpret_cast<float*>(smem);
   float* s_kb = reinterpret_cast<float*>(smem + SZ_F);
   float* s_vn = s_kb;
@@ -103,8 +108,8 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   float* wsdxw = ab.wsdxw + fo * N * V;
   float* wsdV = ab.wsdV + fo * N * V;
 
-  for (int e = tid; e < N; e += blockDim.x) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
-  for (int e = tid; e < K; e += blockDim.x) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
+  for (int e = tid; e < CTK * N; e += blockDim.x) { s_nrm[e] = 0.f; s_rd[e] = 0.f; }
+  for (int e = tid; e < NPW * K; e += blockDim.x) { s_gs[e] = 0.f; s_dg[e] = 0.f; }
 
   // row tile of this wave's t-th tile (its column tile is ctw)
   auto tile = [&](int t, int& rt) -> bool {
@@ -191,7 +196,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       for (int r = 0; r < 4; ++r) sg += softplusf_(xg[t][r] - 4.f);
       sg += __shfl_xor(sg, 16, WAVE);
       sg += __shfl_xor(sg, 32, WAVE);
-      if (lane < 16) atomicAdd(&s_gs[ctw * 16 + lane], sg);
+      if (lane < 16) s_gs[(wv / CTK) * K + ctw * 16 + lane] += sg;
       if (!MERGE) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
           q += __shfl_xor(q, 2, WAVE);
           q += __shfl_xor(q, 4, WAVE);
           q += __shfl_xor(q, 8, WAVE);
-          if (rl == 0) atomicAdd(&s_nrm[rt * 16 + acc_row(r)], q);
+          if (rl == 0) s_nrm[ctw * N + rt * 16 + acc_row(r)] += q;
         }
       }
     }
@@ -208,11 +213,25 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   // dvn staged for phases 4-5 (loads issued before the barrier)
   if constexpr (DVN_LDS) stage_f32<512, N, V>(s_dvn, LD, dvn, V);
   lds_barrier();
+  // the decay and the squared key norms from their per-wave slots, in order
+  if (tid < K) {
+    float x = 0.f;
+#pragma unroll
+    for (int p = 0; p < NPW; ++p) x += s_gs[p * K + tid];
+    s_gam[tid] = expf(-x / (float)N);
+  } else if (!MERGE && tid < K + N) {
+    const int n = tid - K;
+    float x = 0.f;
+#pragma unroll
+    for (int c = 0; c < CTK; ++c) x += s_nrm[c * N + n];
+    s_nsum[n] = x;
+  }
+  lds_barrier();
 
   auto keyval = [&](int t, int rt, int r) -> float {
     const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
     if (MERGE) return n == k ? 1.f : 0.f;
-    return u[t][r] * __builtin_amdgcn_rcpf(fmaxf(sqrtf(s_nrm[n]), 1e-12f));
+    return u[t][r] * __builtin_amdgcn_rcpf(fmaxf(sqrtf(s_nsum[n]), 1e-12f));
   };
 
   // ---- 3. kb = keys * b into LDS; gam = e^g
@@ -225,7 +244,6 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       s_kb[(rt * 16 + acc_row(r)) * LD + ctw * 16 + acc_col()] =
           keyval(t, rt, r) * sigmoidf_(xb[t][r] - 4.f);
   }
-  for (int e = tid; e < K; e += blockDim.x) s_gam[e] = expf(-s_gs[e] / (float)N);
   lds_barrier();
 
   // ---- 4. vn = Vals w - kb s with s = e^g S_j (s^T rows scaled per k);
@@ -321,17 +339,31 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
           rd += __shfl_xor(rd, 2, WAVE);
           rd += __shfl_xor(rd, 4, WAVE);
           rd += __shfl_xor(rd, 8, WAVE);
-          if (rl == 0) atomicAdd(&s_rd[n], rd);
+          if (rl == 0) s_rd[ctw * N + n] += rd;
         }
       }
       cs += __shfl_xor(cs, 16, WAVE);
       cs += __shfl_xor(cs, 32, WAVE);
-      if (lane < 16) atomicAdd(&s_dg[ctw * 16 + lane], -cs);
+      if (lane < 16) s_dg[(wv / CTK) * K + ctw * 16 + lane] += -cs;
     }
     // + sum_v dS'[k][v] s[k][v] (one wave per column tile adds it)
     dgp += __shfl_xor(dgp, 16, WAVE);
     dgp += __shfl_xor(dgp, 32, WAVE);
-    if (wv < CTK && lane < 16) atomicAdd(&s_dg[kc], gk * dgp);
+    if (wv < CTK && lane < 16) s_dg[kc] += gk * dgp;   // the first wave group's slot
+  }
+  lds_barrier();
+  // the key-norm and decay gradients from their per-wave slots, in order
+  if (tid < K) {
+    float x = 0.f;
+#pragma unroll
+    for (int p = 0; p < NPW; ++p) x += s_dg[p * K + tid];
+    s_dgt[tid] = x;
+  } else if (!MERGE && tid < K + N) {
+    const int n = tid - K;
+    float x = 0.f;
+#pragma unroll
+    for (int c = 0; c < CTK; ++c) x += s_rd[c * N + n];
+    s_rdt[n] = x;
   }
   lds_barrier();
 
@@ -347,13 +379,13 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     for (int r = 0; r < 4; ++r) {
       const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
       if (!MERGE) {
-        const float nr = sqrtf(s_nrm[n]);
+        const float nr = sqrtf(s_nsum[n]);
         const float rn = __builtin_amdgcn_rcpf(fmaxf(nr, 1e-12f));
         const float key = u[t][r] * rn;
         // F.normalize: below the clamp the denominator is the constant eps
-        dut[t][r] = nr >= 1e-12f ? (dkt[t][r] - key * s_rd[n]) * rn : dkt[t][r] * 1e12f;
+        dut[t][r] = nr >= 1e-12f ? (dkt[t][r] - key * s_rdt[n]) * rn : dkt[t][r] * 1e12f;
       }
-      dxgt[t][r] = -(s_dg[k] * (1.f / (float)N)) * sigmoidf_(xg[t][r] - 4.f);
+      dxgt[t][r] = -(s_dgt[k] * (1.f / (float)N)) * sigmoidf_(xg[t][r] - 4.f);
     }
   }
   FR qk[NKS], qb[NKS], qw[NKS], qg[NKS];
@@ -515,14 +547,14 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
         dbt[t] = Mma<E>::mma(dbt[t], sDV.get((rt * 16 + rl) * LDT + s * KS + ko), fSk[s]);
     }
     scatter_all(dsb);
-    float* dbank = ab.dbank + (size_t)h * a.Nmax * K;
+    float* dbank = ab.dbank + fo * N * K;   // this firing's partial, summed by ngdn_param_grads
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       int rt;
       if (!tile(t, rt)) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        atomicAdd(&dbank[(rt * 16 + acc_row(r)) * K + ctw * 16 + acc_col()], dbt[t][r]);
+        dbank[(rt * 16 + acc_row(r)) * K + ctw * 16 + acc_col()] = dbt[t][r];
     }
   }
 }
@@ -555,8 +587,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const int items = a.B * NF;
   const int per = (items + a.split - 1) / a.split;
-  const int it0 = part * per, it1 = min(items, it0 + per);
-  if (it0 >= it1) return;
+  const int it0 = part * per, it1 = min(items, it0 + per);   // may be empty: zeros are written
   f4 acc[XTW][YT];
 #pragma unroll
   for (int x = 0; x < XTW; ++x)
@@ -567,7 +598,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
   constexpr int GA = X * R / 4 / 256, GB = Y * R / 4 / 256;   // 4-row groups per thread
   f4 ra[GA], rb[GB];
   const int slabs_per_item = (N + R - 1) / R;
-  const int nslab = (it1 - it0) * slabs_per_item;
+  const int nslab = it1 > it0 ? (it1 - it0) * slabs_per_item : 0;
   auto fetch = [&](int sl) {
     const int it = it0 + sl / slabs_per_item, n0 = (sl % slabs_per_item) * R;
     const int b = it / NF, i = it % NF, nr = min(R, N - n0);
@@ -585,7 +616,7 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
       for (int j = 0; j < 4; ++j) rb[u][j] = r4 + j < nr ? Bp[(row0 + r4 + j) * Y + c] : 0.f;
     }
   };
-  fetch(0);
+  if (nslab > 0) fetch(0);
   for (int sl = 0; sl < nslab; ++sl) {
 #pragma unroll
     for (int u = 0; u < GA; ++u) {
@@ -614,14 +645,38 @@ __global__ __launch_bounds__(256) void atb_kernel(AtBArgs a) {
     }
     lds_barrier();
   }
-  float* C = a.C[prod] + (size_t)h * X * Y;
+  // this workgroup's partial sum, added to C in a fixed order by ordered_sum
+  float* P = a.parts + (((size_t)prod * H + h) * a.split + part) * X * Y;
 #pragma unroll
   for (int x = 0; x < XTW; ++x)
 #pragma unroll
     for (int y = 0; y < YT; ++y)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        atomicAdd(&C[((wv * XTW + x) * 16 + acc_row(r)) * Y + y * 16 + acc_col()], acc[x][y][r]);
+        P[((wv * XTW + x) * 16 + acc_row(r)) * Y + y * 16 + acc_col()] = acc[x][y][r];
+}
+
+// out_w[g][x] += sum over j1 < n1, j2 < n2 (in that order) of
+// parts_w[g pg + j1 s1 + j2 s2 + x]: one thread per output element, so every
+// element is a fixed-order sum written once.
+__global__ __launch_bounds__(256) void ordered_sum_kernel(OrderedSumArgs a) {
+  const int w = blockIdx.x / a.ng, g = blockIdx.x % a.ng;
+  const long long x = (long long)blockIdx.y * 256 + threadIdx.x;
+  if (x >= a.n[w]) return;
+  const float* p = a.parts[w] + g * a.pg[w] + x;
+  float acc = 0.f;
+  for (int j1 = 0; j1 < a.n1[w]; ++j1)
+    for (int j2 = 0; j2 < a.n2[w]; ++j2) acc += p[j1 * a.s1[w] + j2 * a.s2[w]];
+  a.out[w][g * a.og[w] + x] += acc;
+}
+
+hipError_t ordered_sum(const OrderedSumArgs& a, hipStream_t st) {
+  long long nmax = 0;
+  for (int w = 0; w < a.nsum; ++w) nmax = a.n[w] > nmax ? a.n[w] : nmax;
+  if (a.nsum == 0 || nmax == 0 || a.ng == 0) return hipSuccess;
+  const dim3 grid((unsigned)(a.nsum * a.ng), (unsigned)((nmax + 255) / 256));
+  hipLaunchKernelGGL(ordered_sum_kernel, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 template <typename E, int K, int N, bool MERGE>

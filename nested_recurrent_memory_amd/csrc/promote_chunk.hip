@@ -191,7 +191,16 @@ __global__ __launch_bounds__(512) void promote_chain_kernel(PromoteChainArgs a) 
     auto arow_ = [&](int r) { return 4 * (lane_v >> 4) + r; };
     auto acol_ = [&]() { return lane_v & 15; };
 
-    // ---- the firing's parameter fragments (this wave's column tile)
+    // ---- Vals = Bank[:N] Sb (learned) or Sb (merge), Sb the lower snapshot
+    // after firing i
+    // the snapshot's fragments split first (their loads are the oldest in
+    // flight), then the parameter fragments of this wave's column tile are
+    // issued, arriving during the Vals product
+    SF fS[MERGE ? 1 : NKS];
+    if (!MERGE) {
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) fS[s] = Mma<E>::makes([&](int e) { return raw[s * KPL + e]; });
+    }
     FR pk[PRELOAD ? NKS : 1], pb[PRELOAD ? NKS : 1], pw[PRELOAD ? NKS : 1], pg[PRELOAD ? NKS : 1];
     if constexpr (PRELOAD) {
 #pragma unroll
@@ -202,13 +211,7 @@ __global__ __launch_bounds__(512) void promote_chain_kernel(PromoteChainArgs a) 
         pg[s] = Mma<E>::ld(gpH + s * KS);
       }
     }
-
-    // ---- Vals = Bank[:N] Sb (learned) or Sb (merge), Sb the lower snapshot
-    // after firing i
     if (!MERGE) {
-      SF fS[NKS];
-#pragma unroll
-      for (int s = 0; s < NKS; ++s) fS[s] = Mma<E>::makes([&](int e) { return raw[s * KPL + e]; });
       f4 vt[TPW];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
