@@ -265,7 +265,7 @@ def decode_bench(args):
     that fire nothing."""
     from nested_recurrent_memory_amd import prepare_step_params, step_nested_gdn2
 
-    cfg = DECODE
+    cfg = dict(DECODE, B=args.decode_batch or DECODE["B"])
     B, H, K, V, L, N = (cfg[x] for x in ("B", "H", "K", "V", "L", "N"))
     inp = gpu_inputs(dict(cfg, T=1))
     tok = {n: inp[n][:, 0].contiguous() for n in ("q", "k", "v", "g", "b", "w", "mix_weights")}
@@ -317,7 +317,7 @@ def decode_bench(args):
     nbytes = B * H * ((L + 1) * K * V * 4 + (L * K + 3 * K + 2 * V + L) * es + K * 4 + V * es)
     gbs = nbytes / (k_ms * 1e-3) / 1e9
     line = {
-        "metric": "tokens/s decoding step nested GDN op (B64,H16,d128,3 lvl)",
+        "metric": f"tokens/s decoding step nested GDN op (B{B},H{H},d{K},{L} lvl)",
         "value": round(B * args.steps / elapsed, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -333,8 +333,12 @@ def decode_bench(args):
                                f"positions 0..{args.steps - 1}, HIP graph per token",
                    "B": B, "H": H, "K": K, "V": V, "L": L,
                    "firing_intervals": list(cfg["intervals"]), "n_queries": N,
-                   "state": "fp32"},
+                   "state": "fp32", "state_bytes": B * H * L * K * V * 4},
+        # a state below the 256 MB last-level cache can be served from it
+        # between tokens; the HBM figure needs B * H * L * K * V * 4 well
+        # above that (B = 256: 805 MB)
         "roofline": {"kernel": "ngdn_step (step_kernel)", "bound": "hbm",
+                     "cache_resident": B * H * L * K * V * 4 <= 256 * 2**20,
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": nbytes, "avg_ms": round(k_ms, 4)},
@@ -443,6 +447,8 @@ def main():
                     help="train: forward+backward at --config (the headline); "
                          "decode: the decoding step; model: a training step of the "
                          "model at config 4")
+    ap.add_argument("--decode-batch", type=int, default=None,
+                    help="sequences per decoding step (default 64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-table", action="store_true",
                     help="also print per-entry-point times to stderr")

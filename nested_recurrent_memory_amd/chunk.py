@@ -450,6 +450,35 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     return dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, d_init
 
 
+def _flatten(x, tensors):
+    """x with every tensor replaced by its index in ``tensors`` (appended)."""
+    if isinstance(x, torch.Tensor):
+        tensors.append(x)
+        return _Slot(len(tensors) - 1)
+    if isinstance(x, dict):
+        return {k: _flatten(v, tensors) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_flatten(v, tensors) for v in x]
+    return x
+
+
+def _unflatten(x, tensors):
+    if isinstance(x, _Slot):
+        return tensors[x.i]
+    if isinstance(x, dict):
+        return {k: _unflatten(v, tensors) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_unflatten(v, tensors) for v in x]
+    return x
+
+
+class _Slot:
+    __slots__ = ("i",)
+
+    def __init__(self, i):
+        self.i = i
+
+
 class ChunkNestedGDN2Function(torch.autograd.Function):
     """Autograd node for the whole op (ops/chunk.py:567-719)."""
 
@@ -479,17 +508,21 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
                       for t in (q, k, v, g, b, w, mix_weights, query_banks, key_projections,
                                 b_projections, w_projections, g_projections, initial_state)]
         ctx.nmax = query_banks.shape[2] if L > 1 else 0
-        ctx.saved_fwd = saved
+        # the working tensors go through save_for_backward, so that activation
+        # checkpointing (torch.utils.checkpoint) can drop them after the
+        # forward and have them recomputed for the backward
+        tensors = []
+        ctx.skeleton = _flatten(saved, tensors)
+        ctx.save_for_backward(*tensors)
         return o, (final if output_final_state else None)
 
     @staticmethod
     def backward(ctx, do, dfinal):
         L, scale, f, nq, has_init, promotion = ctx.meta
-        sv = ctx.saved_fwd
+        sv = _unflatten(ctx.skeleton, ctx.saved_tensors)
         if sv is None:
             raise RuntimeError("chunk_nested_gdn2: no saved state for the backward")
         grads = _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion)
-        ctx.saved_fwd = None
         (dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, dinit) = grads
         dts = ctx.dtypes
         out = [dq, dk, dv, dg, db, dw, dmix]

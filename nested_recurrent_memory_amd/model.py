@@ -22,6 +22,7 @@ import torch
 import torch.nn as nn
 from transformers import AutoConfig, AutoModel, AutoModelForCausalLM, GenerationMixin
 from transformers.configuration_utils import PretrainedConfig
+from transformers.modeling_layers import GradientCheckpointingLayer
 from transformers.modeling_outputs import BaseModelOutputWithPast, CausalLMOutputWithPast
 from transformers.modeling_utils import PreTrainedModel
 
@@ -100,6 +101,10 @@ class NestedGDN2Cache(dict):
     """Per-layer decoding state keyed by layer index, plus the count of tokens
     seen (``get_seq_length``)."""
 
+    # generate() reads this of any cache it is handed: a recurrent state is
+    # updated in place, so a compiled decoding loop would gain nothing
+    is_compileable = False
+
     def __init__(self):
         super().__init__()
         self.seen_tokens = 0
@@ -117,9 +122,12 @@ class NestedGDN2Cache(dict):
         return cache
 
 
-class NestedGDN2Block(nn.Module):
+class NestedGDN2Block(GradientCheckpointingLayer):
     """Pre-norm token mixing with a residual, then pre-norm channel mixing
-    with a residual (models/modeling_nested_gdn2.py:44-68)."""
+    with a residual (models/modeling_nested_gdn2.py:44-68). A
+    GradientCheckpointingLayer: after gradient_checkpointing_enable() a
+    training forward keeps only the block's inputs and recomputes the rest in
+    the backward (caching is switched off for it, as the base class does)."""
 
     def __init__(self, config, layer_idx):
         super().__init__()
@@ -130,7 +138,7 @@ class NestedGDN2Block(nn.Module):
                             intermediate_size=config.intermediate_size,
                             hidden_act=config.hidden_act, fuse_swiglu=config.fuse_swiglu)
 
-    def forward(self, hidden_states, past_key_values=None, use_cache=False, residual=None,
+    def forward(self, hidden_states, residual=None, past_key_values=None, use_cache=False,
                 defer_residual=False):
         """Same values as norm -> attn -> add -> norm -> mlp -> add. The norms
         write the dtype their consumers compute in (bf16 under autocast: the
@@ -215,9 +223,11 @@ class NestedGDN2Model(NestedGDN2PreTrainedModel):
                 if residual is not None:
                     hidden_states, residual = hidden_states + residual, None
                 all_hidden_states += (hidden_states,)
+            # the tensors positionally, as checkpointing with use_reentrant
+            # needs them
             hidden_states, residual, past_key_values = layer(
-                hidden_states, past_key_values=past_key_values, use_cache=use_cache,
-                residual=residual, defer_residual=True)
+                hidden_states, residual, past_key_values=past_key_values, use_cache=use_cache,
+                defer_residual=True)
         if use_cache:
             past_key_values.seen_tokens += hidden_states.shape[1]
         if residual is not None:
@@ -234,6 +244,16 @@ class NestedGDN2Model(NestedGDN2PreTrainedModel):
 
 class NestedGDN2ForCausalLM(NestedGDN2PreTrainedModel, GenerationMixin):
     _tied_weights_keys = {"lm_head.weight": "model.embeddings.weight"}
+    # the recurrent state cannot be rewound (no assisted decoding)
+    _is_stateful = True
+
+    @classmethod
+    def _supports_default_dynamic_cache(cls):
+        """generate() does not build a key/value cache: the first forward
+        returns a NestedGDN2Cache and the later steps pass it back (the
+        reference's FLAUnsupportedCacheGenerationMixin, imported by
+        models/modeling_nested_gdn2.py:15)."""
+        return False
 
     def __init__(self, config):
         super().__init__(config)
