@@ -365,10 +365,10 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         sp = _lib.ptr_of_stream(st)
         d = _lib.dims(nb, T, H, L, K, V, code, scale)
         # With one group of rows, independent launches go to two side streams:
-        # (a) dmix_0 and the reads' backward of the levels below the top one
+        # (a) the reads' backward of the levels below the top one
         # (each writes its own columns of dmix and dq and its own d_states)
         # beside the top level's read and reverse scan, joined before the top
-        # level's probe backward adds into the level below's d_states; (b) each
+        # level's probe backward adds into the level below's d_states; (b) dmix_0, then each
         # level's parameter-gradient sums (reading only that level's
         # workspaces) beside the rest of the chain, joined at the end. With
         # several groups of rows the sums run once over all rows after the
@@ -381,10 +381,11 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                 a.wait_event(fork)
         ta, tb = (aux[0], aux[1]) if aux else (st, st)
         sa, sb = _lib.ptr_of_stream(ta), _lib.ptr_of_stream(tb)
-        # reads: dmix for every level (level 0 from the stored read), dq and the
-        # group-state gradients for levels >= 1
+        # reads: dmix for every level (level 0 from the stored read, on the
+        # second side stream, which has nothing else to do until the first
+        # parameter-gradient sums), dq and the group-state gradients for levels >= 1
         _lib.call("ngdn_output_bwd", ctypes.byref(d), P(R(sv["read0"])), P(R(do_)),
-                  P(R(dmix)), sa, stream=ta)
+                  P(R(dmix)), sb, stream=tb)
         for lvl in range(1, L):
             ng = n_groups(NT, f[lvl])
             top = lvl == L - 1

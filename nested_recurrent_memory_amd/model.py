@@ -131,9 +131,14 @@ class NestedGDN2Block(GradientCheckpointingLayer):
 
     def __init__(self, config, layer_idx):
         super().__init__()
-        self.attn_norm = RMSNorm(config.hidden_size, eps=config.norm_eps)
+        # fuse_norm=False: torch's nn.RMSNorm and plain residual adds, as the
+        # reference selects (models/modeling_nested_gdn2.py:46); the parameter
+        # names are the same either way
+        self.fused = config.fuse_norm
+        norm = RMSNorm if config.fuse_norm else nn.RMSNorm
+        self.attn_norm = norm(config.hidden_size, eps=config.norm_eps)
         self.attn = NestedGDN2Attention(config, layer_idx=layer_idx)
-        self.mlp_norm = RMSNorm(config.hidden_size, eps=config.norm_eps)
+        self.mlp_norm = norm(config.hidden_size, eps=config.norm_eps)
         self.mlp = GatedMLP(hidden_size=config.hidden_size, hidden_ratio=config.hidden_ratio,
                             intermediate_size=config.intermediate_size,
                             hidden_act=config.hidden_act, fuse_swiglu=config.fuse_swiglu)
@@ -148,6 +153,17 @@ class NestedGDN2Block(GradientCheckpointingLayer):
         hidden_states + residual, added inside the first norm; with
         ``defer_residual`` the block returns (h, mlp_out, cache) for the next
         norm to add instead of h + mlp_out."""
+        if not self.fused:
+            if residual is not None:
+                hidden_states = hidden_states + residual
+            attn_out, _, past_key_values = self.attn(self.attn_norm(hidden_states),
+                                                     past_key_values=past_key_values,
+                                                     use_cache=use_cache)
+            hidden_states = hidden_states + attn_out
+            mlp_out = self.mlp(self.mlp_norm(hidden_states))
+            if defer_residual:
+                return hidden_states, mlp_out, past_key_values
+            return hidden_states + mlp_out, past_key_values
         cdt = (torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda")
                else hidden_states.dtype)
         an, mn = self.attn_norm, self.mlp_norm
@@ -184,7 +200,7 @@ class NestedGDN2PreTrainedModel(PreTrainedModel):
                 nn.init.zeros_(module.bias)
         elif isinstance(module, nn.Embedding):
             nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
-        elif isinstance(module, (RMSNorm, FusedRMSNormGated)):
+        elif isinstance(module, (RMSNorm, nn.RMSNorm, FusedRMSNormGated)):
             nn.init.ones_(module.weight)
 
 
@@ -193,7 +209,8 @@ class NestedGDN2Model(NestedGDN2PreTrainedModel):
         super().__init__(config)
         self.embeddings = nn.Embedding(config.vocab_size, config.hidden_size)
         self.layers = nn.ModuleList(NestedGDN2Block(config, i) for i in range(config.num_hidden_layers))
-        self.norm = RMSNorm(config.hidden_size, eps=config.norm_eps)
+        self.norm = (RMSNorm if config.fuse_norm else nn.RMSNorm)(config.hidden_size,
+                                                                  eps=config.norm_eps)
         self.gradient_checkpointing = False
         self.post_init()
 
@@ -230,9 +247,11 @@ class NestedGDN2Model(NestedGDN2PreTrainedModel):
                 defer_residual=True)
         if use_cache:
             past_key_values.seen_tokens += hidden_states.shape[1]
-        if residual is not None:
+        if residual is not None and self.config.fuse_norm:
             _, hidden_states = add_rms_norm(hidden_states, residual, self.norm.weight, self.norm.eps)
         else:
+            if residual is not None:
+                hidden_states = hidden_states + residual
             hidden_states = self.norm(hidden_states)
         if output_hidden_states:
             all_hidden_states += (hidden_states,)

@@ -103,3 +103,28 @@ def test_autocast(dtype):
         if p.grad is not None:
             assert torch.isfinite(p.grad).all(), name
     assert abs(out.loss.item() - ref.item()) <= 2e-2 * abs(ref.item())
+
+
+def test_unfused_norms_match_fused():
+    """fuse_norm=False builds torch's nn.RMSNorm with plain residual adds
+    (models/modeling_nested_gdn2.py:46,100); with the same parameters the
+    model gives the fused path's loss and gradients (fp32, norm-wise 1e-5)."""
+    torch.manual_seed(0)
+    fused = NestedGDN2ForCausalLM(_config(2, (1, 2), (16,))).to(DEV)
+    plain = NestedGDN2ForCausalLM(_config(2, (1, 2), (16,), fuse_norm=False)).to(DEV)
+    assert isinstance(plain.model.layers[0].attn_norm, torch.nn.RMSNorm)
+    assert isinstance(plain.model.norm, torch.nn.RMSNorm)
+    with torch.no_grad():
+        for p in fused.parameters():
+            p.add_(0.01 * torch.randn_like(p))
+    plain.load_state_dict(fused.state_dict())
+    ids = torch.randint(0, 512, (2, 256), device=DEV)
+    la = fused(input_ids=ids, labels=ids).loss
+    lb = plain(input_ids=ids, labels=ids).loss
+    la.backward()
+    lb.backward()
+    assert abs(la.item() - lb.item()) <= 1e-5 * abs(la.item())
+    named = dict(plain.named_parameters())
+    for name, p in fused.named_parameters():
+        if p.grad is not None:
+            assert _rel(named[name].grad, p.grad) <= 1e-5, name
