@@ -111,6 +111,16 @@ def work_model(cfg):
         units * (L * ck + cm + kv + cv) + up_states,
         units * (wk + kv + wc + wv + (L - 1) * ck + cm + cv + wv) + up_states,
         units * (2 * C * K * V + 2 * C * C * V + (L - 1) * 2 * C * K * V))
+    # the same output in two passes beside the fused promotion ladder: level
+    # 0's share (Qg, hT, Aqk, vnT -> its read, fp32), then the upper levels'
+    # reads added to it with the mix (read_0, q of upper levels, mix, upper
+    # states once per group -> o)
+    m["ngdn_output_l0_fwd"] = (units * (ck + kv),
+                               units * (wk + kv + wc + wv + wv),
+                               units * (2 * C * K * V + 2 * C * C * V))
+    m["ngdn_output_upper_fwd"] = (units * ((L - 1) * ck + cm + cv) + up_states,
+                                  units * (wv + (L - 1) * ck + cm + cv) + up_states,
+                                  units * (L - 1) * 2 * C * K * V)
     # dmix_0 = <do, read_0>: reads read_0 (fp32), do; writes dmix
     m["ngdn_output_bwd"] = (tok * (V * es + 4), tok * (V * 4 + V * es + L * 4), tok * 2 * V)
     # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
@@ -139,6 +149,13 @@ def work_model(cfg):
         m[f"ngdn_upper_scan_fwd.{lvl}"] = (B * H * ng * kv + fin0,
                                            fu * 3 * nk + B * H * ng * 2 * kv,
                                            fu * 2 * 2 * N * K * V)
+        # the fused ladder (probe + update per firing, on chip): the gathered
+        # lower states and the parameters in; group states (both layouts), the
+        # final state and, for the backward, keys, (keys b e^g)^T and e^g out
+        m[f"ngdn_promote_chain_fwd.{lvl}"] = (fu * kv + par_f + B * H * ng * kv + fin0,
+                                              fu * (kv + 2 * nk + 4 * K) + par_f
+                                              + B * H * ng * 2 * kv + fin0,
+                                              fu * 7 * 2 * N * K * V)
         # reads of level lvl, per group: q_l, do, mix, the group state ->
         # d_states, dq_l, dmix_l (read, dq and dS products: 3 x 2 K V per token)
         m[f"ngdn_read_state_bwd.{lvl}"] = (tok * (K * es + V * es + es + K * es + 4)
@@ -155,16 +172,22 @@ def work_model(cfg):
         m[f"ngdn_probe_bwd.{lvl}"] = (fu * 3 * kv + H * (N * K + 8 * K * V) * es,
                                       fu * (4 * kv + kv + nv_ + 6 * nk + kv)
                                       + H * (N * K + 8 * K * V) * es, fu * 14 * 2 * N * K * V)
-        # parameter gradients: four A^T B sums over every firing's N rows
-        m[f"ngdn_param_grads.{lvl}"] = (4 * H * K * V * 4, fu * 5 * nk + 4 * H * K * V * 4,
+        # parameter gradients: four A^T B sums over every firing's N rows,
+        # written as per-slice partials (16 slices per head and product) and
+        # added in order; the bank gradient from its per-firing partials
+        split = max(1, min(16, (B * nf + 3) // 4))
+        m[f"ngdn_param_grads.{lvl}"] = (4 * H * K * V * 4 + H * N * K * 4,
+                                        fu * 6 * nk + 2 * 4 * H * split * K * V * 4
+                                        + 2 * (4 * H * K * V * 4 + H * N * K * 4),
                                         4 * fu * 2 * N * K * V)
     return m, units
 
 
 # entry points whose work is matrix products (intra-chunk, output, probe):
 # the benchmark reports their achieved fraction of the dense MFMA peak
-MFMA_KERNELS = ("ngdn_l0_intra_fwd", "ngdn_output_fwd", "ngdn_l0_bwd_state", "ngdn_l0_bwd_intra",
-                "ngdn_probe_fwd", "ngdn_probe_bwd")
+MFMA_KERNELS = ("ngdn_l0_intra_fwd", "ngdn_output_fwd", "ngdn_output_l0_fwd",
+                "ngdn_output_upper_fwd", "ngdn_l0_bwd_state", "ngdn_l0_bwd_intra",
+                "ngdn_probe_fwd", "ngdn_promote_chain_fwd", "ngdn_probe_bwd")
 
 
 def step_totals(cfg):
