@@ -82,10 +82,16 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
                 f"n_queries={n} exceeds the {query_banks.shape[2]} rows of query_banks")
 
 
-# The promotions of a level with at most 64 pairs per firing (merge: K = 64)
-# run fused, one launch per level (ngdn_promote_chain_fwd); others as a probe
-# launch and a scan launch. False forces the two-launch path everywhere.
-FUSED_PROMOTION = True
+# Two forms of a level's promotions in the forward. Two launches (the
+# default): a probe launch with one workgroup per (batch, head, firing), every
+# firing at once, then the level's scan of updates per (batch, head, 32
+# columns of V). Fused (True; levels with at most 64 pairs per firing, merge
+# at K = 64): one launch per level (ngdn_promote_chain_fwd), one workgroup
+# per (batch, head) running its firings in order with the probe and the
+# update on chip. The fused form keeps the pairs off HBM but runs B H
+# workgroups through a serial chain of firings; at the benchmark shapes the
+# two-launch form is faster (c2: 6.67 against 6.91 ms per fwd+bwd step).
+FUSED_PROMOTION = False
 
 
 def _chain_ok(K, N, merge):

@@ -136,3 +136,27 @@ def test_gradients_golden(name):
         want = exp["grad_initial_state"]
         err = (i_g.grad.cpu() - want).abs()
         assert (err <= 1e-4 * max(1.0, want.abs().max().item()) + 1e-4 * want.abs()).all()
+
+
+# the fused promotion ladder (chunk.FUSED_PROMOTION) in the forward, with the
+# backward reading its keys, (keys b e^g)^T and e^g
+FUSED_CASES = [
+    (1, 1024, 2, 128, 3, 64, (1, 4, 16), None, "learned"),
+    (2, 512, 2, 64, 3, 32, (1, 2, 4), None, "learned"),
+    (1, 512, 2, 64, 3, 16, (1, 2, 4), None, "merge"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("B,T,H,K,L,N,firing,nq,promotion", FUSED_CASES)
+def test_gradients_with_fused_promotion(B, T, H, K, L, N, firing, nq, promotion, dtype):
+    from nested_recurrent_memory_amd import chunk as chunk_mod
+    print(f"fused grads B={B} T={T} K={K} L={L} N={N} f={firing} {promotion} {dtype}", flush=True)
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=K, L=L, N=N, intervals=firing, n_queries=nq,
+                      dtype=dtype, g_scale=1.0, style="reftest")
+    try:
+        chunk_mod.FUSED_PROMOTION = True
+        ours, want = _run(inp, L, promotion, dtype)
+    finally:
+        chunk_mod.FUSED_PROMOTION = False
+    _check(ours, want, dtype, test=f"fused grads B{B} T{T} K{K} L{L} N{N} f{firing} {promotion}")

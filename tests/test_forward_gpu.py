@@ -258,7 +258,7 @@ def test_fused_promotion_matches_two_launch_path(dtype, K, L, N, firing, promoti
                 outs[fused] = chunk_nested_gdn2(**g, L=L, initial_state=init,
                                                 output_final_state=True, promotion=promotion)
     finally:
-        chunk_mod.FUSED_PROMOTION = True
+        chunk_mod.FUSED_PROMOTION = False
     torch.cuda.synchronize()
     tol = TOL[dtype]
     torch.testing.assert_close(outs[True][0].float(), outs[False][0].float(), **tol)
