@@ -66,7 +66,8 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
     if K not in _SUPPORTED_KV or V not in _SUPPORTED_KV:
         raise ValueError(f"head dims K={K}, V={V} unsupported; K and V must be 64 or 128")
     if L > 1 and K != V:
-        raise ValueError(f"promotion needs K == V, got K={K}, V={V}")
+        raise ValueError(f"the promotion kernels need K == V, got K={K}, V={V} "
+                         "(chunk_nested_gdn2 pads K != V to max(K, V) before this)")
     if L > 8:
         raise ValueError(f"at most 8 levels supported, got L={L}")
     if intervals[0] != 1:
@@ -551,11 +552,68 @@ def chunk_nested_gdn2(q, k, v, g, b, w, mix_weights, query_banks, key_projection
     (nested_gdn2/ops/chunk.py:722-743) and its naive twin (ops/naive.py:226-247).
 
     Returns (o [B, T, H, V] in q's dtype, final_state [B, H, L, K, V] fp32 or None).
+
+    K != V with upper levels (the layer's expand_v != 1) runs the K = V
+    kernels at D = max(K, V) on zero-padded inputs and parameters: the padded
+    channels stay exactly zero through every level and carry no gradient into
+    the real ones, so the results are those of the unpadded op (see
+    ``pad_kv``).
     """
+    K, V = q.shape[-1], v.shape[-1]
+    if int(L) > 1 and K != V:
+        if promotion == "merge" and K < V:
+            raise ValueError(f"merge promotion with K < V (K={K}, V={V}) is not supported: "
+                             "its decay is a mean over K pairs")
+        (q, k, v, g, b, w, query_banks, key_projections, b_projections, w_projections,
+         g_projections, initial_state) = pad_kv(
+            K, V, q=q, k=k, v=v, g=g, b=b, w=w, query_banks=query_banks,
+            key_projections=key_projections, b_projections=b_projections,
+            w_projections=w_projections, g_projections=g_projections,
+            initial_state=initial_state)
+        o, fin = ChunkNestedGDN2Function.apply(
+            q, k, v, g, b, w, mix_weights, query_banks, key_projections, b_projections,
+            w_projections, g_projections, n_queries_per_level, firing_intervals, L,
+            K ** -0.5 if scale is None else scale, initial_state, output_final_state,
+            chunk_size, promotion)
+        return o[..., :V], (fin[..., :K, :V] if fin is not None else None)
     return ChunkNestedGDN2Function.apply(
         q, k, v, g, b, w, mix_weights, query_banks, key_projections, b_projections,
         w_projections, g_projections, n_queries_per_level, firing_intervals, L,
         scale, initial_state, output_final_state, chunk_size, promotion)
+
+
+def pad_kv(K, V, *, q=None, k=None, v=None, g=None, b=None, w=None, query_banks=None,
+           key_projections=None, b_projections=None, w_projections=None, g_projections=None,
+           initial_state=None, state=None):
+    """The op's tensors zero-padded to D = max(K, V) in their K and V axes
+    (None stays None), in the order of the keywords. With K < V the key axis
+    grows: q, k, b, g and the bank get zero channels, so those channels of
+    the decay-masked products, of W, Kt, Qg and of every state row stay zero
+    (their decay e^0 = 1 keeps a zero row zero), and the write keys
+    u = Vals Wk^T get zero columns (the norm is unchanged). With V < K the
+    value axis grows: v and w get zero channels, so U, Vn, the states'
+    columns and Vals stay zero there, and the zero rows of the b, g, w
+    projections keep the gates of the real channels unchanged. Gradients
+    reaching the padded channels are zero or are dropped by the padding's
+    backward. (Merge with K < V would average its decay over D pairs instead
+    of K: refused by the caller.)"""
+    D = max(K, V)
+    pk, pv = D - K, D - V
+    F = torch.nn.functional
+
+    def last(t, p):
+        return t if t is None or p == 0 else F.pad(t, (0, p))
+
+    def last2(t, p_row, p_col):
+        return t if t is None or (p_row == 0 and p_col == 0) else F.pad(t, (0, p_col, 0, p_row))
+
+    out = [last(q, pk), last(k, pk), last(v, pv), last(g, pk), last(b, pk), last(w, pv),
+           last(query_banks, pk), last2(key_projections, pk, pv),
+           last2(b_projections, pv, pk), last2(w_projections, pv, pv),
+           last2(g_projections, pv, pk), last2(initial_state, pk, pv)]
+    if state is not None:
+        out.append(last2(state, pk, pv))
+    return out
 
 
 def default_scale(K: int) -> float:

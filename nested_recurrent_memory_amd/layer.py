@@ -40,6 +40,33 @@ from .step import step_nested_gdn2
 __all__ = ["NestedGDN2LayerConfig", "NestedGDN2Attention"]
 
 
+class _nullcontext:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+class _ForwardOnlyTail(torch.autograd.Function):
+    """The stepped tail's output joined to the graph of ``anchor``: forward
+    returns it as is; a backward that carries a nonzero gradient into it
+    raises (the decoding step has no backward)."""
+
+    @staticmethod
+    def forward(ctx, o, anchor):
+        ctx.set_materialize_grads(False)
+        return o.clone()
+
+    @staticmethod
+    def backward(ctx, grad):
+        if grad is None or not bool(grad.ne(0).any()):
+            return None, None
+        raise RuntimeError("NestedGDN2Attention: the tokens past the last whole chunk are "
+                           "stepped, and the decoding step has no backward; train with T a "
+                           "multiple of the chunk size (64) from an aligned position")
+
+
 @dataclass
 class NestedGDN2LayerConfig:
     """The fields of the reference's NestedGDN2Config
@@ -183,15 +210,24 @@ class NestedGDN2Attention(nn.Module):
             position = position + n_chunked
         elif state is None:
             state = x.new_zeros(B, H, L, K, V, dtype=torch.float32)
-        if n_chunked < T and torch.is_grad_enabled() and x.requires_grad:
-            raise ValueError(f"NestedGDN2Attention: the decoding step has no backward; training "
-                             f"needs T a multiple of {BT} from an aligned position (T={T})")
-        for t in range(n_chunked, T):
-            o_t, state = step_nested_gdn2(
-                q[:, t], k[:, t], v[:, t], g0[:, t], b0[:, t], w0[:, t], mix[:, t], state,
-                position, chunk_size=BT, **promo)
-            parts.append(o_t.unsqueeze(1))
-            position = position + 1
+        # The step is forward-only: a tail that is part of a graph is stepped
+        # on detached values and joins the graph through _ForwardOnlyTail,
+        # whose backward raises, so only an actual backward through it fails
+        # (the reference's step is differentiable, ops/naive.py:42-134)
+        anchor = q if (n_chunked < T and torch.is_grad_enabled() and q.requires_grad) else None
+        tail = []
+        with torch.no_grad() if anchor is not None else _nullcontext():
+            if anchor is not None and state is not None:
+                state = state.detach()
+            for t in range(n_chunked, T):
+                o_t, state = step_nested_gdn2(
+                    q[:, t], k[:, t], v[:, t], g0[:, t], b0[:, t], w0[:, t], mix[:, t], state,
+                    position, chunk_size=BT, **promo)
+                tail.append(o_t.unsqueeze(1))
+                position = position + 1
+        if tail:
+            o_tail = tail[0] if len(tail) == 1 else torch.cat(tail, dim=1)
+            parts.append(_ForwardOnlyTail.apply(o_tail, anchor) if anchor is not None else o_tail)
         o = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
         if use_cache:
             if past_key_values is None:

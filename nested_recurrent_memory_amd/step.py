@@ -15,7 +15,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .chunk import PROMOTIONS, _SUPPORTED_KV, _as_ints, _params, _working_dtype
+from .chunk import PROMOTIONS, _SUPPORTED_KV, _as_ints, _params, _working_dtype, pad_kv
 
 __all__ = ["step_nested_gdn2", "prepare_step_params"]
 
@@ -28,6 +28,12 @@ def prepare_step_params(query_banks, key_projections, b_projections, w_projectio
     them as ``params=``; they are a snapshot: prepare again after the
     parameters change."""
     wd, _ = _working_dtype(torch.empty(0, dtype=dtype))
+    K, V = query_banks.shape[-1], w_projections.shape[-1]
+    if K != V:   # laid out for the padded step (pad_kv)
+        (query_banks, key_projections, b_projections, w_projections,
+         g_projections) = pad_kv(K, V, query_banks=query_banks, key_projections=key_projections,
+                                 b_projections=b_projections, w_projections=w_projections,
+                                 g_projections=g_projections)[6:11]
     return _params(query_banks, key_projections, b_projections, w_projections,
                    g_projections, wd, False)
 
@@ -46,7 +52,8 @@ def _validate_step(q, k, v, L, chunk_size, promotion, nq, f, query_banks):
     if K not in _SUPPORTED_KV or V not in _SUPPORTED_KV:
         raise ValueError(f"head dims K={K}, V={V} unsupported; K and V must be 64 or 128")
     if L > 1 and K != V:
-        raise ValueError(f"promotion needs K == V, got K={K}, V={V}")
+        raise ValueError(f"the promotion kernels need K == V, got K={K}, V={V} "
+                         "(step_nested_gdn2 pads K != V to max(K, V) before this)")
     if L > 8:
         raise ValueError(f"at most 8 levels supported, got L={L}")
     if any(x <= 0 for x in f):
@@ -103,6 +110,28 @@ def step_nested_gdn2(
     fixed for graph capture.
     """
     L = int(L)
+    K, V = q.shape[-1], v.shape[-1]
+    if L > 1 and K != V:
+        # the K = V kernels at max(K, V) on zero-padded tensors (pad_kv)
+        if promotion == "merge" and K < V:
+            raise ValueError(f"merge promotion with K < V (K={K}, V={V}) is not supported: "
+                             "its decay is a mean over K pairs")
+        if state.shape[-2:] != (K, V):
+            raise ValueError(f"state must be [B, H, L, {K}, {V}], got {tuple(state.shape)}")
+        padded = pad_kv(K, V, q=q, k=k, v=v, g=g, b=b, w=w, query_banks=query_banks,
+                        key_projections=key_projections, b_projections=b_projections,
+                        w_projections=w_projections, g_projections=g_projections,
+                        state=state.to(torch.float32))
+        qp, kp_, vp, gp, bp, wp, qbp, kpp, bpp, wpp, gpp, _, sp = padded
+        o, s_new = step_nested_gdn2(
+            qp, kp_, vp, gp, bp, wp, mix_weights, sp, position, qbp, kpp, bpp, wpp, gpp,
+            n_queries_per_level, firing_intervals, L, K ** -0.5 if scale is None else scale,
+            chunk_size, promotion, params=params, inplace=False)
+        o, s_new = o[..., :V], s_new[..., :K, :V]
+        if inplace:
+            state.copy_(s_new)
+            return o, state
+        return o, s_new.contiguous()
     f = _as_ints(firing_intervals, L)
     nq = _as_ints(n_queries_per_level, L - 1) if L > 1 else []
     _validate_step(q, k, v, L, chunk_size, promotion, nq, f, query_banks)

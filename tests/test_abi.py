@@ -152,3 +152,12 @@ def test_add_rmsnorm_entry_points_validate_before_launch():
     assert b"NULL" in so.ngdn_last_error()
     # zero rows: nothing to do, nothing launched
     assert so.ngdn_add_rmsnorm_fwd(F32, F32, F32, 0, 1024, 1e-5, *([None] * 7)) == 0
+
+
+def test_merge_with_k_below_v_is_refused():
+    """K != V runs the K = V kernels on zero-padded tensors, except merge with
+    K < V, whose decay would average over max(K, V) pairs: refused before any
+    launch (on CPU tensors the op would otherwise raise for the device)."""
+    inp = make_inputs(B=1, T=64, H=2, K=64, V=128, L=2, N=16, intervals=(1, 1))
+    with pytest.raises(ValueError, match="K < V"):
+        chunk_nested_gdn2(**inp, L=2, promotion="merge")

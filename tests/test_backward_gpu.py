@@ -160,3 +160,26 @@ def test_gradients_with_fused_promotion(B, T, H, K, L, N, firing, nq, promotion,
     finally:
         chunk_mod.FUSED_PROMOTION = False
     _check(ours, want, dtype, test=f"fused grads B{B} T{T} K{K} L{L} N{N} f{firing} {promotion}")
+
+
+# K != V with upper levels (the layer's expand_v != 1): the op runs its K = V
+# kernels at max(K, V) on zero-padded tensors; the results are the unpadded
+# op's, against the oracle at K != V
+KV_CASES = [
+    (2, 320, 2, 128, 64, 3, 16, (1, 2, 4), "learned"),
+    (2, 320, 2, 128, 64, 3, 16, (1, 2, 4), "merge"),
+    (2, 320, 2, 64, 128, 3, 16, (1, 2, 4), "learned"),
+    (1, 256, 2, 64, 128, 2, 32, (1, 1), "learned"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("B,T,H,K,V,L,N,firing,promotion", KV_CASES)
+def test_gradients_k_ne_v(B, T, H, K, V, L, N, firing, promotion, dtype):
+    print(f"grads K={K} V={V} L={L} N={N} f={firing} {promotion} {dtype}", flush=True)
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=V, L=L, N=N, intervals=firing, dtype=dtype,
+                      g_scale=1.0, style="reftest")
+    gen = torch.Generator().manual_seed(6)
+    init = torch.randn(B, H, L, K, V, generator=gen) * 0.1
+    ours, want = _run(inp, L, promotion, dtype, init=init, with_dfinal=True)
+    _check(ours, want, dtype, test=f"grads K{K} V{V} L{L} N{N} f{firing} {promotion}")

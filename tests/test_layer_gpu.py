@@ -197,6 +197,9 @@ LAYER_CASES = [
                          use_short_conv=False, expand_v=2.0)),
     ("L2sigmoid_horizon", dict(num_levels=2, firing_intervals=(1, 1), n_queries_per_level=(32,),
                                read_mix="sigmoid", max_horizon=64)),
+    # expand_v 2 with an upper level: K = 64, V = 128 (layers/nested_gdn2.py:34)
+    ("L2learned_v2", dict(num_levels=2, firing_intervals=(1, 1), n_queries_per_level=(16,),
+                          expand_v=2.0)),
 ]
 # The decay parameters' gradients sum B*T*K terms that cancel, and with
 # max_horizon the clamp at -1/max_horizon flips for channels near it when the
@@ -275,12 +278,24 @@ def test_layer_prefill_and_decode_match_oracle(dtype, case):
             _near("conv_state", got, want, dtype)
 
 
-def test_layer_tail_with_grad_raises():
+def test_layer_tail_with_grad_runs_forward_and_raises_in_backward():
+    """A call whose last tokens are stepped (T = 70: one chunk, then 6 steps)
+    runs with grad enabled and gives the no-grad output; only a backward
+    through the stepped tokens raises (the decoding step has no backward)."""
     cfg, layer, _ = _layer(torch.float32, 31, num_levels=2, firing_intervals=(1, 2),
                            n_queries_per_level=(16,))
     x = torch.randn(1, 70, cfg.hidden_size, device=DEV, requires_grad=True)
-    with pytest.raises(ValueError, match="no backward"):
-        layer(x)
+    o, _, _ = layer(x)
+    assert o.requires_grad
+    with torch.no_grad():
+        want, _, _ = layer(x)
+    assert torch.equal(o.detach(), want)
+    with pytest.raises(RuntimeError, match="no backward"):
+        o.sum().backward()
+    x.grad = None
+    o, _, _ = layer(x)
+    o[:, :64].sum().backward()                 # the chunked part alone differentiates
+    assert x.grad is not None and torch.isfinite(x.grad).all()
 
 
 def test_layer_at_model_config_shape_matches_oracle():

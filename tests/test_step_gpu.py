@@ -42,6 +42,9 @@ CASES = [
     (3, 128, 128, 64, (1, 1, 2), "learned"),
     (3, 64, 64, 32, (1, 2, 4), "merge"),
     (2, 128, 128, 128, (1, 1), "merge"),
+    # K != V with upper levels: the K = V kernels at max(K, V), zero-padded
+    (2, 64, 128, 16, (1, 1), "learned"),
+    (3, 128, 64, 32, (1, 1, 2), "merge"),
 ]
 
 
