@@ -123,9 +123,10 @@ def work_model(cfg):
                                   units * (L - 1) * 2 * C * K * V)
     # dmix_0 = <do, read_0>: reads read_0 (fp32), do; writes dmix
     m["ngdn_output_bwd"] = (tok * (V * es + 4), tok * (V * 4 + V * es + L * 4), tok * 2 * V)
-    # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp, dVn, dVnT
+    # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp
+    # and dVnT (and dVn for the two-launch chunk backward)
     m["ngdn_l0_scan_bwd"] = (units * (cv + cm + kv),
-                             units * (3 * wk + wc + K * 4 + cv + C * es + kv + 2 * wv),
+                             units * (3 * wk + wc + K * 4 + cv + C * es + kv + wv),
                              units * (2 * C * K * V * 3 + 2 * C * C * V))
     # level-0 chunk backward, state half: h, dSp, vn, dVn, do, mix -> dQg, dWT, dKt, dAqk, dgam
     m["ngdn_l0_bwd_state"] = (units * (2 * kv + cv + cm),
@@ -138,6 +139,15 @@ def work_model(cfg):
         units * (3 * ck + 2 * cv + gk + wk + wv + wc + 3 * wk + wc + K * 4 + wv
                  + 3 * ck + 2 * cv + gk),
         units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
+    # level-0 chunk backward in one launch (the default): the state half per
+    # chunk in the same workgroup, dQg and dKt through a workspace;
+    # dX_w = -dX_u S^T replaces T^T dW
+    m["ngdn_l0_bwd"] = (
+        units * (2 * (3 * ck + 2 * cv + gk) + 2 * kv + cv + cm),
+        units * (3 * ck + 2 * cv + gk + wk + wv + wc + 2 * kv + 2 * wv + cv + C * es
+                 + 2 * 2 * wk + 3 * ck + 2 * cv + gk),
+        units * (2 * 2 * C * K * V + 2 * C * C * V + 2 * C * K * V
+                 + 2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     for lvl in range(1, L):
         nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         fu = B * H * nf
@@ -186,7 +196,7 @@ def work_model(cfg):
 # entry points whose work is matrix products (intra-chunk, output, probe):
 # the benchmark reports their achieved fraction of the dense MFMA peak
 MFMA_KERNELS = ("ngdn_l0_intra_fwd", "ngdn_output_fwd", "ngdn_output_l0_fwd",
-                "ngdn_output_upper_fwd", "ngdn_l0_bwd_state", "ngdn_l0_bwd_intra",
+                "ngdn_output_upper_fwd", "ngdn_l0_bwd_state", "ngdn_l0_bwd_intra", "ngdn_l0_bwd",
                 "ngdn_probe_fwd", "ngdn_promote_chain_fwd", "ngdn_probe_bwd")
 
 

@@ -195,8 +195,9 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
  * entering chunk (i+1)*f1, added before that chunk's step (the reference's
  * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
- * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64], and d_initial[:, :, 0]
- * when not NULL. Kt, WT, QgT and AqkT are read split. */
+ * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (either may be NULL, not
+ * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL.
+ * Kt, WT, QgT and AqkT are read split. */
 int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
                          const float* gam, const float* AqkT, const float* QgT,
                          const void* dout, const void* mix, int32_t f1,
@@ -234,6 +235,20 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
                           const float* dKt, const float* dAqk, const float* dgam,
                           const float* dVnT, void* dq, void* dk, void* dv,
                           float* dg, void* db, void* dw, void* stream);
+
+/* The two halves above in one launch (the rest of the vendored
+ * chunk_gdn2_bwd, ops/_vendor/gdn2_chunk_bwd.py:26-187): the state half is
+ * computed per chunk by the workgroup that uses it, from h [B,H,NT,K,V] and
+ * vn [B,H,NT,64,V] of ngdn_l0_scan_fwd, dSp [B,H,NT,K,V] and dVnT of
+ * ngdn_l0_scan_bwd, do and mix; its dQg and dKt pass through the workspaces
+ * ws_dQg, ws_dKt (fp32 [B,H,NT,64,K] each, no initial contents), the rest
+ * stays on chip. Outputs as ngdn_l0_bwd_intra. */
+int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void* v,
+                    const float* g, const void* b, const void* w, const float* W,
+                    const float* U, const float* TT, const float* h, const float* dSp,
+                    const float* vn, const float* dVnT, const void* dout, const void* mix,
+                    float* ws_dQg, float* ws_dKt, void* dq, void* dk, void* dv, float* dg,
+                    void* db, void* dw, void* stream);
 
 /* Backward of level `level`'s firings through its update and probe.
  * The lower level's states as rows (below_kv) and transposed (below_vk):

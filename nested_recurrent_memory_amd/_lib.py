@@ -53,6 +53,7 @@ SIGNATURES = {
     "ngdn_upper_scan_bwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
     "ngdn_l0_bwd_state": [PD] + [P] * 6 + [P] * 5 + [P],
     "ngdn_l0_bwd_intra": [PD] + [P] * 6 + [P] * 3 + [P] * 6 + [P] * 6 + [P],
+    "ngdn_l0_bwd": [PD] + [P] * 6 + [P] * 3 + [P] * 4 + [P] * 2 + [P] * 2 + [P] * 6 + [P],
     "ngdn_probe_bwd": [PD, I32, I32, I32, I32, I32, P, P, I32, P, P, I32, P, P, P, P,
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P, P] + [P],
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, I32, P, P, P, P, P, P, P],

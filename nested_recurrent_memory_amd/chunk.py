@@ -94,6 +94,10 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
 # two-launch form is faster (c2: 6.67 against 6.91 ms per fwd+bwd step).
 FUSED_PROMOTION = False
 
+# The level-0 chunk backward as one launch (ngdn_l0_bwd: the state half per
+# chunk in the same workgroup) or two (ngdn_l0_bwd_state, ngdn_l0_bwd_intra).
+FUSED_L0_BWD = True
+
 
 def _chain_ok(K, N, merge):
     if merge:
@@ -353,9 +357,14 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     # per-slice partials of the parameter-gradient sums, shared by the levels
     # (their sums run one after another on one stream)
     parts = f32(4, H, _lib.PARAM_SPLIT, K, V) if L > 1 else None
-    dSp0, dVn0, dVnT0 = f32(B, H, NT, K, V), f32(B, H, NT, 64, V), f32(B, H, NT, V, 64)
-    dQg, dKt, dWT = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K), f32(B, H, NT, K, 64)
-    dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
+    dSp0, dVnT0 = f32(B, H, NT, K, V), f32(B, H, NT, V, 64)
+    # dQg, dKt: the fused chunk backward's workspaces; the rest only for the
+    # two-launch form
+    dQg, dKt = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K)
+    dVn0 = dWT = dAqk = dgam = None
+    if not FUSED_L0_BWD:
+        dVn0, dWT = f32(B, H, NT, 64, V), f32(B, H, NT, K, 64)
+        dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
     dg = f32(B, T, H, K)
 
@@ -439,12 +448,18 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
             "Kt", "WT", "gam", "AqkT", "QgT")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
             P(R(inj)), nf1, P(R(d_final)), P(R(dSp0)), P(R(dVn0)), P(R(dVnT0)), P(R(d_init)), sp)
-        _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(R(sv["h"])), P(R(dSp0)),
-                  P(R(sv["vn"])), P(R(dVn0)), P(R(do_)), P(R(mix_)),
-                  *(P(R(x)) for x in (dQg, dWT, dKt, dAqk, dgam)), sp)
-        _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), *(P(R(x)) for x in (
-            q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], dQg, dWT, dKt, dAqk, dgam,
-            dVnT0, dq, dk, dv, dg, db, dw)), sp)
+        if FUSED_L0_BWD:
+            # the chunk backward in one launch: the state half per chunk
+            _lib.call("ngdn_l0_bwd", ctypes.byref(d), *(P(R(x)) for x in (
+                q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], sv["h"], dSp0, sv["vn"],
+                dVnT0, do_, mix_, dQg, dKt, dq, dk, dv, dg, db, dw)), sp)
+        else:
+            _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(R(sv["h"])), P(R(dSp0)),
+                      P(R(sv["vn"])), P(R(dVn0)), P(R(do_)), P(R(mix_)),
+                      *(P(R(x)) for x in (dQg, dWT, dKt, dAqk, dgam)), sp)
+            _lib.call("ngdn_l0_bwd_intra", ctypes.byref(d), *(P(R(x)) for x in (
+                q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], dQg, dWT, dKt, dAqk, dgam,
+                dVnT0, dq, dk, dv, dg, db, dw)), sp)
         if aux is not None:
             st.wait_stream(aux[1])
 

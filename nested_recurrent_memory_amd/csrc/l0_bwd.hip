@@ -160,7 +160,9 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 3 : 2) void l0_bwd_state_kern
   }
 }
 
-template <typename E, int K, int V>
+// FUSED (the l0_bwd entry point): the state half is phase 1 and part of
+// phase 2 of this kernel instead of l0_bwd_state's outputs (see below).
+template <typename E, int K, int V, bool FUSED>
 __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) {
   constexpr int C = CH;
   constexpr int NH = K > 64 ? 64 : K;          // columns per pass of the decay backward
@@ -183,8 +185,14 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   constexpr size_t SZ_G = sizeof(float) * C * GH;
   constexpr size_t SZ_IN = STAGE ? sizeof(E) * 3 * C * LDI : 0;
   constexpr size_t SZ_P = SZ_DA + SZ_G + SZ_IN;
-  constexpr size_t SZ_R = SZ_X > SZ_P ? SZ_X : SZ_P;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (5 * K + 256)];
+  // fused phase 1: the chunk's Vn rows (split tile) and do rows (exact)
+  using ST1 = SplitTile<E>;
+  constexpr int LDV1 = V + ST1::PAD, LDO1 = V + 16 / (int)sizeof(E);
+  constexpr size_t SZ_V1 = sizeof(typename ST1::T) * ST1::NPLANE * C * LDV1;
+  constexpr size_t SZ_1 = FUSED ? SZ_V1 + sizeof(E) * C * LDO1 : 0;
+  constexpr size_t SZ_R0 = SZ_X > SZ_P ? SZ_X : SZ_P;
+  constexpr size_t SZ_R = SZ_R0 > SZ_1 ? SZ_R0 : SZ_1;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (6 * K + 256 + C)];
   float* s_dXw = reinterpret_cast<float*>(smem);
   float* s_dXu = s_dXw + C * LXK;
   float* s_dA = reinterpret_cast<float*>(smem);
@@ -196,6 +204,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   float* s_gl = reinterpret_cast<float*>(smem + SZ_R);   // gc of the last row, per column
   float* s_col = s_gl + K;                                // [4 waves][K] column sums of phase 5
   float* s_part = s_col + 4 * K;                          // [256 / NH][NH] block sums of phase 6
+  float* s_dgam = s_part + 256;                           // fused: dgam of the pass columns
+  float* s_m0 = s_dgam + K;                               // fused: mix_0 of the chunk's rows
 
   const int NT = a.NT, H = a.H, T = a.T;
   const int n = blockIdx.x % NT;
@@ -207,6 +217,119 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, T, H, a.L, a.scale);
   const int t0 = in.t0, nvalid = in.nvalid;
   for (int e = tid; e < 4 * K; e += 256) s_col[e] = 0.f;
+
+  constexpr int CPW = CTK / 4;                 // fused: column tiles of K per wave
+  constexpr int NKV = V / KS;                  // k-steps over V
+  f4 daq[4];                                   // fused: this wave's dAqk tiles
+  if constexpr (FUSED) {
+    // ---- 1. the state half (what l0_bwd_state computes), from S = h, dS',
+    // Vn, do and mix_0 of this chunk:
+    //   dQg = dO S^T, dKt = Vn dS'^T  (to the workspaces, read back in phase 4)
+    //   dgam = rowsum(dS' * S)        (LDS, read in phase 6)
+    //   dAqk = mask(dO Vn^T)          (registers until phase 3)
+    // with dO = mix_0 do (a row scale, applied to the products). Wave w owns
+    // CPW column tiles (rows k of S and dS', loaded once per workgroup) and
+    // every row of the chunk; Vn (split) and do (exact) rows come from LDS.
+    // Phase 2 forms dX_w = T^T dW from dX_u instead of reading dW.
+    static_assert(CTK % 4 == 0, "column tiles of K split over the 4 waves");
+    const ST1 sVn1{reinterpret_cast<typename ST1::T*>(smem), C * LDV1};
+    E* s_do1 = reinterpret_cast<E*>(smem + SZ_V1);
+    {
+      constexpr int VE = 16 / (int)sizeof(E);
+      constexpr int PV = C * V / 4 / 256, PO = C * V / VE / 256;
+      static_assert(C * V / 4 % 256 == 0 && C * V / VE % 256 == 0, "whole groups per thread");
+      typedef __attribute__((__vector_size__(16))) int v4i;
+      const float* vnc = a.vn + cix * C * V;
+      const E* dob = static_cast<const E*>(a.dout) + ((size_t)b * T * H + h) * V;
+      f4 xv[PV];
+      v4i xo[PO];
+#pragma unroll
+      for (int u = 0; u < PV; ++u) {
+        const int e = tid + 256 * u;
+        xv[u] = *reinterpret_cast<const f4*>(vnc + (size_t)(e / (V / 4)) * V + (e % (V / 4)) * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < PO; ++u) {
+        const int e = tid + 256 * u, i = e / (V / VE), c = (e % (V / VE)) * VE;
+        const v4i z = {0, 0, 0, 0};
+        xo[u] = i < nvalid ? *reinterpret_cast<const v4i*>(dob + (size_t)(t0 + i) * H * V + c) : z;
+      }
+      if (tid < C)
+        s_m0[tid] = tid < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + tid) * H * a.L +
+                                                                      (size_t)h * a.L])
+                                 : 0.f;
+#pragma unroll
+      for (int u = 0; u < PV; ++u) {
+        const int e = tid + 256 * u;
+        sVn1.put4((e / (V / 4)) * LDV1 + (e % (V / 4)) * 4, xv[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < PO; ++u) {
+        const int e = tid + 256 * u, i = e / (V / VE), c = (e % (V / VE)) * VE;
+        *reinterpret_cast<v4i*>(s_do1 + i * LDO1 + c) = xo[u];
+      }
+    }
+    lds_barrier();
+    const float* Sg = a.h + cix * K * V;
+    const float* dSg = a.dSp + cix * K * V;
+    float* wq = a.wsQ + cix * C * K;
+    float* wk = a.wsK + cix * C * K;
+    constexpr int KPL = Mma<E>::KPL;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int ct = wv * CPW + c, kr = ct * 16 + (lane & 15);
+      SF fS[NKV], fD[NKV];
+      float dgp = 0.f;
+#pragma unroll
+      for (int s = 0; s < NKV; ++s) {
+        const int v0 = s * KS + kofs<E>(lane);
+        float x[KPL], y[KPL];
+        ld_raw<KPL>(Sg + (size_t)kr * V + v0, x);
+        ld_raw<KPL>(dSg + (size_t)kr * V + v0, y);
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) dgp += x[e] * y[e];
+        fS[s] = Mma<E>::makes([&](int e) { return x[e]; });
+        fD[s] = Mma<E>::makes([&](int e) { return y[e]; });
+      }
+      // the four lane groups hold disjoint v ranges of the same row k
+      dgp += __shfl_xor(dgp, 16, WAVE);
+      dgp += __shfl_xor(dgp, 32, WAVE);
+      if (lane < 16) s_dgam[ct * 16 + lane] = dgp;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const int ri1 = rt * 16 + (lane & 15);
+        f4 aq = f4_zero(), ak = f4_zero();
+#pragma unroll
+        for (int s = 0; s < NKV; ++s) {
+          const int v0 = s * KS + kofs<E>(lane);
+          aq = Mma<E>::mma(aq, Mma<E>::ld(s_do1 + ri1 * LDO1 + v0), fS[s]);
+          ak = Mma<E>::mma(ak, sVn1.get(ri1 * LDV1 + v0), fD[s]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rt * 16 + acc_row(r), k = ct * 16 + acc_col();
+          wq[i * K + k] = aq[r] * s_m0[i];
+          wk[i * K + k] = ak[r];
+        }
+      }
+    }
+    // this wave's rows of dAqk, tiles J <= w (lower including the diagonal)
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      daq[J] = f4_zero();
+      if (J <= wv) {
+#pragma unroll
+        for (int s = 0; s < NKV; ++s) {
+          const int v0 = s * KS + kofs<E>(lane);
+          daq[J] = Mma<E>::mma(daq[J], Mma<E>::ld(s_do1 + (wv * 16 + (lane & 15)) * LDO1 + v0),
+                               sVn1.get((J * 16 + (lane & 15)) * LDV1 + v0));
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) daq[J][r] *= s_m0[wv * 16 + acc_row(r)];
+    }
+    lds_barrier();   // phase 2 reuses the space
+  }
 
   // ---- 2. dX_u = T^T dVn, dX_w = T^T dW; wave w owns a quarter of the
   // columns of each and every row, so each wave splits the small T^T (all
@@ -243,9 +366,34 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       }
     };
     product(a.dVnT + cix * V * C, V, s_dXu, LXV);
-    product(a.dWT + cix * K * C, K, s_dXw, LXK);
+    if constexpr (!FUSED) product(a.dWT + cix * K * C, K, s_dXw, LXK);
   }
   lds_barrier();
+  if constexpr (FUSED) {
+    // dW = -dVn S^T, so dX_w = T^T dW = -(T^T dVn) S^T = -dX_u S^T: wave w
+    // owns its CPW column tiles (rows k of S) over every row of the chunk
+    const float* Sg = a.h + cix * K * V;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int ct = wv * CPW + c, kr = ct * 16 + (lane & 15);
+      SF fS[NKV];
+#pragma unroll
+      for (int s = 0; s < NKV; ++s) fS[s] = Mma<E>::ld(Sg + (size_t)kr * V + s * KS + kofs<E>(lane));
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        f4 acc = f4_zero();
+#pragma unroll
+        for (int s = 0; s < NKV; ++s)
+          acc = Mma<E>::mma(acc, Mma<E>::ld(s_dXu + (rt * 16 + (lane & 15)) * LXV + s * KS + kofs<E>(lane)),
+                            fS[s]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_dXw[(rt * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()] = -acc[r];
+      }
+    }
+    // s_dXw complete; phase 1's workspace stores complete and visible to the
+    // whole workgroup (a barrier that also orders global memory)
+    __syncthreads();
+  }
   // this wave's rows of dX_w, kept for phase 5 (the space is reused from phase 4)
 #pragma unroll
   for (int ct = 0; ct < CTK; ++ct)
@@ -272,10 +420,12 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     }
   }
   // dAqk, read before the dv/dw stores
-  constexpr int DQE = C * C / 256;
+  constexpr int DQE = FUSED ? 1 : C * C / 256;
   float dqv[DQE];
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int u = 0; u < DQE; ++u) dqv[u] = a.dAqk[cix * C * C + tid + 256 * u];
+    for (int u = 0; u < DQE; ++u) dqv[u] = a.dAqk[cix * C * C + tid + 256 * u];
+  }
 
   // dv = dX_u * w, dw = dX_u * v: 16-byte rows, all loads of a thread ahead of its stores
   {
@@ -318,21 +468,30 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       s_dA[i * AT_LD + j] = (j < i) ? -dat[J][r] : 0.f;
     }
   }
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int u = 0; u < DQE; ++u) {
-    const int e = tid + 256 * u;
-    s_dQ[(e / C) * AT_LD + e % C] = dqv[u];
+    for (int J = 0; J < 4; ++J)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = wv * 16 + acc_row(r), j = J * 16 + acc_col();
+        s_dQ[i * AT_LD + j] = (J <= wv && j <= i) ? daq[J][r] : 0.f;
+      }
+  } else {
+#pragma unroll
+    for (int u = 0; u < DQE; ++u) {
+      const int e = tid + 256 * u;
+      s_dQ[(e / C) * AT_LD + e % C] = dqv[u];
+    }
   }
 
   const int R0 = 16 * wv;
-  const float* dQg = a.dQg + cix * C * K;
-  const float* dKt = a.dKt + cix * C * K;
+  const float* dQg = (FUSED ? a.wsQ : a.dQg) + cix * C * K;
+  const float* dKt = (FUSED ? a.wsK : a.dKt) + cix * C * K;
   const size_t tok = (size_t)b * T * H + h;
   E* dqo = static_cast<E*>(a.dq) + tok * a.L * K;
   E* dko = static_cast<E*>(a.dk) + tok * K;
   E* dbo = static_cast<E*>(a.db) + tok * K;
   float* dgo = a.dg + tok * K;
-  const float* dgam = a.dgam + cix * K;
 
   // Inputs of one pass (NH columns from c0): g for the in-chunk cumulative
   // sum and, for bf16, the k, b, q columns. They are read into registers ahead
@@ -571,7 +730,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       s_part[blk * NH + col] = part;
       lds_barrier();
       float run = ((s_col[kc] + s_col[K + kc]) + s_col[2 * K + kc]) + s_col[3 * K + kc];
-      run += dgam[kc] * fexp(s_gl[kc]);
+      run += (FUSED ? s_dgam[kc] : a.dgam[cix * K + kc]) * fexp(s_gl[kc]);
       for (int b2 = NB - 1; b2 > blk; --b2) run += s_part[b2 * NH + col];
 #pragma unroll
       for (int i = RB - 1; i >= 0; --i) {
@@ -592,10 +751,10 @@ static hipError_t launch_l0_bwd_state(const L0BwdStateArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename E, int K, int V>
+template <typename E, int K, int V, bool FUSED>
 static hipError_t launch_l0_bwd_intra(const L0BwdIntraArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.B * a.H * a.NT);
-  hipLaunchKernelGGL((l0_bwd_intra_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((l0_bwd_intra_kernel<E, K, V, FUSED>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -611,9 +770,11 @@ hipError_t l0_bwd_state(const L0BwdStateArgs& a, int dtype, int K, int V, hipStr
   return hipErrorInvalidValue;
 }
 
-hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st) {
+template <bool FUSED>
+static hipError_t l0_bwd_intra_dispatch(const L0BwdIntraArgs& a, int dtype, int K, int V,
+                                        hipStream_t st) {
 #define NGDN_BI(E, KK, VV) \
-  if (K == KK && V == VV) return launch_l0_bwd_intra<E, KK, VV>(a, st);
+  if (K == KK && V == VV) return launch_l0_bwd_intra<E, KK, VV, FUSED>(a, st);
   if (dtype == NGDN_BF16) {
     NGDN_BI(bf16, 64, 64) NGDN_BI(bf16, 64, 128) NGDN_BI(bf16, 128, 64) NGDN_BI(bf16, 128, 128)
   } else {
@@ -621,6 +782,14 @@ hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStr
   }
 #undef NGDN_BI
   return hipErrorInvalidValue;
+}
+
+hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st) {
+  return l0_bwd_intra_dispatch<false>(a, dtype, K, V, st);
+}
+
+hipError_t l0_bwd_fused(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st) {
+  return l0_bwd_intra_dispatch<true>(a, dtype, K, V, st);
 }
 
 }  // namespace ngdn

@@ -428,7 +428,15 @@ struct L0BwdIntraArgs {
   void* dq; void* dk; void* dv; float* dg; void* db; void* dw;
   int B, T, H, L, NT;
   float scale;
+  // the fused form (l0_bwd): the state half computed by the same workgroup
+  // from the chunk states h [.,K,V], their gradients dSp [.,K,V], Vn [.,64,V],
+  // do and mix; dQg and dKt pass through the workspaces wsQ, wsK [.,64,K]
+  // (fp32, no initial contents) between its phases; dQg, dWT, dKt, dAqk and
+  // dgam above are then unused
+  const float* h; const float* dSp; const float* vn; const void* dout; const void* mix;
+  float* wsQ; float* wsK;
 };
 hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st);
+hipError_t l0_bwd_fused(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
 }  // namespace ngdn

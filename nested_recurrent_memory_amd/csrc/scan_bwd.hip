@@ -227,9 +227,11 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
               acc = Mma<E>::mma(acc, cur.aqk[p][s], sdO.get(orow + s * KS));
           }
           const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-          float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
+          if (a.dVn) {
+            float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
+            for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
+          }
           sdV.put4(vl * LDS_VN + m0, acc);
           if (a.dVnT)
             *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;

@@ -183,3 +183,20 @@ def test_gradients_k_ne_v(B, T, H, K, V, L, N, firing, promotion, dtype):
     init = torch.randn(B, H, L, K, V, generator=gen) * 0.1
     ours, want = _run(inp, L, promotion, dtype, init=init, with_dfinal=True)
     _check(ours, want, dtype, test=f"grads K{K} V{V} L{L} N{N} f{firing} {promotion}")
+
+
+# the level-0 chunk backward as two launches (ngdn_l0_bwd_state, then
+# ngdn_l0_bwd_intra) instead of the fused ngdn_l0_bwd
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("K,V,L", [(128, 128, 3), (64, 128, 1)])
+def test_gradients_with_two_launch_level0_backward(K, V, L, dtype):
+    from nested_recurrent_memory_amd import chunk as chunk_mod
+    print(f"two-launch l0 bwd K={K} V={V} L={L} {dtype}", flush=True)
+    inp = make_inputs(B=2, T=320, H=2, K=K, V=V, L=L, N=16, intervals=(1, 2, 4)[:L],
+                      dtype=dtype, g_scale=1.0, style="reftest")
+    try:
+        chunk_mod.FUSED_L0_BWD = False
+        ours, want = _run(inp, L, "learned", dtype, with_dfinal=True)
+    finally:
+        chunk_mod.FUSED_L0_BWD = True
+    _check(ours, want, dtype, test=f"two-launch l0 bwd K{K} V{V} L{L}")

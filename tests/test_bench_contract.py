@@ -24,13 +24,18 @@ def test_work_model_covers_every_headline_entry_point():
     assert units == 4 * 16 * 128
     for name in ("ngdn_l0_intra_fwd", "ngdn_l0_scan_fwd", "ngdn_output_fwd", "ngdn_l0_bwd_intra",
                  "ngdn_l0_bwd_state", "ngdn_l0_scan_bwd", "ngdn_probe_fwd.1", "ngdn_probe_bwd.2",
-                 "ngdn_param_grads.1", "ngdn_read_state_bwd.2", "ngdn_output_bwd"):
+                 "ngdn_param_grads.1", "ngdn_read_state_bwd.2", "ngdn_output_bwd", "ngdn_l0_bwd",
+                 "ngdn_promote_chain_fwd.1", "ngdn_output_l0_fwd", "ngdn_output_upper_fwd"):
         nbytes, design, flops = model[name]
         assert 0 < nbytes <= design and flops > 0, name
     # the level-0 intra backward's algorithmic bytes are the op's tensors it
     # touches: reads q0, k, b, v, w (bf16) and g (fp32), writes their
     # gradients: 224 KiB per chunk-head
     assert model["ngdn_l0_bwd_intra"][0] == units * 2 * (5 * 64 * 128 * 2 + 64 * 128 * 4)
+    # the fused chunk backward adds the chunk state and its gradient (fp32
+    # K x V each), do and mix_0..2 (bf16) to those
+    assert model["ngdn_l0_bwd"][0] == units * (2 * (5 * 64 * 128 * 2 + 64 * 128 * 4)
+                                               + 2 * 128 * 128 * 4 + 64 * 128 * 2 + 64 * 3 * 2)
 
 
 def test_step_totals_at_the_headline():
