@@ -72,14 +72,19 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
 
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
- * Writes hT [B,H,NT,V,K] (state entering each chunk, transposed), vnT
- * [B,H,NT,V,64] (the chunk's new values, transposed) and final_state[:, :, 0];
- * for the backward, when not NULL, h [B,H,NT,K,V] (the same states as rows)
- * and vn [B,H,NT,64,V]. initial_state may be NULL (zeros). */
+ * Writes final_state[:, :, 0] and, each when not NULL: hT [B,H,NT,V,K] (the
+ * state entering chunk j, transposed, for chunks j with j % hT_every == 0:
+ * the probes of level 1 read every f1-th), vnT [B,H,NT,V,64] (the chunk's
+ * new values, transposed), for the backward h [B,H,NT,K,V] (the states as
+ * rows) and vn [B,H,NT,64,V], and read0 [B,T,H,V] fp32: level 0's read
+ * Qg h + Aqk Vn of every token (Qg, Aqk from ngdn_l0_intra_fwd, required
+ * with read0), formed while the state is on chip, which
+ * ngdn_output_upper_fwd turns into o. initial_state may be NULL (zeros). */
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
-                         const float* KtT, const float* gam,
-                         const float* initial_state, float* hT, float* vnT,
-                         float* h, float* vn, float* final_state, void* stream);
+                         const float* KtT, const float* gam, const float* Qg,
+                         const float* Aqk, const float* initial_state, int32_t hT_every,
+                         float* hT, float* vnT, float* h, float* vn, float* read0,
+                         float* final_state, void* stream);
 
 /* Promotion probe of level `level` >= 1: PROBES[promotion] applied to the
  * lower level's state after each of this level's firings

@@ -10,16 +10,17 @@ GPU the op raises.
 
 Forward, per call (reference composition ops/chunk.py:159-304):
   ngdn_l0_intra_fwd    per-chunk level-0 terms, all chunks in parallel
-  ngdn_l0_scan_fwd     level-0 state recurrence, states h per chunk
+  ngdn_l0_scan_fwd     level-0 state recurrence: states h per chunk, and
+                       the level-0 read (Qg h + Aqk Vn) per row; the states
+                       the level above reads (every f_1-th) when L > 1
   for each level l >= 1:
     ngdn_promote_chain_fwd  the level's firings in order per (batch, head):
                             gather, probe and update on chip, one state per
                             group stored (up to 64 pairs per firing), or
     ngdn_probe_fwd          probe the level below at this level's firings,
     ngdn_upper_scan_fwd     then this level's write scan (128 pairs)
-  ngdn_output_fwd      level-0 read + every upper read + mix, o written once
-                       (with a fused ladder: ngdn_output_l0_fwd beside it on a
-                       side stream, then ngdn_output_upper_fwd)
+  ngdn_output_upper_fwd  every upper read + mix over the scan's level-0
+                       read, o written once
 """
 
 from __future__ import annotations
@@ -181,7 +182,9 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     gam = f32(B, H, NT, K)
     Kt, WT, QgT = opt(B, H, NT, 64, K), opt(B, H, NT, K, 64), opt(B, H, NT, K, 64)
     AqkT, TT = opt(B, H, NT, 64, 64), opt(B, H, NT, 64, 64)
-    hT, vnT = f32(B, H, NT, V, K), f32(B, H, NT, V, 64)
+    # the state entering each chunk, transposed: read by level 1's probes at
+    # every f1-th chunk only, so only those are written
+    hT = f32(B, H, NT, V, K) if L > 1 else None
     h_, vn_ = opt(B, H, NT, K, V), opt(B, H, NT, 64, V)
     final = torch.empty(B, H, L, K, V, device=dev, dtype=torch.float32)
     states = [None] * L       # group states as rows [B,NG,H,K,V]
@@ -207,11 +210,10 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                                AT=opt(B, H, nf1, K, N))
         states[lvl], statesT[lvl] = f32(B, ng, H, K, V), f32(B, ng, H, V, K)
     o = e(B, T, H, V)
-    # With a fused promotion ladder (one workgroup per (batch, head), a
-    # fraction of the GPU) level 0's share of the output runs beside it on a
-    # side stream, writing its read; a second pass adds the upper levels'.
-    chains = any(levels[lvl]["chain"] for lvl in range(1, L))
-    read0 = f32(B, T, H, V) if (train or chains) else None
+    # level 0's read of every token, formed by the level-0 scan while each
+    # chunk's state is on chip; the output pass adds the upper levels' reads
+    # and the mix (and the backward's dmix_0 reads it again)
+    read0 = f32(B, T, H, V)
     P = _lib.ptr
 
     def param_grads(d, lvl, sp, st):
@@ -229,13 +231,8 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
             q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT)), sp)
         _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-            W, U, KtT, gam, init_, hT, vnT, h_, vn_, final)), sp)
-        split = chains and nb == B
-        if split:
-            side = _aux_streams(dev)[0]
-            side.wait_event(st.record_event())
-            _lib.call("ngdn_output_l0_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-                Qg, Aqk, hT, vnT, read0)), _lib.ptr_of_stream(side), stream=side)
+            W, U, KtT, gam, Qg, Aqk, init_)), f[1] if L > 1 else 1,
+            *(P(R(x)) for x in (hT, None, h_, vn_, read0, final)), sp)
         for lvl in range(1, L):
             lv = levels[lvl]
             fh, fb = f[lvl], f[lvl - 1]
@@ -260,20 +257,15 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                       P(R(states[lvl])), P(R(statesT[lvl])), P(R(final)), sp,
                       tag=f"ngdn_upper_scan_fwd.{lvl}")
         spT, ngs, fs = _level_arrays([R(x) for x in statesT], NT, f, L)
-        if split:
-            st.wait_stream(side)
-            _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(R(read0)), P(R(q_)),
-                      P(R(mix_)), spT, ngs, fs, P(R(o)), sp)
-        else:
-            _lib.call("ngdn_output_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-                Qg, Aqk, hT, vnT, q_, mix_)), spT, ngs, fs, P(R(o)), P(R(read0)), sp)
+        _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(R(read0)), P(R(q_)),
+                  P(R(mix_)), spT, ngs, fs, P(R(o)), sp)
 
     _run_groups(B, dev, launch)
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
                      KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
-                     hT=hT, vnT=vnT, h=h_, vn=vn_, read0=read0, states=states,
+                     hT=hT, h=h_, vn=vn_, read0=read0, states=states,
                      statesT=statesT, levels=levels, final=final, par=par,
                      code=code, wd=wd)
     return o, final, saved

@@ -66,19 +66,23 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
 }
 
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
-                         const float* KtT, const float* gam,
-                         const float* initial_state, float* hT, float* vnT,
-                         float* h, float* vn, float* final_state, void* stream) {
+                         const float* KtT, const float* gam, const float* Qg,
+                         const float* Aqk, const float* initial_state, int32_t hT_every,
+                         float* hT, float* vnT, float* h, float* vn, float* read0,
+                         float* final_state, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_fwd")) return r;
-  if (!W || !U || !KtT || !gam || !hT || !final_state)
+  if (!W || !U || !KtT || !gam || !final_state || (read0 && (!Qg || !Aqk)))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_fwd: NULL tensor");
+  if (hT && hT_every < 1)
+    return fail(NGDN_EINVAL, "ngdn_l0_scan_fwd: hT_every must be >= 1, got %d", hT_every);
   const long long skv = (long long)d->K * d->V;
   ngdn::ScanArgs a{};
   a.A = W; a.BT = KtT; a.U = U; a.gam = gam;
   a.init = initial_state; a.init_sh = d->L * skv; a.init_sb = d->H * a.init_sh;
-  a.st_vk = hT; a.st_kv = h; a.state_mode = 0; a.NG = nchunks(d);
+  a.st_vk = hT; a.vk_every = hT_every; a.st_kv = h; a.state_mode = 0; a.NG = nchunks(d);
   a.vnT = vnT; a.vn = vn;
+  a.Qg = Qg; a.Aqk = Aqk; a.read0 = read0; a.T = d->T;
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");

@@ -57,10 +57,14 @@ struct ScanArgs {
   const float* A; const float* BT; const float* U; const float* gam;
   const float* init; long long init_sb, init_sh;
   float* st_kv; float* st_vk; int state_mode; int NG;
+  int vk_every;       // st_vk written at steps j with j % vk_every == 0 (<= 1: every step)
   float* vnT; float* vn;
   float* fin; long long fin_sb, fin_sh;
   int B, H, S, M, V;
   FireGate gate;
+  // level 0 with read0 set: the chunk's level-0 read Qg S + Aqk Vn (Qg
+  // [B*H,S,64,K], Aqk [B*H,S,64,64], fp32) into read0 [B,T,H,V] fp32
+  const float* Qg; const float* Aqk; float* read0; int T;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 

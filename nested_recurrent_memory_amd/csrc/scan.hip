@@ -26,7 +26,12 @@
 
 namespace ngdn {
 
-template <typename E, int K, int M, int BV, int NWV>
+// OUT (level 0): each step also forms the chunk's level-0 read
+//   read0 = Qg S + Aqk Vn
+// on the same tiles as Vn, with S^T and Vn^T already in LDS as the B
+// operands (the state is on chip, so the output pass needs neither the state
+// sequence nor Vn from HBM).
+template <typename E, int K, int M, int BV, int NWV, bool OUT>
 __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
@@ -84,11 +89,14 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
 
   // Operands of one step, read a step ahead: they do not depend on the state.
   typedef typename Mma<E>::SFrag SF;
+  constexpr int RA = OUT ? NAR : 1, RQ = OUT ? NSK : 1, RP = OUT ? NSM : 1;
   struct Ops {
     SF a[NAR][NSK];             // A rows of this wave's Vn tiles
     float u[NVP][4];            // U at the Vn tiles
     SF bt[TRT][NSM];            // BT rows of this wave's state tiles
     float g[TRT][4];            // gam at the state rows
+    float qg[RA][RQ][KPL];      // OUT: Qg rows of this wave's tiles, fp32 (split at use)
+    float aq[RA][RP][KPL];      // OUT: Aqk rows
   };
   // p-th Vn tile of this wave: valid, row tile, column tile, A row set
   auto vn_tile = [&](int p, int& rt, int& ct) -> bool {
@@ -115,6 +123,15 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
           const int arow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSK; ++s) o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(arow + s * KS);
+          if constexpr (OUT) {
+            const float* Qj = a.Qg + ((size_t)bh * S + j) * M * K + arow;
+            const float* Pj = a.Aqk + ((size_t)bh * S + j) * M * M + (rt * 16 + (lane & 15)) * M +
+                              kofs<E>(lane);
+#pragma unroll
+            for (int s = 0; s < NSK; ++s) ld_raw<KPL>(Qj + s * KS, o.qg[ONE_RT ? 0 : p / CT][s]);
+#pragma unroll
+            for (int s = 0; s < NSM; ++s) ld_raw<KPL>(Pj + s * KS, o.aq[ONE_RT ? 0 : p / CT][s]);
+          }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -140,7 +157,8 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
       const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col(), v = v0 + vl;
-      if (a.st_vk) *reinterpret_cast<f4*>(a.st_vk + base + (size_t)v * K + k0) = st[i];
+      if (a.st_vk && (a.vk_every <= 1 || j % a.vk_every == 0))
+        *reinterpret_cast<f4*>(a.st_vk + base + (size_t)v * K + k0) = st[i];
       if (a.st_kv) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) a.st_kv[base + (size_t)(k0 + r) * V + v] = st[i][r];
@@ -164,16 +182,24 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     }
     lds_barrier();
 
-    // ---- Vn = U - A S
+    // ---- Vn = U - A S (and, OUT, the read's Qg S on the same tiles)
+    f4 rd[OUT ? NVP : 1];
 #pragma unroll
     for (int p = 0; p < NVP; ++p) {
       int rt, ct;
       if (vn_tile(p, rt, ct)) {
         f4 acc = f4_zero();
+        if constexpr (OUT) rd[p] = f4_zero();
         const int brow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < NSK; ++s)
-          acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], sST.get(brow + s * KS));
+        for (int s = 0; s < NSK; ++s) {
+          const auto fb = sST.get(brow + s * KS);
+          acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], fb);
+          if constexpr (OUT) {
+            const float* x = cur.qg[ONE_RT ? 0 : p / CT][s];
+            rd[p] = Mma<E>::mma(rd[p], Mma<E>::makes([&](int e) { return x[e]; }), fb);
+          }
+        }
         const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
         f4 vn;
 #pragma unroll
@@ -189,6 +215,28 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
       }
     }
     lds_barrier();
+
+    // ---- OUT: read0 = Qg S + Aqk Vn for the chunk's rows in the sequence
+    if constexpr (OUT) {
+#pragma unroll
+      for (int p = 0; p < NVP; ++p) {
+        int rt, ct;
+        if (vn_tile(p, rt, ct)) {
+          const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+#pragma unroll
+          for (int s = 0; s < NSM; ++s) {
+            const float* x = cur.aq[ONE_RT ? 0 : p / CT][s];
+            rd[p] = Mma<E>::mma(rd[p], Mma<E>::makes([&](int e) { return x[e]; }), sVn.get(brow + s * KS));
+          }
+          const int vl = ct * 16 + acc_col();
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = j * M + rt * 16 + acc_row(r);
+            if (t < a.T) a.read0[(((size_t)b * a.T + t) * H + h) * V + v0 + vl] = rd[p][r];
+          }
+        }
+      }
+    }
 
     // ---- S <- diag(gam) S + BT Vn
 #pragma unroll
@@ -234,8 +282,15 @@ template <typename E, int K, int M>
 static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   constexpr int NWV = scan_waves<K>();
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
-  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV>), dim3(grid), dim3(NWV * WAVE), 0,
-                     st, a);
+  if constexpr (M == CH) {
+    if (a.read0) {
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true>), dim3(grid),
+                         dim3(NWV * WAVE), 0, st, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false>), dim3(grid), dim3(NWV * WAVE),
+                     0, st, a);
   return hipGetLastError();
 }
 

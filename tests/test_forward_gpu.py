@@ -269,11 +269,10 @@ def test_fused_promotion_matches_two_launch_path(dtype, K, L, N, firing, promoti
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_two_pass_output_equals_one_pass(dtype):
-    """With the fused promotion ladder the output runs in two passes
-    (ngdn_output_l0_fwd beside the ladder, then ngdn_output_upper_fwd); with
-    two stream groups it runs in one (ngdn_output_fwd). Same arithmetic:
-    equal bit for bit."""
+def test_two_row_groups_equal_one(dtype):
+    """The batch rows launched in two groups on two streams give the one-group
+    result bit for bit (every kernel's arithmetic per (batch, head) is the
+    same)."""
     from nested_recurrent_memory_amd import chunk as chunk_mod
     inp = make_inputs(B=2, T=700, H=2, K=128, V=128, L=3, N=64, intervals=(1, 2, 4),
                       dtype=dtype, g_scale=0.5)
@@ -289,3 +288,57 @@ def test_two_pass_output_equals_one_pass(dtype):
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0])
     assert torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("L", [1, 3])
+def test_output_entry_points_agree(dtype, L):
+    """The op forms level 0's read inside the level-0 scan and adds the upper
+    levels' in ngdn_output_upper_fwd. The stand-alone output kernels
+    (ngdn_output_fwd, and ngdn_output_l0_fwd + ngdn_output_upper_fwd) read the
+    chunk states and Vn from HBM instead: called through the C ABI on the
+    op's own working tensors they give the op's o within the bar."""
+    from nested_recurrent_memory_amd import chunk as chunk_mod
+    B, T, H, K = 2, 320, 2, 64
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=K, L=L, N=16, intervals=(1, 2, 4)[:L],
+                      dtype=dtype, g_scale=0.5)
+    g = _gpu(inp)
+    leaves = {n: g[n] for n in NAMES}
+    wd, code = chunk_mod._working_dtype(g["q"])
+    f = (1, 2, 4)[:L]
+    nq = [16] * (L - 1)
+    with torch.no_grad():
+        o, _ = chunk_nested_gdn2(**leaves, L=L, output_final_state=True)
+        # the forward's working tensors, with every chunk's state and Vn^T stored
+        q_, k_, v_, b_, w_, mix_ = (leaves[n].to(wd).contiguous() for n in
+                                    ("q", "k", "v", "b", "w", "mix_weights"))
+        g_ = leaves["g"].float().contiguous()
+        NT = -(-T // 64)
+        e = lambda *sh: torch.empty(*sh, device="cuda", dtype=torch.float32)  # noqa: E731
+        W, U, KtT, Qg, Aqk, gam = (e(B, H, NT, 64, K), e(B, H, NT, 64, K), e(B, H, NT, K, 64),
+                                   e(B, H, NT, 64, K), e(B, H, NT, 64, 64), e(B, H, NT, K))
+        hT, vnT, read0 = e(B, H, NT, K, K), e(B, H, NT, K, 64), e(B, T, H, K)
+        final = e(B, H, L, K, K)
+        d = _lib.dims(B, T, H, L, K, K, code, K ** -0.5)
+        P = _lib.ptr
+        st = _lib.stream_of(q_)
+        _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(x) for x in (
+            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam)), None, None, None, None, None, st)
+        _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(x) for x in (W, U, KtT, gam, None, None,
+                  None)), 1, P(hT), P(vnT), None, None, None, P(final), st)
+        # upper levels' group states: from the op's own path (states of levels >= 1)
+        saved = chunk_mod._forward(*(leaves[n] for n in NAMES[:12]), nq, list(f), L,
+                                   K ** -0.5, None, "learned", True)[2]
+        statesT = saved["statesT"]
+        spT, ngs, fs = chunk_mod._level_arrays(statesT, NT, list(f), L)
+        o1 = torch.empty_like(o)
+        _lib.call("ngdn_output_fwd", ctypes.byref(d), *(P(x) for x in (Qg, Aqk, hT, vnT, q_, mix_)),
+                  spT, ngs, fs, P(o1), None, st)
+        _lib.call("ngdn_output_l0_fwd", ctypes.byref(d), *(P(x) for x in (Qg, Aqk, hT, vnT, read0)), st)
+        o2 = torch.empty_like(o)
+        _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(read0), P(q_), P(mix_), spT, ngs, fs,
+                  P(o2), st)
+    torch.cuda.synchronize()
+    tol = TOL[dtype]
+    torch.testing.assert_close(o1.float(), o.float(), **tol)
+    torch.testing.assert_close(o2.float(), o.float(), **tol)
