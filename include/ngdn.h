@@ -62,8 +62,8 @@ const char* ngdn_arch(void);
  * Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64] and
  * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
  * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
- * may be NULL (inference). W, KtT, Kt, WT, QgT and AqkT are split; U, Qg, Aqk,
- * gam and TT fp32. */
+ * may be NULL (inference). W, KtT, Qg, Aqk, Kt, WT, QgT and AqkT are split;
+ * U, gam and TT fp32. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,

@@ -130,15 +130,15 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 
 // Per-row outputs written while the chunk's rows are in registers (forward
 // only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
-// row-major [64][K] and transposed [K][64]. Qg is fp32; Kt, Kt^T and Qg^T
-// (matrix-core operands of the scans only) are written in split form.
+// row-major [64][K] and transposed [K][64], all four in split form (they
+// enter the matrix cores only).
 struct RowOut {
   float* Qg; float* QgT; float* Kt; float* KtT;
 };
 
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
-// Aqk (lower incl. diagonal) to global fp32 [64][64]; when aqkT_out != null
-// also its transpose, in split form. Wave w computes block-row w. With
+// Aqk (lower incl. diagonal) to global [64][64]; when aqkT_out != null also
+// its transpose; both in split form. Wave w computes block-row w. With
 // per-row outputs, s_x is LDS scratch of 64 x (64 + 4) floats for the
 // transposed ones, and the call ends with a barrier.
 template <typename E, int K, int V>
@@ -247,14 +247,14 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       const int i = r + acc_row(rr), j = 16 * J + acc_col();
       s_A[i * AT_LD + j] = (j < i) ? accAs[J][rr] : 0.f;
       qt[rr] = (j <= i) ? accQs[J][rr] : 0.f;
-      if (aqk_out) aqk_out[i * CH + j] = qt[rr];
+      if (aqk_out) split_at<E>(aqk_out, CH * CH).put1(i * CH + j, qt[rr]);
     }
     if (aqkT_out) split_at<E>(aqkT_out, CH * CH).put4((16 * J + acc_col()) * CH + r + acc_row(0), qt);
   }
   if (ro.Qg) {
-    // Kt (split) and Kt^T (split), then Qg (fp32) and Qg^T (split): each
-    // value computed once into the LDS scratch s_x [64 columns][CH + 4],
-    // then written from there row-major and transposed, 16-byte rows both
+    // Kt and Kt^T, then Qg and Qg^T (split): each value computed once into
+    // the LDS scratch s_x [64 columns][CH + 4], then written from there
+    // row-major and transposed, 16-byte rows both
     constexpr int LDX = CH + 4;
     for (int which = 0; which < 2; ++which) {
       float* tp = which ? ro.QgT : ro.KtT;
@@ -286,8 +286,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
             f4 x;
 #pragma unroll
             for (int j = 0; j < 4; ++j) x[j] = s_x[(kl + j) * LDX + m];
-            if (which) *reinterpret_cast<f4*>(rp + m * K + 64 * hh + kl) = x;   // Qg: fp32
-            else rdst.put4(m * K + 64 * hh + kl, x);
+            rdst.put4(m * K + 64 * hh + kl, x);
           }
         }
         lds_barrier();

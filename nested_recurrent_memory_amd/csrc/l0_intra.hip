@@ -15,8 +15,9 @@
 // The forward consumes W, U, Kt^T, Qg, Aqk; the reverse scan consumes the
 // transposed copies Kt, W^T, Qg^T, Aqk^T, written when their pointers are set.
 // For bf16 inputs the products run on bf16 MFMA with the derived operands
-// split in two (ngdn_common.h); the scans' operands W, Kt^T, Kt, W^T, Qg^T and
-// Aqk^T are stored split (split_at), U, Qg, Aqk, gam and T^T as fp32.
+// split in two (ngdn_common.h); the matrix-core operands W, Kt^T, Qg, Aqk and
+// the copies Kt, W^T, Qg^T, Aqk^T are stored split (split_at), U, gam and T^T
+// as fp32.
 //
 // One workgroup (4 waves) per (batch, head, chunk). Decay products are formed
 // without overflow: inside block-row I (16 rows starting at r = 16 I) every

@@ -45,15 +45,15 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   for (int c = 0; c < CTV; ++c) out[c] = f4_zero();
   f4 acc[CTV];
 
-  // One stage: this wave's A fragments (NKA k-steps from global: fp32
-  // derived rows split, or exact input rows) are read first, so their loads
+  // One stage: this wave's A fragments (NKA k-steps from global, afrag(s):
+  // split derived rows or exact input rows) are read first, so their loads
   // overlap the staging of the B operand; then acc[c] += A s_B[c-th 16 rows]^T.
-  auto stage = [&](const auto* arow, auto nka_c, const float* bsrc, int bsrc_ld, auto bcols_c, int ldb) {
+  auto stage = [&](auto afrag, auto nka_c, const float* bsrc, int bsrc_ld, auto bcols_c, int ldb) {
     constexpr int NKA = decltype(nka_c)::value;
-    using FA = decltype(Mma<E>::ld(arow));
+    using FA = decltype(afrag(0));
     FA fa[NKA];
 #pragma unroll
-    for (int s = 0; s < NKA; ++s) fa[s] = Mma<E>::ld(arow + s * KS);
+    for (int s = 0; s < NKA; ++s) fa[s] = afrag(s);
     stage_split<256, V, decltype(bcols_c)::value>(sB, ldb, bsrc, bsrc_ld);
     lds_barrier();
 #pragma unroll
@@ -86,11 +86,15 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   } else {
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
+    const SplitTile<E> Qg = split_at<E>(a.Qg + cix * C * K, C * K);
+    const SplitTile<E> Aqk = split_at<E>(a.Aqk + cix * C * C, C * C);
     for (int kb = 0; kb < K; kb += KH)
-      stage(a.Qg + cix * C * K + (size_t)ri * K + kb + kofs<E>(lane), std::integral_constant<int, KH / KS>{},
-            a.hT + cix * V * K + kb, K, std::integral_constant<int, KH>{}, LD);
-    stage(a.Aqk + cix * C * C + (size_t)ri * C + kofs<E>(lane), std::integral_constant<int, C / KS>{},
-          a.vnT + cix * V * C, C, std::integral_constant<int, C>{}, LDC);
+      stage([&](int s) { return Qg.get(ri * K + kb + kofs<E>(lane) + s * KS); },
+            std::integral_constant<int, KH / KS>{}, a.hT + cix * V * K + kb, K,
+            std::integral_constant<int, KH>{}, LD);
+    stage([&](int s) { return Aqk.get(ri * C + kofs<E>(lane) + s * KS); },
+          std::integral_constant<int, C / KS>{}, a.vnT + cix * V * C, C,
+          std::integral_constant<int, C>{}, LDC);
   }
   if (a.l0_only) {   // level 0's read only: no mix, no upper levels, no o
 #pragma unroll
@@ -118,7 +122,8 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
     for (int kb = 0; kb < K; kb += KH)   // rows past the end repeat the last row
-      stage(qrow + (size_t)l * K + kb, std::integral_constant<int, KH / KS>{}, Sl + kb, K,
+      stage([&](int s) { return Mma<E>::ld(qrow + (size_t)l * K + kb + s * KS); },
+            std::integral_constant<int, KH / KS>{}, Sl + kb, K,
             std::integral_constant<int, KH>{}, LD);
     fold(l, a.scale);                           // which drops them
   }

@@ -95,8 +95,8 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     float u[NVP][4];            // U at the Vn tiles
     SF bt[TRT][NSM];            // BT rows of this wave's state tiles
     float g[TRT][4];            // gam at the state rows
-    float qg[RA][RQ][KPL];      // OUT: Qg rows of this wave's tiles, fp32 (split at use)
-    float aq[RA][RP][KPL];      // OUT: Aqk rows
+    SF qg[RA][RQ];              // OUT: Qg rows of this wave's tiles
+    SF aq[RA][RP];              // OUT: Aqk rows
   };
   // p-th Vn tile of this wave: valid, row tile, column tile, A row set
   auto vn_tile = [&](int p, int& rt, int& ct) -> bool {
@@ -124,13 +124,13 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
 #pragma unroll
           for (int s = 0; s < NSK; ++s) o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(arow + s * KS);
           if constexpr (OUT) {
-            const float* Qj = a.Qg + ((size_t)bh * S + j) * M * K + arow;
-            const float* Pj = a.Aqk + ((size_t)bh * S + j) * M * M + (rt * 16 + (lane & 15)) * M +
-                              kofs<E>(lane);
+            const SplitTile<E> Qj = split_at<E>(a.Qg + ((size_t)bh * S + j) * M * K, M * K);
+            const SplitTile<E> Pj = split_at<E>(a.Aqk + ((size_t)bh * S + j) * M * M, M * M);
+            const int prow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-            for (int s = 0; s < NSK; ++s) ld_raw<KPL>(Qj + s * KS, o.qg[ONE_RT ? 0 : p / CT][s]);
+            for (int s = 0; s < NSK; ++s) o.qg[ONE_RT ? 0 : p / CT][s] = Qj.get(arow + s * KS);
 #pragma unroll
-            for (int s = 0; s < NSM; ++s) ld_raw<KPL>(Pj + s * KS, o.aq[ONE_RT ? 0 : p / CT][s]);
+            for (int s = 0; s < NSM; ++s) o.aq[ONE_RT ? 0 : p / CT][s] = Pj.get(prow + s * KS);
           }
         }
 #pragma unroll
@@ -196,8 +196,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
           const auto fb = sST.get(brow + s * KS);
           acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], fb);
           if constexpr (OUT) {
-            const float* x = cur.qg[ONE_RT ? 0 : p / CT][s];
-            rd[p] = Mma<E>::mma(rd[p], Mma<E>::makes([&](int e) { return x[e]; }), fb);
+            rd[p] = Mma<E>::mma(rd[p], cur.qg[ONE_RT ? 0 : p / CT][s], fb);
           }
         }
         const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
@@ -225,8 +224,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
           const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSM; ++s) {
-            const float* x = cur.aq[ONE_RT ? 0 : p / CT][s];
-            rd[p] = Mma<E>::mma(rd[p], Mma<E>::makes([&](int e) { return x[e]; }), sVn.get(brow + s * KS));
+            rd[p] = Mma<E>::mma(rd[p], cur.aq[ONE_RT ? 0 : p / CT][s], sVn.get(brow + s * KS));
           }
           const int vl = ct * 16 + acc_col();
 #pragma unroll
@@ -274,8 +272,8 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   }
 }
 
-// Waves per workgroup: K = 128 spreads its 16 state tiles over 8 waves (two
-// per wave), halving each wave's dependent chain per step; K = 64 keeps 4.
+// Waves per workgroup: four, one per SIMD. Eight (two per SIMD) leave each
+// wave half the registers, less than a step's operands read ahead need.
 template <int K> constexpr int scan_waves() { return K == 128 ? SCAN_WAVES_128 : 4; }
 
 template <typename E, int K, int M>

@@ -20,22 +20,16 @@ TOL = {torch.float32: dict(rtol=1e-5, atol=1e-5),
        torch.bfloat16: dict(rtol=1e-2, atol=2e-3)}
 
 
-# working tensors the scans read as matrix-core operands: for bf16 inputs
-# each per-chunk tile [R][C] holds two bf16 planes (hi, then lo) in the bytes
-# of the fp32 tile
-SPLIT = ("W", "KtT", "Kt", "WT", "QgT", "AqkT")
+# working tensors read as matrix-core operands only: for bf16 inputs each
+# per-chunk tile [R][C] holds two bf16 planes (hi, then lo) in the bytes of
+# the fp32 tile
+SPLIT = ("W", "KtT", "Qg", "Aqk", "Kt", "WT", "QgT", "AqkT")
 
 
 def _unsplit(t):
     R, C = t.shape[-2:]
     planes = t.contiguous().view(torch.bfloat16).reshape(*t.shape[:-2], 2, R, C).float()
     return planes[..., 0, :, :] + planes[..., 1, :, :]
-
-
-def _split_round(x):
-    x = x.float()
-    hi = x.to(torch.bfloat16).float()
-    return (hi + (x - hi).to(torch.bfloat16).float()).to(x.dtype)
 
 
 def _gpu(inp):
@@ -94,16 +88,19 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     torch.testing.assert_close(got["W"], t["W"], **tol)
     torch.testing.assert_close(got["U"], t["U"], **tol)
     torch.testing.assert_close(got["TT"], t["T"].transpose(-1, -2), **tol)
-    # transposed copies are exact copies (of the split form where stored split)
-    split = (lambda x: _split_round(x)) if dtype == torch.bfloat16 else (lambda x: x)
+    # transposed copies are exact copies
     assert torch.equal(got["Kt"], got["KtT"].transpose(-1, -2))
     assert torch.equal(got["WT"], got["W"].transpose(-1, -2))
-    assert torch.equal(got["QgT"], split(got["Qg"]).transpose(-1, -2))
-    assert torch.equal(got["AqkT"], split(got["Aqk"]).transpose(-1, -2))
-    # the split form is hi = bf16(x), lo = bf16(x - hi), both round-to-nearest-even
+    assert torch.equal(got["QgT"], got["Qg"].transpose(-1, -2))
+    assert torch.equal(got["AqkT"], got["Aqk"].transpose(-1, -2))
+    # the split form is hi = bf16(x), lo = bf16(x - hi), both round-to-nearest-
+    # even: lo is at most half an ulp of hi
     if dtype == torch.bfloat16:
-        qg = split(out["Qg"].float().cpu())
-        assert (qg - out["Qg"].float().cpu()).abs().max() <= 2.0 ** -16 * out["Qg"].abs().max().cpu()
+        for n in SPLIT:
+            R, C = out[n].shape[-2:]
+            pl = out[n].contiguous().view(torch.bfloat16).reshape(*out[n].shape[:-2], 2, R, C)
+            hi, lo = pl[..., 0, :, :].float().cpu(), pl[..., 1, :, :].float().cpu()
+            assert (lo.abs() <= 2.0 ** -8 * hi.abs()).all(), n
 
 
 # ------------------------------------------------------------- whole forward
