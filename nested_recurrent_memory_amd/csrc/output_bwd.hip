@@ -14,18 +14,47 @@ namespace ngdn {
 
 template <typename E, int V>
 __global__ __launch_bounds__(256) void dmix0_kernel(Dmix0Args a) {
-  // one wave per 16 tokens of one head
+  // V / 8 lanes per (b, t, h) row, 8 consecutive values each (16-byte loads);
+  // a wave takes U passes of 64 / (V / 8) rows with every load in flight
+  // before the first dot product. Each row's sum: per lane in order, then a
+  // butterfly over its lanes.
+  constexpr int LPR = V / 8, RPW = WAVE / LPR, U = 4;
   const int lane = lane_id();
-  const size_t row0 = ((size_t)blockIdx.x * 4 + wave_id()) * 16;    // (b, t) * H + h rows
+  const int sub = lane / LPR, c = (lane % LPR) * 8;
   const size_t rows = (size_t)a.B * a.T * a.H;
+  const size_t base = ((size_t)blockIdx.x * 4 + wave_id()) * RPW * U;
   const E* dob = static_cast<const E*>(a.dout);
-  for (int q = 0; q < 16; ++q) {
-    const size_t r = row0 + q;
-    if (r >= rows) break;
+  float x[U][8], y[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t r = base + (size_t)u * RPW + sub;
+    if (r < rows) {
+      if constexpr (std::is_same<E, float>::value) {
+        const f4 x0 = *reinterpret_cast<const f4*>(dob + r * V + c);
+        const f4 x1 = *reinterpret_cast<const f4*>(dob + r * V + c + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[u][e] = x0[e]; x[u][e + 4] = x1[e]; }
+      } else {
+        ld_vals<E>(dob + r * V + c, x[u]);
+      }
+      const f4 y0 = *reinterpret_cast<const f4*>(a.read0 + r * V + c);
+      const f4 y1 = *reinterpret_cast<const f4*>(a.read0 + r * V + c + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { y[u][e] = y0[e]; y[u][e + 4] = y1[e]; }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[u][e] = y[u][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
     float s = 0.f;
-    for (int v = lane; v < V; v += WAVE) s += to_f(dob[r * V + v]) * a.read0[r * V + v];
-    s = wave_sum(s);
-    if (lane == 0) a.dmix[r * a.L] = s;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[u][e] * y[u][e];
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, WAVE);
+    const size_t r = base + (size_t)u * RPW + sub;
+    if (lane % LPR == 0 && r < rows) a.dmix[r * a.L] = s;
   }
 }
 
@@ -191,7 +220,8 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
 template <typename E, int V>
 static hipError_t launch_dmix0(const Dmix0Args& a, hipStream_t st) {
   const size_t rows = (size_t)a.B * a.T * a.H;
-  const unsigned grid = (unsigned)((rows + 63) / 64);
+  const size_t per = (size_t)4 * (WAVE / (V / 8)) * 4;   // rows per workgroup
+  const unsigned grid = (unsigned)((rows + per - 1) / per);
   hipLaunchKernelGGL((dmix0_kernel<E, V>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
