@@ -424,6 +424,22 @@ __device__ __forceinline__ float softplusf_(float x) {
   return fmaxf(x, 0.f) + l;
 }
 
+// Sum over each row of 16 lanes (lanes 16r .. 16r + 15), every lane of the
+// row receiving it: pairs, quads, halves, then the whole row, each step a DPP
+// move inside the row (no trip through the LDS crossbar). Every lane of a
+// row adds the same two partials, so all of them hold the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_row_mov<0xB1>(x);    // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp_row_mov<0x4E>(x);    // quad_perm [2,3,0,1]: lane ^ 2
+  x += dpp_row_mov<0x141>(x);   // row_half_mirror: lane i <-> 7 - i within 8
+  x += dpp_row_mov<0x140>(x);   // row_mirror: lane i <-> 15 - i
+  return x;
+}
+
 // Bounded per-block LDS reductions are written inline in the kernels; this is
 // the wave-level sum.
 __device__ __forceinline__ float wave_sum(float x) {

@@ -113,13 +113,14 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   const int rt = wv % 4, half = wv / 4;
   const int ri = rt * 16 + (lane & 15);          // this wave's rows of the chunk
   const int n1 = min((j + 1) * a.f, NT);
-  // The next chunk's rows are read into registers while this chunk computes
-  // (before its stores), then written to LDS at the top of the next iteration.
+  // The next chunk's rows (and the mix of its rows, kept raw until staging)
+  // are read into registers while this chunk computes, then written to LDS
+  // at the top of the next iteration.
   constexpr int QG = C * K / PE / NTH, DG = C * V / PE / NTH;   // 16-byte groups per thread
   static_assert(C * K / PE % NTH == 0 && C * V / PE % NTH == 0, "whole groups per thread");
   typedef E EV __attribute__((__vector_size__(16)));
   EV qv[QG], dv[DG];
-  float mv[DG];
+  E mv[DG], mrow;
   auto fetch = [&](int n) {
     const int t0 = n * C, nv = min(C, T - t0);
 #pragma unroll
@@ -131,34 +132,42 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
     for (int u = 0; u < DG; ++u) {
       const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
       dv[u] = i < nv ? *reinterpret_cast<const EV*>(db + (size_t)(t0 + i) * rowV + c) : EV{};
-      mv[u] = i < nv ? to_f(mb[(size_t)(t0 + i) * H * L]) : 0.f;
+      mv[u] = i < nv ? mb[(size_t)(t0 + i) * H * L] : E(0.f);
+    }
+    mrow = tid < nv ? mb[(size_t)(t0 + min(tid, C - 1)) * H * L] : E(0.f);
+  };
+  // The fetched rows of chunk n into LDS.
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < QG; ++u) {
+      const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+#pragma unroll
+      for (int x = 0; x < PE; ++x) s_qt[(c + x) * LDQT + i] = qv[u][x];
+    }
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
+      if constexpr (STAGE_DO) *reinterpret_cast<EV*>(s_do + i * LDD + c) = dv[u];
+      const float m = to_f(mv[u]);
+#pragma unroll
+      for (int x = 0; x < PE; ++x) sDT.put1((c + x) * LDDT + i, to_f(dv[u][x]) * m);
+    }
+    if (tid < C) {
+      s_mix[tid] = to_f(mrow);
+      s_dm[tid] = s_dm[C + tid] = 0.f;
     }
   };
-  if (j * a.f < n1) fetch(j * a.f);
-  for (int n = j * a.f; n < n1; ++n) {
-    const int t0 = n * C, nv = min(C, T - t0);
-    // ---- staging of the fetched rows
-    {
-#pragma unroll
-      for (int u = 0; u < QG; ++u) {
-        const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
-#pragma unroll
-        for (int x = 0; x < PE; ++x) s_qt[(c + x) * LDQT + i] = qv[u][x];
-      }
-#pragma unroll
-      for (int u = 0; u < DG; ++u) {
-        const int e = tid + NTH * u, i = e % C, c = (e / C) * PE;
-        if constexpr (STAGE_DO) *reinterpret_cast<EV*>(s_do + i * LDD + c) = dv[u];
-#pragma unroll
-        for (int x = 0; x < PE; ++x) sDT.put1((c + x) * LDDT + i, to_f(dv[u][x]) * mv[u]);
-      }
-      if (tid < C) {
-        s_mix[tid] = tid < nv ? to_f(mb[(size_t)(t0 + tid) * H * L]) : 0.f;
-        s_dm[tid] = s_dm[C + tid] = 0.f;
-      }
-    }
+  // One chunk, its rows already staged; the next chunk's rows are fetched
+  // at its start and staged at its end, so the loads and the stores in
+  // between are counted within one iteration. FULL (every chunk but a
+  // partial last one): the stores carry no row guards, so the compiler's
+  // wait before the staging covers the fetch only, not the stores after it.
+  auto chunk = [&](auto full_c, int n) {
+    constexpr bool FULL = decltype(full_c)::value;
+    const int t0 = n * C, nv = FULL ? C : min(C, T - t0);
+    const bool more = n + 1 < n1;
     lds_barrier();
-    if (n + 1 < n1) fetch(n + 1);
+    if (more) fetch(n + 1);
 
     // ---- P = do S^T on this wave's rows and half of K; dq and partial dmix
     {
@@ -184,12 +193,9 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         for (int x = 0; x < KTH; ++x) {
           const int k = (half * KTH + x) * 16 + acc_col();
           sm += to_f(s_qt[k * LDQT + i]) * pp[x][r];
-          if (i < nv) dqb[(size_t)(t0 + i) * rowQ + k] = from_f<E>(pp[x][r] * m);
+          if (FULL || i < nv) dqb[(size_t)(t0 + i) * rowQ + k] = from_f<E>(pp[x][r] * m);
         }
-        sm += __shfl_xor(sm, 1, WAVE);
-        sm += __shfl_xor(sm, 2, WAVE);
-        sm += __shfl_xor(sm, 4, WAVE);
-        sm += __shfl_xor(sm, 8, WAVE);
+        sm = row16_sum(sm);
         if ((lane & 15) == 0) s_dm[half * C + i] = sm;   // each slot has one writer
       }
     }
@@ -205,8 +211,17 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
       }
     }
     lds_barrier();
-    if (tid < nv) dmb[(size_t)(t0 + tid) * H * L] = (s_dm[tid] + s_dm[C + tid]) * a.scale;
+    // each thread reads its two dmix slots before its own staging clears them
+    if (FULL ? tid < C : tid < nv) dmb[(size_t)(t0 + tid) * H * L] = (s_dm[tid] + s_dm[C + tid]) * a.scale;
+    if (more) stage();
+  };
+  const int n_full = min(n1, T / C);   // chunks [j f, n_full) are whole
+  if (j * a.f < n1) {
+    fetch(j * a.f);
+    stage();
   }
+  for (int n = j * a.f; n < n_full; ++n) chunk(std::true_type{}, n);
+  for (int n = max(j * a.f, n_full); n < n1; ++n) chunk(std::false_type{}, n);
   float* out = a.d_states + (((size_t)b * NG + j) * H + h) * K * V;
 #pragma unroll
   for (int x = 0; x < NDS; ++x) {

@@ -162,10 +162,7 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float q = xu[r] * xu[r];
-          q += __shfl_xor(q, 1, WAVE);
-          q += __shfl_xor(q, 2, WAVE);
-          q += __shfl_xor(q, 4, WAVE);
-          q += __shfl_xor(q, 8, WAVE);
+          q = row16_sum(q);
           if (rl == 0) s_nrm[wv][rt * 16 + acc_row(r)] += q;
         }
       }

@@ -201,10 +201,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float q = u[t][r] * u[t][r];
-          q += __shfl_xor(q, 1, WAVE);
-          q += __shfl_xor(q, 2, WAVE);
-          q += __shfl_xor(q, 4, WAVE);
-          q += __shfl_xor(q, 8, WAVE);
+          q = row16_sum(q);
           if (rl == 0) s_nrm[ctw * N + rt * 16 + acc_row(r)] += q;
         }
       }
@@ -335,10 +332,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
         dxbt[t][r] = dbg * bb * (1.f - bb);
         if (!MERGE) {
           float rd = key * dkey;
-          rd += __shfl_xor(rd, 1, WAVE);
-          rd += __shfl_xor(rd, 2, WAVE);
-          rd += __shfl_xor(rd, 4, WAVE);
-          rd += __shfl_xor(rd, 8, WAVE);
+          rd = row16_sum(rd);
           if (rl == 0) s_rd[ctw * N + n] += rd;
         }
       }

@@ -325,10 +325,7 @@ __global__ __launch_bounds__(512) void promote_chain_kernel(PromoteChainArgs a) 
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float q = ut[t][r] * ut[t][r];
-            q += __shfl_xor(q, 1, WAVE);
-            q += __shfl_xor(q, 2, WAVE);
-            q += __shfl_xor(q, 4, WAVE);
-            q += __shfl_xor(q, 8, WAVE);
+            q = row16_sum(q);
             if (rl == 0) s_nrm[wv * N + rt * 16 + arow_(r)] += q;
           }
         }

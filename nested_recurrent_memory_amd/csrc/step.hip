@@ -303,10 +303,7 @@ __device__ __forceinline__ void promote_level(const PromoteArgs& a, char* smem, 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float q = xu[r] * xu[r];
-          q += __shfl_xor(q, 1, WAVE);
-          q += __shfl_xor(q, 2, WAVE);
-          q += __shfl_xor(q, 4, WAVE);
-          q += __shfl_xor(q, 8, WAVE);
+          q = row16_sum(q);
           if (rl == 0) s_nrm[wv * N + rt * 16 + acc_row(r)] += q;
         }
       }
