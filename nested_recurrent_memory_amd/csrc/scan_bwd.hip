@@ -101,13 +101,16 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 
   // Operands of one step, read a step ahead: they do not depend on the state gradient.
   typedef typename Mma<E>::SFrag SF;
+  typedef E DV __attribute__((__vector_size__(DOE * sizeof(E))));
   struct Ops {
     SF bop[RPW][NSK];           // Bop rows of this wave's dVn tiles
     SF aqk[RPW][NSM];           // Aqk^T rows (level 0)
     SF at[TRT][NSM];            // A^T rows of this wave's state tiles
     SF qg[TRT][NSM];            // Qg^T rows (level 0)
     float g[TRT][4];
-    float dov[DOE];             // mix_0 do at this thread's staging slots (level 0)
+    DV dor;                     // do at this thread's staging slots (level 0), raw
+    E dm;                       // and mix_0 of its token, raw: both are converted
+                                // when staged, so the load is not waited for here
     f4 add[TPW];                // injection (level 0) or read gradient (upper) of the step
     bool has_add;
   };
@@ -149,25 +152,11 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       // DOE consecutive columns of one token per thread: one vector load
       const int c = tid / (BV / DOE), vl = (tid % (BV / DOE)) * DOE, t = j * M + c;
       if (t < a.T) {
-        const E* src = dob + (size_t)t * H * V + v0 + vl;
-        const float m = to_f(mixb[(size_t)t * H * a.L]);
-        float x[DOE];
-        if constexpr (std::is_same<E, float>::value) {
-#pragma unroll
-          for (int q = 0; q < DOE; q += 4) {
-            const f4 y = *reinterpret_cast<const f4*>(src + q);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) x[q + u] = y[u];
-          }
-        } else {
-#pragma unroll
-          for (int q = 0; q < DOE; q += 8) ld_vals<E>(src + q, x + q);
-        }
-#pragma unroll
-        for (int q = 0; q < DOE; ++q) o.dov[q] = x[q] * m;
+        o.dor = *reinterpret_cast<const DV*>(dob + (size_t)t * H * V + v0 + vl);
+        o.dm = mixb[(size_t)t * H * a.L];
       } else {
-#pragma unroll
-        for (int q = 0; q < DOE; ++q) o.dov[q] = 0.f;
+        o.dor = DV{};
+        o.dm = E(0.f);
       }
     }
     // added before the step (level-0 injection) or after it (upper read gradient)
@@ -203,8 +192,9 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     }
     if (l0) {
       const int c = tid / (BV / DOE), vl = (tid % (BV / DOE)) * DOE;
+      const float m = to_f(cur.dm);
 #pragma unroll
-      for (int q = 0; q < DOE; ++q) sdO.put1((vl + q) * LDS_VN + c, cur.dov[q]);
+      for (int q = 0; q < DOE; ++q) sdO.put1((vl + q) * LDS_VN + c, to_f(cur.dor[q]) * m);
     }
     lds_barrier();
 
