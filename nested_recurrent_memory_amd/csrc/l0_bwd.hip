@@ -409,12 +409,23 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     for (int J = 0; J < 4; ++J) {
       f4 acc = f4_zero();
       if (J <= wv) {
-        const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
+        // the tile's W and U rows from global first, all in flight together
         const int wr = (J * 16 + (lane & 15)) * K + kofs<E>(lane);
+        const float* ur = Ug + (size_t)(J * 16 + (lane & 15)) * V + kofs<E>(lane);
+        typename Mma<E>::SFrag wf[K / KS];
+        float uf[V / KS][Mma<E>::KPL];
 #pragma unroll
-        for (int k0 = 0; k0 < K; k0 += KS)
-          acc = Mma<E>::mma(acc, Mma<E>::ld(xr + k0), Ws.get(wr + k0));
-        acc = mma_tile<E>(acc, s_dXu + wv * 16 * LXV, LXV, Ug + (size_t)J * 16 * V, V, V);
+        for (int s = 0; s < K / KS; ++s) wf[s] = Ws.get(wr + s * KS);
+#pragma unroll
+        for (int s = 0; s < V / KS; ++s) ld_raw<Mma<E>::KPL>(ur + s * KS, uf[s]);
+        const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, Mma<E>::ld(xr + s * KS), wf[s]);
+        const float* xu = s_dXu + (wv * 16 + (lane & 15)) * LXV + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < V / KS; ++s)
+          acc = Mma<E>::mma(acc, Mma<E>::ld(xu + s * KS),
+                            Mma<E>::makes([&](int e) { return uf[s][e]; }));
       }
       dat[J] = acc;
     }
@@ -434,24 +445,28 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     static_assert(C * V / VE % 256 == 0, "whole 16-byte groups per thread");
     E* dvo = static_cast<E*>(a.dv) + ((size_t)b * T * H + h) * V;
     E* dwo = static_cast<E*>(a.dw) + ((size_t)b * T * H + h) * V;
-    float wx[PER][VE], vx[PER][VE];
+    // raw until used, so no load waits where it is issued
+    typename ChunkIn<E, K, V>::R16 wr16[PER], vr16[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int e = tid + 256 * q, i = e / (V / VE), c = (e % (V / VE)) * VE;
-      in.vec16(in.w, in.rowV, i, c, wx[q]);
-      in.vec16(in.v, in.rowV, i, c, vx[q]);
+      wr16[q] = in.raw16(in.w, in.rowV, i, c);
+      vr16[q] = in.raw16(in.v, in.rowV, i, c);
     }
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int e = tid + 256 * q, i = e / (V / VE), c = (e % (V / VE)) * VE;
+      float wx[VE], vx[VE];
+      ChunkIn<E, K, V>::raw16_vals(wr16[q], wx);
+      ChunkIn<E, K, V>::raw16_vals(vr16[q], vx);
       if (i < nvalid) {
         typedef E EV __attribute__((__vector_size__(16)));
         EV dvv, dwv;
 #pragma unroll
         for (int j = 0; j < VE; ++j) {
           const float x = s_dXu[i * LXV + c + j];
-          dvv[j] = from_f<E>(x * wx[q][j]);
-          dwv[j] = from_f<E>(x * vx[q][j]);
+          dvv[j] = from_f<E>(x * wx[j]);
+          dwv[j] = from_f<E>(x * vx[j]);
         }
         *reinterpret_cast<EV*>(dvo + (size_t)(t0 + i) * H * V + c) = dvv;
         *reinterpret_cast<EV*>(dwo + (size_t)(t0 + i) * H * V + c) = dwv;

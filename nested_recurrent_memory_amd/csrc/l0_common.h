@@ -56,6 +56,26 @@ struct ChunkIn {
       for (int e = 0; e < VE; ++e) out[e] = 0.f;
     }
   }
+  // 16 bytes of row i from column c0, kept raw (zero past the end), and
+  // their VE values as floats: a load read ahead this way is not waited for
+  // until raw16_vals converts it.
+  typedef __attribute__((__vector_size__(16))) int R16;
+  __device__ __forceinline__ R16 raw16(const E* p, size_t row, int i, int c0) const {
+    R16 r = {0, 0, 0, 0};
+    if (i < nvalid) r = *reinterpret_cast<const R16*>(p + (size_t)(t0 + i) * row + c0);
+    return r;
+  }
+  __device__ __forceinline__ static void raw16_vals(R16 x, float* out) {
+    if constexpr (std::is_same<E, float>::value) {
+      const f4 v = __builtin_bit_cast(f4, x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = v[e];
+    } else {
+      const bf16x8 v = __builtin_bit_cast(bf16x8, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (float)v[e];
+    }
+  }
   // Mma<E>::KPL consecutive elements of row i from column c0 (zero past the end)
   __device__ __forceinline__ void vals(const E* p, size_t row, int i, int c0, float* out) const {
     if (i < nvalid) {

@@ -78,18 +78,20 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int VE = ChunkIn<E, K, V>::VE;      // elements per 16-byte load
   constexpr int PW = C * K / VE / 256, PU = C * V / VE / 256;
   static_assert(C * K / VE % 256 == 0 && C * V / VE % 256 == 0, "whole 16-byte groups per thread");
-  float rb[PW][VE], rk[PW][VE], rw[PU][VE], rv[PU][VE];
+  // (raw: converted only where they are used, so nothing waits for them here)
+  typedef typename ChunkIn<E, K, V>::R16 R16;
+  R16 rb[PW], rk[PW], rw[PU], rv[PU];
 #pragma unroll
   for (int q = 0; q < PW; ++q) {
     const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
-    in.vec16(in.b, in.rowK, m, c, rb[q]);
-    in.vec16(in.k, in.rowK, m, c, rk[q]);
+    rb[q] = in.raw16(in.b, in.rowK, m, c);
+    rk[q] = in.raw16(in.k, in.rowK, m, c);
   }
 #pragma unroll
   for (int q = 0; q < PU; ++q) {
     const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
-    in.vec16(in.w, in.rowV, m, c, rw[q]);
-    in.vec16(in.v, in.rowV, m, c, rv[q]);
+    rw[q] = in.raw16(in.w, in.rowV, m, c);
+    rv[q] = in.raw16(in.v, in.rowV, m, c);
   }
 
   // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
@@ -133,9 +135,12 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
       const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+      float xb[VE], xk[VE];
+      ChunkIn<E, K, V>::raw16_vals(rb[q], xb);
+      ChunkIn<E, K, V>::raw16_vals(rk[q], xk);
 #pragma unroll
       for (int j = 0; j < VE; ++j)
-        sX.put1((c + j) * LDX + m, rb[q][j] * rk[q][j] * fexp(s_gc[m * GL + c + j]));
+        sX.put1((c + j) * LDX + m, xb[j] * xk[j] * fexp(s_gc[m * GL + c + j]));
     }
     lds_barrier();
 #pragma unroll
@@ -152,8 +157,11 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
 #pragma unroll
     for (int q = 0; q < PU; ++q) {
       const int e = tid + 256 * q, m = e % C, c = (e / C) * VE;
+      float xw[VE], xv[VE];
+      ChunkIn<E, K, V>::raw16_vals(rw[q], xw);
+      ChunkIn<E, K, V>::raw16_vals(rv[q], xv);
 #pragma unroll
-      for (int j = 0; j < VE; ++j) sX.put1((c + j) * LDX + m, rw[q][j] * rv[q][j]);
+      for (int j = 0; j < VE; ++j) sX.put1((c + j) * LDX + m, xw[j] * xv[j]);
     }
     lds_barrier();
 #pragma unroll
