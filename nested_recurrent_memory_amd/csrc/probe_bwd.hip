@@ -122,13 +122,22 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
     const int v = ctw * 16 + rl;
-    SF fS[NKS];
+    // the state rows' loads first, all in flight, then their splits; each
+    // tile's bank rows likewise before its products
+    float xs[NKS][KPL];
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       const int k0 = s * KS + ko;
-      fS[s] = Svk ? Mma<E>::ld(Svk + (size_t)v * K + k0)
-                  : Mma<E>::makes([&](int e) { return Skv[(size_t)(k0 + e) * V + v]; });
+      if (Svk) {
+        ld_raw<KPL>(Svk + (size_t)v * K + k0, xs[s]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) xs[s][e] = Skv[(size_t)(k0 + e) * V + v];
+      }
     }
+    SF fS[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) fS[s] = Mma<E>::makes([&](int e) { return xs[s][e]; });
     f4 vt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -136,8 +145,11 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       int rt;
       if (!tile(t, rt)) continue;
       const E* arow = bank + (size_t)(rt * 16 + rl) * K + ko;
+      FR fb[NKS];   // the tile's bank rows, all in flight before its products
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fS[s]);
+      for (int s = 0; s < NKS; ++s) fb[s] = Mma<E>::ld(arow + s * KS);
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], fb[s], fS[s]);
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
