@@ -35,10 +35,19 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   const size_t cix = ((size_t)bh * NT + n);
   const int ri = wv * 16 + (lane & 15);      // A-operand row of this lane
 
-  const E* mixp = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L;
-  auto mixw = [&](int i, int l) -> float {
-    return i < nvalid ? to_f(mixp[(size_t)(t0 + i) * H * L + l]) : 0.f;
-  };
+  // the mix weights of this lane's four rows for every level, read up front
+  // and kept raw, so no level's fold waits for a load (none for a launch
+  // without mix weights: level 0's read alone)
+  const bool has_mix = a.mix != nullptr;
+  const E* mixp = has_mix ? static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L : nullptr;
+  E mraw[MAXL][4];
+#pragma unroll
+  for (int l = 0; l < MAXL; ++l)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = wv * 16 + acc_row(r);
+      mraw[l][r] = (has_mix && l < L && i < nvalid) ? mixp[(size_t)(t0 + i) * H * L + l] : E(0.f);
+    }
 
   f4 out[CTV];
 #pragma unroll
@@ -66,8 +75,11 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   auto fold = [&](int l, float sc) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = wv * 16 + acc_row(r);
-      const float m = mixw(i, l) * sc;
+      float mr = 0.f;
+#pragma unroll
+      for (int q = 0; q < MAXL; ++q)
+        if (q == l) mr = to_f(mraw[q][r]);
+      const float m = mr * sc;
 #pragma unroll
       for (int c = 0; c < CTV; ++c) out[c][r] += m * acc[c][r];
     }

@@ -74,13 +74,22 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
   if (!MERGE) {
     const E* bank = static_cast<const E*>(a.bank) + (size_t)h * a.Nmax * K;
     const int v = ctw * 16 + rl;
-    SF fS[NKS];
+    // the state rows' loads first, all in flight, then their splits; each
+    // tile's bank rows likewise before its products
+    float xs[NKS][KPL];
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       const int k0 = s * KS + ko;
-      fS[s] = Sh ? Mma<E>::ld(Sh + (size_t)v * K + k0)
-                 : Mma<E>::makes([&](int e) { return Sf[(size_t)(k0 + e) * V + v]; });
+      if (Sh) {
+        ld_raw<KPL>(Sh + (size_t)v * K + k0, xs[s]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) xs[s][e] = Sf[(size_t)(k0 + e) * V + v];
+      }
     }
+    SF fS[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) fS[s] = Mma<E>::makes([&](int e) { return xs[s][e]; });
     f4 vt[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -88,8 +97,11 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
       int rt;
       if (!tile(t, rt)) continue;
       const E* arow = bank + (size_t)(rt * 16 + rl) * K + ko;
+      typename Mma<E>::Frag fb[NKS];
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], Mma<E>::ld(arow + s * KS), fS[s]);
+      for (int s = 0; s < NKS; ++s) fb[s] = Mma<E>::ld(arow + s * KS);
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], fb[s], fS[s]);
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
