@@ -418,6 +418,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
         for (int s = 0; s < K / KS; ++s) wf[s] = Ws.get(wr + s * KS);
 #pragma unroll
         for (int s = 0; s < V / KS; ++s) ld_raw<Mma<E>::KPL>(ur + s * KS, uf[s]);
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the products
         const float* xr = s_dXw + (wv * 16 + (lane & 15)) * LXK + kofs<E>(lane);
 #pragma unroll
         for (int s = 0; s < K / KS; ++s) acc = Mma<E>::mma(acc, Mma<E>::ld(xr + s * KS), wf[s]);

@@ -38,16 +38,25 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   // the mix weights of this lane's four rows for every level, read up front
   // and kept raw, so no level's fold waits for a load (none for a launch
   // without mix weights: level 0's read alone)
-  const bool has_mix = a.mix != nullptr;
-  const E* mixp = has_mix ? static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L : nullptr;
+  // Rows past the sequence end and levels past L read the last valid ones
+  // (the loads carry no condition, so nothing waits for them here); fold
+  // drops those rows.
   E mraw[MAXL][4];
+  if (a.mix != nullptr) {
+    const E* mixp = static_cast<const E*>(a.mix) + ((size_t)b * T * H + h) * L;
 #pragma unroll
-  for (int l = 0; l < MAXL; ++l)
+    for (int l = 0; l < MAXL; ++l)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = wv * 16 + acc_row(r);
-      mraw[l][r] = (has_mix && l < L && i < nvalid) ? mixp[(size_t)(t0 + i) * H * L + l] : E(0.f);
-    }
+      for (int r = 0; r < 4; ++r) {
+        const int i = min(wv * 16 + acc_row(r), nvalid - 1), lc = min(l, L - 1);
+        mraw[l][r] = mixp[(size_t)(t0 + i) * H * L + lc];
+      }
+  } else {
+#pragma unroll
+    for (int l = 0; l < MAXL; ++l)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mraw[l][r] = E(0.f);
+  }
 
   f4 out[CTV];
 #pragma unroll
@@ -79,7 +88,7 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
 #pragma unroll
       for (int q = 0; q < MAXL; ++q)
         if (q == l) mr = to_f(mraw[q][r]);
-      const float m = mr * sc;
+      const float m = (wv * 16 + acc_row(r) < nvalid ? mr : 0.f) * sc;
 #pragma unroll
       for (int c = 0; c < CTV; ++c) out[c][r] += m * acc[c][r];
     }

@@ -135,6 +135,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
         for (int e = 0; e < KPL; ++e) xs[s][e] = Skv[(size_t)(k0 + e) * V + v];
       }
     }
+    __builtin_amdgcn_sched_barrier(0);   // the state loads stay ahead of their splits
     SF fS[NKS];
 #pragma unroll
     for (int s = 0; s < NKS; ++s) fS[s] = Mma<E>::makes([&](int e) { return xs[s][e]; });
@@ -148,6 +149,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       FR fb[NKS];   // the tile's bank rows, all in flight before its products
 #pragma unroll
       for (int s = 0; s < NKS; ++s) fb[s] = Mma<E>::ld(arow + s * KS);
+      __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the products
 #pragma unroll
       for (int s = 0; s < NKS; ++s) vt[t] = Mma<E>::mma(vt[t], fb[s], fS[s]);
     }
