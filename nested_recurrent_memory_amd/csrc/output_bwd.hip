@@ -89,6 +89,10 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
   __shared__ __attribute__((aligned(16))) typename ST::T s_dt[ST::NPLANE * V * LDDT];
   __shared__ __attribute__((aligned(16))) E s_do[STAGE_DO ? C * LDD : 4];
   __shared__ __attribute__((aligned(16))) E s_qt[K * LDQT];
+  // bf16: the chunk's dq rows gather here and leave as 16-byte rows (fp32
+  // stores them from the registers: its tiles leave no room)
+  constexpr int LDQ = K + PE;
+  __shared__ __attribute__((aligned(16))) E s_dq[STAGE_DO ? C * LDQ : 4];
   __shared__ float s_mix[C], s_dm[2 * C];   // dmix partials of the two halves of K
   const ST sS{s_s, K * LDS_}, sDT{s_dt, V * LDDT};
 
@@ -193,7 +197,8 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
         for (int x = 0; x < KTH; ++x) {
           const int k = (half * KTH + x) * 16 + acc_col();
           sm += to_f(s_qt[k * LDQT + i]) * pp[x][r];
-          if (FULL || i < nv) dqb[(size_t)(t0 + i) * rowQ + k] = from_f<E>(pp[x][r] * m);
+          if constexpr (STAGE_DO) s_dq[i * LDQ + k] = from_f<E>(pp[x][r] * m);
+          else if (FULL || i < nv) dqb[(size_t)(t0 + i) * rowQ + k] = from_f<E>(pp[x][r] * m);
         }
         sm = row16_sum(sm);
         if ((lane & 15) == 0) s_dm[half * C + i] = sm;   // each slot has one writer
@@ -213,6 +218,17 @@ __global__ __launch_bounds__(512) void read_state_bwd_kernel(ReadStateBwdArgs a)
     lds_barrier();
     // each thread reads its two dmix slots before its own staging clears them
     if (FULL ? tid < C : tid < nv) dmb[(size_t)(t0 + tid) * H * L] = (s_dm[tid] + s_dm[C + tid]) * a.scale;
+    if constexpr (STAGE_DO) {
+      constexpr int RG = K / PE;                 // 16-byte groups per dq row
+      static_assert(C * RG % NTH == 0, "whole groups per thread");
+#pragma unroll
+      for (int u = 0; u < C * RG / NTH; ++u) {
+        const int e = tid + NTH * u, i = e / RG, c = (e % RG) * PE;
+        if (FULL || i < nv)
+          *reinterpret_cast<EV*>(dqb + (size_t)(t0 + i) * rowQ + c) =
+              *reinterpret_cast<const EV*>(s_dq + i * LDQ + c);
+      }
+    }
     if (more) stage();
   };
   const int n_full = min(n1, T / C);   // chunks [j f, n_full) are whole
