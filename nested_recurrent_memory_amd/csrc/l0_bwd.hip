@@ -221,6 +221,9 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   constexpr int CPW = CTK / 4;                 // fused: column tiles of K per wave
   constexpr int NKV = V / KS;                  // k-steps over V
   f4 daq[4];                                   // fused: this wave's dAqk tiles
+  // fused: this wave's rows k of S as B fragments (8 consecutive v per lane),
+  // loaded in phase 1 and used again for dX_w in phase 2
+  SF fSk[FUSED ? CPW : 1][NKV];
   if constexpr (FUSED) {
     // ---- 1. the state half (what l0_bwd_state computes), from S = h, dS',
     // Vn, do and mix_0 of this chunk:
@@ -278,7 +281,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       const int ct = wv * CPW + c, kr = ct * 16 + (lane & 15);
-      SF fS[NKV], fD[NKV];
+      SF (&fS)[NKV] = fSk[c];
+      SF fD[NKV];
       float dgp = 0.f;
 #pragma unroll
       for (int s = 0; s < NKV; ++s) {
@@ -371,14 +375,12 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   lds_barrier();
   if constexpr (FUSED) {
     // dW = -dVn S^T, so dX_w = T^T dW = -(T^T dVn) S^T = -dX_u S^T: wave w
-    // owns its CPW column tiles (rows k of S) over every row of the chunk
-    const float* Sg = a.h + cix * K * V;
+    // owns its CPW column tiles (rows k of S) over every row of the chunk,
+    // the same rows it held as B fragments in phase 1 (kept, not re-read)
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
-      const int ct = wv * CPW + c, kr = ct * 16 + (lane & 15);
-      SF fS[NKV];
-#pragma unroll
-      for (int s = 0; s < NKV; ++s) fS[s] = Mma<E>::ld(Sg + (size_t)kr * V + s * KS + kofs<E>(lane));
+      const int ct = wv * CPW + c;
+      const SF (&fS)[NKV] = fSk[c];
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         f4 acc = f4_zero();
