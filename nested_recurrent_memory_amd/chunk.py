@@ -98,6 +98,12 @@ FUSED_PROMOTION = False
 # The level-0 chunk backward as one launch (ngdn_l0_bwd: the state half per
 # chunk in the same workgroup) or two (ngdn_l0_bwd_state, ngdn_l0_bwd_intra).
 FUSED_L0_BWD = True
+# dmix_0 (a bandwidth pass over do and the stored read) on the second side
+# stream: at the fork, beside the reads' backward (False), or after the
+# level-1 probe backward, beside the level-0 reverse scan (True: the reads'
+# backward, which the top level's probe backward waits for, then shares the
+# GPU with one kernel less; 6.14 -> 6.08 ms at c2)
+DMIX0_LATE = True
 
 
 def _chain_ok(K, N, merge):
@@ -376,9 +382,10 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         # (a) the reads' backward of the levels below the top one
         # (each writes its own columns of dmix and dq and its own d_states)
         # beside the top level's read and reverse scan, joined before the top
-        # level's probe backward adds into the level below's d_states; (b) dmix_0, then each
+        # level's probe backward adds into the level below's d_states; (b) each
         # level's parameter-gradient sums (reading only that level's
-        # workspaces) beside the rest of the chain, joined at the end. With
+        # workspaces) and dmix_0 (before level 1's sums, or at the fork when
+        # DMIX0_LATE is off) beside the rest of the chain, joined at the end. With
         # several groups of rows the sums run once over all rows after the
         # groups join, so every row group's partials are in place and the
         # result does not depend on the grouping.
@@ -390,10 +397,15 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         ta, tb = (aux[0], aux[1]) if aux else (st, st)
         sa, sb = _lib.ptr_of_stream(ta), _lib.ptr_of_stream(tb)
         # reads: dmix for every level (level 0 from the stored read, on the
-        # second side stream, which has nothing else to do until the first
-        # parameter-gradient sums), dq and the group-state gradients for levels >= 1
-        _lib.call("ngdn_output_bwd", ctypes.byref(d), P(R(sv["read0"])), P(R(do_)),
-                  P(R(dmix)), sb, stream=tb)
+        # second side stream), dq and the group-state gradients for levels >= 1
+        dmix0_done = []
+
+        def dmix0():
+            _lib.call("ngdn_output_bwd", ctypes.byref(d), P(R(sv["read0"])), P(R(do_)),
+                      P(R(dmix)), sb, stream=tb)
+            dmix0_done.append(True)
+        if not (DMIX0_LATE and aux is not None):
+            dmix0()
         for lvl in range(1, L):
             ng = n_groups(NT, f[lvl])
             top = lvl == L - 1
@@ -433,9 +445,14 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
             if nb == B:
                 if aux is not None:
                     aux[1].wait_stream(st)
+                if DMIX0_LATE and aux is not None and lvl == 1:
+                    dmix0()
                 param_grads(d, lvl, sb, tb)
         if not joined:
             st.wait_stream(aux[0])
+        if not dmix0_done:
+            # (late placement) after the upper levels' parameter-gradient sums
+            dmix0()
         # level 0
         _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
             "Kt", "WT", "gam", "AqkT", "QgT")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
