@@ -166,14 +166,51 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     }
   };
 
+  // Vn and (OUT) the read of a step are stored at the start of the next
+  // step, beside the state entering it and ahead of that step's operand
+  // loads: the vector memory pipe is in order, so stores issued after the
+  // loads would wait for them to drain and hold the wave up mid-step.
+  // (fp32 operands with K = 128 and M >= 64 keep the stores in place: the
+  // held Vn tiles would not fit in their registers)
+  constexpr bool DEFER = OUT || sizeof(E) == 2 || K < 128 || M < 64;
+  f4 pvn[NVP], prd[OUT ? NVP : 1];
+  auto flush_tile = [&](int jj, int p) {
+      int rt, ct;
+      if (vn_tile(p, rt, ct)) {
+        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+        if (a.vnT)
+          *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + jj) * V + v0 + vl) * M + m0) = pvn[p];
+        if (a.vn) {
+          float* vp = a.vn + ((size_t)bh * S + jj) * M * V + (size_t)m0 * V + v0 + vl;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = pvn[p][r];
+        }
+        if constexpr (OUT) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = jj * M + rt * 16 + acc_row(r);
+            if (t < a.T) a.read0[(((size_t)b * a.T + t) * H + h) * V + v0 + vl] = prd[p][r];
+          }
+        }
+      }
+  };
+  auto flush = [&](int jj) {
+#pragma unroll
+    for (int p = 0; p < NVP; ++p) flush_tile(jj, p);
+  };
+
   Ops nxt;
   if (S > 0) load(0, nxt);
   for (int j = 0; j < S; ++j) {
     const Ops cur = nxt;
+
+    // ---- state entering step j (and the previous step's Vn and read) to
+    // global, then the next step's operand loads
+    store_state(j);
+    if (DEFER && j > 0) flush(j - 1);
     if (j + 1 < S) load(j + 1, nxt);
 
-    // ---- state entering step j: to global and (transposed) to LDS
-    store_state(j);
+    // ---- the state, transposed, to LDS
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
@@ -204,13 +241,8 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][r] - acc[r];
         sVn.put4(vl * LDS_VN + m0, vn);
-        if (a.vnT)
-          *reinterpret_cast<f4*>(a.vnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = vn;
-        if (a.vn) {
-          float* vp = a.vn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) vp[(size_t)r * V] = vn[r];
-        }
+        pvn[p] = vn;
+        if constexpr (!DEFER) flush_tile(j, p);
       }
     }
     lds_barrier();
@@ -226,12 +258,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
           for (int s = 0; s < NSM; ++s) {
             rd[p] = Mma<E>::mma(rd[p], cur.aq[ONE_RT ? 0 : p / CT][s], sVn.get(brow + s * KS));
           }
-          const int vl = ct * 16 + acc_col();
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = j * M + rt * 16 + acc_row(r);
-            if (t < a.T) a.read0[(((size_t)b * a.T + t) * H + h) * V + v0 + vl] = rd[p][r];
-          }
+          prd[p] = rd[p];
         }
       }
     }
@@ -258,6 +285,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     // no barrier needed here: the next writes to s_st do not alias s_vn, and
     // the next writes to s_vn follow the next step's barrier
   }
+  if (DEFER && S > 0) flush(S - 1);
   if (a.state_mode == 1) {
     for (int j = S; j < a.NG; ++j) store_state(j);
   }
