@@ -170,17 +170,45 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     }
   };
 
+  // dVn of a step is stored at the start of the step after it, beside dS',
+  // ahead of that step's operand loads: the vector memory pipe is in order,
+  // so stores issued after the loads would wait for them to drain and hold
+  // the wave up mid-step. (M = K = 128 keeps the stores in place: its
+  // registers are already short.)
+  constexpr bool DEFER = !(K == 128 && M == 128);
+  f4 pdv[RPW][CT];
+  auto store_dv = [&](int jj, int p, int ct) {
+    const int rt = wv + 4 * p;
+    const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+    if (a.dVn) {
+      float* o = a.dVn + ((size_t)bh * S + jj) * M * V + (size_t)m0 * V + v0 + vl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[(size_t)r * V] = pdv[p][ct][r];
+    }
+    if (a.dVnT)
+      *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + jj) * V + v0 + vl) * M + m0) = pdv[p][ct];
+  };
+  auto flush_dv = [&](int jj) {
+#pragma unroll
+    for (int p = 0; p < RPW; ++p) {
+      if (wv + 4 * p < RTV) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) store_dv(jj, p, ct);
+      }
+    }
+  };
+
   Ops nxt;
   if (S > 0) load(S - 1, nxt);
   for (int j = S - 1; j >= 0; --j) {
     const Ops cur = nxt;
-    if (j > 0) load(j - 1, nxt);
     if (a.inj && cur.has_add) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
     }
 
-    // ---- store dS' and stage it (transposed) as the B operand of Bop dS'
+    // ---- dS' (and the previous step's dVn) to global, then the next step's
+    // operand loads
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
@@ -188,6 +216,15 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       float* o = a.dSp + ((size_t)bh * S + j) * K * V + (size_t)k0 * V + v0 + vl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[(size_t)r * V] = ds[i][r];
+    }
+    if (DEFER && j + 1 < S) flush_dv(j + 1);
+    if (j > 0) load(j - 1, nxt);
+
+    // ---- dS' staged (transposed) as the B operand of Bop dS'
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
       sdS.put4(vl * LDS_ST + k0, ds[i]);
     }
     if (l0) {
@@ -217,14 +254,9 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
               acc = Mma<E>::mma(acc, cur.aqk[p][s], sdO.get(orow + s * KS));
           }
           const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-          if (a.dVn) {
-            float* o = a.dVn + ((size_t)bh * S + j) * M * V + (size_t)m0 * V + v0 + vl;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[(size_t)r * V] = acc[r];
-          }
           sdV.put4(vl * LDS_VN + m0, acc);
-          if (a.dVnT)
-            *reinterpret_cast<f4*>(a.dVnT + (((size_t)bh * S + j) * V + v0 + vl) * M + m0) = acc;
+          pdv[p][ct] = acc;
+          if constexpr (!DEFER) store_dv(j, p, ct);
         }
       }
     }
@@ -260,6 +292,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     // s_dot and s_dvn are rewritten by the next step
     lds_barrier();
   }
+  if (DEFER && S > 0) flush_dv(0);
   if (a.dinit) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
