@@ -63,7 +63,12 @@ const char* ngdn_arch(void);
  * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
  * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
  * may be NULL (inference). W, KtT, Qg, Aqk, Kt, WT, QgT and AqkT are split;
- * U, gam and TT fp32. */
+ * U, gam and TT fp32. For bf16 inputs KtT, Kt, WT, QgT and AqkT (read only
+ * by the scans, as matrix-core A operands by row tile) are in fragment order:
+ * in each plane of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512
+ * consecutive elements at 512 (rb C/32 + cb), element (r, c) of the block at
+ * 8 (16 (c / 8) + r) + c % 8, so one operand fragment is one contiguous
+ * 1 KB read; W, Qg and Aqk stay row-major. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
@@ -79,7 +84,9 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
  * rows) and vn [B,H,NT,64,V], and read0 [B,T,H,V] fp32: level 0's read
  * Qg h + Aqk Vn of every token (Qg, Aqk from ngdn_l0_intra_fwd, required
  * with read0), formed while the state is on chip, which
- * ngdn_output_upper_fwd turns into o. initial_state may be NULL (zeros). */
+ * ngdn_output_upper_fwd turns into o. initial_state may be NULL (zeros).
+ * W, U, KtT, gam as ngdn_l0_intra_fwd writes them (bf16: KtT in fragment
+ * order). */
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam, const float* Qg,
                          const float* Aqk, const float* initial_state, int32_t hT_every,
@@ -202,7 +209,8 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
  * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (either may be NULL, not
  * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL.
- * Kt, WT, QgT and AqkT are read split. */
+ * Kt, WT, QgT and AqkT are read split (bf16: in fragment order, as
+ * ngdn_l0_intra_fwd writes them). */
 int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
                          const float* gam, const float* AqkT, const float* QgT,
                          const void* dout, const void* mix, int32_t f1,

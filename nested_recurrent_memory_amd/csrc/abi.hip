@@ -85,6 +85,7 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
   a.Qg = Qg; a.Aqk = Aqk; a.read0 = read0; a.T = d->T;
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
+  a.frag = d->dtype == NGDN_BF16;   // KtT from ngdn_l0_intra_fwd, fragment order
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");
 }
 
@@ -334,6 +335,7 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
   a.dSp = dSp; a.dVn = dVn; a.dVnT = dVnT;
   a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
+  a.frag = d->dtype == NGDN_BF16;   // Kt, WT, AqkT, QgT: fragment order
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
 }
 

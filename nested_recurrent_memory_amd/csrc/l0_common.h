@@ -150,8 +150,9 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 
 // Per-row outputs written while the chunk's rows are in registers (forward
 // only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
-// row-major [64][K] and transposed [K][64], all four in split form (they
-// enter the matrix cores only).
+// [64][K] and transposed [K][64], all four in split form (they enter the
+// matrix cores only); for bf16, Kt, Kt^T and Qg^T in fragment order, Qg
+// row-major.
 struct RowOut {
   float* Qg; float* QgT; float* Kt; float* KtT;
 };
@@ -172,6 +173,9 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   typedef typename Mma<E>::SFrag SF;
   const int lane = lane_id(), I = wave_id(), r = 16 * I;
   const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
+  // bf16: the copies only the scans read (Aqk^T, Kt^T, Qg^T, Kt) are written
+  // in fragment order
+  constexpr bool FRAG = std::is_same<E, bf16>::value;
   typedef typename Mma<E>::Frag FR;
   const int ri = r + (lane & 15);
   // Every global load of the phase first, all in flight together: this
@@ -269,7 +273,10 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       qt[rr] = (j <= i) ? accQs[J][rr] : 0.f;
       if (aqk_out) split_at<E>(aqk_out, CH * CH).put1(i * CH + j, qt[rr]);
     }
-    if (aqkT_out) split_at<E>(aqkT_out, CH * CH).put4((16 * J + acc_col()) * CH + r + acc_row(0), qt);
+    if (aqkT_out) {
+      const int tr = 16 * J + acc_col(), tc = r + acc_row(0);
+      split_at<E>(aqkT_out, CH * CH).put4(FRAG ? frag_ofs(tr, tc, CH) : tr * CH + tc, qt);
+    }
   }
   if (ro.Qg) {
     // Kt and Kt^T, then Qg and Qg^T (split): each value computed once into
@@ -295,18 +302,38 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
         }
         lds_barrier();
         if (tp) {
+          // rows 64 hh .. + 63 of the transposed copy: contiguous in either order
           for (int idx = threadIdx.x; idx < 64 * CH / 4; idx += blockDim.x) {
-            const int kl = idx / (CH / 4), m = (idx % (CH / 4)) * 4;
-            tdst.put4((64 * hh + kl) * CH + m, *reinterpret_cast<const f4*>(s_x + kl * LDX + m));
+            int kl, m;
+            if (FRAG) {
+              frag_pos(idx * 4, CH, kl, m);
+            } else {
+              kl = idx / (CH / 4);
+              m = (idx % (CH / 4)) * 4;
+            }
+            tdst.put4(64 * hh * CH + idx * 4, *reinterpret_cast<const f4*>(s_x + kl * LDX + m));
           }
         }
         if (rp) {
+          // Kt in fragment order (the reverse scan's), Qg row-major
+          const bool fr = FRAG && !which;
           for (int idx = threadIdx.x; idx < CH * 64 / 4; idx += blockDim.x) {
-            const int m = idx / 16, kl = (idx % 16) * 4;
+            int m, kl, off;
+            if (fr) {
+              // column blocks 2 hh, 2 hh + 1 of every row block
+              const int q = idx * 4, bl = q >> 9, w = q & 511, l = w >> 3;
+              m = (bl >> 1) * 16 + (l & 15);
+              kl = (bl & 1) * 32 + (l >> 4) * 8 + (w & 7);
+              off = ((bl >> 1) * (K / 32) + 2 * hh + (bl & 1)) * 512 + w;
+            } else {
+              m = idx / 16;
+              kl = (idx % 16) * 4;
+              off = m * K + 64 * hh + kl;
+            }
             f4 x;
 #pragma unroll
             for (int j = 0; j < 4; ++j) x[j] = s_x[(kl + j) * LDX + m];
-            rdst.put4(m * K + 64 * hh + kl, x);
+            rdst.put4(off, x);
           }
         }
         lds_barrier();

@@ -199,15 +199,22 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
       const int i = e / (V / 4), c = (e % (V / 4)) * 4;
       *reinterpret_cast<f4*>(Uo + i * V + c) = *reinterpret_cast<const f4*>(s_u + i * LUU + c);
     }
-    // W^T [K][C] (split): four consecutive rows of one column per thread
+    // W^T [K][C] (split; bf16: in fragment order, as the reverse scan reads
+    // it): four consecutive rows of one column per thread
     if (a.WT) {
       const SplitTile<E> WTo = split_at<E>(a.WT + cix * K * C, K * C);
       for (int e = tid; e < K * C / 4; e += 256) {
-        const int c = e / (C / 4), i = (e % (C / 4)) * 4;
+        int c, i;
+        if (std::is_same<E, bf16>::value) {
+          frag_pos(e * 4, C, c, i);
+        } else {
+          c = e / (C / 4);
+          i = (e % (C / 4)) * 4;
+        }
         f4 x;
 #pragma unroll
         for (int j = 0; j < 4; ++j) x[j] = s_w[(i + j) * LW + c];
-        WTo.put4(c * C + i, x);
+        WTo.put4(e * 4, x);
       }
     }
   }

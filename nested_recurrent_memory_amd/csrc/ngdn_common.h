@@ -199,6 +199,29 @@ __device__ __forceinline__ SplitTile<E> split_at(const float* unit, int plane) {
   return SplitTile<E>{reinterpret_cast<typename SplitTile<E>::T*>(const_cast<float*>(unit)), plane};
 }
 
+// Fragment order of a split bf16 tile [R][C] (R % 16 == 0, C % 32 == 0), for
+// tensors read only as MFMA A operands by row tile: each 16 x 32 block (row
+// block rb, column block cb) is 512 consecutive elements of a plane, at block
+// rb * C/32 + cb, and inside it lane l of a 16x16x32 operand fragment holds
+// row l % 16, columns 8 (l / 16) .. + 7 at element 8 l. The fragment of row
+// tile rt, k-step s is then one contiguous 1 KB read per plane (row-major, it
+// is 16 rows of 64 bytes).
+__device__ __forceinline__ int frag_ofs(int row, int col, int C) {
+  return ((row >> 4) * (C >> 5) + (col >> 5)) * 512 +
+         ((((col & 31) >> 3) << 4) + (row & 15)) * 8 + (col & 7);
+}
+// the element (row, col) at fragment-order position p of a [.][C] tile
+__device__ __forceinline__ void frag_pos(int p, int C, int& row, int& col) {
+  const int blk = p >> 9, w = p & 511, l = w >> 3;
+  row = (blk / (C >> 5)) * 16 + (l & 15);
+  col = (blk % (C >> 5)) * 32 + (l >> 4) * 8 + (w & 7);
+}
+// offset of the fragment of row tile rt, k-step s in a fragment-order tile
+// with rows of C elements
+__device__ __forceinline__ int frag_at(int rt, int s, int C) {
+  return (rt * (C >> 5) + s) * 512 + lane_id() * 8;
+}
+
 template <typename E> __device__ __forceinline__ int kofs(int lane) {
   return Mma<E>::KPL * (lane >> 4);
 }

@@ -65,6 +65,8 @@ struct ScanArgs {
   // level 0 with read0 set: the chunk's level-0 read Qg S + Aqk Vn (Qg
   // [B*H,S,64,K], Aqk [B*H,S,64,64], fp32) into read0 [B,T,H,V] fp32
   const float* Qg; const float* Aqk; float* read0; int T;
+  // bf16 level 0: BT (Kt^T from the chunk terms) in fragment order
+  int frag;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 
@@ -89,6 +91,8 @@ struct ScanBwdArgs {
   float* dVnT;
   float* dinit; long long di_sb, di_sh;
   int B, H, S, M, V;
+  // bf16 level 0: Bop, AT, AqkT and QgT (Kt, W^T, Aqk^T, Qg^T) in fragment order
+  int frag;
 };
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st);
 

@@ -31,7 +31,8 @@ namespace ngdn {
 // on the same tiles as Vn, with S^T and Vn^T already in LDS as the B
 // operands (the state is on chip, so the output pass needs neither the state
 // sequence nor Vn from HBM).
-template <typename E, int K, int M, int BV, int NWV, bool OUT>
+// FR (bf16, M = 64): BT in fragment order.
+template <typename E, int K, int M, int BV, int NWV, bool OUT, bool FR>
 __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
@@ -144,7 +145,9 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
       const int brow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s)
-        o.bt[t][s] = (!PADM || s * KS + kofs<E>(lane) < M) ? Bj.get(brow + s * KS) : Mma<E>::szero();
+        o.bt[t][s] = FR ? Bj.get(frag_at(rt, s, M))
+                        : (!PADM || s * KS + kofs<E>(lane) < M) ? Bj.get(brow + s * KS)
+                                                                : Mma<E>::szero();
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
     }
@@ -308,15 +311,28 @@ template <typename E, int K, int M>
 static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   constexpr int NWV = scan_waves<K>();
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
+  constexpr bool CAN_FR = M == CH && std::is_same<E, bf16>::value;
+  if (a.frag && !CAN_FR) return hipErrorInvalidValue;
+  if constexpr (CAN_FR) {
+    if (a.frag) {
+      if (a.read0)
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, true>), dim3(grid),
+                           dim3(NWV * WAVE), 0, st, a);
+      else
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, true>), dim3(grid),
+                           dim3(NWV * WAVE), 0, st, a);
+      return hipGetLastError();
+    }
+  }
   if constexpr (M == CH) {
     if (a.read0) {
-      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true>), dim3(grid),
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, false>), dim3(grid),
                          dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false>), dim3(grid), dim3(NWV * WAVE),
-                     0, st, a);
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, false>), dim3(grid),
+                     dim3(NWV * WAVE), 0, st, a);
   return hipGetLastError();
 }
 

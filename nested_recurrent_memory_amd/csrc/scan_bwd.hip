@@ -25,7 +25,8 @@
 
 namespace ngdn {
 
-template <typename E, int K, int M>
+// FR (bf16, M = 64): Bop, AT, AqkT and QgT in fragment order.
+template <typename E, int K, int M, bool FR>
 __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;
@@ -124,12 +125,12 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       if (rt < RTV) {
         const int brow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < NSK; ++s) o.bop[p][s] = Bj.get(brow + s * KS);
+        for (int s = 0; s < NSK; ++s) o.bop[p][s] = Bj.get(FR ? frag_at(rt, s, K) : brow + s * KS);
         if (l0) {
           const SplitTile<E> Qj = split_at<E>(a.AqkT + ((size_t)bh * S + j) * M * M, M * M);
           const int qrow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSM; ++s) o.aqk[p][s] = Qj.get(qrow + s * KS);
+          for (int s = 0; s < NSM; ++s) o.aqk[p][s] = Qj.get(FR ? frag_at(rt, s, M) : qrow + s * KS);
         }
       }
     }
@@ -139,11 +140,13 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       const int arow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s)
-        o.at[t][s] = (!PADM || s * KS + kofs<E>(lane) < M) ? Aj.get(arow + s * KS) : Mma<E>::szero();
+        o.at[t][s] = FR ? Aj.get(frag_at(rt, s, M))
+                        : (!PADM || s * KS + kofs<E>(lane) < M) ? Aj.get(arow + s * KS)
+                                                                : Mma<E>::szero();
       if (l0) {
         const SplitTile<E> QTj = split_at<E>(a.QgT + ((size_t)bh * S + j) * K * M, K * M);
 #pragma unroll
-        for (int s = 0; s < NSM; ++s) o.qg[t][s] = QTj.get(arow + s * KS);
+        for (int s = 0; s < NSM; ++s) o.qg[t][s] = QTj.get(FR ? frag_at(rt, s, M) : arow + s * KS);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
@@ -309,7 +312,12 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 template <typename E, int K, int M>
 static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
-  hipLaunchKernelGGL((scan_bwd_kernel<E, K, M>), dim3(grid), dim3(256), 0, st, a);
+  constexpr bool CAN_FR = M == CH && std::is_same<E, bf16>::value;
+  if (a.frag && !CAN_FR) return hipErrorInvalidValue;
+  if (CAN_FR && a.frag)
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN_FR>), dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, false>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -24,11 +24,25 @@ TOL = {torch.float32: dict(rtol=1e-5, atol=1e-5),
 # per-chunk tile [R][C] holds two bf16 planes (hi, then lo) in the bytes of
 # the fp32 tile
 SPLIT = ("W", "KtT", "Qg", "Aqk", "Kt", "WT", "QgT", "AqkT")
+# read by the scans only, and for bf16 stored in fragment order: per plane,
+# block (rb, cb) of 16 rows x 32 columns at 512 (rb C/32 + cb), element
+# (r, c) of the block at 8 (16 (c // 8) + r) + c % 8
+FRAG = ("KtT", "Kt", "WT", "QgT", "AqkT")
 
 
-def _unsplit(t):
+def _unfrag(p, R, C):
+    """[..., R*C] in fragment order -> [..., R, C] row-major."""
+    x = p.reshape(*p.shape[:-1], R // 16, C // 32, 4, 16, 8)
+    n = x.dim()
+    x = x.permute(*range(n - 5), n - 5, n - 2, n - 4, n - 3, n - 1)
+    return x.reshape(*p.shape[:-1], R, C)
+
+
+def _unsplit(t, frag=False):
     R, C = t.shape[-2:]
-    planes = t.contiguous().view(torch.bfloat16).reshape(*t.shape[:-2], 2, R, C).float()
+    planes = t.contiguous().view(torch.bfloat16).reshape(*t.shape[:-2], 2, R * C)
+    planes = _unfrag(planes, R, C) if frag else planes.reshape(*t.shape[:-2], 2, R, C)
+    planes = planes.float()
     return planes[..., 0, :, :] + planes[..., 1, :, :]
 
 
@@ -79,7 +93,7 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     t = ref.l0_chunk_terms(prep(inp["q"])[..., 0, :], prep(inp["k"]), prep(inp["v"]),
                            prep(inp["g"]), prep(inp["b"]), prep(inp["w"]), scale)
     tol = TOL[dtype]
-    got = {n: (_unsplit(out[n]) if dtype == torch.bfloat16 and n in SPLIT else out[n])
+    got = {n: (_unsplit(out[n], n in FRAG) if dtype == torch.bfloat16 and n in SPLIT else out[n])
            .double().cpu() for n in out}
     torch.testing.assert_close(got["gam"], t["gam"], rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(got["Aqk"], t["Aqk"], **tol)
