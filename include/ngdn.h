@@ -63,12 +63,12 @@ const char* ngdn_arch(void);
  * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
  * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
  * may be NULL (inference). W, KtT, Qg, Aqk, Kt, WT, QgT and AqkT are split;
- * U, gam and TT fp32. For bf16 inputs KtT, Kt, WT, QgT and AqkT (read only
- * by the scans, as matrix-core A operands by row tile) are in fragment order:
- * in each plane of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512
- * consecutive elements at 512 (rb C/32 + cb), element (r, c) of the block at
+ * U, gam and TT fp32. For bf16 inputs the split tensors (read only as
+ * matrix-core A operands by row tile) are in fragment order: in each plane
+ * of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512 consecutive
+ * elements at 512 (rb C/32 + cb), element (r, c) of the block at
  * 8 (16 (c / 8) + r) + c % 8, so one operand fragment is one contiguous
- * 1 KB read; W, Qg and Aqk stay row-major. */
+ * 1 KB read. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
@@ -85,8 +85,8 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
  * Qg h + Aqk Vn of every token (Qg, Aqk from ngdn_l0_intra_fwd, required
  * with read0), formed while the state is on chip, which
  * ngdn_output_upper_fwd turns into o. initial_state may be NULL (zeros).
- * W, U, KtT, gam as ngdn_l0_intra_fwd writes them (bf16: KtT in fragment
- * order). */
+ * W, U, KtT, gam, Qg, Aqk as ngdn_l0_intra_fwd writes them (bf16: the split
+ * ones in fragment order). */
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam, const float* Qg,
                          const float* Aqk, const float* initial_state, int32_t hT_every,

@@ -85,7 +85,7 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
   a.Qg = Qg; a.Aqk = Aqk; a.read0 = read0; a.T = d->T;
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
-  a.frag = d->dtype == NGDN_BF16;   // KtT from ngdn_l0_intra_fwd, fragment order
+  a.frag = d->dtype == NGDN_BF16;   // W, KtT, Qg, Aqk: fragment order
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");
 }
 

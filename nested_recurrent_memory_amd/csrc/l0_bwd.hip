@@ -405,7 +405,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
   f4 dat[4];
   {
-    const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);   // W in split form
+    // W in split form (bf16: fragment order)
+    const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);
     const float* Ug = a.U + cix * C * V;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
@@ -417,7 +418,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
         typename Mma<E>::SFrag wf[K / KS];
         float uf[V / KS][Mma<E>::KPL];
 #pragma unroll
-        for (int s = 0; s < K / KS; ++s) wf[s] = Ws.get(wr + s * KS);
+        for (int s = 0; s < K / KS; ++s)
+          wf[s] = Ws.get(std::is_same<E, bf16>::value ? frag_at(J, s, K) : wr + s * KS);
 #pragma unroll
         for (int s = 0; s < V / KS; ++s) ld_raw<Mma<E>::KPL>(ur + s * KS, uf[s]);
         __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the products

@@ -151,8 +151,8 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 // Per-row outputs written while the chunk's rows are in registers (forward
 // only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
 // [64][K] and transposed [K][64], all four in split form (they enter the
-// matrix cores only); for bf16, Kt, Kt^T and Qg^T in fragment order, Qg
-// row-major.
+// matrix cores only, as A operands by row tile), for bf16 in fragment
+// order.
 struct RowOut {
   float* Qg; float* QgT; float* Kt; float* KtT;
 };
@@ -173,8 +173,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   typedef typename Mma<E>::SFrag SF;
   const int lane = lane_id(), I = wave_id(), r = 16 * I;
   const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
-  // bf16: the copies only the scans read (Aqk^T, Kt^T, Qg^T, Kt) are written
-  // in fragment order
+  // bf16: every split output in fragment order
   constexpr bool FRAG = std::is_same<E, bf16>::value;
   typedef typename Mma<E>::Frag FR;
   const int ri = r + (lane & 15);
@@ -271,7 +270,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       const int i = r + acc_row(rr), j = 16 * J + acc_col();
       s_A[i * AT_LD + j] = (j < i) ? accAs[J][rr] : 0.f;
       qt[rr] = (j <= i) ? accQs[J][rr] : 0.f;
-      if (aqk_out) split_at<E>(aqk_out, CH * CH).put1(i * CH + j, qt[rr]);
+      if (aqk_out) split_at<E>(aqk_out, CH * CH).put1(FRAG ? frag_ofs(i, j, CH) : i * CH + j, qt[rr]);
     }
     if (aqkT_out) {
       const int tr = 16 * J + acc_col(), tc = r + acc_row(0);
@@ -315,8 +314,7 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
           }
         }
         if (rp) {
-          // Kt in fragment order (the reverse scan's), Qg row-major
-          const bool fr = FRAG && !which;
+          const bool fr = FRAG;
           for (int idx = threadIdx.x; idx < CH * 64 / 4; idx += blockDim.x) {
             int m, kl, off;
             if (fr) {

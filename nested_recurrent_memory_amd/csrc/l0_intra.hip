@@ -188,11 +188,18 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) s_u[(R0 + acc_row(r)) * LUU + t * 16 + acc_col()] = ut[t][r];
     lds_barrier();
-    // W [C][K] (split), U [C][V] (fp32): four consecutive columns per thread
+    // W [C][K] (split; bf16: in fragment order), U [C][V] (fp32): four
+    // consecutive columns per thread
     const SplitTile<E> Wo = split_at<E>(a.W + cix * C * K, C * K);
     for (int e = tid; e < C * K / 4; e += 256) {
-      const int i = e / (K / 4), c = (e % (K / 4)) * 4;
-      Wo.put4(i * K + c, *reinterpret_cast<const f4*>(s_w + i * LW + c));
+      int i, c;
+      if (std::is_same<E, bf16>::value) {
+        frag_pos(e * 4, K, i, c);
+      } else {
+        i = e / (K / 4);
+        c = (e % (K / 4)) * 4;
+      }
+      Wo.put4(e * 4, *reinterpret_cast<const f4*>(s_w + i * LW + c));
     }
     float* Uo = a.U + cix * C * V;
     for (int e = tid; e < C * V / 4; e += 256) {

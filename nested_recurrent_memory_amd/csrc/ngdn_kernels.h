@@ -65,7 +65,7 @@ struct ScanArgs {
   // level 0 with read0 set: the chunk's level-0 read Qg S + Aqk Vn (Qg
   // [B*H,S,64,K], Aqk [B*H,S,64,64], fp32) into read0 [B,T,H,V] fp32
   const float* Qg; const float* Aqk; float* read0; int T;
-  // bf16 level 0: BT (Kt^T from the chunk terms) in fragment order
+  // bf16 level 0: A, BT, Qg, Aqk (the chunk terms) in fragment order
   int frag;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);

@@ -107,13 +107,15 @@ __global__ __launch_bounds__(256) void output_fwd_kernel(OutputArgs a) {
   } else {
 #pragma unroll
     for (int c = 0; c < CTV; ++c) acc[c] = f4_zero();
+    // bf16: Qg and Aqk in fragment order, as the chunk terms write them
+    constexpr bool FR = std::is_same<E, bf16>::value;
     const SplitTile<E> Qg = split_at<E>(a.Qg + cix * C * K, C * K);
     const SplitTile<E> Aqk = split_at<E>(a.Aqk + cix * C * C, C * C);
     for (int kb = 0; kb < K; kb += KH)
-      stage([&](int s) { return Qg.get(ri * K + kb + kofs<E>(lane) + s * KS); },
+      stage([&](int s) { return Qg.get(FR ? frag_at(wv, kb / KS + s, K) : ri * K + kb + kofs<E>(lane) + s * KS); },
             std::integral_constant<int, KH / KS>{}, a.hT + cix * V * K + kb, K,
             std::integral_constant<int, KH>{}, LD);
-    stage([&](int s) { return Aqk.get(ri * C + kofs<E>(lane) + s * KS); },
+    stage([&](int s) { return Aqk.get(FR ? frag_at(wv, s, C) : ri * C + kofs<E>(lane) + s * KS); },
           std::integral_constant<int, C / KS>{}, a.vnT + cix * V * C, C,
           std::integral_constant<int, C>{}, LDC);
   }

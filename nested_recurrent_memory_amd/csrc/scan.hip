@@ -31,7 +31,7 @@ namespace ngdn {
 // on the same tiles as Vn, with S^T and Vn^T already in LDS as the B
 // operands (the state is on chip, so the output pass needs neither the state
 // sequence nor Vn from HBM).
-// FR (bf16, M = 64): BT in fragment order.
+// FR (bf16, M = 64): A, BT, Qg and Aqk in fragment order.
 template <typename E, int K, int M, int BV, int NWV, bool OUT, bool FR>
 __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
@@ -123,15 +123,18 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
         if (ONE_RT ? p == 0 : p % CT == 0) {
           const int arow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSK; ++s) o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(arow + s * KS);
+          for (int s = 0; s < NSK; ++s)
+            o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(FR ? frag_at(rt, s, K) : arow + s * KS);
           if constexpr (OUT) {
             const SplitTile<E> Qj = split_at<E>(a.Qg + ((size_t)bh * S + j) * M * K, M * K);
             const SplitTile<E> Pj = split_at<E>(a.Aqk + ((size_t)bh * S + j) * M * M, M * M);
             const int prow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-            for (int s = 0; s < NSK; ++s) o.qg[ONE_RT ? 0 : p / CT][s] = Qj.get(arow + s * KS);
+            for (int s = 0; s < NSK; ++s)
+              o.qg[ONE_RT ? 0 : p / CT][s] = Qj.get(FR ? frag_at(rt, s, K) : arow + s * KS);
 #pragma unroll
-            for (int s = 0; s < NSM; ++s) o.aq[ONE_RT ? 0 : p / CT][s] = Pj.get(prow + s * KS);
+            for (int s = 0; s < NSM; ++s)
+              o.aq[ONE_RT ? 0 : p / CT][s] = Pj.get(FR ? frag_at(rt, s, M) : prow + s * KS);
           }
         }
 #pragma unroll

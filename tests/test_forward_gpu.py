@@ -24,10 +24,10 @@ TOL = {torch.float32: dict(rtol=1e-5, atol=1e-5),
 # per-chunk tile [R][C] holds two bf16 planes (hi, then lo) in the bytes of
 # the fp32 tile
 SPLIT = ("W", "KtT", "Qg", "Aqk", "Kt", "WT", "QgT", "AqkT")
-# read by the scans only, and for bf16 stored in fragment order: per plane,
-# block (rb, cb) of 16 rows x 32 columns at 512 (rb C/32 + cb), element
-# (r, c) of the block at 8 (16 (c // 8) + r) + c % 8
-FRAG = ("KtT", "Kt", "WT", "QgT", "AqkT")
+# for bf16 every split tile is stored in fragment order: per plane, block
+# (rb, cb) of 16 rows x 32 columns at 512 (rb C/32 + cb), element (r, c) of
+# the block at 8 (16 (c // 8) + r) + c % 8
+FRAG = SPLIT
 
 
 def _unfrag(p, R, C):
