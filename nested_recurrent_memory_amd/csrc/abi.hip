@@ -85,7 +85,7 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
   a.Qg = Qg; a.Aqk = Aqk; a.read0 = read0; a.T = d->T;
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
-  a.frag = d->dtype == NGDN_BF16;   // W, KtT, Qg, Aqk: fragment order
+  a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // W, KtT, Qg, Aqk: fragment order
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");
 }
 
@@ -222,6 +222,7 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   a.vnT = nullptr; a.vn = nullptr;
   a.fin = final_state + (long long)level * skv; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nf; a.M = n_pairs; a.V = d->V;
+  a.frag = d->dtype == NGDN_BF16 && n_pairs % 32 == 0;   // KT as ngdn_probe_fwd writes it
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_fwd");
 }
 
@@ -335,7 +336,7 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
   a.dSp = dSp; a.dVn = dVn; a.dVnT = dVnT;
   a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
-  a.frag = d->dtype == NGDN_BF16;   // Kt, WT, AqkT, QgT: fragment order
+  a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // Kt, WT, AqkT, QgT: fragment order
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
 }
 
@@ -366,6 +367,7 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
   a.dinit = d_initial ? d_initial + (long long)level * skv : nullptr;
   a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = nf; a.M = n_pairs; a.V = d->V;
+  a.frag = d->dtype == NGDN_BF16 && n_pairs % 32 == 0;   // AT as the probes write it
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_upper_scan_bwd");
 }
 
@@ -674,6 +676,7 @@ int32_t step_run(const ngdn_dims* d, const void* q, const void* k, const void* v
       ca.state_mode = 0; ca.NG = 1;
       ca.fin = srow + (long long)l * skv; ca.fin_sh = ca.init_sh; ca.fin_sb = ca.init_sb;
       ca.B = nb; ca.H = d->H; ca.S = 1; ca.M = N; ca.V = V;
+      ca.frag = d->dtype == NGDN_BF16 && N % 32 == 0;   // KT as probe_fwd wrote it
       ca.gate = gate;
       if (int32_t r = launched(ngdn::scan_fwd(ca, d->dtype, K, st), what)) return r;
     }

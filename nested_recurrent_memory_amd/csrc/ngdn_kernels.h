@@ -65,7 +65,8 @@ struct ScanArgs {
   // level 0 with read0 set: the chunk's level-0 read Qg S + Aqk Vn (Qg
   // [B*H,S,64,K], Aqk [B*H,S,64,64], fp32) into read0 [B,T,H,V] fp32
   const float* Qg; const float* Aqk; float* read0; int T;
-  // bf16 level 0: A, BT, Qg, Aqk (the chunk terms) in fragment order
+  // bf16, fragment order as the chunk terms and the probes write them:
+  // 1, BT (M % 32 == 0); 3, also A, Qg, Aqk (level 0); 0, none
   int frag;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
@@ -91,7 +92,7 @@ struct ScanBwdArgs {
   float* dVnT;
   float* dinit; long long di_sb, di_sh;
   int B, H, S, M, V;
-  // bf16 level 0: Bop, AT, AqkT and QgT (Kt, W^T, Aqk^T, Qg^T) in fragment order
+  // bf16, fragment order: 1, AT (M % 32 == 0); 3, Bop, AT, AqkT, QgT (level 0)
   int frag;
 };
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st);

@@ -204,7 +204,9 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
     a.gam[fo * K + tid] = expf(g);
     if (a.go) a.go[ro * K + tid] = g;
   }
-  // the scan's operands in split form
+  // the scan's operands in split form (bf16 with N % 32 == 0: KT and AT in
+  // fragment order, where a put4 of 16 lanes is 512 contiguous bytes)
+  constexpr bool FRG = std::is_same<E, bf16>::value && N % 32 == 0;
   const SplitTile<E> Ao = split_at<E>(a.A + fo * N * K, N * K);
   const SplitTile<E> KTo = split_at<E>(a.KT + fo * K * N, K * N);
   const SplitTile<E> KNo = split_at<E>(a.keysN ? a.keysN + fo * N * K : nullptr, N * K);
@@ -236,8 +238,8 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
       if (a.keys) a.keys[ro * N * K + n * K + k] = key;
       if (a.bo) a.bo[ro * N * K + n * K + k] = bt[t][r];
     }
-    KTo.put4(k * N + n0, kv4);
-    if (a.AT) ATo.put4(k * N + n0, av4);
+    KTo.put4(FRG ? frag_ofs(k, n0, N) : k * N + n0, kv4);
+    if (a.AT) ATo.put4(FRG ? frag_ofs(k, n0, N) : k * N + n0, av4);
   }
 }
 

@@ -356,6 +356,8 @@ __global__ __launch_bounds__(512) void promote_chain_kernel(PromoteChainArgs a) 
     // ---- keys b and keys^T as split tiles, the backward's copies; S~ = e^g S
     // in registers and S~^T in LDS; the partial sums cleared for the next firing
     {
+      // (bf16 with N % 32 == 0: AT in fragment order, as the reverse scan reads it)
+      constexpr bool FRG = std::is_same<E, bf16>::value && N % 32 == 0;
       const SplitTile<E> KNo = split_at<E>(a.keysN ? a.keysN + fo * N * K : nullptr, N * K);
       const SplitTile<E> ATo = split_at<E>(a.AT ? a.AT + fo * K * N : nullptr, K * N);
       const int k = ctw * 16 + acol_();
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(512) void promote_chain_kernel(PromoteChainArgs a) 
           if (a.keysN) KNo.put1(n * K + k, key);
         }
         sKT.put4(k * LDKT + n0, kv4);
-        if (a.AT) ATo.put4(k * N + n0, av4);
+        if (a.AT) ATo.put4(FRG ? frag_ofs(k, n0, N) : k * N + n0, av4);
       }
     }
     for (int e = tid; e < NW * N; e += blockDim.x) s_nrm[e] = 0.f;

@@ -31,8 +31,9 @@ namespace ngdn {
 // on the same tiles as Vn, with S^T and Vn^T already in LDS as the B
 // operands (the state is on chip, so the output pass needs neither the state
 // sequence nor Vn from HBM).
-// FR (bf16, M = 64): A, BT, Qg and Aqk in fragment order.
-template <typename E, int K, int M, int BV, int NWV, bool OUT, bool FR>
+// FRM (bf16): bit 0, BT in fragment order (M % 32 == 0); bit 1, A (and, OUT,
+// Qg and Aqk) too.
+template <typename E, int K, int M, int BV, int NWV, bool OUT, int FRM>
 __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int CT = BV / 16;                 // column tiles
   constexpr int RTS = K / 16;                 // state row tiles
@@ -54,6 +55,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int NSK = K / KS;                 // k-steps over K
   constexpr int NSM = (M + KS - 1) / KS;      // k-steps over M
   constexpr bool PADM = (M % KS) != 0;
+  constexpr bool FRB = FRM & 1, FRA = FRM & 2;
   static_assert(TPW >= 1 && (TPW % CT == 0 || CT % TPW == 0),
                 "state tiles of a wave: whole rows, or a part of one row");
   static_assert(ONE_RT || RTV % NWV == 0, "Vn row tiles spread evenly over the waves");
@@ -124,17 +126,17 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
           const int arow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
           for (int s = 0; s < NSK; ++s)
-            o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(FR ? frag_at(rt, s, K) : arow + s * KS);
+            o.a[ONE_RT ? 0 : p / CT][s] = Aj.get(FRA ? frag_at(rt, s, K) : arow + s * KS);
           if constexpr (OUT) {
             const SplitTile<E> Qj = split_at<E>(a.Qg + ((size_t)bh * S + j) * M * K, M * K);
             const SplitTile<E> Pj = split_at<E>(a.Aqk + ((size_t)bh * S + j) * M * M, M * M);
             const int prow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
             for (int s = 0; s < NSK; ++s)
-              o.qg[ONE_RT ? 0 : p / CT][s] = Qj.get(FR ? frag_at(rt, s, K) : arow + s * KS);
+              o.qg[ONE_RT ? 0 : p / CT][s] = Qj.get(FRA ? frag_at(rt, s, K) : arow + s * KS);
 #pragma unroll
             for (int s = 0; s < NSM; ++s)
-              o.aq[ONE_RT ? 0 : p / CT][s] = Pj.get(FR ? frag_at(rt, s, M) : prow + s * KS);
+              o.aq[ONE_RT ? 0 : p / CT][s] = Pj.get(FRA ? frag_at(rt, s, M) : prow + s * KS);
           }
         }
 #pragma unroll
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
       const int brow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s)
-        o.bt[t][s] = FR ? Bj.get(frag_at(rt, s, M))
+        o.bt[t][s] = FRB ? Bj.get(frag_at(rt, s, M))
                         : (!PADM || s * KS + kofs<E>(lane) < M) ? Bj.get(brow + s * KS)
                                                                 : Mma<E>::szero();
 #pragma unroll
@@ -314,27 +316,35 @@ template <typename E, int K, int M>
 static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   constexpr int NWV = scan_waves<K>();
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
-  constexpr bool CAN_FR = M == CH && std::is_same<E, bf16>::value;
-  if (a.frag && !CAN_FR) return hipErrorInvalidValue;
-  if constexpr (CAN_FR) {
-    if (a.frag) {
+  constexpr bool BF = std::is_same<E, bf16>::value;
+  if (a.frag && !(BF && M % 32 == 0 && (a.frag == 1 || (a.frag == 3 && M == CH))))
+    return hipErrorInvalidValue;
+  if constexpr (BF && M == CH) {
+    if (a.frag == 3) {
       if (a.read0)
-        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, true>), dim3(grid),
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, 3>), dim3(grid),
                            dim3(NWV * WAVE), 0, st, a);
       else
-        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, true>), dim3(grid),
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 3>), dim3(grid),
                            dim3(NWV * WAVE), 0, st, a);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (BF && M % 32 == 0) {
+    if (a.frag == 1) {
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 1>), dim3(grid),
+                         dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
   if constexpr (M == CH) {
     if (a.read0) {
-      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, false>), dim3(grid),
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, 0>), dim3(grid),
                          dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, false>), dim3(grid),
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 0>), dim3(grid),
                      dim3(NWV * WAVE), 0, st, a);
   return hipGetLastError();
 }

@@ -25,8 +25,9 @@
 
 namespace ngdn {
 
-// FR (bf16, M = 64): Bop, AT, AqkT and QgT in fragment order.
-template <typename E, int K, int M, bool FR>
+// FRM (bf16, M % 32 == 0): bit 0, AT (and, level 0, QgT) in fragment order;
+// bit 1, Bop (and, level 0, AqkT) too.
+template <typename E, int K, int M, int FRM>
 __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;
@@ -43,6 +44,7 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   constexpr int NSK = K / KS;
   constexpr int NSM = (M + KS - 1) / KS;
   constexpr bool PADM = (M % KS) != 0;
+  constexpr bool FRB = FRM & 1, FRA = FRM & 2;
   constexpr int DOE = M * BV / 256;           // dO elements staged per thread
   static_assert(M != CH || (BV % DOE == 0 && 256 / (BV / DOE) == M && DOE % 8 == 0),
                 "level 0: one token row slice per thread");
@@ -125,12 +127,12 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       if (rt < RTV) {
         const int brow = (rt * 16 + (lane & 15)) * K + kofs<E>(lane);
 #pragma unroll
-        for (int s = 0; s < NSK; ++s) o.bop[p][s] = Bj.get(FR ? frag_at(rt, s, K) : brow + s * KS);
+        for (int s = 0; s < NSK; ++s) o.bop[p][s] = Bj.get(FRA ? frag_at(rt, s, K) : brow + s * KS);
         if (l0) {
           const SplitTile<E> Qj = split_at<E>(a.AqkT + ((size_t)bh * S + j) * M * M, M * M);
           const int qrow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSM; ++s) o.aqk[p][s] = Qj.get(FR ? frag_at(rt, s, M) : qrow + s * KS);
+          for (int s = 0; s < NSM; ++s) o.aqk[p][s] = Qj.get(FRA ? frag_at(rt, s, M) : qrow + s * KS);
         }
       }
     }
@@ -140,13 +142,13 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       const int arow = (rt * 16 + (lane & 15)) * M + kofs<E>(lane);
 #pragma unroll
       for (int s = 0; s < NSM; ++s)
-        o.at[t][s] = FR ? Aj.get(frag_at(rt, s, M))
+        o.at[t][s] = FRB ? Aj.get(frag_at(rt, s, M))
                         : (!PADM || s * KS + kofs<E>(lane) < M) ? Aj.get(arow + s * KS)
                                                                 : Mma<E>::szero();
       if (l0) {
         const SplitTile<E> QTj = split_at<E>(a.QgT + ((size_t)bh * S + j) * K * M, K * M);
 #pragma unroll
-        for (int s = 0; s < NSM; ++s) o.qg[t][s] = QTj.get(FR ? frag_at(rt, s, M) : arow + s * KS);
+        for (int s = 0; s < NSM; ++s) o.qg[t][s] = QTj.get(FRB ? frag_at(rt, s, M) : arow + s * KS);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
@@ -312,12 +314,14 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
 template <typename E, int K, int M>
 static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
-  constexpr bool CAN_FR = M == CH && std::is_same<E, bf16>::value;
-  if (a.frag && !CAN_FR) return hipErrorInvalidValue;
-  if (CAN_FR && a.frag)
-    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN_FR>), dim3(grid), dim3(256), 0, st, a);
+  constexpr bool CAN = M % 32 == 0 && std::is_same<E, bf16>::value;
+  if (a.frag && !(CAN && (a.frag == 1 || a.frag == 3))) return hipErrorInvalidValue;
+  if (CAN && a.frag == 3)
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN ? 3 : 0>), dim3(grid), dim3(256), 0, st, a);
+  else if (CAN && a.frag == 1)
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN ? 1 : 0>), dim3(grid), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, false>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, 0>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
