@@ -41,13 +41,28 @@ MFMA_BF16_TFLOPS = 2500.0        # dense bf16
 MFMA_FP32_TFLOPS = 157.3
 
 
+# The reference's published rows (benchmarks/bench_matched.py:49-52,77-110,
+# results/h100/depth.csv): firings 1, 2, 4 ..., queries min(8 * 2^l, d) per
+# level, the harness's own input distributions. "ref3" is its depth row at
+# d=128, L=3 (H100: forward 10.40 ms, forward+backward 44.46 ms, 13.42 GB).
+REF_SHAPES = {
+    "ref3": dict(B=4, T=8192, H=16, K=128, V=128, L=3, N=32, n_queries=(16, 32),
+                 intervals=(1, 2, 4), dtype=torch.bfloat16, g_scale=1.0, style="reftest"),
+}
+
+
 def gpu_inputs(cfg, seed=0):
-    """Inputs of the configuration's distributions, drawn on the GPU."""
+    """Inputs of the configuration's distributions, drawn on the GPU: the
+    benchmark configurations' (``baseline``), or the reference harness's
+    (``reftest``: q ~ N(0,1), v = 0.5 N(0,1), g = logsigmoid(N(0,1)) in the
+    input dtype, b, w ~ U(0,1); bench_matched.py:77-110)."""
     B, T, H, K, V, L, N = (cfg[x] for x in ("B", "T", "H", "K", "V", "L", "N"))
     dt = cfg["dtype"]
     g = torch.Generator(device="cuda").manual_seed(seed)
     r = lambda *s: torch.randn(*s, generator=g, device="cuda", dtype=torch.float32)  # noqa: E731
+    u = lambda *s: torch.rand(*s, generator=g, device="cuda", dtype=torch.float32)  # noqa: E731
     F = torch.nn.functional
+    nq = tuple(cfg.get("n_queries") or [N] * (L - 1))
     inp = dict(
         q=F.normalize(r(B, T, H, L, K), dim=-1).to(dt),
         k=F.normalize(r(B, T, H, K), dim=-1).to(dt),
@@ -56,14 +71,18 @@ def gpu_inputs(cfg, seed=0):
         b=torch.sigmoid(r(B, T, H, K)).to(dt),
         w=torch.sigmoid(r(B, T, H, V)).to(dt),
         mix_weights=torch.softmax(r(B, T, H, L), dim=-1).to(dt),
-        query_banks=(r(L - 1, H, N, K) * K ** -0.5).to(dt),
+        query_banks=(r(L - 1, H, max(nq, default=1), K) * K ** -0.5).to(dt),
         key_projections=(r(L - 1, H, K, V) * V ** -0.5).to(dt),
         b_projections=(r(L - 1, H, V, K) * V ** -0.5).to(dt),
         w_projections=(r(L - 1, H, V, V) * V ** -0.5).to(dt),
         g_projections=(r(L - 1, H, V, K) * V ** -0.5).to(dt),
-        n_queries_per_level=tuple([N] * (L - 1)),
+        n_queries_per_level=nq,
         firing_intervals=tuple(cfg["intervals"]),
     )
+    if cfg.get("style") == "reftest":
+        inp.update(q=r(B, T, H, L, K).to(dt), v=(r(B, T, H, V) * 0.5).to(dt),
+                   g=F.logsigmoid(r(B, T, H, K)).to(dt).float(),
+                   b=u(B, T, H, K).to(dt), w=u(B, T, H, V).to(dt))
     return inp
 
 
@@ -200,7 +219,7 @@ MFMA_KERNELS = ("ngdn_l0_intra_fwd", "ngdn_output_fwd", "ngdn_output_l0_fwd",
                 "ngdn_probe_fwd", "ngdn_promote_chain_fwd", "ngdn_probe_bwd")
 
 
-def step_totals(cfg):
+def step_totals(cfg, fwd_only=False):
     """Algorithmic HBM bytes and flops of one fwd+bwd step of the op as a
     whole. Flops are the dense tile products of the op's mathematics with
     C = 64: forward, per chunk-head 2C^2(3K+2V) + 6CKV + C^3/3 for level 0,
@@ -224,11 +243,14 @@ def step_totals(cfg):
     C = 64
     units = B * H * NT
     fires = sum(B * H * n_firings(NT, f[l]) for l in range(1, L))
-    flops = (units * (2 * C * C * (3 * K + 2 * V) + 6 * C * K * V + C ** 3 // 3)
-             + tok * (L - 1) * 2 * K * V + fires * 14 * N * K * V
-             + units * (2 * C * C * (6 * K + 4 * V) + 12 * C * K * V + 4 * C ** 3)
-             + tok * (L - 1) * 4 * K * V + fires * 28 * N * K * V)
-    return fwd + bwd, flops
+    flops_f = (units * (2 * C * C * (3 * K + 2 * V) + 6 * C * K * V + C ** 3 // 3)
+               + tok * (L - 1) * 2 * K * V + fires * 14 * N * K * V)
+    flops_b = (units * (2 * C * C * (6 * K + 4 * V) + 12 * C * K * V + 4 * C ** 3)
+               + tok * (L - 1) * 4 * K * V + fires * 28 * N * K * V)
+    if fwd_only:
+        # without a backward nothing is saved: inputs in, o and the final state out
+        return fwd - states, flops_f
+    return fwd + bwd, flops_f + flops_b
 
 
 def profiled_traffic(config, entry):
@@ -245,6 +267,15 @@ def profiled_traffic(config, entry):
     return None
 
 
+def fwd_fn(inp, L):
+    """The op's forward alone, on inputs that need no gradient (nothing is
+    kept for a backward)."""
+    def fwd():
+        with torch.no_grad():
+            chunk_nested_gdn2(**inp, L=L)
+    return fwd
+
+
 def step_fn(inp, leaves, L, do):
     def step():
         o, _ = chunk_nested_gdn2(**{**inp, **leaves}, L=L)
@@ -252,15 +283,16 @@ def step_fn(inp, leaves, L, do):
     return step
 
 
-def cpu_baseline(cfg, budget_s=20.0):
+def cpu_baseline(cfg, budget_s=20.0, backward=True):
     """The CPU restatement (float32 PyTorch) on one-head slices of the
-    workload, forward + backward, extrapolated to the whole step."""
+    workload, forward (+ backward), extrapolated to the whole step."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import ngdn_oracle
 
     from nested_recurrent_memory_amd.inputs import make_cotangent, make_inputs
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    cores = len(os.sched_getaffinity(0))
+    threads = min(16, cores)
     torch.set_num_threads(threads)
     B, T, H = cfg["B"], cfg["T"], cfg["H"]
     one = dict(cfg)
@@ -271,16 +303,20 @@ def cpu_baseline(cfg, budget_s=20.0):
         lv = {n: inp[n].float().requires_grad_(True) for n in LEAVES}
         args = [lv[n] for n in LEAVES] + [inp["n_queries_per_level"], inp["firing_intervals"]]
         t0 = time.perf_counter()
-        o, _ = ngdn_oracle.chunk_forward(*args, L=cfg["L"], output_final_state=True,
-                                         dtype=torch.float32, out_dtype=torch.float32)
-        o.backward(make_cotangent(o.shape))
+        with torch.enable_grad() if backward else torch.no_grad():
+            o, _ = ngdn_oracle.chunk_forward(*args, L=cfg["L"], output_final_state=True,
+                                             dtype=torch.float32, out_dtype=torch.float32)
+            if backward:
+                o.backward(make_cotangent(o.shape))
         t_total += time.perf_counter() - t0
         slices += 1
         done += T
     per_slice = t_total / slices
     full = per_slice * B * H
-    return {"value": B * T / full, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{slices} of the {B * H} (batch, head) slices (T={T}) forward+backward, "
+    return {"value": B * T / full, "unit": "tokens/s", "cores": cores,
+            "threads": torch.get_num_threads(), "torch": torch.__version__, "kind": "port",
+            "sample": f"{slices} of the {B * H} (batch, head) slices (T={T}) "
+                      f"{'forward+backward' if backward else 'forward'}, "
                       f"{t_total:.1f} s, scaled by {B * H}/{slices}"}
 
 
@@ -476,7 +512,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2")
+    ap.add_argument("--config", default="c2",
+                    help="c0..c3 (BASELINE.json configs) or ref3 (the reference's published "
+                         "depth row at d=128, L=3)")
+    ap.add_argument("--mode", default=None, choices=("fwdbwd", "fwd"),
+                    help="a step is forward+backward (default) or forward only (default for "
+                         "c3, which BASELINE.json quotes forward only)")
     ap.add_argument("--stream-groups", type=int, default=None,
                     help="groups of batch rows run on their own streams (default: the "
                          "package's STREAM_GROUPS)")
@@ -505,14 +546,16 @@ def main():
         model_bench(args)
         return
 
-    cfg = dict(CONFIGS[args.config])
+    cfg = dict(CONFIGS[args.config] if args.config in CONFIGS else REF_SHAPES[args.config])
+    fwd_only = (args.mode or ("fwd" if args.config == "c3" else "fwdbwd")) == "fwd"
     L = cfg["L"]
     inp = gpu_inputs(cfg)
     leaves = {n: inp[n].detach().clone().requires_grad_(True) for n in LEAVES}
     B, T, H, V = cfg["B"], cfg["T"], cfg["H"], cfg["V"]
     gen = torch.Generator(device="cuda").manual_seed(1)
     do = torch.randn(B, T, H, V, generator=gen, device="cuda").to(cfg["dtype"])
-    step = step_fn(inp, leaves, L, do)
+    fwd = fwd_fn(inp, L)
+    step = fwd if fwd_only else step_fn(inp, leaves, L, do)
 
     for _ in range(args.warmup):
         step()
@@ -539,6 +582,27 @@ def main():
             t.grad = None
     torch.cuda.synchronize()
     timing, _lib.TIMING = _lib.TIMING, None
+
+    # the reference harness's columns (bench_matched.py:124-149): forward
+    # alone (inputs that need no gradient), forward+backward, and the peak of
+    # allocated memory over one forward+backward (inputs included)
+    cols = None
+    if not fwd_only:
+        fwd()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            fwd()
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t1) / args.steps * 1e3
+        torch.cuda.reset_peak_memory_stats()
+        step()
+        for t in leaves.values():
+            t.grad = None
+        torch.cuda.synchronize()
+        cols = {"nested_fwd_ms": round(fwd_ms, 3),
+                "nested_fb_ms": round(elapsed / args.steps * 1e3, 3),
+                "nested_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3)}
 
     ms = {}
     for name, evs in timing.items():
@@ -583,7 +647,7 @@ def main():
                 mf[n] = {"tflops": round(tf, 2), "frac": round(tf / peak_f, 4),
                          "avg_ms": round(ms[n], 4)}
         roof["mfma_kernels"] = mf
-        sb, sf = step_totals(cfg)
+        sb, sf = step_totals(cfg, fwd_only)
         st = elapsed / args.steps
         roof["step"] = {"algorithmic_bytes": sb, "hbm_frac": round(sb / st / 1e9 / HBM_PEAK_GBS, 4),
                         "algorithmic_flops": sf,
@@ -602,9 +666,13 @@ def main():
 
     ms_step = elapsed / args.steps * 1e3
     tokens = B * T * args.steps
-    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, backward=not fwd_only)
+    what = "fwd" if fwd_only else "fwd+bwd"
+    metric = ("tokens/s fwd+bwd nested GDN op (B4,T8192,H16,d128,3 lvl)" if args.config == "c2"
+              and not fwd_only else f"tokens/s {what} nested GDN op ({args.config}: B{B},T{T},"
+              f"H{H},d{cfg['K']},{L} lvl)")
     line = {
-        "metric": "tokens/s fwd+bwd nested GDN op (B4,T8192,H16,d128,3 lvl)",
+        "metric": metric,
         "value": round(tokens / elapsed, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -616,10 +684,13 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}: chunk_nested_gdn2 forward+backward", "B": B,
+        "config": {"workload": f"{args.config}: chunk_nested_gdn2 "
+                               f"{'forward' if fwd_only else 'forward+backward'}", "B": B,
                    "T": T, "H": H, "K": cfg["K"], "V": V, "L": L,
-                   "firing_intervals": list(cfg["intervals"]), "n_queries": cfg["N"],
-                   "chunk": 64, "state": "fp32"},
+                   "firing_intervals": list(cfg["intervals"]),
+                   "n_queries": list(inp["n_queries_per_level"]),
+                   "inputs": cfg.get("style", "baseline"), "chunk": 64, "state": "fp32"},
+        "reference_columns": cols,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

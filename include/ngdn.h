@@ -50,7 +50,15 @@ typedef struct ngdn_dims {
 
 /* Last error message on this thread ("" when none). */
 const char* ngdn_last_error(void);
-/* Library version, major * 10000 + minor * 100 + patch. */
+/* Version of this interface, major * 10000 + minor * 100 + patch. A caller
+ * built against this header checks ngdn_version() == NGDN_VERSION before its
+ * first call: the layouts of the working tensors and the meaning of some
+ * arguments changed between versions while the signatures stayed the same
+ * (for instance ngdn_probe_bwd's bank-gradient argument: an accumulator
+ * [L-1,H,n_max,K] before 0.2.0, the per-firing workspace ws_dbank
+ * [B,H,NF,N,K] since), so an older caller can link and then write past its
+ * buffers. */
+#define NGDN_VERSION 300
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -105,7 +113,11 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
  * A = keys*b*e^g [N,K] (split), KT = keys^T [K,N] (split), U = values*w [N,V],
  * gam = e^g [K]; for the backward, keysN = keys [N,K] and AT = A^T
  * [K,N] (both split; may be NULL). keys/vals/bo/wo/go (fp32, [B,NF,H,N,K|V] and [B,NF,H,K])
- * receive the probe outputs in the reference layout when not NULL. */
+ * receive the probe outputs in the reference layout when not NULL.
+ * Fragment order: for NGDN_BF16 with N % 32 == 0, each plane of the [K][N]
+ * tiles KT and AT is in the fragment order described at ngdn_l0_intra_fwd
+ * (C = N); A and keysN stay row-major. ngdn_upper_scan_fwd / _bwd read KT and
+ * AT that way; a caller that writes or reads them itself must use it too. */
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
                        const float* below, int32_t ng_below,
@@ -117,7 +129,9 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        float* go, void* stream);
 
 /* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
- * probe's scan-ready pairs: NF firings, NG = ceil(NT / f) stored group
+ * probe's scan-ready pairs (A row-major; KT in fragment order for NGDN_BF16
+ * with n_pairs % 32 == 0, as ngdn_probe_fwd and ngdn_promote_chain_fwd write
+ * it): NF firings, NG = ceil(NT / f) stored group
  * states. Writes states [B,NG,H,K,V] fp32 (state entering each group; groups
  * past the last firing hold the final state), statesT [B,NG,H,V,K] (the same,
  * transposed; may be NULL) and final_state[:, :, level]. initial_state may be
@@ -142,8 +156,9 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
  * [B,NG,H,V,K] (NG = ceil(NT / f_here); the state entering each group,
  * groups past the last firing hold the final state) and
  * final_state[:, :, level]. For the backward (all three or none): keysN
- * [B,H,NF,N,K] and AT = (keys b e^g)^T [B,H,NF,K,N] (split), gam = e^g
- * [B,H,NF,K] fp32, as ngdn_probe_fwd writes them. Up to 64 pairs per firing
+ * [B,H,NF,N,K] and AT = (keys b e^g)^T [B,H,NF,K,N] (split; AT in fragment
+ * order for NGDN_BF16 with N % 32 == 0), gam = e^g [B,H,NF,K] fp32, as
+ * ngdn_probe_fwd writes them. Up to 64 pairs per firing
  * (merge: K = 64); other levels use ngdn_probe_fwd + ngdn_upper_scan_fwd. */
 int32_t ngdn_promote_chain_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                                int32_t n_queries, int32_t f_below, int32_t f_here,
@@ -219,7 +234,8 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
                          void* stream);
 
 /* Reverse write scan of level `level` >= 1 (ops/update_bwd.py:19-164): keys
- * [B,H,NF,N,K] and AT = (keys*b*e^g)^T [B,H,NF,K,N] (both split) from ngdn_probe_fwd, gam
+ * [B,H,NF,N,K] and AT = (keys*b*e^g)^T [B,H,NF,K,N] (both split; AT in
+ * fragment order for NGDN_BF16 with n_pairs % 32 == 0) from ngdn_probe_fwd, gam
  * [B,H,NF,K]; d_states fp32 [B,NG,H,K,V] (read gradients plus the level
  * above's scatter); d_final [B,H,L,K,V]. Writes dSp fp32 [B,H,NF,K,V], dvn
  * fp32 [B,H,NF,N,V] and d_initial[:, :, level] when not NULL. */

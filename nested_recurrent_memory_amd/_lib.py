@@ -17,6 +17,10 @@ LIB_PATH = os.path.join(HERE, "libngdn.so")
 
 NGDN_F32 = 0
 NGDN_BF16 = 1
+# NGDN_VERSION of include/ngdn.h: the interface the signatures below describe.
+# The loader refuses a library of another version (working-tensor layouts and
+# argument meanings changed between versions under unchanged signatures).
+VERSION = 300
 
 
 class Dims(ctypes.Structure):
@@ -98,6 +102,9 @@ def lib():
             fn = getattr(so, name)
             fn.argtypes = args
             fn.restype = _RESTYPES.get(name, ctypes.c_int32)
+        if so.ngdn_version() != VERSION:
+            raise NgdnError(f"{LIB_PATH} implements interface version {so.ngdn_version()}, "
+                            f"this package calls version {VERSION}: rebuild the library")
         _lib = so
     return _lib
 

@@ -47,7 +47,7 @@ inline int nchunks(const ngdn_dims* d) { return (d->T + ngdn::CH - 1) / ngdn::CH
 extern "C" {
 
 const char* ngdn_last_error(void) { return g_err; }
-int32_t ngdn_version(void) { return 100; }
+int32_t ngdn_version(void) { return NGDN_VERSION; }
 const char* ngdn_arch(void) { return "gfx950"; }
 
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,

@@ -319,6 +319,9 @@ static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   constexpr bool BF = std::is_same<E, bf16>::value;
   if (a.frag && !(BF && M % 32 == 0 && (a.frag == 1 || (a.frag == 3 && M == CH))))
     return hipErrorInvalidValue;
+  // level 0's read is formed only by the chunk-step (M == CH) kernels whose
+  // operand groups share one layout (frag 0 or 3)
+  if (a.read0 && (M != CH || a.frag == 1)) return hipErrorInvalidValue;
   if constexpr (BF && M == CH) {
     if (a.frag == 3) {
       if (a.read0)

@@ -31,7 +31,14 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(so, name), name
     assert so.ngdn_arch() == b"gfx950"
-    assert so.ngdn_version() >= 100
+
+
+def test_interface_version_matches_header_and_loader():
+    """The header's NGDN_VERSION, the library's ngdn_version() and the version
+    the Python signatures describe are one number."""
+    text = open(os.path.join(ROOT, "include", "ngdn.h")).read()
+    macro = int(re.search(r"#define NGDN_VERSION (\d+)", text).group(1))
+    assert _lib.lib().ngdn_version() == macro == _lib.VERSION
 
 
 def test_invalid_arguments_return_error_without_launch():
