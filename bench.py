@@ -114,10 +114,10 @@ def work_model(cfg):
     tok = B * T * H                                   # token-heads
     fin0 = B * H * kv                                 # one level's final state
     # level-0 intra: reads q0,k,b,v,w + g (fp32); writes W,U,KtT,Qg,Aqk,gam
-    # and the backward layouts Kt, WT, QgT, AqkT, TT
+    # and, for the backward, TT
     m["ngdn_l0_intra_fwd"] = (
         units * (3 * ck + 2 * cv + gk),
-        units * (3 * ck + 2 * cv + gk + 4 * wk + wv + wc + K * 4 + 3 * wk + 2 * wc),
+        units * (3 * ck + 2 * cv + gk + 3 * wk + wv + wc + K * 4 + wc),
         units * (2 * 2 * C * C * K + 2 * C * C * (K + V) + C ** 3 // 3))
     # level-0 scan: reads W, U, KtT, gam; writes hT, vnT and (training) h, vn; + final
     m["ngdn_l0_scan_fwd"] = (units * kv + fin0,
@@ -142,8 +142,9 @@ def work_model(cfg):
                                   units * (L - 1) * 2 * C * K * V)
     # dmix_0 = <do, read_0>: reads read_0 (fp32), do; writes dmix
     m["ngdn_output_bwd"] = (tok * (V * es + 4), tok * (V * 4 + V * es + L * 4), tok * 2 * V)
-    # level-0 reverse scan: reads Kt, WT, QgT, AqkT, gam, do, mix; writes dSp
-    # and dVnT (and dVn for the two-launch chunk backward)
+    # level-0 reverse scan: reads the forward's W, KtT, Qg, Aqk (transposed on
+    # chip), gam, do, mix; writes dSp and dVnT (and dVn for the two-launch
+    # chunk backward)
     m["ngdn_l0_scan_bwd"] = (units * (cv + cm + kv),
                              units * (3 * wk + wc + K * 4 + cv + C * es + kv + wv),
                              units * (2 * C * K * V * 3 + 2 * C * C * V))

@@ -66,22 +66,18 @@ const char* ngdn_arch(void);
 /* Level-0 per-chunk terms: the intra-chunk half of fla's chunk_gdn2_fwd as
  * called at nested_gdn2/ops/chunk.py:236-248 (semantics ops/naive.py:329-358).
  * Outputs: W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64],
- * Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64], gam [B,H,NT,K].
- * Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64] and
- * AqkT [B,H,NT,64,64] are the transposed copies the reverse scan reads,
- * TT [B,H,NT,64,64] = ((I + A)^-1)^T the one the chunk backward reads; each
- * may be NULL (inference). W, KtT, Qg, Aqk, Kt, WT, QgT and AqkT are split;
- * U, gam and TT fp32. For bf16 inputs the split tensors (read only as
- * matrix-core A operands by row tile) are in fragment order: in each plane
- * of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512 consecutive
- * elements at 512 (rb C/32 + cb), element (r, c) of the block at
- * 8 (16 (c / 8) + r) + c % 8, so one operand fragment is one contiguous
- * 1 KB read. */
+ * Qg [B,H,NT,64,K] (scale folded in), Aqk [B,H,NT,64,64], gam [B,H,NT,K],
+ * and TT [B,H,NT,64,64] = ((I + A)^-1)^T, which only the chunk backward
+ * reads (may be NULL: inference). W, KtT, Qg and Aqk are split; U, gam and
+ * TT fp32. For bf16 inputs the split tensors are in fragment order: in each
+ * plane of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512
+ * consecutive elements at 512 (rb C/32 + cb), element (r, c) of the block
+ * at 8 (16 (c / 8) + r) + c % 8, so one matrix-core A fragment of a row tile
+ * is one contiguous 1 KB read. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
-                          float* Aqk, float* gam, float* Kt, float* WT, float* QgT,
-                          float* AqkT, float* TT, void* stream);
+                          float* Aqk, float* gam, float* TT, void* stream);
 
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
@@ -216,18 +212,18 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
                             void* stream);
 
 /* Reverse level-0 state recurrence (the vendored fla dh kernel with dh_ext,
- * ops/_vendor/common_chunk_delta_h.py:25-380). Kt [B,H,NT,64,K],
- * WT/QgT [B,H,NT,K,64], AqkT [B,H,NT,64,64] from ngdn_l0_intra_fwd; inj
+ * ops/_vendor/common_chunk_delta_h.py:25-380). W, KtT, Qg, Aqk and gam as
+ * ngdn_l0_intra_fwd writes them (split; bf16 in fragment order): the scan
+ * takes their transposes (Kt, W^T, Qg^T, Aqk^T) as its operands and forms
+ * them on chip; inj
  * (fp32 [B,H,nf1,K,V], may be NULL) is level 1's gradient of the state
  * entering chunk (i+1)*f1, added before that chunk's step (the reference's
  * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
  * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (either may be NULL, not
- * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL.
- * Kt, WT, QgT and AqkT are read split (bf16: in fragment order, as
- * ngdn_l0_intra_fwd writes them). */
-int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
-                         const float* gam, const float* AqkT, const float* QgT,
+ * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL. */
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
+                         const float* gam, const float* Qg, const float* Aqk,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
                          float* dSp, float* dVn, float* dVnT, float* d_initial,

@@ -41,7 +41,7 @@ SIGNATURES = {
     "ngdn_last_error": [],
     "ngdn_version": [],
     "ngdn_arch": [],
-    "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P] * 5 + [P],
+    "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P] + [P],
     "ngdn_l0_scan_fwd": [PD, P, P, P, P, P, P, P, I32, P, P, P, P, P, P, P],
     "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
                       + [P] * 11 + [P],

@@ -186,8 +186,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     W, U, Qg = f32(B, H, NT, 64, K), f32(B, H, NT, 64, V), f32(B, H, NT, 64, K)
     KtT, Aqk = f32(B, H, NT, K, 64), f32(B, H, NT, 64, 64)
     gam = f32(B, H, NT, K)
-    Kt, WT, QgT = opt(B, H, NT, 64, K), opt(B, H, NT, K, 64), opt(B, H, NT, K, 64)
-    AqkT, TT = opt(B, H, NT, 64, 64), opt(B, H, NT, 64, 64)
+    TT = opt(B, H, NT, 64, 64)
     # the state entering each chunk, transposed: read by level 1's probes at
     # every f1-th chunk only, so only those are written
     hT = f32(B, H, NT, V, K) if L > 1 else None
@@ -235,7 +234,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         sp = _lib.ptr_of_stream(st)
         d = _lib.dims(nb, T, H, L, K, V, code, scale)
         _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT)), sp)
+            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, TT)), sp)
         _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
             W, U, KtT, gam, Qg, Aqk, init_)), f[1] if L > 1 else 1,
             *(P(R(x)) for x in (hT, None, h_, vn_, read0, final)), sp)
@@ -270,7 +269,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
-                     KtT=KtT, Aqk=Aqk, gam=gam, Kt=Kt, WT=WT, QgT=QgT, AqkT=AqkT, TT=TT,
+                     KtT=KtT, Aqk=Aqk, gam=gam, TT=TT,
                      hT=hT, h=h_, vn=vn_, read0=read0, states=states,
                      statesT=statesT, levels=levels, final=final, par=par,
                      code=code, wd=wd)
@@ -455,7 +454,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
             dmix0()
         # level 0
         _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
-            "Kt", "WT", "gam", "AqkT", "QgT")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
+            "W", "KtT", "gam", "Qg", "Aqk")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
             P(R(inj)), nf1, P(R(d_final)), P(R(dSp0)), P(R(dVn0)), P(R(dVnT0)), P(R(d_init)), sp)
         if FUSED_L0_BWD:
             # the chunk backward in one launch: the state half per chunk

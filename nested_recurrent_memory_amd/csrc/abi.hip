@@ -53,13 +53,12 @@ const char* ngdn_arch(void) { return "gfx950"; }
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
-                          float* Aqk, float* gam, float* Kt, float* WT, float* QgT,
-                          float* AqkT, float* TT, void* stream) {
+                          float* Aqk, float* gam, float* TT, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_intra_fwd")) return r;
   if (!q || !k || !v || !g || !b || !w || !W || !U || !KtT || !Qg || !Aqk || !gam)
     return fail(NGDN_EINVAL, "ngdn_l0_intra_fwd: NULL tensor");
-  ngdn::L0IntraArgs a{q, k, v, g, b, w, W, U, KtT, Qg, Aqk, gam, Kt, WT, QgT, AqkT, TT,
+  ngdn::L0IntraArgs a{q, k, v, g, b, w, W, U, KtT, Qg, Aqk, gam, TT,
                       d->B, d->T, d->H, d->L, nchunks(d), d->scale};
   return launched(ngdn::l0_intra_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_intra_fwd");
@@ -313,30 +312,30 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
                   "ngdn_read_state_bwd");
 }
 
-int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* Kt, const float* WT,
-                         const float* gam, const float* AqkT, const float* QgT,
+int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
+                         const float* gam, const float* Qg, const float* Aqk,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
                          float* dSp, float* dVn, float* dVnT, float* d_initial,
                          void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_bwd")) return r;
-  if (!Kt || !WT || !gam || !AqkT || !QgT || !dout || !mix || !dSp || (!dVn && !dVnT))
+  if (!W || !KtT || !gam || !Qg || !Aqk || !dout || !mix || !dSp || (!dVn && !dVnT))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: NULL tensor");
   const int NT = nchunks(d);
   if (inj && (f1 <= 0 || nf1 != NT / f1))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: injection count %d inconsistent with f1=%d", nf1, f1);
   const long long skv = (long long)d->K * d->V;
   ngdn::ScanBwdArgs a{};
-  a.Bop = Kt; a.AT = WT; a.gam = gam;
-  a.AqkT = AqkT; a.QgT = QgT; a.dout = dout; a.mix = mix; a.T = d->T; a.L = d->L;
+  a.W = W; a.KtT = KtT; a.Qg = Qg; a.Aqk = Aqk; a.gam = gam;
+  a.dout = dout; a.mix = mix; a.T = d->T; a.L = d->L;
   a.inj = inj; a.inj_every = inj ? f1 : 1; a.inj_nf = nf1;
   a.d_states = nullptr; a.NG = NT;
   a.d_final = d_final; a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
   a.dSp = dSp; a.dVn = dVn; a.dVnT = dVnT;
   a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
-  a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // Kt, WT, AqkT, QgT: fragment order
+  a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // W, KtT, Qg, Aqk: fragment order
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
 }
 

@@ -149,30 +149,30 @@ __device__ __forceinline__ bool l0_block_safe(const float* s_gc, int I) {
 }
 
 // Per-row outputs written while the chunk's rows are in registers (forward
-// only; any pointer may be null): Qg = scale q e^gc and Kt = k e^(gc_last - gc)
-// [64][K] and transposed [K][64], all four in split form (they enter the
+// only; either pointer may be null): Qg = scale q e^gc [64][K] and
+// Kt^T = (k e^(gc_last - gc))^T [K][64], both in split form (they enter the
 // matrix cores only, as A operands by row tile), for bf16 in fragment
 // order.
 struct RowOut {
-  float* Qg; float* QgT; float* Kt; float* KtT;
+  float* Qg; float* KtT;
 };
 
 // A (strictly lower, into s_A fp32 [64][AT_LD]) and, when aqk_out != null,
-// Aqk (lower incl. diagonal) to global [64][64]; when aqkT_out != null also
-// its transpose; both in split form. Wave w computes block-row w. With
-// per-row outputs, s_x is LDS scratch of 64 x (64 + 4) floats for the
-// transposed ones, and the call ends with a barrier.
+// Aqk (lower incl. diagonal) to global [64][64] in split form. Wave w
+// computes block-row w. With per-row outputs, s_x is LDS scratch of
+// 64 x (64 + 4) floats for the transposed one, and the call ends with a
+// barrier.
 template <typename E, int K, int V>
 __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
                                            const ChunkIn<E, K, V>& in, float* aqk_out,
-                                           float* aqkT_out, const RowOut& ro = RowOut{},
+                                           const RowOut& ro = RowOut{},
                                            float* s_x = nullptr) {
   constexpr int GL = K + GCP;
   constexpr int NKS = K / Mma<E>::KS;
   constexpr int KPL = Mma<E>::KPL;
   typedef typename Mma<E>::SFrag SF;
   const int lane = lane_id(), I = wave_id(), r = 16 * I;
-  const bool want_q = aqk_out != nullptr || aqkT_out != nullptr;
+  const bool want_q = aqk_out != nullptr;
   // bf16: every split output in fragment order
   constexpr bool FRAG = std::is_same<E, bf16>::value;
   typedef typename Mma<E>::Frag FR;
@@ -264,27 +264,24 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   }
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
-    f4 qt;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = r + acc_row(rr), j = 16 * J + acc_col();
       s_A[i * AT_LD + j] = (j < i) ? accAs[J][rr] : 0.f;
-      qt[rr] = (j <= i) ? accQs[J][rr] : 0.f;
-      if (aqk_out) split_at<E>(aqk_out, CH * CH).put1(FRAG ? frag_ofs(i, j, CH) : i * CH + j, qt[rr]);
-    }
-    if (aqkT_out) {
-      const int tr = 16 * J + acc_col(), tc = r + acc_row(0);
-      split_at<E>(aqkT_out, CH * CH).put4(FRAG ? frag_ofs(tr, tc, CH) : tr * CH + tc, qt);
+      if (aqk_out)
+        split_at<E>(aqk_out, CH * CH).put1(FRAG ? frag_ofs(i, j, CH) : i * CH + j,
+                                           (j <= i) ? accQs[J][rr] : 0.f);
     }
   }
-  if (ro.Qg) {
-    // Kt and Kt^T, then Qg and Qg^T (split): each value computed once into
-    // the LDS scratch s_x [64 columns][CH + 4], then written from there
-    // row-major and transposed, 16-byte rows both
+  if (ro.Qg || ro.KtT) {
+    // Kt^T, then Qg (split): each value computed once into the LDS scratch
+    // s_x [64 columns][CH + 4], then written from there (transposed for
+    // Kt^T), 16-byte rows both
     constexpr int LDX = CH + 4;
     for (int which = 0; which < 2; ++which) {
-      float* tp = which ? ro.QgT : ro.KtT;
-      float* rp = which ? ro.Qg : ro.Kt;
+      float* tp = which ? nullptr : ro.KtT;
+      float* rp = which ? ro.Qg : nullptr;
+      if (!tp && !rp) continue;
       const SplitTile<E> tdst = split_at<E>(tp, K * CH), rdst = split_at<E>(rp, CH * K);
       for (int hh = 0; hh < K / 64; ++hh) {
 #pragma unroll

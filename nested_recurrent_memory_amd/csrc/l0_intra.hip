@@ -12,12 +12,12 @@
 //   Qg   = scale * q0 * e^gc
 //   Aqk  = sum_k scale q_i k_j e^(gc_i - gc_j)            j <= i
 //   gam  = e^gc_last
-// The forward consumes W, U, Kt^T, Qg, Aqk; the reverse scan consumes the
-// transposed copies Kt, W^T, Qg^T, Aqk^T, written when their pointers are set.
-// For bf16 inputs the products run on bf16 MFMA with the derived operands
-// split in two (ngdn_common.h); the matrix-core operands W, Kt^T, Qg, Aqk and
-// the copies Kt, W^T, Qg^T, Aqk^T are stored split (split_at), U, gam and T^T
-// as fp32.
+// The forward scan consumes W, U, Kt^T, Qg, Aqk; the reverse scan reads the
+// same split tiles and transposes them on chip; the chunk backward reads
+// T^T, written when its pointer is set. For bf16 inputs the products run on
+// bf16 MFMA with the derived operands split in two (ngdn_common.h); the
+// matrix-core operands W, Kt^T, Qg, Aqk are stored split (split_at), U, gam
+// and T^T as fp32.
 //
 // One workgroup (4 waves) per (batch, head, chunk). Decay products are formed
 // without overflow: inside block-row I (16 rows starting at r = 16 I) every
@@ -31,7 +31,7 @@
 namespace ngdn {
 
 template <typename E, int K, int V>
-__global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
+__global__ __launch_bounds__(256, sizeof(E) == 2 ? 2 : 1) void l0_intra_fwd_kernel(L0IntraArgs a) {
   constexpr int C = CH;
   constexpr int GL = K + GCP;                // gc rows
   constexpr int LT = C + 4;                  // T rows, 16-byte aligned for fragment loads
@@ -62,13 +62,11 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   l0_cumsum(s_gc, in);
   lds_barrier();
 
-  // ---- 2. A and Aqk; Qg, Kt and their transposes while the rows are loaded
+  // ---- 2. A and Aqk; Qg and Kt^T while the rows are loaded
   {
-    RowOut ro{a.Qg + cix * C * K, a.QgT ? a.QgT + cix * K * C : nullptr,
-              a.Kt ? a.Kt + cix * C * K : nullptr, a.KtT + cix * K * C};
+    RowOut ro{a.Qg + cix * C * K, a.KtT + cix * K * C};
     // s_T (free until the inversion) is the scratch for the transposed rows
-    l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, a.AqkT ? a.AqkT + cix * C * C : nullptr, ro,
-               s_T);
+    l0_build_A(s_A, s_gc, in, a.Aqk + cix * C * C, ro, s_T);
   }
   if (tid < K) a.gam[cix * K + tid] = fexp(s_gc[(C - 1) * GL + tid]);
   lds_barrier();
@@ -122,8 +120,7 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
   // of m, each value split once by the thread that writes it), so every B
   // fragment is a 16-byte read. All tiles stay in registers until both
   // products are done; then W and U replace everything in LDS and leave in
-  // 16-byte rows (W, W^T and U), instead of 2- and 4-byte column-strided
-  // stores.
+  // 16-byte rows, instead of 2- and 4-byte column-strided stores.
   {
     using ST = SplitTile<E>;
     constexpr int LDX = C + ST::PAD;
@@ -205,24 +202,6 @@ __global__ __launch_bounds__(256) void l0_intra_fwd_kernel(L0IntraArgs a) {
     for (int e = tid; e < C * V / 4; e += 256) {
       const int i = e / (V / 4), c = (e % (V / 4)) * 4;
       *reinterpret_cast<f4*>(Uo + i * V + c) = *reinterpret_cast<const f4*>(s_u + i * LUU + c);
-    }
-    // W^T [K][C] (split; bf16: in fragment order, as the reverse scan reads
-    // it): four consecutive rows of one column per thread
-    if (a.WT) {
-      const SplitTile<E> WTo = split_at<E>(a.WT + cix * K * C, K * C);
-      for (int e = tid; e < K * C / 4; e += 256) {
-        int c, i;
-        if (std::is_same<E, bf16>::value) {
-          frag_pos(e * 4, C, c, i);
-        } else {
-          c = e / (C / 4);
-          i = (e % (C / 4)) * 4;
-        }
-        f4 x;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = s_w[(i + j) * LW + c];
-        WTo.put4(e * 4, x);
-      }
     }
   }
 }

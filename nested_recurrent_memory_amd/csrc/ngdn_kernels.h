@@ -10,15 +10,14 @@ namespace ngdn {
 // q [B,T,H,L,K] (level-0 slice read), k, b [B,T,H,K], v, w [B,T,H,V] in the
 // working dtype, g [B,T,H,K] fp32. Outputs, per (b, h, chunk):
 // W [B,H,NT,64,K], U [B,H,NT,64,V], KtT [B,H,NT,K,64], Qg [B,H,NT,64,K],
-// Aqk [B,H,NT,64,64], gam [B,H,NT,K]. When set, the transposed copies for the
-// backward: Kt [B,H,NT,64,K], WT [B,H,NT,K,64], QgT [B,H,NT,K,64],
-// AqkT [B,H,NT,64,64], TT [B,H,NT,64,64] (= T^T). W, KtT, Kt, WT, QgT and
-// AqkT are written in split form (split_at), the rest as fp32.
+// Aqk [B,H,NT,64,64], gam [B,H,NT,K]; when set, TT [B,H,NT,64,64] (= T^T)
+// for the chunk backward. W, KtT, Qg and Aqk are written in split form
+// (split_at), U, gam and TT as fp32.
 struct L0IntraArgs {
   const void* q; const void* k; const void* v; const float* g;
   const void* b; const void* w;
   float* W; float* U; float* KtT; float* Qg; float* Aqk; float* gam;
-  float* Kt; float* WT; float* QgT; float* AqkT; float* TT;
+  float* TT;
   int B, T, H, L, NT;
   float scale;
 };
@@ -71,19 +70,21 @@ struct ScanArgs {
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 
-// Reverse of scan_fwd. Bop [B*H,S,M,K] (= BT^T: level 0 Kt, upper keys),
-// AT [B*H,S,K,M] (= A^T), gam [B*H,S,K]. Level 0 sets AqkT [B*H,S,64,64],
-// QgT [B*H,S,K,64] (Bop, AT, AqkT and QgT in split form), dout [B,T,H,V], mix [B,T,H,L] and inj (fp32
-// [B*H,inj_nf,K,V], added before step j when (j+1) % inj_every == 0). Upper
-// levels set d_states (fp32 [B,NG,H,K,V], added after step j, and for every
-// stored group past the last step before the first). d_final seeds the state
+// Reverse of scan_fwd. Upper levels: Bop [B*H,S,M,K] (= BT^T, the keys) and
+// AT [B*H,S,K,M] (= A^T), both split, and d_states (fp32 [B,NG,H,K,V], added
+// after step j, and for every stored group past the last step before the
+// first). Level 0 (M = 64) sets instead the forward's own split tiles W
+// [B*H,S,64,K], KtT [B*H,S,K,64], Qg [B*H,S,64,K], Aqk [B*H,S,64,64] (bf16:
+// in fragment order), whose transposes it takes as its operands, dout
+// [B,T,H,V], mix [B,T,H,L] and inj (fp32 [B*H,inj_nf,K,V], added before step
+// j when (j+1) % inj_every == 0). gam [B*H,S,K]. d_final seeds the state
 // gradient. Outputs (fp32): dSp [B*H,S,K,V] (gradient of the state after
 // each step), dVn [B*H,S,M,V], dVnT = dVn^T [B*H,S,V,M] (when set), dinit
-// ([K][V] at strides, when set). All working tensors are fp32; dout and mix
-// are in the working dtype.
+// ([K][V] at strides, when set). dout and mix are in the working dtype.
 struct ScanBwdArgs {
   const float* Bop; const float* AT; const float* gam;
-  const float* AqkT; const float* QgT; const void* dout; const void* mix; int T, L;
+  const float* W; const float* KtT; const float* Qg; const float* Aqk;
+  const void* dout; const void* mix; int T, L;
   const float* inj; int inj_every, inj_nf;
   const float* d_states; int NG;
   const float* d_final; long long df_sb, df_sh;
@@ -92,7 +93,8 @@ struct ScanBwdArgs {
   float* dVnT;
   float* dinit; long long di_sb, di_sh;
   int B, H, S, M, V;
-  // bf16, fragment order: 1, AT (M % 32 == 0); 3, Bop, AT, AqkT, QgT (level 0)
+  // bf16, fragment order: 1, AT (upper levels, M % 32 == 0); 3, the level-0
+  // tiles W, KtT, Qg, Aqk
   int frag;
 };
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st);
