@@ -337,11 +337,21 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   }
 }
 
-// T = (I + A)^-1 by 16-row blocks: diagonal blocks by forward substitution,
-// then T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ by sub-diagonal. s_T has row
-// stride LDT; s_P is scratch [3][16][17]. Ends with a barrier.
+// T = (I + A)^-1 by 16-row blocks. The diagonal blocks by forward
+// substitution (wave 0, one column of one block per lane); the blocks below
+// the diagonal by two levels of 2 x 2 block inversion on the fp32 matrix
+// cores (products exact in fp32, v_mfma_f32_16x16x4_f32), in three rounds:
+//   T10 = -T11 A10 T00,  T32 = -T33 A32 T22         (waves 0, 1)
+//   Y = A[32:64, 0:32] T[0:32, 0:32]                  (one 16 x 16 block per wave)
+//   T[32:64, 0:32] = -T[32:64, 32:64] Y               (one block per wave)
+// since [[L1, 0], [A21, L2]]^-1 = [[L1^-1, 0], [-L2^-1 A21 L1^-1, L2^-1]].
+// The blocks of s_A above the diagonal are never read here: they hold the
+// four Y blocks ((0,1), (0,2), (0,3), (1,2)) and the middle factor of the
+// first round's triple products ((1,3) for wave 0, (2,3) for wave 1). s_T
+// has row stride LDT. Ends with a barrier.
 template <int LDT>
-__device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s_P) {
+__device__ __forceinline__ void l0_invert(float* s_A, float* s_T) {
+  typedef Mma<float> MF;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   if (wv == 0) {
     const int I = lane >> 4, c = lane & 15, o = 16 * I;
@@ -363,28 +373,61 @@ __device__ __forceinline__ void l0_invert(const float* s_A, float* s_T, float* s
     }
   }
   lds_barrier();
-  for (int d = 1; d < 4; ++d) {
-    const int nb = 4 - d;
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
-      const int I = d + blk, J = I - d;
-      float acc = 0.f;
-      for (int m = 16 * J; m < 16 * I; ++m)
-        acc += s_A[(16 * I + i) * AT_LD + m] * s_T[m * LDT + 16 * J + j];
-      s_P[blk * 272 + i * 17 + j] = acc;
-    }
-    lds_barrier();
-    for (int e = tid; e < nb * 256; e += 256) {
-      const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
-      const int I = d + blk, J = I - d;
-      float acc = 0.f;
+  // fp32 fragments (one k-value per lane): A operand of block (I, M) at
+  // k-step s, B operand of block (M, J); accumulators hold rows
+  // 4 (lane / 16) + r, column lane % 16
+  const int lr = lane & 15, lk = lane >> 4;
+  auto aA = [&](int I, int M, int s) { return s_A[(16 * I + lr) * AT_LD + 16 * M + 4 * s + lk]; };
+  auto aT = [&](int I, int M, int s) { return s_T[(16 * I + lr) * LDT + 16 * M + 4 * s + lk]; };
+  auto bT = [&](int M, int J, int s) { return s_T[(16 * M + 4 * s + lk) * LDT + 16 * J + lr]; };
+  auto bP = [&](const float* p, int s) { return p[(4 * s + lk) * AT_LD + lr]; };
+  auto put = [&](float* dst, int ld, f4 acc, float sign) {
 #pragma unroll
-      for (int m = 0; m < 16; ++m)
-        acc += s_T[(16 * I + i) * LDT + 16 * I + m] * s_P[blk * 272 + m * 17 + j];
-      s_T[(16 * I + i) * LDT + 16 * J + j] = -acc;
-    }
-    lds_barrier();
+    for (int r = 0; r < 4; ++r) dst[(4 * lk + r) * ld + lr] = sign * acc[r];
+  };
+  // block (r, c) of s_A above the diagonal, as scratch
+  auto up = [&](int r, int c) { return s_A + 16 * r * AT_LD + 16 * c; };
+  const int yr[4] = {0, 0, 0, 1}, yc[4] = {1, 2, 3, 2};   // Y_{M,J} in block q = 2 (M - 2) + J
+  if (wv < 2) {
+    const int I = wv ? 3 : 1, J = I - 1;
+    float* own = up(wv + 1, 3);
+    f4 p = f4_zero(), t = f4_zero();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) p = MF::mma(p, aA(I, J, s), bT(J, J, s));
+    put(own, AT_LD, p, 1.f);   // this wave's own scratch: read back in its program order
+#pragma unroll
+    for (int s = 0; s < 4; ++s) t = MF::mma(t, aT(I, I, s), bP(own, s));
+    put(s_T + 16 * I * LDT + 16 * J, LDT, t, -1.f);
   }
+  lds_barrier();
+  const int I = 2 + (wv >> 1), J = wv & 1;
+  {
+    // Y_IJ = sum_{M = J..1} A_IM T_MJ
+    f4 y = f4_zero();
+#pragma unroll
+    for (int M = 0; M < 2; ++M)
+      if (M >= J) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) y = MF::mma(y, aA(I, M, s), bT(M, J, s));
+      }
+    put(up(yr[wv], yc[wv]), AT_LD, y, 1.f);
+  }
+  lds_barrier();
+  {
+    // T_IJ = -sum_{M = 2..I} T_IM Y_MJ
+    f4 t = f4_zero();
+#pragma unroll
+    for (int M = 2; M < 4; ++M)
+      if (M <= I) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int q = (M - 2) * 2 + J;
+          t = MF::mma(t, aT(I, M, s), bP(up(yr[q], yc[q]), s));
+        }
+      }
+    put(s_T + 16 * I * LDT + 16 * J, LDT, t, -1.f);
+  }
+  lds_barrier();
 }
 
 // Right-hand sides transposed into s_X fp32 [(K+V)][LDX]: X[k][c] = b k e^gc,

@@ -43,16 +43,19 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 2 : 1) void l0_intra_fwd_kern
   const int h = bh % H, b = bh / H;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
 
-  // LDS: gc, and a region holding A, T and the inversion scratch, later the
+  // LDS: gc, and a region holding A and T, later the
   // transposed right-hand sides X_w^T, then X_u^T. Each wave keeps its 16 rows
   // of T in registers across the reuse.
   constexpr size_t SZ_GC = sizeof(float) * C * GL;
-  constexpr size_t SZ_R = sizeof(float) * (C * AT_LD + C * LT + 3 * 16 * 17);
+  constexpr size_t SZ_AT = sizeof(float) * (C * AT_LD + C * LT);
+  constexpr size_t SZ_XT = sizeof(typename SplitTile<E>::T) * SplitTile<E>::NPLANE *
+                           (K > V ? K : V) * (C + SplitTile<E>::PAD);
+  constexpr size_t SZ_WU = sizeof(float) * C * (K + 4 + V + 4) - SZ_GC;
+  constexpr size_t SZ_R = SZ_AT > SZ_XT ? (SZ_AT > SZ_WU ? SZ_AT : SZ_WU) : (SZ_XT > SZ_WU ? SZ_XT : SZ_WU);
   __shared__ __attribute__((aligned(16))) char smem[SZ_GC + SZ_R];
   float* s_gc = reinterpret_cast<float*>(smem);
   float* s_A = reinterpret_cast<float*>(smem + SZ_GC);
   float* s_T = s_A + C * AT_LD;
-  float* s_P = s_T + C * LT;                   // [3][16][17]
 
   ChunkIn<E, K, V> in;
   in.init(a.q, a.k, a.v, a.g, a.b, a.w, b, h, n, a.T, H, a.L, a.scale);
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 2 : 1) void l0_intra_fwd_kern
   }
 
   // ---- 3. T = (I + A)^-1; each wave takes its block-row into registers
-  l0_invert<LT>(s_A, s_T, s_P);
+  l0_invert<LT>(s_A, s_T);
   const int I = wv, R0 = 16 * I;
   const int kd = tri_depth<E>(I);
   SF tf[C / KS];
