@@ -42,10 +42,18 @@ extern "C" {
  * backward entry points ([NGDN_WPARTS][n] fp32, n the weight's size) */
 #define NGDN_WPARTS 1024
 
+/* Sizes of one call. hold_partial (0 or 1): with 1 a partial last chunk
+ * (T % 64 != 0) completes no upper level's firing, as the reference's
+ * decoding step treats an incomplete chunk (nested_gdn2/ops/naive.py:101-113);
+ * with 0, as the reference's chunk form (ops/chunk.py:257-290), every chunk
+ * end counts, the partial last one's included. The firings of level l are
+ * then NF = NTF / f_l, NTF = T / 64 (hold) or ceil(T / 64); the stored group
+ * states stay NG = ceil(ceil(T / 64) / f_l) either way. */
 typedef struct ngdn_dims {
   int32_t B, T, H, L, K, V;
   int32_t dtype;
   float scale;
+  int32_t hold_partial;
 } ngdn_dims;
 
 /* Last error message on this thread ("" when none). */
@@ -57,8 +65,8 @@ const char* ngdn_last_error(void);
  * (for instance ngdn_probe_bwd's bank-gradient argument: an accumulator
  * [L-1,H,n_max,K] before 0.2.0, the per-firing workspace ws_dbank
  * [B,H,NF,N,K] since), so an older caller can link and then write past its
- * buffers. */
-#define NGDN_VERSION 300
+ * buffers. 0.4.0 added ngdn_dims.hold_partial (the struct grew by 4 bytes). */
+#define NGDN_VERSION 400
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);

@@ -20,13 +20,14 @@ NGDN_BF16 = 1
 # NGDN_VERSION of include/ngdn.h: the interface the signatures below describe.
 # The loader refuses a library of another version (working-tensor layouts and
 # argument meanings changed between versions under unchanged signatures).
-VERSION = 300
+VERSION = 400
 
 
 class Dims(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int32), ("T", ctypes.c_int32), ("H", ctypes.c_int32),
                 ("L", ctypes.c_int32), ("K", ctypes.c_int32), ("V", ctypes.c_int32),
-                ("dtype", ctypes.c_int32), ("scale", ctypes.c_float)]
+                ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
+                ("hold_partial", ctypes.c_int32)]
 
 
 P = ctypes.c_void_p
@@ -163,5 +164,5 @@ class GateArgs(ctypes.Structure):
                     "dbz", "dwz", "dml", "dpar", "ws")])
 
 
-def dims(B, T, H, L, K, V, dtype_code, scale):
-    return Dims(B, T, H, L, K, V, dtype_code, float(scale))
+def dims(B, T, H, L, K, V, dtype_code, scale, hold_partial=False):
+    return Dims(B, T, H, L, K, V, dtype_code, float(scale), int(hold_partial))

@@ -164,8 +164,17 @@ def _rows(b0, nb):
     return lambda t: None if t is None else t[b0:b0 + nb]
 
 
+def _fire_chunks(T, fire_partial):
+    """Chunks whose end can complete an upper level's firing: every chunk,
+    or (fire_partial False) the whole ones only, so that a partial last
+    chunk fires nothing, as the decoding step treats an incomplete chunk
+    (the library's ngdn_dims.hold_partial)."""
+    NT = -(-T // 64)
+    return NT if fire_partial else T // 64
+
+
 def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
-             init, promotion, train):
+             init, promotion, train, fire_partial=True):
     """Runs the forward kernels. Returns (o, final_state [B,H,L,K,V] fp32,
     working tensors kept for the backward when ``train``)."""
     B, T, H, _, K = q.shape
@@ -173,6 +182,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     dev = q.device
     wd, code = _working_dtype(q)
     NT = -(-T // 64)
+    NTF = _fire_chunks(T, fire_partial)
     cvt = lambda x: x.to(wd).contiguous()  # noqa: E731
     q_, k_, v_, b_, w_, mix_ = (cvt(x) for x in (q, k, v, b, w, mix))
     g_ = g.to(torch.float32).contiguous()
@@ -200,7 +210,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     if L > 1:
         par = _params(qb, kp, bp, wp, gp, wd, train)
     for lvl in range(1, L):
-        nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
+        nf, ng = n_firings(NTF, f[lvl]), n_groups(NT, f[lvl])
         N = K if merge else nq[lvl - 1]
         nf1 = max(nf, 1)
         if FUSED_PROMOTION and _chain_ok(K, N, merge):
@@ -232,7 +242,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     def launch(b0, nb, st):
         R = _rows(b0, nb)
         sp = _lib.ptr_of_stream(st)
-        d = _lib.dims(nb, T, H, L, K, V, code, scale)
+        d = _lib.dims(nb, T, H, L, K, V, code, scale, hold_partial=NTF < NT)
         _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
             q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, TT)), sp)
         _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
@@ -269,7 +279,7 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     saved = None
     if train:
         saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
-                     KtT=KtT, Aqk=Aqk, gam=gam, TT=TT,
+                     KtT=KtT, Aqk=Aqk, gam=gam, TT=TT, NTF=NTF,
                      hT=hT, h=h_, vn=vn_, read0=read0, states=states,
                      statesT=statesT, levels=levels, final=final, par=par,
                      code=code, wd=wd)
@@ -376,7 +386,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     def launch(b0, nb, st):
         R = _rows(b0, nb)
         sp = _lib.ptr_of_stream(st)
-        d = _lib.dims(nb, T, H, L, K, V, code, scale)
+        d = _lib.dims(nb, T, H, L, K, V, code, scale, hold_partial=sv["NTF"] < NT)
         # With one group of rows, independent launches go to two side streams:
         # (a) the reads' backward of the levels below the top one
         # (each writes its own columns of dmix and dq and its own d_states)
@@ -474,7 +484,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     groups = _run_groups(B, dev, launch)
     if groups > 1:
         st = torch.cuda.current_stream(dev)
-        d = _lib.dims(B, T, H, L, K, V, code, scale)
+        d = _lib.dims(B, T, H, L, K, V, code, scale, hold_partial=sv["NTF"] < NT)
         for lvl in range(L - 1, 0, -1):
             if levels[lvl]["nf"] > 0:
                 param_grads(d, lvl, _lib.ptr_of_stream(st), st)
@@ -517,7 +527,7 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
     def forward(ctx, q, k, v, g, b, w, mix_weights, query_banks, key_projections,
                 b_projections, w_projections, g_projections, n_queries_per_level,
                 firing_intervals, L, scale, initial_state, output_final_state,
-                chunk_size, promotion):
+                chunk_size, promotion, fire_partial_chunk=True):
         L = int(L)
         f = _as_ints(firing_intervals, L)
         nq = _as_ints(n_queries_per_level, L - 1) if L > 1 else []
@@ -532,7 +542,7 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         o, final, saved = _forward(q, k, v, g, b, w, mix_weights, query_banks,
                                    key_projections, b_projections, w_projections,
                                    g_projections, nq, f, L, scale, initial_state,
-                                   promotion, train)
+                                   promotion, train, fire_partial_chunk)
         o = o.to(q.dtype)
         ctx.meta = (L, scale, f, nq, initial_state is not None, promotion)
         ctx.dtypes = [None if t is None else t.dtype
@@ -564,17 +574,25 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         else:
             out += [None] * 5
         return (*out, None, None, None, None,
-                dinit.to(dts[12]) if dinit is not None else None, None, None, None)
+                dinit.to(dts[12]) if dinit is not None else None, None, None, None, None)
 
 
 def chunk_nested_gdn2(q, k, v, g, b, w, mix_weights, query_banks, key_projections,
                       b_projections, w_projections, g_projections, n_queries_per_level,
                       firing_intervals, L, scale=None, initial_state=None,
-                      output_final_state=False, chunk_size=64, promotion="learned"):
+                      output_final_state=False, chunk_size=64, promotion="learned",
+                      fire_partial_chunk=True):
     """Differentiable chunkwise NestedGDN-2. Signature matches the reference op
     (nested_gdn2/ops/chunk.py:722-743) and its naive twin (ops/naive.py:226-247).
 
     Returns (o [B, T, H, V] in q's dtype, final_state [B, H, L, K, V] fp32 or None).
+
+    ``fire_partial_chunk`` (an addition; the reference's chunk form always
+    fires): with False, a partial last chunk completes no upper level's
+    firing, as the reference's decoding step treats an incomplete chunk
+    (ops/naive.py:101-113). The op then gives, for any T, what the reference
+    layer computes by running whole chunks through the chunk op and stepping
+    the rest (layers/nested_gdn2.py:196-224), differentiable throughout.
 
     K != V with upper levels (the layer's expand_v != 1) runs the K = V
     kernels at D = max(K, V) on zero-padded inputs and parameters: the padded
@@ -597,12 +615,12 @@ def chunk_nested_gdn2(q, k, v, g, b, w, mix_weights, query_banks, key_projection
             q, k, v, g, b, w, mix_weights, query_banks, key_projections, b_projections,
             w_projections, g_projections, n_queries_per_level, firing_intervals, L,
             K ** -0.5 if scale is None else scale, initial_state, output_final_state,
-            chunk_size, promotion)
+            chunk_size, promotion, fire_partial_chunk)
         return o[..., :V], (fin[..., :K, :V] if fin is not None else None)
     return ChunkNestedGDN2Function.apply(
         q, k, v, g, b, w, mix_weights, query_banks, key_projections, b_projections,
         w_projections, g_projections, n_queries_per_level, firing_intervals, L,
-        scale, initial_state, output_final_state, chunk_size, promotion)
+        scale, initial_state, output_final_state, chunk_size, promotion, fire_partial_chunk)
 
 
 def pad_kv(K, V, *, q=None, k=None, v=None, g=None, b=None, w=None, query_banks=None,

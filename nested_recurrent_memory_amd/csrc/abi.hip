@@ -37,10 +37,16 @@ int32_t check_dims(const ngdn_dims* d, const char* what) {
     return fail(NGDN_EINVAL, "%s: K=%d V=%d unsupported (64 or 128)", what, d->K, d->V);
   if (d->dtype != NGDN_F32 && d->dtype != NGDN_BF16)
     return fail(NGDN_EINVAL, "%s: dtype %d unsupported", what, d->dtype);
+  if (d->hold_partial != 0 && d->hold_partial != 1)
+    return fail(NGDN_EINVAL, "%s: hold_partial %d is neither 0 nor 1", what, d->hold_partial);
   return NGDN_OK;
 }
 
 inline int nchunks(const ngdn_dims* d) { return (d->T + ngdn::CH - 1) / ngdn::CH; }
+// chunks whose end can complete an upper level's firing
+inline int fire_chunks(const ngdn_dims* d) {
+  return d->hold_partial ? d->T / ngdn::CH : nchunks(d);
+}
 
 }  // namespace
 
@@ -115,7 +121,6 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
     return fail(NGDN_EINVAL, "ngdn_probe_fwd: firing intervals must be positive");
   if (!below || !final_state || !bpT || !wpT || !gpT || !A || !KT || !U || !gam)
     return fail(NGDN_EINVAL, "ngdn_probe_fwd: NULL tensor");
-  const int NT = nchunks(d);
   const long long skv = (long long)d->K * d->V;
   ngdn::ProbeArgs a{};
   a.below = below; a.below_mode = level == 1 ? 0 : 1; a.NGb = ng_below;
@@ -133,7 +138,7 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.merge = promotion;
   a.A = A; a.KT = KT; a.U = U; a.gam = gam; a.keysN = keysN; a.AT = AT;
   a.keys = keys; a.vals = vals; a.bo = bo; a.wo = wo; a.go = go;
-  a.B = d->B; a.H = d->H; a.NF = NT / f_here; a.N = N; a.V = d->V;
+  a.B = d->B; a.H = d->H; a.NF = fire_chunks(d) / f_here; a.N = N; a.V = d->V;
   if (a.NF == 0) return NGDN_OK;
   return launched(ngdn::probe_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_probe_fwd");
 }
@@ -191,7 +196,7 @@ int32_t ngdn_promote_chain_fwd(const ngdn_dims* d, int32_t level, int32_t promot
   a.st_kv = states; a.st_vk = statesT;
   a.fin = final_state + (long long)level * skv; a.fin_sh = a.init_sh; a.fin_sb = a.init_sb;
   a.keysN = keysN; a.AT = AT; a.gam = gam;
-  a.B = d->B; a.H = d->H; a.NF = NT / f_here; a.NG = (NT + f_here - 1) / f_here;
+  a.B = d->B; a.H = d->H; a.NF = fire_chunks(d) / f_here; a.NG = (NT + f_here - 1) / f_here;
   return launched(ngdn::promote_chain_fwd(a, d->dtype, d->K, N, promotion == 1,
                                           (hipStream_t)stream), what);
 }
@@ -323,7 +328,7 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
   if (!W || !KtT || !gam || !Qg || !Aqk || !dout || !mix || !dSp || (!dVn && !dVnT))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: NULL tensor");
   const int NT = nchunks(d);
-  if (inj && (f1 <= 0 || nf1 != NT / f1))
+  if (inj && (f1 <= 0 || nf1 != fire_chunks(d) / f1))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: injection count %d inconsistent with f1=%d", nf1, f1);
   const long long skv = (long long)d->K * d->V;
   ngdn::ScanBwdArgs a{};
@@ -454,7 +459,6 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: NULL tensor");
   if (level == 1 ? !inj : (!d_below || !d_final))
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: lower-level gradient destination missing");
-  const int NT = nchunks(d);
   const long long skv = (long long)d->K * d->V;
   ngdn::ProbeBwdArgs a{};
   a.f.below = nullptr; a.f.below_mode = level == 1 ? 0 : 1; a.f.NGb = ng_below;
@@ -471,7 +475,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.f.kp = lvl(key_projections, hkv);
   a.f.bpT = lvl(bpT, hkv); a.f.wpT = lvl(wpT, hkv); a.f.gpT = lvl(gpT, hkv);
   a.f.merge = promotion;
-  a.f.B = d->B; a.f.H = d->H; a.f.NF = NT / f_here; a.f.N = N; a.f.V = d->V;
+  a.f.B = d->B; a.f.H = d->H; a.f.NF = fire_chunks(d) / f_here; a.f.N = N; a.f.V = d->V;
   a.kpT = lvl(kpT, hkv); a.bankT = lvl(bankT, (size_t)d->H * n_max * d->K);
   a.bp = lvl(bp, hkv); a.wp = lvl(wp, hkv); a.gp = lvl(gp, hkv);
   a.Sg = states; a.SgT = statesT; a.NG = ng;

@@ -482,7 +482,7 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
       o.dor = DV{};
       o.dm = E(0.f);
     }
-    o.has_add = a.inj && (j + 1) % a.inj_every == 0;
+    o.has_add = a.inj && (j + 1) % a.inj_every == 0 && (j + 1) / a.inj_every <= a.inj_nf;
     if (o.has_add) read_kv(a.inj + ((size_t)bh * a.inj_nf + (j + 1) / a.inj_every - 1) * K * V, o.add);
   };
   // the operand fragments of the current step

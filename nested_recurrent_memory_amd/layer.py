@@ -8,7 +8,8 @@ projections -> ShortConvolution + SiLU (or a plain SiLU) -> per-head L2
 normalisation of q and k -> decay g0 = -exp(A_log) softplus(f_proj x + dt_bias)
 (clamped at -1/max_horizon when set), gates b0 = sigmoid(b_proj x),
 w0 = sigmoid(w_proj x), mix = softmax (or sigmoid) of mix_proj x -> the op
-over whole chunks from an aligned position and the decoding step for the rest
+from an aligned position (its partial last chunk firing no upper level, as
+the reference's stepped tail does not) and the decoding step from any other
 -> FusedRMSNormGated(o, g_proj x) -> o_proj.
 
 The matrix products of the projections are torch.nn.Linear (hipBLASLt); the
@@ -49,7 +50,7 @@ class _nullcontext:
 
 
 class _ForwardOnlyTail(torch.autograd.Function):
-    """The stepped tail's output joined to the graph of ``anchor``: forward
+    """The stepped tokens' output joined to the graph of ``anchor``: forward
     returns it as is; a backward that carries a nonzero gradient into it
     raises (the decoding step has no backward)."""
 
@@ -62,9 +63,9 @@ class _ForwardOnlyTail(torch.autograd.Function):
     def backward(ctx, grad):
         if grad is None or not bool(grad.ne(0).any()):
             return None, None
-        raise RuntimeError("NestedGDN2Attention: the tokens past the last whole chunk are "
-                           "stepped, and the decoding step has no backward; train with T a "
-                           "multiple of the chunk size (64) from an aligned position")
+        raise RuntimeError("NestedGDN2Attention: a call continuing a cache from a position "
+                           "that is not a multiple of the chunk size (64) is stepped, and the "
+                           "decoding step has no backward; train from an aligned position")
 
 
 @dataclass
@@ -192,29 +193,33 @@ class NestedGDN2Attention(nn.Module):
         state, position = (last["recurrent_state"] if last is not None
                            else (None, x.new_zeros(B, dtype=torch.long)))
         BT = cfg.op_chunk_size
-        # whole chunks from an aligned position run chunkwise, the rest steps
-        # (the chunk form fires on a partial last chunk, the step form does
-        # not). The position is read back to the host only when it matters:
-        # without a cache it is 0, and a call shorter than a chunk (a decoding
-        # step) steps whatever it is; a host synchronisation per layer would
-        # stall the launch queue
-        aligned = T >= BT and (last is None or bool((position % BT == 0).all()))
-        n_chunked = (T // BT) * BT if aligned else 0
+        # From an aligned position the whole call runs chunkwise, its partial
+        # last chunk firing nothing: the reference's composition (whole chunks
+        # chunkwise, the rest stepped, the step firing only at a chunk's end,
+        # layers/nested_gdn2.py:196-224) in one differentiable op. From an
+        # unaligned position every token steps. The position is read back to
+        # the host only when it matters: without a cache it is 0, and a call
+        # shorter than a chunk with no gradient to carry (a decoding step)
+        # steps whatever it is; a host synchronisation per layer would stall
+        # the launch queue
+        grad = torch.is_grad_enabled() and q.requires_grad
+        aligned = last is None or ((T >= BT or grad) and bool((position % BT == 0).all()))
+        n_chunked = T if aligned else 0
         parts = []
         if n_chunked:
             o_chunk, state = chunk_nested_gdn2(
-                q=q[:, :n_chunked], k=k[:, :n_chunked], v=v[:, :n_chunked], g=g0[:, :n_chunked],
-                b=b0[:, :n_chunked], w=w0[:, :n_chunked], mix_weights=mix[:, :n_chunked],
-                initial_state=state, output_final_state=True, chunk_size=BT, **promo)
+                q=q, k=k, v=v, g=g0, b=b0, w=w0, mix_weights=mix, initial_state=state,
+                output_final_state=True, chunk_size=BT, fire_partial_chunk=False, **promo)
             parts.append(o_chunk)
             position = position + n_chunked
         elif state is None:
             state = x.new_zeros(B, H, L, K, V, dtype=torch.float32)
-        # The step is forward-only: a tail that is part of a graph is stepped
-        # on detached values and joins the graph through _ForwardOnlyTail,
-        # whose backward raises, so only an actual backward through it fails
-        # (the reference's step is differentiable, ops/naive.py:42-134)
-        anchor = q if (n_chunked < T and torch.is_grad_enabled() and q.requires_grad) else None
+        # The step is forward-only: a stepped call that is part of a graph
+        # runs on detached values and joins the graph through
+        # _ForwardOnlyTail, whose backward raises, so only an actual backward
+        # through it fails (the reference's step is differentiable,
+        # ops/naive.py:42-134)
+        anchor = q if (n_chunked < T and grad) else None
         tail = []
         with torch.no_grad() if anchor is not None else _nullcontext():
             if anchor is not None and state is not None:

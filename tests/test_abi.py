@@ -51,6 +51,24 @@ def test_invalid_arguments_return_error_without_launch():
     rc = so.ngdn_probe_fwd(ctypes.byref(d), 1, 0, 24, 1, 2, None, 0, None, None, 32,
                            *([None] * 16))
     assert rc == 1 and b"power of two" in so.ngdn_last_error()
+    d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
+    d.hold_partial = 2
+    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 14))
+    assert rc == 1 and b"hold_partial 2" in so.ngdn_last_error()
+
+
+def test_dims_struct_matches_header():
+    """The ctypes mirror of ngdn_dims has the header's fields, in order and
+    with the header's types, so the library reads hold_partial where the
+    caller wrote it."""
+    text = open(os.path.join(ROOT, "include", "ngdn.h")).read()
+    body = re.search(r"typedef struct ngdn_dims \{(.*?)\} ngdn_dims;", text, re.S).group(1)
+    fields = []
+    for ty, names in re.findall(r"(int32_t|float)\s+([^;]+);", body):
+        fields += [(n.strip(), ty) for n in names.split(",")]
+    ct = {"int32_t": ctypes.c_int32, "float": ctypes.c_float}
+    assert [(n, ct[t]) for n, t in fields] == list(_lib.Dims._fields_)
+    assert ctypes.sizeof(_lib.Dims) == 36
 
 
 def test_step_noalloc_validates_before_any_hip_call():

@@ -8,7 +8,8 @@
   max(1, max|ref|).
 * NestedGDN2Attention: output and every gradient (input and parameters)
   against the oracle layer with the same parameter values, for training
-  (whole chunks), prefill with a stepped tail, and decoding with the cache.
+  (whole chunks, and ragged lengths through the op with a held partial
+  chunk), prefill, and decoding with the cache.
   The layer's projections are torch Linear layers whose outputs round to the
   activation dtype between the kernels, so the bar here is norm-wise:
   ||got - ref|| <= tol ||ref|| with tol 1e-4 in fp32 and 2e-2 in bf16 (one
@@ -254,8 +255,9 @@ def test_layer_training_step_matches_oracle(dtype, case):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("case", LAYER_CASES[:2], ids=[c[0] for c in LAYER_CASES[:2]])
 def test_layer_prefill_and_decode_match_oracle(dtype, case):
-    """Prefill of 100 tokens (one chunk, then 36 decoding steps), then three
-    single-token calls with the cache, as generation runs the layer."""
+    """Prefill of 100 tokens (through the op, its partial second chunk firing
+    nothing), then three single-token calls with the cache (stepped from
+    position 100), as generation runs the layer."""
     name, kw = case
     print(f"layer decode dtype={dtype} case={name}", flush=True)
     cfg, layer, p64 = _layer(dtype, 21, **kw)
@@ -278,24 +280,60 @@ def test_layer_prefill_and_decode_match_oracle(dtype, case):
             _near("conv_state", got, want, dtype)
 
 
-def test_layer_tail_with_grad_runs_forward_and_raises_in_backward():
-    """A call whose last tokens are stepped (T = 70: one chunk, then 6 steps)
-    runs with grad enabled and gives the no-grad output; only a backward
-    through the stepped tokens raises (the decoding step has no backward)."""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("T", [70, 100])
+@pytest.mark.parametrize("case", LAYER_CASES[:2], ids=[c[0] for c in LAYER_CASES[:2]])
+def test_layer_ragged_training_matches_oracle(dtype, T, case):
+    """T not a multiple of the chunk: the layer runs the whole call through
+    the op with its partial last chunk firing nothing, differentiably; the
+    oracle layer composes the reference's way (whole chunks chunkwise, the
+    rest stepped, layers/nested_gdn2.py:196-224). Output, the cached state
+    and every gradient."""
+    name, kw = case
+    print(f"layer ragged train dtype={dtype} T={T} case={name}", flush=True)
+    cfg, layer, p64 = _layer(dtype, 13, **kw)
+    g = _gen(14)
+    x = torch.randn(2, T, cfg.hidden_size, generator=g).to(dtype)
+    dy = torch.randn(2, T, cfg.hidden_size, generator=g).to(dtype)
+
+    x64 = x.double().requires_grad_()
+    o64, c64 = lref.layer_forward(p64, x64, cfg)
+    (o64 * dy.double()).sum().backward()
+
+    xd = x.to(DEV).requires_grad_()
+    o, _, pkv = layer(xd, past_key_values={}, use_cache=True)
+    o.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    _near("o", o, o64, dtype)
+    state, pos = pkv[0]["recurrent_state"]
+    assert pos.tolist() == [T, T]
+    _near("state", state, c64["recurrent_state"][0], dtype)
+    _near("dx", xd.grad, x64.grad, dtype)
+    for pname, p in layer.named_parameters():
+        wide = dtype == torch.bfloat16 and pname in ("A_log", "dt_bias")
+        _near(f"d{pname}", p.grad, p64[pname].grad, dtype, DECAY_BF16_TOL if wide else None)
+
+
+def test_layer_unaligned_continuation_with_grad_raises_in_backward():
+    """A call continuing a cache from position 70 (not a multiple of 64) is
+    stepped: with grad enabled it gives the no-grad output, and only a
+    backward through the stepped tokens raises (the decoding step has no
+    backward)."""
     cfg, layer, _ = _layer(torch.float32, 31, num_levels=2, firing_intervals=(1, 2),
                            n_queries_per_level=(16,))
-    x = torch.randn(1, 70, cfg.hidden_size, device=DEV, requires_grad=True)
-    o, _, _ = layer(x)
-    assert o.requires_grad
+    x = torch.randn(1, 80, cfg.hidden_size, device=DEV)
     with torch.no_grad():
-        want, _, _ = layer(x)
+        _, _, pkv = layer(x[:, :70], past_key_values={}, use_cache=True)
+    snap = {0: {"recurrent_state": tuple(t.clone() for t in pkv[0]["recurrent_state"]),
+                "conv_state": tuple(t.clone() for t in pkv[0]["conv_state"])}}
+    with torch.no_grad():
+        want, _, _ = layer(x[:, 70:], past_key_values=snap, use_cache=True)
+    xg = x[:, 70:].clone().requires_grad_()
+    o, _, _ = layer(xg, past_key_values=pkv, use_cache=True)
+    assert o.requires_grad
     assert torch.equal(o.detach(), want)
     with pytest.raises(RuntimeError, match="no backward"):
         o.sum().backward()
-    x.grad = None
-    o, _, _ = layer(x)
-    o[:, :64].sum().backward()                 # the chunked part alone differentiates
-    assert x.grad is not None and torch.isfinite(x.grad).all()
 
 
 def test_layer_at_model_config_shape_matches_oracle():
