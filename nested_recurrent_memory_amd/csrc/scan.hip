@@ -23,6 +23,9 @@
 #ifndef SCAN_WAVES_128
 #define SCAN_WAVES_128 4
 #endif
+#ifndef SCAN_LATE_STORES
+#define SCAN_LATE_STORES 1
+#endif
 
 namespace ngdn {
 
@@ -97,7 +100,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     SF a[NAR][NSK];             // A rows of this wave's Vn tiles
     float u[NVP][4];            // U at the Vn tiles
     SF bt[TRT][NSM];            // BT rows of this wave's state tiles
-    float g[TRT][4];            // gam at the state rows
+    f4 g[TRT];                  // gam at the state rows (one 16-byte load)
     SF qg[RA][RQ];              // OUT: Qg rows of this wave's tiles
     SF aq[RA][RP];              // OUT: Aqk rows
   };
@@ -153,8 +156,7 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
         o.bt[t][s] = FRB ? Bj.get(frag_at(rt, s, M))
                         : (!PADM || s * KS + kofs<E>(lane) < M) ? Bj.get(brow + s * KS)
                                                                 : Mma<E>::szero();
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
+      o.g[t] = *reinterpret_cast<const f4*>(Gj + rt * 16 + acc_row(0));
     }
   };
 
@@ -181,6 +183,8 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   // (fp32 operands with K = 128 and M >= 64 keep the stores in place: the
   // held Vn tiles would not fit in their registers)
   constexpr bool DEFER = OUT || sizeof(E) == 2 || K < 128 || M < 64;
+  // LATE: stores after the step's products instead of at its start
+  constexpr bool LATE = SCAN_LATE_STORES && DEFER;
   f4 pvn[NVP], prd[OUT ? NVP : 1];
   auto flush_tile = [&](int jj, int p) {
       int rt, ct;
@@ -207,93 +211,111 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
     for (int p = 0; p < NVP; ++p) flush_tile(jj, p);
   };
 
-  Ops nxt;
-  if (S > 0) load(0, nxt);
-  for (int j = 0; j < S; ++j) {
-    const Ops cur = nxt;
-
-    // ---- state entering step j (and the previous step's Vn and read) to
-    // global, then the next step's operand loads
-    store_state(j);
-    if (DEFER && j > 0) flush(j - 1);
-    if (j + 1 < S) load(j + 1, nxt);
-
-    // ---- the state, transposed, to LDS
+  // One step with its operands already loaded.
+  auto step = [&](int j, const Ops& cur) {
+      // ---- the state, transposed, to LDS
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
-      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-      sST.put4(vl * LDS_ST + k0, st[i]);
-    }
-    lds_barrier();
-
-    // ---- Vn = U - A S (and, OUT, the read's Qg S on the same tiles)
-    f4 rd[OUT ? NVP : 1];
-#pragma unroll
-    for (int p = 0; p < NVP; ++p) {
-      int rt, ct;
-      if (vn_tile(p, rt, ct)) {
-        f4 acc = f4_zero();
-        if constexpr (OUT) rd[p] = f4_zero();
-        const int brow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
-#pragma unroll
-        for (int s = 0; s < NSK; ++s) {
-          const auto fb = sST.get(brow + s * KS);
-          acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], fb);
-          if constexpr (OUT) {
-            rd[p] = Mma<E>::mma(rd[p], cur.qg[ONE_RT ? 0 : p / CT][s], fb);
-          }
-        }
-        const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-        f4 vn;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][r] - acc[r];
-        sVn.put4(vl * LDS_VN + m0, vn);
-        pvn[p] = vn;
-        if constexpr (!DEFER) flush_tile(j, p);
+      for (int i = 0; i < TPW; ++i) {
+        const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+        const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+        sST.put4(vl * LDS_ST + k0, st[i]);
       }
-    }
-    lds_barrier();
+      lds_barrier();
 
-    // ---- OUT: read0 = Qg S + Aqk Vn for the chunk's rows in the sequence
-    if constexpr (OUT) {
+      // ---- Vn = U - A S (and, OUT, the read's Qg S on the same tiles)
+      f4 rd[OUT ? NVP : 1];
 #pragma unroll
       for (int p = 0; p < NVP; ++p) {
         int rt, ct;
         if (vn_tile(p, rt, ct)) {
-          const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+          f4 acc = f4_zero();
+          if constexpr (OUT) rd[p] = f4_zero();
+          const int brow = (ct * 16 + (lane & 15)) * LDS_ST + kofs<E>(lane);
 #pragma unroll
-          for (int s = 0; s < NSM; ++s) {
-            rd[p] = Mma<E>::mma(rd[p], cur.aq[ONE_RT ? 0 : p / CT][s], sVn.get(brow + s * KS));
+          for (int s = 0; s < NSK; ++s) {
+            const auto fb = sST.get(brow + s * KS);
+            acc = Mma<E>::mma(acc, cur.a[ONE_RT ? 0 : p / CT][s], fb);
+            if constexpr (OUT) {
+              rd[p] = Mma<E>::mma(rd[p], cur.qg[ONE_RT ? 0 : p / CT][s], fb);
+            }
           }
-          prd[p] = rd[p];
+          const int m0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+          f4 vn;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vn[r] = cur.u[p][r] - acc[r];
+          sVn.put4(vl * LDS_VN + m0, vn);
+          pvn[p] = vn;
+          if constexpr (!DEFER) flush_tile(j, p);
         }
       }
-    }
+      lds_barrier();
 
-    // ---- S <- diag(gam) S + BT Vn
+      // ---- OUT: read0 = Qg S + Aqk Vn for the chunk's rows in the sequence
+      if constexpr (OUT) {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      // t must be a compile-time index into the operand registers
-      constexpr bool WHOLE = TPW % CT == 0;
-      const int t = WHOLE ? i / CT : 0;
-      const int ct = WHOLE ? i % CT : (wv * TPW + i) % CT;
+        for (int p = 0; p < NVP; ++p) {
+          int rt, ct;
+          if (vn_tile(p, rt, ct)) {
+            const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) st[i][r] *= cur.g[t][r];
-      const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
-#pragma unroll
-      for (int s = 0; s < NSM; ++s) {
-        // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
-        const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
-        typename Mma<E>::SFrag fb = Mma<E>::szero();
-        if (live) fb = sVn.get(brow + s * KS);
-        st[i] = Mma<E>::mma(st[i], cur.bt[t][s], fb);
+            for (int s = 0; s < NSM; ++s) {
+              rd[p] = Mma<E>::mma(rd[p], cur.aq[ONE_RT ? 0 : p / CT][s], sVn.get(brow + s * KS));
+            }
+            prd[p] = rd[p];
+          }
+        }
       }
-    }
+      if constexpr (LATE) {
+        // ---- this step's stores after its products, while the next step's
+        // operand loads (issued before them) are in flight: the stores neither
+        // hold the wave up behind those loads nor delay their completion. The
+        // state registers still hold the state entering step j.
+        store_state(j);
+        flush(j);
+      }
+
+      // ---- S <- diag(gam) S + BT Vn
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        // t must be a compile-time index into the operand registers
+        constexpr bool WHOLE = TPW % CT == 0;
+        const int t = WHOLE ? i / CT : 0;
+        const int ct = WHOLE ? i % CT : (wv * TPW + i) % CT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[i][r] *= cur.g[t][r];
+        const int brow = (ct * 16 + (lane & 15)) * LDS_VN + kofs<E>(lane);
+#pragma unroll
+        for (int s = 0; s < NSM; ++s) {
+          // M = 16 with 32-deep bf16 MFMAs: the upper half of the k range is zero
+          const bool live = !PADM || (s * KS + kofs<E>(lane) < M);
+          typename Mma<E>::SFrag fb = Mma<E>::szero();
+          if (live) fb = sVn.get(brow + s * KS);
+          st[i] = Mma<E>::mma(st[i], cur.bt[t][s], fb);
+        }
+      }
     // no barrier needed here: the next writes to s_st do not alias s_vn, and
     // the next writes to s_vn follow the next step's barrier
+  };
+
+  Ops nxt;
+  if (S > 0) load(0, nxt);
+  for (int j = 0; j < S; ++j) {
+    const Ops cur = nxt;
+    if constexpr (LATE) {
+      // ---- the next step's operand loads first (the last step reloads its
+      // own, so that no branch guards them); this step's stores follow its
+      // products
+      load(j + 1 < S ? j + 1 : j, nxt);
+    } else {
+      // ---- state entering step j (and the previous step's Vn and read) to
+      // global, then the next step's operand loads
+      store_state(j);
+      if (DEFER && j > 0) flush(j - 1);
+      if (j + 1 < S) load(j + 1, nxt);
+    }
+    step(j, cur);
   }
-  if (DEFER && S > 0) flush(S - 1);
+  if (!LATE && DEFER && S > 0) flush(S - 1);
   if (a.state_mode == 1) {
     for (int j = S; j < a.NG; ++j) store_state(j);
   }

@@ -499,8 +499,7 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
     if constexpr (BF) return CW::frag(oG, t, s); else return o.qg[t][s];
   };
 
-  // dVn of a step is stored at the start of the step after it, beside dS',
-  // ahead of that step's operand loads (the vector memory pipe is in order)
+  // dVn of a step, stored after the step's dVn products
   f4 pdv[CT];
   auto flush_dv = [&](int jj) {
 #pragma unroll
@@ -533,18 +532,10 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
       for (int i = 0; i < TPW; ++i) ds[i] += cur.add[i];
     }
 
-    // ---- dS' (and the previous step's dVn) to global, then the next step's
-    // operand loads
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
-      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
-      float* o = a.dSp + ((size_t)bh * S + j) * K * V + (size_t)k0 * V + v0 + vl;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[(size_t)r * V] = ds[i][r];
-    }
-    if (j + 1 < S) flush_dv(j + 1);
-    if (j > 0) load(j - 1, nxt);
+    // ---- the next step's operand loads (the last step reloads its own, so
+    // that no branch guards them); this step's dS' and dVn are stored after
+    // its dVn products, while those loads are in flight
+    load(j > 0 ? j - 1 : 0, nxt);
 
     // ---- dS' and mix_0 dO staged (transposed) as B operands
 #pragma unroll
@@ -584,6 +575,17 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
     }
     lds_barrier();
 
+    // ---- dS' (the state gradient still holds it) and dVn to global
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int g = wv * TPW + i, rt = g / CT, ct = g % CT;
+      const int k0 = rt * 16 + acc_row(0), vl = ct * 16 + acc_col();
+      float* o = a.dSp + ((size_t)bh * S + j) * K * V + (size_t)k0 * V + v0 + vl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[(size_t)r * V] = ds[i][r];
+    }
+    flush_dv(j);
+
     // ---- dS = diag(gam) dS' - W^T dVn + Qg^T dO
 #pragma unroll
     for (int t = 0; t < TRT; ++t) {
@@ -610,7 +612,6 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
     // s_dot and s_dvn are rewritten by the next step
     lds_barrier();
   }
-  if (S > 0) flush_dv(0);
   if (a.dinit) {
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
