@@ -255,7 +255,9 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
       for (int u = 0; u < PO; ++u) {
         const int e = tid + 256 * u, i = e / (V / VE), c = (e % (V / VE)) * VE;
         const v4i z = {0, 0, 0, 0};
-        xo[u] = i < nvalid ? *reinterpret_cast<const v4i*>(dob + (size_t)(t0 + i) * H * V + c) : z;
+        // rows past the end read the last valid row, then take zero (no branch)
+        const v4i x = *reinterpret_cast<const v4i*>(dob + (size_t)(t0 + min(i, nvalid - 1)) * H * V + c);
+        xo[u] = i < nvalid ? x : z;
       }
       if (tid < C)
         s_m0[tid] = tid < nvalid ? to_f(static_cast<const E*>(a.mix)[((size_t)b * T + t0 + tid) * H * a.L +

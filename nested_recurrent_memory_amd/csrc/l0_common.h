@@ -60,10 +60,14 @@ struct ChunkIn {
   // their VE values as floats: a load read ahead this way is not waited for
   // until raw16_vals converts it.
   typedef __attribute__((__vector_size__(16))) int R16;
+  // Rows past the end read the last valid row and then take zero: the load
+  // is not under a branch, so no register copy at a branch merge has to wait
+  // for it (and for every load issued before it).
   __device__ __forceinline__ R16 raw16(const E* p, size_t row, int i, int c0) const {
-    R16 r = {0, 0, 0, 0};
-    if (i < nvalid) r = *reinterpret_cast<const R16*>(p + (size_t)(t0 + i) * row + c0);
-    return r;
+    const int ic = i < nvalid ? i : nvalid - 1;
+    const R16 x = *reinterpret_cast<const R16*>(p + (size_t)(t0 + ic) * row + c0);
+    const R16 z = {0, 0, 0, 0};
+    return i < nvalid ? x : z;
   }
   __device__ __forceinline__ static void raw16_vals(R16 x, float* out) {
     if constexpr (std::is_same<E, float>::value) {
@@ -180,16 +184,24 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
   // Every global load of the phase first, all in flight together: this
   // wave's rows of b, k, q, and the k rows of the earlier tiles J < I (the
   // rows of tile I are this wave's own)
+  // The loads are unconditional (rows past the sequence end read its last
+  // row, tiles J >= I this wave's own rows again) and the unwanted values are
+  // zeroed afterwards: a load under a branch leaves a register copy at the
+  // merge, and the copy waits for every load issued before it.
   FR bo[NKS], ko[NKS], qo[NKS], kj[3][NKS];
   {
     const bool live = ri < in.nvalid;
-    const size_t rowk = (size_t)(in.t0 + ri) * in.rowK, rowq = (size_t)(in.t0 + ri) * in.rowQ;
+    const int ric = live ? ri : in.nvalid - 1;
+    const size_t rowk = (size_t)(in.t0 + ric) * in.rowK, rowq = (size_t)(in.t0 + ric) * in.rowQ;
+    const bool use_q = live && (want_q || ro.Qg);
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-      bo[s] = live ? Mma<E>::ld(in.b + rowk + c0) : Mma<E>::zero();
-      ko[s] = live ? Mma<E>::ld(in.k + rowk + c0) : Mma<E>::zero();
-      qo[s] = (live && (want_q || ro.Qg)) ? Mma<E>::ld(in.q + rowq + c0) : Mma<E>::zero();
+      const FR xb = Mma<E>::ld(in.b + rowk + c0), xk = Mma<E>::ld(in.k + rowk + c0);
+      const FR xq = Mma<E>::ld(in.q + rowq + c0);
+      bo[s] = live ? xb : Mma<E>::zero();
+      ko[s] = live ? xk : Mma<E>::zero();
+      qo[s] = use_q ? xq : Mma<E>::zero();
     }
 #pragma unroll
     for (int J = 0; J < 3; ++J) {
@@ -197,10 +209,12 @@ __device__ __forceinline__ void l0_build_A(float* s_A, const float* s_gc,
       // wave's own rows do (a partial last chunk): those read as zero
       const int rj = 16 * J + (lane & 15);
       const bool in_seq = J < I && rj < in.nvalid;
+      const int rjc = J < I ? (rj < in.nvalid ? rj : in.nvalid - 1) : ric;
 #pragma unroll
       for (int s = 0; s < NKS; ++s) {
         const int c0 = s * Mma<E>::KS + kofs<E>(lane);
-        kj[J][s] = in_seq ? Mma<E>::ld(in.k + (size_t)(in.t0 + rj) * in.rowK + c0) : Mma<E>::zero();
+        const FR x = Mma<E>::ld(in.k + (size_t)(in.t0 + rjc) * in.rowK + c0);
+        kj[J][s] = in_seq ? x : Mma<E>::zero();
       }
     }
   }
