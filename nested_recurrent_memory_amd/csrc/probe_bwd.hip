@@ -464,11 +464,17 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     for (int s = 0; s < NKS; ++s) fSk[s] = Mma<E>::ld(srow + s * KS);
 #pragma unroll
     for (int t = 0; t < TPW2; ++t) {
+      // unconditional loads (an unused slot reads column 0 of a valid row)
+      // whose unwanted values are zeroed: a load under a branch leaves a
+      // register copy at the merge that waits for every load before it
       const int g = wv + NW * t;
-      const E* arow = bankT + (size_t)((g / CTK) * 16 + rl) * a.Nmax + ko;
+      const E* arow = bankT + (size_t)(((g < NTKV ? g : 0) / CTK) * 16 + rl) * a.Nmax;
 #pragma unroll
-      for (int s = 0; s < NSN; ++s)
-        fBt[t][s] = (g < NTKV && s * KS + ko < N) ? Mma<E>::ld(arow + s * KS) : Mma<E>::zero();
+      for (int s = 0; s < NSN; ++s) {
+        const bool ok = g < NTKV && s * KS + ko < N;
+        const FR x = Mma<E>::ld(arow + (ok ? s * KS + ko : 0));
+        fBt[t][s] = ok ? x : Mma<E>::zero();
+      }
     }
   }
   lds_barrier();   // dVals replaces the workspace tiles
