@@ -330,14 +330,20 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   }
 }
 
+// The bf16 forward scans run 16-column slices when the 32-column grid has at
+// most this many workgroups (a quarter of the CUs).
+#ifndef NARROW_GRID
+#define NARROW_GRID 64
+#endif
+
 // Waves per workgroup: four, one per SIMD. Eight (two per SIMD) leave each
 // wave half the registers, less than a step's operands read ahead need.
 template <int K> constexpr int scan_waves() { return K == 128 ? SCAN_WAVES_128 : 4; }
 
-template <typename E, int K, int M>
-static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
+template <typename E, int K, int M, int BV>
+static hipError_t launch_scan_bv(const ScanArgs& a, hipStream_t st) {
   constexpr int NWV = scan_waves<K>();
-  const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
+  const unsigned grid = (unsigned)(a.B * a.H * (a.V / BV));
   constexpr bool BF = std::is_same<E, bf16>::value;
   if (a.frag && !(BF && M % 32 == 0 && (a.frag == 1 || (a.frag == 3 && M == CH))))
     return hipErrorInvalidValue;
@@ -347,31 +353,45 @@ static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   if constexpr (BF && M == CH) {
     if (a.frag == 3) {
       if (a.read0)
-        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, 3>), dim3(grid),
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, BV, NWV, true, 3>), dim3(grid),
                            dim3(NWV * WAVE), 0, st, a);
       else
-        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 3>), dim3(grid),
+        hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, BV, NWV, false, 3>), dim3(grid),
                            dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
   if constexpr (BF && M % 32 == 0) {
     if (a.frag == 1) {
-      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 1>), dim3(grid),
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, BV, NWV, false, 1>), dim3(grid),
                          dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
   if constexpr (M == CH) {
     if (a.read0) {
-      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, true, 0>), dim3(grid),
+      hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, BV, NWV, true, 0>), dim3(grid),
                          dim3(NWV * WAVE), 0, st, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, SCAN_BV, NWV, false, 0>), dim3(grid),
+  hipLaunchKernelGGL((scan_fwd_kernel<E, K, M, BV, NWV, false, 0>), dim3(grid),
                      dim3(NWV * WAVE), 0, st, a);
   return hipGetLastError();
+}
+
+template <typename E, int K, int M>
+static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
+  // Few (batch, head) pairs (a long sequence in a small batch): the bf16
+  // matrix-core paths take 16-column slices, twice the workgroups with half
+  // the products per step each; a step's operands are then read by twice as
+  // many workgroups, which costs more than it saves once the grid fills the
+  // chip.
+  if constexpr (std::is_same<E, bf16>::value && M % 32 == 0) {
+    if (a.frag && a.B * a.H * (a.V / SCAN_BV) <= NARROW_GRID)
+      return launch_scan_bv<E, K, M, 16>(a, st);
+  }
+  return launch_scan_bv<E, K, M, SCAN_BV>(a, st);
 }
 
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st) {
