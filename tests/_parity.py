@@ -6,13 +6,17 @@ inputs, elementwise
 with (atol, rtol) = (2e-3, 1e-2) for bf16 inputs and (1e-5, 1e-5) for fp32
 inputs. This unscaled form is asserted for every tensor of a bf16 run
 (outputs, states and all gradients, the per-head parameter gradients
-included), and for the outputs and states of an fp32 run.
+included), and for every tensor of an fp32 run but two gradients.
 
-The gradients of an fp32 run are sums whose summands reach tens (the
-parameter gradients sum over every firing and batch row, dk over a chunk's
-decay products): there the absolute part is scaled by m = max(1, max|ref|),
+The two exceptions are the fp32 gradients of k and of the query banks, sums
+whose summands reach tens (dk over a chunk's decay products, the banks over
+every firing and batch row): there the absolute part is scaled by
+m = max(1, max|ref|),
     |got - ref| <= atol m + rtol |ref|
-(1e-5 m is 8 fp32 ulps of the tensor's largest value), and the unscaled
+(1e-5 m is 8 fp32 ulps of the tensor's largest value). Over the GPU suite
+they reach 1.21 (dk) and 1.62 (query banks) of the unscaled bound; the
+reference's own chunk form evaluated in fp32 reaches 0.80 and 0.82 of it on
+the case where they peak (tests/test_fp32_noise_floor.py). Their unscaled
 figures are still measured and reported.
 
 Every comparison prints one line (name, max-abs error, max |ref|, and the
@@ -35,22 +39,22 @@ LEAVES = ("q", "k", "v", "g", "b", "w", "mix_weights", "query_banks", "key_proje
           "b_projections", "w_projections", "g_projections", "initial_state")
 
 
-def is_grad(name: str) -> bool:
-    """Gradients are named by their leaf ("k") or with a d prefix ("dk")."""
-    return name in LEAVES or name.startswith("d")
+# fp32 gradients held to the scaled bar (see the module docstring); gradients
+# are named by their leaf ("k") or with a d prefix ("dk")
+SCALED_FP32 = ("k", "dk", "query_banks", "dquery_banks")
 
 
 def check(name, got, want, dtype, *, scaled=None, test=""):
     """Asserts the bar for ``got`` against ``want``; returns the figures.
 
-    ``scaled``: None picks the form (scaled for the gradients of an fp32
-    run, unscaled for everything else); True / False force it."""
+    ``scaled``: None picks the form (scaled for the fp32 gradients of k and
+    the query banks, unscaled for everything else); True / False force it."""
     atol, rtol = TOL[dtype]
     got = got.detach().double().cpu()
     want = want.detach().double().cpu()
     assert got.shape == want.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(want.shape)}"
     if scaled is None:
-        scaled = dtype in (torch.float32, torch.float64) and is_grad(name)
+        scaled = dtype in (torch.float32, torch.float64) and name in SCALED_FP32
     err = (got - want).abs()
     if not torch.isfinite(got).all():
         raise AssertionError(f"{name}: non-finite values")
