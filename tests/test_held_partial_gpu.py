@@ -58,6 +58,27 @@ def _grads(inp, L, promotion, init, do, ds, dtype):
     return ours, want
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("K,V", [(64, 128), (128, 64)])
+def test_held_partial_chunk_k_ne_v(K, V, dtype):
+    """K != V (the layer's expand_v): the op pads to max(K, V) and slices
+    back; the held partial chunk goes through the padding unchanged. fp16
+    inputs compute in fp32 and return fp16 (bar of their input precision,
+    the bf16 one)."""
+    B, T, H, L, N, firing = 1, 150, 2, 2, 16, (1, 1)
+    print(f"held partial K={K} V={V} {dtype}", flush=True)
+    inp = make_inputs(B=B, T=T, H=H, K=K, V=V, L=L, N=N, intervals=firing, dtype=dtype,
+                      g_scale=1.0, style="reftest")
+    gen = torch.Generator().manual_seed(T)
+    init = torch.randn(B, H, L, K, V, generator=gen) * 0.1
+    do = make_cotangent((B, T, H, V), seed=3).to(dtype).float()
+    ds = make_cotangent((B, H, L, K, V), seed=4)
+    ours, want = _grads(inp, L, "learned", init, do, ds, dtype)
+    _parity.check_all([(n, ours[n], want[n]) for n in want], dtype,
+                      test=f"held K{K} V{V} {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("promotion", ["learned", "merge"])
 @pytest.mark.parametrize("B,T,H,K,L,N,firing", CASES)
