@@ -161,13 +161,13 @@ def work_model(cfg):
         units * (2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     # level-0 chunk backward in one launch (the default): the state half per
     # chunk in the same workgroup, dQg and dKt through a workspace;
-    # dX_w = -dX_u S^T replaces T^T dW
+    # dX_w = -dX_u S^T replaces T^T dW, dA = -dX_u Vn^T (no W, U read)
     m["ngdn_l0_bwd"] = (
         units * (2 * (3 * ck + 2 * cv + gk) + 2 * kv + cv + cm),
-        units * (3 * ck + 2 * cv + gk + wk + wv + wc + 2 * kv + 2 * wv + cv + C * es
+        units * (3 * ck + 2 * cv + gk + wc + 2 * kv + 2 * wv + cv + C * es
                  + 2 * 2 * wk + 3 * ck + 2 * cv + gk),
         units * (2 * 2 * C * K * V + 2 * C * C * V + 2 * C * K * V
-                 + 2 * C * C * (K + V) + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
+                 + 2 * C * C * V + 2 * 2 * C * C * K + 4 * 2 * C * C * K))
     for lvl in range(1, L):
         nf, ng = n_firings(NT, f[lvl]), n_groups(NT, f[lvl])
         fu = B * H * nf

@@ -65,8 +65,9 @@ const char* ngdn_last_error(void);
  * (for instance ngdn_probe_bwd's bank-gradient argument: an accumulator
  * [L-1,H,n_max,K] before 0.2.0, the per-firing workspace ws_dbank
  * [B,H,NF,N,K] since), so an older caller can link and then write past its
- * buffers. 0.4.0 added ngdn_dims.hold_partial (the struct grew by 4 bytes). */
-#define NGDN_VERSION 400
+ * buffers. 0.4.0 added ngdn_dims.hold_partial (the struct grew by 4 bytes);
+ * 0.5.0 took W and U out of ngdn_l0_bwd. */
+#define NGDN_VERSION 500
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -275,10 +276,12 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
  * vn [B,H,NT,64,V] of ngdn_l0_scan_fwd, dSp [B,H,NT,K,V] and dVnT of
  * ngdn_l0_scan_bwd, do and mix; its dQg and dKt pass through the workspaces
  * ws_dQg, ws_dKt (fp32 [B,H,NT,64,K] each, no initial contents), the rest
- * stays on chip. Outputs as ngdn_l0_bwd_intra. */
+ * stays on chip. dA = -(dX_w W^T + dX_u U^T) is formed as -dX_u Vn^T (the
+ * same, since dX_w = -dX_u S^T and W S = U - Vn), so W and U are not read; TT
+ * from ngdn_l0_intra_fwd. Outputs as ngdn_l0_bwd_intra. */
 int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void* v,
-                    const float* g, const void* b, const void* w, const float* W,
-                    const float* U, const float* TT, const float* h, const float* dSp,
+                    const float* g, const void* b, const void* w,
+                    const float* TT, const float* h, const float* dSp,
                     const float* vn, const float* dVnT, const void* dout, const void* mix,
                     float* ws_dQg, float* ws_dKt, void* dq, void* dk, void* dv, float* dg,
                     void* db, void* dw, void* stream);

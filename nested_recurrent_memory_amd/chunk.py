@@ -469,7 +469,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         if FUSED_L0_BWD:
             # the chunk backward in one launch: the state half per chunk
             _lib.call("ngdn_l0_bwd", ctypes.byref(d), *(P(R(x)) for x in (
-                q_, k_, v_, g_, b_, w_, sv["W"], sv["U"], sv["TT"], sv["h"], dSp0, sv["vn"],
+                q_, k_, v_, g_, b_, w_, sv["TT"], sv["h"], dSp0, sv["vn"],
                 dVnT0, do_, mix_, dQg, dKt, dq, dk, dv, dg, db, dw)), sp)
         else:
             _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(R(sv["h"])), P(R(dSp0)),

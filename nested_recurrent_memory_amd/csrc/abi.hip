@@ -408,18 +408,18 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
 }
 
 int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void* v,
-                    const float* g, const void* b, const void* w, const float* W,
-                    const float* U, const float* TT, const float* h, const float* dSp,
+                    const float* g, const void* b, const void* w,
+                    const float* TT, const float* h, const float* dSp,
                     const float* vn, const float* dVnT, const void* dout, const void* mix,
                     float* ws_dQg, float* ws_dKt, void* dq, void* dk, void* dv, float* dg,
                     void* db, void* dw, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_bwd")) return r;
-  if (!q || !k || !v || !g || !b || !w || !W || !U || !TT || !h || !dSp || !vn || !dVnT ||
+  if (!q || !k || !v || !g || !b || !w || !TT || !h || !dSp || !vn || !dVnT ||
       !dout || !mix || !ws_dQg || !ws_dKt || !dq || !dk || !dv || !dg || !db || !dw)
     return fail(NGDN_EINVAL, "ngdn_l0_bwd: NULL tensor");
   ngdn::L0BwdIntraArgs a{};
-  a.q = q; a.k = k; a.v = v; a.g = g; a.b = b; a.w = w; a.W = W; a.U = U; a.TT = TT;
+  a.q = q; a.k = k; a.v = v; a.g = g; a.b = b; a.w = w; a.TT = TT;
   a.dVnT = dVnT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.db = db; a.dw = dw;
   a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
   a.h = h; a.dSp = dSp; a.vn = vn; a.dout = dout; a.mix = mix; a.wsQ = ws_dQg; a.wsK = ws_dKt;

@@ -12,6 +12,8 @@
 //     dgam = rowsum(dS' * S)
 //   intra half (l0_bwd_intra):
 //     dX_u = T^T dVn, dX_w = T^T dW, dA = -mask(dX_w W^T + dX_u U^T)
+//     (in one launch, l0_bwd: dX_w = -dX_u S^T, and as W S = U - Vn,
+//     dA = -mask(dX_u Vn^T))
 //     then through the decay products of A and Aqk, the gates and the
 //     cumulative sum of g (reverse cumsum within the chunk).
 #include "l0_common.h"
@@ -190,11 +192,18 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   constexpr int LDV1 = V + ST1::PAD, LDO1 = V + 16 / (int)sizeof(E);
   constexpr size_t SZ_V1 = sizeof(typename ST1::T) * ST1::NPLANE * C * LDV1;
   constexpr size_t SZ_1 = FUSED ? SZ_V1 + sizeof(E) * C * LDO1 : 0;
-  constexpr size_t SZ_R0 = SZ_X > SZ_P ? SZ_X : SZ_P;
+  // fused phases 2-3: phase 1's Vn tile stays at the start until dA is formed
+  // from it, dX_u follows it, and dX_w then takes the Vn tile's space (or
+  // follows dX_u where that space is smaller); two-launch form: dX_w, dX_u
+  constexpr size_t SZ_XW = sizeof(float) * C * LXK, SZ_XU = sizeof(float) * C * LXV;
+  constexpr size_t OFF_XU = FUSED ? SZ_V1 : SZ_XW;
+  constexpr size_t OFF_XW = (!FUSED || SZ_XW <= SZ_V1) ? 0 : SZ_V1 + SZ_XU;
+  constexpr size_t SZ_2 = FUSED ? (OFF_XW ? OFF_XW + SZ_XW : SZ_V1 + SZ_XU) : SZ_X;
+  constexpr size_t SZ_R0 = SZ_2 > SZ_P ? SZ_2 : SZ_P;
   constexpr size_t SZ_R = SZ_R0 > SZ_1 ? SZ_R0 : SZ_1;
   __shared__ __attribute__((aligned(16))) char smem[SZ_R + sizeof(float) * (6 * K + 256 + C)];
-  float* s_dXw = reinterpret_cast<float*>(smem);
-  float* s_dXu = s_dXw + C * LXK;
+  float* s_dXw = reinterpret_cast<float*>(smem + OFF_XW);
+  float* s_dXu = reinterpret_cast<float*>(smem + OFF_XU);
   float* s_dA = reinterpret_cast<float*>(smem);
   float* s_dQ = s_dA + C * AT_LD;
   float* s_g = reinterpret_cast<float*>(smem + SZ_DA);
@@ -224,6 +233,8 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   // fused: this wave's rows k of S as B fragments (8 consecutive v per lane),
   // loaded in phase 1 and used again for dX_w in phase 2
   SF fSk[FUSED ? CPW : 1][NKV];
+  // fused: the chunk's Vn rows (split), phases 1-2
+  const ST1 sVn1{reinterpret_cast<typename ST1::T*>(smem), C * LDV1};
   if constexpr (FUSED) {
     // ---- 1. the state half (what l0_bwd_state computes), from S = h, dS',
     // Vn, do and mix_0 of this chunk:
@@ -235,7 +246,6 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     // every row of the chunk; Vn (split) and do (exact) rows come from LDS.
     // Phase 2 forms dX_w = T^T dW from dX_u instead of reading dW.
     static_assert(CTK % 4 == 0, "column tiles of K split over the 4 waves");
-    const ST1 sVn1{reinterpret_cast<typename ST1::T*>(smem), C * LDV1};
     E* s_do1 = reinterpret_cast<E*>(smem + SZ_V1);
     {
       constexpr int VE = 16 / (int)sizeof(E);
@@ -375,7 +385,26 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
     if constexpr (!FUSED) product(a.dWT + cix * K * C, K, s_dXw, LXK);
   }
   lds_barrier();
+  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower; tiles J <= w of this
+  // wave's block-row, held until the space is free
+  f4 dat[4];
   if constexpr (FUSED) {
+    // With dX_w = -dX_u S^T (below) and W S = U - Vn, the sum in dA is
+    // -dX_u (U - Vn)^T + dX_u U^T = dX_u Vn^T: formed from dX_u and phase 1's
+    // Vn tile, with no W or U read and no cancellation of two large terms
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      dat[J] = f4_zero();
+      if (J <= wv) {
+#pragma unroll
+        for (int s = 0; s < NKV; ++s) {
+          const int v0 = s * KS + kofs<E>(lane);
+          dat[J] = Mma<E>::mma(dat[J], Mma<E>::ld(s_dXu + (wv * 16 + (lane & 15)) * LXV + v0),
+                               sVn1.get((J * 16 + (lane & 15)) * LDV1 + v0));
+        }
+      }
+    }
+    if constexpr (OFF_XW == 0) lds_barrier();   // dX_w takes the Vn tile's space
     // dW = -dVn S^T, so dX_w = T^T dW = -(T^T dVn) S^T = -dX_u S^T: wave w
     // owns its CPW column tiles (rows k of S) over every row of the chunk,
     // the same rows it held as B fragments in phase 1 (kept, not re-read)
@@ -404,9 +433,7 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
 #pragma unroll
     for (int r = 0; r < 4; ++r) dxw[ct][r] = s_dXw[(wv * 16 + acc_row(r)) * LXK + ct * 16 + acc_col()];
 
-  // ---- 3. dA = -(dX_w W^T + dX_u U^T), strictly lower (tiles held until the space is free)
-  f4 dat[4];
-  {
+  if constexpr (!FUSED) {
     // W in split form (bf16: fragment order)
     const SplitTile<E> Ws = split_at<E>(a.W + cix * C * K, C * K);
     const float* Ug = a.U + cix * C * V;

@@ -442,8 +442,8 @@ struct L0BwdIntraArgs {
   // the fused form (l0_bwd): the state half computed by the same workgroup
   // from the chunk states h [.,K,V], their gradients dSp [.,K,V], Vn [.,64,V],
   // do and mix; dQg and dKt pass through the workspaces wsQ, wsK [.,64,K]
-  // (fp32, no initial contents) between its phases; dQg, dWT, dKt, dAqk and
-  // dgam above are then unused
+  // (fp32, no initial contents) between its phases; W, U, dQg, dWT, dKt, dAqk
+  // and dgam above are then unused
   const float* h; const float* dSp; const float* vn; const void* dout; const void* mix;
   float* wsQ; float* wsK;
 };
