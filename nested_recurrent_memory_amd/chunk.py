@@ -96,7 +96,8 @@ def _validate(q, k, v, L, chunk_size, promotion, n_queries, intervals, query_ban
 FUSED_PROMOTION = False
 
 # The level-0 chunk backward as one launch (ngdn_l0_bwd: the state half per
-# chunk in the same workgroup) or two (ngdn_l0_bwd_state, ngdn_l0_bwd_intra).
+# chunk in the same workgroup) or two (ngdn_l0_bwd_state, ngdn_l0_bwd_intra);
+# read by the forward, which keeps U for the two-launch form only.
 FUSED_L0_BWD = True
 # dmix_0 (a bandwidth pass over do and the stored read) on the second side
 # stream: at the fork, beside the reads' backward (False), or after the
@@ -278,7 +279,10 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
     _run_groups(B, dev, launch)
     saved = None
     if train:
-        saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W, U=U, Qg=Qg,
+        # U only for the two-launch chunk backward (the fused one forms dA
+        # from Vn instead)
+        saved = dict(q=q_, k=k_, v=v_, b=b_, w=w_, mix=mix_, g=g_, W=W,
+                     U=None if FUSED_L0_BWD else U, Qg=Qg,
                      KtT=KtT, Aqk=Aqk, gam=gam, TT=TT, NTF=NTF,
                      hT=hT, h=h_, vn=vn_, read0=read0, states=states,
                      statesT=statesT, levels=levels, final=final, par=par,
@@ -369,7 +373,9 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     # two-launch form
     dQg, dKt = f32(B, H, NT, 64, K), f32(B, H, NT, 64, K)
     dVn0 = dWT = dAqk = dgam = None
-    if not FUSED_L0_BWD:
+    # the form the forward saved for (U is kept only for the two-launch form)
+    fused_l0 = sv["U"] is None
+    if not fused_l0:
         dVn0, dWT = f32(B, H, NT, 64, V), f32(B, H, NT, K, 64)
         dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
     dk, dv, db, dw = e(B, T, H, K), e(B, T, H, V), e(B, T, H, K), e(B, T, H, V)
@@ -466,7 +472,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
             "W", "KtT", "gam", "Qg", "Aqk")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
             P(R(inj)), nf1, P(R(d_final)), P(R(dSp0)), P(R(dVn0)), P(R(dVnT0)), P(R(d_init)), sp)
-        if FUSED_L0_BWD:
+        if fused_l0:
             # the chunk backward in one launch: the state half per chunk
             _lib.call("ngdn_l0_bwd", ctypes.byref(d), *(P(R(x)) for x in (
                 q_, k_, v_, g_, b_, w_, sv["TT"], sv["h"], dSp0, sv["vn"],
