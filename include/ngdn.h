@@ -66,8 +66,10 @@ const char* ngdn_last_error(void);
  * [L-1,H,n_max,K] before 0.2.0, the per-firing workspace ws_dbank
  * [B,H,NF,N,K] since), so an older caller can link and then write past its
  * buffers. 0.4.0 added ngdn_dims.hold_partial (the struct grew by 4 bytes);
- * 0.5.0 took W and U out of ngdn_l0_bwd. */
-#define NGDN_VERSION 500
+ * 0.5.0 took W and U out of ngdn_l0_bwd; 0.6.0 moved the upper levels'
+ * lower-state gradients from ngdn_probe_bwd's d_below to an injection that
+ * ngdn_upper_scan_bwd adds. */
+#define NGDN_VERSION 600
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -241,13 +243,18 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
 /* Reverse write scan of level `level` >= 1 (ops/update_bwd.py:19-164): keys
  * [B,H,NF,N,K] and AT = (keys*b*e^g)^T [B,H,NF,K,N] (both split; AT in
  * fragment order for NGDN_BF16 with n_pairs % 32 == 0) from ngdn_probe_fwd, gam
- * [B,H,NF,K]; d_states fp32 [B,NG,H,K,V] (read gradients plus the level
- * above's scatter); d_final [B,H,L,K,V]. Writes dSp fp32 [B,H,NF,K,V], dvn
- * fp32 [B,H,NF,N,V] and d_initial[:, :, level] when not NULL. */
+ * [B,H,NF,K]; d_states fp32 [B,NG,H,K,V] (the reads' gradients); inj, when
+ * not NULL, the level above's injection from its ngdn_probe_bwd (fp32
+ * [B,H,nf_above,K,V]; firing i of interval f_above read this level's state
+ * entering group ((i+1) f_above) / f_here, f_here this level's interval,
+ * and its slot joins that group's gradient); d_final [B,H,L,K,V]. Writes dSp
+ * fp32 [B,H,NF,K,V], dvn fp32 [B,H,NF,N,V] and d_initial[:, :, level] when
+ * not NULL. */
 int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* keys,
                             const float* AT, const float* gam,
-                            const float* d_states, const float* d_final,
+                            const float* d_states, const float* inj, int32_t f_here,
+                            int32_t f_above, int32_t nf_above, const float* d_final,
                             float* dSp, float* dvn, float* d_initial,
                             void* stream);
 
@@ -297,8 +304,11 @@ int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void
  * Workspace (fp32): ws_vals, ws_du, ws_dxb, ws_dxg [B,H,NF,N,K], ws_dxw,
  * ws_dvals [B,H,NF,N,V], and ws_dbank [B,H,NF,N,K] (learned only): each
  * firing's bank-gradient partial, summed by ngdn_param_grads. The gradient
- * of the lower state goes to inj (level 1, fp32 [B,H,NF,K,V]) or is added to
- * d_below (fp32 [B,ng_below,H,K,V]) / d_final[:, :, level-1]. */
+ * of the lower state a firing read goes to its slot of inj (fp32
+ * [B,H,NF,K,V], written), which the lower level's reverse scan adds
+ * (ngdn_l0_scan_bwd for level 1, ngdn_upper_scan_bwd otherwise); a firing
+ * of level >= 2 that read the lower level's final state adds it to
+ * d_final[:, :, level-1] instead. */
 int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
                        const float* below_kv, const float* below_vk,
@@ -312,7 +322,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* dvn, float* ws_vals, float* ws_du,
                        float* ws_dxb, float* ws_dxg, float* ws_dxw,
                        float* ws_dvals, float* ws_dbank, float* inj,
-                       float* d_below, float* d_final, void* stream);
+                       float* d_final, void* stream);
 
 /* Slices of firings per head in the parameter-gradient sums (the first
  * dimension of ws_parts' slices). */

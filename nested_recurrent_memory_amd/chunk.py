@@ -364,7 +364,7 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
                          ws=[f32(B, H, nfa, N, K) for _ in range(4)]
                          + [f32(B, H, nfa, N, V) for _ in range(2)],
                          dbank=None if merge else f32(B, H, nfa, N, K),
-                         inj=f32(B, H, nfa, K, V) if lvl == 1 else None)
+                         inj=f32(B, H, nfa, K, V))
     # per-slice partials of the parameter-gradient sums, shared by the levels
     # (their sums run one after another on one stream)
     parts = f32(4, H, _lib.PARAM_SPLIT, K, V) if L > 1 else None
@@ -396,8 +396,9 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         # With one group of rows, independent launches go to two side streams:
         # (a) the reads' backward of the levels below the top one
         # (each writes its own columns of dmix and dq and its own d_states)
-        # beside the top level's read and reverse scan, joined before the top
-        # level's probe backward adds into the level below's d_states; (b) each
+        # beside the top level's read, reverse scan and probe backward (whose
+        # lower-state gradient goes to an injection, not into d_states),
+        # joined before the first reverse scan that reads those d_states; (b) each
         # level's parameter-gradient sums (reading only that level's
         # workspaces) and dmix_0 (before level 1's sums, or at the fork when
         # DMIX0_LATE is off) beside the rest of the chain, joined at the end. With
@@ -432,30 +433,35 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         for lvl in range(L - 1, 0, -1):
             lv, wk = levels[lvl], work[lvl]
             N, nf, ng = lv["N"], lv["nf"], lv["ng"]
+            if not joined and lvl < L - 1:
+                st.wait_stream(aux[0])
+                joined = True
+            # the level above's injection (its probe backward's lower-state
+            # gradients), added by this level's reverse scan
+            up = lvl + 1 < L and levels[lvl + 1]["nf"] > 0
             _lib.call("ngdn_upper_scan_bwd", ctypes.byref(d), lvl, N, nf, ng,
-                      *(P(R(x)) for x in (lv["keys"], lv["AT"], lv["gam"], d_states[lvl],
-                                          d_final, wk["dSp"], wk["dvn"], d_init)),
+                      *(P(R(x)) for x in (lv["keys"], lv["AT"], lv["gam"], d_states[lvl])),
+                      P(R(work[lvl + 1]["inj"])) if up else None, f[lvl],
+                      f[lvl + 1] if up else 1, levels[lvl + 1]["nf"] if up else 0,
+                      *(P(R(x)) for x in (d_final, wk["dSp"], wk["dvn"], d_init)),
                       sp, tag=f"ngdn_upper_scan_bwd.{lvl}")
             if nf == 0:
                 continue
             fh, fb = f[lvl], f[lvl - 1]
             if lvl == 1:
                 inj, nf1 = wk["inj"], nf
-                b_kv, b_vk, ngb, d_below = sv["h"], sv["hT"], NT, None
+                b_kv, b_vk, ngb = sv["h"], sv["hT"], NT
             else:
                 b_kv, b_vk = states[lvl - 1], sv["statesT"][lvl - 1]
-                ngb, d_below = n_groups(NT, fb), d_states[lvl - 1]
+                ngb = n_groups(NT, fb)
             ws = wk["ws"]
-            if not joined:
-                st.wait_stream(aux[0])
-                joined = True
             _lib.call("ngdn_probe_bwd", ctypes.byref(d), lvl, int(merge), N, fb, fh,
                       P(R(b_kv)), P(R(b_vk)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
                       P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
                       P(par["kpT"]), P(par["bankT"]), P(par["bp"]), P(par["wp"]),
                       P(par["gp"]), P(R(states[lvl])), P(R(sv["statesT"][lvl])), ng,
                       P(R(wk["dSp"])), P(R(wk["dvn"])), *(P(R(x)) for x in ws),
-                      P(R(wk["dbank"])), P(R(wk["inj"])), P(R(d_below)), P(R(d_final)), sp,
+                      P(R(wk["dbank"])), P(R(wk["inj"])), P(R(d_final)), sp,
                       tag=f"ngdn_probe_bwd.{lvl}")
             if nb == B:
                 if aux is not None:

@@ -347,7 +347,8 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
 int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* keys,
                             const float* AT, const float* gam,
-                            const float* d_states, const float* d_final,
+                            const float* d_states, const float* inj, int32_t f_here,
+                            int32_t f_above, int32_t nf_above, const float* d_final,
                             float* dSp, float* dvn, float* d_initial,
                             void* stream) {
   g_err[0] = 0;
@@ -361,10 +362,15 @@ int32_t ngdn_upper_scan_bwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
     return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: NF=%d inconsistent with NG=%d", nf, ng);
   if ((nf > 0 && (!keys || !AT || !gam || !dSp || !dvn)) || !d_states)
     return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: NULL tensor");
+  if (inj && (level + 1 >= d->L || f_here < 1 || f_above < f_here || nf_above < 0 ||
+              nf_above > fire_chunks(d) / f_above))
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_bwd: injection of level %d with intervals %d / %d "
+                "and %d firings inconsistent", level + 1, f_above, f_here, nf_above);
   const long long skv = (long long)d->K * d->V;
   ngdn::ScanBwdArgs a{};
   a.Bop = keys; a.AT = AT; a.gam = gam;
   a.d_states = d_states; a.NG = ng;
+  a.inj = inj; a.inj_fh = f_here; a.inj_fa = f_above; a.inj_nf = inj ? nf_above : 0;
   a.d_final = d_final ? d_final + (long long)level * skv : nullptr;
   a.df_sh = d->L * skv; a.df_sb = d->H * a.df_sh;
   a.dSp = dSp; a.dVn = dvn; a.dVnT = nullptr;
@@ -440,7 +446,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const float* dvn, float* ws_vals, float* ws_du,
                        float* ws_dxb, float* ws_dxg, float* ws_dxw,
                        float* ws_dvals, float* ws_dbank, float* inj,
-                       float* d_below, float* d_final, void* stream) {
+                       float* d_final, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_bwd")) return r;
   if (level < 1 || level >= d->L || d->K != d->V || (promotion != 0 && promotion != 1))
@@ -457,7 +463,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
       !states || !statesT || !dSp || !dvn || !ws_vals || !ws_du || !ws_dxb || !ws_dxg ||
       !ws_dxw || !ws_dvals)
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: NULL tensor");
-  if (level == 1 ? !inj : (!d_below || !d_final))
+  if (!inj || (level > 1 && !d_final))
     return fail(NGDN_EINVAL, "ngdn_probe_bwd: lower-level gradient destination missing");
   const long long skv = (long long)d->K * d->V;
   ngdn::ProbeBwdArgs a{};
@@ -483,7 +489,7 @@ int32_t ngdn_probe_bwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.wsV = ws_vals; a.wsdu = ws_du; a.wsdxb = ws_dxb; a.wsdxg = ws_dxg; a.wsdxw = ws_dxw;
   a.wsdV = ws_dvals;
   a.dbank = ws_dbank;   // [B,H,NF,N,K], summed by ngdn_param_grads
-  a.inj = inj; a.d_below = d_below;
+  a.inj = inj;
   a.d_below_fin = d_final ? d_final + (long long)(level - 1) * skv : nullptr;
   if (a.f.NF == 0) return NGDN_OK;
   return launched(ngdn::probe_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_probe_bwd");

@@ -85,7 +85,11 @@ struct ScanBwdArgs {
   const float* Bop; const float* AT; const float* gam;
   const float* W; const float* KtT; const float* Qg; const float* Aqk;
   const void* dout; const void* mix; int T, L;
-  const float* inj; int inj_every, inj_nf;
+  // level 0: injection inj[(n+1)/inj_every - 1] before the step of chunk n;
+  // levels >= 1: the level above's injection inj [B,H,inj_nf,K,V] joins the
+  // group j that its firing i read, j = ((i+1) inj_fa) / inj_fh (the level's
+  // interval inj_fh, the level above's inj_fa)
+  const float* inj; int inj_every, inj_nf, inj_fh, inj_fa;
   const float* d_states; int NG;
   const float* d_final; long long df_sb, df_sh;
   float* dSp;
@@ -317,10 +321,10 @@ hipError_t cross_entropy(const XentArgs& a, int dtype, hipStream_t st);
 // dxg [N,K-or-V], dxw, dVals [N,V]; the parameter-gradient reduction reads
 // them. dbank: this firing's bank-gradient partial (fp32 [B,H,NF,N,K],
 // written), summed per head in a fixed order by the parameter-gradient pass.
-// The gradient of the gathered lower state goes to: inj (level 1; fp32
-// [B,H,NF,K,V], written) or d_below (level >= 2; fp32 [B,NGb,H,K,V], added)
-// / d_below_fin (fp32 [K][V] at strides, added) when the firing reads the
-// lower final state.
+// The gradient of the gathered lower state goes to inj (fp32 [B,H,NF,K,V],
+// written; the lower level's reverse scan adds it), except at a level >= 2
+// firing that reads the lower final state: added to d_below_fin (fp32
+// [K][V] at strides).
 struct ProbeBwdArgs {
   ProbeArgs f;                // gather indices, params as in the forward (f.below, f.A .. unused)
   const float* below_kv;      // lower states as rows [K][V] (level 0: h, mode 0 layout)
@@ -330,7 +334,7 @@ struct ProbeBwdArgs {
   const float* dSp; const float* dvn;
   float* wsV; float* wsdu; float* wsdxb; float* wsdxg; float* wsdxw; float* wsdV;
   float* dbank;
-  float* inj; float* d_below; float* d_below_fin;
+  float* inj; float* d_below_fin;
 };
 hipError_t probe_bwd(const ProbeBwdArgs& a, int dtype, int K, hipStream_t st);
 

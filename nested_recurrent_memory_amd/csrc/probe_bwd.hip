@@ -495,10 +495,15 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
   lds_barrier();
 
   // ---- 8. dS_below and dBank
-  // Adds (or, for level 1, writes) the [K,V] tiles g = wv + NW t: every
-  // addend read before any store
+  // The [K,V] tiles g = wv + NW t of dS_below go to this firing's slot of
+  // the injection inj [B,H,NF,K,V], which the lower level's reverse scan adds
+  // to the gradient of the state the firing read (level 1: every firing; a
+  // level above: firings that read a stored state), or, for a firing above
+  // level 1 that reads the lower level's final state, are added to that
+  // state's gradient (every addend read before any store)
   auto scatter_all = [&](const f4* x) {
     constexpr int NT2 = TPW2;
+    const bool to_fin = a.below_mode != 0 && fin;
     float prev[NT2][4];
 #pragma unroll
     for (int t = 0; t < NT2; ++t) {
@@ -506,11 +511,9 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         prev[t][r] = 0.f;
-        if (g >= NTKV) continue;
+        if (g >= NTKV || !to_fin) continue;
         const int k = (g / CTK) * 16 + acc_row(r), v = (g % CTK) * 16 + acc_col();
-        if (a.f_below == 1 && a.below_mode == 0) continue;
-        prev[t][r] = fin ? ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v]
-                         : ab.d_below[(((size_t)b * a.NGb + src) * H + h) * K * V + (size_t)k * V + v];
+        prev[t][r] = ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v];
       }
     }
 #pragma unroll
@@ -520,13 +523,10 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int k = (g / CTK) * 16 + acc_row(r), v = (g % CTK) * 16 + acc_col();
-        if (a.f_below == 1 && a.below_mode == 0)
-          ab.inj[fo * K * V + (size_t)k * V + v] = x[t][r];
-        else if (fin)
+        if (to_fin)
           ab.d_below_fin[b * a.bf_sb + h * a.bf_sh + (long long)k * V + v] = prev[t][r] + x[t][r];
         else
-          ab.d_below[(((size_t)b * a.NGb + src) * H + h) * K * V + (size_t)k * V + v] =
-              prev[t][r] + x[t][r];
+          ab.inj[fo * K * V + (size_t)k * V + v] = x[t][r];
       }
     }
   };

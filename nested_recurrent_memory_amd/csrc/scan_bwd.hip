@@ -14,7 +14,9 @@
 // added -- the gradient of the state entering chunk n+1, which the reference
 // hands to fla as dh_ext (ops/chunk.py:519-528).
 // Levels >= 1 (ops/update_bwd.py:93-158): after group j's firing, the read
-// gradient of the state entering group j joins: dS += d_states[j].
+// gradient of the state entering group j joins: dS += d_states[j], plus, when
+// a firing i of the level above read that state (j = ((i+1) f_above) /
+// f_here), that firing's injection inj[i] (the level above's probe gradient).
 //
 // Stores, per step (fp32): dS' (the gradient of the state after it) and dVn.
 // Every operand but do is derived; for bf16 inputs each product is three bf16
@@ -81,9 +83,24 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
   auto dstates = [&](int j) {
     return a.d_states + (((size_t)b * a.NG + j) * H + h) * K * V;
   };
+  // the injection of the firing i of the level above that read the state
+  // entering group j, if any: i + 1 = m = ceil(j f_here / f_above) when
+  // (m f_above) / f_here == j (intervals f_above >= f_here: at most one m)
+  auto inj_tile = [&](int j) -> const float* {
+    if (!a.inj || j < 1) return nullptr;
+    const int m = (j * a.inj_fh + a.inj_fa - 1) / a.inj_fa;
+    if (m < 1 || m > a.inj_nf || (m * a.inj_fa) / a.inj_fh != j) return nullptr;
+    return a.inj + ((size_t)bh * a.inj_nf + m - 1) * K * V;
+  };
   for (int j = a.NG - 1; j >= S; --j) {
     f4 x[TPW];
     read_kv(dstates(j), x);
+    if (const float* p = inj_tile(j)) {
+      f4 y[TPW];
+      read_kv(p, y);
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) x[i] += y[i];
+    }
 #pragma unroll
     for (int i = 0; i < TPW; ++i) ds[i] += x[i];
   }
@@ -99,6 +116,8 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
     SF at[TRT][NSM];            // A^T rows of this wave's state tiles
     float g[TRT][4];
     f4 add[TPW];                // the read gradient of the group the step starts
+    f4 inj[TPW];                // and, when has_inj, the injection into it
+    bool has_inj;
   };
   auto load = [&](int j, Ops& o) {
     const SplitTile<E> Bj = split_at<E>(Bb + (size_t)j * M * K, M * K);
@@ -126,6 +145,9 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
       for (int r = 0; r < 4; ++r) o.g[t][r] = Gj[rt * 16 + acc_row(r)];
     }
     read_kv(dstates(j), o.add);
+    const float* ip = inj_tile(j);
+    o.has_inj = ip != nullptr;
+    if (o.has_inj) read_kv(ip, o.inj);
   };
 
   // dVn of a step is stored at the start of the step after it, beside dS',
@@ -217,8 +239,10 @@ __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
         if (live) fb = sdV.get(vrow + s * KS);
         acc = Mma<E>::mma(acc, cur.at[t][s], fb);
       }
+      f4 add = cur.add[i];
+      if (cur.has_inj) add += cur.inj[i];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ds[i][r] = cur.g[t][r] * ds[i][r] - acc[r] + cur.add[i][r];
+      for (int r = 0; r < 4; ++r) ds[i][r] = cur.g[t][r] * ds[i][r] - acc[r] + add[r];
     }
     // no barrier here: the next step's writes of s_dst follow this step's
     // second barrier, after every read of s_dst, and its writes of s_dvn
