@@ -581,8 +581,18 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         out = [dq, dk, dv, dg, db, dw, dmix]
         out = [x.to(dt) for x, dt in zip(out, dts[:7])]
         if L > 1:
-            dqb = dqb[:, :, :ctx.nmax]          # drop the alignment padding rows
-            out += [x.to(dt) for x, dt in zip((dqb, dkp, dbp, dwp, dgp), dts[7:12])]
+            pg = (dqb, dkp, dbp, dwp, dgp)
+            pdt = dts[7]
+            n = [x.numel() for x in pg]
+            if (pdt != torch.float32 and all(dt == pdt for dt in dts[8:12])
+                    and all(pg[i + 1].data_ptr() == pg[i].data_ptr() + 4 * n[i] for i in range(4))):
+                # the five sums are consecutive in one fp32 buffer: one cast
+                flat = dqb.view(-1).as_strided((sum(n),), (1,)).to(pdt)
+                pg = [y.view(x.shape) for x, y in zip(pg, flat.split(n))]
+            else:
+                pg = [x.to(dt) for x, dt in zip(pg, dts[7:12])]
+            pg[0] = pg[0][:, :, :ctx.nmax]      # drop the alignment padding rows
+            out += pg
         else:
             out += [None] * 5
         return (*out, None, None, None, None,
