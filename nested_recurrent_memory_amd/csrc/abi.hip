@@ -407,8 +407,12 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
   if (!q || !k || !v || !g || !b || !w || !W || !U || !TT || !dQg || !dWT || !dKt || !dAqk ||
       !dgam || !dVnT || !dq || !dk || !dv || !dg || !db || !dw)
     return fail(NGDN_EINVAL, "ngdn_l0_bwd_intra: NULL tensor");
-  ngdn::L0BwdIntraArgs a{q, k, v, g, b, w, W, U, TT, dQg, dWT, dKt, dAqk, dgam, dVnT,
-                         dq, dk, dv, dg, db, dw, d->B, d->T, d->H, d->L, nchunks(d), d->scale};
+  // the fused form's fields (h .. wsK) stay NULL
+  ngdn::L0BwdIntraArgs a{};
+  a.q = q; a.k = k; a.v = v; a.g = g; a.b = b; a.w = w; a.W = W; a.U = U; a.TT = TT;
+  a.dQg = dQg; a.dWT = dWT; a.dKt = dKt; a.dAqk = dAqk; a.dgam = dgam; a.dVnT = dVnT;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.db = db; a.dw = dw;
+  a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
   return launched(ngdn::l0_bwd_intra(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_bwd_intra");
 }

@@ -54,7 +54,6 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   constexpr int LDS_ST = K + ST::PAD;
   constexpr int LDS_VN = M + ST::PAD;
   constexpr int KS = Mma<E>::KS;
-  constexpr int KPL = Mma<E>::KPL;
   constexpr int NSK = K / KS;                 // k-steps over K
   constexpr int NSM = (M + KS - 1) / KS;      // k-steps over M
   constexpr bool PADM = (M % KS) != 0;
