@@ -26,6 +26,42 @@ def test_header_declares_entry_points():
     assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
 
 
+def _declarations():
+    """name -> parameter type strings of every function the header declares
+    (comments and preprocessor lines dropped)."""
+    text = open(os.path.join(ROOT, "include", "ngdn.h")).read()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = "\n".join(line for line in text.splitlines() if not line.lstrip().startswith("#"))
+    out = {}
+    for m in re.finditer(r"\b[a-z0-9_]+\s*\**\s*\b(ngdn_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        args = " ".join(m.group(2).split())
+        parts = [] if args in ("", "void") else [a.strip() for a in args.split(",")]
+        # drop the parameter name, keep the type
+        out[m.group(1)] = [re.sub(r"\s*\b[A-Za-z_][A-Za-z0-9_]*$", "", a) if not a.endswith("*")
+                           else a for a in parts]
+    return out
+
+
+def _ctype_of(decl):
+    d = decl.replace(" ", "")
+    if d.endswith("*"):
+        return "ptr"
+    return {"int32_t": "i32", "int64_t": "i64", "float": "f32"}[d]
+
+
+def test_signature_table_matches_header():
+    """Every declaration's parameters, one by one, against the ctypes table
+    the package calls through: a pointer where the header has a pointer, the
+    same integer width, the same count."""
+    kind = {_lib.P: "ptr", _lib.PD: "ptr", _lib.I32: "i32", _lib.I64: "i64", ctypes.c_float: "f32"}
+    decls = _declarations()
+    assert set(decls) == set(_declared())
+    for name, params in decls.items():
+        want = [_ctype_of(re.sub(r"\b(const|struct)\b", "", p)) for p in params]
+        got = [kind[t] for t in _lib.SIGNATURES[name]]
+        assert got == want, (name, got, want)
+
+
 def test_library_exports_every_declared_symbol():
     so = _lib.lib()
     for name in _declared():
