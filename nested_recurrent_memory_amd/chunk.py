@@ -105,6 +105,12 @@ FUSED_L0_BWD = True
 # backward, which the top level's probe backward waits for, then shares the
 # GPU with one kernel less; 6.14 -> 6.08 ms at c2)
 DMIX0_LATE = True
+# The reads' backward of the levels below the top one on the first side
+# stream: beside the top level's (False), or after it, beside the top level's
+# reverse scan and probe backward (True: the top level's reads backward,
+# which starts the chain, then has the GPU to itself; at c2 0.234 -> 0.162
+# ms, step 5.32-5.33 -> 5.30-5.31 ms)
+READS_AFTER_TOP = True
 
 
 def _chain_ok(K, N, merge):
@@ -396,8 +402,10 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
         # With one group of rows, independent launches go to two side streams:
         # (a) the reads' backward of the levels below the top one
         # (each writes its own columns of dmix and dq and its own d_states)
-        # beside the top level's read, reverse scan and probe backward (whose
-        # lower-state gradient goes to an injection, not into d_states),
+        # beside the top level's reverse scan and probe backward (after the
+        # top level's read, or beside it when READS_AFTER_TOP is off; the
+        # probe backward's lower-state gradient goes to an injection, not
+        # into d_states),
         # joined before the first reverse scan that reads those d_states; (b) each
         # level's parameter-gradient sums (reading only that level's
         # workspaces) and dmix_0 (before level 1's sums, or at the fork when
@@ -422,12 +430,15 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
             dmix0_done.append(True)
         if not (DMIX0_LATE and aux is not None):
             dmix0()
-        for lvl in range(1, L):
+        late = READS_AFTER_TOP and aux is not None
+        for lvl in ([L - 1] + list(range(1, L - 1)) if late else range(1, L)):
             ng = n_groups(NT, f[lvl])
             top = lvl == L - 1
             _lib.call("ngdn_read_state_bwd", ctypes.byref(d), lvl, f[lvl], ng,
                       *(P(R(x)) for x in (q_, mix_, do_, states[lvl], d_states[lvl], dq, dmix)),
                       sp if top else sa, tag=f"ngdn_read_state_bwd.{lvl}", stream=st if top else ta)
+            if late and top:
+                aux[0].wait_stream(st)
         joined = aux is None
         inj, nf1 = None, 0
         for lvl in range(L - 1, 0, -1):
