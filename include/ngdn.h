@@ -69,7 +69,7 @@ const char* ngdn_last_error(void);
  * 0.5.0 took W and U out of ngdn_l0_bwd; 0.6.0 moved the upper levels'
  * lower-state gradients from ngdn_probe_bwd's d_below to an injection that
  * ngdn_upper_scan_bwd adds. */
-#define NGDN_VERSION 600
+#define NGDN_VERSION 700
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -84,11 +84,14 @@ const char* ngdn_arch(void);
  * plane of a unit tile [R][C], the 16 x 32 block (rb, cb) is 512
  * consecutive elements at 512 (rb C/32 + cb), element (r, c) of the block
  * at 8 (16 (c / 8) + r) + c % 8, so one matrix-core A fragment of a row tile
- * is one contiguous 1 KB read. */
+ * is one contiguous 1 KB read. Only chunks [chunk0, chunk0 + nchunk) of every
+ * (batch, head) are formed (1 <= nchunk, chunk0 + nchunk <= NT): a caller can
+ * form later chunks while the level-0 scan runs over earlier ones. */
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
-                          float* Aqk, float* gam, float* TT, void* stream);
+                          float* Aqk, float* gam, float* TT, int32_t chunk0,
+                          int32_t nchunk, void* stream);
 
 /* Level-0 state recurrence over chunks: the inter-chunk half of fla's
  * chunk_gdn2_fwd (ops/chunk.py:236-248; semantics ops/naive.py:367-392).
@@ -101,12 +104,17 @@ int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
  * with read0), formed while the state is on chip, which
  * ngdn_output_upper_fwd turns into o. initial_state may be NULL (zeros).
  * W, U, KtT, gam, Qg, Aqk as ngdn_l0_intra_fwd writes them (bf16: the split
- * ones in fragment order). */
+ * ones in fragment order). Runs chunks [chunk0, chunk0 + nchunk) (1 <=
+ * nchunk, chunk0 + nchunk <= NT): initial_state is then the state entering
+ * chunk chunk0 and final_state receives the state after the last; the
+ * per-chunk outputs are written at their chunks' places. initial_state may
+ * be final_state itself (each workgroup reads its slice before writing it),
+ * so consecutive ranges carry the state through final_state. */
 int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam, const float* Qg,
                          const float* Aqk, const float* initial_state, int32_t hT_every,
                          float* hT, float* vnT, float* h, float* vn, float* read0,
-                         float* final_state, void* stream);
+                         float* final_state, int32_t chunk0, int32_t nchunk, void* stream);
 
 /* Promotion probe of level `level` >= 1: PROBES[promotion] applied to the
  * lower level's state after each of this level's firings

@@ -9,7 +9,8 @@ stream. There is no CPU or PyTorch fallback: without the built library or a
 GPU the op raises.
 
 Forward, per call (reference composition ops/chunk.py:159-304):
-  ngdn_l0_intra_fwd    per-chunk level-0 terms, all chunks in parallel
+  ngdn_l0_intra_fwd    per-chunk level-0 terms, all chunks in parallel (on
+                       small grids range by range, beside the scan)
   ngdn_l0_scan_fwd     level-0 state recurrence: states h per chunk, and
                        the level-0 read (Qg h + Aqk Vn) per row; the states
                        the level above reads (every f_1-th) when L > 1
@@ -111,6 +112,28 @@ DMIX0_LATE = True
 # which starts the chain, then has the GPU to itself; at c2 0.234 -> 0.162
 # ms, step 5.32-5.33 -> 5.30-5.31 ms)
 READS_AFTER_TOP = True
+
+
+# Small grids (a long sequence in a small batch: the bf16 level-0 scan then
+# runs at most 128 workgroups of 16 columns, half the CUs or fewer): the
+# level-0 chunk terms and scan run over L0_PARTS consecutive ranges of
+# chunks (at least 64 chunks each), the chunk terms of a range on a side
+# stream while the scan works through the range before it; the scan carries
+# its state from range to range through the final state, so every chunk's
+# arithmetic is that of one launch over all chunks. "Small" is the C
+# library's own test for 16-column scan slices (a 32-column grid of at most
+# 64 workgroups). Config 3 (T = 65536, B H = 16): 5.47 -> 5.01 ms per forward
+# (4 ranges 5.16, 16 ranges 5.08).
+L0_PARTS = 8
+
+
+def _l0_ranges(B, H, V, NT, code):
+    """Chunk ranges (c0, n) of the level-0 forward: one for a grid that
+    fills the GPU, else up to L0_PARTS of at least 64 chunks."""
+    narrow = code == _lib.NGDN_BF16 and B * H * (V // 32) <= 64
+    parts = max(1, min(int(L0_PARTS), NT // 64)) if narrow else 1
+    bounds = [NT * p // parts for p in range(parts + 1)]
+    return [(bounds[p], bounds[p + 1] - bounds[p]) for p in range(parts)]
 
 
 def _chain_ok(K, N, merge):
@@ -250,11 +273,25 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
         R = _rows(b0, nb)
         sp = _lib.ptr_of_stream(st)
         d = _lib.dims(nb, T, H, L, K, V, code, scale, hold_partial=NTF < NT)
-        _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, TT)), sp)
-        _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
-            W, U, KtT, gam, Qg, Aqk, init_)), f[1] if L > 1 else 1,
-            *(P(R(x)) for x in (hT, None, h_, vn_, read0, final)), sp)
+        ranges = _l0_ranges(nb, H, V, NT, code) if nb == B else [(0, NT)]
+        ts = _aux_streams(dev)[0] if len(ranges) > 1 else st
+        if ts is not st:
+            ts.wait_event(st.record_event())
+        # every range's chunk terms queued at once on the side stream (holding
+        # them to one or two ranges ahead of the scan measured slower)
+        ready = []
+        for c0, n in ranges:
+            _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+                q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, TT)), c0, n,
+                _lib.ptr_of_stream(ts), stream=ts)
+            ready.append(ts.record_event() if ts is not st else None)
+        for p, (c0, n) in enumerate(ranges):
+            if ready[p] is not None:
+                st.wait_event(ready[p])
+            # a range after the first starts from the state the one before left in final
+            _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
+                W, U, KtT, gam, Qg, Aqk, init_ if p == 0 else final)), f[1] if L > 1 else 1,
+                *(P(R(x)) for x in (hT, None, h_, vn_, read0, final)), c0, n, sp)
         for lvl in range(1, L):
             lv = levels[lvl]
             fh, fb = f[lvl], f[lvl - 1]

@@ -43,6 +43,13 @@ int32_t check_dims(const ngdn_dims* d, const char* what) {
 }
 
 inline int nchunks(const ngdn_dims* d) { return (d->T + ngdn::CH - 1) / ngdn::CH; }
+// chunks [chunk0, chunk0 + nchunk) inside the sequence's NT chunks
+int32_t check_range(const ngdn_dims* d, int32_t chunk0, int32_t nchunk, const char* what) {
+  if (chunk0 < 0 || nchunk < 1 || chunk0 > nchunks(d) - nchunk)
+    return fail(NGDN_EINVAL, "%s: chunks [%d, %d + %d) outside the %d chunks of the sequence",
+                what, chunk0, chunk0, nchunk, nchunks(d));
+  return NGDN_OK;
+}
 // chunks whose end can complete an upper level's firing
 inline int fire_chunks(const ngdn_dims* d) {
   return d->hold_partial ? d->T / ngdn::CH : nchunks(d);
@@ -59,13 +66,15 @@ const char* ngdn_arch(void) { return "gfx950"; }
 int32_t ngdn_l0_intra_fwd(const ngdn_dims* d, const void* q, const void* k,
                           const void* v, const float* g, const void* b,
                           const void* w, float* W, float* U, float* KtT, float* Qg,
-                          float* Aqk, float* gam, float* TT, void* stream) {
+                          float* Aqk, float* gam, float* TT, int32_t chunk0,
+                          int32_t nchunk, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_intra_fwd")) return r;
   if (!q || !k || !v || !g || !b || !w || !W || !U || !KtT || !Qg || !Aqk || !gam)
     return fail(NGDN_EINVAL, "ngdn_l0_intra_fwd: NULL tensor");
+  if (int32_t r = check_range(d, chunk0, nchunk, "ngdn_l0_intra_fwd")) return r;
   ngdn::L0IntraArgs a{q, k, v, g, b, w, W, U, KtT, Qg, Aqk, gam, TT,
-                      d->B, d->T, d->H, d->L, nchunks(d), d->scale};
+                      d->B, d->T, d->H, d->L, nchunks(d), d->scale, chunk0, nchunk};
   return launched(ngdn::l0_intra_fwd(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_intra_fwd");
 }
@@ -74,11 +83,12 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
                          const float* KtT, const float* gam, const float* Qg,
                          const float* Aqk, const float* initial_state, int32_t hT_every,
                          float* hT, float* vnT, float* h, float* vn, float* read0,
-                         float* final_state, void* stream) {
+                         float* final_state, int32_t chunk0, int32_t nchunk, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_fwd")) return r;
   if (!W || !U || !KtT || !gam || !final_state || (read0 && (!Qg || !Aqk)))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_fwd: NULL tensor");
+  if (int32_t r = check_range(d, chunk0, nchunk, "ngdn_l0_scan_fwd")) return r;
   if (hT && hT_every < 1)
     return fail(NGDN_EINVAL, "ngdn_l0_scan_fwd: hT_every must be >= 1, got %d", hT_every);
   const long long skv = (long long)d->K * d->V;
@@ -91,6 +101,7 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
   a.fin = final_state; a.fin_sh = d->L * skv; a.fin_sb = d->H * a.fin_sh;
   a.B = d->B; a.H = d->H; a.S = nchunks(d); a.M = ngdn::CH; a.V = d->V;
   a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // W, KtT, Qg, Aqk: fragment order
+  a.j0 = chunk0; a.j1 = chunk0 + nchunk;
   return launched(ngdn::scan_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_fwd");
 }
 

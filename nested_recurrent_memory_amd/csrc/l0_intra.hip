@@ -38,8 +38,9 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 2 : 1) void l0_intra_fwd_kern
   constexpr int KS = Mma<E>::KS;
   typedef typename Mma<E>::SFrag SF;
   const int NT = a.NT, H = a.H;
-  const int n = blockIdx.x % NT;
-  const int bh = blockIdx.x / NT;
+  const int nn = a.nn > 0 ? a.nn : NT;
+  const int n = a.n0 + (int)(blockIdx.x % nn);
+  const int bh = blockIdx.x / nn;
   const int h = bh % H, b = bh / H;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
 
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256, sizeof(E) == 2 ? 2 : 1) void l0_intra_fwd_kern
 
 template <typename E, int K, int V>
 static hipError_t launch_l0_intra(const L0IntraArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * a.NT);
+  const unsigned grid = (unsigned)(a.B * a.H * (a.nn > 0 ? a.nn : a.NT));
   hipLaunchKernelGGL((l0_intra_fwd_kernel<E, K, V>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }

@@ -20,6 +20,7 @@ struct L0IntraArgs {
   float* TT;
   int B, T, H, L, NT;
   float scale;
+  int n0, nn;         // chunks [n0, n0 + nn) of every (batch, head) (nn 0: all NT)
 };
 hipError_t l0_intra_fwd(const L0IntraArgs& a, int dtype, int K, int V, hipStream_t st);
 
@@ -67,6 +68,8 @@ struct ScanArgs {
   // bf16, fragment order as the chunk terms and the probes write them:
   // 1, BT (M % 32 == 0); 3, also A, Qg, Aqk (level 0); 0, none
   int frag;
+  // steps [j0, j1) from init, the state entering step j0 (j1 0: all S)
+  int j0, j1;
 };
 hipError_t scan_fwd(const ScanArgs& a, int dtype, int K, hipStream_t st);
 

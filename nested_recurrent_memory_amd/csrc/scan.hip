@@ -297,25 +297,27 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   };
 
   Ops nxt;
-  if (S > 0) load(0, nxt);
-  for (int j = 0; j < S; ++j) {
+  // steps [j0, j1): the state registers start from init, the state entering j0
+  const int j0 = a.j0, j1 = a.j1 > 0 ? a.j1 : S;
+  if (j1 > j0) load(j0, nxt);
+  for (int j = j0; j < j1; ++j) {
     const Ops cur = nxt;
     if constexpr (LATE) {
       // ---- the next step's operand loads first (the last step reloads its
       // own, so that no branch guards them); this step's stores follow its
       // products
-      load(j + 1 < S ? j + 1 : j, nxt);
+      load(j + 1 < j1 ? j + 1 : j, nxt);
     } else {
       // ---- state entering step j (and the previous step's Vn and read) to
       // global, then the next step's operand loads
       store_state(j);
-      if (DEFER && j > 0) flush(j - 1);
-      if (j + 1 < S) load(j + 1, nxt);
+      if (DEFER && j > j0) flush(j - 1);
+      if (j + 1 < j1) load(j + 1, nxt);
     }
     step(j, cur);
   }
-  if (!LATE && DEFER && S > 0) flush(S - 1);
-  if (a.state_mode == 1) {
+  if (!LATE && DEFER && j1 > j0) flush(j1 - 1);
+  if (a.state_mode == 1 && j1 == S) {
     for (int j = S; j < a.NG; ++j) store_state(j);
   }
 #pragma unroll

@@ -80,7 +80,7 @@ def test_interface_version_matches_header_and_loader():
 def test_invalid_arguments_return_error_without_launch():
     so = _lib.lib()
     d = _lib.dims(1, 64, 1, 1, 96, 64, _lib.NGDN_BF16, 0.1)   # K=96 unsupported
-    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 14))
+    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 13), 0, 1, None)
     assert rc == 1
     assert b"K=96" in so.ngdn_last_error()
     d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
@@ -89,7 +89,7 @@ def test_invalid_arguments_return_error_without_launch():
     assert rc == 1 and b"power of two" in so.ngdn_last_error()
     d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
     d.hold_partial = 2
-    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 14))
+    rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([None] * 13), 0, 1, None)
     assert rc == 1 and b"hold_partial 2" in so.ngdn_last_error()
 
 

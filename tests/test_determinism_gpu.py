@@ -60,3 +60,26 @@ def test_three_levels_two_runs_and_two_row_groups_are_bit_identical(promotion, d
     finally:
         chunk_mod.STREAM_GROUPS = 1
     _assert_equal(first, grouped)
+
+
+@pytest.mark.parametrize("T", [64 * 256, 64 * 200 + 17])
+def test_level0_chunk_ranges_equal_one_launch(T):
+    """On small grids the forward forms the level-0 chunk terms and runs the
+    level-0 scan over consecutive ranges of chunks, the chunk terms of a range
+    on a side stream beside the scan of the range before, the state carried
+    from range to range through the final state. Outputs, final states and
+    every gradient equal those of one launch over all chunks, bit for bit
+    (including a partial last chunk in the last range)."""
+    NT = -(-T // 64)
+    from nested_recurrent_memory_amd import _lib
+    assert len(chunk_mod._l0_ranges(1, 2, 64, NT, _lib.NGDN_BF16)) > 1
+    inp = make_inputs(B=1, T=T, H=2, K=64, V=64, L=3, N=32,
+                      intervals=(1, 4, 16), dtype=torch.bfloat16, g_scale=0.1)
+    ranged = _grads(inp, 3, "learned")
+    saved = chunk_mod.L0_PARTS
+    try:
+        chunk_mod.L0_PARTS = 1
+        single = _grads(inp, 3, "learned")
+    finally:
+        chunk_mod.L0_PARTS = saved
+    _assert_equal(ranged, single)

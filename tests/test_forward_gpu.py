@@ -79,7 +79,7 @@ def test_l0_intra_terms(dtype, K, V, T, g_scale):
     P = _lib.ptr
     _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(g[n]) for n in ("q", "k", "v", "g", "b", "w")),
               *(P(out[n]) for n in ("W", "U", "KtT", "Qg", "Aqk", "gam")),
-              P(out["TT"]), _lib.stream_of(g["q"]))
+              P(out["TT"]), 0, NT, _lib.stream_of(g["q"]))
     torch.cuda.synchronize()
 
     pad = NT * 64 - T
@@ -328,9 +328,9 @@ def test_output_entry_points_agree(dtype, L):
         P = _lib.ptr
         st = _lib.stream_of(q_)
         _lib.call("ngdn_l0_intra_fwd", ctypes.byref(d), *(P(x) for x in (
-            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam)), None, None, None, None, None, st)
+            q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam)), None, 0, NT, st)
         _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(x) for x in (W, U, KtT, gam, None, None,
-                  None)), 1, P(hT), P(vnT), None, None, None, P(final), st)
+                  None)), 1, P(hT), P(vnT), None, None, None, P(final), 0, NT, st)
         # upper levels' group states: from the op's own path (states of levels >= 1)
         saved = chunk_mod._forward(*(leaves[n] for n in NAMES[:12]), nq, list(f), L,
                                    K ** -0.5, None, "learned", True)[2]
