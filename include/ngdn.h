@@ -69,7 +69,7 @@ const char* ngdn_last_error(void);
  * 0.5.0 took W and U out of ngdn_l0_bwd; 0.6.0 moved the upper levels'
  * lower-state gradients from ngdn_probe_bwd's d_below to an injection that
  * ngdn_upper_scan_bwd adds. */
-#define NGDN_VERSION 700
+#define NGDN_VERSION 800
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -132,7 +132,10 @@ int32_t ngdn_l0_scan_fwd(const ngdn_dims* d, const float* W, const float* U,
  * Fragment order: for NGDN_BF16 with N % 32 == 0, each plane of the [K][N]
  * tiles KT and AT is in the fragment order described at ngdn_l0_intra_fwd
  * (C = N); A and keysN stay row-major. ngdn_upper_scan_fwd / _bwd read KT and
- * AT that way; a caller that writes or reads them itself must use it too. */
+ * AT that way; a caller that writes or reads them itself must use it too.
+ * Only firings [firing0, firing0 + nfiring) are probed (0 <= firing0,
+ * firing0 + nfiring <= NF; nfiring 0 does nothing): a caller can probe the
+ * firings whose lower state is stored while the lower level still runs. */
 int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        int32_t n_queries, int32_t f_below, int32_t f_here,
                        const float* below, int32_t ng_below,
@@ -141,7 +144,7 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const void* bpT, const void* wpT, const void* gpT,
                        float* A, float* KT, float* U, float* gam, float* keysN,
                        float* AT, float* keys, float* vals, float* bo, float* wo,
-                       float* go, void* stream);
+                       float* go, int32_t firing0, int32_t nfiring, void* stream);
 
 /* Write scan of level `level` >= 1 (ops/update_fwd.py:131-204) from the
  * probe's scan-ready pairs (A row-major; KT in fragment order for NGDN_BF16
@@ -150,12 +153,18 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
  * states. Writes states [B,NG,H,K,V] fp32 (state entering each group; groups
  * past the last firing hold the final state), statesT [B,NG,H,V,K] (the same,
  * transposed; may be NULL) and final_state[:, :, level]. initial_state may be
- * NULL. */
+ * NULL. Runs firings [step0, step0 + nstep) (1 <= nstep, step0 + nstep <= NF;
+ * with NF = 0, step0 = nstep = 0): initial_state[:, :, level] is then the
+ * state entering firing step0 and final_state[:, :, level] receives the
+ * state after the last; the range ending at NF also stores the groups past
+ * the last firing. initial_state may be final_state itself, so consecutive
+ * ranges carry the state through it. */
 int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* A,
                             const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
-                            float* statesT, float* final_state, void* stream);
+                            float* statesT, float* final_state, int32_t step0,
+                            int32_t nstep, void* stream);
 
 /* The promotions of level `level` >= 1, fused: the reference's per-level
  * chain gather_source -> probe_learned / probe_merge -> update_state

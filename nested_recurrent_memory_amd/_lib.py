@@ -20,7 +20,7 @@ NGDN_BF16 = 1
 # NGDN_VERSION of include/ngdn.h: the interface the signatures below describe.
 # The loader refuses a library of another version (working-tensor layouts and
 # argument meanings changed between versions under unchanged signatures).
-VERSION = 700
+VERSION = 800
 
 
 class Dims(ctypes.Structure):
@@ -45,8 +45,8 @@ SIGNATURES = {
     "ngdn_l0_intra_fwd": [PD] + [P] * 6 + [P] * 6 + [P] + [I32, I32] + [P],
     "ngdn_l0_scan_fwd": [PD, P, P, P, P, P, P, P, I32, P, P, P, P, P, P, I32, I32, P],
     "ngdn_probe_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
-                      + [P] * 11 + [P],
-    "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P],
+                      + [P] * 11 + [I32, I32, P],
+    "ngdn_upper_scan_fwd": [PD, I32, I32, I32, I32, P, P, P, P, P, P, P, P, I32, I32, P],
     "ngdn_promote_chain_fwd": [PD, I32, I32, I32, I32, I32, P, I32, P, P, I32, P, P, P, P]
                               + [P] * 6 + [P],
     "ngdn_output_fwd": [PD, P, P, P, P, P, P, P, P, P, P, P, P],

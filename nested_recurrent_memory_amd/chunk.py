@@ -285,6 +285,12 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                 q_, k_, v_, g_, b_, w_, W, U, KtT, Qg, Aqk, gam, TT)), c0, n,
                 _lib.ptr_of_stream(ts), stream=ts)
             ready.append(ts.record_event() if ts is not st else None)
+        # with several ranges and unfused promotions, the upper levels follow
+        # on a second side stream, one range behind: after level-0 range p,
+        # each level probes and scans the firings whose lower state is stored
+        tu = (_aux_streams(dev)[1] if len(ranges) > 1 and L > 1
+              and not any(levels[lvl]["chain"] for lvl in range(1, L)) else None)
+        done = [0] * L          # firings of each level probed and scanned so far
         for p, (c0, n) in enumerate(ranges):
             if ready[p] is not None:
                 st.wait_event(ready[p])
@@ -292,9 +298,34 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
             _lib.call("ngdn_l0_scan_fwd", ctypes.byref(d), *(P(R(x)) for x in (
                 W, U, KtT, gam, Qg, Aqk, init_ if p == 0 else final)), f[1] if L > 1 else 1,
                 *(P(R(x)) for x in (hT, None, h_, vn_, read0, final)), c0, n, sp)
+            if tu is not None:
+                tu.wait_event(st.record_event())
+                upper_batch(d, R, done, c0 + n, p == len(ranges) - 1, tu)
+        if tu is not None:
+            st.wait_event(tu.record_event())
+        else:
+            upper_batch(d, R, done, NT, True, st)
+        spT, ngs, fs = _level_arrays([R(x) for x in statesT], NT, f, L)
+        _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(R(read0)), P(R(q_)),
+                  P(R(mix_)), spT, ngs, fs, P(R(o)), sp)
+
+    def upper_batch(d, R, done, avail, last, su):
+        """Probes and scans of every upper level for the firings whose lower
+        state is stored: level 0 has stored the states entering chunks
+        [0, avail); each level then has stored the groups entering its firings
+        so far. A firing i reads the lower level's stored state
+        ((i + 1) f_here) / f_below, so the firings with (i + 1) f_here <
+        avail f_below are ready; the last batch takes the rest (including
+        those that read the lower final state) and stores every level's
+        trailing groups. d and R: the launch's dims and batch rows; su: the
+        stream."""
+        sp = _lib.ptr_of_stream(su)
         for lvl in range(1, L):
             lv = levels[lvl]
             fh, fb = f[lvl], f[lvl - 1]
+            nf = lv["nf"]
+            upto = nf if last else min(nf, max(0, (avail * fb - 1) // fh))
+            i0 = done[lvl]
             if lv["chain"]:
                 belowT, ngb = (hT, NT) if lvl == 1 else (statesT[lvl - 1], n_groups(NT, fb))
                 _lib.call("ngdn_promote_chain_fwd", ctypes.byref(d), lvl, int(merge), lv["N"], fb,
@@ -305,19 +336,23 @@ def _forward(q, k, v, g, b, w, mix, qb, kp, bp, wp, gp, nq, f, L, scale,
                           tag=f"ngdn_promote_chain_fwd.{lvl}")
                 continue
             below, ngb = (hT, NT) if lvl == 1 else (states[lvl - 1], n_groups(NT, fb))
-            if lv["nf"] > 0:
+            if upto > i0:
                 _lib.call("ngdn_probe_fwd", ctypes.byref(d), lvl, int(merge), lv["N"], fb, fh,
                           P(R(below)), ngb, P(R(final)), P(par["qb"]), par["nmax"],
                           P(par["kp"]), P(par["bpT"]), P(par["wpT"]), P(par["gpT"]),
                           *(P(R(lv[x])) for x in ("A", "KT", "U", "gam", "keys", "AT")),
-                          None, None, None, None, None, sp, tag=f"ngdn_probe_fwd.{lvl}")
-            _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, lv["N"], lv["nf"], lv["ng"],
-                      *(P(R(lv[x])) for x in ("A", "KT", "U", "gam")), P(R(init_)),
-                      P(R(states[lvl])), P(R(statesT[lvl])), P(R(final)), sp,
-                      tag=f"ngdn_upper_scan_fwd.{lvl}")
-        spT, ngs, fs = _level_arrays([R(x) for x in statesT], NT, f, L)
-        _lib.call("ngdn_output_upper_fwd", ctypes.byref(d), P(R(read0)), P(R(q_)),
-                  P(R(mix_)), spT, ngs, fs, P(R(o)), sp)
+                          None, None, None, None, None, i0, upto - i0, sp,
+                          tag=f"ngdn_probe_fwd.{lvl}", stream=su)
+            if upto > i0 or (last and nf == 0):
+                # a range after the level's first starts from the state in final
+                _lib.call("ngdn_upper_scan_fwd", ctypes.byref(d), lvl, lv["N"], nf, lv["ng"],
+                          *(P(R(lv[x])) for x in ("A", "KT", "U", "gam")),
+                          P(R(init_ if i0 == 0 else final)),
+                          P(R(states[lvl])), P(R(statesT[lvl])), P(R(final)), i0, upto - i0, sp,
+                          tag=f"ngdn_upper_scan_fwd.{lvl}", stream=su)
+            done[lvl] = upto
+            # the groups of this level stored so far bound the level above's firings
+            avail = upto
 
     _run_groups(B, dev, launch)
     saved = None

@@ -113,7 +113,7 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
                        const void* bpT, const void* wpT, const void* gpT,
                        float* A, float* KT, float* U, float* gam, float* keysN,
                        float* AT, float* keys, float* vals, float* bo, float* wo,
-                       float* go, void* stream) {
+                       float* go, int32_t firing0, int32_t nfiring, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_probe_fwd")) return r;
   if (level < 1 || level >= d->L)
@@ -150,7 +150,11 @@ int32_t ngdn_probe_fwd(const ngdn_dims* d, int32_t level, int32_t promotion,
   a.A = A; a.KT = KT; a.U = U; a.gam = gam; a.keysN = keysN; a.AT = AT;
   a.keys = keys; a.vals = vals; a.bo = bo; a.wo = wo; a.go = go;
   a.B = d->B; a.H = d->H; a.NF = fire_chunks(d) / f_here; a.N = N; a.V = d->V;
-  if (a.NF == 0) return NGDN_OK;
+  if (firing0 < 0 || nfiring < 0 || firing0 > a.NF - nfiring)
+    return fail(NGDN_EINVAL, "ngdn_probe_fwd: firings [%d, %d + %d) outside the level's %d",
+                firing0, firing0, nfiring, a.NF);
+  if (nfiring == 0) return NGDN_OK;
+  a.i0 = firing0; a.ni = nfiring;
   return launched(ngdn::probe_fwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_probe_fwd");
 }
 
@@ -216,7 +220,8 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
                             int32_t nf, int32_t ng, const float* A,
                             const float* KT, const float* U, const float* gam,
                             const float* initial_state, float* states,
-                            float* statesT, float* final_state, void* stream) {
+                            float* statesT, float* final_state, int32_t step0,
+                            int32_t nstep, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_upper_scan_fwd")) return r;
   if (level < 1 || level >= d->L)
@@ -228,9 +233,13 @@ int32_t ngdn_upper_scan_fwd(const ngdn_dims* d, int32_t level, int32_t n_pairs,
     return fail(NGDN_EINVAL, "ngdn_upper_scan_fwd: NF=%d inconsistent with n_groups=%d", nf, ng);
   if ((nf > 0 && (!A || !KT || !U || !gam)) || !states || !final_state)
     return fail(NGDN_EINVAL, "ngdn_upper_scan_fwd: NULL tensor");
+  if (nf > 0 ? (step0 < 0 || nstep < 1 || step0 > nf - nstep) : (step0 != 0 || nstep != 0))
+    return fail(NGDN_EINVAL, "ngdn_upper_scan_fwd: firings [%d, %d + %d) outside the level's %d",
+                step0, step0, nstep, nf);
   const long long skv = (long long)d->K * d->V;
   ngdn::ScanArgs a{};
   a.A = A; a.BT = KT; a.U = U; a.gam = gam;
+  a.j0 = step0; a.j1 = step0 + nstep;
   a.init = initial_state ? initial_state + (long long)level * skv : nullptr;
   a.init_sh = d->L * skv; a.init_sb = d->H * a.init_sh;
   a.st_kv = states; a.st_vk = statesT; a.state_mode = 1; a.NG = ng;

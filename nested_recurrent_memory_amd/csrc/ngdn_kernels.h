@@ -132,6 +132,7 @@ struct ProbeArgs {
   float* keys; float* vals; float* bo; float* wo; float* go;
   int B, H, NF, N, V;
   FireGate gate;
+  int i0, ni;         // firings [i0, i0 + ni) (ni 0: all NF)
 };
 hipError_t probe_fwd(const ProbeArgs& a, int dtype, int K, hipStream_t st);
 

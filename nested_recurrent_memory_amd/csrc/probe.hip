@@ -44,7 +44,8 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
 
   const int NF = a.NF, H = a.H;
   int b, h, i;
-  head_xcd_split(blockIdx.x, H, NF, b, h, i);
+  head_xcd_split(blockIdx.x, H, a.ni > 0 ? a.ni : NF, b, h, i);
+  i += a.i0;
   const int bh = b * H + h;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const int rl = lane & 15, ko = kofs<E>(lane);
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(512) void probe_fwd_kernel(ProbeArgs a) {
 
 template <typename E, int K, int N, bool MERGE>
 static hipError_t launch_probe(const ProbeArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * a.NF);
+  const unsigned grid = (unsigned)(a.B * a.H * (a.ni > 0 ? a.ni : a.NF));
   if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL((probe_fwd_kernel<E, K, N, MERGE>), dim3(grid), dim3(512), 0, st, a);
   return hipGetLastError();

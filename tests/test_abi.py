@@ -85,7 +85,7 @@ def test_invalid_arguments_return_error_without_launch():
     assert b"K=96" in so.ngdn_last_error()
     d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
     rc = so.ngdn_probe_fwd(ctypes.byref(d), 1, 0, 24, 1, 2, None, 0, None, None, 32,
-                           *([None] * 16))
+                           *([None] * 15), 0, 0, None)
     assert rc == 1 and b"power of two" in so.ngdn_last_error()
     d = _lib.dims(1, 64, 1, 2, 64, 64, _lib.NGDN_BF16, 0.1)
     d.hold_partial = 2
