@@ -17,10 +17,11 @@ from nested_recurrent_memory_amd.inputs import CONFIGS, LEAVES, NAMES, make_cota
 pytestmark = pytest.mark.gpu
 
 
-def _grads(inp, L, promotion, seed=3):
+def _grads(inp, L, promotion, seed=3, fire_partial=True):
     gpu = {n: (inp[n].cuda().requires_grad_(True) if n in LEAVES else inp[n].cuda())
            for n in NAMES}
-    o, s = chunk_nested_gdn2(**gpu, L=L, output_final_state=True, promotion=promotion)
+    o, s = chunk_nested_gdn2(**gpu, L=L, output_final_state=True, promotion=promotion,
+                             fire_partial_chunk=fire_partial)
     do = make_cotangent(o.shape, seed=seed).cuda().to(o.dtype)
     ds = make_cotangent(s.shape, seed=seed + 1).cuda()
     torch.autograd.backward([o, s], [do, ds])
@@ -62,24 +63,31 @@ def test_three_levels_two_runs_and_two_row_groups_are_bit_identical(promotion, d
     _assert_equal(first, grouped)
 
 
-@pytest.mark.parametrize("T", [64 * 256, 64 * 200 + 17])
-def test_level0_chunk_ranges_equal_one_launch(T):
+@pytest.mark.parametrize("T,promotion,fire_partial,fused", [
+    (64 * 256, "learned", True, False), (64 * 200 + 17, "learned", True, False),
+    (64 * 200 + 17, "merge", True, False), (64 * 200 + 17, "learned", False, False),
+    (64 * 200 + 17, "learned", True, True)])
+def test_level0_chunk_ranges_equal_one_launch(T, promotion, fire_partial, fused):
     """On small grids the forward forms the level-0 chunk terms and runs the
     level-0 scan over consecutive ranges of chunks, the chunk terms of a range
     on a side stream beside the scan of the range before, the state carried
-    from range to range through the final state. Outputs, final states and
-    every gradient equal those of one launch over all chunks, bit for bit
-    (including a partial last chunk in the last range)."""
+    from range to range through the final state; the upper levels' probes and
+    scans follow one range behind on a second side stream. Outputs, final
+    states and every gradient equal those of one launch over all chunks, bit
+    for bit: with a partial last chunk, firings that read a lower final state
+    (T = 64 * 256), merge promotion, a held partial chunk, and the fused
+    promotion ladder (whose levels then run after the level-0 ranges)."""
     NT = -(-T // 64)
     from nested_recurrent_memory_amd import _lib
     assert len(chunk_mod._l0_ranges(1, 2, 64, NT, _lib.NGDN_BF16)) > 1
     inp = make_inputs(B=1, T=T, H=2, K=64, V=64, L=3, N=32,
                       intervals=(1, 4, 16), dtype=torch.bfloat16, g_scale=0.1)
-    ranged = _grads(inp, 3, "learned")
-    saved = chunk_mod.L0_PARTS
+    saved = chunk_mod.L0_PARTS, chunk_mod.FUSED_PROMOTION
     try:
+        chunk_mod.FUSED_PROMOTION = fused
+        ranged = _grads(inp, 3, promotion, fire_partial=fire_partial)
         chunk_mod.L0_PARTS = 1
-        single = _grads(inp, 3, "learned")
+        single = _grads(inp, 3, promotion, fire_partial=fire_partial)
     finally:
-        chunk_mod.L0_PARTS = saved
+        chunk_mod.L0_PARTS, chunk_mod.FUSED_PROMOTION = saved
     _assert_equal(ranged, single)
