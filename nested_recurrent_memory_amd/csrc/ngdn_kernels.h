@@ -43,6 +43,10 @@ __device__ __forceinline__ bool gated_out(const FireGate& g, int b) {
 // Columns of V per scan workgroup (each step's operands are read by V / 32
 // workgroups of one (batch, head)).
 constexpr int SCAN_BV = 32;
+// The bf16 scans take 16-column slices, twice the workgroups with half the
+// products per step, when the 32-column grid has at most this many
+// workgroups (a quarter of the CUs).
+constexpr int SCAN_NARROW_GRID = 64;
 
 // A sequence of delta-rule steps per (b, h):
 //   Vn = U - A S;   S <- diag(gam) S + BT Vn

@@ -331,11 +331,6 @@ __global__ __launch_bounds__(NWV * WAVE) void scan_fwd_kernel(ScanArgs a) {
   }
 }
 
-// The bf16 forward scans run 16-column slices when the 32-column grid has at
-// most this many workgroups (a quarter of the CUs).
-#ifndef NARROW_GRID
-#define NARROW_GRID 64
-#endif
 
 // Waves per workgroup: four, one per SIMD. Eight (two per SIMD) leave each
 // wave half the registers, less than a step's operands read ahead need.
@@ -389,7 +384,7 @@ static hipError_t launch_scan(const ScanArgs& a, hipStream_t st) {
   // many workgroups, which costs more than it saves once the grid fills the
   // chip.
   if constexpr (std::is_same<E, bf16>::value && M % 32 == 0) {
-    if (a.frag && a.B * a.H * (a.V / SCAN_BV) <= NARROW_GRID)
+    if (a.frag && a.B * a.H * (a.V / SCAN_BV) <= SCAN_NARROW_GRID)
       return launch_scan_bv<E, K, M, 16>(a, st);
   }
   return launch_scan_bv<E, K, M, SCAN_BV>(a, st);

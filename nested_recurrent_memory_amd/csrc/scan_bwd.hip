@@ -30,9 +30,8 @@ namespace ngdn {
 // ---------------------------------------------------------------- levels >= 1
 //
 // FRB (bf16, M % 32 == 0): AT in fragment order, as the probes write it.
-template <typename E, int K, int M, bool FRB>
+template <typename E, int K, int M, bool FRB, int BV>
 __global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
-  constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;
   constexpr int RTS = K / 16;
   constexpr int TPW = RTS * CT / 4;
@@ -374,10 +373,9 @@ struct SliceCopy {
   }
 };
 
-template <typename E, int K>
+template <typename E, int K, int BV>
 __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
   constexpr int M = CH;
-  constexpr int BV = SCAN_BV;
   constexpr int CT = BV / 16;
   constexpr int RTS = K / 16;
   constexpr int TPW = RTS * CT / 4;           // state tiles per wave
@@ -391,7 +389,7 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
   constexpr int NSM = M / KS;
   constexpr int DOE = M * BV / 256;           // dO elements staged per thread
   constexpr bool BF = std::is_same<E, bf16>::value;
-  static_assert(BV % DOE == 0 && 256 / (BV / DOE) == M && DOE % 8 == 0,
+  static_assert(BV % DOE == 0 && 256 / (BV / DOE) == M && DOE % 4 == 0,
                 "one token row slice per thread");
   static_assert(TPW % CT == 0 && (NCW == 16 || NCW == 32), "state tiles of a wave in whole rows");
   typedef typename Mma<E>::SFrag SF;
@@ -649,16 +647,16 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
   }
 }
 
-template <typename E, int K, int M>
-static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * (a.V / SCAN_BV));
+template <typename E, int K, int M, int BV>
+static hipError_t launch_scan_bwd_bv(const ScanBwdArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.B * a.H * (a.V / BV));
   constexpr bool BF = std::is_same<E, bf16>::value;
   if (a.Qg) {
     // level 0: the forward's tiles, in fragment order for bf16
     if constexpr (M == CH) {
       if (a.frag != (BF ? 3 : 0) || !a.W || !a.KtT || !a.Aqk || !a.dout || !a.mix)
         return hipErrorInvalidValue;
-      hipLaunchKernelGGL((scan_bwd_l0_kernel<E, K>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((scan_bwd_l0_kernel<E, K, BV>), dim3(grid), dim3(256), 0, st, a);
       return hipGetLastError();
     }
     return hipErrorInvalidValue;
@@ -666,10 +664,20 @@ static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
   constexpr bool CAN = M % 32 == 0 && BF;
   if (a.frag && !(CAN && a.frag == 1)) return hipErrorInvalidValue;
   if (CAN && a.frag == 1)
-    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, CAN, BV>), dim3(grid), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, false>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((scan_bwd_kernel<E, K, M, false, BV>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+template <typename E, int K, int M>
+static hipError_t launch_scan_bwd(const ScanBwdArgs& a, hipStream_t st) {
+  // few (batch, head) pairs: the bf16 reverse scans take 16-column slices,
+  // as the forward scans do
+  if constexpr (std::is_same<E, bf16>::value) {
+    if (a.B * a.H * (a.V / SCAN_BV) <= SCAN_NARROW_GRID) return launch_scan_bwd_bv<E, K, M, 16>(a, st);
+  }
+  return launch_scan_bwd_bv<E, K, M, SCAN_BV>(a, st);
 }
 
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st) {
