@@ -69,7 +69,7 @@ const char* ngdn_last_error(void);
  * 0.5.0 took W and U out of ngdn_l0_bwd; 0.6.0 moved the upper levels'
  * lower-state gradients from ngdn_probe_bwd's d_below to an injection that
  * ngdn_upper_scan_bwd adds. */
-#define NGDN_VERSION 800
+#define NGDN_VERSION 900
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -249,13 +249,18 @@ int32_t ngdn_read_state_bwd(const ngdn_dims* d, int32_t level, int32_t f,
  * dh_ext, ops/chunk.py:519-528). d_final [B,H,L,K,V] fp32 (level-0 slot read,
  * may be NULL). Writes dSp [B,H,NT,K,V] (gradient of the state after each
  * chunk), dVn [B,H,NT,64,V] and dVnT [B,H,NT,V,64] (either may be NULL, not
- * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL. */
+ * both; ngdn_l0_bwd reads only dVnT), and d_initial[:, :, 0] when not NULL.
+ * Runs chunks [chunk0, chunk0 + nchunk) (1 <= nchunk, chunk0 + nchunk <= NT)
+ * in reverse: d_final is then the gradient of the state after the range's
+ * last chunk and d_initial receives that of the state entering chunk0; the
+ * two may be the same buffer (each workgroup reads its slice before writing
+ * it), so consecutive ranges, last first, carry the gradient through it. */
 int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
                          const float* gam, const float* Qg, const float* Aqk,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
                          float* dSp, float* dVn, float* dVnT, float* d_initial,
-                         void* stream);
+                         int32_t chunk0, int32_t nchunk, void* stream);
 
 /* Reverse write scan of level `level` >= 1 (ops/update_bwd.py:19-164): keys
  * [B,H,NF,N,K] and AT = (keys*b*e^g)^T [B,H,NF,K,N] (both split; AT in
@@ -302,13 +307,15 @@ int32_t ngdn_l0_bwd_intra(const ngdn_dims* d, const void* q, const void* k,
  * ws_dQg, ws_dKt (fp32 [B,H,NT,64,K] each, no initial contents), the rest
  * stays on chip. dA = -(dX_w W^T + dX_u U^T) is formed as -dX_u Vn^T (the
  * same, since dX_w = -dX_u S^T and W S = U - Vn), so W and U are not read; TT
- * from ngdn_l0_intra_fwd. Outputs as ngdn_l0_bwd_intra. */
+ * from ngdn_l0_intra_fwd. Outputs as ngdn_l0_bwd_intra. Only chunks [chunk0,
+ * chunk0 + nchunk) (1 <= nchunk, chunk0 + nchunk <= NT) are formed: a
+ * caller can run them as soon as ngdn_l0_scan_bwd has covered them. */
 int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void* v,
                     const float* g, const void* b, const void* w,
                     const float* TT, const float* h, const float* dSp,
                     const float* vn, const float* dVnT, const void* dout, const void* mix,
                     float* ws_dQg, float* ws_dKt, void* dq, void* dk, void* dv, float* dg,
-                    void* db, void* dw, void* stream);
+                    void* db, void* dw, int32_t chunk0, int32_t nchunk, void* stream);
 
 /* Backward of level `level`'s firings through its update and probe.
  * The lower level's states as rows (below_kv) and transposed (below_vk):

@@ -20,7 +20,7 @@ NGDN_BF16 = 1
 # NGDN_VERSION of include/ngdn.h: the interface the signatures below describe.
 # The loader refuses a library of another version (working-tensor layouts and
 # argument meanings changed between versions under unchanged signatures).
-VERSION = 800
+VERSION = 900
 
 
 class Dims(ctypes.Structure):
@@ -54,11 +54,11 @@ SIGNATURES = {
     "ngdn_output_upper_fwd": [PD, P, P, P, P, P, P, P, P],
     "ngdn_output_bwd": [PD, P, P, P, P],
     "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P, P, P, P],
-    "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, P],
+    "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, I32, I32, P],
     "ngdn_upper_scan_bwd": [PD, I32, I32, I32, I32, P, P, P, P, P, I32, I32, I32, P, P, P, P, P],
     "ngdn_l0_bwd_state": [PD] + [P] * 6 + [P] * 5 + [P],
     "ngdn_l0_bwd_intra": [PD] + [P] * 6 + [P] * 3 + [P] * 6 + [P] * 6 + [P],
-    "ngdn_l0_bwd": [PD] + [P] * 6 + [P] + [P] * 4 + [P] * 2 + [P] * 2 + [P] * 6 + [P],
+    "ngdn_l0_bwd": [PD] + [P] * 6 + [P] + [P] * 4 + [P] * 2 + [P] * 2 + [P] * 6 + [I32, I32, P],
     "ngdn_probe_bwd": [PD, I32, I32, I32, I32, I32, P, P, I32, P, P, I32, P, P, P, P,
                        P, P, P, P, P, P, P, I32, P, P] + [P] * 6 + [P, P, P] + [P],
     "ngdn_param_grads": [PD, I32, I32, I32, I32, P, P, P, P, P, P, I32, P, P, P, P, P, P, P],

@@ -453,6 +453,14 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
     dVn0 = dWT = dAqk = dgam = None
     # the form the forward saved for (U is kept only for the two-launch form)
     fused_l0 = sv["U"] is None
+    # small grids, one group of rows, the fused chunk backward: the level-0
+    # reverse scan runs the chunk ranges of the forward last first, the
+    # gradient of the state between ranges carried in l0_carry, and each
+    # range's chunk backward runs on a side stream beside the scan of the
+    # range before it
+    l0_ranges = (_l0_ranges(B, H, V, NT, code)
+                 if fused_l0 and max(1, min(STREAM_GROUPS, B)) == 1 else [(0, NT)])
+    l0_carry = f32(B, H, L, K, V) if len(l0_ranges) > 1 else None
     if not fused_l0:
         dVn0, dWT = f32(B, H, NT, 64, V), f32(B, H, NT, K, 64)
         dAqk, dgam = f32(B, H, NT, 64, 64), f32(B, H, NT, K)
@@ -558,15 +566,26 @@ def _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion):
             # (late placement) after the upper levels' parameter-gradient sums
             dmix0()
         # level 0
-        _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
-            "W", "KtT", "gam", "Qg", "Aqk")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
-            P(R(inj)), nf1, P(R(d_final)), P(R(dSp0)), P(R(dVn0)), P(R(dVnT0)), P(R(d_init)), sp)
-        if fused_l0:
-            # the chunk backward in one launch: the state half per chunk
-            _lib.call("ngdn_l0_bwd", ctypes.byref(d), *(P(R(x)) for x in (
-                q_, k_, v_, g_, b_, w_, sv["TT"], sv["h"], dSp0, sv["vn"],
-                dVnT0, do_, mix_, dQg, dKt, dq, dk, dv, dg, db, dw)), sp)
-        else:
+        ranges = l0_ranges if nb == B else [(0, NT)]
+        tl = _aux_streams(dev)[0] if len(ranges) > 1 else st
+        for p in reversed(range(len(ranges))):
+            c0, n = ranges[p]
+            last = p == len(ranges) - 1
+            _lib.call("ngdn_l0_scan_bwd", ctypes.byref(d), *(P(R(sv[x])) for x in (
+                "W", "KtT", "gam", "Qg", "Aqk")), P(R(do_)), P(R(mix_)), f[1] if L > 1 else 1,
+                P(R(inj)), nf1, P(R(d_final if last else l0_carry)), P(R(dSp0)), P(R(dVn0)),
+                P(R(dVnT0)), P(R(d_init if p == 0 else l0_carry)), c0, n, sp)
+            if fused_l0:
+                # the chunk backward in one launch: the state half per chunk
+                if tl is not st:
+                    tl.wait_event(st.record_event())
+                _lib.call("ngdn_l0_bwd", ctypes.byref(d), *(P(R(x)) for x in (
+                    q_, k_, v_, g_, b_, w_, sv["TT"], sv["h"], dSp0, sv["vn"],
+                    dVnT0, do_, mix_, dQg, dKt, dq, dk, dv, dg, db, dw)), c0, n,
+                    _lib.ptr_of_stream(tl), stream=tl)
+        if tl is not st:
+            st.wait_stream(tl)
+        if not fused_l0:
             _lib.call("ngdn_l0_bwd_state", ctypes.byref(d), P(R(sv["h"])), P(R(dSp0)),
                       P(R(sv["vn"])), P(R(dVn0)), P(R(do_)), P(R(mix_)),
                       *(P(R(x)) for x in (dQg, dWT, dKt, dAqk, dgam)), sp)

@@ -342,9 +342,10 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
                          const void* dout, const void* mix, int32_t f1,
                          const float* inj, int32_t nf1, const float* d_final,
                          float* dSp, float* dVn, float* dVnT, float* d_initial,
-                         void* stream) {
+                         int32_t chunk0, int32_t nchunk, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_scan_bwd")) return r;
+  if (int32_t r = check_range(d, chunk0, nchunk, "ngdn_l0_scan_bwd")) return r;
   if (!W || !KtT || !gam || !Qg || !Aqk || !dout || !mix || !dSp || (!dVn && !dVnT))
     return fail(NGDN_EINVAL, "ngdn_l0_scan_bwd: NULL tensor");
   const int NT = nchunks(d);
@@ -361,6 +362,7 @@ int32_t ngdn_l0_scan_bwd(const ngdn_dims* d, const float* W, const float* KtT,
   a.dinit = d_initial; a.di_sh = d->L * skv; a.di_sb = d->H * a.di_sh;
   a.B = d->B; a.H = d->H; a.S = NT; a.M = ngdn::CH; a.V = d->V;
   a.frag = d->dtype == NGDN_BF16 ? 3 : 0;   // W, KtT, Qg, Aqk: fragment order
+  a.j0 = chunk0; a.j1 = chunk0 + nchunk;
   return launched(ngdn::scan_bwd(a, d->dtype, d->K, (hipStream_t)stream), "ngdn_l0_scan_bwd");
 }
 
@@ -442,9 +444,10 @@ int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void
                     const float* TT, const float* h, const float* dSp,
                     const float* vn, const float* dVnT, const void* dout, const void* mix,
                     float* ws_dQg, float* ws_dKt, void* dq, void* dk, void* dv, float* dg,
-                    void* db, void* dw, void* stream) {
+                    void* db, void* dw, int32_t chunk0, int32_t nchunk, void* stream) {
   g_err[0] = 0;
   if (int32_t r = check_dims(d, "ngdn_l0_bwd")) return r;
+  if (int32_t r = check_range(d, chunk0, nchunk, "ngdn_l0_bwd")) return r;
   if (!q || !k || !v || !g || !b || !w || !TT || !h || !dSp || !vn || !dVnT ||
       !dout || !mix || !ws_dQg || !ws_dKt || !dq || !dk || !dv || !dg || !db || !dw)
     return fail(NGDN_EINVAL, "ngdn_l0_bwd: NULL tensor");
@@ -453,6 +456,7 @@ int32_t ngdn_l0_bwd(const ngdn_dims* d, const void* q, const void* k, const void
   a.dVnT = dVnT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.db = db; a.dw = dw;
   a.B = d->B; a.T = d->T; a.H = d->H; a.L = d->L; a.NT = nchunks(d); a.scale = d->scale;
   a.h = h; a.dSp = dSp; a.vn = vn; a.dout = dout; a.mix = mix; a.wsQ = ws_dQg; a.wsK = ws_dKt;
+  a.n0 = chunk0; a.nn = nchunk;
   return launched(ngdn::l0_bwd_fused(a, d->dtype, d->K, d->V, (hipStream_t)stream),
                   "ngdn_l0_bwd");
 }

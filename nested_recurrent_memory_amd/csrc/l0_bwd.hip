@@ -217,8 +217,9 @@ __global__ __launch_bounds__(256, 2) void l0_bwd_intra_kernel(L0BwdIntraArgs a) 
   float* s_m0 = s_dgam + K;                               // fused: mix_0 of the chunk's rows
 
   const int NT = a.NT, H = a.H, T = a.T;
-  const int n = blockIdx.x % NT;
-  const int bh = blockIdx.x / NT;
+  const int nn = a.nn > 0 ? a.nn : NT;
+  const int n = a.n0 + (int)(blockIdx.x % nn);
+  const int bh = blockIdx.x / nn;
   const int h = bh % H, b = bh / H;
   const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
   const size_t cix = (size_t)bh * NT + n;
@@ -802,7 +803,7 @@ static hipError_t launch_l0_bwd_state(const L0BwdStateArgs& a, hipStream_t st) {
 
 template <typename E, int K, int V, bool FUSED>
 static hipError_t launch_l0_bwd_intra(const L0BwdIntraArgs& a, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.B * a.H * a.NT);
+  const unsigned grid = (unsigned)(a.B * a.H * (a.nn > 0 ? a.nn : a.NT));
   hipLaunchKernelGGL((l0_bwd_intra_kernel<E, K, V, FUSED>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }

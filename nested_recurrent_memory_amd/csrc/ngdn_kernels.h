@@ -107,6 +107,9 @@ struct ScanBwdArgs {
   // bf16, fragment order: 1, AT (upper levels, M % 32 == 0); 3, the level-0
   // tiles W, KtT, Qg, Aqk
   int frag;
+  // level 0: steps [j0, j1) (j1 0: all S), from d_final, the gradient of the
+  // state after step j1 - 1, to dinit, the gradient of the state entering j0
+  int j0, j1;
 };
 hipError_t scan_bwd(const ScanBwdArgs& a, int dtype, int K, hipStream_t st);
 
@@ -458,6 +461,7 @@ struct L0BwdIntraArgs {
   // and dgam above are then unused
   const float* h; const float* dSp; const float* vn; const void* dout; const void* mix;
   float* wsQ; float* wsK;
+  int n0, nn;         // chunks [n0, n0 + nn) of every (batch, head) (nn 0: all NT)
 };
 hipError_t l0_bwd_intra(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st);
 hipError_t l0_bwd_fused(const L0BwdIntraArgs& a, int dtype, int K, int V, hipStream_t st);

@@ -538,8 +538,10 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
   };
 
   Ops nxt;
-  if (S > 0) load(S - 1, nxt);
-  for (int j = S - 1; j >= 0; --j) {
+  // steps [j0, j1) in reverse, from the state gradient after step j1 - 1
+  const int j0 = a.j0, j1 = a.j1 > 0 ? a.j1 : S;
+  if (j1 > j0) load(j1 - 1, nxt);
+  for (int j = j1 - 1; j >= j0; --j) {
     // ---- this step's slices into the wave's region (bf16; the previous
     // step's reads of the region were issued before, in this wave's order)
     if constexpr (BF) {
@@ -557,7 +559,7 @@ __global__ __launch_bounds__(256) void scan_bwd_l0_kernel(ScanBwdArgs a) {
     // ---- the next step's operand loads (the last step reloads its own, so
     // that no branch guards them); this step's dS' and dVn are stored after
     // its dVn products, while those loads are in flight
-    load(j > 0 ? j - 1 : 0, nxt);
+    load(j > j0 ? j - 1 : j0, nxt);
 
     // ---- dS' and mix_0 dO staged (transposed) as B operands
 #pragma unroll
