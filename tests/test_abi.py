@@ -222,3 +222,30 @@ def test_merge_with_k_below_v_is_refused():
     inp = make_inputs(B=1, T=64, H=2, K=64, V=128, L=2, N=16, intervals=(1, 1))
     with pytest.raises(ValueError, match="K < V"):
         chunk_nested_gdn2(**inp, L=2, promotion="merge")
+
+
+def test_ranges_outside_the_sequence_are_refused_before_any_launch():
+    """The chunk and firing ranges (interface 0.7.0 to 0.9.0) are checked on
+    the host: a range outside the sequence returns NGDN_EINVAL with its
+    message before any pointer is read (the pointers here are placeholders
+    that are never dereferenced)."""
+    so = _lib.lib()
+    x = ctypes.c_void_p(256)
+    d = _lib.dims(1, 128, 1, 2, 64, 64, _lib.NGDN_BF16, 0.125)     # NT = 2
+    for c0, n in ((-1, 1), (0, 0), (1, 2), (2, 1)):
+        rc = so.ngdn_l0_intra_fwd(ctypes.byref(d), *([x] * 13), c0, n, None)
+        assert rc == 1 and b"outside the 2 chunks" in so.ngdn_last_error(), (c0, n)
+        rc = so.ngdn_l0_scan_fwd(ctypes.byref(d), *([x] * 7), 1, *([x] * 6), c0, n, None)
+        assert rc == 1 and b"outside the 2 chunks" in so.ngdn_last_error(), (c0, n)
+        rc = so.ngdn_l0_scan_bwd(ctypes.byref(d), *([x] * 7), 1, None, 0, *([x] * 5), c0, n, None)
+        assert rc == 1 and b"outside the 2 chunks" in so.ngdn_last_error(), (c0, n)
+        rc = so.ngdn_l0_bwd(ctypes.byref(d), *([x] * 21), c0, n, None)
+        assert rc == 1 and b"outside the 2 chunks" in so.ngdn_last_error(), (c0, n)
+    # level 1 fires every chunk: NF = 2
+    for i0, n in ((-1, 1), (1, 2), (3, 0)):
+        rc = so.ngdn_probe_fwd(ctypes.byref(d), 1, 0, 16, 1, 1, x, 2, x, x, 16,
+                               *([x] * 15), i0, n, None)
+        assert rc == 1 and b"outside the level's 2" in so.ngdn_last_error(), (i0, n)
+    for s0, n in ((0, 0), (1, 2), (-1, 1)):
+        rc = so.ngdn_upper_scan_fwd(ctypes.byref(d), 1, 16, 2, 2, *([x] * 8), s0, n, None)
+        assert rc == 1 and b"outside the level's 2" in so.ngdn_last_error(), (s0, n)
