@@ -69,7 +69,7 @@ const char* ngdn_last_error(void);
  * 0.5.0 took W and U out of ngdn_l0_bwd; 0.6.0 moved the upper levels'
  * lower-state gradients from ngdn_probe_bwd's d_below to an injection that
  * ngdn_upper_scan_bwd adds. */
-#define NGDN_VERSION 900
+#define NGDN_VERSION 1000
 int32_t ngdn_version(void);
 /* Offload architecture the library was built for ("gfx950"). */
 const char* ngdn_arch(void);
@@ -221,6 +221,24 @@ int32_t ngdn_output_upper_fwd(const ngdn_dims* d, const float* read0, const void
 /* ---------------------------------------------------------------- backward
  * The backward of ChunkNestedGDN2Function (ops/chunk.py:650-719,
  * chunk_nested_gdn2_bwd :374-564), one entry point per stage. */
+
+/* No counterpart in the reference (whose gradients leave its autograd in the
+ * inputs' dtype): `count` (at most 16) fp32 arrays src[w] of n[w] elements
+ * cast to bf16 into dst[w], rounding to nearest even, in one launch; the op
+ * casts its fp32 gradients (dg, dmix, the parameter sums) this way into
+ * separately allocated outputs. */
+int32_t ngdn_cast_bf16(int32_t count, const float* const* src, void* const* dst,
+                       const int64_t* n, void* stream);
+
+/* No counterpart in the reference (whose kernels read the parameters as they
+ * are): `count` (at most 8) arrays src[w] [batch[w]][rows[w]][cols[w]] of
+ * elem_bytes-byte elements (2 or 4) transposed in their last two axes into
+ * dst[w] [batch[w]][cols[w]][rows[w]], in one launch; the op lays out the
+ * per-level parameters this way for the promotion kernels (the projections
+ * and, for the backward, the bank with its last two axes swapped). */
+int32_t ngdn_transpose(int32_t count, const void* const* src, void* const* dst,
+                       const int32_t* batch, const int32_t* rows, const int32_t* cols,
+                       int32_t elem_bytes, void* stream);
 
 /* dmix for level 0 (ops/chunk.py:423): dmix[..., 0] = <do, read0> per token,
  * read0 fp32 [B,T,H,V] from ngdn_output_fwd, do [B,T,H,V]; dmix fp32

@@ -20,7 +20,7 @@ NGDN_BF16 = 1
 # NGDN_VERSION of include/ngdn.h: the interface the signatures below describe.
 # The loader refuses a library of another version (working-tensor layouts and
 # argument meanings changed between versions under unchanged signatures).
-VERSION = 900
+VERSION = 1000
 
 
 class Dims(ctypes.Structure):
@@ -53,6 +53,8 @@ SIGNATURES = {
     "ngdn_output_l0_fwd": [PD, P, P, P, P, P, P],
     "ngdn_output_upper_fwd": [PD, P, P, P, P, P, P, P, P],
     "ngdn_output_bwd": [PD, P, P, P, P],
+    "ngdn_cast_bf16": [I32, P, P, P, P],
+    "ngdn_transpose": [I32, P, P, P, P, P, I32, P],
     "ngdn_read_state_bwd": [PD, I32, I32, I32, P, P, P, P, P, P, P, P],
     "ngdn_l0_scan_bwd": [PD, P, P, P, P, P, P, P, I32, P, I32, P, P, P, P, P, I32, I32, P],
     "ngdn_upper_scan_bwd": [PD, I32, I32, I32, I32, P, P, P, P, P, I32, I32, I32, P, P, P, P, P],

@@ -378,13 +378,29 @@ def _params(qb, kp, bp, wp, gp, wd, train):
     qb_ = qb.to(wd)
     if nmax8 != nmax:
         qb_ = torch.nn.functional.pad(qb_, (0, 0, 0, nmax8 - nmax))
-    t = lambda x: x.to(wd).transpose(-1, -2).contiguous()  # noqa: E731
-    par = dict(qb=qb_.contiguous(), nmax=nmax8, kp=kp.to(wd).contiguous(),
-               bpT=t(bp), wpT=t(wp), gpT=t(gp))
+    c = lambda x: x.to(wd).contiguous()  # noqa: E731
+    qb_, kp_, bp_, wp_, gp_ = (c(x) for x in (qb_, kp, bp, wp, gp))
+    # the transposes in one launch
+    tr = _transpose_last2([bp_, wp_, gp_] + ([kp_, qb_] if train else []))
+    par = dict(qb=qb_, nmax=nmax8, kp=kp_, bpT=tr[0], wpT=tr[1], gpT=tr[2])
     if train:
-        par.update(kpT=t(kp), bankT=t(qb_), bp=bp.to(wd).contiguous(),
-                   wp=wp.to(wd).contiguous(), gp=gp.to(wd).contiguous())
+        par.update(kpT=tr[3], bankT=tr[4], bp=bp_, wp=wp_, gp=gp_)
     return par
+
+
+def _transpose_last2(xs):
+    """Contiguous tensors of one dtype transposed in their last two axes
+    (ngdn_transpose: one launch on the current stream)."""
+    outs = [torch.empty(x.shape[:-2] + (x.shape[-1], x.shape[-2]), device=x.device, dtype=x.dtype)
+            for x in xs]
+    n = len(xs)
+    _lib.call("ngdn_transpose", n, (ctypes.c_void_p * n)(*(x.data_ptr() for x in xs)),
+              (ctypes.c_void_p * n)(*(y.data_ptr() for y in outs)),
+              (ctypes.c_int32 * n)(*(x.numel() // max(1, x.shape[-1] * x.shape[-2]) for x in xs)),
+              (ctypes.c_int32 * n)(*(x.shape[-2] for x in xs)),
+              (ctypes.c_int32 * n)(*(x.shape[-1] for x in xs)),
+              xs[0].element_size(), _lib.stream_of(xs[0]))
+    return outs
 
 
 def _level_arrays(states, NT, f, L):
@@ -680,25 +696,39 @@ class ChunkNestedGDN2Function(torch.autograd.Function):
         grads = _backward(sv, do, dfinal, L, scale, f, nq, has_init, promotion)
         (dq, dk, dv, dg, db, dw, dmix, dqb, dkp, dbp, dwp, dgp, dinit) = grads
         dts = ctx.dtypes
-        out = [dq, dk, dv, dg, db, dw, dmix]
-        out = [x.to(dt) for x, dt in zip(out, dts[:7])]
+        grads = [dq, dk, dv, dg, db, dw, dmix] + ([dqb, dkp, dbp, dwp, dgp] if L > 1 else [])
+        out = _cast_grads(grads, dts[:len(grads)])
         if L > 1:
-            pg = (dqb, dkp, dbp, dwp, dgp)
-            pdt = dts[7]
-            n = [x.numel() for x in pg]
-            if (pdt != torch.float32 and all(dt == pdt for dt in dts[8:12])
-                    and all(pg[i + 1].data_ptr() == pg[i].data_ptr() + 4 * n[i] for i in range(4))):
-                # the five sums are consecutive in one fp32 buffer: one cast
-                flat = dqb.view(-1).as_strided((sum(n),), (1,)).to(pdt)
-                pg = [y.view(x.shape) for x, y in zip(pg, flat.split(n))]
-            else:
-                pg = [x.to(dt) for x, dt in zip(pg, dts[7:12])]
-            pg[0] = pg[0][:, :, :ctx.nmax]      # drop the alignment padding rows
-            out += pg
+            if out[7].shape[2] != ctx.nmax:
+                out[7] = out[7][:, :, :ctx.nmax]      # drop the alignment padding rows
         else:
             out += [None] * 5
         return (*out, None, None, None, None,
                 dinit.to(dts[12]) if dinit is not None else None, None, None, None, None)
+
+
+def _cast_grads(grads, dtypes):
+    """The gradients in their inputs' dtypes. The fp32 -> bf16 casts (dg,
+    dmix, the parameter sums for bf16 inputs) run in one launch into
+    separately allocated tensors, which autograd takes as the leaves'
+    gradients without copying them (views of one shared buffer it copies);
+    the rest cast with torch."""
+    out = list(grads)
+    batch = [i for i, (x, dt) in enumerate(zip(grads, dtypes))
+             if x is not None and x.dtype == torch.float32 and dt == torch.bfloat16
+             and x.is_contiguous()]
+    if len(batch) > 1:
+        for i in batch:
+            out[i] = torch.empty(grads[i].shape, device=grads[i].device, dtype=torch.bfloat16)
+        n = len(batch)
+        srcs = (ctypes.c_void_p * n)(*(grads[i].data_ptr() for i in batch))
+        dsts = (ctypes.c_void_p * n)(*(out[i].data_ptr() for i in batch))
+        cnt = (ctypes.c_int64 * n)(*(grads[i].numel() for i in batch))
+        _lib.call("ngdn_cast_bf16", n, srcs, dsts, cnt, _lib.stream_of(grads[batch[0]]))
+    else:
+        batch = []
+    return [x if x is None or i in batch else x.to(dt)
+            for i, (x, dt) in enumerate(zip(out, dtypes))]
 
 
 def chunk_nested_gdn2(q, k, v, g, b, w, mix_weights, query_banks, key_projections,

@@ -309,6 +309,46 @@ int32_t ngdn_output_upper_fwd(const ngdn_dims* d, const float* read0, const void
                   "ngdn_output_upper_fwd");
 }
 
+int32_t ngdn_cast_bf16(int32_t count, const float* const* src, void* const* dst,
+                       const int64_t* n, void* stream) {
+  g_err[0] = 0;
+  if (count < 0 || count > ngdn::CAST_MAX || (count > 0 && (!src || !dst || !n)))
+    return fail(NGDN_EINVAL, "ngdn_cast_bf16: %d arrays (at most %d)", count, ngdn::CAST_MAX);
+  ngdn::CastArgs a{};
+  a.count = count;
+  for (int w = 0; w < count; ++w) {
+    if (n[w] < 0 || (n[w] > 0 && (!src[w] || !dst[w])))
+      return fail(NGDN_EINVAL, "ngdn_cast_bf16: array %d NULL or of negative size", w);
+    a.src[w] = src[w]; a.dst[w] = dst[w]; a.n[w] = n[w];
+  }
+  return launched(ngdn::cast_bf16(a, (hipStream_t)stream), "ngdn_cast_bf16");
+}
+
+int32_t ngdn_transpose(int32_t count, const void* const* src, void* const* dst,
+                       const int32_t* batch, const int32_t* rows, const int32_t* cols,
+                       int32_t elem_bytes, void* stream) {
+  g_err[0] = 0;
+  if (count < 0 || count > ngdn::TR_MAX || (count > 0 && (!src || !dst || !batch || !rows || !cols)))
+    return fail(NGDN_EINVAL, "ngdn_transpose: %d arrays (at most %d)", count, ngdn::TR_MAX);
+  if (elem_bytes != 2 && elem_bytes != 4)
+    return fail(NGDN_EINVAL, "ngdn_transpose: elements of %d bytes (2 or 4)", elem_bytes);
+  ngdn::TransposeArgs a{};
+  a.count = count; a.esz = elem_bytes;
+  long long tiles = 0;
+  for (int w = 0; w < count; ++w) {
+    if (batch[w] < 0 || rows[w] < 0 || cols[w] < 0 ||
+        (batch[w] > 0 && rows[w] > 0 && cols[w] > 0 && (!src[w] || !dst[w])))
+      return fail(NGDN_EINVAL, "ngdn_transpose: array %d NULL or of negative size", w);
+    a.src[w] = src[w]; a.dst[w] = dst[w];
+    a.batch[w] = batch[w]; a.R[w] = rows[w]; a.C[w] = cols[w];
+    a.tiles0[w] = (int)tiles;
+    tiles += (long long)batch[w] * ((rows[w] + 31) / 32) * ((cols[w] + 31) / 32);
+    if (tiles > (1LL << 30)) return fail(NGDN_EINVAL, "ngdn_transpose: too many tiles");
+  }
+  a.tiles0[count] = (int)tiles;
+  return launched(ngdn::transpose(a, (hipStream_t)stream), "ngdn_transpose");
+}
+
 int32_t ngdn_output_bwd(const ngdn_dims* d, const float* read0, const void* dout,
                         float* dmix, void* stream) {
   g_err[0] = 0;

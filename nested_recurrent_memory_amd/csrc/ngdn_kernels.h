@@ -409,6 +409,27 @@ struct Dmix0Args {
 };
 hipError_t dmix0_bwd(const Dmix0Args& a, int dtype, hipStream_t st);
 
+// fp32 arrays cast to bf16 in one launch (the op's gradients in its inputs'
+// dtype): dst[w][i] = src[w][i] rounded to nearest even, w < count.
+constexpr int CAST_MAX = 16;
+struct CastArgs {
+  const float* src[CAST_MAX]; void* dst[CAST_MAX]; long long n[CAST_MAX];
+  int count;
+};
+hipError_t cast_bf16(const CastArgs& a, hipStream_t st);
+
+// Batched transposes of the last two axes in one launch: array w is
+// src [batch][R][C] -> dst [batch][C][R], elements of esz bytes (2 or 4);
+// tiles0 holds the prefix sums of the arrays' 32 x 32 tile counts.
+constexpr int TR_MAX = 8;
+struct TransposeArgs {
+  const void* src[TR_MAX]; void* dst[TR_MAX];
+  int batch[TR_MAX], R[TR_MAX], C[TR_MAX];
+  int tiles0[TR_MAX + 1];
+  int count, esz;
+};
+hipError_t transpose(const TransposeArgs& a, hipStream_t st);
+
 // Backward of level l's reads, per (batch, group j, head), over the group's
 // chunks (read_level_bwd, ops/chunk.py:307-336, and the dq/dmix terms of
 // :423-449). With S = S_l[j] (rows [K][V] fp32, staged once) and

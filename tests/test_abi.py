@@ -249,3 +249,17 @@ def test_ranges_outside_the_sequence_are_refused_before_any_launch():
     for s0, n in ((0, 0), (1, 2), (-1, 1)):
         rc = so.ngdn_upper_scan_fwd(ctypes.byref(d), 1, 16, 2, 2, *([x] * 8), s0, n, None)
         assert rc == 1 and b"outside the level's 2" in so.ngdn_last_error(), (s0, n)
+
+
+def test_utilities_refuse_bad_arguments():
+    """ngdn_transpose and ngdn_cast_bf16 check their counts and element
+    size on the host (no launch)."""
+    so = _lib.lib()
+    assert so.ngdn_transpose(9, None, None, None, None, None, 2, None) == 1
+    assert b"at most 8" in so.ngdn_last_error()
+    one = (ctypes.c_int32 * 1)(1)
+    ptr = (ctypes.c_void_p * 1)(256)
+    assert so.ngdn_transpose(1, ptr, ptr, one, one, one, 3, None) == 1
+    assert b"2 or 4" in so.ngdn_last_error()
+    assert so.ngdn_cast_bf16(17, None, None, None, None) == 1
+    assert b"at most 16" in so.ngdn_last_error()
