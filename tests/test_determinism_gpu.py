@@ -63,11 +63,12 @@ def test_three_levels_two_runs_and_two_row_groups_are_bit_identical(promotion, d
     _assert_equal(first, grouped)
 
 
-@pytest.mark.parametrize("T,K,promotion,fire_partial,fused", [
-    (64 * 256, 64, "learned", True, False), (64 * 200 + 17, 64, "learned", True, False),
-    (64 * 200 + 17, 64, "merge", True, False), (64 * 200 + 17, 64, "learned", False, False),
-    (64 * 200 + 17, 64, "learned", True, True), (64 * 256, 128, "learned", True, False)])
-def test_level0_chunk_ranges_equal_one_launch(T, K, promotion, fire_partial, fused):
+@pytest.mark.parametrize("T,K,L,promotion,fire_partial,fused", [
+    (64 * 256, 64, 3, "learned", True, False), (64 * 200 + 17, 64, 3, "learned", True, False),
+    (64 * 200 + 17, 64, 3, "merge", True, False), (64 * 200 + 17, 64, 3, "learned", False, False),
+    (64 * 200 + 17, 64, 3, "learned", True, True), (64 * 256, 128, 3, "learned", True, False),
+    (64 * 200 + 17, 64, 2, "learned", True, False), (64 * 200 + 17, 64, 1, "learned", True, False)])
+def test_level0_chunk_ranges_equal_one_launch(T, K, L, promotion, fire_partial, fused):
     """On small grids the forward forms the level-0 chunk terms and runs the
     level-0 scan over consecutive ranges of chunks, the chunk terms of a range
     on a side stream beside the scan of the range before, the state carried
@@ -80,14 +81,14 @@ def test_level0_chunk_ranges_equal_one_launch(T, K, promotion, fire_partial, fus
     NT = -(-T // 64)
     from nested_recurrent_memory_amd import _lib
     assert len(chunk_mod._l0_ranges(1, 2, K, NT, _lib.NGDN_BF16)) > 1
-    inp = make_inputs(B=1, T=T, H=2, K=K, V=K, L=3, N=32,
-                      intervals=(1, 4, 16), dtype=torch.bfloat16, g_scale=0.1)
+    inp = make_inputs(B=1, T=T, H=2, K=K, V=K, L=L, N=32,
+                      intervals=(1, 4, 16)[:L], dtype=torch.bfloat16, g_scale=0.1)
     saved = chunk_mod.L0_PARTS, chunk_mod.FUSED_PROMOTION
     try:
         chunk_mod.FUSED_PROMOTION = fused
-        ranged = _grads(inp, 3, promotion, fire_partial=fire_partial)
+        ranged = _grads(inp, L, promotion, fire_partial=fire_partial)
         chunk_mod.L0_PARTS = 1
-        single = _grads(inp, 3, promotion, fire_partial=fire_partial)
+        single = _grads(inp, L, promotion, fire_partial=fire_partial)
     finally:
         chunk_mod.L0_PARTS, chunk_mod.FUSED_PROMOTION = saved
     _assert_equal(ranged, single)
