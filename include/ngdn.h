@@ -233,7 +233,8 @@ int32_t ngdn_cast_bf16(int32_t count, const float* const* src, void* const* dst,
 /* No counterpart in the reference (whose kernels read the parameters as they
  * are): `count` (at most 8) arrays src[w] [batch[w]][rows[w]][cols[w]] of
  * elem_bytes-byte elements (2 or 4) transposed in their last two axes into
- * dst[w] [batch[w]][cols[w]][rows[w]], in one launch; the op lays out the
+ * dst[w] [batch[w]][cols[w]][rows[w]], in one launch (at most 2^24 - 1
+ * tiles of 32 x 32 in all, one 256-thread block each); the op lays out the
  * per-level parameters this way for the promotion kernels (the projections
  * and, for the backward, the bank with its last two axes swapped). */
 int32_t ngdn_transpose(int32_t count, const void* const* src, void* const* dst,

@@ -343,7 +343,10 @@ int32_t ngdn_transpose(int32_t count, const void* const* src, void* const* dst,
     a.batch[w] = batch[w]; a.R[w] = rows[w]; a.C[w] = cols[w];
     a.tiles0[w] = (int)tiles;
     tiles += (long long)batch[w] * ((rows[w] + 31) / 32) * ((cols[w] + 31) / 32);
-    if (tiles > (1LL << 30)) return fail(NGDN_EINVAL, "ngdn_transpose: too many tiles");
+    // one 256-thread block per tile: the grid's work-items must fit 32 bits
+    if (tiles > (1LL << 24) - 1)
+      return fail(NGDN_EINVAL, "ngdn_transpose: %lld tiles of 32 x 32 (at most %lld)", tiles,
+                  (1LL << 24) - 1);
   }
   a.tiles0[count] = (int)tiles;
   return launched(ngdn::transpose(a, (hipStream_t)stream), "ngdn_transpose");

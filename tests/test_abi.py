@@ -261,5 +261,10 @@ def test_utilities_refuse_bad_arguments():
     ptr = (ctypes.c_void_p * 1)(256)
     assert so.ngdn_transpose(1, ptr, ptr, one, one, one, 3, None) == 1
     assert b"2 or 4" in so.ngdn_last_error()
+    # 2^24 tiles would need 2^32 work-items: refused before any launch
+    big = (ctypes.c_int32 * 1)(1 << 12)     # 128 x 128 tiles per matrix
+    many = (ctypes.c_int32 * 1)(1 << 10)    # 2^10 matrices
+    assert so.ngdn_transpose(1, ptr, ptr, many, big, big, 2, None) == 1
+    assert b"at most 16777215" in so.ngdn_last_error()
     assert so.ngdn_cast_bf16(17, None, None, None, None) == 1
     assert b"at most 16" in so.ngdn_last_error()
