@@ -391,6 +391,8 @@ def _params(qb, kp, bp, wp, gp, wd, train):
 def _transpose_last2(xs):
     """Contiguous tensors of one dtype transposed in their last two axes
     (ngdn_transpose: one launch on the current stream)."""
+    if any(not x.is_contiguous() or x.dtype != xs[0].dtype or x.dim() < 2 for x in xs):
+        raise ValueError("_transpose_last2: contiguous tensors of one dtype, at least 2-D")
     outs = [torch.empty(x.shape[:-2] + (x.shape[-1], x.shape[-2]), device=x.device, dtype=x.dtype)
             for x in xs]
     n = len(xs)

@@ -268,3 +268,14 @@ def test_utilities_refuse_bad_arguments():
     assert b"at most 16777215" in so.ngdn_last_error()
     assert so.ngdn_cast_bf16(17, None, None, None, None) == 1
     assert b"at most 16" in so.ngdn_last_error()
+
+
+def test_transpose_wrapper_refuses_strided_or_mixed():
+    """The host wrapper hands raw pointers to ngdn_transpose, so it refuses a
+    strided view or mixed dtypes before any call."""
+    from nested_recurrent_memory_amd.chunk import _transpose_last2
+    x = torch.zeros(4, 6)
+    with pytest.raises(ValueError):
+        _transpose_last2([x.t()])
+    with pytest.raises(ValueError):
+        _transpose_last2([x, x.double()])
