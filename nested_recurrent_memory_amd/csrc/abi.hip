@@ -39,6 +39,11 @@ int32_t check_dims(const ngdn_dims* d, const char* what) {
     return fail(NGDN_EINVAL, "%s: dtype %d unsupported", what, d->dtype);
   if (d->hold_partial != 0 && d->hold_partial != 1)
     return fail(NGDN_EINVAL, "%s: hold_partial %d is neither 0 nor 1", what, d->hold_partial);
+  // the largest grids are one 512-thread workgroup per (batch, head, chunk):
+  // their work-items must fit 32 bits
+  const long long bhc = (long long)d->B * d->H * ((d->T + ngdn::CH - 1) / ngdn::CH);
+  if (bhc > (1LL << 23) - 1)
+    return fail(NGDN_EINVAL, "%s: B*H*chunks = %lld exceeds %lld", what, bhc, (1LL << 23) - 1);
   return NGDN_OK;
 }
 

@@ -279,3 +279,18 @@ def test_transpose_wrapper_refuses_strided_or_mixed():
         _transpose_last2([x.t()])
     with pytest.raises(ValueError):
         _transpose_last2([x, x.double()])
+
+
+def test_grid_bound_is_checked_before_any_launch():
+    """B*H*chunks at most 2^23 - 1 (one 512-thread workgroup per (batch, head,
+    chunk) must keep the grid within 32-bit work-items): the bound itself
+    passes the size check and fails only on its empty range, one more is
+    refused as too large. Placeholder pointers are never dereferenced."""
+    so = _lib.lib()
+    x = ctypes.c_void_p(256)
+    d = _lib.dims(128, 1024 * 64, 64, 1, 64, 64, _lib.NGDN_BF16, 0.125)   # 2^23
+    assert so.ngdn_l0_intra_fwd(ctypes.byref(d), *([x] * 13), 0, 1, None) == 1
+    assert b"exceeds 8388607" in so.ngdn_last_error()
+    d = _lib.dims((1 << 23) - 1, 64, 1, 1, 64, 64, _lib.NGDN_BF16, 0.125)
+    assert so.ngdn_l0_intra_fwd(ctypes.byref(d), *([x] * 13), 0, 0, None) == 1
+    assert b"outside the 1 chunks" in so.ngdn_last_error()
