@@ -259,7 +259,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
 
   // ---- 4. vn = Vals w - kb s with s = e^g S_j (s^T rows scaled per k);
   // dw-side terms
-  f4 vnt[TPW], dvd[TPW], dxwt[TPW];
+  f4 vnt[TPW], dvd[TPW];
   {
     SF fT[NKS];
     const float* brow = SjT + (size_t)(ctw * 16 + rl) * K + ko;
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
     }
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      vnt[t] = dvd[t] = dxwt[t] = f4_zero();
+      vnt[t] = dvd[t] = f4_zero();
       int rt;
       if (!tile(t, rt)) continue;
       const float* arow = s_kb + (rt * 16 + rl) * LD + ko;
@@ -287,7 +287,9 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
         const float dv = DVN_LDS ? s_dvn[n * LD + v] : dvn[(size_t)n * V + v];
         vnt[t][r] = val * w - ks[r];
         dvd[t][r] = dv * w;
-        dxwt[t][r] = dv * val * w * (1.f - w);
+        // dxw goes to its workspace at once (not held through phase 5);
+        // phase 6 reads this lane's own values back for the LDS tile
+        wsdxw[(size_t)n * V + v] = dv * val * w * (1.f - w);
       }
     }
   }
@@ -422,12 +424,11 @@ __global__ __launch_bounds__(512) void probe_bwd_kernel(ProbeBwdArgs ab) {
       const int n = rt * 16 + acc_row(r), k = ctw * 16 + acc_col();
       if (!MERGE) wsdu[(size_t)n * K + k] = dut[t][r];
       wsdxb[(size_t)n * K + k] = dxbt[t][r];
-      wsdxw[(size_t)n * V + k] = dxwt[t][r];
       wsdxg[(size_t)n * K + k] = dxgt[t][r];
       if constexpr (WS_LDS) {
         if (!MERGE) ws_tile(0).put1(n * LDT + k, dut[t][r]);
         ws_tile(1).put1(n * LDT + k, dxbt[t][r]);
-        ws_tile(2).put1(n * LDT + k, dxwt[t][r]);
+        ws_tile(2).put1(n * LDT + k, wsdxw[(size_t)n * V + k]);
         ws_tile(3).put1(n * LDT + k, dxgt[t][r]);
       }
     }
